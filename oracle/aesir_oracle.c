@@ -1,0 +1,574 @@
+/*
+ * aesir_oracle.c -- CPU restatement of A.E.S.I.R.'s verified Llama F16 forward path.
+ *
+ * TEST INFRASTRUCTURE ONLY (the checker, never the thing measured or shipped): loaded by
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg. Single-threaded, like the
+ * reference (which has no parallelize anywhere).
+ *
+ * Citations are to the reference repository (paths under aesir_engine/).
+ *
+ * Arithmetic conventions that the reference fixes:
+ *   - binary16 storage after every op, round-to-nearest-even (Mojo .cast[f16]()).
+ *   - f16 x f16 -> f16 ops (RMSNorm scale, RoPE rotation, SiLU, SwiGLU mul, residual add) are
+ *     evaluated in f32 and rounded once to f16. For +, -, *, / this equals the correctly rounded
+ *     binary16 result (24 >= 2*11+2, so the double rounding is innocuous).
+ *   - No floating-point contraction anywhere (built with -ffp-contract=off).
+ *   - The 16-lane SIMD reduce_add of the reference (simd_w_f16 = 16, compute.mojo:19-20) is
+ *     evaluated as a halving tree: lanes i and i+8, then i and i+4, i and i+2, then 0 and 1.
+ *     That lane order is Mojo-stdlib behaviour that this repository cannot run; it is
+ *     documented as the unpinned last bit of gemm_f16 and rmsnorm.
+ */
+#include "aesir_oracle.h"
+
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#if defined(__x86_64__)
+#include <immintrin.h>
+#define AO_HAVE_X86 1
+#else
+#define AO_HAVE_X86 0
+#endif
+
+static __thread char g_err[512];
+
+static int ao_fail(int code, const char *msg) {
+    snprintf(g_err, sizeof g_err, "%s", msg);
+    return code;
+}
+
+const char *ao_last_error(void) { return g_err; }
+
+/* ------------------------------------------------------------------ binary16 */
+
+uint16_t ao_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t a = x & 0x7fffffffu;
+    if (a >= 0x7f800000u) {
+        if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((a >> 13) & 0x3ffu)); /* quiet NaN */
+        return (uint16_t)(sign | 0x7c00u);
+    }
+    if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* >= 65520 rounds to infinity */
+    if (a < 0x38800000u) {                                   /* below 2^-14: subnormal or zero */
+        if (a < 0x33000000u) return (uint16_t)sign;          /* below 2^-25 rounds to zero */
+        uint32_t e = a >> 23;
+        uint32_t m = (a & 0x7fffffu) | 0x800000u;
+        uint32_t shift = 126u - e; /* value / 2^-24 = m * 2^(e-126) */
+        uint32_t q = m >> shift;
+        uint32_t rem = m & ((1u << shift) - 1u);
+        uint32_t half = 1u << (shift - 1u);
+        if (rem > half || (rem == half && (q & 1u))) q++;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t r = ((a >> 23) - 112u) << 10 | ((a >> 13) & 0x3ffu);
+    uint32_t rem = a & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) r++;
+    return (uint16_t)(sign | r);
+}
+
+float ao_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1fu;
+    uint32_t m = h & 0x3ffu;
+    uint32_t bits;
+    if (e == 0) {
+        if (m == 0) {
+            bits = sign;
+        } else { /* subnormal: m * 2^-24 is exact in f32 */
+            float v = (float)m * 5.9604644775390625e-08f;
+            memcpy(&bits, &v, 4);
+            bits |= sign;
+        }
+    } else if (e == 31) {
+        bits = sign | 0x7f800000u | (m << 13);
+    } else {
+        bits = sign | ((e + 112u) << 23) | (m << 13);
+    }
+    float out;
+    memcpy(&out, &bits, 4);
+    return out;
+}
+
+void ao_f32_to_f16_array(const float *src, uint16_t *dst, int64_t n) {
+    for (int64_t i = 0; i < n; i++) dst[i] = ao_f32_to_f16(src[i]);
+}
+
+void ao_f16_to_f32_array(const uint16_t *src, float *dst, int64_t n) {
+    for (int64_t i = 0; i < n; i++) dst[i] = ao_f16_to_f32(src[i]);
+}
+
+#define H2F(h) ao_f16_to_f32(h)
+#define F2H(f) ao_f32_to_f16(f)
+
+/* f16 op f16 -> f16, one rounding (see header note). */
+static inline uint16_t hmul(uint16_t a, uint16_t b) { return F2H(H2F(a) * H2F(b)); }
+static inline uint16_t hadd(uint16_t a, uint16_t b) { return F2H(H2F(a) + H2F(b)); }
+static inline uint16_t hsub(uint16_t a, uint16_t b) { return F2H(H2F(a) - H2F(b)); }
+static inline uint16_t hdiv(uint16_t a, uint16_t b) { return F2H(H2F(a) / H2F(b)); }
+
+/* ------------------------------------------------- 16-lane chunk dot products */
+
+/* One simd_w_f16 = 16 chunk: products in f32 (exact for f16 inputs), then the halving tree. */
+static float chunk16_dot_scalar(const uint16_t *a, const uint16_t *b) {
+    float p[16];
+    for (int i = 0; i < 16; i++) p[i] = H2F(a[i]) * H2F(b[i]);
+    float s8[8], s4[4], s2[2];
+    for (int i = 0; i < 8; i++) s8[i] = p[i] + p[i + 8];
+    for (int i = 0; i < 4; i++) s4[i] = s8[i] + s8[i + 4];
+    for (int i = 0; i < 2; i++) s2[i] = s4[i] + s4[i + 2];
+    return s2[0] + s2[1];
+}
+
+#if AO_HAVE_X86
+__attribute__((target("avx2,f16c"))) static float dot_f16_avx2(const uint16_t *a, const uint16_t *b, int64_t n16,
+                                                              float sum) {
+    for (int64_t c = 0; c < n16; c += 16) {
+        __m256 a0 = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(a + c)));
+        __m256 a1 = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(a + c + 8)));
+        __m256 b0 = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(b + c)));
+        __m256 b1 = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(b + c + 8)));
+        __m256 s8 = _mm256_add_ps(_mm256_mul_ps(a0, b0), _mm256_mul_ps(a1, b1));
+        __m128 s4 = _mm_add_ps(_mm256_castps256_ps128(s8), _mm256_extractf128_ps(s8, 1));
+        __m128 s2 = _mm_add_ps(s4, _mm_movehl_ps(s4, s4));
+        __m128 s1 = _mm_add_ss(s2, _mm_shuffle_ps(s2, s2, 1));
+        sum += _mm_cvtss_f32(s1);
+    }
+    return sum;
+}
+static int g_simd = -1;
+static int simd_ok(void) {
+    if (g_simd < 0) g_simd = (__builtin_cpu_supports("avx2") && __builtin_cpu_supports("f16c")) ? 1 : 0;
+    return g_simd;
+}
+#else
+static int simd_ok(void) { return 0; }
+#endif
+
+int ao_simd_enabled(void) { return simd_ok(); }
+
+/* Sum over the 16-lane chunks of a.b, in chunk order, starting from `sum`. */
+static float dot_chunks(const uint16_t *a, const uint16_t *b, int64_t n16, float sum) {
+#if AO_HAVE_X86
+    if (simd_ok()) return dot_f16_avx2(a, b, n16, sum);
+#endif
+    for (int64_t c = 0; c < n16; c += 16) sum += chunk16_dot_scalar(a + c, b + c);
+    return sum;
+}
+
+/* ------------------------------------------------------------------ kernels */
+
+/* gemm_f16, compute.mojo:1751-1854 (dense F16 loop :1831-1854). C[m,n] = f16(sum_k A[m,k]*B[n,k]). */
+int ao_gemm_f16(const uint16_t *A, int64_t a_rows, int64_t a_cols, const uint16_t *B, int64_t b_rows,
+                int64_t b_cols, uint16_t *C, int64_t c_rows, int64_t c_cols) {
+    if (a_rows <= 0 || a_cols <= 0 || b_rows <= 0 || b_cols <= 0)
+        return ao_fail(AO_ERR_INVALID, "gemm_f16: matrix dimensions must be positive");
+    if (a_cols != b_cols) return ao_fail(AO_ERR_SHAPE, "gemm_f16: inner matrix dimension mismatch");
+    if (c_rows != a_rows || c_cols != b_rows) return ao_fail(AO_ERR_SHAPE, "gemm_f16: output matrix shape mismatch");
+    const int64_t K = a_cols;
+    const int64_t simd_end = (K / 16) * 16;
+    for (int64_t row = 0; row < a_rows; row++) {
+        const uint16_t *a = A + row * K;
+        for (int64_t n = 0; n < b_rows; n++) {
+            const uint16_t *b = B + n * K;
+            float sum = dot_chunks(a, b, simd_end, 0.0f);
+            for (int64_t k = simd_end; k < K; k++) sum += H2F(a[k]) * H2F(b[k]); /* scalar tail :1847-1853 */
+            C[row * b_rows + n] = F2H(sum);
+        }
+    }
+    return AO_OK;
+}
+
+/* rmsnorm, compute.mojo:2166-2204. In place; inv_rms rounded to f16; two f16 roundings per element. */
+int ao_rmsnorm_f16(uint16_t *T, int64_t rows, int64_t cols, const uint16_t *w, int64_t w_size, float eps) {
+    if (rows <= 0 || cols <= 0) return ao_fail(AO_ERR_INVALID, "rmsnorm: tensor dimensions must be positive");
+    if (w_size < cols) return ao_fail(AO_ERR_SHAPE, "rmsnorm: weight dimension mismatch");
+    if (!(eps > 0.0f)) return ao_fail(AO_ERR_INVALID, "rmsnorm: epsilon must be positive");
+    const int64_t simd_end = (cols / 16) * 16;
+    for (int64_t r = 0; r < rows; r++) {
+        uint16_t *x = T + r * cols;
+        float ss = dot_chunks(x, x, simd_end, 0.0f);
+        for (int64_t c = simd_end; c < cols; c++) {
+            float v = H2F(x[c]);
+            ss += v * v;
+        }
+        float rms = sqrtf(ss / (float)cols + eps);
+        uint16_t inv_rms = F2H(1.0f / rms);
+        for (int64_t c = 0; c < cols; c++) x[c] = hmul(hmul(x[c], inv_rms), w[c]);
+    }
+    return AO_OK;
+}
+
+/* apply_rope, compute.mojo:2207-2244. Adjacent-pair rotation in f16 arithmetic; angle in f32. */
+int ao_rope_f16(uint16_t *Q, int64_t q_rows, int64_t q_cols, uint16_t *K, int64_t k_rows, int64_t k_cols,
+                int64_t start_pos, int64_t head_dim, float theta) {
+    if (start_pos < 0) return ao_fail(AO_ERR_INVALID, "apply_rope: start_pos cannot be negative");
+    if (head_dim <= 0 || head_dim % 2 != 0)
+        return ao_fail(AO_ERR_INVALID, "apply_rope: head_dim must be positive and even");
+    if (q_cols % head_dim != 0 || k_cols % head_dim != 0)
+        return ao_fail(AO_ERR_SHAPE, "apply_rope: tensor columns must be a multiple of head_dim");
+    if (q_rows <= 0 || k_rows <= 0) return ao_fail(AO_ERR_INVALID, "apply_rope: tensor dimensions must be positive");
+    /* The reference indexes K with Q's row count; a shorter K would be written out of bounds. */
+    if (k_rows < q_rows) return ao_fail(AO_ERR_SHAPE, "apply_rope: K rows must cover Q rows");
+    const int64_t nq = q_cols / head_dim, nk = k_cols / head_dim;
+    /* The reference loops over Q.rows only and indexes K with the same row (:2226-2244). */
+    for (int64_t r = 0; r < q_rows; r++) {
+        int64_t pos = start_pos + r;
+        for (int64_t i = 0; i < head_dim; i += 2) {
+            float freq = 1.0f / powf(theta, (float)i / (float)head_dim);
+            float val = (float)pos * freq;
+            uint16_t fcr = F2H(cosf(val));
+            uint16_t fci = F2H(sinf(val));
+            for (int64_t h = 0; h < nq; h++) {
+                uint16_t *p = Q + r * q_cols + h * head_dim + i;
+                uint16_t q0 = p[0], q1 = p[1];
+                p[0] = hsub(hmul(q0, fcr), hmul(q1, fci));
+                p[1] = hadd(hmul(q0, fci), hmul(q1, fcr));
+            }
+            for (int64_t h = 0; h < nk; h++) {
+                uint16_t *p = K + r * k_cols + h * head_dim + i;
+                uint16_t k0 = p[0], k1 = p[1];
+                p[0] = hsub(hmul(k0, fcr), hmul(k1, fci));
+                p[1] = hadd(hmul(k0, fci), hmul(k1, fcr));
+            }
+        }
+    }
+    return AO_OK;
+}
+
+/* flash_attention_gqa, compute.mojo:1950-2015. One query row; the output accumulator is stored as
+ * f16 after every position (:1994-2004). Invalid inputs return with the output untouched. */
+void ao_attn_gqa(const uint16_t *q, int64_t q_rows, const uint16_t *keys, int64_t keys_cols,
+                 const uint16_t *values, int64_t values_cols, uint16_t *out, int64_t out_rows,
+                 int64_t seq_len, int64_t head_dim, int64_t nq, int64_t nkv) {
+    if (seq_len <= 0 || q_rows != 1 || out_rows != 1) return;
+    if (nq <= 0 || nkv <= 0 || head_dim <= 0) return;
+    if (nq % nkv != 0) return;
+    const int64_t per_kv = nq / nkv;
+    const float scale = (float)(1.0 / pow((double)head_dim, 0.5));
+    for (int64_t h = 0; h < nq; h++) {
+        const int64_t g = h / per_kv;
+        const uint16_t *qh = q + h * head_dim;
+        uint16_t *o = out + h * head_dim;
+        for (int64_t d = 0; d < head_dim; d++) o[d] = 0;
+        float running_max = -1e20f, running_sum = 0.0f;
+        for (int64_t p = 0; p < seq_len; p++) {
+            const uint16_t *kp = keys + p * keys_cols + g * head_dim;
+            const uint16_t *vp = values + p * values_cols + g * head_dim;
+            float score = 0.0f;
+            for (int64_t d = 0; d < head_dim; d++) score += H2F(qh[d]) * H2F(kp[d]);
+            score *= scale;
+            float next_max = running_max > score ? running_max : score;
+            float prev_scale = expf(running_max - next_max);
+            float prob = expf(score - next_max);
+            float next_sum = running_sum * prev_scale + prob;
+            for (int64_t d = 0; d < head_dim; d++) {
+                float prev = H2F(o[d]);
+                o[d] = F2H(prev * prev_scale + prob * H2F(vp[d]));
+            }
+            running_max = next_max;
+            running_sum = next_sum;
+        }
+        for (int64_t d = 0; d < head_dim; d++) o[d] = F2H(H2F(o[d]) / running_sum);
+    }
+}
+
+/* silu, compute.mojo:2113-2126: x * (1 / (1 + exp(-x))) with every op in f16. Mojo's exp on f16
+ * evaluates in f32 and rounds to f16; expf stands in for it here. */
+void ao_silu_f16(uint16_t *T, int64_t size) {
+    if (size <= 0) return;
+    const uint16_t one = 0x3c00;
+    for (int64_t i = 0; i < size; i++) {
+        uint16_t x = T[i];
+        uint16_t e = F2H(expf(-H2F(x)));
+        uint16_t sig = hdiv(one, hadd(one, e));
+        T[i] = hmul(x, sig);
+    }
+}
+
+/* SwiGLU product, inference.mojo:257-260: up[i] = f16(up[i] * gate[i]). */
+void ao_mul_f16(uint16_t *up, const uint16_t *gate, int64_t size) {
+    for (int64_t i = 0; i < size; i++) up[i] = hmul(up[i], gate[i]);
+}
+
+/* Residual add, inference.mojo:230-232 and :271-273: x = f16(x + residual). */
+void ao_residual_add_f16(uint16_t *x, const uint16_t *residual, int64_t size) {
+    for (int64_t i = 0; i < size; i++) x[i] = hadd(x[i], residual[i]);
+}
+
+/* Argmax, inference.mojo:508-515: floor f16(-10000), strict '>', first maximal index wins,
+ * NaN never selected, 0 when nothing exceeds the floor. */
+int64_t ao_argmax_f16(const uint16_t *logits, int64_t n) {
+    float max_val = H2F(F2H(-10000.0f));
+    int64_t best = 0;
+    for (int64_t i = 0; i < n; i++) {
+        float v = H2F(logits[i]);
+        if (v > max_val) {
+            max_val = v;
+            best = i;
+        }
+    }
+    return best;
+}
+
+/* sanitize_logit, sampler.mojo:9-14 */
+static float sanitize_logit(float v) { return (isnan(v) || isinf(v)) ? -1e9f : v; }
+
+/* Greedy branch of sample_token_from_logits, sampler.mojo:241-261. */
+int64_t ao_greedy_sample_f16(const uint16_t *logits, int64_t n, const int64_t *suppress, int64_t n_suppress) {
+    if (n <= 0) return 0;
+    int64_t best = 0;
+    float max_val = sanitize_logit(H2F(logits[0]));
+    for (int64_t s = 0; s < n_suppress; s++)
+        if (suppress[s] == 0) {
+            max_val = -1e9f;
+            break;
+        }
+    for (int64_t i = 1; i < n; i++) {
+        float v = sanitize_logit(H2F(logits[i]));
+        for (int64_t s = 0; s < n_suppress; s++)
+            if (suppress[s] == i) {
+                v = -1e9f;
+                break;
+            }
+        if (v > max_val) {
+            max_val = v;
+            best = i;
+        }
+    }
+    return best;
+}
+
+/* GGUF block_q8_0: { f16 d; int8 qs[32]; } packed, 34 bytes. */
+#define Q8_0_BLOCK_BYTES 34
+
+static inline uint16_t q8_0_weight(const uint8_t *blk, int i) {
+    uint16_t d;
+    memcpy(&d, blk, 2);
+    int8_t q = (int8_t)blk[2 + i];
+    return hmul(F2H((float)q), d); /* Scalar[f16](qs[i]) * scale, compute.mojo:1057-1063 */
+}
+
+/* dequantize_q8_0, compute.mojo:343-353 */
+void ao_dequantize_q8_0(const uint8_t *blocks, uint16_t *out, int64_t n_blocks) {
+    for (int64_t b = 0; b < n_blocks; b++)
+        for (int i = 0; i < 32; i++) out[b * 32 + i] = q8_0_weight(blocks + b * Q8_0_BLOCK_BYTES, i);
+}
+
+/* gemm_q8_0, compute.mojo:1038-1065: per-element f32 products accumulated sequentially. */
+int ao_gemm_q8_0(const uint16_t *A, int64_t a_rows, int64_t a_cols, const uint8_t *blocks, int64_t b_rows,
+                 uint16_t *C, int64_t c_rows, int64_t c_cols) {
+    if (a_rows <= 0 || a_cols <= 0 || b_rows <= 0)
+        return ao_fail(AO_ERR_INVALID, "gemm_q8_0: matrix dimensions must be positive");
+    if (a_cols % 32 != 0) return ao_fail(AO_ERR_SHAPE, "gemm_q8_0: inner dimension must be a multiple of 32");
+    if (c_rows != a_rows || c_cols != b_rows) return ao_fail(AO_ERR_SHAPE, "gemm_q8_0: output matrix shape mismatch");
+    const int64_t K = a_cols, bpr = K / 32;
+    for (int64_t row = 0; row < a_rows; row++) {
+        for (int64_t n = 0; n < b_rows; n++) {
+            float sum = 0.0f;
+            for (int64_t b = 0; b < bpr; b++) {
+                const uint8_t *blk = blocks + (n * bpr + b) * Q8_0_BLOCK_BYTES;
+                for (int i = 0; i < 32; i++) sum += H2F(A[row * K + b * 32 + i]) * H2F(q8_0_weight(blk, i));
+            }
+            C[row * b_rows + n] = F2H(sum);
+        }
+    }
+    return AO_OK;
+}
+
+/* ------------------------------------------------------------------ KV cache */
+
+/* KVCache.append, mimir_well.mojo:488-501 */
+int ao_kv_append(ao_kv *kv, int64_t layer, int64_t pos, const uint16_t *key, int64_t key_size,
+                 const uint16_t *val, int64_t val_size) {
+    if (layer < 0 || layer >= kv->num_layers) return ao_fail(AO_ERR_INVALID, "KVCache.append: layer_idx out of bounds");
+    if (pos < 0) return ao_fail(AO_ERR_INVALID, "KVCache.append: pos must be non-negative");
+    if (key_size < kv->kv_dim || val_size < kv->kv_dim) return ao_fail(AO_ERR_SHAPE, "KVCache.append: key/val width mismatch");
+    int64_t slot = pos % kv->max_seq;
+    int64_t off = (layer * kv->max_seq + slot) * kv->kv_dim;
+    memcpy(kv->k + off, key, (size_t)kv->kv_dim * 2);
+    memcpy(kv->v + off, val, (size_t)kv->kv_dim * 2);
+    return AO_OK;
+}
+
+/* KVCache.get_k_slice / get_v_slice, mimir_well.mojo:503-521 */
+int ao_kv_slice(const ao_kv *kv, int64_t layer, int64_t seq_len, const uint16_t **k_out, const uint16_t **v_out) {
+    if (layer < 0 || layer >= kv->num_layers) return ao_fail(AO_ERR_INVALID, "KVCache.get_k_slice: layer_idx out of bounds");
+    if (seq_len <= 0 || seq_len > kv->max_seq) return ao_fail(AO_ERR_INVALID, "KVCache.get_k_slice: seq_len out of bounds");
+    int64_t off = layer * kv->max_seq * kv->kv_dim;
+    *k_out = kv->k + off;
+    *v_out = kv->v + off;
+    return AO_OK;
+}
+
+/* ------------------------------------------------------------------ forward pass */
+
+int64_t ao_forward_scratch_elems(const ao_config *c) {
+    int64_t kvd = (c->dim / c->n_heads) * c->n_kv_heads;
+    /* x, residual, q, k, v, attn_out, up, gate, logits (inference.mojo:166-259, 458-503) */
+    return 4 * c->dim + 2 * kvd + 2 * c->ffn + c->vocab + 64;
+}
+
+/* TransformerBlock.forward single-device path, inference.mojo:162-275. */
+static int block_forward(const ao_model *m, int64_t l, uint16_t *x, ao_kv *kv, int64_t start_pos, uint16_t *ws) {
+    const ao_config *c = &m->cfg;
+    const int64_t dim = c->dim, hd = dim / c->n_heads, kvd = hd * c->n_kv_heads, ffn = c->ffn;
+    uint16_t *residual = ws;
+    uint16_t *q = residual + dim;
+    uint16_t *k = q + dim;
+    uint16_t *v = k + kvd;
+    uint16_t *attn = v + kvd;
+    uint16_t *up = attn + dim;
+    uint16_t *gate = up + ffn;
+    int rc;
+    memcpy(residual, x, (size_t)dim * 2);                                  /* :166-169 */
+    if ((rc = ao_rmsnorm_f16(x, 1, dim, m->attn_norm[l], dim, c->eps))) return rc; /* :171 */
+    if ((rc = ao_gemm_f16(x, 1, dim, m->wq[l], dim, dim, q, 1, dim))) return rc;   /* :194-196 */
+    if ((rc = ao_gemm_f16(x, 1, dim, m->wk[l], kvd, dim, k, 1, kvd))) return rc;
+    if ((rc = ao_gemm_f16(x, 1, dim, m->wv[l], kvd, dim, v, 1, kvd))) return rc;
+    if ((rc = ao_rope_f16(q, 1, dim, k, 1, kvd, start_pos, hd, c->theta))) return rc; /* :200 */
+    if ((rc = ao_kv_append(kv, l, start_pos, k, kvd, v, kvd))) return rc;            /* :203 */
+    int64_t active = start_pos + 1 < kv->max_seq ? start_pos + 1 : kv->max_seq;     /* :204 */
+    const uint16_t *ks, *vs;
+    if ((rc = ao_kv_slice(kv, l, active, &ks, &vs))) return rc;
+    ao_attn_gqa(q, 1, ks, kvd, vs, kvd, attn, 1, active, hd, c->n_heads, c->n_kv_heads); /* :210-219 */
+    if ((rc = ao_gemm_f16(attn, 1, dim, m->wo[l], dim, dim, x, 1, dim))) return rc;    /* :227 */
+    ao_residual_add_f16(x, residual, dim);                                             /* :231-232 */
+    memcpy(residual, x, (size_t)dim * 2);                                              /* :235-236 */
+    if ((rc = ao_rmsnorm_f16(x, 1, dim, m->ffn_norm[l], dim, c->eps))) return rc;     /* :238 */
+    if ((rc = ao_gemm_f16(x, 1, dim, m->w_up[l], ffn, dim, up, 1, ffn))) return rc;   /* :254-255 */
+    if ((rc = ao_gemm_f16(x, 1, dim, m->w_gate[l], ffn, dim, gate, 1, ffn))) return rc;
+    ao_silu_f16(gate, ffn);                                                            /* :258 */
+    ao_mul_f16(up, gate, ffn);                                                         /* :259-260 */
+    if ((rc = ao_gemm_f16(up, 1, ffn, m->w_down[l], dim, ffn, x, 1, dim))) return rc; /* :268 */
+    ao_residual_add_f16(x, residual, dim);                                             /* :272-273 */
+    return AO_OK;
+}
+
+/* forward_pass, inference.mojo:424-518. */
+int ao_forward_partial(const ao_model *m, ao_kv *kv, const int64_t *tokens, int64_t n_tokens, int64_t start_pos,
+                       int64_t n_layers_run, uint16_t *scratch, uint16_t *logits_out, int64_t *next_token) {
+    const ao_config *c = &m->cfg;
+    if (n_tokens == 0) { /* :446-447 */
+        *next_token = 0;
+        return AO_OK;
+    }
+    int64_t idx = start_pos < 0 ? 0 : start_pos; /* :449-450 */
+    if (idx > n_tokens - 1) idx = n_tokens - 1;
+    int64_t tok = tokens[idx];
+    if (tok < 0 || tok >= c->vocab) return ao_fail(AO_ERR_INVALID, "Prompt token ID is outside the embedding vocabulary");
+    uint16_t *x = scratch;
+    uint16_t *ws = x + c->dim;
+    memcpy(x, m->token_embd + tok * c->dim, (size_t)c->dim * 2); /* :461-467 */
+    int rc;
+    for (int64_t l = 0; l < n_layers_run; l++)
+        if ((rc = block_forward(m, l, x, kv, start_pos, ws))) return rc;
+    float eps = c->eps > 0.0f ? c->eps : 1e-5f; /* :484-488 */
+    if ((rc = ao_rmsnorm_f16(x, 1, c->dim, m->output_norm, c->dim, eps))) return rc;
+    uint16_t *logits = ws; /* the per-layer workspace is released by then (:275) */
+    if ((rc = ao_gemm_f16(x, 1, c->dim, m->output, c->vocab, c->dim, logits, 1, c->vocab))) return rc; /* :495-505 */
+    if (logits_out) memcpy(logits_out, logits, (size_t)c->vocab * 2);
+    *next_token = ao_argmax_f16(logits, c->vocab); /* :508-515 */
+    return AO_OK;
+}
+
+int ao_forward_pass(const ao_model *m, ao_kv *kv, const int64_t *tokens, int64_t n_tokens, int64_t start_pos,
+                    uint16_t *scratch, uint16_t *logits_out, int64_t *next_token) {
+    return ao_forward_partial(m, kv, tokens, n_tokens, start_pos, m->cfg.n_layers, scratch, logits_out, next_token);
+}
+
+/* generation_stop_reason, aesir.mojo:195-212. Returns -1 to continue. */
+int ao_generation_stop_reason(int64_t token, int64_t eos, int64_t generated_count, int64_t max_new,
+                              const int64_t *stop_tokens, int64_t n_stop, int64_t next_position, int64_t ctx_len) {
+    if (eos >= 0 && token == eos) return 0;
+    for (int64_t i = 0; i < n_stop; i++)
+        if (stop_tokens[i] == token) return 1;
+    if (generated_count >= max_new) return 2;
+    if (next_position >= ctx_len) return 3;
+    return -1;
+}
+
+/* AesirEngine._run_generation, aesir.mojo:323-462 (token IDs in and out; no text side). */
+int ao_generate(const ao_model *m, ao_kv *kv, const int64_t *prompt, int64_t n_prompt, int64_t max_new, int64_t eos,
+                const int64_t *stop_tokens, int64_t n_stop, uint16_t *scratch, int64_t *out_tokens, int64_t *n_out,
+                int32_t *stop_reason, uint16_t *last_logits) {
+    const int64_t ctx_len = m->cfg.ctx_len;
+    *n_out = 0;
+    if (max_new <= 0) return ao_fail(AO_ERR_INVALID, "GenerationConfig max_new_tokens must be a positive integer");
+    if (max_new > ctx_len) return ao_fail(AO_ERR_INVALID, "GenerationConfig max_new_tokens exceeds context_length boundary");
+    if (n_prompt <= 0) return ao_fail(AO_ERR_INVALID, "RuneWeaver produced no prompt tokens");
+    if (n_prompt > ctx_len) return ao_fail(AO_ERR_INVALID, "Prompt token count exceeds the model context length");
+    int64_t *current = (int64_t *)malloc(sizeof(int64_t) * (size_t)(n_prompt + max_new + 1));
+    if (!current) return ao_fail(AO_ERR_EXHAUSTED, "oracle: host allocation failed");
+    memcpy(current, prompt, sizeof(int64_t) * (size_t)n_prompt);
+    int64_t n_cur = n_prompt, next = 0;
+    int rc = AO_OK;
+    for (int64_t p = 0; p < n_prompt; p++) /* prefill by position, :358-374 */
+        if ((rc = ao_forward_pass(m, kv, current, n_cur, p, scratch, last_logits, &next))) goto done;
+    int reason = -1;
+    for (int64_t it = 0; it < max_new; it++) { /* :381-445 */
+        out_tokens[(*n_out)++] = next;
+        current[n_cur++] = next;
+        if (next == eos) {
+            reason = 0;
+            break;
+        }
+        int is_stop = 0;
+        for (int64_t s = 0; s < n_stop; s++) is_stop |= stop_tokens[s] == next;
+        if (is_stop) {
+            reason = 1;
+            break;
+        }
+        int64_t next_position = n_cur - 1;
+        reason = ao_generation_stop_reason(next, eos, *n_out, max_new, stop_tokens, n_stop, next_position, ctx_len);
+        if (reason >= 0) break;
+        if ((rc = ao_forward_pass(m, kv, current, n_cur, next_position, scratch, last_logits, &next))) goto done;
+    }
+    if (reason < 0) reason = 2;
+    *stop_reason = reason;
+done:
+    free(current);
+    return rc;
+}
+
+/* ------------------------------------------------------------------ synthetic inputs */
+
+static inline uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    return z ^ (z >> 31);
+}
+
+/* RuneRNG.next_u64, sampler.mojo:34-37: the state itself is advanced through the mixer. */
+uint64_t ao_rune_rng_next(uint64_t *state) {
+    uint64_t s = *state;
+    s = (s ^ (s >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    s = (s ^ (s >> 27)) * 0x94D049BB133111EBULL;
+    *state = s;
+    return s ^ (s >> 31);
+}
+
+#define GOLDEN 0x9E3779B97F4A7C15ULL
+
+/* Counter-based normal: element i of (seed, stream) from two mixer outputs, Box-Muller in f64.
+ * The same formula runs on the device for weights too large to generate on the host. */
+static double normal_at(uint64_t base, int64_t i) {
+    uint64_t a = mix64(base + (uint64_t)(2 * i + 1) * GOLDEN);
+    uint64_t b = mix64(base + (uint64_t)(2 * i + 2) * GOLDEN);
+    double u1 = (double)((a >> 40) + 1) * (1.0 / 16777216.0); /* (0, 1] */
+    double u2 = (double)(b >> 40) * (1.0 / 16777216.0);       /* [0, 1) */
+    return sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+}
+
+void ao_fill_normal_f32(float *dst, int64_t n, uint64_t seed, uint64_t stream, float mean, float std) {
+    uint64_t base = mix64(seed ^ mix64(stream + GOLDEN));
+    for (int64_t i = 0; i < n; i++) dst[i] = (float)((double)mean + (double)std * normal_at(base, i));
+}
+
+void ao_fill_normal_f16(uint16_t *dst, int64_t n, uint64_t seed, uint64_t stream, float mean, float std) {
+    uint64_t base = mix64(seed ^ mix64(stream + GOLDEN));
+    for (int64_t i = 0; i < n; i++) dst[i] = F2H((float)((double)mean + (double)std * normal_at(base, i)));
+}

@@ -1,0 +1,251 @@
+/*
+ * aesir_hip.h -- C ABI of libaesir_hip.so, the MI355X (gfx950) implementation of A.E.S.I.R.'s
+ * Llama F16 forward path.
+ *
+ * Plain C: opaque handles, raw device pointers, int64 sizes, float scalars. No C++ or torch
+ * types cross this boundary, so Mojo's external_call, ctypes, cgo or JNI can bind it directly.
+ *
+ * Every function returns int32_t: 0 (AESIR_OK) on success or a negative AESIR_ERR_* code, with
+ * the message in aesir_last_error(). Where the reference raises, the message text is the
+ * reference's own (paths below are relative to the reference repo's aesir_engine/ directory).
+ * Where the reference returns silently on invalid input (flash_attention_gqa, silu), the call
+ * returns AESIR_OK and leaves its output untouched.
+ *
+ * Ordering: all device work of one context runs in order on that context's single HIP stream.
+ * Calls return after enqueueing, except those that hand a value back to the host
+ * (aesir_argmax_f16, aesir_forward_pass, aesir_generate, aesir_memcpy_d2h,
+ * aesir_ctx_synchronize), which wait for the stream. A context is not thread-safe, like the
+ * reference engine (core/thread_pool.mojo:23-29 is a stub; nothing runs in parallel).
+ */
+#ifndef AESIR_HIP_H
+#define AESIR_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AESIR_ABI_VERSION 1
+
+#define AESIR_OK 0
+#define AESIR_ERR_INVALID (-1)     /* invalid argument: non-positive dims, bad index, bad eps */
+#define AESIR_ERR_SHAPE (-2)       /* shape mismatch between operands */
+#define AESIR_ERR_EXHAUSTED (-3)   /* "MimirWell: memory pool exhausted" */
+#define AESIR_ERR_HIP (-4)         /* HIP runtime failure (message names the call) */
+#define AESIR_ERR_FORMAT (-5)      /* GGUF contract violation */
+#define AESIR_ERR_IO (-6)          /* file open / mmap failure */
+#define AESIR_ERR_UNSUPPORTED (-7) /* shape this build does not implement (message says which) */
+
+/* GGML tensor type ids accepted by aesir_model_set_tensor (loader/gguf.mojo:17-19). */
+#define AESIR_GGML_F32 0
+#define AESIR_GGML_F16 1
+
+/* GPURealmType.AMD_ROCM_HIP (core/mimir_well.mojo:99): the realm id this library serves. */
+#define AESIR_REALM_AMD_ROCM_HIP 1
+
+typedef struct aesir_ctx aesir_ctx;
+typedef struct aesir_kv aesir_kv;
+typedef struct aesir_model aesir_model;
+
+/* Thread-local message of the last failing call on this thread (empty string if none). */
+const char *aesir_last_error(void);
+int32_t aesir_abi_version(void);
+
+/* ======================================================================= context + arena
+ * One context = one GPU, one HIP stream and one hipMalloc'd HBM arena (the MimirWell).
+ * Replaces MimirWell.__init__ (core/mimir_well.mojo:533-541), which allocates and zeroes a host
+ * pool; here the pool is device memory, zeroed at creation. */
+int32_t aesir_ctx_create(int32_t device, int64_t well_bytes, aesir_ctx **out);
+int32_t aesir_ctx_destroy(aesir_ctx *ctx);
+int32_t aesir_ctx_synchronize(aesir_ctx *ctx);
+/* The context's hipStream_t, for callers that interleave their own work. */
+void *aesir_ctx_stream(aesir_ctx *ctx);
+/* Device name (e.g. "gfx950"), compute-unit count and HBM bytes of the context's GPU. */
+int32_t aesir_ctx_device_info(aesir_ctx *ctx, char *arch_out, int32_t arch_cap, int32_t *cu_count,
+                              int64_t *hbm_bytes);
+
+/* MimirWell.allocate (core/mimir_well.mojo:543-551): bump-allocates `elements` f16 elements
+ * (2 bytes each, 256-byte aligned) and returns a device pointer. Raises
+ * "MimirWell: allocation count must be positive" / "MimirWell: memory pool exhausted". */
+int32_t aesir_well_allocate(aesir_ctx *ctx, int64_t elements, void **dev_ptr);
+/* MimirWell.reset_kv_cache (core/mimir_well.mojo:562-566): "MimirWell: invalid reset offset". */
+int32_t aesir_well_reset(aesir_ctx *ctx, int64_t offset);
+/* MimirWell.offset / .capacity, in f16 elements (core/mimir_well.mojo:529-531). */
+int64_t aesir_well_offset(const aesir_ctx *ctx);
+int64_t aesir_well_capacity(const aesir_ctx *ctx);
+
+/* Host<->device copies on the context stream (the reference's AMDGate.memcpy_* hooks,
+ * core/amd_gate.mojo:71-111, which are no-ops there). d2h waits for completion. */
+int32_t aesir_memcpy_h2d(aesir_ctx *ctx, void *dev_dst, const void *host_src, int64_t bytes);
+int32_t aesir_memcpy_d2h(aesir_ctx *ctx, void *host_dst, const void *dev_src, int64_t bytes);
+int32_t aesir_memcpy_d2d(aesir_ctx *ctx, void *dev_dst, const void *dev_src, int64_t bytes);
+
+/* HIP-event timer on the context stream: start, then stop returns elapsed milliseconds. */
+int32_t aesir_timer_start(aesir_ctx *ctx);
+int32_t aesir_timer_stop(aesir_ctx *ctx, float *elapsed_ms);
+
+/* ======================================================================= kernels
+ * Tensors are RuneTensor views {device ptr, rows, cols}, row-major, f16 unless stated
+ * (core/mimir_well.mojo:379-430). */
+
+/* gemm_f16 (core/compute.mojo:1751-1854) and the AMD realm hook gemm_f16_gpu(...,
+ * AMD_ROCM_HIP) -> AMDGate.launch_gemm_amd (core/compute.mojo:2554-2556,
+ * core/amd_gate.mojo:113-167). C[m,n] = f16(sum_k f32(A[m,k]) * f32(B[n,k])), f32 accumulation.
+ * Raises "gemm_f16: matrix dimensions must be positive", "gemm_f16: inner matrix dimension
+ * mismatch", "gemm_f16: output matrix shape mismatch". */
+int32_t aesir_gemm_f16(aesir_ctx *ctx, const void *A, int64_t a_rows, int64_t a_cols, const void *B,
+                       int64_t b_rows, int64_t b_cols, void *C, int64_t c_rows, int64_t c_cols);
+
+/* rmsnorm (core/compute.mojo:2166-2204), in place on T [rows x cols]; weight has weight_size
+ * elements. Raises "rmsnorm: tensor dimensions must be positive", "rmsnorm: weight dimension
+ * mismatch", "rmsnorm: epsilon must be positive". */
+int32_t aesir_rmsnorm_f16(aesir_ctx *ctx, void *T, int64_t rows, int64_t cols, const void *weight,
+                          int64_t weight_size, float epsilon);
+
+/* apply_rope (core/compute.mojo:2207-2244), in place on Q and K, adjacent-pair rotation,
+ * row r at position start_pos + r. Raises the reference's four messages, plus
+ * "apply_rope: K rows must cover Q rows" where the reference would index K out of bounds. */
+int32_t aesir_rope_f16(aesir_ctx *ctx, void *Q, int64_t q_rows, int64_t q_cols, void *K, int64_t k_rows,
+                       int64_t k_cols, int64_t start_pos, int64_t head_dim, float theta);
+
+/* flash_attention_gqa (core/compute.mojo:1950-2015): one query row, keys/values views of
+ * seq_len rows with row strides keys_cols/values_cols. Invalid inputs (seq_len <= 0, rows != 1,
+ * counts <= 0, nq % nkv != 0) return AESIR_OK with output untouched, as the reference does.
+ * head_dim above 256 returns AESIR_ERR_UNSUPPORTED. Split-KV with an fp32 online softmax. */
+int32_t aesir_attn_gqa_decode(aesir_ctx *ctx, const void *query, int64_t query_rows, const void *keys,
+                              int64_t keys_cols, const void *values, int64_t values_cols, void *output,
+                              int64_t output_rows, int64_t seq_len, int64_t head_dim, int64_t nq,
+                              int64_t nkv);
+
+/* silu (core/compute.mojo:2113-2126), in place; size <= 0 is a no-op. */
+int32_t aesir_silu_f16(aesir_ctx *ctx, void *T, int64_t size);
+/* SwiGLU as TransformerBlock.forward does it (core/inference.mojo:258-260): silu(gate) in
+ * place, then up[i] = f16(up[i] * gate[i]). */
+int32_t aesir_swiglu_f16(aesir_ctx *ctx, void *up, void *gate, int64_t size);
+/* Residual add (core/inference.mojo:231-232, 272-273): x[i] = f16(x[i] + residual[i]). */
+int32_t aesir_residual_add_f16(aesir_ctx *ctx, void *x, const void *residual, int64_t size);
+/* Embedding row copy (core/inference.mojo:452-467): x = table[token]. Raises "Prompt token ID is
+ * outside the embedding vocabulary". */
+int32_t aesir_embed_f16(aesir_ctx *ctx, const void *table, int64_t vocab, int64_t dim, int64_t token,
+                        void *x);
+/* Greedy argmax (core/inference.mojo:508-515): floor f16(-10000), strict '>', lowest index
+ * wins ties, NaN never chosen, 0 if nothing exceeds the floor. Waits; result in *index. */
+int32_t aesir_argmax_f16(aesir_ctx *ctx, const void *logits, int64_t n, int64_t *index);
+
+/* gemm_q8_0 (core/compute.mojo:1038-1065) reached through gemm_f16's quant dispatch (:1776-1778):
+ * B is b_rows x a_cols weights as GGUF block_q8_0 {f16 d; int8 qs[32]} (34 bytes, packed).
+ * w = f16(f16(q) * d); C = f16(sum f32(A) * f32(w)). a_cols must be a multiple of 32. */
+int32_t aesir_gemm_q8_0(aesir_ctx *ctx, const void *A, int64_t a_rows, int64_t a_cols, const void *blocks,
+                        int64_t b_rows, void *C, int64_t c_rows, int64_t c_cols);
+/* Q8_0 block matvec with f32 activations and f32 output: y[n] = sum_k x[k] * d*q (f32 math). */
+int32_t aesir_q8_0_matvec_f32(aesir_ctx *ctx, const void *blocks, int64_t n_rows, int64_t k, const float *x,
+                              float *y);
+
+/* ======================================================================= KV cache
+ * KVCache (core/mimir_well.mojo:434-521): K and V each [num_layers][max_seq_len][hidden_dim]
+ * f16, carved from the context's well. */
+int32_t aesir_kv_create(aesir_ctx *ctx, int64_t max_seq_len, int64_t hidden_dim, int64_t num_layers,
+                        aesir_kv **out);
+int32_t aesir_kv_destroy(aesir_kv *kv); /* frees the descriptor; the memory belongs to the well */
+/* KVCache.append (:488-501): writes key/val rows at slot pos % max_seq_len. */
+int32_t aesir_kv_append(aesir_ctx *ctx, aesir_kv *kv, int64_t layer_idx, int64_t pos, const void *key,
+                        int64_t key_size, const void *val, int64_t val_size);
+/* KVCache.get_k_slice / get_v_slice (:503-521): device pointer of row 0 of the layer. */
+int32_t aesir_kv_k_slice(const aesir_kv *kv, int64_t layer_idx, int64_t seq_len, void **dev_ptr);
+int32_t aesir_kv_v_slice(const aesir_kv *kv, int64_t layer_idx, int64_t seq_len, void **dev_ptr);
+
+/* ======================================================================= model + engine */
+typedef struct {
+    int64_t dim;        /* llama.embedding_length */
+    int64_t n_layers;   /* llama.block_count */
+    int64_t n_heads;    /* llama.attention.head_count */
+    int64_t n_kv_heads; /* llama.attention.head_count_kv */
+    int64_t ffn;        /* llama.feed_forward_length */
+    int64_t vocab;      /* rows of token_embd.weight */
+    int64_t ctx_len;    /* llama.context_length: KV cache rows */
+    float rms_eps;      /* llama.attention.layer_norm_rms_epsilon (default 1e-5) */
+    float rope_theta;   /* the reference always applies 10000 (core/inference.mojo:200) */
+    int64_t bos_token_id;
+    int64_t eos_token_id;
+} aesir_model_config;
+
+/* Lays out one model in the well: f16 weights (Q/K/V rows concatenated, gate/up rows
+ * interleaved), norms, KV cache [layers][ctx_len][kv_dim] x2, decode workspace. The weights
+ * start zeroed. Validates the GGUFModelConfig contract (loader/gguf.mojo:133-149). */
+int32_t aesir_model_create(aesir_ctx *ctx, const aesir_model_config *cfg, aesir_model **out);
+int32_t aesir_model_destroy(aesir_model *model);
+int32_t aesir_model_get_config(const aesir_model *model, aesir_model_config *cfg);
+/* Uploads one tensor by its GGUF name ("token_embd.weight", "blk.N.attn_q.weight", ...),
+ * host data in GGUF order (rows x cols, cols fastest). F32 tensors are rounded to f16 as
+ * loader/gguf.mojo:486-493 does. Shape and type are checked against
+ * _validate_required_tensors (loader/gguf.mojo:567-628) with its messages. */
+int32_t aesir_model_set_tensor(aesir_model *model, const char *name, const void *host_data, int64_t rows,
+                               int64_t cols, int32_t ggml_type);
+/* Reads a tensor back in GGUF order as f16 (for verification). */
+int32_t aesir_model_get_tensor(aesir_model *model, const char *name, void *host_out, int64_t elements);
+/* Device-side seeded random init: every weight N(0, std), every norm N(norm_mean, norm_std),
+ * rounded to f16; element i of tensor t uses the same counter-based Box-Muller stream as the
+ * test oracle's generator. For models too large to build on the host. */
+int32_t aesir_model_init_random(aesir_model *model, uint64_t seed, float std, float norm_mean, float norm_std);
+/* GGUFSeer.mmap_and_load (loader/gguf.mojo:664-690) + AesirEngine.__init__'s layer setup
+ * (aesir.mojo:237-296): parses a GGUF v3 Llama F16 file, enforces the reference loader
+ * contract, creates the model (KV rows = ctx_len_override if > 0, else llama.context_length)
+ * and uploads every tensor into HBM. */
+int32_t aesir_model_load_gguf(aesir_ctx *ctx, const char *path, int64_t ctx_len_override, aesir_model **out);
+
+/* GGUFSeer.inspect_metadata (loader/gguf.mojo:649-662), extended to the tensor table: parses and
+ * validates a GGUF v3 file against the same contract as aesir_model_load_gguf (header, metadata,
+ * tokenizer arrays, required tensors with shapes and types) without touching a GPU, and fills
+ * *cfg (ctx_len = llama.context_length, rope_theta = 10000 as the reference applies).
+ * *rope_freq_base receives llama.rope.freq_base when present (else 10000). */
+int32_t aesir_gguf_inspect(const char *path, aesir_model_config *cfg, float *rope_freq_base);
+
+/* forward_pass (core/inference.mojo:424-518): evaluates tokens[min(max(0,start_pos),n-1)] at
+ * position start_pos through all layers (appending K/V at start_pos), then output norm, lm_head
+ * and argmax. Waits; *next_token is the greedy token. */
+int32_t aesir_forward_pass(aesir_model *model, const int64_t *tokens, int64_t n_tokens, int64_t start_pos,
+                           int64_t *next_token);
+/* f16 logits [vocab] of the last forward pass, copied to the host. */
+int32_t aesir_model_logits(aesir_model *model, void *host_out);
+
+/* Device-autoregressive decode: starting from token at start_pos, runs n_steps forward passes
+ * back to back, each consuming the previous step's argmax on the device (one HIP graph per
+ * step when use_graph != 0). Tokens produced are copied to out_tokens[n_steps]; *elapsed_ms is
+ * the HIP-event time of the n_steps passes on the context stream. */
+int32_t aesir_decode_loop(aesir_model *model, int64_t token, int64_t start_pos, int64_t n_steps,
+                          int32_t use_graph, int64_t *out_tokens, float *elapsed_ms);
+
+/* Average per-launch device time (ms, HIP events on the context stream) of each decode-step
+ * kernel class, over `iters` eager steps at position pos. Order of times[]: 0 embed, 1 QKV+RoPE+KV,
+ * 2 attention, 3 O+residual, 4 gate/up+SwiGLU, 5 down+residual, 6 lm_head+argmax. n_times >= 7. */
+int32_t aesir_model_kernel_times(aesir_model *model, int64_t pos, int32_t iters, float *times, int32_t n_times);
+
+/* GenerationConfig subset that the token path needs (aesir.mojo:58-152). */
+typedef struct {
+    int64_t max_new_tokens;
+    const int64_t *stop_tokens;
+    int64_t n_stop_tokens;
+    int32_t batched_prefill; /* 0: prefill by position as the reference does (aesir.mojo:358-374) */
+} aesir_generation_config;
+
+/* Stop reasons of generation_stop_reason (aesir.mojo:195-212). */
+#define AESIR_STOP_EOS 0
+#define AESIR_STOP_TOKEN 1
+#define AESIR_STOP_LENGTH 2
+#define AESIR_STOP_CONTEXT_EXHAUSTED 3
+
+/* generation_stop_reason (aesir.mojo:195-212); returns -1 to continue. */
+int32_t aesir_generation_stop_reason(int64_t token, int64_t eos_token_id, int64_t generated_count,
+                                     int64_t max_new_tokens, const int64_t *stop_tokens, int64_t n_stop,
+                                     int64_t next_position, int64_t context_length);
+/* AesirEngine._run_generation (aesir.mojo:323-462) on token IDs: prefill, greedy decode loop,
+ * stop policy. out_tokens must hold max_new_tokens entries. */
+int32_t aesir_generate(aesir_model *model, const int64_t *prompt, int64_t n_prompt,
+                       const aesir_generation_config *cfg, int64_t *out_tokens, int64_t *n_out,
+                       int32_t *stop_reason);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

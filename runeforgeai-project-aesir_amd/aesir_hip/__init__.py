@@ -1,0 +1,449 @@
+"""Python host-side binding of libaesir_hip.so (ctypes over the C ABI in include/aesir_hip.h).
+
+It mirrors the reference's kernel-call and engine API (aesir_engine/core/compute.mojo,
+core/mimir_well.mojo, core/inference.mojo, aesir.mojo) with the same names, argument meaning and
+error behaviour: failing calls raise AesirError carrying the library's message, which is the
+reference's own text where the reference raises. Tensors are device buffers carved from the
+context's HBM arena (the MimirWell); numpy arrays are the host side.
+
+There is no fallback: if libaesir_hip.so is missing, importing this module raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libaesir_hip.so")
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError(f"libaesir_hip.so not built at {LIB_PATH}: run python runeforgeai-project-aesir_amd/build.py")
+
+_L = C.CDLL(LIB_PATH)
+
+P = C.c_void_p
+I64 = C.c_int64
+I32 = C.c_int32
+F32 = C.c_float
+
+
+class AesirError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(msg)
+        self.code = code
+
+
+class _ModelConfig(C.Structure):
+    _fields_ = [("dim", I64), ("n_layers", I64), ("n_heads", I64), ("n_kv_heads", I64), ("ffn", I64),
+                ("vocab", I64), ("ctx_len", I64), ("rms_eps", F32), ("rope_theta", F32),
+                ("bos_token_id", I64), ("eos_token_id", I64)]
+
+
+class _GenConfig(C.Structure):
+    _fields_ = [("max_new_tokens", I64), ("stop_tokens", P), ("n_stop_tokens", I64), ("batched_prefill", I32)]
+
+
+def _sig(name, args, res=I32):
+    f = getattr(_L, name)
+    f.argtypes = args
+    f.restype = res
+    return f
+
+
+_sig("aesir_last_error", [], C.c_char_p)
+_sig("aesir_abi_version", [])
+_sig("aesir_ctx_create", [I32, I64, C.POINTER(P)])
+_sig("aesir_ctx_destroy", [P])
+_sig("aesir_ctx_synchronize", [P])
+_sig("aesir_ctx_stream", [P], P)
+_sig("aesir_ctx_device_info", [P, C.c_char_p, I32, C.POINTER(I32), C.POINTER(I64)])
+_sig("aesir_well_allocate", [P, I64, C.POINTER(P)])
+_sig("aesir_well_reset", [P, I64])
+_sig("aesir_well_offset", [P], I64)
+_sig("aesir_well_capacity", [P], I64)
+_sig("aesir_memcpy_h2d", [P, P, P, I64])
+_sig("aesir_memcpy_d2h", [P, P, P, I64])
+_sig("aesir_memcpy_d2d", [P, P, P, I64])
+_sig("aesir_timer_start", [P])
+_sig("aesir_timer_stop", [P, C.POINTER(F32)])
+_sig("aesir_gemm_f16", [P, P, I64, I64, P, I64, I64, P, I64, I64])
+_sig("aesir_rmsnorm_f16", [P, P, I64, I64, P, I64, F32])
+_sig("aesir_rope_f16", [P, P, I64, I64, P, I64, I64, I64, I64, F32])
+_sig("aesir_attn_gqa_decode", [P, P, I64, P, I64, P, I64, P, I64, I64, I64, I64, I64])
+_sig("aesir_silu_f16", [P, P, I64])
+_sig("aesir_swiglu_f16", [P, P, P, I64])
+_sig("aesir_residual_add_f16", [P, P, P, I64])
+_sig("aesir_embed_f16", [P, P, I64, I64, I64, P])
+_sig("aesir_argmax_f16", [P, P, I64, C.POINTER(I64)])
+_sig("aesir_gemm_q8_0", [P, P, I64, I64, P, I64, P, I64, I64])
+_sig("aesir_q8_0_matvec_f32", [P, P, I64, I64, P, P])
+_sig("aesir_kv_create", [P, I64, I64, I64, C.POINTER(P)])
+_sig("aesir_kv_destroy", [P])
+_sig("aesir_kv_append", [P, P, I64, I64, P, I64, P, I64])
+_sig("aesir_kv_k_slice", [P, I64, I64, C.POINTER(P)])
+_sig("aesir_kv_v_slice", [P, I64, I64, C.POINTER(P)])
+_sig("aesir_model_create", [P, C.POINTER(_ModelConfig), C.POINTER(P)])
+_sig("aesir_model_destroy", [P])
+_sig("aesir_model_get_config", [P, C.POINTER(_ModelConfig)])
+_sig("aesir_model_set_tensor", [P, C.c_char_p, P, I64, I64, I32])
+_sig("aesir_model_get_tensor", [P, C.c_char_p, P, I64])
+_sig("aesir_model_init_random", [P, C.c_uint64, F32, F32, F32])
+_sig("aesir_model_load_gguf", [P, C.c_char_p, I64, C.POINTER(P)])
+_sig("aesir_gguf_inspect", [C.c_char_p, C.POINTER(_ModelConfig), C.POINTER(F32)])
+_sig("aesir_forward_pass", [P, P, I64, I64, C.POINTER(I64)])
+_sig("aesir_model_logits", [P, P])
+_sig("aesir_decode_loop", [P, I64, I64, I64, I32, P, C.POINTER(F32)])
+_sig("aesir_model_kernel_times", [P, I64, I32, P, I32])
+_sig("aesir_generation_stop_reason", [I64, I64, I64, I64, P, I64, I64, I64])
+_sig("aesir_generate", [P, P, I64, C.POINTER(_GenConfig), P, C.POINTER(I64), C.POINTER(I32)])
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(_HERE)), "include", "aesir_hip.h")
+
+
+def declared_functions(header: str = HEADER) -> list:
+    """Names of every function include/aesir_hip.h declares."""
+    import re
+
+    text = open(header).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(aesir_[a-z0-9_]+)\s*\(", text)))
+
+
+def missing_exports() -> list:
+    """Declared functions that the loaded library does not export (should be empty)."""
+    out = []
+    for name in declared_functions():
+        try:
+            getattr(_L, name)
+        except AttributeError:
+            out.append(name)
+    return out
+
+
+def _check(rc: int):
+    if rc != 0:
+        raise AesirError(rc, _L.aesir_last_error().decode())
+
+
+def last_error() -> str:
+    return _L.aesir_last_error().decode()
+
+
+def abi_version() -> int:
+    return _L.aesir_abi_version()
+
+
+STOP_REASONS = {0: "eos", 1: "stop_token", 2: "length", 3: "context_exhausted"}
+KERNEL_CLASSES = ["embed", "qkv_rope_kv", "attention", "o_residual", "gate_up_swiglu", "down_residual",
+                  "lm_head_argmax"]
+
+
+class Tensor:
+    """RuneTensor view: a device pointer with (rows, cols); dtype f16 unless stated."""
+
+    def __init__(self, ctx: "Context", ptr: int, rows: int, cols: int, dtype=np.float16):
+        self.ctx, self.ptr, self.rows, self.cols, self.dtype = ctx, ptr, rows, cols, np.dtype(dtype)
+
+    @property
+    def size(self) -> int:
+        return self.rows * self.cols
+
+    @property
+    def nbytes(self) -> int:
+        return self.size * self.dtype.itemsize
+
+    def numpy(self) -> np.ndarray:
+        out = np.empty((self.rows, self.cols), dtype=self.dtype)
+        if self.size:
+            _check(_L.aesir_memcpy_d2h(self.ctx.h, out.ctypes.data, self.ptr, self.nbytes))
+        return out
+
+    def upload(self, a: np.ndarray) -> "Tensor":
+        a = np.ascontiguousarray(a, dtype=self.dtype)
+        assert a.size == self.size, (a.shape, self.rows, self.cols)
+        _check(_L.aesir_memcpy_h2d(self.ctx.h, self.ptr, a.ctypes.data, self.nbytes))
+        return self
+
+    def view(self, rows: int, cols: int, offset_elems: int = 0) -> "Tensor":
+        return Tensor(self.ctx, self.ptr + offset_elems * self.dtype.itemsize, rows, cols, self.dtype)
+
+
+class Context:
+    """One GPU, one HIP stream, one HBM arena (MimirWell, core/mimir_well.mojo:524-569)."""
+
+    def __init__(self, well_bytes: int = 1 << 30, device: int = 0):
+        h = P()
+        _check(_L.aesir_ctx_create(device, int(well_bytes), C.byref(h)))
+        self.h = h.value
+
+    def close(self):
+        if self.h:
+            _L.aesir_ctx_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def device_info(self) -> dict:
+        buf = C.create_string_buffer(64)
+        cu = I32()
+        hbm = I64()
+        _check(_L.aesir_ctx_device_info(self.h, buf, 64, C.byref(cu), C.byref(hbm)))
+        return {"arch": buf.value.decode(), "cu_count": cu.value, "hbm_bytes": hbm.value}
+
+    def synchronize(self):
+        _check(_L.aesir_ctx_synchronize(self.h))
+
+    # ---- MimirWell
+    def allocate(self, elements: int) -> int:
+        p = P()
+        _check(_L.aesir_well_allocate(self.h, int(elements), C.byref(p)))
+        return p.value
+
+    @property
+    def offset(self) -> int:
+        return _L.aesir_well_offset(self.h)
+
+    @property
+    def capacity(self) -> int:
+        return _L.aesir_well_capacity(self.h)
+
+    def reset(self, offset: int):
+        _check(_L.aesir_well_reset(self.h, int(offset)))
+
+    def tensor(self, rows: int, cols: int, dtype=np.float16) -> Tensor:
+        itemsize = np.dtype(dtype).itemsize
+        elems = max(1, (rows * cols * itemsize + 1) // 2)
+        return Tensor(self, self.allocate(elems), rows, cols, dtype)
+
+    def from_numpy(self, a: np.ndarray, dtype=np.float16) -> Tensor:
+        a = np.asarray(a)
+        rows, cols = (1, a.size) if a.ndim == 1 else a.shape
+        return self.tensor(rows, cols, dtype).upload(a)
+
+    # ---- timing (HIP events on the context stream)
+    def timer_start(self):
+        _check(_L.aesir_timer_start(self.h))
+
+    def timer_stop(self) -> float:
+        ms = F32()
+        _check(_L.aesir_timer_stop(self.h, C.byref(ms)))
+        return ms.value
+
+
+# ------------------------------------------------------------------ kernel-call API
+
+def gemm_f16(ctx: Context, A: Tensor, B: Tensor, C_: Tensor):
+    """gemm_f16(A, B, C): C[m,n] = f16(sum_k A[m,k] B[n,k]) (core/compute.mojo:1751-1854)."""
+    _check(_L.aesir_gemm_f16(ctx.h, A.ptr, A.rows, A.cols, B.ptr, B.rows, B.cols, C_.ptr, C_.rows, C_.cols))
+
+
+def rmsnorm(ctx: Context, T: Tensor, weight: Tensor, epsilon: float = 1e-5):
+    _check(_L.aesir_rmsnorm_f16(ctx.h, T.ptr, T.rows, T.cols, weight.ptr, weight.size, epsilon))
+
+
+def apply_rope(ctx: Context, Q: Tensor, K: Tensor, start_pos: int, head_dim: int, theta: float = 10000.0):
+    _check(_L.aesir_rope_f16(ctx.h, Q.ptr, Q.rows, Q.cols, K.ptr, K.rows, K.cols, start_pos, head_dim, theta))
+
+
+def flash_attention_gqa(ctx: Context, query: Tensor, keys: Tensor, values: Tensor, output: Tensor,
+                        sequence_length: int, head_dim: int, query_head_count: int, kv_head_count: int):
+    _check(_L.aesir_attn_gqa_decode(ctx.h, query.ptr, query.rows, keys.ptr, keys.cols, values.ptr, values.cols,
+                                    output.ptr, output.rows, sequence_length, head_dim, query_head_count,
+                                    kv_head_count))
+
+
+def silu(ctx: Context, T: Tensor):
+    _check(_L.aesir_silu_f16(ctx.h, T.ptr, T.size))
+
+
+def swiglu(ctx: Context, up: Tensor, gate: Tensor):
+    _check(_L.aesir_swiglu_f16(ctx.h, up.ptr, gate.ptr, up.size))
+
+
+def residual_add(ctx: Context, x: Tensor, residual: Tensor):
+    _check(_L.aesir_residual_add_f16(ctx.h, x.ptr, residual.ptr, x.size))
+
+
+def embed(ctx: Context, table: Tensor, token: int, x: Tensor):
+    _check(_L.aesir_embed_f16(ctx.h, table.ptr, table.rows, table.cols, token, x.ptr))
+
+
+def argmax(ctx: Context, logits: Tensor) -> int:
+    out = I64()
+    _check(_L.aesir_argmax_f16(ctx.h, logits.ptr, logits.size, C.byref(out)))
+    return out.value
+
+
+def gemm_q8_0(ctx: Context, A: Tensor, blocks_ptr: int, b_rows: int, C_: Tensor):
+    _check(_L.aesir_gemm_q8_0(ctx.h, A.ptr, A.rows, A.cols, blocks_ptr, b_rows, C_.ptr, C_.rows, C_.cols))
+
+
+def q8_0_matvec_f32(ctx: Context, blocks_ptr: int, n_rows: int, k: int, x: Tensor, y: Tensor):
+    _check(_L.aesir_q8_0_matvec_f32(ctx.h, blocks_ptr, n_rows, k, x.ptr, y.ptr))
+
+
+class KVCache:
+    """KVCache (core/mimir_well.mojo:434-521) carved from the context's well."""
+
+    def __init__(self, ctx: Context, max_seq_len: int, hidden_dim: int, num_layers: int = 32):
+        h = P()
+        _check(_L.aesir_kv_create(ctx.h, max_seq_len, hidden_dim, num_layers, C.byref(h)))
+        self.ctx, self.h = ctx, h.value
+        self.max_seq_len, self.hidden_dim, self.num_layers = max_seq_len, hidden_dim, num_layers
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            _L.aesir_kv_destroy(self.h)
+            self.h = None
+
+    def append(self, layer_idx: int, pos: int, key: Tensor, val: Tensor):
+        _check(_L.aesir_kv_append(self.ctx.h, self.h, layer_idx, pos, key.ptr, key.size, val.ptr, val.size))
+
+    def get_k_slice(self, layer_idx: int, seq_len: int) -> Tensor:
+        p = P()
+        _check(_L.aesir_kv_k_slice(self.h, layer_idx, seq_len, C.byref(p)))
+        return Tensor(self.ctx, p.value, seq_len, self.hidden_dim)
+
+    def get_v_slice(self, layer_idx: int, seq_len: int) -> Tensor:
+        p = P()
+        _check(_L.aesir_kv_v_slice(self.h, layer_idx, seq_len, C.byref(p)))
+        return Tensor(self.ctx, p.value, seq_len, self.hidden_dim)
+
+
+# ------------------------------------------------------------------ model / engine
+
+@dataclass
+class ModelConfig:
+    dim: int
+    n_layers: int
+    n_heads: int
+    n_kv_heads: int
+    ffn: int
+    vocab: int
+    ctx_len: int
+    rms_eps: float = 1e-5
+    rope_theta: float = 10000.0
+    bos_token_id: int = 1
+    eos_token_id: int = 2
+
+    def _c(self) -> _ModelConfig:
+        return _ModelConfig(self.dim, self.n_layers, self.n_heads, self.n_kv_heads, self.ffn, self.vocab,
+                            self.ctx_len, self.rms_eps, self.rope_theta, self.bos_token_id, self.eos_token_id)
+
+
+class Model:
+    """One Llama F16 model in HBM: forward_pass (core/inference.mojo:424-518) and the generation
+    loop (aesir.mojo:323-462)."""
+
+    def __init__(self, ctx: Context, handle: int):
+        self.ctx, self.h = ctx, handle
+        c = _ModelConfig()
+        _check(_L.aesir_model_get_config(self.h, C.byref(c)))
+        self.cfg = ModelConfig(c.dim, c.n_layers, c.n_heads, c.n_kv_heads, c.ffn, c.vocab, c.ctx_len, c.rms_eps,
+                               c.rope_theta, c.bos_token_id, c.eos_token_id)
+
+    @classmethod
+    def create(cls, ctx: Context, cfg: ModelConfig) -> "Model":
+        h = P()
+        c = cfg._c()
+        _check(_L.aesir_model_create(ctx.h, C.byref(c), C.byref(h)))
+        return cls(ctx, h.value)
+
+    @classmethod
+    def load_gguf(cls, ctx: Context, path: str, ctx_len: int = 0) -> "Model":
+        h = P()
+        _check(_L.aesir_model_load_gguf(ctx.h, path.encode(), ctx_len, C.byref(h)))
+        return cls(ctx, h.value)
+
+    def close(self):
+        if self.h:
+            _L.aesir_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_tensor(self, name: str, data: np.ndarray):
+        data = np.asarray(data)
+        ggml = 0 if data.dtype == np.float32 else 1
+        data = np.ascontiguousarray(data, dtype=np.float32 if ggml == 0 else np.float16)
+        rows, cols = (1, data.size) if data.ndim == 1 else data.shape
+        _check(_L.aesir_model_set_tensor(self.h, name.encode(), data.ctypes.data, rows, cols, ggml))
+
+    def set_weights(self, weights: dict):
+        for k, v in weights.items():
+            self.set_tensor(k, v)
+
+    def get_tensor(self, name: str, shape) -> np.ndarray:
+        out = np.empty(shape, dtype=np.float16)
+        _check(_L.aesir_model_get_tensor(self.h, name.encode(), out.ctypes.data, out.size))
+        return out
+
+    def init_random(self, seed: int, std: float = 0.02, norm_mean: float = 0.0, norm_std: float = 0.02):
+        _check(_L.aesir_model_init_random(self.h, seed, std, norm_mean, norm_std))
+
+    def forward_pass(self, tokens, start_pos: int) -> int:
+        t = np.ascontiguousarray(np.array(tokens, dtype=np.int64))
+        out = I64()
+        _check(_L.aesir_forward_pass(self.h, t.ctypes.data if t.size else None, t.size, start_pos, C.byref(out)))
+        return out.value
+
+    def logits(self) -> np.ndarray:
+        out = np.empty(self.cfg.vocab, dtype=np.float16)
+        _check(_L.aesir_model_logits(self.h, out.ctypes.data))
+        return out
+
+    def decode_loop(self, token: int, start_pos: int, n_steps: int, use_graph: bool = True):
+        out = np.zeros(n_steps, dtype=np.int64)
+        ms = F32()
+        _check(_L.aesir_decode_loop(self.h, token, start_pos, n_steps, 1 if use_graph else 0, out.ctypes.data,
+                                    C.byref(ms)))
+        return out.tolist(), ms.value
+
+    def kernel_times(self, pos: int, iters: int = 10) -> dict:
+        t = np.zeros(7, dtype=np.float32)
+        _check(_L.aesir_model_kernel_times(self.h, pos, iters, t.ctypes.data, 7))
+        return dict(zip(KERNEL_CLASSES, t.tolist()))
+
+    def generate(self, prompt, max_new_tokens: int, stop_tokens=(), batched_prefill: bool = False):
+        p = np.ascontiguousarray(np.array(prompt, dtype=np.int64))
+        st = np.ascontiguousarray(np.array(list(stop_tokens) or [0], dtype=np.int64))
+        g = _GenConfig(max_new_tokens, st.ctypes.data, len(stop_tokens), 1 if batched_prefill else 0)
+        out = np.zeros(max(1, max_new_tokens), dtype=np.int64)
+        n = I64()
+        reason = I32(-1)
+        _check(_L.aesir_generate(self.h, p.ctypes.data if p.size else None, p.size, C.byref(g), out.ctypes.data,
+                                 C.byref(n), C.byref(reason)))
+        return out[: n.value].tolist(), STOP_REASONS[reason.value]
+
+
+def gguf_inspect(path: str):
+    """Validates a GGUF file without a GPU; returns (ModelConfig, rope_freq_base)."""
+    c = _ModelConfig()
+    fb = F32()
+    _check(_L.aesir_gguf_inspect(path.encode(), C.byref(c), C.byref(fb)))
+    return (ModelConfig(c.dim, c.n_layers, c.n_heads, c.n_kv_heads, c.ffn, c.vocab, c.ctx_len, c.rms_eps,
+                        c.rope_theta, c.bos_token_id, c.eos_token_id), fb.value)
+
+
+def generation_stop_reason(token, eos, generated_count, max_new, stop_tokens, next_position, ctx_len) -> str:
+    st = np.ascontiguousarray(np.array(list(stop_tokens) or [0], dtype=np.int64))
+    r = _L.aesir_generation_stop_reason(token, eos, generated_count, max_new, st.ctypes.data, len(stop_tokens),
+                                        next_position, ctx_len)
+    return STOP_REASONS.get(r, "")

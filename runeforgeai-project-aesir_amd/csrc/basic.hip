@@ -1,0 +1,188 @@
+// Elementwise and row-reduction kernels of the decode path for gfx950: standalone RMSNorm, RoPE,
+// SiLU, SwiGLU, residual add, embedding copy, KV append, and the seeded device-side init.
+// All are HBM/latency bound; every f16 rounding point of the reference is kept (see device.hpp).
+#include "device.hpp"
+#include "kernels.hpp"
+
+namespace aesir {
+
+constexpr int kEThreads = 256;
+
+static unsigned grid_for(int64_t n, int64_t per_block) {
+    int64_t g = (n + per_block - 1) / per_block;
+    if (g < 1) g = 1;
+    if (g > 1048576) g = 1048576;
+    return (unsigned)g;
+}
+
+// ------------------------------------------------------------------ rmsnorm
+// One workgroup per row (compute.mojo:2178-2204): f32 sum of squares, inv = f16(1/sqrt(ss/N+eps)),
+// x = f16(f16(x * inv) * w).
+__global__ __launch_bounds__(kEThreads) void rmsnorm_kernel(h16 *__restrict__ T, int64_t cols,
+                                                            const h16 *__restrict__ w, float eps) {
+    __shared__ float red[kEThreads / kWave];
+    h16 *x = T + (int64_t)blockIdx.x * cols;
+    float ss = 0.0f;
+    for (int64_t c = threadIdx.x; c < cols; c += kEThreads) {
+        float v = (float)x[c];
+        ss = fmaf(v, v, ss);
+    }
+    ss = block_sum<kEThreads / kWave>(ss, red);
+    const h16 inv = (h16)(1.0f / sqrtf(ss / (float)cols + eps));
+    for (int64_t c = threadIdx.x; c < cols; c += kEThreads) x[c] = hmul(hmul(x[c], inv), w[c]);
+}
+
+int32_t launch_rmsnorm(hipStream_t s, void *T, int64_t rows, int64_t cols, const void *w, float eps) {
+    if (rows > 2147483647) return fail(AESIR_ERR_UNSUPPORTED, "rmsnorm: too many rows");
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(kEThreads), 0, s, (h16 *)T, cols, (const h16 *)w, eps);
+    AESIR_LAUNCH_CHECK("rmsnorm_kernel");
+    return AESIR_OK;
+}
+
+// ------------------------------------------------------------------ rope
+// One thread per (row, pair index j, head): the reference's f16 rotation (compute.mojo:2232-2244)
+// with cos/sin from the host-built table at position start_pos + row.
+__global__ __launch_bounds__(kEThreads) void rope_kernel(h16 *__restrict__ Q, int64_t q_rows, int64_t q_cols,
+                                                         h16 *__restrict__ K, int64_t k_cols, int64_t start_pos,
+                                                         int64_t hd, const h16x2 *__restrict__ table) {
+    const int64_t half = hd / 2;
+    const int64_t pairs_q = q_cols / 2, pairs_k = k_cols / 2;
+    const int64_t per_row = pairs_q + pairs_k;
+    const int64_t total = q_rows * per_row;
+    for (int64_t i = (int64_t)blockIdx.x * kEThreads + threadIdx.x; i < total; i += (int64_t)gridDim.x * kEThreads) {
+        const int64_t r = i / per_row, e = i % per_row;
+        h16 *p = e < pairs_q ? Q + r * q_cols + 2 * e : K + r * k_cols + 2 * (e - pairs_q);
+        const int64_t col = e < pairs_q ? 2 * e : 2 * (e - pairs_q);
+        const h16x2 cs = table[(start_pos + r) * half + ((col % hd) >> 1)];
+        const h16 a = p[0], b = p[1];
+        p[0] = hsub(hmul(a, cs.x), hmul(b, cs.y));
+        p[1] = hadd(hmul(a, cs.y), hmul(b, cs.x));
+    }
+}
+
+int32_t launch_rope(hipStream_t s, void *Q, int64_t q_rows, int64_t q_cols, void *K, int64_t k_cols,
+                    int64_t start_pos, int64_t head_dim, const void *table) {
+    const int64_t total = q_rows * (q_cols / 2 + k_cols / 2);
+    hipLaunchKernelGGL(rope_kernel, dim3(grid_for(total, kEThreads)), dim3(kEThreads), 0, s, (h16 *)Q, q_rows,
+                       q_cols, (h16 *)K, k_cols, start_pos, head_dim, (const h16x2 *)table);
+    AESIR_LAUNCH_CHECK("rope_kernel");
+    return AESIR_OK;
+}
+
+// ------------------------------------------------------------------ silu / swiglu / residual
+__global__ __launch_bounds__(kEThreads) void silu_kernel(h16 *__restrict__ T, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * kEThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kEThreads)
+        T[i] = silu_h(T[i]);
+}
+
+// silu(gate) in place, then up = f16(up * gate) (inference.mojo:258-260).
+__global__ __launch_bounds__(kEThreads) void swiglu_kernel(h16 *__restrict__ up, h16 *__restrict__ gate, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * kEThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kEThreads) {
+        const h16 g = silu_h(gate[i]);
+        gate[i] = g;
+        up[i] = hmul(up[i], g);
+    }
+}
+
+__global__ __launch_bounds__(kEThreads) void residual_kernel(h16 *__restrict__ x, const h16 *__restrict__ r, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * kEThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kEThreads)
+        x[i] = hadd(x[i], r[i]);
+}
+
+int32_t launch_silu(hipStream_t s, void *T, int64_t n) {
+    hipLaunchKernelGGL(silu_kernel, dim3(grid_for(n, kEThreads)), dim3(kEThreads), 0, s, (h16 *)T, n);
+    AESIR_LAUNCH_CHECK("silu_kernel");
+    return AESIR_OK;
+}
+
+int32_t launch_swiglu(hipStream_t s, void *up, void *gate, int64_t n) {
+    hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for(n, kEThreads)), dim3(kEThreads), 0, s, (h16 *)up, (h16 *)gate, n);
+    AESIR_LAUNCH_CHECK("swiglu_kernel");
+    return AESIR_OK;
+}
+
+int32_t launch_residual_add(hipStream_t s, void *x, const void *r, int64_t n) {
+    hipLaunchKernelGGL(residual_kernel, dim3(grid_for(n, kEThreads)), dim3(kEThreads), 0, s, (h16 *)x, (const h16 *)r, n);
+    AESIR_LAUNCH_CHECK("residual_kernel");
+    return AESIR_OK;
+}
+
+// ------------------------------------------------------------------ embedding / KV append
+// x = table[token] (inference.mojo:461-467); the token comes from `state` when given (graph replay).
+__global__ __launch_bounds__(kEThreads) void embed_kernel(const h16 *__restrict__ table, int64_t dim, int64_t token,
+                                                          const DecodeState *state, h16 *__restrict__ x) {
+    const int64_t tok = state ? state->token : token;
+    const h16 *row = table + tok * dim;
+    for (int64_t i = threadIdx.x; i < dim; i += kEThreads) x[i] = row[i];
+}
+
+int32_t launch_embed(hipStream_t s, const void *table, int64_t dim, int64_t token, const DecodeState *state, void *x) {
+    hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(kEThreads), 0, s, (const h16 *)table, dim, token, state, (h16 *)x);
+    AESIR_LAUNCH_CHECK("embed_kernel");
+    return AESIR_OK;
+}
+
+__global__ __launch_bounds__(kEThreads) void kv_append_kernel(h16 *__restrict__ kc, h16 *__restrict__ vc,
+                                                              const h16 *__restrict__ k, const h16 *__restrict__ v,
+                                                              int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * kEThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kEThreads) {
+        kc[i] = k[i];
+        vc[i] = v[i];
+    }
+}
+
+int32_t launch_kv_append(hipStream_t s, void *kc, void *vc, const void *k, const void *v, int64_t n) {
+    hipLaunchKernelGGL(kv_append_kernel, dim3(grid_for(n, kEThreads)), dim3(kEThreads), 0, s, (h16 *)kc, (h16 *)vc,
+                       (const h16 *)k, (const h16 *)v, n);
+    AESIR_LAUNCH_CHECK("kv_append_kernel");
+    return AESIR_OK;
+}
+
+// ------------------------------------------------------------------ seeded init
+// Counter-based normal: element i of stream (seed, stream) from two SplitMix64-mixer outputs
+// (the RuneRNG mixer of sampler.mojo:34-37) and Box-Muller in f64, rounded to f32 then f16.
+__host__ __device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    return z ^ (z >> 31);
+}
+
+constexpr uint64_t kGolden = 0x9E3779B97F4A7C15ULL;
+
+// Element i (row i / cols, column i % cols) lands at dst[(i / cols) * dst_stride + i % cols], so a
+// tensor can be generated straight into an interleaved layout.
+__global__ __launch_bounds__(kEThreads) void fill_normal_kernel(h16 *__restrict__ dst, int64_t n, int64_t cols,
+                                                                int64_t dst_stride, uint64_t base, double mean,
+                                                                double std) {
+    for (int64_t i = (int64_t)blockIdx.x * kEThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kEThreads) {
+        const uint64_t a = mix64(base + (uint64_t)(2 * i + 1) * kGolden);
+        const uint64_t b = mix64(base + (uint64_t)(2 * i + 2) * kGolden);
+        const double u1 = (double)((a >> 40) + 1) * (1.0 / 16777216.0);
+        const double u2 = (double)(b >> 40) * (1.0 / 16777216.0);
+        const double z = sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+        dst[(i / cols) * dst_stride + i % cols] = (h16)(float)(mean + std * z);
+    }
+}
+
+int32_t launch_fill_normal(hipStream_t s, void *dst, int64_t n, int64_t cols, int64_t dst_stride, uint64_t seed,
+                           uint64_t stream, float mean, float std) {
+    const uint64_t base = mix64(seed ^ mix64(stream + kGolden));
+    hipLaunchKernelGGL(fill_normal_kernel, dim3(grid_for(n, kEThreads * 8)), dim3(kEThreads), 0, s, (h16 *)dst, n,
+                       cols, dst_stride, base, (double)mean, (double)std);
+    AESIR_LAUNCH_CHECK("fill_normal_kernel");
+    return AESIR_OK;
+}
+
+__global__ __launch_bounds__(kEThreads) void f32_to_f16_kernel(const float *__restrict__ src, h16 *__restrict__ dst,
+                                                               int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * kEThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kEThreads)
+        dst[i] = (h16)src[i];
+}
+
+int32_t launch_f32_to_f16(hipStream_t s, const float *src, void *dst, int64_t n) {
+    hipLaunchKernelGGL(f32_to_f16_kernel, dim3(grid_for(n, kEThreads)), dim3(kEThreads), 0, s, src, (h16 *)dst, n);
+    AESIR_LAUNCH_CHECK("f32_to_f16_kernel");
+    return AESIR_OK;
+}
+
+}  // namespace aesir

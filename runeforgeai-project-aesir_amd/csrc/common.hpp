@@ -1,0 +1,107 @@
+// Internal host-side definitions shared by the translation units of libaesir_hip.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+#include <vector>
+
+#include "aesir_hip.h"
+
+namespace aesir {
+
+// ------------------------------------------------------------------ errors
+
+// Records the message for aesir_last_error() and returns `code`.
+int32_t fail(int32_t code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+
+#define AESIR_HIP_TRY(expr)                                                                        \
+    do {                                                                                           \
+        hipError_t _e = (expr);                                                                    \
+        if (_e != hipSuccess)                                                                      \
+            return ::aesir::fail(AESIR_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(_e));  \
+    } while (0)
+
+#define AESIR_TRY(expr)                                                                            \
+    do {                                                                                           \
+        int32_t _rc = (expr);                                                                      \
+        if (_rc != AESIR_OK) return _rc;                                                           \
+    } while (0)
+
+// Checks the launch that was just enqueued.
+#define AESIR_LAUNCH_CHECK(name)                                                                   \
+    do {                                                                                           \
+        hipError_t _e = hipGetLastError();                                                         \
+        if (_e != hipSuccess)                                                                      \
+            return ::aesir::fail(AESIR_ERR_HIP, "launch of %s failed: %s", name, hipGetErrorString(_e)); \
+    } while (0)
+
+// ------------------------------------------------------------------ f16 on the host
+
+uint16_t f32_to_f16_bits(float f);  // round to nearest even
+float f16_bits_to_f32(uint16_t h);
+
+// ------------------------------------------------------------------ context
+
+// Cached cos/sin table for one (theta, head_dim): [n_pos][head_dim/2] pairs of f16 (cos, sin),
+// built on the host with the reference's f32 expressions (compute.mojo:2227-2230).
+struct RopeTable {
+    float theta = 0.0f;
+    int64_t head_dim = 0;
+    int64_t n_pos = 0;
+    void *dev = nullptr;
+};
+
+// Device scratch owned by the context for the standalone kernel entry points.
+struct CtxScratch {
+    void *base = nullptr;
+    int64_t bytes = 0;
+    // carved regions
+    float *attn_part = nullptr;     // attention partials (m, l, acc)
+    int64_t attn_part_floats = 0;
+    uint32_t *counters = nullptr;   // self-resetting completion counters (zeroed once)
+    int64_t n_counters = 0;
+    void *argmax_part = nullptr;    // argmax partials
+    int64_t argmax_part_entries = 0;
+    int64_t *result = nullptr;      // device int64 results
+};
+
+}  // namespace aesir
+
+struct aesir_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    char *well_base = nullptr;
+    int64_t well_capacity = 0;  // f16 elements
+    int64_t well_offset = 0;    // f16 elements
+    int cu_count = 0;
+    int64_t hbm_bytes = 0;
+    char arch[64] = {0};
+    hipEvent_t ev_start = nullptr, ev_stop = nullptr;
+    bool timer_running = false;
+    aesir::CtxScratch scratch;
+    std::vector<aesir::RopeTable> rope_tables;
+    int64_t *pinned_i64 = nullptr;  // small pinned staging area (64 entries)
+};
+
+struct aesir_kv {
+    aesir_ctx *ctx = nullptr;
+    uint16_t *k = nullptr;  // [num_layers * max_seq][hidden_dim]
+    uint16_t *v = nullptr;
+    int64_t max_seq = 0, hidden_dim = 0, num_layers = 0;
+};
+
+namespace aesir {
+
+// Makes ctx->device current for the calling thread.
+int32_t bind(aesir_ctx *ctx);
+// Returns (building if needed) a RoPE table covering positions [0, min_pos).
+int32_t rope_table(aesir_ctx *ctx, float theta, int64_t head_dim, int64_t min_pos, const void **table);
+// Bump allocation in bytes from the well (256-byte aligned).
+int32_t well_alloc_bytes(aesir_ctx *ctx, int64_t bytes, void **out);
+
+}  // namespace aesir

@@ -1,0 +1,108 @@
+// Launchers of the gfx950 kernels (host-callable), shared by the C-ABI wrappers and the model.
+#pragma once
+
+#include "common.hpp"
+
+namespace aesir {
+
+// Position state of one decode step, resident in device memory so that a captured HIP graph
+// can be replayed for every step: kernels read token/pos from here, and the lm_head kernel
+// writes the greedy token back (and, in autoregressive mode, advances token/pos).
+struct DecodeState {
+    int64_t token;       // token evaluated by this step
+    int64_t pos;         // its position (start_pos)
+    int64_t next_token;  // argmax written by the lm_head kernel
+    int64_t step;        // autoregressive step counter (index into the token ring)
+    int64_t advance;     // nonzero: lm_head sets token = next_token, pos += 1, step += 1
+    int64_t ring_cap;    // capacity of the token ring
+    int64_t pad[2];
+};
+
+// ------------------------------------------------------------------ GEMV / GEMM (gemv.hip)
+
+// C[m, n] = f16(sum_k A[m,k] B[n,k]) for M rows of A (decode GEMV per row; f32 accumulation).
+int32_t launch_gemm_f16(aesir_ctx *ctx, const void *A, int64_t M, int64_t K, const void *B, int64_t N, void *C);
+// Batched-prefill GEMM on MFMA tiles (M > 1); falls back to the GEMV path for shapes it does
+// not tile.
+int32_t launch_gemm_f16_mfma(aesir_ctx *ctx, const void *A, int64_t M, int64_t K, const void *B, int64_t N,
+                             void *C);
+
+// Fused decode-step GEMVs. All pointers are device pointers inside the model's arena.
+struct QkvArgs {
+    const void *x;          // residual stream [dim] (pre-norm)
+    const void *norm_w;     // attn_norm [dim]
+    float eps;
+    const void *w;          // [dim + 2*kvd][dim]: Q rows, K rows, V rows
+    int64_t dim, kvd, head_dim;
+    void *q_out;            // [dim]
+    void *k_cache, *v_cache;  // this layer's [max_seq][kvd]
+    int64_t max_seq;
+    const void *rope;       // [n_pos][head_dim/2] (cos, sin) f16 pairs
+    const DecodeState *state;
+};
+int32_t launch_qkv_rope_kv(hipStream_t s, const QkvArgs &a);
+
+// x[n] = f16(f16(W x_in)[n] + x[n]) (O projection and down projection with the residual add).
+int32_t launch_gemv_residual(hipStream_t s, const void *w, int64_t N, int64_t K, const void *x_in, void *x);
+
+// act[i] = f16(f16(up_i) * silu(f16(gate_i))) with W rows interleaved (2i gate, 2i+1 up),
+// after an RMSNorm prologue of x with norm_w.
+int32_t launch_gate_up_swiglu(hipStream_t s, const void *x, const void *norm_w, float eps, const void *w,
+                              int64_t ffn, int64_t dim, void *act);
+
+// lm_head with RMSNorm prologue, f16 logits, and the argmax reduction (last workgroup).
+struct LmHeadArgs {
+    const void *x, *norm_w;
+    float eps;
+    const void *w;  // [vocab][dim]
+    int64_t vocab, dim;
+    void *logits;   // [vocab] f16
+    void *partials; // [n_groups] (value, index)
+    uint32_t *counter;
+    DecodeState *state;
+    int64_t *ring;  // token ring (autoregressive loop), may be null
+};
+int32_t launch_lm_head_argmax(hipStream_t s, const LmHeadArgs &a);
+int64_t lm_head_groups(int64_t vocab);
+
+// ------------------------------------------------------------------ attention (attention.hip)
+struct AttnArgs {
+    const void *q;              // [nq * hd]
+    const void *k, *v;          // row 0 of the key/value views
+    int64_t k_stride, v_stride; // elements per row
+    void *out;                  // [nq * hd]
+    int64_t nq, nkv, hd;
+    float scale;
+    int64_t seq_len;            // >= 1, or 0 to read S = min(pos + 1, max_seq) from state
+    const DecodeState *state;
+    int64_t max_seq;
+    float *part;                // partials [nq][max_split][hd + 2]
+    uint32_t *counters;         // [nkv], zero on entry, left zero
+    int64_t max_split;
+};
+int32_t launch_attention_decode(hipStream_t s, const AttnArgs &a);
+int64_t attention_partial_floats(int64_t nq, int64_t hd, int64_t max_split);
+
+// ------------------------------------------------------------------ elementwise (basic.hip)
+int32_t launch_rmsnorm(hipStream_t s, void *T, int64_t rows, int64_t cols, const void *w, float eps);
+int32_t launch_rope(hipStream_t s, void *Q, int64_t q_rows, int64_t q_cols, void *K, int64_t k_cols,
+                    int64_t start_pos, int64_t head_dim, const void *table);
+int32_t launch_silu(hipStream_t s, void *T, int64_t n);
+int32_t launch_swiglu(hipStream_t s, void *up, void *gate, int64_t n);
+int32_t launch_residual_add(hipStream_t s, void *x, const void *r, int64_t n);
+int32_t launch_embed(hipStream_t s, const void *table, int64_t dim, int64_t token, const DecodeState *state,
+                     void *x);
+int32_t launch_kv_append(hipStream_t s, void *kc, void *vc, const void *k, const void *v, int64_t n);
+int32_t launch_argmax(hipStream_t s, const void *logits, int64_t n, void *partials, int64_t max_parts,
+                      uint32_t *counter, int64_t *result);
+int32_t launch_fill_normal(hipStream_t s, void *dst, int64_t n, int64_t cols, int64_t dst_stride, uint64_t seed,
+                           uint64_t stream, float mean, float std);
+int32_t launch_f32_to_f16(hipStream_t s, const float *src, void *dst, int64_t n);
+
+// ------------------------------------------------------------------ Q8_0 (q8_0.hip)
+int32_t launch_gemm_q8_0(hipStream_t s, const void *A, int64_t M, int64_t K, const void *blocks, int64_t N,
+                         void *C);
+int32_t launch_q8_0_matvec_f32(hipStream_t s, const void *blocks, int64_t N, int64_t K, const float *x,
+                               float *y);
+
+}  // namespace aesir

@@ -1,0 +1,569 @@
+// One Llama F16 model resident in the context's HBM arena, its decode step, and the engine loop.
+//
+// Replaces TransformerBlock.forward / forward_pass (core/inference.mojo:143-275, 424-518) and
+// AesirEngine._run_generation (aesir.mojo:323-462). A decode step is 1 + 5 * n_layers + 1 kernel
+// launches, all reading the token and position from a device-resident DecodeState, so one
+// captured HIP graph replays every step:
+//   embed                                x = token_embd[token]
+//   per layer  qkv_rope_kv               rmsnorm(x) -> [Q|K|V] GEMV -> RoPE(Q,K) -> K,V into the cache
+//              attention                 split-KV GQA over positions [0, min(pos+1, ctx))
+//              o + residual              x = f16(f16(Wo attn) + x)
+//              gate_up_swiglu            rmsnorm(x) -> [gate,up] GEMV -> f16(up * silu(gate))
+//              down + residual           x = f16(f16(Wdown act) + x)
+//   lm_head_argmax                       rmsnorm(x) -> logits -> greedy token (-> next step's state)
+#include <cmath>
+#include <cstring>
+#include <string>
+
+#include "common.hpp"
+#include "kernels.hpp"
+#include "model.hpp"
+
+namespace aesir {
+
+static int32_t carve(aesir_ctx *ctx, int64_t bytes, void **p) { return well_alloc_bytes(ctx, bytes, p); }
+
+// Parses "blk.<l>.<base>.weight" / "<global>.weight" into a tensor id.
+int32_t parse_tensor_name(const aesir_model *m, const char *name, TensorRef *ref) {
+    std::string s(name ? name : "");
+    const std::string suffix = ".weight";
+    if (s.size() <= suffix.size() || s.compare(s.size() - suffix.size(), suffix.size(), suffix) != 0)
+        return fail(AESIR_ERR_FORMAT, "GGUF tensor name is not a weight: %s", s.c_str());
+    std::string stem = s.substr(0, s.size() - suffix.size());
+    ref->layer = -1;
+    if (stem == "token_embd") {
+        ref->kind = TensorKind::TokenEmbd;
+        return AESIR_OK;
+    }
+    if (stem == "output_norm") {
+        ref->kind = TensorKind::OutputNorm;
+        return AESIR_OK;
+    }
+    if (stem == "output") {
+        ref->kind = TensorKind::Output;
+        return AESIR_OK;
+    }
+    if (stem.rfind("blk.", 0) == 0) {
+        size_t dot = stem.find('.', 4);
+        if (dot == std::string::npos) return fail(AESIR_ERR_FORMAT, "GGUF tensor name is malformed: %s", s.c_str());
+        char *end = nullptr;
+        long layer = std::strtol(stem.c_str() + 4, &end, 10);
+        if (end != stem.c_str() + dot || layer < 0 || layer >= m->cfg.n_layers)
+            return fail(AESIR_ERR_FORMAT, "GGUF tensor layer index out of range: %s", s.c_str());
+        std::string base = stem.substr(dot + 1);
+        static const struct {
+            const char *n;
+            TensorKind k;
+        } table[] = {{"attn_norm", TensorKind::AttnNorm}, {"attn_q", TensorKind::AttnQ},
+                     {"attn_k", TensorKind::AttnK},       {"attn_v", TensorKind::AttnV},
+                     {"attn_output", TensorKind::AttnOut}, {"ffn_norm", TensorKind::FfnNorm},
+                     {"ffn_gate", TensorKind::FfnGate},   {"ffn_up", TensorKind::FfnUp},
+                     {"ffn_down", TensorKind::FfnDown}};
+        for (auto &t : table) {
+            if (base == t.n) {
+                ref->kind = t.k;
+                ref->layer = (int)layer;
+                return AESIR_OK;
+            }
+        }
+    }
+    return fail(AESIR_ERR_FORMAT, "GGUF tensor is not part of the Llama F16 path: %s", s.c_str());
+}
+
+// Expected GGUF shape (rows, cols) and the device placement of a tensor: element (r, c) of the
+// GGUF tensor lives at base + r * row_stride + c.
+TensorPlace place_tensor(const aesir_model *m, const TensorRef &ref) {
+    const int64_t d = m->cfg.dim, kvd = m->kvd, f = m->cfg.ffn, V = m->cfg.vocab;
+    TensorPlace p{};
+    const ModelLayer *L = ref.layer >= 0 ? &m->layers[ref.layer] : nullptr;
+    switch (ref.kind) {
+        case TensorKind::TokenEmbd: p = {V, d, m->tok_embd, d, false}; break;
+        case TensorKind::OutputNorm: p = {1, d, m->out_norm, d, true}; break;
+        case TensorKind::Output: p = {V, d, m->out_w, d, false}; break;
+        case TensorKind::AttnNorm: p = {1, d, L->attn_norm, d, true}; break;
+        case TensorKind::AttnQ: p = {d, d, L->wqkv, d, false}; break;
+        case TensorKind::AttnK: p = {kvd, d, (uint16_t *)L->wqkv + d * d, d, false}; break;
+        case TensorKind::AttnV: p = {kvd, d, (uint16_t *)L->wqkv + (d + kvd) * d, d, false}; break;
+        case TensorKind::AttnOut: p = {d, d, L->wo, d, false}; break;
+        case TensorKind::FfnNorm: p = {1, d, L->ffn_norm, d, true}; break;
+        case TensorKind::FfnGate: p = {f, d, L->wgu, 2 * d, false}; break;
+        case TensorKind::FfnUp: p = {f, d, (uint16_t *)L->wgu + d, 2 * d, false}; break;
+        case TensorKind::FfnDown: p = {d, f, L->wdown, f, false}; break;
+    }
+    return p;
+}
+
+static int64_t stream_id(const TensorRef &ref) {
+    // Same numbering as the test oracle's generator: globals 0..2, then 100 + 16 * layer + slot.
+    switch (ref.kind) {
+        case TensorKind::TokenEmbd: return 0;
+        case TensorKind::OutputNorm: return 1;
+        case TensorKind::Output: return 2;
+        default: break;
+    }
+    int slot = 0;
+    switch (ref.kind) {
+        case TensorKind::AttnNorm: slot = 0; break;
+        case TensorKind::AttnQ: slot = 1; break;
+        case TensorKind::AttnK: slot = 2; break;
+        case TensorKind::AttnV: slot = 3; break;
+        case TensorKind::AttnOut: slot = 4; break;
+        case TensorKind::FfnNorm: slot = 5; break;
+        case TensorKind::FfnGate: slot = 6; break;
+        case TensorKind::FfnUp: slot = 7; break;
+        case TensorKind::FfnDown: slot = 8; break;
+        default: break;
+    }
+    return 100 + 16 * ref.layer + slot;
+}
+
+std::vector<TensorRef> all_tensors(const aesir_model *m) {
+    std::vector<TensorRef> v;
+    v.push_back({TensorKind::TokenEmbd, -1});
+    v.push_back({TensorKind::OutputNorm, -1});
+    v.push_back({TensorKind::Output, -1});
+    const TensorKind per[] = {TensorKind::AttnNorm, TensorKind::AttnQ,   TensorKind::AttnK,
+                              TensorKind::AttnV,    TensorKind::AttnOut, TensorKind::FfnNorm,
+                              TensorKind::FfnGate,  TensorKind::FfnUp,   TensorKind::FfnDown};
+    for (int l = 0; l < m->cfg.n_layers; l++)
+        for (auto k : per) v.push_back({k, l});
+    return v;
+}
+
+std::string tensor_name(const TensorRef &ref) {
+    static const char *names[] = {"token_embd", "output_norm", "output",   "attn_norm", "attn_q", "attn_k",
+                                  "attn_v",     "attn_output", "ffn_norm", "ffn_gate",  "ffn_up", "ffn_down"};
+    std::string base = names[(int)ref.kind];
+    if (ref.layer >= 0) return "blk." + std::to_string(ref.layer) + "." + base + ".weight";
+    return base + ".weight";
+}
+
+int32_t model_upload(aesir_model *m, const TensorRef &ref, const void *host, int64_t rows, int64_t cols, int32_t type) {
+    const TensorPlace p = place_tensor(m, ref);
+    const std::string nm = tensor_name(ref);
+    if (rows != p.rows || cols != p.cols)
+        return fail(AESIR_ERR_FORMAT, "GGUF required tensor has an invalid shape: %s", nm.c_str());
+    if (type != AESIR_GGML_F16 && !(p.is_norm && type == AESIR_GGML_F32))
+        return fail(AESIR_ERR_FORMAT, "GGUF required tensor has an invalid type: %s", nm.c_str());
+    hipStream_t s = m->ctx->stream;
+    std::vector<uint16_t> conv;
+    const void *src = host;
+    if (type == AESIR_GGML_F32) {  // loader/gguf.mojo:486-493: F32 -> f16 (round to nearest even)
+        conv.resize((size_t)(rows * cols));
+        const float *f = (const float *)host;
+        for (int64_t i = 0; i < rows * cols; i++) conv[i] = f32_to_f16_bits(f[i]);
+        src = conv.data();
+    }
+    AESIR_HIP_TRY(hipMemcpy2DAsync(p.base, (size_t)p.row_stride * 2, src, (size_t)cols * 2, (size_t)cols * 2,
+                                   (size_t)rows, hipMemcpyHostToDevice, s));
+    AESIR_HIP_TRY(hipStreamSynchronize(s));
+    return AESIR_OK;
+}
+
+// ------------------------------------------------------------------ decode step
+
+static int32_t enqueue_step(aesir_model *m, hipStream_t s) {
+    const aesir_model_config &c = m->cfg;
+    const int64_t d = c.dim, kvd = m->kvd;
+    AESIR_TRY(launch_embed(s, m->tok_embd, d, 0, m->state, m->x));
+    for (int64_t l = 0; l < c.n_layers; l++) {
+        const ModelLayer &L = m->layers[l];
+        uint16_t *kc = (uint16_t *)m->k_cache + l * c.ctx_len * kvd;
+        uint16_t *vc = (uint16_t *)m->v_cache + l * c.ctx_len * kvd;
+        QkvArgs q{m->x, L.attn_norm, c.rms_eps, L.wqkv, d, kvd, m->hd, m->q, kc, vc, c.ctx_len, m->rope, m->state};
+        AESIR_TRY(launch_qkv_rope_kv(s, q));
+        AttnArgs a{};
+        a.q = m->q;
+        a.k = kc;
+        a.v = vc;
+        a.k_stride = kvd;
+        a.v_stride = kvd;
+        a.out = m->attn;
+        a.nq = c.n_heads;
+        a.nkv = c.n_kv_heads;
+        a.hd = m->hd;
+        a.scale = m->attn_scale;
+        a.seq_len = 0;
+        a.state = m->state;
+        a.max_seq = c.ctx_len;
+        a.part = m->attn_part;
+        a.counters = m->attn_counters;
+        a.max_split = m->attn_max_split;
+        AESIR_TRY(launch_attention_decode(s, a));
+        AESIR_TRY(launch_gemv_residual(s, L.wo, d, d, m->attn, m->x));
+        AESIR_TRY(launch_gate_up_swiglu(s, m->x, L.ffn_norm, c.rms_eps, L.wgu, c.ffn, d, m->act));
+        AESIR_TRY(launch_gemv_residual(s, L.wdown, d, c.ffn, m->act, m->x));
+    }
+    LmHeadArgs h{m->x, m->out_norm, m->out_eps, m->out_w, c.vocab, d, m->logits, m->lm_parts, m->lm_counter,
+                 m->state, m->ring};
+    return launch_lm_head_argmax(s, h);
+}
+
+static int32_t ensure_rope(aesir_model *m, int64_t max_pos) {
+    const void *t = nullptr;
+    AESIR_TRY(rope_table(m->ctx, m->cfg.rope_theta, m->hd, max_pos, &t));
+    if (t != m->rope) {
+        m->rope = t;
+        if (m->graph_ready) {  // the table pointer is baked into the captured graph
+            (void)hipGraphExecDestroy(m->graph_exec);
+            (void)hipGraphDestroy(m->graph);
+            m->graph_ready = false;
+        }
+    }
+    return AESIR_OK;
+}
+
+static int32_t ensure_graph(aesir_model *m) {
+    if (m->graph_ready || !m->use_graph) return AESIR_OK;
+    hipStream_t s = m->ctx->stream;
+    AESIR_HIP_TRY(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    int32_t rc = enqueue_step(m, s);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(s, &g);
+    if (rc != AESIR_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+    }
+    if (e != hipSuccess) return fail(AESIR_ERR_HIP, "hipStreamEndCapture failed: %s", hipGetErrorString(e));
+    e = hipGraphInstantiate(&m->graph_exec, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        return fail(AESIR_ERR_HIP, "hipGraphInstantiate failed: %s", hipGetErrorString(e));
+    }
+    m->graph = g;
+    m->graph_ready = true;
+    return AESIR_OK;
+}
+
+static int32_t run_step(aesir_model *m, bool graph) {
+    hipStream_t s = m->ctx->stream;
+    if (graph && m->use_graph) {
+        AESIR_TRY(ensure_graph(m));
+        AESIR_HIP_TRY(hipGraphLaunch(m->graph_exec, s));
+        return AESIR_OK;
+    }
+    return enqueue_step(m, s);
+}
+
+static int32_t upload_state(aesir_model *m, int64_t token, int64_t pos, int64_t advance, int64_t ring_cap) {
+    DecodeState *h = m->state_host;
+    std::memset(h, 0, sizeof(DecodeState));
+    h->token = token;
+    h->pos = pos;
+    h->next_token = 0;
+    h->step = 0;
+    h->advance = advance;
+    h->ring_cap = ring_cap;
+    AESIR_HIP_TRY(hipMemcpyAsync(m->state, h, sizeof(DecodeState), hipMemcpyHostToDevice, m->ctx->stream));
+    return AESIR_OK;
+}
+
+}  // namespace aesir
+
+using namespace aesir;
+
+extern "C" {
+
+int32_t aesir_model_create(aesir_ctx *ctx, const aesir_model_config *cfg, aesir_model **out) {
+    AESIR_TRY(bind(ctx));
+    if (!cfg || !out) return fail(AESIR_ERR_INVALID, "aesir_model_create: null argument");
+    *out = nullptr;
+    const aesir_model_config c = *cfg;
+    // GGUFModelConfig.validate (loader/gguf.mojo:133-149)
+    if (c.ctx_len <= 0 || c.dim <= 0) return fail(AESIR_ERR_FORMAT, "GGUF model dimensions are incomplete");
+    if (c.ffn <= 0 || c.n_layers <= 0) return fail(AESIR_ERR_FORMAT, "GGUF layer metadata is incomplete");
+    if (c.n_heads <= 0 || c.n_kv_heads <= 0) return fail(AESIR_ERR_FORMAT, "GGUF attention metadata is incomplete");
+    if (c.dim % c.n_heads != 0) return fail(AESIR_ERR_FORMAT, "GGUF embedding length is not divisible by head count");
+    if (c.n_heads % c.n_kv_heads != 0) return fail(AESIR_ERR_FORMAT, "GGUF query heads are not divisible by KV heads");
+    if (c.vocab <= 0) return fail(AESIR_ERR_FORMAT, "GGUF vocabulary is empty");
+    if (!(c.rms_eps > 0.0f)) return fail(AESIR_ERR_INVALID, "rmsnorm: epsilon must be positive");
+    const int64_t hd = c.dim / c.n_heads;
+    if (hd % 2 != 0) return fail(AESIR_ERR_INVALID, "apply_rope: head_dim must be positive and even");
+    if (hd > 256 || c.n_heads / c.n_kv_heads > 16)
+        return fail(AESIR_ERR_UNSUPPORTED, "model: head_dim <= 256 and <= 16 query heads per KV head are supported");
+
+    auto *m = new aesir_model();
+    m->ctx = ctx;
+    m->cfg = c;
+    m->hd = hd;
+    m->kvd = hd * c.n_kv_heads;
+    m->attn_scale = (float)(1.0 / std::pow((double)hd, 0.5));  // compute.mojo:1968
+    m->out_eps = c.rms_eps > 0.0f ? c.rms_eps : 1e-5f;           // inference.mojo:484-488
+    m->well_start = ctx->well_offset;
+    const int64_t d = c.dim, kvd = m->kvd, f = c.ffn, V = c.vocab;
+    auto fail_cleanup = [&](int32_t rc) {
+        ctx->well_offset = m->well_start;
+        delete m;
+        return rc;
+    };
+    int32_t rc = AESIR_OK;
+    auto take = [&](int64_t bytes, void **p) {
+        if (rc == AESIR_OK) rc = carve(ctx, bytes, p);
+    };
+    take(V * d * 2, &m->tok_embd);
+    take(d * 2, &m->out_norm);
+    take(V * d * 2, &m->out_w);
+    m->layers.resize((size_t)c.n_layers);
+    for (auto &L : m->layers) {
+        take(d * 2, &L.attn_norm);
+        take((d + 2 * kvd) * d * 2, &L.wqkv);
+        take(d * d * 2, &L.wo);
+        take(d * 2, &L.ffn_norm);
+        take(2 * f * d * 2, &L.wgu);
+        take(d * f * 2, &L.wdown);
+    }
+    take(c.n_layers * c.ctx_len * kvd * 2, &m->k_cache);
+    take(c.n_layers * c.ctx_len * kvd * 2, &m->v_cache);
+    take(d * 2, &m->x);
+    take(d * 2, &m->q);
+    take(d * 2, &m->attn);
+    take(f * 2, &m->act);
+    take(V * 2, &m->logits);
+    int64_t max_split = (c.ctx_len + 63) / 64;
+    if (max_split > 128) max_split = 128;
+    m->attn_max_split = max_split;
+    void *p = nullptr;
+    take(attention_partial_floats(c.n_heads, hd, max_split) * 4, &p);
+    m->attn_part = (float *)p;
+    take((c.n_kv_heads + 1) * 4, &p);
+    m->attn_counters = (uint32_t *)p;
+    m->lm_counter = m->attn_counters + c.n_kv_heads;
+    take(lm_head_groups(V) * 8, &m->lm_parts);
+    take(sizeof(DecodeState), &p);
+    m->state = (DecodeState *)p;
+    m->ring_cap = 65536;
+    take(m->ring_cap * 8, &p);
+    m->ring = (int64_t *)p;
+    if (rc != AESIR_OK) return fail_cleanup(rc);
+    // The well may hold an earlier model's bytes: clear the weights and every counter.
+    const int64_t used = (ctx->well_offset - m->well_start) * 2;
+    if (hipMemsetAsync(ctx->well_base + m->well_start * 2, 0, (size_t)used, ctx->stream) != hipSuccess)
+        return fail_cleanup(fail(AESIR_ERR_HIP, "hipMemsetAsync of the model region failed"));
+    if (hipHostMalloc((void **)&m->state_host, sizeof(DecodeState), hipHostMallocDefault) != hipSuccess)
+        return fail_cleanup(fail(AESIR_ERR_HIP, "hipHostMalloc failed"));
+    m->use_graph = true;
+    if (const char *e = std::getenv("AESIR_NO_GRAPH")) m->use_graph = e[0] == '0';
+    if ((rc = ensure_rope(m, c.ctx_len)) != AESIR_OK) return fail_cleanup(rc);
+    if (hipStreamSynchronize(ctx->stream) != hipSuccess) return fail_cleanup(fail(AESIR_ERR_HIP, "sync failed"));
+    *out = m;
+    return AESIR_OK;
+}
+
+int32_t aesir_model_destroy(aesir_model *m) {
+    if (!m) return AESIR_OK;
+    (void)hipSetDevice(m->ctx->device);
+    (void)hipStreamSynchronize(m->ctx->stream);
+    if (m->graph_ready) {
+        (void)hipGraphExecDestroy(m->graph_exec);
+        (void)hipGraphDestroy(m->graph);
+    }
+    if (m->state_host) (void)hipHostFree(m->state_host);
+    delete m;
+    return AESIR_OK;
+}
+
+int32_t aesir_model_get_config(const aesir_model *m, aesir_model_config *cfg) {
+    if (!m || !cfg) return fail(AESIR_ERR_INVALID, "aesir_model_get_config: null argument");
+    *cfg = m->cfg;
+    return AESIR_OK;
+}
+
+int32_t aesir_model_set_tensor(aesir_model *m, const char *name, const void *host_data, int64_t rows, int64_t cols,
+                               int32_t ggml_type) {
+    if (!m || !host_data) return fail(AESIR_ERR_INVALID, "aesir_model_set_tensor: null argument");
+    AESIR_TRY(bind(m->ctx));
+    TensorRef ref;
+    AESIR_TRY(parse_tensor_name(m, name, &ref));
+    return model_upload(m, ref, host_data, rows, cols, ggml_type);
+}
+
+int32_t aesir_model_get_tensor(aesir_model *m, const char *name, void *host_out, int64_t elements) {
+    if (!m || !host_out) return fail(AESIR_ERR_INVALID, "aesir_model_get_tensor: null argument");
+    AESIR_TRY(bind(m->ctx));
+    TensorRef ref;
+    AESIR_TRY(parse_tensor_name(m, name, &ref));
+    const TensorPlace p = place_tensor(m, ref);
+    if (elements < p.rows * p.cols) return fail(AESIR_ERR_SHAPE, "aesir_model_get_tensor: output too small");
+    AESIR_HIP_TRY(hipMemcpy2DAsync(host_out, (size_t)p.cols * 2, p.base, (size_t)p.row_stride * 2, (size_t)p.cols * 2,
+                                   (size_t)p.rows, hipMemcpyDeviceToHost, m->ctx->stream));
+    AESIR_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+    return AESIR_OK;
+}
+
+int32_t aesir_model_init_random(aesir_model *m, uint64_t seed, float std, float norm_mean, float norm_std) {
+    if (!m) return fail(AESIR_ERR_INVALID, "aesir_model_init_random: null model");
+    AESIR_TRY(bind(m->ctx));
+    for (const TensorRef &ref : all_tensors(m)) {
+        const TensorPlace p = place_tensor(m, ref);
+        AESIR_TRY(launch_fill_normal(m->ctx->stream, p.base, p.rows * p.cols, p.cols, p.row_stride, seed,
+                                     (uint64_t)stream_id(ref), p.is_norm ? norm_mean : 0.0f,
+                                     p.is_norm ? norm_std : std));
+    }
+    AESIR_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+    return AESIR_OK;
+}
+
+int32_t aesir_forward_pass(aesir_model *m, const int64_t *tokens, int64_t n_tokens, int64_t start_pos,
+                           int64_t *next_token) {
+    if (!m || !next_token) return fail(AESIR_ERR_INVALID, "forward_pass: null argument");
+    AESIR_TRY(bind(m->ctx));
+    if (n_tokens <= 0) {  // inference.mojo:446-447
+        *next_token = 0;
+        return AESIR_OK;
+    }
+    if (!tokens) return fail(AESIR_ERR_INVALID, "forward_pass: null token list");
+    if (start_pos < 0) return fail(AESIR_ERR_INVALID, "apply_rope: start_pos cannot be negative");
+    int64_t idx = start_pos < n_tokens - 1 ? start_pos : n_tokens - 1;  // inference.mojo:449-450
+    const int64_t tok = tokens[idx];
+    if (tok < 0 || tok >= m->cfg.vocab) return fail(AESIR_ERR_INVALID, "Prompt token ID is outside the embedding vocabulary");
+    AESIR_TRY(ensure_rope(m, start_pos + 1));
+    AESIR_TRY(upload_state(m, tok, start_pos, 0, m->ring_cap));
+    AESIR_TRY(run_step(m, true));
+    AESIR_HIP_TRY(hipMemcpyAsync(m->state_host, m->state, sizeof(DecodeState), hipMemcpyDeviceToHost, m->ctx->stream));
+    AESIR_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+    *next_token = m->state_host->next_token;
+    return AESIR_OK;
+}
+
+int32_t aesir_model_logits(aesir_model *m, void *host_out) {
+    if (!m || !host_out) return fail(AESIR_ERR_INVALID, "aesir_model_logits: null argument");
+    return aesir_memcpy_d2h(m->ctx, host_out, m->logits, m->cfg.vocab * 2);
+}
+
+int32_t aesir_decode_loop(aesir_model *m, int64_t token, int64_t start_pos, int64_t n_steps, int32_t use_graph,
+                          int64_t *out_tokens, float *elapsed_ms) {
+    if (!m) return fail(AESIR_ERR_INVALID, "aesir_decode_loop: null model");
+    AESIR_TRY(bind(m->ctx));
+    if (n_steps <= 0) return fail(AESIR_ERR_INVALID, "aesir_decode_loop: n_steps must be positive");
+    if (start_pos < 0) return fail(AESIR_ERR_INVALID, "apply_rope: start_pos cannot be negative");
+    if (token < 0 || token >= m->cfg.vocab) return fail(AESIR_ERR_INVALID, "Prompt token ID is outside the embedding vocabulary");
+    if (n_steps > m->ring_cap) return fail(AESIR_ERR_INVALID, "aesir_decode_loop: at most %lld steps per call", (long long)m->ring_cap);
+    AESIR_TRY(ensure_rope(m, start_pos + n_steps));
+    if (use_graph) AESIR_TRY(ensure_graph(m));
+    AESIR_TRY(upload_state(m, token, start_pos, 1, m->ring_cap));
+    hipStream_t s = m->ctx->stream;
+    AESIR_HIP_TRY(hipEventRecord(m->ctx->ev_start, s));
+    for (int64_t i = 0; i < n_steps; i++) AESIR_TRY(run_step(m, use_graph != 0));
+    AESIR_HIP_TRY(hipEventRecord(m->ctx->ev_stop, s));
+    AESIR_HIP_TRY(hipEventSynchronize(m->ctx->ev_stop));
+    float ms = 0.0f;
+    AESIR_HIP_TRY(hipEventElapsedTime(&ms, m->ctx->ev_start, m->ctx->ev_stop));
+    if (elapsed_ms) *elapsed_ms = ms;
+    if (out_tokens)
+        AESIR_HIP_TRY(hipMemcpy(out_tokens, m->ring, (size_t)n_steps * sizeof(int64_t), hipMemcpyDeviceToHost));
+    return AESIR_OK;
+}
+
+int32_t aesir_model_kernel_times(aesir_model *m, int64_t pos, int32_t iters, float *times, int32_t n_times) {
+    if (!m || !times || n_times < 7) return fail(AESIR_ERR_INVALID, "aesir_model_kernel_times: need 7 outputs");
+    AESIR_TRY(bind(m->ctx));
+    if (iters <= 0) return fail(AESIR_ERR_INVALID, "aesir_model_kernel_times: iters must be positive");
+    AESIR_TRY(ensure_rope(m, pos + 1));
+    AESIR_TRY(upload_state(m, 0, pos, 0, m->ring_cap));
+    hipStream_t s = m->ctx->stream;
+    const aesir_model_config &c = m->cfg;
+    const int64_t d = c.dim, kvd = m->kvd;
+    // Class k is launched back to back, cycling through the layers so that no layer's weights
+    // are re-read from cache; time per launch = events / launches.
+    for (int cls = 0; cls < 7; cls++) {
+        const int64_t per_iter = (cls == 0 || cls == 6) ? 1 : c.n_layers;
+        int32_t rc = AESIR_OK;
+        auto launch = [&](int64_t l) -> int32_t {
+            const ModelLayer &L = m->layers[l];
+            uint16_t *kc = (uint16_t *)m->k_cache + l * c.ctx_len * kvd;
+            uint16_t *vc = (uint16_t *)m->v_cache + l * c.ctx_len * kvd;
+            switch (cls) {
+                case 0: return launch_embed(s, m->tok_embd, d, 0, m->state, m->x);
+                case 1: {
+                    QkvArgs q{m->x, L.attn_norm, c.rms_eps, L.wqkv, d, kvd, m->hd, m->q, kc, vc, c.ctx_len, m->rope, m->state};
+                    return launch_qkv_rope_kv(s, q);
+                }
+                case 2: {
+                    AttnArgs a{};
+                    a.q = m->q; a.k = kc; a.v = vc; a.k_stride = kvd; a.v_stride = kvd; a.out = m->attn;
+                    a.nq = c.n_heads; a.nkv = c.n_kv_heads; a.hd = m->hd; a.scale = m->attn_scale;
+                    a.seq_len = 0; a.state = m->state; a.max_seq = c.ctx_len; a.part = m->attn_part;
+                    a.counters = m->attn_counters; a.max_split = m->attn_max_split;
+                    return launch_attention_decode(s, a);
+                }
+                case 3: return launch_gemv_residual(s, L.wo, d, d, m->attn, m->x);
+                case 4: return launch_gate_up_swiglu(s, m->x, L.ffn_norm, c.rms_eps, L.wgu, c.ffn, d, m->act);
+                case 5: return launch_gemv_residual(s, L.wdown, d, c.ffn, m->act, m->x);
+                default: {
+                    LmHeadArgs h{m->x, m->out_norm, m->out_eps, m->out_w, c.vocab, d, m->logits, m->lm_parts,
+                                 m->lm_counter, m->state, nullptr};
+                    return launch_lm_head_argmax(s, h);
+                }
+            }
+        };
+        for (int64_t l = 0; l < per_iter && rc == AESIR_OK; l++) rc = launch(l);  // warm-up
+        if (rc != AESIR_OK) return rc;
+        AESIR_HIP_TRY(hipEventRecord(m->ctx->ev_start, s));
+        for (int32_t it = 0; it < iters && rc == AESIR_OK; it++)
+            for (int64_t l = 0; l < per_iter && rc == AESIR_OK; l++) rc = launch(l);
+        if (rc != AESIR_OK) return rc;
+        AESIR_HIP_TRY(hipEventRecord(m->ctx->ev_stop, s));
+        AESIR_HIP_TRY(hipEventSynchronize(m->ctx->ev_stop));
+        float ms = 0.0f;
+        AESIR_HIP_TRY(hipEventElapsedTime(&ms, m->ctx->ev_start, m->ctx->ev_stop));
+        times[cls] = ms / (float)(iters * per_iter);
+    }
+    return AESIR_OK;
+}
+
+int32_t aesir_generation_stop_reason(int64_t token, int64_t eos_token_id, int64_t generated_count,
+                                     int64_t max_new_tokens, const int64_t *stop_tokens, int64_t n_stop,
+                                     int64_t next_position, int64_t context_length) {
+    // aesir.mojo:195-212
+    if (eos_token_id >= 0 && token == eos_token_id) return AESIR_STOP_EOS;
+    for (int64_t i = 0; i < n_stop; i++)
+        if (stop_tokens && stop_tokens[i] == token) return AESIR_STOP_TOKEN;
+    if (generated_count >= max_new_tokens) return AESIR_STOP_LENGTH;
+    if (next_position >= context_length) return AESIR_STOP_CONTEXT_EXHAUSTED;
+    return -1;
+}
+
+int32_t aesir_generate(aesir_model *m, const int64_t *prompt, int64_t n_prompt, const aesir_generation_config *gc,
+                       int64_t *out_tokens, int64_t *n_out, int32_t *stop_reason) {
+    if (!m || !gc || !out_tokens || !n_out || !stop_reason) return fail(AESIR_ERR_INVALID, "aesir_generate: null argument");
+    AESIR_TRY(bind(m->ctx));
+    *n_out = 0;
+    const int64_t ctx_len = m->cfg.ctx_len, max_new = gc->max_new_tokens;
+    // GenerationConfig.validate (aesir.mojo:125-128) and _run_generation's prompt checks (:343-346)
+    if (max_new <= 0) return fail(AESIR_ERR_INVALID, "GenerationConfig max_new_tokens must be a positive integer");
+    if (max_new > ctx_len) return fail(AESIR_ERR_INVALID, "GenerationConfig max_new_tokens exceeds context_length boundary");
+    if (n_prompt <= 0 || !prompt) return fail(AESIR_ERR_INVALID, "RuneWeaver produced no prompt tokens");
+    if (n_prompt > ctx_len) return fail(AESIR_ERR_INVALID, "Prompt token count exceeds the model context length");
+    std::vector<int64_t> cur(prompt, prompt + n_prompt);
+    int64_t next = 0;
+    if (gc->batched_prefill)
+        AESIR_TRY(model_prefill(m, cur.data(), n_prompt, &next));
+    else
+        for (int64_t p = 0; p < n_prompt; p++) AESIR_TRY(aesir_forward_pass(m, cur.data(), (int64_t)cur.size(), p, &next));
+    int32_t reason = -1;
+    const int64_t eos = m->cfg.eos_token_id;
+    for (int64_t it = 0; it < max_new; it++) {  // aesir.mojo:381-445
+        out_tokens[(*n_out)++] = next;
+        cur.push_back(next);
+        if (next == eos) {
+            reason = AESIR_STOP_EOS;
+            break;
+        }
+        bool is_stop = false;
+        for (int64_t s = 0; s < gc->n_stop_tokens; s++) is_stop |= gc->stop_tokens[s] == next;
+        if (is_stop) {
+            reason = AESIR_STOP_TOKEN;
+            break;
+        }
+        const int64_t next_position = (int64_t)cur.size() - 1;
+        reason = aesir_generation_stop_reason(next, eos, *n_out, max_new, gc->stop_tokens, gc->n_stop_tokens,
+                                              next_position, ctx_len);
+        if (reason >= 0) break;
+        AESIR_TRY(aesir_forward_pass(m, cur.data(), (int64_t)cur.size(), next_position, &next));
+    }
+    if (reason < 0) reason = AESIR_STOP_LENGTH;
+    *stop_reason = reason;
+    return AESIR_OK;
+}
+
+}  // extern "C"

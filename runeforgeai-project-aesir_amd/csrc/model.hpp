@@ -1,0 +1,93 @@
+// Internal layout of aesir_model (one Llama F16 model in the context's HBM arena).
+#pragma once
+
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace aesir {
+
+// Per-layer device tensors. Q, K and V rows are concatenated ([dim + 2 kvd][dim]) so one GEMV
+// produces q|k|v; gate and up rows are interleaved (row 2i = gate i, row 2i+1 = up i) so the
+// SwiGLU pair of an output lands in one workgroup.
+struct ModelLayer {
+    void *attn_norm = nullptr;  // [dim]
+    void *wqkv = nullptr;       // [dim + 2 kvd][dim]
+    void *wo = nullptr;         // [dim][dim]
+    void *ffn_norm = nullptr;   // [dim]
+    void *wgu = nullptr;        // [2 ffn][dim]
+    void *wdown = nullptr;      // [dim][ffn]
+};
+
+enum class TensorKind : int {
+    TokenEmbd = 0,
+    OutputNorm,
+    Output,
+    AttnNorm,
+    AttnQ,
+    AttnK,
+    AttnV,
+    AttnOut,
+    FfnNorm,
+    FfnGate,
+    FfnUp,
+    FfnDown
+};
+
+struct TensorRef {
+    TensorKind kind;
+    int layer;  // -1 for global tensors
+};
+
+// GGUF shape and device placement: element (r, c) at base + r * row_stride + c (f16 elements).
+struct TensorPlace {
+    int64_t rows, cols;
+    void *base;
+    int64_t row_stride;
+    bool is_norm;
+};
+
+}  // namespace aesir
+
+struct aesir_model {
+    aesir_ctx *ctx = nullptr;
+    aesir_model_config cfg{};
+    int64_t hd = 0, kvd = 0;
+    float attn_scale = 0.0f, out_eps = 1e-5f;
+    int64_t well_start = 0;
+    void *tok_embd = nullptr, *out_norm = nullptr, *out_w = nullptr;
+    std::vector<aesir::ModelLayer> layers;
+    void *k_cache = nullptr, *v_cache = nullptr;  // [n_layers][ctx_len][kvd]
+    void *x = nullptr, *q = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr;
+    float *attn_part = nullptr;
+    uint32_t *attn_counters = nullptr, *lm_counter = nullptr;
+    int64_t attn_max_split = 1;
+    void *lm_parts = nullptr;
+    aesir::DecodeState *state = nullptr;  // device
+    aesir::DecodeState *state_host = nullptr;  // pinned staging
+    int64_t *ring = nullptr;
+    int64_t ring_cap = 0;
+    const void *rope = nullptr;
+    bool use_graph = true;
+    bool graph_ready = false;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t graph_exec = nullptr;
+    // batched prefill workspace (allocated on first use)
+    int64_t prefill_cap = 0;
+    void *pf_x = nullptr, *pf_h = nullptr, *pf_qkv = nullptr, *pf_attn = nullptr, *pf_gu = nullptr, *pf_act = nullptr,
+         *pf_tmp = nullptr;
+};
+
+namespace aesir {
+
+int32_t parse_tensor_name(const aesir_model *m, const char *name, TensorRef *ref);
+TensorPlace place_tensor(const aesir_model *m, const TensorRef &ref);
+std::vector<TensorRef> all_tensors(const aesir_model *m);
+std::string tensor_name(const TensorRef &ref);
+int32_t model_upload(aesir_model *m, const TensorRef &ref, const void *host, int64_t rows, int64_t cols, int32_t type);
+// Batched prefill of tokens[0..n) at positions 0..n-1; *next is the greedy token after the last.
+int32_t model_prefill(aesir_model *m, const int64_t *tokens, int64_t n, int64_t *next);
+
+}  // namespace aesir

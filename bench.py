@@ -1,0 +1,171 @@
+"""Batch-1 decode benchmark of the MI355X Llama F16 forward path (BASELINE metric).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--kv 2048] [--no-cpu-baseline]
+
+Workload: Llama-3-8B shape F16, random-init N(0, 0.02) on the device, batch 1,
+greedy decode with the KV cache pre-filled to --kv positions (N(0,1) f16). A step is one full
+forward pass (embedding, 32 layers, output norm, lm_head, argmax) on one token, each step
+consuming the previous step's argmax on the device (HIP graph replay). Prints one JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "runeforgeai-project-aesir_amd"))
+sys.path.insert(0, REPO)
+
+HBM_PEAK_GBS = 8000.0
+
+# Llama-3-8B shape. head_dim = 4096 / 32 = 128, kv_dim = 1024.
+DIM, LAYERS, HEADS, KV_HEADS, FFN, VOCAB = 4096, 32, 32, 8, 14336, 128256
+KV_DIM = DIM // HEADS * KV_HEADS
+
+# Algorithmic HBM bytes of one decode token: every weight matrix once, norms, one embedding row,
+# K+V read over L positions and written at one (SURVEY 8(d) / BASELINE 2b).
+LAYER_WEIGHT_BYTES = 2 * ((DIM + 2 * KV_DIM) * DIM + DIM * DIM + 2 * FFN * DIM + DIM * FFN + 2 * DIM)
+TOKEN_WEIGHT_BYTES = LAYERS * LAYER_WEIGHT_BYTES + 2 * VOCAB * DIM + 2 * DIM + 2 * DIM
+KV_BYTES_PER_POS = LAYERS * 2 * KV_DIM * 2
+assert TOKEN_WEIGHT_BYTES == 15_009_857_536
+
+
+def token_bytes(kv_len: int) -> int:
+    return TOKEN_WEIGHT_BYTES + KV_BYTES_PER_POS * kv_len + KV_BYTES_PER_POS
+
+
+# Dominant kernel: fused RMSNorm + gate/up GEMV + SwiGLU of one layer.
+GATE_UP_BYTES = 2 * FFN * DIM * 2 + DIM * 2 + DIM * 2 + FFN * 2
+
+
+def cpu_baseline(kv_len: int, reps: int) -> dict:
+    """Times the CPU oracle (single-threaded C restatement of the reference path) on a bounded
+    sample: forward passes with 1 and with 2 Llama-3-8B-shape layers plus the lm_head at KV
+    length kv_len; per-layer and head costs are taken from the difference and scaled to 32 layers."""
+    from oracle import oracle as O
+
+    cfg = O.Config(dim=DIM, n_layers=2, n_heads=HEADS, n_kv_heads=KV_HEADS, ffn=FFN, vocab=VOCAB,
+                   ctx_len=kv_len + 8)
+    rng = np.random.default_rng(5)
+    block = (rng.standard_normal(1 << 24, dtype=np.float32) * 0.02).astype(np.float16)
+    weights = {}
+    for name, (r, c) in O.tensor_shapes(cfg).items():
+        if name == "token_embd.weight":
+            weights[name] = np.zeros((r, c), np.float16)  # only one row is read
+        else:
+            weights[name] = np.resize(block, r * c).reshape(r, c)
+    m = O.Model(cfg, weights)
+    kv = m.new_kv()
+    kv.k[:] = np.resize(block, kv.k.size).reshape(kv.k.shape) * np.float16(50)
+    kv.v[:] = kv.k
+    toks = [1] * (kv_len + 1)
+    m.forward(kv, toks, kv_len, n_layers_run=1)  # warm caches/pages
+
+    def timed(n_layers):
+        best = float("inf")
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            m.forward(kv, toks, kv_len, n_layers_run=n_layers)
+            best = min(best, time.perf_counter() - t0)
+        return best
+
+    t1, t2 = timed(1), timed(2)
+    per_layer = max(t2 - t1, 1e-9)
+    head = max(t1 - per_layer, 0.0)
+    sec_per_token = LAYERS * per_layer + head
+    return {"value": 1.0 / sec_per_token, "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": (f"C oracle (restatement of the reference CPU path, single thread), Llama-3-8B-shape "
+                       f"forward at KV {kv_len} with 1 and 2 layers + lm_head, best of {reps}; "
+                       f"{per_layer * 1e3:.1f} ms/layer, {head * 1e3:.1f} ms head, scaled to 32 layers"),
+            "simd": bool(O.lib().ao_simd_enabled())}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--kv", type=int, default=2048, help="KV length at the start of the timed steps")
+    ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--kernel-iters", type=int, default=5)
+    ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--eager", action="store_true", help="launch kernels one by one instead of graph replay")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build runs on one GPU only (the decode path is single-GPU; multi-GPU tensor "
+              "parallelism is a design, not an implementation). Use --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import aesir_hip as A
+
+    ctx_len = args.kv + max(args.steps, args.warmup) + 64
+    well = int(TOKEN_WEIGHT_BYTES + 2 * LAYERS * ctx_len * KV_DIM * 2 + (1 << 30))
+    ctx = A.Context(well)
+    info = ctx.device_info()
+    m = A.Model.create(ctx, A.ModelConfig(DIM, LAYERS, HEADS, KV_HEADS, FFN, VOCAB, ctx_len))
+    m.init_random(args.seed, 0.02, 0.0, 0.02)
+    m.fill_kv_random(args.kv, seed=args.seed + 1)
+    use_graph = not args.eager
+
+    # warm-up (graph capture happens here), then the timed steps from the same KV length
+    m.decode_loop(1, args.kv, args.warmup, use_graph=use_graph)
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    toks, event_ms = m.decode_loop(1, args.kv, args.steps, use_graph=use_graph)
+    ctx.synchronize()
+    wall = time.perf_counter() - t0
+
+    tok_s = args.steps / wall
+    ms_per_step = wall * 1e3 / args.steps
+    mean_kv = args.kv + (args.steps - 1) / 2.0 + 1
+    step_bytes = TOKEN_WEIGHT_BYTES + KV_BYTES_PER_POS * mean_kv + KV_BYTES_PER_POS
+
+    kt = m.kernel_times(args.kv, iters=args.kernel_iters)
+    gu_ms = kt["gate_up_swiglu"]
+    gu_gbs = GATE_UP_BYTES / (gu_ms * 1e-3) / 1e9
+
+    out = {
+        "metric": "batch-1 decode tok/s + achieved HBM GB/s (% of peak), Llama-3-8B-shape F16",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 (f32 accumulate)",
+        "data": "synthetic: random-init N(0,0.02) weights generated on device, KV pre-filled N(0,1)",
+        "config": {"workload": "llama3-8b-shape f16 batch-1 greedy decode", "kv_len": args.kv,
+                   "dim": DIM, "layers": LAYERS, "heads": HEADS, "kv_heads": KV_HEADS, "ffn": FFN,
+                   "vocab": VOCAB, "graph": use_graph, "device": info["arch"], "cu": info["cu_count"]},
+        "step_hbm": {"bytes_per_token": int(step_bytes), "achieved_gbs": round(step_bytes * tok_s / 1e9, 1),
+                     "frac": round(step_bytes * tok_s / 1e9 / HBM_PEAK_GBS, 4),
+                     "event_ms_per_step": round(event_ms / args.steps, 4)},
+        "roofline": {"bound": "hbm", "kernel": "gate_up_swiglu (rmsnorm + [2x14336x4096] GEMV + SwiGLU)",
+                     "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "avg_launch_ms": round(gu_ms, 5), "bytes_per_launch": GATE_UP_BYTES},
+        "kernel_ms": {k: round(v, 5) for k, v in kt.items()},
+        "tokens_head": toks[:8],
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(args.kv, args.cpu_reps)
+        out["cpu_baseline"]["value"] = round(out["cpu_baseline"]["value"], 4)
+    else:
+        out["cpu_baseline"] = None
+    m.close()
+    ctx.close()
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -216,6 +216,11 @@ int32_t aesir_model_logits(aesir_model *model, void *host_out);
 int32_t aesir_decode_loop(aesir_model *model, int64_t token, int64_t start_pos, int64_t n_steps,
                           int32_t use_graph, int64_t *out_tokens, float *elapsed_ms);
 
+/* Fills the first n_pos positions of every layer's K and V cache with N(0, std) f16 values from
+ * the counter-based generator (seeded). No reference counterpart: it lets a throughput run start
+ * at a given KV length without prefilling that many tokens. */
+int32_t aesir_model_fill_kv_random(aesir_model *model, int64_t n_pos, uint64_t seed, float std);
+
 /* Average per-launch device time (ms, HIP events on the context stream) of each decode-step
  * kernel class, over `iters` eager steps at position pos. Order of times[]: 0 embed, 1 QKV+RoPE+KV,
  * 2 attention, 3 O+residual, 4 gate/up+SwiGLU, 5 down+residual, 6 lm_head+argmax. n_times >= 7. */

@@ -97,6 +97,7 @@ _sig("aesir_forward_pass", [P, P, I64, I64, C.POINTER(I64)])
 _sig("aesir_model_logits", [P, P])
 _sig("aesir_decode_loop", [P, I64, I64, I64, I32, P, C.POINTER(F32)])
 _sig("aesir_model_kernel_times", [P, I64, I32, P, I32])
+_sig("aesir_model_fill_kv_random", [P, I64, C.c_uint64, F32])
 _sig("aesir_generation_stop_reason", [I64, I64, I64, I64, P, I64, I64, I64])
 _sig("aesir_generate", [P, P, I64, C.POINTER(_GenConfig), P, C.POINTER(I64), C.POINTER(I32)])
 
@@ -415,6 +416,9 @@ class Model:
         _check(_L.aesir_decode_loop(self.h, token, start_pos, n_steps, 1 if use_graph else 0, out.ctypes.data,
                                     C.byref(ms)))
         return out.tolist(), ms.value
+
+    def fill_kv_random(self, n_pos: int, seed: int = 1, std: float = 1.0):
+        _check(_L.aesir_model_fill_kv_random(self.h, n_pos, seed, std))
 
     def kernel_times(self, pos: int, iters: int = 10) -> dict:
         t = np.zeros(7, dtype=np.float32)

@@ -454,6 +454,22 @@ int32_t aesir_decode_loop(aesir_model *m, int64_t token, int64_t start_pos, int6
     return AESIR_OK;
 }
 
+int32_t aesir_model_fill_kv_random(aesir_model *m, int64_t n_pos, uint64_t seed, float std) {
+    if (!m) return fail(AESIR_ERR_INVALID, "aesir_model_fill_kv_random: null model");
+    AESIR_TRY(bind(m->ctx));
+    if (n_pos <= 0 || n_pos > m->cfg.ctx_len)
+        return fail(AESIR_ERR_INVALID, "aesir_model_fill_kv_random: n_pos must be in [1, ctx_len]");
+    const int64_t per_layer = m->cfg.ctx_len * m->kvd;
+    for (int64_t l = 0; l < m->cfg.n_layers; l++) {
+        AESIR_TRY(launch_fill_normal(m->ctx->stream, (uint16_t *)m->k_cache + l * per_layer, n_pos * m->kvd, m->kvd,
+                                     m->kvd, seed, 1000000 + 2 * (uint64_t)l, 0.0f, std));
+        AESIR_TRY(launch_fill_normal(m->ctx->stream, (uint16_t *)m->v_cache + l * per_layer, n_pos * m->kvd, m->kvd,
+                                     m->kvd, seed, 1000001 + 2 * (uint64_t)l, 0.0f, std));
+    }
+    AESIR_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+    return AESIR_OK;
+}
+
 int32_t aesir_model_kernel_times(aesir_model *m, int64_t pos, int32_t iters, float *times, int32_t n_times) {
     if (!m || !times || n_times < 7) return fail(AESIR_ERR_INVALID, "aesir_model_kernel_times: need 7 outputs");
     AESIR_TRY(bind(m->ctx));

@@ -89,7 +89,11 @@ def test_gemv_vs_oracle(A, ctx, oracle, M, K, N):
     got = c.numpy()
     ref = oracle.gemm_f16(x, w)
     d = ulp_diff(got, ref)
-    assert d.max() <= 1, (d.max(), np.argmax(d))
+    # Beyond 1 ulp only where cancellation leaves a result so small that f32 summation-order noise
+    # (bounded by 2^-17 of the sum of |products|) exceeds an f16 ulp.
+    noise = 2.0 ** -17 * (np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).T)
+    bad = (d > 1) & (np.abs(got.astype(np.float64) - ref.astype(np.float64)) > noise)
+    assert not bad.any(), (d.max(), np.argmax(d))
     assert (d > 0).mean() < 0.01
 
 
@@ -384,4 +388,6 @@ def test_q8_0_matvec_f32_closed_form(A, ctx, N, K):
     W = (q.astype(np.float64) * d.astype(np.float64)[:, None]).reshape(N, K)
     ref = W @ x.astype(np.float64)
     got = y.numpy()[0].astype(np.float64)
-    assert np.max(np.abs(got - ref) / (np.abs(ref) + 1e-2)) < 1e-4
+    # f32 arithmetic: error bounded by 2^-17 of the sum of |products|
+    noise = 2.0 ** -17 * (np.abs(W) @ np.abs(x.astype(np.float64)))
+    assert np.all(np.abs(got - ref) <= noise)

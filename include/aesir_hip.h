@@ -222,8 +222,11 @@ int32_t aesir_decode_loop(aesir_model *model, int64_t token, int64_t start_pos, 
 int32_t aesir_model_fill_kv_random(aesir_model *model, int64_t n_pos, uint64_t seed, float std);
 
 /* Average per-launch device time (ms, HIP events on the context stream) of each decode-step
- * kernel class, over `iters` eager steps at position pos. Order of times[]: 0 embed, 1 QKV+RoPE+KV,
- * 2 attention, 3 O+residual, 4 gate/up+SwiGLU, 5 down+residual, 6 lm_head+argmax. n_times >= 7. */
+ * kernel, over `iters` rounds of back-to-back launches at position pos (the per-layer kernels
+ * cycle through all layers). Order of times[]: 0 QKV+RoPE+KV append (layer 0 also embeds),
+ * 1 attention (split-KV partials + merge), 2 O projection + residual, 3 RMSNorm + gate/up +
+ * SwiGLU, 4 down projection + residual, 5 RMSNorm + lm_head, 6 argmax finish. n_times >= 7.
+ * Leaves the decode workspace and the KV row at pos overwritten. */
 int32_t aesir_model_kernel_times(aesir_model *model, int64_t pos, int32_t iters, float *times, int32_t n_times);
 
 /* GenerationConfig subset that the token path needs (aesir.mojo:58-152). */

@@ -138,8 +138,8 @@ def abi_version() -> int:
 
 
 STOP_REASONS = {0: "eos", 1: "stop_token", 2: "length", 3: "context_exhausted"}
-KERNEL_CLASSES = ["embed", "qkv_rope_kv", "attention", "o_residual", "gate_up_swiglu", "down_residual",
-                  "lm_head_argmax"]
+KERNEL_CLASSES = ["qkv_rope_kv", "attention", "o_residual", "gate_up_swiglu", "down_residual", "lm_head",
+                  "argmax_finish"]
 
 
 class Tensor:

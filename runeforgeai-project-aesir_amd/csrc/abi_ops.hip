@@ -83,10 +83,8 @@ int32_t aesir_attn_gqa_decode(aesir_ctx *ctx, const void *query, int64_t query_r
     if (attention_partial_floats(nq, head_dim, max_split) > ctx->scratch.attn_part_floats)
         return fail(AESIR_ERR_UNSUPPORTED, "flash_attention_gqa: %lld heads x %lld dims exceed the context scratch",
                     (long long)nq, (long long)head_dim);
-    if (nkv > ctx->scratch.n_counters) return fail(AESIR_ERR_UNSUPPORTED, "flash_attention_gqa: too many KV heads");
     a.max_split = max_split;
     a.part = ctx->scratch.attn_part;
-    a.counters = ctx->scratch.counters;
     return launch_attention_decode(ctx->stream, a);
 }
 
@@ -129,7 +127,7 @@ int32_t aesir_argmax_f16(aesir_ctx *ctx, const void *logits, int64_t n, int64_t 
     if (!logits) return fail(AESIR_ERR_INVALID, "argmax: null logits");
     if (n > 2147483647) return fail(AESIR_ERR_UNSUPPORTED, "argmax: more than 2^31-1 logits");
     AESIR_TRY(launch_argmax(ctx->stream, logits, n, ctx->scratch.argmax_part, ctx->scratch.argmax_part_entries,
-                            ctx->scratch.counters + ctx->scratch.n_counters - 1, ctx->scratch.result));
+                            ctx->scratch.result));
     AESIR_HIP_TRY(hipMemcpyAsync(ctx->pinned_i64, ctx->scratch.result, sizeof(int64_t), hipMemcpyDeviceToHost, ctx->stream));
     AESIR_HIP_TRY(hipStreamSynchronize(ctx->stream));
     *index = ctx->pinned_i64[0];

@@ -6,8 +6,9 @@
 // positions. K/V tiles of 64 positions are staged in LDS with 16-byte loads (K rows padded by 16
 // bytes against bank conflicts); scores use v_dot2_f32_f16; each head's 64 tile scores sit in
 // one wave so the tile max/sum are wave reductions; the f32 accumulator is rescaled per tile
-// (online softmax). Partials (m, l, acc) go to global memory; the last workgroup of each KV head
-// to finish (completion counter, no waiting) merges them and writes f16 outputs.
+// (online softmax). Partials (m, l, acc) go to global memory and a second kernel merges them
+// (one workgroup per query head); a single split writes the f16 output directly. No workgroup
+// waits on another, and no device-scope fence is needed inside either kernel.
 //
 // Numerics: the reference rounds its running accumulator to f16 after every position; this
 // kernel keeps it in f32 and rounds once at the end (within the 2e-2 / 1e-2 tolerance).
@@ -23,6 +24,8 @@ constexpr int kTile = 64;          // positions per LDS tile (one wave of scores
 constexpr int kMaxHd = 256;
 constexpr int kMaxG = 16;          // query heads per KV head
 constexpr int kMaxPvPasses = 8;    // G * hd / 2 <= 256 * kMaxPvPasses
+constexpr int kMaxSplit = 128;     // splits per KV head (one merge thread each)
+constexpr int kMergeThreads = 128;
 
 int64_t attention_partial_floats(int64_t nq, int64_t hd, int64_t max_split) { return nq * max_split * (hd + 2); }
 
@@ -143,7 +146,8 @@ __global__ __launch_bounds__(kAThreads) void attn_decode_kernel(AttnArgs a) {
         }
     }
 
-    // ---- write partials (or the final output when this is the only split)
+    // ---- write partials (or the final output when this is the only split); partial rows are
+    // [m, l, acc[hd]] with acc unnormalized, merged by attn_merge_kernel
     const int64_t part_stride = a.max_split * (hd + 2);
     float *mlbuf = reinterpret_cast<float *>(smem_raw);  // reuse LDS: [G] m, [G] l
     __syncthreads();
@@ -183,34 +187,63 @@ __global__ __launch_bounds__(kAThreads) void attn_decode_kernel(AttnArgs a) {
             pp[1] = mlbuf[G + h];
         }
     }
-    __syncthreads();
-    __shared__ int s_last;
-    if (tid == 0) s_last = arrive_is_last(a.counters + g, (uint32_t)nsplit) ? 1 : 0;
-    __syncthreads();
-    if (!s_last) return;
-    last_block_acquire();
+}
 
-    // ---- merge: out = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M)
-#pragma unroll
-    for (int r = 0; r < kMaxPvPasses; r++) {
-        const int item = tid + kAThreads * r;
-        if (r >= pv_passes || item >= pv_items) continue;
-        const int h = item / (hd / 2), d = (item % (hd / 2)) * 2;
-        const float *base = a.part + ((int64_t)(g * G + h)) * part_stride;
-        float M = -INFINITY;
-        for (int64_t s = 0; s < nsplit; s++) M = fmaxf(M, base[s * (hd + 2)]);
-        float L = 0.0f, x0 = 0.0f, x1 = 0.0f;
-        for (int64_t s = 0; s < nsplit; s++) {
-            const float *pp = base + s * (hd + 2);
-            const float w = expf(pp[0] - M);
-            L = fmaf(pp[1], w, L);
-            x0 = fmaf(pp[2 + d], w, x0);
-            x1 = fmaf(pp[2 + d + 1], w, x1);
-        }
-        out[h * hd + d] = (h16)(x0 / L);
-        out[h * hd + d + 1] = (h16)(x1 / L);
+// Merge of the split partials: one workgroup per query head, one split per thread for the
+// max/sum bookkeeping, then each thread owns a pair of output dims and accumulates over splits
+// with 8 independent loads in flight.
+__global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(AttnArgs a) {
+    __shared__ float wsh[kMaxSplit];
+    __shared__ float red[kMergeThreads / kWave];
+    const int tid = threadIdx.x;
+    const int hd = (int)a.hd;
+    int64_t S = a.seq_len;
+    if (S <= 0) {
+        const int64_t pos = a.state->pos;
+        S = pos + 1 < a.max_seq ? pos + 1 : a.max_seq;
     }
-    if (tid == 0) a.counters[g] = 0;
+    int64_t chunk = (S + a.max_split - 1) / a.max_split;
+    chunk = (chunk + kTile - 1) / kTile * kTile;
+    const int nsplit = (int)((S + chunk - 1) / chunk);
+    if (nsplit <= 1) return;  // the partial kernel wrote the output directly
+    const int h = blockIdx.x;
+    const int64_t stride = hd + 2;
+    const float *base = a.part + (int64_t)h * a.max_split * stride;
+    const float m_s = tid < nsplit ? base[tid * stride] : -INFINITY;
+    const float l_s = tid < nsplit ? base[tid * stride + 1] : 0.0f;
+    // M = max_s m_s
+    float M = wave_max(m_s);
+    if ((tid & 63) == 0) red[tid >> 6] = M;
+    __syncthreads();
+    M = red[0];
+#pragma unroll
+    for (int w = 1; w < kMergeThreads / kWave; w++) M = fmaxf(M, red[w]);
+    __syncthreads();
+    const float w_s = tid < nsplit ? expf(m_s - M) : 0.0f;
+    if (tid < kMaxSplit) wsh[tid] = w_s;
+    const float L = block_sum<kMergeThreads / kWave>(l_s * w_s, red);  // synchronizes wsh too
+    h16 *out = reinterpret_cast<h16 *>(a.out) + (int64_t)h * hd;
+    for (int d = 2 * tid; d < hd; d += 2 * kMergeThreads) {
+        float x0 = 0.0f, x1 = 0.0f;
+        int s = 0;
+        for (; s + 8 <= nsplit; s += 8) {
+            float2 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = *reinterpret_cast<const float2 *>(base + (s + j) * stride + 2 + d);
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                x0 = fmaf(v[j].x, wsh[s + j], x0);
+                x1 = fmaf(v[j].y, wsh[s + j], x1);
+            }
+        }
+        for (; s < nsplit; s++) {
+            const float2 v = *reinterpret_cast<const float2 *>(base + s * stride + 2 + d);
+            x0 = fmaf(v.x, wsh[s], x0);
+            x1 = fmaf(v.y, wsh[s], x1);
+        }
+        out[d] = (h16)(x0 / L);
+        out[d + 1] = (h16)(x1 / L);
+    }
 }
 
 static int64_t attn_lds_bytes(int64_t G, int64_t hd) {
@@ -224,7 +257,8 @@ int32_t launch_attention_decode(hipStream_t s, const AttnArgs &a) {
     if (G > kMaxG) return fail(AESIR_ERR_UNSUPPORTED, "attention: %lld query heads per KV head exceeds %d", (long long)G, kMaxG);
     if (G * a.hd / 2 > (int64_t)kAThreads * kMaxPvPasses)
         return fail(AESIR_ERR_UNSUPPORTED, "attention: query group x head_dim too large");
-    if (a.max_split < 1 || a.max_split > 65535) return fail(AESIR_ERR_INVALID, "attention: bad split count");
+    if (a.max_split < 1 || a.max_split > kMaxSplit) return fail(AESIR_ERR_INVALID, "attention: bad split count");
+    if (a.hd / 2 > kMergeThreads * 64) return fail(AESIR_ERR_UNSUPPORTED, "attention: head_dim too large for the merge");
     const bool vec = a.hd % 8 == 0 && a.k_stride % 8 == 0 && a.v_stride % 8 == 0 && ((uintptr_t)a.k & 15) == 0 &&
                      ((uintptr_t)a.v & 15) == 0 && ((uintptr_t)a.q & 15) == 0;
     const int64_t lds = attn_lds_bytes(G, a.hd);
@@ -241,6 +275,8 @@ int32_t launch_attention_decode(hipStream_t s, const AttnArgs &a) {
         hipLaunchKernelGGL(attn_decode_kernel<false>, grid, dim3(kAThreads), (unsigned)lds, s, a);
     }
     AESIR_LAUNCH_CHECK("attn_decode_kernel");
+    hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)a.nq), dim3(kMergeThreads), 0, s, a);
+    AESIR_LAUNCH_CHECK("attn_merge_kernel");
     return AESIR_OK;
 }
 

@@ -63,8 +63,6 @@ struct CtxScratch {
     // carved regions
     float *attn_part = nullptr;     // attention partials (m, l, acc)
     int64_t attn_part_floats = 0;
-    uint32_t *counters = nullptr;   // self-resetting completion counters (zeroed once)
-    int64_t n_counters = 0;
     void *argmax_part = nullptr;    // argmax partials
     int64_t argmax_part_entries = 0;
     int64_t *result = nullptr;      // device int64 results

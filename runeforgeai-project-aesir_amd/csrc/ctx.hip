@@ -132,20 +132,17 @@ int32_t aesir_ctx_create(int32_t device, int64_t well_bytes, aesir_ctx **out) {
     // MimirWell zeroes its pool at creation (core/mimir_well.mojo:541).
     if (hipMemsetAsync(ctx->well_base, 0, (size_t)ctx->well_capacity * 2, ctx->stream) != hipSuccess)
         return cleanup(fail(AESIR_ERR_HIP, "hipMemsetAsync of the well failed"));
-    // Context scratch for the standalone kernels: attention partials (4M floats), 4096
-    // counters, 64K argmax partials, 64 result slots.
+    // Context scratch for the standalone kernels: attention partials (4M floats), 64K argmax
+    // partials, 64 result slots.
     CtxScratch &s = ctx->scratch;
     s.attn_part_floats = 4 << 20;
-    s.n_counters = 4096;
     s.argmax_part_entries = 65536;
-    s.bytes = s.attn_part_floats * 4 + s.n_counters * 4 + s.argmax_part_entries * 8 + 64 * 8;
+    s.bytes = s.attn_part_floats * 4 + s.argmax_part_entries * 8 + 64 * 8;
     if (hipMalloc(&s.base, (size_t)s.bytes) != hipSuccess)
         return cleanup(fail(AESIR_ERR_HIP, "hipMalloc of context scratch failed"));
     char *p = (char *)s.base;
     s.attn_part = (float *)p;
     p += s.attn_part_floats * 4;
-    s.counters = (uint32_t *)p;
-    p += s.n_counters * 4;
     s.argmax_part = p;
     p += s.argmax_part_entries * 8;
     s.result = (int64_t *)p;

@@ -1,5 +1,5 @@
 // Device-side helpers for gfx950 (CDNA4): binary16 arithmetic with the reference's rounding
-// points, 16-byte vector loads, wave64 reductions and the completion-counter handshake.
+// points, 16-byte vector loads and wave64 reductions.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -108,19 +108,5 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
     __syncthreads();
     return s;
 }
-
-// ------------------------------------------------------------------ completion counter
-// The "last workgroup finishes the reduction" handshake: thread 0 of every workgroup calls this
-// after writing its partial; it returns true in exactly one workgroup (the last to arrive),
-// which then reads every partial. The release fence publishes this workgroup's partial before
-// the counter increment; the acquire fence in the last workgroup (issued by every thread via
-// last_block_acquire) makes the other partials visible. The last workgroup resets the counter
-// so the next launch starts from zero. No workgroup ever waits on another.
-__device__ __forceinline__ bool arrive_is_last(uint32_t *counter, uint32_t total) {
-    __threadfence();
-    uint32_t ticket = atomicAdd(counter, 1u);
-    return ticket == total - 1;
-}
-__device__ __forceinline__ void last_block_acquire() { __threadfence(); }
 
 }  // namespace aesir

@@ -56,33 +56,87 @@ __device__ __forceinline__ u32x4 norm8(u32x4 x, u32x4 w, h16 inv) {
     return u32x4{o[0], o[1], o[2], o[3]};
 }
 
-// Stages x (length K, zero-padded to a multiple of 8) into LDS; with NORM, applies rmsnorm with
-// weight nw. Each thread normalizes exactly the chunks it loaded, so only the sum of squares
-// needs a workgroup exchange.
-template <bool VEC, bool NORM>
-__device__ __forceinline__ void stage_x(h16 *xs, const h16 *__restrict__ x, int64_t K, const h16 *__restrict__ nw,
-                                        float eps, float *red) {
-    const int tid = threadIdx.x;
+// x staging: x (length K) goes to LDS zero-padded to nslab whole slabs (uniform trip counts),
+// optionally RMS-normalized (rmsnorm with weight nw). Loads are issued in batches of 8 slabs with
+// clamped addresses (no divergent branches around them); the first batch is issued by the
+// caller before the weight prefetch so that waiting for x does not wait for the weights.
+constexpr int kXBatch = 8;
+
+template <bool VEC>
+__device__ __forceinline__ void x_load_batch(u32x4 (&v)[kXBatch], const h16 *__restrict__ x, int64_t K, int nslab,
+                                             int i0) {
     const int64_t Kp = (K + 7) & ~int64_t(7);
-    float ss = 0.0f;
-    for (int64_t k = (int64_t)tid * 8; k < Kp; k += kSlab) {
-        u32x4 v = VEC ? ld16(x + k) : gather8(x, k, K);
-        st16(xs + k, v);
-        if (NORM) ss = sumsq8(v, ss);
+#pragma unroll
+    for (int j = 0; j < kXBatch; j++) {
+        v[j] = u32x4{0u, 0u, 0u, 0u};
+        if (i0 + j < nslab) {  // uniform across the workgroup
+            const int64_t k = (int64_t)threadIdx.x * 8 + (int64_t)(i0 + j) * kSlab;
+            const bool ok = k < Kp;  // false only in a partial last slab
+            v[j] = VEC ? ld16(x + (ok ? k : 0)) : gather8(x, ok ? k : 0, K);
+            if (!ok) v[j] = u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+}
+
+template <bool VEC, bool NORM>
+__device__ __forceinline__ float x_store_batch(const u32x4 (&v)[kXBatch], h16 *xs, int64_t K, int nslab, int i0,
+                                               h16 *xcopy, float ss) {
+    const int64_t Kp = (K + 7) & ~int64_t(7);
+#pragma unroll
+    for (int j = 0; j < kXBatch; j++) {
+        if (i0 + j >= nslab) break;
+        const int64_t k = (int64_t)threadIdx.x * 8 + (int64_t)(i0 + j) * kSlab;
+        st16(xs + k, v[j]);
+        if (xcopy && k < Kp) {  // raw (pre-norm) copy of x, written by workgroup 0 only
+            if (VEC) {
+                st16(xcopy + k, v[j]);
+            } else {
+                for (int t = 0; t < 8 && k + t < K; t++) xcopy[k + t] = xs[k + t];
+            }
+        }
+        if (NORM) ss = sumsq8(v[j], ss);
+    }
+    return ss;
+}
+
+// Finishes staging after the first batch was loaded into `first`: stores it, loads and stores
+// the remaining batches, then applies the RMSNorm scale (each thread to the chunks it loaded, so
+// only the sum of squares needs a workgroup exchange).
+template <bool VEC, bool NORM>
+__device__ __forceinline__ void x_stage_finish(const u32x4 (&first)[kXBatch], h16 *xs, const h16 *__restrict__ x,
+                                               int64_t K, int nslab, const h16 *__restrict__ nw, float eps,
+                                               float *red, h16 *xcopy) {
+    float ss = x_store_batch<VEC, NORM>(first, xs, K, nslab, 0, xcopy, 0.0f);
+    for (int i0 = kXBatch; i0 < nslab; i0 += kXBatch) {
+        u32x4 v[kXBatch];
+        x_load_batch<VEC>(v, x, K, nslab, i0);
+        ss = x_store_batch<VEC, NORM>(v, xs, K, nslab, i0, xcopy, ss);
     }
     if (NORM) {
+        const int64_t Kp = (K + 7) & ~int64_t(7);
         ss = block_sum<kThreads / kWave>(ss, red);
         const h16 inv = (h16)(1.0f / sqrtf(ss / (float)K + eps));
-        for (int64_t k = (int64_t)tid * 8; k < Kp; k += kSlab) {
+        for (int i = 0; i < nslab; i++) {
+            const int64_t k = (int64_t)threadIdx.x * 8 + (int64_t)i * kSlab;
+            if (k >= Kp) break;
             u32x4 w = VEC ? ld16(nw + k) : gather8(nw, k, K);
             st16(xs + k, norm8(ld16(xs + k), w, inv));
         }
     }
 }
 
+// x source of one launch: x = xin + m * x_stride, or, with `token` set, row token->token of xin
+// (the embedding table: the layer-0 launch of a decode step reads x straight from it and
+// workgroup 0 writes the raw row to xcopy, which becomes the residual stream).
+struct XSrc {
+    const h16 *xin;
+    int64_t x_stride;
+    const DecodeState *token;
+    h16 *xcopy;
+};
+
 template <int ROWS, bool VEC, bool NORM, class Epi>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(const h16 *__restrict__ W, int64_t N, int64_t K,
-                                                        const h16 *__restrict__ xin, int64_t x_stride,
+__global__ __launch_bounds__(kThreads) void gemv_kernel(const h16 *__restrict__ W, int64_t N, int64_t K, XSrc src,
                                                         const h16 *__restrict__ nw, float eps, Epi epi) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     h16 *xs = reinterpret_cast<h16 *>(smem_raw);
@@ -91,27 +145,129 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const h16 *__restrict__ 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t n0 = (int64_t)blockIdx.x * ROWS;
     const int64_t m = blockIdx.y;
-
-    stage_x<VEC, NORM>(xs, xin + m * x_stride, K, nw, eps, red);
-    __syncthreads();
+    const int64_t Kp = (K + 7) & ~int64_t(7);
+    const int64_t k0 = (int64_t)tid * 8;
 
     // Rows past N (last group only) re-read row N-1; the epilogue drops them.
     const h16 *wr[ROWS];
 #pragma unroll
     for (int r = 0; r < ROWS; r++) wr[r] = W + (n0 + r < N ? n0 + r : N - 1) * K;
 
+    // Weights stream through a register double buffer: every ROWS-row slab is requested one
+    // slab ahead of its use, so each thread keeps 2 x ROWS 16-byte loads in flight. The slab
+    // count is uniform across the workgroup (x is zero-padded in LDS and tail addresses are
+    // clamped into the row), so the loop runs under scalar control. The first slab is
+    // requested right after x, overlapping its latency with the prologue.
+    const int nslab = (int)((Kp + kSlab - 1) / kSlab);
+    auto kw = [&](int i) -> int64_t {
+        const int64_t k = k0 + (int64_t)i * kSlab;
+        return k < Kp ? k : Kp - 8;
+    };
+    u32x4 wa[ROWS], wb[ROWS];
+    auto fetch = [&](u32x4 (&w)[ROWS], int i) {
+        const int64_t k = kw(i);
+#pragma unroll
+        for (int r = 0; r < ROWS; r++) w[r] = VEC ? ld16_stream(wr[r] + k) : gather8(wr[r], k, K);
+    };
     float acc[ROWS];
 #pragma unroll
     for (int r = 0; r < ROWS; r++) acc[r] = 0.0f;
-    const int64_t Kp = (K + 7) & ~int64_t(7);
-#pragma unroll 2
-    for (int64_t k = (int64_t)tid * 8; k < Kp; k += kSlab) {
-        const u32x4 xv = ld16(xs + k);
-        u32x4 wv[ROWS];
+    auto consume = [&](const u32x4 (&w)[ROWS], int i) {
+        const u32x4 xv = ld16(xs + k0 + (int64_t)i * kSlab);  // zero beyond K
 #pragma unroll
-        for (int r = 0; r < ROWS; r++) wv[r] = VEC ? ld16_stream(wr[r] + k) : gather8(wr[r], k, K);
+        for (int r = 0; r < ROWS; r++) acc[r] = dot8(w[r], xv, acc[r]);
+    };
+    const h16 *x = src.token ? src.xin + src.token->token * src.x_stride : src.xin + m * src.x_stride;
+    u32x4 xfirst[kXBatch];
+    x_load_batch<VEC>(xfirst, x, K, nslab, 0);
+    __builtin_amdgcn_sched_barrier(0);  // keep the x requests ahead of the weight requests
+    fetch(wa, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    x_stage_finish<VEC, NORM>(xfirst, xs, x, K, nslab, nw, eps, red,
+                              (src.xcopy && blockIdx.x == 0) ? src.xcopy : nullptr);
+    __syncthreads();
+
+    for (int i = 0; i < nslab; i += 2) {
+        if (i + 1 < nslab) fetch(wb, i + 1);
+        consume(wa, i);
+        if (i + 1 >= nslab) break;
+        if (i + 2 < nslab) fetch(wa, i + 2);
+        consume(wb, i + 1);
+    }
+
+    wave_multi_sum<ROWS>(acc, lane);
+    constexpr int G = kWave / ROWS;
+    if ((lane & (G - 1)) == 0) red[wave * ROWS + lane / G] = acc[0];
+    __syncthreads();
+    if (tid < ROWS) sums[tid] = (red[tid] + red[ROWS + tid]) + (red[2 * ROWS + tid] + red[3 * ROWS + tid]);
+    __syncthreads();
+    epi.template apply<ROWS>(n0, m, N, sums, tid);
+}
+
+// Fixed-shape fast path (K % 8 == 0, 16-byte aligned, NS = ceil(K / 2048) slabs known at
+// compile time). Thread t only ever multiplies its own x chunks (k = 8t + 2048i), so x stays in
+// registers, RMS-normalized in place; the only workgroup exchange before the dot products is
+// the sum of squares (NORM), and plain GEMVs have no barrier at all. Request order: x chunks,
+// norm weights, then the first weight slab; weights then stream through a register double
+// buffer one slab ahead of their use.
+template <int ROWS, int NS, bool NORM, class Epi>
+__global__ __launch_bounds__(kThreads) void gemv_fixed_kernel(const h16 *__restrict__ W, int64_t N, int64_t K,
+                                                              XSrc src, const h16 *__restrict__ nw, float eps,
+                                                              Epi epi) {
+    __shared__ float red[4 * ROWS];
+    __shared__ float sums[ROWS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t n0 = (int64_t)blockIdx.x * ROWS;
+    const int64_t m = blockIdx.y;
+    const int64_t k0 = (int64_t)tid * 8;
+    const h16 *wr[ROWS];
 #pragma unroll
-        for (int r = 0; r < ROWS; r++) acc[r] = dot8(wv[r], xv, acc[r]);
+    for (int r = 0; r < ROWS; r++) wr[r] = W + (n0 + r < N ? n0 + r : N - 1) * K;
+    const h16 *x = src.token ? src.xin + src.token->token * src.x_stride : src.xin + m * src.x_stride;
+
+    u32x4 xr[NS], nr[NS];
+    bool live[NS];
+#pragma unroll
+    for (int i = 0; i < NS; i++) {
+        const int64_t k = k0 + (int64_t)i * kSlab;
+        live[i] = k < K;  // false only in a partial last slab
+        xr[i] = ld16(x + (live[i] ? k : 0));
+        if (NORM) nr[i] = ld16(nw + (live[i] ? k : 0));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 wbuf[2][ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; r++) wbuf[0][r] = ld16_stream(wr[r] + k0);  // k0 < 2048 <= K
+    __builtin_amdgcn_sched_barrier(0);
+
+    float ss = 0.0f;
+    h16 *xcopy = (src.xcopy && blockIdx.x == 0) ? src.xcopy : nullptr;
+#pragma unroll
+    for (int i = 0; i < NS; i++) {
+        if (!live[i]) xr[i] = u32x4{0u, 0u, 0u, 0u};
+        if (xcopy && live[i]) st16(xcopy + k0 + (int64_t)i * kSlab, xr[i]);
+        if (NORM) ss = sumsq8(xr[i], ss);
+    }
+    if (NORM) {
+        ss = block_sum<kThreads / kWave>(ss, red);
+        const h16 inv = (h16)(1.0f / sqrtf(ss / (float)K + eps));
+#pragma unroll
+        for (int i = 0; i < NS; i++) xr[i] = norm8(xr[i], nr[i], inv);  // zero chunks stay zero
+    }
+
+    float acc[ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; r++) acc[r] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NS; i++) {
+        if (i + 1 < NS) {
+            const int64_t k = k0 + (int64_t)(i + 1) * kSlab;
+            const int64_t kc = k < K ? k : k0;  // dead lanes of a partial slab re-read slab 0
+#pragma unroll
+            for (int r = 0; r < ROWS; r++) wbuf[(i + 1) & 1][r] = ld16_stream(wr[r] + kc);
+        }
+#pragma unroll
+        for (int r = 0; r < ROWS; r++) acc[r] = dot8(wbuf[i & 1][r], xr[i], acc[r]);
     }
 
     wave_multi_sum<ROWS>(acc, lane);
@@ -199,31 +355,6 @@ constexpr float kArgmaxFloor = -10000.0f;  // f16(-10000) is exact (inference.mo
 // which reproduces the reference's ascending scan with strict '>' (inference.mojo:510-514).
 __device__ __forceinline__ ArgPart arg_combine(ArgPart a, ArgPart b) { return b.v > a.v ? b : a; }
 
-// Final argmax over `count` ordered partials by one workgroup (256 threads); returns the
-// reference's answer (0 if nothing exceeds the floor) to every thread.
-__device__ int64_t argmax_finish(const ArgPart *parts, int64_t count) {
-    __shared__ ArgPart tree[kThreads];
-    const int tid = threadIdx.x;
-    const int64_t per = (count + kThreads - 1) / kThreads;
-    ArgPart cur{-INFINITY, -1};
-    for (int64_t g = (int64_t)tid * per; g < (int64_t)(tid + 1) * per && g < count; g++) {
-        ArgPart p = parts[g];
-        cur = arg_combine(cur, p);
-    }
-    tree[tid] = cur;
-    __syncthreads();
-    for (int s = 1; s < kThreads; s <<= 1) {
-        ArgPart a = tree[tid];
-        if ((tid & (2 * s - 1)) == 0 && tid + s < kThreads) a = arg_combine(a, tree[tid + s]);
-        __syncthreads();
-        tree[tid] = a;
-        __syncthreads();
-    }
-    ArgPart best = tree[0];
-    __syncthreads();
-    return (best.v > kArgmaxFloor && best.i >= 0) ? (int64_t)best.i : 0;
-}
-
 // Per-group scan of the ROWS logits of one workgroup in ascending order.
 template <int ROWS>
 __device__ __forceinline__ ArgPart group_scan(int64_t n0, int64_t N, const float *s) {
@@ -239,40 +370,65 @@ __device__ __forceinline__ ArgPart group_scan(int64_t n0, int64_t N, const float
     return ci >= 0 ? ArgPart{cv, ci} : ArgPart{-INFINITY, -1};
 }
 
+// lm_head: f16 logits plus one ordered (value, index) partial per workgroup; argmax_finish_kernel
+// reduces the partials in a second launch.
 struct EpiLmHead {
     h16 *logits;
     ArgPart *parts;
-    uint32_t *counter;
-    DecodeState *state;
-    int64_t *ring;
     template <int ROWS>
     __device__ __forceinline__ void apply(int64_t n0, int64_t, int64_t N, const float *s, int tid) const {
-        __shared__ int s_last;
         if (tid < ROWS && n0 + tid < N) logits[n0 + tid] = (h16)s[tid];
-        if (tid == 0) {
-            parts[blockIdx.x] = group_scan<ROWS>(n0, N, s);
-            s_last = arrive_is_last(counter, gridDim.x) ? 1 : 0;
-        }
-        __syncthreads();
-        if (!s_last) return;
-        last_block_acquire();
-        const int64_t idx = argmax_finish(parts, gridDim.x);
-        if (tid == 0) {
-            state->next_token = idx;
-            if (state->advance) {
-                if (ring) ring[state->step % state->ring_cap] = idx;
-                state->token = idx;
-                state->pos = state->pos + 1;
-                state->step = state->step + 1;
-            }
-            *counter = 0;
-        }
+        if (tid == 0) parts[blockIdx.x] = group_scan<ROWS>(n0, N, s);
     }
 };
 
+// Final argmax over ordered partials (one workgroup). Writes *result and/or the decode state:
+// next_token, and in autoregressive mode token <- next, pos += 1, step += 1, ring[step] = next.
+constexpr int kFinishThreads = 1024;
+__global__ __launch_bounds__(kFinishThreads) void argmax_finish_kernel(const ArgPart *__restrict__ parts,
+                                                                        int64_t count, DecodeState *state,
+                                                                        int64_t *ring, int64_t *result) {
+    __shared__ ArgPart tree[kFinishThreads];
+    const int tid = threadIdx.x;
+    const int64_t per = (count + kFinishThreads - 1) / kFinishThreads;
+    ArgPart cur{-INFINITY, -1};
+    const int64_t g0 = (int64_t)tid * per, g1 = g0 + per < count ? g0 + per : count;
+    int64_t g = g0;
+    for (; g + 16 <= g1; g += 16) {  // 16 independent loads in flight, combined in order
+        ArgPart v[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) v[j] = parts[g + j];
+#pragma unroll
+        for (int j = 0; j < 16; j++) cur = arg_combine(cur, v[j]);
+    }
+    for (; g < g1; g++) cur = arg_combine(cur, parts[g]);
+    tree[tid] = cur;
+    __syncthreads();
+    for (int st = 1; st < kFinishThreads; st <<= 1) {
+        ArgPart a = tree[tid];
+        if ((tid & (2 * st - 1)) == 0 && tid + st < kFinishThreads) a = arg_combine(a, tree[tid + st]);
+        __syncthreads();
+        tree[tid] = a;
+        __syncthreads();
+    }
+    if (tid != 0) return;
+    const ArgPart best = tree[0];
+    const int64_t idx = (best.v > kArgmaxFloor && best.i >= 0) ? (int64_t)best.i : 0;
+    if (result) *result = idx;
+    if (state) {
+        state->next_token = idx;
+        if (state->advance) {
+            if (ring) ring[state->step % state->ring_cap] = idx;
+            state->token = idx;
+            state->pos = state->pos + 1;
+            state->step = state->step + 1;
+        }
+    }
+}
+
 // ------------------------------------------------------------------ launchers
 
-static int64_t lds_bytes(int64_t K) { return ((K + 7) & ~int64_t(7)) * 2; }
+static int64_t lds_bytes(int64_t K) { return (((K + 7) & ~int64_t(7)) + kSlab - 1) / kSlab * kSlab * 2; }
 
 template <class KernelPtr>
 static int32_t ensure_lds(KernelPtr k, int64_t bytes) {
@@ -285,22 +441,44 @@ static int32_t ensure_lds(KernelPtr k, int64_t bytes) {
 static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 template <int ROWS, bool NORM, class Epi>
-static int32_t gemv_dispatch(hipStream_t s, const void *W, int64_t N, int64_t K, const void *x, int64_t x_stride,
-                             int64_t M, const void *nw, float eps, const Epi &epi, const char *name) {
-    const bool vec = (K % 8 == 0) && aligned16(W) && aligned16(x) && (x_stride % 8 == 0) && (!NORM || aligned16(nw));
+static int32_t gemv_dispatch(hipStream_t s, const void *W, int64_t N, int64_t K, const XSrc &src, int64_t M,
+                             const void *nw, float eps, const Epi &epi, const char *name) {
+    const bool vec = (K % 8 == 0) && aligned16(W) && aligned16(src.xin) && (src.x_stride % 8 == 0) &&
+                     (!NORM || aligned16(nw)) && (!src.xcopy || aligned16(src.xcopy));
     const int64_t lds = lds_bytes(K);
     const dim3 grid((unsigned)((N + ROWS - 1) / ROWS), (unsigned)M);
     if (grid.x == 0 || grid.y == 0) return AESIR_OK;
+    const int64_t ns = (K + kSlab - 1) / kSlab;
+    if (vec && ns <= 8 && K >= kSlab) {
+        switch (ns) {
+#define AESIR_GEMV_FIXED(NSV)                                                                                    \
+    case NSV:                                                                                                   \
+        hipLaunchKernelGGL((gemv_fixed_kernel<ROWS, NSV, NORM, Epi>), grid, dim3(kThreads), 0, s, (const h16 *)W, N, K, \
+                           src, (const h16 *)nw, eps, epi);                                                      \
+        break;
+            AESIR_GEMV_FIXED(1)
+            AESIR_GEMV_FIXED(2)
+            AESIR_GEMV_FIXED(3)
+            AESIR_GEMV_FIXED(4)
+            AESIR_GEMV_FIXED(5)
+            AESIR_GEMV_FIXED(6)
+            AESIR_GEMV_FIXED(7)
+            AESIR_GEMV_FIXED(8)
+#undef AESIR_GEMV_FIXED
+        }
+        AESIR_LAUNCH_CHECK(name);
+        return AESIR_OK;
+    }
     if (vec) {
         auto k = gemv_kernel<ROWS, true, NORM, Epi>;
         AESIR_TRY(ensure_lds(k, lds));
-        hipLaunchKernelGGL(k, grid, dim3(kThreads), (unsigned)lds, s, (const h16 *)W, N, K, (const h16 *)x, x_stride,
-                           (const h16 *)nw, eps, epi);
+        hipLaunchKernelGGL(k, grid, dim3(kThreads), (unsigned)lds, s, (const h16 *)W, N, K, src, (const h16 *)nw, eps,
+                           epi);
     } else {
         auto k = gemv_kernel<ROWS, false, NORM, Epi>;
         AESIR_TRY(ensure_lds(k, lds));
-        hipLaunchKernelGGL(k, grid, dim3(kThreads), (unsigned)lds, s, (const h16 *)W, N, K, (const h16 *)x, x_stride,
-                           (const h16 *)nw, eps, epi);
+        hipLaunchKernelGGL(k, grid, dim3(kThreads), (unsigned)lds, s, (const h16 *)W, N, K, src, (const h16 *)nw, eps,
+                           epi);
     }
     AESIR_LAUNCH_CHECK(name);
     return AESIR_OK;
@@ -309,40 +487,58 @@ static int32_t gemv_dispatch(hipStream_t s, const void *W, int64_t N, int64_t K,
 int32_t launch_gemm_f16(aesir_ctx *ctx, const void *A, int64_t M, int64_t K, const void *B, int64_t N, void *C) {
     if (M > 65535) return fail(AESIR_ERR_UNSUPPORTED, "gemm_f16: more than 65535 rows of A");
     EpiStore e{(h16 *)C, N};
-    return gemv_dispatch<8, false>(ctx->stream, B, N, K, A, K, M, nullptr, 0.0f, e, "gemv_store");
+    return gemv_dispatch<8, false>(ctx->stream, B, N, K, XSrc{(const h16 *)A, K, nullptr, nullptr}, M, nullptr, 0.0f, e,
+                                   "gemv_store");
 }
 
 int32_t launch_qkv_rope_kv(hipStream_t s, const QkvArgs &a) {
     EpiQkv e{(h16 *)a.q_out, (h16 *)a.k_cache, (h16 *)a.v_cache, (const h16x2 *)a.rope, a.state,
              a.dim, a.kvd, a.head_dim, a.max_seq};
-    return gemv_dispatch<8, true>(s, a.w, a.dim + 2 * a.kvd, a.dim, a.x, 0, 1, a.norm_w, a.eps, e, "gemv_qkv_rope_kv");
+    XSrc src = a.embd ? XSrc{(const h16 *)a.embd, a.dim, a.state, (h16 *)a.x} : XSrc{(const h16 *)a.x, 0, nullptr, nullptr};
+    return gemv_dispatch<8, true>(s, a.w, a.dim + 2 * a.kvd, a.dim, src, 1, a.norm_w, a.eps, e, "gemv_qkv_rope_kv");
 }
 
 int32_t launch_gemv_residual(hipStream_t s, const void *w, int64_t N, int64_t K, const void *x_in, void *x) {
     EpiResidual e{(h16 *)x};
-    return gemv_dispatch<8, false>(s, w, N, K, x_in, 0, 1, nullptr, 0.0f, e, "gemv_residual");
+    return gemv_dispatch<8, false>(s, w, N, K, XSrc{(const h16 *)x_in, 0, nullptr, nullptr}, 1, nullptr, 0.0f, e,
+                                   "gemv_residual");
 }
 
 int32_t launch_gate_up_swiglu(hipStream_t s, const void *x, const void *norm_w, float eps, const void *w,
                               int64_t ffn, int64_t dim, void *act) {
     EpiSwiglu e{(h16 *)act};
-    return gemv_dispatch<8, true>(s, w, 2 * ffn, dim, x, 0, 1, norm_w, eps, e, "gemv_gate_up_swiglu");
+    return gemv_dispatch<8, true>(s, w, 2 * ffn, dim, XSrc{(const h16 *)x, 0, nullptr, nullptr}, 1, norm_w, eps, e,
+                                  "gemv_gate_up_swiglu");
 }
 
 int64_t lm_head_groups(int64_t vocab) { return (vocab + 7) / 8; }
 
+int32_t launch_lm_head(hipStream_t s, const LmHeadArgs &a) {
+    EpiLmHead e{(h16 *)a.logits, (ArgPart *)a.partials};
+    return gemv_dispatch<8, true>(s, a.w, a.vocab, a.dim, XSrc{(const h16 *)a.x, 0, nullptr, nullptr}, 1, a.norm_w,
+                                  a.eps, e, "gemv_lm_head");
+}
+
+int32_t launch_argmax_finish(hipStream_t s, const void *partials, int64_t count, DecodeState *state, int64_t *ring,
+                             int64_t *result) {
+    hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(kFinishThreads), 0, s, (const ArgPart *)partials, count,
+                       state, ring, result);
+    AESIR_LAUNCH_CHECK("argmax_finish_kernel");
+    return AESIR_OK;
+}
+
 int32_t launch_lm_head_argmax(hipStream_t s, const LmHeadArgs &a) {
-    EpiLmHead e{(h16 *)a.logits, (ArgPart *)a.partials, a.counter, a.state, a.ring};
-    return gemv_dispatch<8, true>(s, a.w, a.vocab, a.dim, a.x, 0, 1, a.norm_w, a.eps, e, "gemv_lm_head_argmax");
+    AESIR_TRY(launch_lm_head(s, a));
+    return launch_argmax_finish(s, a.partials, lm_head_groups(a.vocab), a.state, a.ring, nullptr);
 }
 
 // ------------------------------------------------------------------ standalone argmax
 
-// Stage 1: each workgroup scans a contiguous chunk in ascending order (strict '>').
+// Stage 1 of the standalone argmax: each workgroup scans a contiguous chunk in ascending order
+// (strict '>') and writes one ordered partial; argmax_finish_kernel reduces them.
 __global__ __launch_bounds__(kThreads) void argmax_kernel(const h16 *__restrict__ x, int64_t n, int64_t chunk,
-                                                          ArgPart *parts, uint32_t *counter, int64_t *result) {
+                                                          ArgPart *parts) {
     __shared__ ArgPart tree[kThreads];
-    __shared__ int s_last;
     const int tid = threadIdx.x;
     const int64_t base = (int64_t)blockIdx.x * chunk;
     const int64_t end = base + chunk < n ? base + chunk : n;
@@ -358,40 +554,27 @@ __global__ __launch_bounds__(kThreads) void argmax_kernel(const h16 *__restrict_
     }
     tree[tid] = cur;
     __syncthreads();
-    for (int s = 1; s < kThreads; s <<= 1) {
+    for (int st = 1; st < kThreads; st <<= 1) {
         ArgPart a = tree[tid];
-        if ((tid & (2 * s - 1)) == 0 && tid + s < kThreads) a = arg_combine(a, tree[tid + s]);
+        if ((tid & (2 * st - 1)) == 0 && tid + st < kThreads) a = arg_combine(a, tree[tid + st]);
         __syncthreads();
         tree[tid] = a;
         __syncthreads();
     }
-    if (tid == 0) {
-        parts[blockIdx.x] = tree[0];
-        s_last = arrive_is_last(counter, gridDim.x) ? 1 : 0;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    last_block_acquire();
-    const int64_t idx = argmax_finish(parts, gridDim.x);
-    if (tid == 0) {
-        *result = idx;
-        *counter = 0;
-    }
+    if (tid == 0) parts[blockIdx.x] = tree[0];
 }
 
-int32_t launch_argmax(hipStream_t s, const void *logits, int64_t n, void *partials, int64_t max_parts,
-                      uint32_t *counter, int64_t *result) {
-    // 8 elements per thread per group keeps ~2K groups at n = 128256 ... 16 groups minimum work
-    int64_t chunk = 2048;
+int32_t launch_argmax(hipStream_t s, const void *logits, int64_t n, void *partials, int64_t max_parts, int64_t *result) {
+    int64_t chunk = 2048;  // 8 elements per thread per workgroup
     int64_t groups = (n + chunk - 1) / chunk;
     if (groups > max_parts) {
         groups = max_parts;
         chunk = (n + groups - 1) / groups;
     }
     hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)groups), dim3(kThreads), 0, s, (const h16 *)logits, n, chunk,
-                       (ArgPart *)partials, counter, result);
+                       (ArgPart *)partials);
     AESIR_LAUNCH_CHECK("argmax_kernel");
-    return AESIR_OK;
+    return launch_argmax_finish(s, partials, groups, nullptr, nullptr, result);
 }
 
 }  // namespace aesir

@@ -30,6 +30,8 @@ int32_t launch_gemm_f16_mfma(aesir_ctx *ctx, const void *A, int64_t M, int64_t K
 // Fused decode-step GEMVs. All pointers are device pointers inside the model's arena.
 struct QkvArgs {
     const void *x;          // residual stream [dim] (pre-norm)
+    const void *embd;       // layer 0 only: token_embd [vocab][dim]; x = embd[state->token] is
+                            // staged from it and copied to `x` (the embedding lookup, fused)
     const void *norm_w;     // attn_norm [dim]
     float eps;
     const void *w;          // [dim + 2*kvd][dim]: Q rows, K rows, V rows
@@ -50,7 +52,8 @@ int32_t launch_gemv_residual(hipStream_t s, const void *w, int64_t N, int64_t K,
 int32_t launch_gate_up_swiglu(hipStream_t s, const void *x, const void *norm_w, float eps, const void *w,
                               int64_t ffn, int64_t dim, void *act);
 
-// lm_head with RMSNorm prologue, f16 logits, and the argmax reduction (last workgroup).
+// lm_head with RMSNorm prologue and f16 logits, then the argmax of its per-workgroup partials
+// (second launch), which writes the decode state.
 struct LmHeadArgs {
     const void *x, *norm_w;
     float eps;
@@ -58,11 +61,13 @@ struct LmHeadArgs {
     int64_t vocab, dim;
     void *logits;   // [vocab] f16
     void *partials; // [n_groups] (value, index)
-    uint32_t *counter;
     DecodeState *state;
     int64_t *ring;  // token ring (autoregressive loop), may be null
 };
 int32_t launch_lm_head_argmax(hipStream_t s, const LmHeadArgs &a);
+int32_t launch_lm_head(hipStream_t s, const LmHeadArgs &a);
+int32_t launch_argmax_finish(hipStream_t s, const void *partials, int64_t count, DecodeState *state, int64_t *ring,
+                             int64_t *result);
 int64_t lm_head_groups(int64_t vocab);
 
 // ------------------------------------------------------------------ attention (attention.hip)
@@ -77,9 +82,9 @@ struct AttnArgs {
     const DecodeState *state;
     int64_t max_seq;
     float *part;                // partials [nq][max_split][hd + 2]
-    uint32_t *counters;         // [nkv], zero on entry, left zero
-    int64_t max_split;
+    int64_t max_split;          // <= 128
 };
+// Two launches: split-KV partials, then the merge (one workgroup per query head).
 int32_t launch_attention_decode(hipStream_t s, const AttnArgs &a);
 int64_t attention_partial_floats(int64_t nq, int64_t hd, int64_t max_split);
 
@@ -94,7 +99,7 @@ int32_t launch_embed(hipStream_t s, const void *table, int64_t dim, int64_t toke
                      void *x);
 int32_t launch_kv_append(hipStream_t s, void *kc, void *vc, const void *k, const void *v, int64_t n);
 int32_t launch_argmax(hipStream_t s, const void *logits, int64_t n, void *partials, int64_t max_parts,
-                      uint32_t *counter, int64_t *result);
+                      int64_t *result);
 int32_t launch_fill_normal(hipStream_t s, void *dst, int64_t n, int64_t cols, int64_t dst_stride, uint64_t seed,
                            uint64_t stream, float mean, float std);
 int32_t launch_f32_to_f16(hipStream_t s, const float *src, void *dst, int64_t n);

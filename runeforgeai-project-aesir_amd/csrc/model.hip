@@ -162,41 +162,53 @@ int32_t model_upload(aesir_model *m, const TensorRef &ref, const void *host, int
 
 // ------------------------------------------------------------------ decode step
 
+static QkvArgs qkv_args(aesir_model *m, int64_t l) {
+    const aesir_model_config &c = m->cfg;
+    const ModelLayer &L = m->layers[l];
+    return QkvArgs{m->x, l == 0 ? m->tok_embd : nullptr, L.attn_norm, c.rms_eps, L.wqkv, c.dim, m->kvd, m->hd, m->q,
+                   (uint16_t *)m->k_cache + l * c.ctx_len * m->kvd, (uint16_t *)m->v_cache + l * c.ctx_len * m->kvd,
+                   c.ctx_len, m->rope, m->state};
+}
+
+static AttnArgs attn_args(aesir_model *m, int64_t l) {
+    const aesir_model_config &c = m->cfg;
+    AttnArgs a{};
+    a.q = m->q;
+    a.k = (uint16_t *)m->k_cache + l * c.ctx_len * m->kvd;
+    a.v = (uint16_t *)m->v_cache + l * c.ctx_len * m->kvd;
+    a.k_stride = m->kvd;
+    a.v_stride = m->kvd;
+    a.out = m->attn;
+    a.nq = c.n_heads;
+    a.nkv = c.n_kv_heads;
+    a.hd = m->hd;
+    a.scale = m->attn_scale;
+    a.seq_len = 0;  // S = min(pos + 1, ctx_len) from the device state
+    a.state = m->state;
+    a.max_seq = c.ctx_len;
+    a.part = m->attn_part;
+    a.max_split = m->attn_max_split;
+    return a;
+}
+
+static LmHeadArgs lm_args(aesir_model *m, bool with_ring) {
+    const aesir_model_config &c = m->cfg;
+    return LmHeadArgs{m->x, m->out_norm, m->out_eps, m->out_w, c.vocab, c.dim, m->logits, m->lm_parts, m->state,
+                      with_ring ? m->ring : nullptr};
+}
+
 static int32_t enqueue_step(aesir_model *m, hipStream_t s) {
     const aesir_model_config &c = m->cfg;
-    const int64_t d = c.dim, kvd = m->kvd;
-    AESIR_TRY(launch_embed(s, m->tok_embd, d, 0, m->state, m->x));
+    const int64_t d = c.dim;
     for (int64_t l = 0; l < c.n_layers; l++) {
         const ModelLayer &L = m->layers[l];
-        uint16_t *kc = (uint16_t *)m->k_cache + l * c.ctx_len * kvd;
-        uint16_t *vc = (uint16_t *)m->v_cache + l * c.ctx_len * kvd;
-        QkvArgs q{m->x, L.attn_norm, c.rms_eps, L.wqkv, d, kvd, m->hd, m->q, kc, vc, c.ctx_len, m->rope, m->state};
-        AESIR_TRY(launch_qkv_rope_kv(s, q));
-        AttnArgs a{};
-        a.q = m->q;
-        a.k = kc;
-        a.v = vc;
-        a.k_stride = kvd;
-        a.v_stride = kvd;
-        a.out = m->attn;
-        a.nq = c.n_heads;
-        a.nkv = c.n_kv_heads;
-        a.hd = m->hd;
-        a.scale = m->attn_scale;
-        a.seq_len = 0;
-        a.state = m->state;
-        a.max_seq = c.ctx_len;
-        a.part = m->attn_part;
-        a.counters = m->attn_counters;
-        a.max_split = m->attn_max_split;
-        AESIR_TRY(launch_attention_decode(s, a));
+        AESIR_TRY(launch_qkv_rope_kv(s, qkv_args(m, l)));  // layer 0 also performs the embedding lookup
+        AESIR_TRY(launch_attention_decode(s, attn_args(m, l)));
         AESIR_TRY(launch_gemv_residual(s, L.wo, d, d, m->attn, m->x));
         AESIR_TRY(launch_gate_up_swiglu(s, m->x, L.ffn_norm, c.rms_eps, L.wgu, c.ffn, d, m->act));
         AESIR_TRY(launch_gemv_residual(s, L.wdown, d, c.ffn, m->act, m->x));
     }
-    LmHeadArgs h{m->x, m->out_norm, m->out_eps, m->out_w, c.vocab, d, m->logits, m->lm_parts, m->lm_counter,
-                 m->state, m->ring};
-    return launch_lm_head_argmax(s, h);
+    return launch_lm_head_argmax(s, lm_args(m, true));
 }
 
 static int32_t ensure_rope(aesir_model *m, int64_t max_pos) {
@@ -325,9 +337,6 @@ int32_t aesir_model_create(aesir_ctx *ctx, const aesir_model_config *cfg, aesir_
     void *p = nullptr;
     take(attention_partial_floats(c.n_heads, hd, max_split) * 4, &p);
     m->attn_part = (float *)p;
-    take((c.n_kv_heads + 1) * 4, &p);
-    m->attn_counters = (uint32_t *)p;
-    m->lm_counter = m->attn_counters + c.n_kv_heads;
     take(lm_head_groups(V) * 8, &m->lm_parts);
     take(sizeof(DecodeState), &p);
     m->state = (DecodeState *)p;
@@ -335,7 +344,7 @@ int32_t aesir_model_create(aesir_ctx *ctx, const aesir_model_config *cfg, aesir_
     take(m->ring_cap * 8, &p);
     m->ring = (int64_t *)p;
     if (rc != AESIR_OK) return fail_cleanup(rc);
-    // The well may hold an earlier model's bytes: clear the weights and every counter.
+    // The well may hold an earlier model's bytes: clear the whole model region.
     const int64_t used = (ctx->well_offset - m->well_start) * 2;
     if (hipMemsetAsync(ctx->well_base + m->well_start * 2, 0, (size_t)used, ctx->stream) != hipSuccess)
         return fail_cleanup(fail(AESIR_ERR_HIP, "hipMemsetAsync of the model region failed"));
@@ -478,40 +487,24 @@ int32_t aesir_model_kernel_times(aesir_model *m, int64_t pos, int32_t iters, flo
     AESIR_TRY(upload_state(m, 0, pos, 0, m->ring_cap));
     hipStream_t s = m->ctx->stream;
     const aesir_model_config &c = m->cfg;
-    const int64_t d = c.dim, kvd = m->kvd;
+    const int64_t d = c.dim;
     // Class k is launched back to back, cycling through the layers so that no layer's weights
-    // are re-read from cache; time per launch = events / launches.
+    // are re-read from cache; time per launch = HIP-event time / launches.
     for (int cls = 0; cls < 7; cls++) {
-        const int64_t per_iter = (cls == 0 || cls == 6) ? 1 : c.n_layers;
-        int32_t rc = AESIR_OK;
+        const int64_t per_iter = cls >= 5 ? 1 : c.n_layers;
         auto launch = [&](int64_t l) -> int32_t {
             const ModelLayer &L = m->layers[l];
-            uint16_t *kc = (uint16_t *)m->k_cache + l * c.ctx_len * kvd;
-            uint16_t *vc = (uint16_t *)m->v_cache + l * c.ctx_len * kvd;
             switch (cls) {
-                case 0: return launch_embed(s, m->tok_embd, d, 0, m->state, m->x);
-                case 1: {
-                    QkvArgs q{m->x, L.attn_norm, c.rms_eps, L.wqkv, d, kvd, m->hd, m->q, kc, vc, c.ctx_len, m->rope, m->state};
-                    return launch_qkv_rope_kv(s, q);
-                }
-                case 2: {
-                    AttnArgs a{};
-                    a.q = m->q; a.k = kc; a.v = vc; a.k_stride = kvd; a.v_stride = kvd; a.out = m->attn;
-                    a.nq = c.n_heads; a.nkv = c.n_kv_heads; a.hd = m->hd; a.scale = m->attn_scale;
-                    a.seq_len = 0; a.state = m->state; a.max_seq = c.ctx_len; a.part = m->attn_part;
-                    a.counters = m->attn_counters; a.max_split = m->attn_max_split;
-                    return launch_attention_decode(s, a);
-                }
-                case 3: return launch_gemv_residual(s, L.wo, d, d, m->attn, m->x);
-                case 4: return launch_gate_up_swiglu(s, m->x, L.ffn_norm, c.rms_eps, L.wgu, c.ffn, d, m->act);
-                case 5: return launch_gemv_residual(s, L.wdown, d, c.ffn, m->act, m->x);
-                default: {
-                    LmHeadArgs h{m->x, m->out_norm, m->out_eps, m->out_w, c.vocab, d, m->logits, m->lm_parts,
-                                 m->lm_counter, m->state, nullptr};
-                    return launch_lm_head_argmax(s, h);
-                }
+                case 0: return launch_qkv_rope_kv(s, qkv_args(m, l));
+                case 1: return launch_attention_decode(s, attn_args(m, l));
+                case 2: return launch_gemv_residual(s, L.wo, d, d, m->attn, m->x);
+                case 3: return launch_gate_up_swiglu(s, m->x, L.ffn_norm, c.rms_eps, L.wgu, c.ffn, d, m->act);
+                case 4: return launch_gemv_residual(s, L.wdown, d, c.ffn, m->act, m->x);
+                case 5: return launch_lm_head(s, lm_args(m, false));
+                default: return launch_argmax_finish(s, m->lm_parts, lm_head_groups(c.vocab), m->state, nullptr, nullptr);
             }
         };
+        int32_t rc = AESIR_OK;
         for (int64_t l = 0; l < per_iter && rc == AESIR_OK; l++) rc = launch(l);  // warm-up
         if (rc != AESIR_OK) return rc;
         AESIR_HIP_TRY(hipEventRecord(m->ctx->ev_start, s));

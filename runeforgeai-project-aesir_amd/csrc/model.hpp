@@ -62,7 +62,6 @@ struct aesir_model {
     void *k_cache = nullptr, *v_cache = nullptr;  // [n_layers][ctx_len][kvd]
     void *x = nullptr, *q = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr;
     float *attn_part = nullptr;
-    uint32_t *attn_counters = nullptr, *lm_counter = nullptr;
     int64_t attn_max_split = 1;
     void *lm_parts = nullptr;
     aesir::DecodeState *state = nullptr;  // device

@@ -76,8 +76,7 @@ int32_t aesir_attn_gqa_decode(aesir_ctx *ctx, const void *query, int64_t query_r
     a.seq_len = seq_len;
     a.state = nullptr;
     a.max_seq = seq_len;
-    int64_t max_split = (seq_len + 63) / 64;
-    if (max_split > 128) max_split = 128;
+    int64_t max_split = attention_split_count(head_dim, seq_len);
     while (max_split > 1 && attention_partial_floats(nq, head_dim, max_split) > ctx->scratch.attn_part_floats)
         max_split >>= 1;
     if (attention_partial_floats(nq, head_dim, max_split) > ctx->scratch.attn_part_floats)

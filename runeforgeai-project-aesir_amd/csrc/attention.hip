@@ -47,7 +47,7 @@ __global__ __launch_bounds__(kAThreads) void attn_decode_kernel(AttnArgs a) {
     int64_t chunk = (S + a.max_split - 1) / a.max_split;
     chunk = (chunk + kTile - 1) / kTile * kTile;
     const int64_t nsplit = (S + chunk - 1) / chunk;
-    if (split >= nsplit) return;  // idle workgroup: does not take part in the merge count
+    if (split >= nsplit) return;  // idle workgroup
     const int64_t p0 = split * chunk;
     const int64_t p1 = p0 + chunk < S ? p0 + chunk : S;
 
@@ -246,6 +246,294 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(AttnArgs a) {
     }
 }
 
+// ------------------------------------------------------------------ fast path (head_dim 64 / 128)
+//
+// Partial kernel, grid (split, kv_head, head_group). A workgroup owns GH query heads of one KV
+// head and a chunk of whole 64-position rounds (one round for S <= 64 * max_split). All K and V
+// requests of a round are issued together before any of them is used, so a round costs one HBM
+// round trip:
+//   scores   thread t holds dims [16c, 16c + 16) (c = t % TPP) of K rows t / TPP (+ 256 / TPP)
+//            and the matching q slices of its GH heads; fdot2 partials are reduced over the TPP
+//            lanes of a row, one score per (head, position) lands in LDS
+//   V        16-byte loads into LDS, one 256-byte row slice per position
+//   softmax  wave h owns head h: one position per lane, round max and sum are wave reductions,
+//            the running max / sum stay in that wave's registers (f32 online softmax across
+//            rounds), probabilities go back to LDS
+//   P V      thread t owns one (head, dim pair) and accumulates over the round from LDS
+// The next round's K/V requests are issued before the current round is consumed.
+// Each split writes [m, l, acc[HD]] (f32, acc unnormalized); with a single split the kernel
+// writes the f16 output itself. attn_fast_merge_kernel (one workgroup per query head) merges.
+constexpr int kRound = 64;           // positions per round (one softmax lane each)
+constexpr int kMaxFastSplit = 2048;  // splits per KV head of the fast path
+
+// S of a decode launch: the view length, or min(pos + 1, max_seq) from the device state.
+__device__ __forceinline__ int64_t decode_seq_len(const AttnArgs &a) {
+    if (a.seq_len > 0) return a.seq_len;
+    const int64_t pos = a.state->pos;
+    return pos + 1 < a.max_seq ? pos + 1 : a.max_seq;
+}
+
+// Positions per split for S positions (whole rounds, at most max_split splits).
+__device__ __forceinline__ int64_t split_chunk(int64_t S, int64_t max_split) {
+    int64_t chunk = (S + max_split - 1) / max_split;
+    return (chunk + kRound - 1) / kRound * kRound;
+}
+
+template <int HD, int GH>
+__global__ __launch_bounds__(kAThreads) void attn_fast_kernel(AttnArgs a) {
+    constexpr int TPP = HD / 16;              // score threads per K row (16 dims each)
+    constexpr int RPP = kAThreads / TPP;      // K rows per score pass
+    constexpr int NSP = kRound / RPP;         // score passes per round (2 for HD 128, 1 for HD 64)
+    constexpr int VCH = HD / 8;               // 16-byte chunks per V row slice
+    constexpr int NVL = kRound * VCH / kAThreads;  // V loads per thread per round
+    constexpr int kItems = GH * HD / 2;       // PV items: (head, dim pair)
+    constexpr int PVS = kAThreads / kItems;   // PV position groups (1, 2, 4 or 8)
+    constexpr int NPOS = kRound / PVS;        // positions per thread per round in the PV pass
+    static_assert(NSP * RPP == kRound && NVL * kAThreads == kRound * VCH && kItems * PVS == kAThreads, "shape");
+    __shared__ __align__(16) float sc[GH][kRound];  // scores, then probabilities
+    __shared__ __align__(16) h16 vs[kRound][HD];
+    __shared__ float alpha[GH], mrun[GH], lrun[GH];
+    __shared__ float2 pvx[PVS > 1 ? PVS - 1 : 1][kItems];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t G = a.nq / a.nkv;
+    const int g = blockIdx.y, hg = blockIdx.z;
+    const int split = blockIdx.x;
+    const int64_t S = decode_seq_len(a);
+    const int64_t chunk = split_chunk(S, a.max_split);
+    const int64_t p0 = (int64_t)split * chunk;
+    if (p0 >= S) return;  // idle workgroup
+    const int nsplit = (int)((S + chunk - 1) / chunk);
+    const int64_t p1 = p0 + chunk < S ? p0 + chunk : S;
+    const int64_t head0 = (int64_t)g * G + (int64_t)hg * GH;  // first query head of this workgroup
+
+    const int sp = tid / TPP, sc_c = tid % TPP;                  // score row / dim chunk
+    const int item = tid % kItems, pg = tid / kItems;            // PV item / position group
+    const int ph = item / (HD / 2), pd = (item % (HD / 2)) * 2;  // PV head / dim pair
+    const h16 *Kb = reinterpret_cast<const h16 *>(a.k) + (int64_t)g * HD + 16 * sc_c;
+    const h16 *Vb = reinterpret_cast<const h16 *>(a.v) + (int64_t)g * HD;
+
+    // K/V requests of one round (rows past p1 re-read row t0 and are masked)
+    auto load_round = [&](int64_t t0, u32x4 (&kr)[NSP][2], u32x4 (&vr)[NVL]) {
+        const int n = (int)(p1 - t0 < kRound ? p1 - t0 : kRound);
+#pragma unroll
+        for (int i = 0; i < NSP; i++) {
+            const int r = sp + i * RPP;
+            const int64_t p = t0 + (r < n ? r : 0);
+            kr[i][0] = ld16(Kb + p * a.k_stride);
+            kr[i][1] = ld16(Kb + p * a.k_stride + 8);
+        }
+#pragma unroll
+        for (int i = 0; i < NVL; i++) {
+            const int e = tid + i * kAThreads, r = e / VCH, c = e % VCH;
+            vr[i] = ld16(Vb + (t0 + (r < n ? r : 0)) * a.v_stride + 8 * c);
+        }
+    };
+    u32x4 kr[NSP][2], vr[NVL], kn[NSP][2], vn[NVL];
+    load_round(p0, kr, vr);
+    u32x4 qr[GH][2];
+    {
+        const h16 *qb = reinterpret_cast<const h16 *>(a.q) + head0 * HD + 16 * sc_c;
+#pragma unroll
+        for (int h = 0; h < GH; h++) {
+            qr[h][0] = ld16(qb + h * HD);
+            qr[h][1] = ld16(qb + h * HD + 8);
+        }
+    }
+    float m_w = -INFINITY, l_w = 0.0f;  // running softmax state of head `wave` (waves < GH)
+    float acc0 = 0.0f, acc1 = 0.0f;
+    for (int64_t t0 = p0; t0 < p1; t0 += kRound) {
+        const int n_here = (int)(p1 - t0 < kRound ? p1 - t0 : kRound);
+        const bool more = t0 + kRound < p1;  // uniform
+        if (more) load_round(t0 + kRound, kn, vn);  // next round in flight during this one
+        // scores
+#pragma unroll
+        for (int i = 0; i < NSP; i++) {
+#pragma unroll
+            for (int h = 0; h < GH; h++) {
+                float d = dot8(kr[i][0], qr[h][0], 0.0f);
+                d = dot8(kr[i][1], qr[h][1], d);
+#pragma unroll
+                for (int o = 1; o < TPP; o <<= 1) d += __shfl_xor(d, o, kWave);
+                if (sc_c == 0) sc[h][sp + i * RPP] = d * a.scale;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NVL; i++) {
+            const int e = tid + i * kAThreads, r = e / VCH, c = e % VCH;
+            st16(&vs[r][8 * c], vr[i]);
+        }
+        __syncthreads();
+        // online softmax of head `wave` over the round (one position per lane)
+        if (wave < GH) {
+            const float s = lane < n_here ? sc[wave][lane] : -INFINITY;
+            const float mn = fmaxf(m_w, wave_max(s));
+            const float pr = lane < n_here ? expf(s - mn) : 0.0f;
+            const float al = expf(m_w - mn);  // 0 on the first round (m_w = -inf)
+            l_w = l_w * al + wave_sum(pr);
+            m_w = mn;
+            sc[wave][lane] = pr;
+            if (lane == 0) alpha[wave] = al;
+        }
+        __syncthreads();
+        // P V over this thread's positions of the round (probabilities are 0 beyond n_here)
+        {
+            const float al = alpha[ph];
+            acc0 *= al;
+            acc1 *= al;
+#pragma unroll
+            for (int j = 0; j < NPOS; j += 4) {
+                const f32x4 w = *reinterpret_cast<const f32x4 *>(&sc[ph][pg * NPOS + j]);
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const h16x2 v = *reinterpret_cast<const h16x2 *>(&vs[pg * NPOS + j + u][pd]);
+                    acc0 = fmaf(w[u], (float)v.x, acc0);
+                    acc1 = fmaf(w[u], (float)v.y, acc1);
+                }
+            }
+        }
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < NSP; i++) {
+                kr[i][0] = kn[i][0];
+                kr[i][1] = kn[i][1];
+            }
+#pragma unroll
+            for (int i = 0; i < NVL; i++) vr[i] = vn[i];
+        }
+        __syncthreads();  // sc and vs are rewritten by the next round
+    }
+
+    // combine the PV position groups, then write the partial (or the output for one split)
+    if (wave < GH && lane == 0) {
+        mrun[wave] = m_w;
+        lrun[wave] = l_w;
+    }
+    if (PVS > 1 && pg > 0) pvx[pg - 1][item] = float2{acc0, acc1};
+    __syncthreads();
+    if (pg != 0) return;
+#pragma unroll
+    for (int j = 0; j < PVS - 1; j++) {
+        const float2 o = pvx[j][item];
+        acc0 += o.x;
+        acc1 += o.y;
+    }
+    if (nsplit == 1) {
+        h16 *out = reinterpret_cast<h16 *>(a.out) + (head0 + ph) * HD + pd;
+        out[0] = (h16)(acc0 / lrun[ph]);
+        out[1] = (h16)(acc1 / lrun[ph]);
+    } else {
+        float *pp = a.part + ((head0 + ph) * a.max_split + split) * (HD + 2);
+        *reinterpret_cast<float2 *>(pp + 2 + pd) = float2{acc0, acc1};
+        if (pd == 0) *reinterpret_cast<float2 *>(pp) = float2{mrun[ph], lrun[ph]};
+    }
+}
+
+// Merge of the split partials, one workgroup per query head: w_s = exp(m_s - max m),
+// out = f16(sum_s w_s acc_s / sum_s w_s l_s). Thread t owns dim pair t % (HD/2) over the splits
+// s = t / (HD/2) (mod NG); its first accumulator loads are issued before the weights are known.
+template <int HD>
+__global__ __launch_bounds__(kAThreads) void attn_fast_merge_kernel(AttnArgs a) {
+    constexpr int NDP = HD / 2;
+    constexpr int NG = kAThreads / NDP;
+    constexpr int kPre = 8;
+    constexpr int kW = kAThreads / kWave;
+    __shared__ float wsh[kMaxFastSplit];
+    __shared__ float red[kW];
+    __shared__ float2 gx[NG][NDP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t S = decode_seq_len(a);
+    const int64_t chunk = split_chunk(S, a.max_split);
+    const int nsplit = (int)((S + chunk - 1) / chunk);
+    if (nsplit <= 1) return;  // the partial kernel wrote the output
+    const int64_t h = blockIdx.x;
+    const float *base = a.part + h * a.max_split * (HD + 2);
+    const int dp = tid % NDP, sg = tid / NDP;
+
+    float2 pre[kPre];
+#pragma unroll
+    for (int j = 0; j < kPre; j++) {
+        const int s = sg + NG * j;
+        pre[j] = s < nsplit ? *reinterpret_cast<const float2 *>(base + (int64_t)s * (HD + 2) + 2 + 2 * dp)
+                            : float2{0.0f, 0.0f};
+    }
+    float mloc = -INFINITY;
+    for (int s = tid; s < nsplit; s += kAThreads) mloc = fmaxf(mloc, base[(int64_t)s * (HD + 2)]);
+    mloc = wave_max(mloc);
+    if (lane == 0) red[wave] = mloc;
+    __syncthreads();
+    float M = red[0];
+#pragma unroll
+    for (int w = 1; w < kW; w++) M = fmaxf(M, red[w]);
+    __syncthreads();
+    float lsum = 0.0f;
+    for (int s = tid; s < nsplit; s += kAThreads) {
+        const float2 ml = *reinterpret_cast<const float2 *>(base + (int64_t)s * (HD + 2));
+        const float e = expf(ml.x - M);
+        wsh[s] = e;
+        lsum = fmaf(ml.y, e, lsum);
+    }
+    const float L = block_sum<kW>(lsum, red);  // also publishes wsh
+    float x0 = 0.0f, x1 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kPre; j++) {
+        const int s = sg + NG * j;
+        if (s < nsplit) {
+            x0 = fmaf(pre[j].x, wsh[s], x0);
+            x1 = fmaf(pre[j].y, wsh[s], x1);
+        }
+    }
+    for (int s0 = sg + NG * kPre; s0 < nsplit; s0 += NG * kPre) {  // kPre loads in flight per batch
+        float2 v[kPre];
+#pragma unroll
+        for (int j = 0; j < kPre; j++) {
+            const int s = s0 + NG * j;
+            v[j] = s < nsplit ? *reinterpret_cast<const float2 *>(base + (int64_t)s * (HD + 2) + 2 + 2 * dp)
+                              : float2{0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int j = 0; j < kPre; j++) {
+            const int s = s0 + NG * j;
+            if (s < nsplit) {
+                x0 = fmaf(v[j].x, wsh[s], x0);
+                x1 = fmaf(v[j].y, wsh[s], x1);
+            }
+        }
+    }
+    gx[sg][dp] = float2{x0, x1};
+    __syncthreads();
+    if (sg != 0) return;
+#pragma unroll
+    for (int j = 1; j < NG; j++) {
+        x0 += gx[j][dp].x;
+        x1 += gx[j][dp].y;
+    }
+    h16 *out = reinterpret_cast<h16 *>(a.out) + h * HD + 2 * dp;
+    out[0] = (h16)(x0 / L);
+    out[1] = (h16)(x1 / L);
+}
+
+// Query heads per workgroup of the fast path (0: the generic kernels serve this shape).
+static int fast_group(const AttnArgs &a) {
+    const int64_t G = a.nq / a.nkv;
+    if (a.hd != 64 && a.hd != 128) return 0;
+    if (a.max_split > kMaxFastSplit) return 0;
+    if (a.k_stride % 8 != 0 || a.v_stride % 8 != 0) return 0;
+    if (((uintptr_t)a.k & 15) || ((uintptr_t)a.v & 15) || ((uintptr_t)a.q & 15)) return 0;
+    return G % 4 == 0 ? 4 : G % 2 == 0 ? 2 : 1;
+}
+
+// Split count: one 64-position round per split up to 64 splits (more splits cost more in the
+// merge than they gain in parallelism on MI355X; longer views give each split several rounds).
+int64_t attention_split_count(int64_t hd, int64_t max_positions) {
+    const bool fast = hd == 64 || hd == 128;
+    const int64_t per = fast ? kRound : kTile;
+    const int64_t cap = fast ? 64 : kMaxSplit;
+    int64_t n = (max_positions + per - 1) / per;
+    if (n > cap) n = cap;
+    return n < 1 ? 1 : n;
+}
+
 static int64_t attn_lds_bytes(int64_t G, int64_t hd) {
     return (int64_t)kTile * (hd + 8) * 2 + (int64_t)kTile * hd * 2 + G * kTile * 4 + G * hd * 2 + G * 4 + 64;
 }
@@ -257,8 +545,28 @@ int32_t launch_attention_decode(hipStream_t s, const AttnArgs &a) {
     if (G > kMaxG) return fail(AESIR_ERR_UNSUPPORTED, "attention: %lld query heads per KV head exceeds %d", (long long)G, kMaxG);
     if (G * a.hd / 2 > (int64_t)kAThreads * kMaxPvPasses)
         return fail(AESIR_ERR_UNSUPPORTED, "attention: query group x head_dim too large");
-    if (a.max_split < 1 || a.max_split > kMaxSplit) return fail(AESIR_ERR_INVALID, "attention: bad split count");
+    if (a.max_split < 1 || a.max_split > kMaxFastSplit) return fail(AESIR_ERR_INVALID, "attention: bad split count");
     if (a.hd / 2 > kMergeThreads * 64) return fail(AESIR_ERR_UNSUPPORTED, "attention: head_dim too large for the merge");
+    if (const int gh = fast_group(a)) {
+        const dim3 grid((unsigned)a.max_split, (unsigned)a.nkv, (unsigned)(G / gh));
+#define AESIR_ATTN_FAST(HDV, GHV)                                                              \
+    if (a.hd == HDV && gh == GHV) hipLaunchKernelGGL((attn_fast_kernel<HDV, GHV>), grid, dim3(kAThreads), 0, s, a);
+        AESIR_ATTN_FAST(128, 4)
+        AESIR_ATTN_FAST(128, 2)
+        AESIR_ATTN_FAST(128, 1)
+        AESIR_ATTN_FAST(64, 4)
+        AESIR_ATTN_FAST(64, 2)
+        AESIR_ATTN_FAST(64, 1)
+#undef AESIR_ATTN_FAST
+        AESIR_LAUNCH_CHECK("attn_fast_kernel");
+        if (a.hd == 128)
+            hipLaunchKernelGGL(attn_fast_merge_kernel<128>, dim3((unsigned)a.nq), dim3(kAThreads), 0, s, a);
+        else
+            hipLaunchKernelGGL(attn_fast_merge_kernel<64>, dim3((unsigned)a.nq), dim3(kAThreads), 0, s, a);
+        AESIR_LAUNCH_CHECK("attn_fast_merge_kernel");
+        return AESIR_OK;
+    }
+    if (a.max_split > kMaxSplit) return fail(AESIR_ERR_INVALID, "attention: bad split count");
     const bool vec = a.hd % 8 == 0 && a.k_stride % 8 == 0 && a.v_stride % 8 == 0 && ((uintptr_t)a.k & 15) == 0 &&
                      ((uintptr_t)a.v & 15) == 0 && ((uintptr_t)a.q & 15) == 0;
     const int64_t lds = attn_lds_bytes(G, a.hd);

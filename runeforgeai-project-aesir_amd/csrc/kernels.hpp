@@ -84,9 +84,12 @@ struct AttnArgs {
     float *part;                // partials [nq][max_split][hd + 2]
     int64_t max_split;          // <= 128
 };
-// Two launches: split-KV partials, then the merge (one workgroup per query head).
+// Two launches: split-KV partials (register/LDS fast path for head_dim 64 and 128, generic
+// LDS-tiled kernel otherwise), then the merge (one workgroup per query head).
 int32_t launch_attention_decode(hipStream_t s, const AttnArgs &a);
 int64_t attention_partial_floats(int64_t nq, int64_t hd, int64_t max_split);
+// Split count for a KV view of up to max_positions rows.
+int64_t attention_split_count(int64_t hd, int64_t max_positions);
 
 // ------------------------------------------------------------------ elementwise (basic.hip)
 int32_t launch_rmsnorm(hipStream_t s, void *T, int64_t rows, int64_t cols, const void *w, float eps);

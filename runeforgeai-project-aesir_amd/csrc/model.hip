@@ -331,8 +331,7 @@ int32_t aesir_model_create(aesir_ctx *ctx, const aesir_model_config *cfg, aesir_
     take(d * 2, &m->attn);
     take(f * 2, &m->act);
     take(V * 2, &m->logits);
-    int64_t max_split = (c.ctx_len + 63) / 64;
-    if (max_split > 128) max_split = 128;
+    const int64_t max_split = attention_split_count(hd, c.ctx_len);
     m->attn_max_split = max_split;
     void *p = nullptr;
     take(attention_partial_floats(c.n_heads, hd, max_split) * 4, &p);

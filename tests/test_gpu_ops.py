@@ -206,11 +206,18 @@ def test_attention_single_position_maps_heads(A, ctx):
 
 
 @pytest.mark.parametrize("S,hd,nq,nkv", [(37, 16, 8, 2), (80, 8, 8, 4), (512, 64, 32, 4), (2048, 128, 32, 8),
-                                         (8192, 128, 32, 8), (200, 40, 4, 2), (65, 128, 32, 8)])
+                                         (8192, 128, 32, 8), (200, 40, 4, 2), (65, 128, 32, 8),
+                                         # register-resident path (head_dim 64/128): one split, a
+                                         # partial last tile, ragged splits, 1/2/3/4/8 heads per KV
+                                         # head, many tiles per split
+                                         (31, 128, 32, 8), (33, 128, 32, 8), (2049, 128, 32, 8),
+                                         (100, 128, 16, 8), (777, 64, 8, 8), (300, 64, 12, 4),
+                                         (1000, 64, 32, 4), (4097, 64, 32, 4), (32768, 128, 32, 8)])
 def test_attention_vs_oracle_and_f64(A, ctx, oracle, S, hd, nq, nkv):
     q, K, V, out = attn_case(ctx, A, S, hd, nq, nkv)
-    ref_o = oracle.attn_gqa(q, K, V, np.zeros((1, nq * hd), np.float16), S, hd, nq, nkv)
-    assert within_tol(out, ref_o)
+    if S <= 8192:  # beyond this the reference's per-position f16 accumulator itself drifts
+        ref_o = oracle.attn_gqa(q, K, V, np.zeros((1, nq * hd), np.float16), S, hd, nq, nkv)
+        assert within_tol(out, ref_o)
     # the f32 accumulator is closer to the exact value than the reference's f16 accumulator
     assert within_tol(out[0], f64_attention(q, K, V, S, hd, nq, nkv), atol=2e-3, rtol=2e-3)
 
@@ -219,6 +226,16 @@ def test_attention_peaked_scores(A, ctx, oracle):
     """Large logits: the online softmax must rescale across tiles and splits correctly."""
     q, K, V, out = attn_case(ctx, A, 3000, 128, 32, 8, scale_kv=4.0)
     assert within_tol(out[0], f64_attention(q, K, V, 3000, 128, 32, 8), atol=2e-3, rtol=2e-3)
+
+
+def test_attention_repeated_calls_reuse_merge_counters(A, ctx):
+    """The split merge of the head_dim 64/128 path finds its last workgroup with device counters that
+    the merging workgroup resets; back-to-back calls with shrinking and growing split counts must
+    all merge."""
+    hd, nq, nkv = 128, 32, 8
+    for S in (2048, 40, 1, 700, 2048, 33):
+        q, K, V, out = attn_case(ctx, A, S, hd, nq, nkv)
+        assert within_tol(out[0], f64_attention(q, K, V, S, hd, nq, nkv), atol=2e-3, rtol=2e-3), S
 
 
 def test_attention_no_op_cases(A, ctx):

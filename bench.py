@@ -85,6 +85,36 @@ def cpu_baseline(kv_len: int, reps: int) -> dict:
             "simd": bool(O.lib().ao_simd_enabled())}
 
 
+COPY_BYTES = 256 << 20
+
+
+def calibrate_copy():
+    """One plain copy of COPY_BYTES between two device buffers (after a warm-up copy): the kernel
+    whose FETCH_SIZE / WRITE_SIZE readings calibrate the counters against a known byte count."""
+    import torch
+
+    a = torch.empty(COPY_BYTES // 4, dtype=torch.int32, device="cuda").fill_(1)
+    b = torch.empty_like(a)
+    b.copy_(a)
+    torch.cuda.synchronize()
+    b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy_bytes": COPY_BYTES}))
+
+
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, each scaled by its copy-kernel calibration factor), or None."""
+    path = os.path.join(REPO, "profiles", "pmc_gate_up_swiglu_llama3_8b.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -96,7 +126,13 @@ def main():
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="launch kernels one by one instead of graph replay")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run only a plain 256 MiB device-to-device copy (the FETCH_SIZE / WRITE_SIZE calibration "
+                         "of the HBM traffic figure) and exit")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU only (the decode path is single-GPU; multi-GPU tensor "
@@ -152,7 +188,7 @@ def main():
                      "event_ms_per_step": round(event_ms / args.steps, 4)},
         "roofline": {"bound": "hbm", "kernel": "gate_up_swiglu (rmsnorm + [2x14336x4096] GEMV + SwiGLU)",
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "avg_launch_ms": round(gu_ms, 5), "bytes_per_launch": GATE_UP_BYTES},
         "kernel_ms": {k: round(v, 5) for k, v in kt.items()},
         "tokens_head": toks[:8],

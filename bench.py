@@ -1,8 +1,8 @@
-"""Batch-1 decode benchmark of the MI355X Llama F16 forward path (BASELINE metric).
+"""Batch-1 decode benchmark of the MI355X Llama F16 forward path: tok/s and achieved HBM GB/s.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--kv 2048] [--no-cpu-baseline]
 
-Workload (BASELINE config 4): Llama-3-8B shape F16, random-init N(0, 0.02) on the device, batch 1,
+Workload: Llama-3-8B shape F16, random-init N(0, 0.02) on the device, batch 1,
 greedy decode with the KV cache pre-filled to --kv positions (N(0,1) f16). A step is one full
 forward pass (embedding, 32 layers, output norm, lm_head, argmax) on one token, each step
 consuming the previous step's argmax on the device (HIP graph replay). Prints one JSON line.
@@ -23,12 +23,12 @@ sys.path.insert(0, REPO)
 
 HBM_PEAK_GBS = 8000.0
 
-# Llama-3-8B shape (BASELINE config 4). head_dim = 4096 / 32 = 128, kv_dim = 1024.
+# Llama-3-8B shape. head_dim = 4096 / 32 = 128, kv_dim = 1024.
 DIM, LAYERS, HEADS, KV_HEADS, FFN, VOCAB = 4096, 32, 32, 8, 14336, 128256
 KV_DIM = DIM // HEADS * KV_HEADS
 
 # Algorithmic HBM bytes of one decode token: every weight matrix once, norms, one embedding row,
-# K+V read over L positions and written at one (SURVEY 8(d) / BASELINE 2b).
+# K+V read over L positions and written at one.
 LAYER_WEIGHT_BYTES = 2 * ((DIM + 2 * KV_DIM) * DIM + DIM * DIM + 2 * FFN * DIM + DIM * FFN + 2 * DIM)
 TOKEN_WEIGHT_BYTES = LAYERS * LAYER_WEIGHT_BYTES + 2 * VOCAB * DIM + 2 * DIM + 2 * DIM
 KV_BYTES_PER_POS = LAYERS * 2 * KV_DIM * 2

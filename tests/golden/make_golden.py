@@ -2,7 +2,7 @@
 
     python tests/golden/make_golden.py
 
-tiny_stream.npz: BASELINE config 1 (stories260K shape, random-init N(0, 0.02) from SEED), a
+tiny_stream.npz: the tiny model (stories260K shape, random-init N(0, 0.02) from SEED), a
 16-token RuneRNG prompt and the 64 greedy tokens the oracle produces, plus its last f16 logits.
 micro_small.npz: small-size micro-suite outputs (GEMV, RMSNorm, RoPE, argmax) on seeded inputs.
 """

@@ -1,6 +1,6 @@
 """GPU parity of the whole forward path (forward_pass / generation loop) against the CPU oracle.
 
-- tiny model (BASELINE config 1, stories260K shape): identical greedy token stream (16-token seeded
+- tiny model (stories260K shape): identical greedy token stream (16-token seeded
   prompt, 64 tokens) and per-step logits within max-abs 2e-2 / rel 1e-2, also from a GGUF v3 file;
 - TinyLlama shape (dims of config 3, 2 of its 22 layers so the oracle stays in seconds): logits
   within tolerance, identical tokens;

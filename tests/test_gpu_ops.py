@@ -5,7 +5,7 @@ Bars: bit-exact for integer/index work (argmax, KV copies, embedding) and for th
 f16 ops whose arithmetic is fully determined (RoPE with the host-built table, SwiGLU product,
 residual add, SiLU). Reductions in f32 (GEMV, RMSNorm's sum of squares) may differ from the
 oracle's summation order by at most 1 f16 ulp. Attention keeps an f32 accumulator where the
-reference stores f16 per position: max-abs 2e-2 / rel 1e-2 (BASELINE tolerance).
+reference stores f16 per position: max-abs 2e-2 / rel 1e-2 (the task tolerance).
 """
 import math
 

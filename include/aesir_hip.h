@@ -13,7 +13,7 @@
  *
  * Ordering: all device work of one context runs in order on that context's single HIP stream.
  * Calls return after enqueueing, except those that hand a value back to the host
- * (aesir_argmax_f16, aesir_forward_pass, aesir_generate, aesir_memcpy_d2h,
+ * (aesir_argmax_f16, aesir_forward_pass, aesir_prefill, aesir_generate, aesir_memcpy_d2h,
  * aesir_ctx_synchronize), which wait for the stream. A context is not thread-safe, like the
  * reference engine (core/thread_pool.mojo:23-29 is a stub; nothing runs in parallel).
  */
@@ -206,6 +206,15 @@ int32_t aesir_gguf_inspect(const char *path, aesir_model_config *cfg, float *rop
  * and argmax. Waits; *next_token is the greedy token. */
 int32_t aesir_forward_pass(aesir_model *model, const int64_t *tokens, int64_t n_tokens, int64_t start_pos,
                            int64_t *next_token);
+/* Batched prefill: the same result as forward_pass at each position start_pos .. start_pos +
+ * n_tokens - 1 in turn (the per-position prefill loop of _run_generation, aesir.mojo:358-374),
+ * computed with all positions of a 128-row chunk going through each layer together: MFMA f16
+ * GEMMs (f32 accumulate), causal GQA attention over the cache, K/V appended for every position.
+ * tokens[i] is evaluated at position start_pos + i. Waits; *next_token is the greedy token after
+ * the last position and aesir_model_logits returns its logits. f32 summation order differs from
+ * the per-position path (results within the forward-pass tolerance). */
+int32_t aesir_prefill(aesir_model *model, const int64_t *tokens, int64_t n_tokens, int64_t start_pos,
+                      int64_t *next_token);
 /* f16 logits [vocab] of the last forward pass, copied to the host. */
 int32_t aesir_model_logits(aesir_model *model, void *host_out);
 

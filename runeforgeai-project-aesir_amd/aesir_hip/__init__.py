@@ -97,6 +97,7 @@ _sig("aesir_forward_pass", [P, P, I64, I64, C.POINTER(I64)])
 _sig("aesir_model_logits", [P, P])
 _sig("aesir_decode_loop", [P, I64, I64, I64, I32, P, C.POINTER(F32)])
 _sig("aesir_model_kernel_times", [P, I64, I32, P, I32])
+_sig("aesir_prefill", [P, P, I64, I64, P])
 _sig("aesir_model_fill_kv_random", [P, I64, C.c_uint64, F32])
 _sig("aesir_generation_stop_reason", [I64, I64, I64, I64, P, I64, I64, I64])
 _sig("aesir_generate", [P, P, I64, C.POINTER(_GenConfig), P, C.POINTER(I64), C.POINTER(I32)])
@@ -404,6 +405,14 @@ class Model:
         out = I64()
         _check(_L.aesir_forward_pass(self.h, t.ctypes.data if t.size else None, t.size, start_pos, C.byref(out)))
         return out.value
+
+    def prefill(self, tokens, start_pos: int = 0) -> int:
+        """Batched prefill of tokens at positions start_pos..: the same KV cache and next token as
+        forward_pass at each position in turn (aesir.mojo:358-374), one pass per 128-row chunk."""
+        t = np.ascontiguousarray(np.array(tokens, dtype=np.int64))
+        nxt = I64()
+        _check(_L.aesir_prefill(self.h, t.ctypes.data, len(t), start_pos, C.byref(nxt)))
+        return nxt.value
 
     def logits(self) -> np.ndarray:
         out = np.empty(self.cfg.vocab, dtype=np.float16)

@@ -191,7 +191,7 @@ static AttnArgs attn_args(aesir_model *m, int64_t l) {
     return a;
 }
 
-static LmHeadArgs lm_args(aesir_model *m, bool with_ring) {
+LmHeadArgs lm_args(aesir_model *m, bool with_ring) {
     const aesir_model_config &c = m->cfg;
     return LmHeadArgs{m->x, m->out_norm, m->out_eps, m->out_w, c.vocab, c.dim, m->logits, m->lm_parts, m->state,
                       with_ring ? m->ring : nullptr};
@@ -211,7 +211,7 @@ static int32_t enqueue_step(aesir_model *m, hipStream_t s) {
     return launch_lm_head_argmax(s, lm_args(m, true));
 }
 
-static int32_t ensure_rope(aesir_model *m, int64_t max_pos) {
+int32_t ensure_rope(aesir_model *m, int64_t max_pos) {
     const void *t = nullptr;
     AESIR_TRY(rope_table(m->ctx, m->cfg.rope_theta, m->hd, max_pos, &t));
     if (t != m->rope) {
@@ -257,7 +257,7 @@ static int32_t run_step(aesir_model *m, bool graph) {
     return enqueue_step(m, s);
 }
 
-static int32_t upload_state(aesir_model *m, int64_t token, int64_t pos, int64_t advance, int64_t ring_cap) {
+int32_t upload_state(aesir_model *m, int64_t token, int64_t pos, int64_t advance, int64_t ring_cap) {
     DecodeState *h = m->state_host;
     std::memset(h, 0, sizeof(DecodeState));
     h->token = token;
@@ -337,6 +337,16 @@ int32_t aesir_model_create(aesir_ctx *ctx, const aesir_model_config *cfg, aesir_
     take(attention_partial_floats(c.n_heads, hd, max_split) * 4, &p);
     m->attn_part = (float *)p;
     take(lm_head_groups(V) * 8, &m->lm_parts);
+    m->pf_rows = c.ctx_len < 128 ? c.ctx_len : 128;  // batched-prefill chunk
+    const int64_t pr = m->pf_rows;
+    take(pr * d * 2, &m->pf_x);
+    take(pr * d * 2, &m->pf_xn);
+    take(pr * (d + 2 * kvd) * 2, &m->pf_qkv);
+    take(pr * d * 2, &m->pf_q);
+    take(pr * d * 2, &m->pf_att);
+    take(pr * f * 2, &m->pf_act);
+    take(pr * 2 * f * 2, &m->pf_gu);
+    take(pr * 8, &m->pf_tokens);
     take(sizeof(DecodeState), &p);
     m->state = (DecodeState *)p;
     m->ring_cap = 65536;
@@ -545,7 +555,7 @@ int32_t aesir_generate(aesir_model *m, const int64_t *prompt, int64_t n_prompt, 
     std::vector<int64_t> cur(prompt, prompt + n_prompt);
     int64_t next = 0;
     if (gc->batched_prefill)
-        AESIR_TRY(model_prefill(m, cur.data(), n_prompt, &next));
+        AESIR_TRY(model_prefill(m, cur.data(), n_prompt, 0, &next));
     else
         for (int64_t p = 0; p < n_prompt; p++) AESIR_TRY(aesir_forward_pass(m, cur.data(), (int64_t)cur.size(), p, &next));
     int32_t reason = -1;

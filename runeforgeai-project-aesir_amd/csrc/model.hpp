@@ -63,6 +63,11 @@ struct aesir_model {
     void *x = nullptr, *q = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr;
     float *attn_part = nullptr;
     int64_t attn_max_split = 1;
+    // batched prefill workspace: pf_rows rows of x, normed x, q|k|v, q, attention out, act,
+    // gate/up products (non-MFMA shapes only) and the rows' token IDs
+    int64_t pf_rows = 0;
+    void *pf_x = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_att = nullptr, *pf_act = nullptr;
+    void *pf_gu = nullptr, *pf_tokens = nullptr;
     void *lm_parts = nullptr;
     aesir::DecodeState *state = nullptr;  // device
     aesir::DecodeState *state_host = nullptr;  // pinned staging
@@ -73,10 +78,6 @@ struct aesir_model {
     bool graph_ready = false;
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
-    // batched prefill workspace (allocated on first use)
-    int64_t prefill_cap = 0;
-    void *pf_x = nullptr, *pf_h = nullptr, *pf_qkv = nullptr, *pf_attn = nullptr, *pf_gu = nullptr, *pf_act = nullptr,
-         *pf_tmp = nullptr;
 };
 
 namespace aesir {
@@ -86,7 +87,12 @@ TensorPlace place_tensor(const aesir_model *m, const TensorRef &ref);
 std::vector<TensorRef> all_tensors(const aesir_model *m);
 std::string tensor_name(const TensorRef &ref);
 int32_t model_upload(aesir_model *m, const TensorRef &ref, const void *host, int64_t rows, int64_t cols, int32_t type);
-// Batched prefill of tokens[0..n) at positions 0..n-1; *next is the greedy token after the last.
-int32_t model_prefill(aesir_model *m, const int64_t *tokens, int64_t n, int64_t *next);
+// Batched prefill of tokens[0..n) at positions start_pos.., in chunks of pf_rows rows; *next is the
+// greedy token after the last position.
+int32_t model_prefill(aesir_model *m, const int64_t *tokens, int64_t n, int64_t start_pos, int64_t *next);
+// Decode-step helpers shared with the prefill.
+int32_t ensure_rope(aesir_model *m, int64_t max_pos);
+int32_t upload_state(aesir_model *m, int64_t token, int64_t pos, int64_t advance, int64_t ring_cap);
+LmHeadArgs lm_args(aesir_model *m, bool with_ring);
 
 }  // namespace aesir

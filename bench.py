@@ -102,6 +102,48 @@ def calibrate_copy():
     print(json.dumps({"calibrate_copy_bytes": COPY_BYTES}))
 
 
+# TinyLlama-1.1B shape (dim 2048, 22 layers, 32 q / 4 kv heads, head_dim 64, ffn 5632, vocab 32000):
+# the batched-prefill workload, 128 prompt positions then 256 greedy decode steps.
+TL = dict(dim=2048, layers=22, heads=32, kv_heads=4, ffn=5632, vocab=32000)
+TL_KVD = TL["dim"] // TL["heads"] * TL["kv_heads"]
+TL_GEMM_PARAMS = TL["layers"] * ((TL["dim"] + 2 * TL_KVD) * TL["dim"] + TL["dim"] ** 2 + 3 * TL["ffn"] * TL["dim"])
+TL_WEIGHT_BYTES = 2 * (TL_GEMM_PARAMS + TL["layers"] * 2 * TL["dim"] + TL["vocab"] * TL["dim"] + 2 * TL["dim"])
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense f16
+
+
+def prefill_bench(A, seed: int, n_prompt: int = 128, n_decode: int = 256, reps: int = 5) -> dict:
+    """Batched prefill of n_prompt positions on the TinyLlama shape (MFMA GEMMs; wall time of the
+    blocking aesir_prefill call, host launches included), then n_decode graph-replayed greedy steps."""
+    ctx = A.Context(TL_WEIGHT_BYTES + (1 << 30))
+    m = A.Model.create(ctx, A.ModelConfig(TL["dim"], TL["layers"], TL["heads"], TL["kv_heads"], TL["ffn"],
+                                          TL["vocab"], n_prompt + n_decode + 64))
+    m.init_random(seed, 0.02, 0.0, 0.02)
+    rng = np.random.default_rng(seed)
+    prompt = rng.integers(0, TL["vocab"], n_prompt).tolist()
+    nxt = m.prefill(prompt)  # warm-up
+    best = float("inf")
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        nxt = m.prefill(prompt)
+        best = min(best, time.perf_counter() - t0)
+    toks, dec = [], float("nan")
+    if n_decode > 0:
+        m.decode_loop(nxt, n_prompt, 8)  # graph capture / warm-up
+        ctx.synchronize()
+        t0 = time.perf_counter()
+        toks, _ = m.decode_loop(nxt, n_prompt, n_decode)
+        dec = time.perf_counter() - t0
+    flops = 2.0 * TL_GEMM_PARAMS * n_prompt
+    m.close()
+    ctx.close()
+    return {"workload": f"tinyllama-1.1b shape f16: {n_prompt}-token batched prefill, then {n_decode} greedy decode steps",
+            "prefill_ms": round(best * 1e3, 3), "prefill_tok_s": round(n_prompt / best, 1),
+            "gemm_tflops": round(flops / best / 1e12, 2),
+            "mfma_frac": round(flops / best / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+            "weight_gbs": round(TL_WEIGHT_BYTES / best / 1e9, 1),
+            "decode_tok_s": round(n_decode / dec, 1) if n_decode > 0 else None, "first_tokens": [nxt] + toks[:3]}
+
+
 def measured_traffic():
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary
     (FETCH_SIZE + WRITE_SIZE, each scaled by its copy-kernel calibration factor), or None."""
@@ -126,6 +168,10 @@ def main():
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="launch kernels one by one instead of graph replay")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the TinyLlama batched-prefill measurement")
+    ap.add_argument("--prefill-only", action="store_true", help="run only the TinyLlama prefill measurement")
+    ap.add_argument("--prefill-decode-steps", type=int, default=256,
+                    help="greedy decode steps after the prefill in --prefill-only runs (0: none)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain 256 MiB device-to-device copy (the FETCH_SIZE / WRITE_SIZE calibration "
                          "of the HBM traffic figure) and exit")
@@ -140,6 +186,10 @@ def main():
         sys.exit(2)
 
     import aesir_hip as A
+
+    if args.prefill_only:
+        print(json.dumps({"prefill": prefill_bench(A, args.seed, n_decode=args.prefill_decode_steps)}))
+        return
 
     ctx_len = args.kv + max(args.steps, args.warmup) + 64
     well = int(TOKEN_WEIGHT_BYTES + 2 * LAYERS * ctx_len * KV_DIM * 2 + (1 << 30))
@@ -193,13 +243,15 @@ def main():
         "kernel_ms": {k: round(v, 5) for k, v in kt.items()},
         "tokens_head": toks[:8],
     }
+    m.close()
+    ctx.close()
+    if not args.no_prefill:
+        out["prefill"] = prefill_bench(A, args.seed)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.kv, args.cpu_reps)
         out["cpu_baseline"]["value"] = round(out["cpu_baseline"]["value"], 4)
     else:
         out["cpu_baseline"] = None
-    m.close()
-    ctx.close()
     print(json.dumps(out))
 
 

@@ -347,6 +347,11 @@ int32_t aesir_model_create(aesir_ctx *ctx, const aesir_model_config *cfg, aesir_
     take(pr * f * 2, &m->pf_act);
     take(pr * 2 * f * 2, &m->pf_gu);
     take(pr * 8, &m->pf_tokens);
+    m->pf_part_floats = prefill_part_floats(pr, d, d + 2 * kvd, f);
+    if (m->pf_part_floats > 0) {
+        take(m->pf_part_floats * 4, &p);
+        m->pf_part = (float *)p;
+    }
     take(sizeof(DecodeState), &p);
     m->state = (DecodeState *)p;
     m->ring_cap = 65536;

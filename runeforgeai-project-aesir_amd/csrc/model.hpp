@@ -68,6 +68,8 @@ struct aesir_model {
     int64_t pf_rows = 0;
     void *pf_x = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_att = nullptr, *pf_act = nullptr;
     void *pf_gu = nullptr, *pf_tokens = nullptr;
+    float *pf_part = nullptr;  // f32 split-K partials of the prefill GEMMs
+    int64_t pf_part_floats = 0;
     void *lm_parts = nullptr;
     aesir::DecodeState *state = nullptr;  // device
     aesir::DecodeState *state_host = nullptr;  // pinned staging
@@ -90,6 +92,8 @@ int32_t model_upload(aesir_model *m, const TensorRef &ref, const void *host, int
 // Batched prefill of tokens[0..n) at positions start_pos.., in chunks of pf_rows rows; *next is the
 // greedy token after the last position.
 int32_t model_prefill(aesir_model *m, const int64_t *tokens, int64_t n, int64_t start_pos, int64_t *next);
+// f32 split-K partial floats the prefill GEMMs of a model with these shapes need at `rows` rows.
+int64_t prefill_part_floats(int64_t rows, int64_t dim, int64_t qkv_n, int64_t ffn);
 // Decode-step helpers shared with the prefill.
 int32_t ensure_rope(aesir_model *m, int64_t max_pos);
 int32_t upload_state(aesir_model *m, int64_t token, int64_t pos, int64_t advance, int64_t ring_cap);

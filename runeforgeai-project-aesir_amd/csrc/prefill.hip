@@ -6,12 +6,14 @@
 // MFMA GEMM  C[M][N] = A[M][K] . B[N][K]^T, f16 in, f32 accumulate (v_mfma_f32_16x16x32_f16).
 //   A (activations) and B (weights) are both K-contiguous, so every MFMA operand fragment is one
 //   16-byte row load: lane l holds row (l % 16) and k = 8 (l / 16) .. +7 of its 16 x 32 slice, the
-//   same k order for A and B. A workgroup is 4 waves; wave w owns 16 weight rows (output
-//   columns) and all 128 rows of its M tile, i.e. 8 accumulator tiles (rows 16i + 4 (l / 16) + e,
-//   column l % 16 in lane l). The 4 waves read the same A fragments (the activation tile stays in
-//   L1/L2) while each streams its own weight rows from HBM exactly once, one 32-wide k step ahead
-//   of the MFMAs. At M = 128 the GEMM is HBM-bound (128 flop/byte against MI355X's 312 flop/byte
-//   ridge), so the design favours streaming the weights over LDS tiling of A.
+//   same k order for A and B. A workgroup is 4 waves over 64 adjacent output columns (16 weight
+//   rows per wave) and a 128-row M tile; the waves walk the same k-steps, so their A fragment
+//   loads hit the same addresses and are served once from L2 into L1, while each wave streams
+//   its own weight rows from HBM exactly once. Each wave keeps 8 accumulator tiles (rows
+//   16i + 4 (l / 16) + e, column l % 16 in lane l) and two k-steps of operands in flight.
+//   Small-N GEMMs also split K over grid.z to put enough weight bytes in flight; their f32
+//   partials are summed in a fixed order by the epilogue kernel (deterministic, no atomics).
+//   At M = 128 the GEMM is HBM-bound (128 flop/byte against MI355X's 312 flop/byte ridge).
 #include <cmath>
 #include <vector>
 
@@ -28,55 +30,86 @@ constexpr int kGemmMT = 128;  // rows of A per workgroup tile
 constexpr int kGemmWaves = 4;
 constexpr int kGemmNW = 16;   // output columns per wave
 constexpr int kGemmNT = kGemmWaves * kGemmNW;
+constexpr int kGemmThreads = kGemmWaves * kWave;
 
 enum GemmEpi : int { kEpiStore = 0, kEpiResidual = 1, kEpiSwiglu = 2 };
+
+// Third dword of a raw buffer resource (V#) on gfx9-family GPUs, gfx950 included.
+constexpr int kBufferDword3 = 0x00020000;
 
 __device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h16x8, a), __builtin_bit_cast(h16x8, b), c, 0, 0,
                                                   0);
 }
 
-// EPI: kEpiStore C[m][n] = f16(acc); kEpiResidual C[m][n] = f16(f16(acc) + C[m][n]);
-// kEpiSwiglu with interleaved gate/up columns (2i gate, 2i + 1 up): C[m][i] = f16(up * silu(gate)).
-// Requires K % 32 == 0 and 16-byte aligned rows (checked by the launcher).
+// Applies the epilogue to output (m, n) with f32 value v; `partner` is the value of column n ^ 1
+// in the same row (used by kEpiSwiglu: 2i gate, 2i + 1 up -> C[m][i] = f16(up * silu(gate))).
+// kEpiStore: C[m][n] = f16(v); kEpiResidual: C[m][n] = f16(f16(v) + C[m][n]).
 template <int EPI>
-__global__ __launch_bounds__(kGemmWaves * kWave) void gemm_mfma_kernel(const h16 *__restrict__ A, int64_t M,
-                                                                       int64_t K, const h16 *__restrict__ B, int64_t N,
-                                                                       h16 *__restrict__ C, int64_t ldc) {
+__device__ __forceinline__ void gemm_epilogue(h16 *C, int64_t ldc, int64_t M, int64_t N, int64_t m, int64_t n, float v,
+                                              float partner) {
+    if (EPI == kEpiSwiglu) {
+        if ((n & 1) == 0 && m < M && n + 1 < N) C[m * ldc + n / 2] = hmul((h16)partner, silu_h((h16)v));
+    } else if (m < M && n < N) {
+        h16 *c = C + m * ldc + n;
+        *c = EPI == kEpiResidual ? hadd((h16)v, *c) : (h16)v;
+    }
+}
+
+// grid (N / 64, ceil(M / 128), splits). With one split the epilogue is applied here; otherwise
+// split z writes its f32 partial to P[z][M][N] for gemm_reduce_kernel. Requires K % 32 == 0 and
+// 16-byte aligned rows (checked by the launcher).
+template <int EPI>
+__global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(const h16 *__restrict__ A, int64_t M, int64_t K,
+                                                                 const h16 *__restrict__ B, int64_t N,
+                                                                 h16 *__restrict__ C, int64_t ldc,
+                                                                 float *__restrict__ P) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t m0 = (int64_t)blockIdx.y * kGemmMT;
-    const int64_t n0 = ((int64_t)blockIdx.x * kGemmWaves + wave) * kGemmNW;
-    if (n0 >= N) return;  // no workgroup-wide synchronization below
+    const int64_t n0 = (int64_t)blockIdx.x * kGemmNT + wave * kGemmNW;
     const int r = lane & 15, g = lane >> 4;
-    const h16 *ap[8];
+    const int64_t nks = K / 32, splits = gridDim.z, z = blockIdx.z;
+    const int64_t ks0 = nks * z / splits, ks1 = nks * (z + 1) / splits;
+    // Buffer loads: one V# per operand (range = the whole matrix, so rows past M or N read 0),
+    // a 32-bit per-lane byte offset per row block, the k offset as a uniform SGPR offset.
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void *)A, 0, (int)(M * K * 2), kBufferDword3);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void *)B, 0, (int)(N * K * 2), kBufferDword3);
+    int aoff[8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int64_t m = m0 + 16 * i + r;
-        ap[i] = A + (m < M ? m : M - 1) * K + 8 * g;  // rows past M re-read row M - 1, never stored
-    }
-    const h16 *bp = B + (n0 + r < N ? n0 + r : N - 1) * K + 8 * g;
+    for (int i = 0; i < 8; i++) aoff[i] = (int)(((m0 + 16 * i + r) * K + 8 * g) * 2);
+    const int boff = (int)(((n0 + r) * K + 8 * g) * 2);
 
     f32x4 acc[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    u32x4 a0[8], a1[8], b0, b1;
-    auto load = [&](u32x4 (&a)[8], u32x4 &b, int64_t k) {
-        b = ld16_stream(bp + k);
+    // Two operand sets (even / odd k-steps): the fragments of step ks + 2 are requested right
+    // after step ks is consumed. The loads are unconditional (steps past the range re-read the
+    // last step, an L2 hit) so that the compiler's wait counts stay exact across iterations:
+    // a conditional load would make it wait for every outstanding request at the loop head.
+    u32x4 ax[8], ay[8], bx, by;
+    auto load = [&](u32x4 (&a)[8], u32x4 &b, int64_t ks) {
+        const int kb = (int)((ks < ks1 ? ks : ks1 - 1) * 64);
+        b = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, boff, kb, 0));
 #pragma unroll
-        for (int i = 0; i < 8; i++) a[i] = ld16(ap[i] + k);
+        for (int i = 0; i < 8; i++) a[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, aoff[i], kb, 0));
     };
     auto mma = [&](const u32x4 (&a)[8], u32x4 b) {
 #pragma unroll
         for (int i = 0; i < 8; i++) acc[i] = mfma16x16x32(a[i], b, acc[i]);
     };
-    load(a0, b0, 0);
-    for (int64_t k = 0; k < K; k += 64) {
-        const bool two = k + 32 < K;
-        if (two) load(a1, b1, k + 32);
-        mma(a0, b0);
-        if (!two) break;
-        if (k + 64 < K) load(a0, b0, k + 64);
-        mma(a1, b1);
+    if (ks0 < ks1) {  // the scheduling barriers keep each operand set's requests contiguous
+        load(ax, bx, ks0);
+        __builtin_amdgcn_sched_barrier(0);
+        load(ay, by, ks0 + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        for (int64_t ks = ks0; ks < ks1; ks += 2) {
+            mma(ax, bx);
+            load(ax, bx, ks + 2);
+            __builtin_amdgcn_sched_barrier(0);
+            if (ks + 1 < ks1) mma(ay, by);
+            load(ay, by, ks + 3);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
 
     const int64_t n = n0 + r;
@@ -86,36 +119,82 @@ __global__ __launch_bounds__(kGemmWaves * kWave) void gemm_mfma_kernel(const h16
         for (int e = 0; e < 4; e++) {
             const int64_t m = m0 + 16 * i + 4 * g + e;
             const float v = acc[i][e];
-            if (EPI == kEpiSwiglu) {
-                const float up = __shfl_xor(v, 1, kWave);  // lane r ^ 1 holds column n ^ 1
-                if ((r & 1) == 0 && m < M && n + 1 < N)
-                    C[m * ldc + n / 2] = hmul((h16)up, silu_h((h16)v));
+            if (splits == 1) {
+                const float partner = __shfl_xor(v, 1, kWave);  // lane r ^ 1 holds column n ^ 1
+                gemm_epilogue<EPI>(C, ldc, M, N, m, n, v, partner);
             } else if (m < M && n < N) {
-                h16 *c = C + m * ldc + n;
-                *c = EPI == kEpiResidual ? hadd((h16)v, *c) : (h16)v;
+                P[(z * M + m) * N + n] = v;
             }
         }
     }
 }
 
-static bool mfma_shape_ok(const void *A, int64_t K, const void *B) {
-    return K % 32 == 0 && ((uintptr_t)A & 15) == 0 && ((uintptr_t)B & 15) == 0;
+// Sums the split partials of each output in split order and applies the epilogue; one thread
+// per output, consecutive threads on consecutive columns (pairs of SwiGLU columns are adjacent).
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(const float *__restrict__ P, int64_t splits, int64_t M,
+                                                          int64_t N, h16 *__restrict__ C, int64_t ldc) {
+    const int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t total = M * N;
+    const int64_t oc = o < total ? o : total - 1;  // tail threads repeat the last output, store nothing
+    float v = 0.0f;
+    for (int64_t z = 0; z < splits; z++) v += P[z * total + oc];
+    const float partner = __shfl_xor(v, 1, kWave);  // N even for SwiGLU: o ^ 1 is column n ^ 1
+    if (o < total) gemm_epilogue<EPI>(C, ldc, M, N, oc / N, oc % N, v, partner);
+}
+
+// The kernel addresses each operand through a buffer resource with a 32-bit byte range.
+static bool mfma_shape_ok(const void *A, int64_t M, int64_t K, const void *B, int64_t N) {
+    const int64_t lim = (int64_t)1 << 31;
+    return K % 32 == 0 && ((uintptr_t)A & 15) == 0 && ((uintptr_t)B & 15) == 0 && (M + kGemmMT) * K * 2 < lim &&
+           (N + kGemmNT) * K * 2 < lim;
+}
+
+// K splits for a GEMM: enough workgroups to keep the chip's memory pipes full (about 256
+// workgroups, 1024 waves) while every split keeps at least 8 k-steps.
+static int64_t gemm_splits(int64_t M, int64_t K, int64_t N) {
+    const int64_t tiles = ((N + kGemmNT - 1) / kGemmNT) * ((M + kGemmMT - 1) / kGemmMT);
+    int64_t s = (256 + tiles - 1) / tiles;
+    const int64_t max_s = K / 32 / 8;
+    if (s > max_s) s = max_s;
+    return s < 1 ? 1 : s;
+}
+
+int64_t prefill_part_floats(int64_t rows, int64_t dim, int64_t qkv_n, int64_t ffn) {
+    const int64_t shapes[4][2] = {{dim, qkv_n}, {dim, dim}, {dim, 2 * ffn}, {ffn, dim}};  // (K, N)
+    int64_t most = 0;
+    for (auto &kn : shapes) {
+        if (kn[0] % 32 != 0) continue;
+        const int64_t need = gemm_splits(rows, kn[0], kn[1]) * rows * kn[1];
+        if (gemm_splits(rows, kn[0], kn[1]) > 1 && need > most) most = need;
+    }
+    return most;
 }
 
 template <int EPI>
 static int32_t launch_mfma(hipStream_t s, const void *A, int64_t M, int64_t K, const void *B, int64_t N, void *C,
-                           int64_t ldc, const char *name) {
+                           int64_t ldc, float *part, int64_t part_floats, const char *name) {
     const int64_t gx = (N + kGemmNT - 1) / kGemmNT, gy = (M + kGemmMT - 1) / kGemmMT;
     if (gx > 2147483647 || gy > 65535) return fail(AESIR_ERR_UNSUPPORTED, "%s: GEMM grid too large", name);
-    hipLaunchKernelGGL(gemm_mfma_kernel<EPI>, dim3((unsigned)gx, (unsigned)gy), dim3(kGemmWaves * kWave), 0, s,
-                       (const h16 *)A, M, K, (const h16 *)B, N, (h16 *)C, ldc);
+    int64_t splits = gemm_splits(M, K, N);
+    while (splits > 1 && splits * M * N > part_floats) splits--;
+    if (EPI == kEpiSwiglu && (N & 1)) return fail(AESIR_ERR_INVALID, "%s: odd gate/up column count", name);
+    hipLaunchKernelGGL(gemm_mfma_kernel<EPI>, dim3((unsigned)gx, (unsigned)gy, (unsigned)splits), dim3(kGemmThreads),
+                       0, s, (const h16 *)A, M, K, (const h16 *)B, N, (h16 *)C, ldc, part);
     AESIR_LAUNCH_CHECK(name);
+    if (splits > 1) {
+        const int64_t blocks = (M * N + 255) / 256;
+        hipLaunchKernelGGL(gemm_reduce_kernel<EPI>, dim3((unsigned)blocks), dim3(256), 0, s, (const float *)part, splits,
+                           M, N, (h16 *)C, ldc);
+        AESIR_LAUNCH_CHECK("gemm_reduce_kernel");
+    }
     return AESIR_OK;
 }
 
 int32_t launch_gemm_f16_mfma(aesir_ctx *ctx, const void *A, int64_t M, int64_t K, const void *B, int64_t N, void *C) {
-    if (!mfma_shape_ok(A, K, B)) return launch_gemm_f16(ctx, A, M, K, B, N, C);
-    return launch_mfma<kEpiStore>(ctx->stream, A, M, K, B, N, C, N, "gemm_mfma_kernel");
+    if (!mfma_shape_ok(A, M, K, B, N)) return launch_gemm_f16(ctx, A, M, K, B, N, C);
+    return launch_mfma<kEpiStore>(ctx->stream, A, M, K, B, N, C, N, ctx->scratch.attn_part,
+                                  ctx->scratch.attn_part_floats, "gemm_mfma_kernel");
 }
 
 // ------------------------------------------------------------------ row kernels of the prefill
@@ -179,18 +258,19 @@ __global__ __launch_bounds__(kPThreads) void qkv_post_rows_kernel(const h16 *__r
 // ... over the round's positions. Same arithmetic as flash_attention_gqa (compute.mojo:1950-2015)
 // with an f32 accumulator.
 constexpr int kMaxHdPerLane = 4;  // head_dim <= 256
+template <bool VEC>
 __global__ __launch_bounds__(kWave) void prefill_attention_kernel(const h16 *__restrict__ Q, const h16 *__restrict__ kc,
                                                                   const h16 *__restrict__ vc, h16 *__restrict__ out,
                                                                   int64_t dim, int64_t kvd, int64_t hd, int64_t G,
                                                                   int64_t p0, int64_t max_seq, float scale) {
-    __shared__ float qs[256];
+    __shared__ __align__(16) h16 qs[256];
     __shared__ float ps[kWave];
     const int lane = threadIdx.x;
     const int64_t r = blockIdx.x, h = blockIdx.y, g = h / G;
     const int64_t pos = p0 + r;
     const int64_t S = pos + 1 < max_seq ? pos + 1 : max_seq;
     const h16 *q = Q + r * dim + h * hd;
-    for (int64_t d = lane; d < hd; d += kWave) qs[d] = (float)q[d];
+    for (int64_t d = lane; d < hd; d += kWave) qs[d] = q[d];
     __syncthreads();
     const h16 *Kg = kc + g * hd;
     const h16 *Vg = vc + g * hd;
@@ -203,7 +283,11 @@ __global__ __launch_bounds__(kWave) void prefill_attention_kernel(const h16 *__r
         if (p < S) {
             const h16 *k = Kg + p * kvd;
             float d = 0.0f;
-            for (int64_t i = 0; i < hd; i++) d = fmaf(qs[i], (float)k[i], d);
+            if (VEC) {  // 16-byte K loads, v_dot2_f32_f16 against the q row in LDS
+                for (int64_t i = 0; i < hd; i += 8) d = dot8(ld16(k + i), ld16(qs + i), d);
+            } else {
+                for (int64_t i = 0; i < hd; i++) d = fmaf((float)qs[i], (float)k[i], d);
+            }
             s = d * scale;
         }
         const float mn = fmaxf(m, wave_max(s));
@@ -250,6 +334,8 @@ static int32_t launch_swiglu_pairs(hipStream_t s, const void *gu, void *act, int
 
 // ------------------------------------------------------------------ the batched pass
 
+static const void *L0(const aesir_model *m) { return m->layers[0].wqkv; }
+
 // Runs positions [p0, p0 + n) of tokens through every layer (n <= the model's prefill rows).
 static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t p0, int64_t n) {
     const aesir_model_config &c = m->cfg;
@@ -262,7 +348,11 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
     hipLaunchKernelGGL(embed_rows_kernel, dim3((unsigned)n), dim3(kPThreads), 0, s, (const h16 *)m->tok_embd, d,
                        (const int64_t *)m->pf_tokens, X);
     AESIR_LAUNCH_CHECK("embed_rows_kernel");
-    const bool mfma = d % 32 == 0 && f % 32 == 0;
+    // every GEMM of the layer on the matrix cores when all four shapes qualify (arena buffers
+    // and weights are 256-byte aligned)
+    const int64_t pr = m->pf_rows;
+    const bool mfma = mfma_shape_ok(Xn, pr, d, L0(m), qkv_n) && mfma_shape_ok(Xn, pr, d, L0(m), d) &&
+                      mfma_shape_ok(Xn, pr, d, L0(m), 2 * f) && mfma_shape_ok(Xn, pr, f, L0(m), d);
     for (int64_t l = 0; l < c.n_layers; l++) {
         const ModelLayer &L = m->layers[l];
         h16 *kc = (h16 *)m->k_cache + l * c.ctx_len * kvd, *vc = (h16 *)m->v_cache + l * c.ctx_len * kvd;
@@ -270,16 +360,20 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
         hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3((unsigned)n), dim3(kPThreads), 0, s, X, Xn, d,
                            (const h16 *)L.attn_norm, c.rms_eps);
         AESIR_LAUNCH_CHECK("rmsnorm_rows_kernel");
-        if (mfma) AESIR_TRY(launch_mfma<kEpiStore>(s, Xn, n, d, L.wqkv, qkv_n, QKV, qkv_n, "gemm_mfma_qkv"));
+        if (mfma) AESIR_TRY(launch_mfma<kEpiStore>(s, Xn, n, d, L.wqkv, qkv_n, QKV, qkv_n, m->pf_part, m->pf_part_floats, "gemm_mfma_qkv"));
         else AESIR_TRY(launch_gemm_f16(m->ctx, Xn, n, d, L.wqkv, qkv_n, QKV));
         hipLaunchKernelGGL(qkv_post_rows_kernel, dim3((unsigned)n), dim3(kPThreads), 0, s, QKV, d, kvd, hd, p0,
                            c.ctx_len, (const h16x2 *)m->rope, Q, kc, vc);
         AESIR_LAUNCH_CHECK("qkv_post_rows_kernel");
-        hipLaunchKernelGGL(prefill_attention_kernel, dim3((unsigned)n, (unsigned)c.n_heads), dim3(kWave), 0, s, Q, kc,
-                           vc, ATT, d, kvd, hd, c.n_heads / c.n_kv_heads, p0, c.ctx_len, m->attn_scale);
+        if (hd % 8 == 0)  // rows of K are then 16-byte aligned (kvd and the cache base are)
+            hipLaunchKernelGGL(prefill_attention_kernel<true>, dim3((unsigned)n, (unsigned)c.n_heads), dim3(kWave), 0,
+                               s, Q, kc, vc, ATT, d, kvd, hd, c.n_heads / c.n_kv_heads, p0, c.ctx_len, m->attn_scale);
+        else
+            hipLaunchKernelGGL(prefill_attention_kernel<false>, dim3((unsigned)n, (unsigned)c.n_heads), dim3(kWave), 0,
+                               s, Q, kc, vc, ATT, d, kvd, hd, c.n_heads / c.n_kv_heads, p0, c.ctx_len, m->attn_scale);
         AESIR_LAUNCH_CHECK("prefill_attention_kernel");
         if (mfma) {
-            AESIR_TRY(launch_mfma<kEpiResidual>(s, ATT, n, d, L.wo, d, X, d, "gemm_mfma_o_residual"));
+            AESIR_TRY(launch_mfma<kEpiResidual>(s, ATT, n, d, L.wo, d, X, d, m->pf_part, m->pf_part_floats, "gemm_mfma_o_residual"));
         } else {
             AESIR_TRY(launch_gemm_f16(m->ctx, ATT, n, d, L.wo, d, Xn));
             AESIR_TRY(launch_residual_add(s, X, Xn, n * d));
@@ -289,8 +383,10 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
                            (const h16 *)L.ffn_norm, c.rms_eps);
         AESIR_LAUNCH_CHECK("rmsnorm_rows_kernel");
         if (mfma) {
-            AESIR_TRY(launch_mfma<kEpiSwiglu>(s, Xn, n, d, L.wgu, 2 * f, ACT, f, "gemm_mfma_gate_up_swiglu"));
-            AESIR_TRY(launch_mfma<kEpiResidual>(s, ACT, n, f, L.wdown, d, X, d, "gemm_mfma_down_residual"));
+            AESIR_TRY(launch_mfma<kEpiSwiglu>(s, Xn, n, d, L.wgu, 2 * f, ACT, f, m->pf_part, m->pf_part_floats,
+                                                "gemm_mfma_gate_up_swiglu"));
+            AESIR_TRY(launch_mfma<kEpiResidual>(s, ACT, n, f, L.wdown, d, X, d, m->pf_part, m->pf_part_floats,
+                                                  "gemm_mfma_down_residual"));
         } else {
             // interleaved gate/up rows -> [n][2f] products, then the SwiGLU over the pairs
             AESIR_TRY(launch_gemm_f16(m->ctx, Xn, n, d, L.wgu, 2 * f, m->pf_gu));

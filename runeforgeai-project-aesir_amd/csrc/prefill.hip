@@ -7,10 +7,11 @@
 //   A (activations) and B (weights) are both K-contiguous, so every MFMA operand fragment is one
 //   16-byte row load: lane l holds row (l % 16) and k = 8 (l / 16) .. +7 of its 16 x 32 slice, the
 //   same k order for A and B. A workgroup is 4 waves over 64 adjacent output columns (16 weight
-//   rows per wave) and a 128-row M tile; the waves walk the same k-steps, so their A fragment
-//   loads hit the same addresses and are served once from L2 into L1, while each wave streams
-//   its own weight rows from HBM exactly once. Each wave keeps 8 accumulator tiles (rows
-//   16i + 4 (l / 16) + e, column l % 16 in lane l) and two k-steps of operands in flight.
+//   rows per wave) and a 128-row M tile. Each 64-wide K chunk of A is copied once per workgroup
+//   into a double-buffered LDS tile (rows padded to 144 bytes) and every wave reads its A
+//   fragments from there with ds_read_b128, while it streams its own weight rows from HBM
+//   exactly once, one chunk ahead of the MFMAs. Each wave keeps 8 accumulator tiles (rows
+//   16i + 4 (l / 16) + e, column l % 16 in lane l).
 //   Small-N GEMMs also split K over grid.z to put enough weight bytes in flight; their f32
 //   partials are summed in a fixed order by the epilogue kernel (deterministic, no atomics).
 //   At M = 128 the GEMM is HBM-bound (128 flop/byte against MI355X's 312 flop/byte ridge).
@@ -57,58 +58,91 @@ __device__ __forceinline__ void gemm_epilogue(h16 *C, int64_t ldc, int64_t M, in
 }
 
 // grid (N / 64, ceil(M / 128), splits). With one split the epilogue is applied here; otherwise
-// split z writes its f32 partial to P[z][M][N] for gemm_reduce_kernel. Requires K % 32 == 0 and
+// split z writes its f32 partial to P[z][M][N] for gemm_reduce_kernel. Requires K % 64 == 0 and
 // 16-byte aligned rows (checked by the launcher).
+constexpr int kGemmKC = 64;           // k per LDS chunk (two MFMA k-steps)
+constexpr int kGemmLdsRow = kGemmKC + 8;  // padded LDS row (halves): 144 bytes, no bank conflicts
 template <int EPI>
 __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(const h16 *__restrict__ A, int64_t M, int64_t K,
                                                                  const h16 *__restrict__ B, int64_t N,
                                                                  h16 *__restrict__ C, int64_t ldc,
                                                                  float *__restrict__ P) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __shared__ __align__(16) h16 as[2][kGemmMT][kGemmLdsRow];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t m0 = (int64_t)blockIdx.y * kGemmMT;
     const int64_t n0 = (int64_t)blockIdx.x * kGemmNT + wave * kGemmNW;
     const int r = lane & 15, g = lane >> 4;
-    const int64_t nks = K / 32, splits = gridDim.z, z = blockIdx.z;
-    const int64_t ks0 = nks * z / splits, ks1 = nks * (z + 1) / splits;
+    const int64_t nkc = K / kGemmKC, splits = gridDim.z, z = blockIdx.z;
+    const int64_t c0 = nkc * z / splits, c1 = nkc * (z + 1) / splits;
     // Buffer loads: one V# per operand (range = the whole matrix, so rows past M or N read 0),
-    // a 32-bit per-lane byte offset per row block, the k offset as a uniform SGPR offset.
+    // a 32-bit per-lane byte offset, the k offset as a uniform SGPR offset.
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void *)A, 0, (int)(M * K * 2), kBufferDword3);
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void *)B, 0, (int)(N * K * 2), kBufferDword3);
-    int aoff[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) aoff[i] = (int)(((m0 + 16 * i + r) * K + 8 * g) * 2);
+    // A chunk staging: thread t copies row t / 2, k-halves 32 (t % 2) .. +31 (four 16-byte loads)
+    const int arow = tid >> 1, acol = (tid & 1) * 32;
+    const int aoff = (int)(((m0 + arow) * K + acol) * 2);
     const int boff = (int)(((n0 + r) * K + 8 * g) * 2);
 
     f32x4 acc[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    // Two operand sets (even / odd k-steps): the fragments of step ks + 2 are requested right
-    // after step ks is consumed. The loads are unconditional (steps past the range re-read the
-    // last step, an L2 hit) so that the compiler's wait counts stay exact across iterations:
-    // a conditional load would make it wait for every outstanding request at the loop head.
-    u32x4 ax[8], ay[8], bx, by;
-    auto load = [&](u32x4 (&a)[8], u32x4 &b, int64_t ks) {
-        const int kb = (int)((ks < ks1 ? ks : ks1 - 1) * 64);
-        b = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, boff, kb, 0));
+    if (c0 < c1) {
+        // Pipeline: chunk c computes from LDS buffer (c - c0) % 2 and weight slot (c - c0) % 4
+        // while A(c + 2) (two register sets by chunk parity) and the weights of chunk c + 3 (a
+        // four-slot ring) are in flight; at its end A(c + 1), requested a chunk earlier, goes to
+        // the other LDS buffer. Requests are unconditional (past the range they re-read the last
+        // chunk) so the compiler's wait counts stay exact.
+        u32x4 ax[4], ay[4], b0[2], b1[2], b2[2], b3[2];
+        auto load_a = [&](u32x4 (&av)[4], int64_t c) {
+            c = c < c1 ? c : c1 - 1;
+            const int kb = (int)(c * kGemmKC * 2);
 #pragma unroll
-        for (int i = 0; i < 8; i++) a[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, aoff[i], kb, 0));
-    };
-    auto mma = [&](const u32x4 (&a)[8], u32x4 b) {
+            for (int j = 0; j < 4; j++)
+                av[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, aoff + 16 * j, kb, 0));
+        };
+        auto load_b = [&](u32x4 (&bv)[2], int64_t c) {
+            c = c < c1 ? c : c1 - 1;
+            const int kb = (int)(c * kGemmKC * 2);
 #pragma unroll
-        for (int i = 0; i < 8; i++) acc[i] = mfma16x16x32(a[i], b, acc[i]);
-    };
-    if (ks0 < ks1) {  // the scheduling barriers keep each operand set's requests contiguous
-        load(ax, bx, ks0);
-        __builtin_amdgcn_sched_barrier(0);
-        load(ay, by, ks0 + 1);
-        __builtin_amdgcn_sched_barrier(0);
-        for (int64_t ks = ks0; ks < ks1; ks += 2) {
-            mma(ax, bx);
-            load(ax, bx, ks + 2);
+            for (int j = 0; j < 2; j++)
+                bv[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, boff, kb + 64 * j, 0));
+        };
+        auto store_a = [&](const u32x4 (&av)[4], int buf) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) st16(&as[buf][arow][acol + 8 * j], av[j]);
+        };
+        auto chunk = [&](int64_t c, int buf, const u32x4 (&bcur)[2], u32x4 (&bnext)[2], u32x4 (&afree)[4],
+                         const u32x4 (&anext)[4]) {
+            load_a(afree, c + 2);
+            load_b(bnext, c + 3);
             __builtin_amdgcn_sched_barrier(0);
-            if (ks + 1 < ks1) mma(ay, by);
-            load(ay, by, ks + 3);
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                u32x4 a[8];
+#pragma unroll
+                for (int i = 0; i < 8; i++) a[i] = ld16(&as[buf][16 * i + r][32 * j + 8 * g]);
+#pragma unroll
+                for (int i = 0; i < 8; i++) acc[i] = mfma16x16x32(a[i], bcur[j], acc[i]);
+            }
             __builtin_amdgcn_sched_barrier(0);
+            store_a(anext, buf ^ 1);  // A(c + 1); past the range a copy nothing reads
+            __syncthreads();
+        };
+        load_a(ax, c0);
+        load_b(b0, c0);
+        load_a(ay, c0 + 1);
+        load_b(b1, c0 + 1);
+        load_b(b2, c0 + 2);
+        store_a(ax, 0);
+        __syncthreads();
+        for (int64_t c = c0; c < c1; c += 4) {
+            chunk(c, 0, b0, b3, ax, ay);
+            if (c + 1 >= c1) break;
+            chunk(c + 1, 1, b1, b0, ay, ax);
+            if (c + 2 >= c1) break;
+            chunk(c + 2, 0, b2, b1, ax, ay);
+            if (c + 3 >= c1) break;
+            chunk(c + 3, 1, b3, b2, ay, ax);
         }
     }
 
@@ -146,7 +180,7 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const float *__restric
 // The kernel addresses each operand through a buffer resource with a 32-bit byte range.
 static bool mfma_shape_ok(const void *A, int64_t M, int64_t K, const void *B, int64_t N) {
     const int64_t lim = (int64_t)1 << 31;
-    return K % 32 == 0 && ((uintptr_t)A & 15) == 0 && ((uintptr_t)B & 15) == 0 && (M + kGemmMT) * K * 2 < lim &&
+    return K % 64 == 0 && ((uintptr_t)A & 15) == 0 && ((uintptr_t)B & 15) == 0 && (M + kGemmMT) * K * 2 < lim &&
            (N + kGemmNT) * K * 2 < lim;
 }
 
@@ -155,7 +189,7 @@ static bool mfma_shape_ok(const void *A, int64_t M, int64_t K, const void *B, in
 static int64_t gemm_splits(int64_t M, int64_t K, int64_t N) {
     const int64_t tiles = ((N + kGemmNT - 1) / kGemmNT) * ((M + kGemmMT - 1) / kGemmMT);
     int64_t s = (256 + tiles - 1) / tiles;
-    const int64_t max_s = K / 32 / 8;
+    const int64_t max_s = K / 256;  // at least four 64-wide chunks per split
     if (s > max_s) s = max_s;
     return s < 1 ? 1 : s;
 }
@@ -164,7 +198,7 @@ int64_t prefill_part_floats(int64_t rows, int64_t dim, int64_t qkv_n, int64_t ff
     const int64_t shapes[4][2] = {{dim, qkv_n}, {dim, dim}, {dim, 2 * ffn}, {ffn, dim}};  // (K, N)
     int64_t most = 0;
     for (auto &kn : shapes) {
-        if (kn[0] % 32 != 0) continue;
+        if (kn[0] % 64 != 0) continue;
         const int64_t need = gemm_splits(rows, kn[0], kn[1]) * rows * kn[1];
         if (gemm_splits(rows, kn[0], kn[1]) > 1 && need > most) most = need;
     }

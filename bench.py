@@ -192,7 +192,10 @@ def main():
         return
 
     ctx_len = args.kv + max(args.steps, args.warmup) + 64
-    well = int(TOKEN_WEIGHT_BYTES + 2 * LAYERS * ctx_len * KV_DIM * 2 + (1 << 30))
+    # arena: all weights (the whole embedding table, not the one row a token reads), the KV cache
+    # and 512 MiB for the decode and prefill workspaces
+    model_bytes = TOKEN_WEIGHT_BYTES - 2 * DIM + 2 * VOCAB * DIM
+    well = int(model_bytes + 2 * LAYERS * ctx_len * KV_DIM * 2 + (512 << 20))
     ctx = A.Context(well)
     info = ctx.device_info()
     m = A.Model.create(ctx, A.ModelConfig(DIM, LAYERS, HEADS, KV_HEADS, FFN, VOCAB, ctx_len))

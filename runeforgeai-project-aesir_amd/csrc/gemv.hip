@@ -183,6 +183,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const h16 *__restrict__ 
     __builtin_amdgcn_sched_barrier(0);  // keep the x requests ahead of the weight requests
     fetch(wa, 0);
     __builtin_amdgcn_sched_barrier(0);
+    const auto pre = epi.template prefetch<ROWS>(n0, m, N, tid);  // epilogue operands, off the tail
     x_stage_finish<VEC, NORM>(xfirst, xs, x, K, nslab, nw, eps, red,
                               (src.xcopy && blockIdx.x == 0) ? src.xcopy : nullptr);
     __syncthreads();
@@ -201,7 +202,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const h16 *__restrict__ 
     __syncthreads();
     if (tid < ROWS) sums[tid] = (red[tid] + red[ROWS + tid]) + (red[2 * ROWS + tid] + red[3 * ROWS + tid]);
     __syncthreads();
-    epi.template apply<ROWS>(n0, m, N, sums, tid);
+    epi.template apply<ROWS>(n0, m, N, sums, tid, pre);
 }
 
 // Fixed-shape fast path (K % 8 == 0, 16-byte aligned, NS = ceil(K / 2048) slabs known at
@@ -239,6 +240,7 @@ __global__ __launch_bounds__(kThreads) void gemv_fixed_kernel(const h16 *__restr
 #pragma unroll
     for (int r = 0; r < ROWS; r++) wbuf[0][r] = ld16_stream(wr[r] + k0);  // k0 < 2048 <= K
     __builtin_amdgcn_sched_barrier(0);
+    const auto pre = epi.template prefetch<ROWS>(n0, m, N, tid);  // epilogue operands, off the tail
 
     float ss = 0.0f;
     h16 *xcopy = (src.xcopy && blockIdx.x == 0) ? src.xcopy : nullptr;
@@ -276,16 +278,23 @@ __global__ __launch_bounds__(kThreads) void gemv_fixed_kernel(const h16 *__restr
     __syncthreads();
     if (tid < ROWS) sums[tid] = (red[tid] + red[ROWS + tid]) + (red[2 * ROWS + tid] + red[3 * ROWS + tid]);
     __syncthreads();
-    epi.template apply<ROWS>(n0, m, N, sums, tid);
+    epi.template apply<ROWS>(n0, m, N, sums, tid, pre);
 }
 
 // ------------------------------------------------------------------ epilogues
+
+// Each epilogue has a prefetch() that the kernels call right after the first weight requests, so
+// any operand the epilogue reads from memory arrives with the weights instead of adding a
+// dependent round trip at the end of the workgroup.
+struct NoPre {};
 
 struct EpiStore {
     h16 *y;
     int64_t ldy;
     template <int ROWS>
-    __device__ __forceinline__ void apply(int64_t n0, int64_t m, int64_t N, const float *s, int tid) const {
+    __device__ __forceinline__ NoPre prefetch(int64_t, int64_t, int64_t, int) const { return {}; }
+    template <int ROWS>
+    __device__ __forceinline__ void apply(int64_t n0, int64_t m, int64_t N, const float *s, int tid, NoPre) const {
         if (tid < ROWS && n0 + tid < N) y[m * ldy + n0 + tid] = (h16)s[tid];
     }
 };
@@ -294,8 +303,12 @@ struct EpiStore {
 struct EpiResidual {
     h16 *x;
     template <int ROWS>
-    __device__ __forceinline__ void apply(int64_t n0, int64_t, int64_t N, const float *s, int tid) const {
-        if (tid < ROWS && n0 + tid < N) x[n0 + tid] = hadd((h16)s[tid], x[n0 + tid]);
+    __device__ __forceinline__ h16 prefetch(int64_t n0, int64_t, int64_t N, int tid) const {
+        return (tid < ROWS && n0 + tid < N) ? x[n0 + tid] : (h16)0.0f;  // only this workgroup writes it
+    }
+    template <int ROWS>
+    __device__ __forceinline__ void apply(int64_t n0, int64_t, int64_t N, const float *s, int tid, h16 old) const {
+        if (tid < ROWS && n0 + tid < N) x[n0 + tid] = hadd((h16)s[tid], old);
     }
 };
 
@@ -308,18 +321,32 @@ struct EpiQkv {
     const h16x2 *rope;
     const DecodeState *state;
     int64_t dim, kvd, hd, max_seq;
+    struct Pre {
+        int64_t pos;
+        h16x2 cs;  // cos/sin of this thread's pair (Q and K rows)
+    };
     template <int ROWS>
-    __device__ __forceinline__ void apply(int64_t n0, int64_t, int64_t N, const float *s, int tid) const {
+    __device__ __forceinline__ Pre prefetch(int64_t n0, int64_t, int64_t N, int tid) const {
+        Pre p{state->pos, h16x2{(h16)1.0f, (h16)0.0f}};
+        const int64_t n = n0 + 2 * tid;
+        if (tid < ROWS / 2 && n < N && n < dim + kvd) {
+            const int64_t nn = n < dim ? n : n - dim;
+            p.cs = rope[p.pos * (hd / 2) + ((nn % hd) >> 1)];
+        }
+        return p;
+    }
+    template <int ROWS>
+    __device__ __forceinline__ void apply(int64_t n0, int64_t, int64_t N, const float *s, int tid, const Pre &pre) const {
         static_assert(ROWS % 2 == 0, "pairs must stay in one workgroup");
         if (tid >= ROWS / 2) return;
         const int64_t n = n0 + 2 * tid;
         if (n >= N) return;
         const h16 s0 = (h16)s[2 * tid], s1 = (h16)s[2 * tid + 1];
-        const int64_t pos = state->pos;
+        const int64_t pos = pre.pos;
         const int64_t slot = pos % max_seq;
         if (n < dim + kvd) {
             const int64_t nn = n < dim ? n : n - dim;
-            const h16x2 cs = rope[pos * (hd / 2) + ((nn % hd) >> 1)];
+            const h16x2 cs = pre.cs;
             const h16 r0 = hsub(hmul(s0, cs.x), hmul(s1, cs.y));
             const h16 r1 = hadd(hmul(s0, cs.y), hmul(s1, cs.x));
             h16 *dst = n < dim ? q + nn : kc + slot * kvd + nn;
@@ -337,7 +364,9 @@ struct EpiQkv {
 struct EpiSwiglu {
     h16 *act;
     template <int ROWS>
-    __device__ __forceinline__ void apply(int64_t n0, int64_t, int64_t N, const float *s, int tid) const {
+    __device__ __forceinline__ NoPre prefetch(int64_t, int64_t, int64_t, int) const { return {}; }
+    template <int ROWS>
+    __device__ __forceinline__ void apply(int64_t n0, int64_t, int64_t N, const float *s, int tid, NoPre) const {
         if (tid >= ROWS / 2 || n0 + 2 * tid >= N) return;
         const h16 g = (h16)s[2 * tid], u = (h16)s[2 * tid + 1];
         act[n0 / 2 + tid] = hmul(u, silu_h(g));
@@ -376,7 +405,9 @@ struct EpiLmHead {
     h16 *logits;
     ArgPart *parts;
     template <int ROWS>
-    __device__ __forceinline__ void apply(int64_t n0, int64_t, int64_t N, const float *s, int tid) const {
+    __device__ __forceinline__ NoPre prefetch(int64_t, int64_t, int64_t, int) const { return {}; }
+    template <int ROWS>
+    __device__ __forceinline__ void apply(int64_t n0, int64_t, int64_t N, const float *s, int tid, NoPre) const {
         if (tid < ROWS && n0 + tid < N) logits[n0 + tid] = (h16)s[tid];
         if (tid == 0) parts[blockIdx.x] = group_scan<ROWS>(n0, N, s);
     }

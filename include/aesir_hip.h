@@ -142,6 +142,33 @@ int32_t aesir_gemm_q8_0(aesir_ctx *ctx, const void *A, int64_t a_rows, int64_t a
 int32_t aesir_q8_0_matvec_f32(aesir_ctx *ctx, const void *blocks, int64_t n_rows, int64_t k, const float *x,
                               float *y);
 
+/* ======================================================================= sampler
+ * sample_token_from_logits (core/sampler.mojo:217-305): the whole sampler stack on the device.
+ * Parameter meaning as in the reference: temperature <= 0 or top_k == 1 is the greedy branch
+ * (first maximum of the sanitized logits, suppressed ids at -1e9); otherwise the suppress mask,
+ * repetition penalty (1 = off), frequency / presence penalties (0 = off) and temperature scale
+ * every candidate, then top_k (> 0), top_p (< 1) and min_p (in (0, 1)) truncate the stably
+ * sorted list, and RuneRNG.next_float32 drives the draw. */
+typedef struct {
+    float temperature;
+    int64_t top_k;
+    float top_p;
+    float min_p;
+    float repetition_penalty;
+    float frequency_penalty;
+    float presence_penalty;
+} aesir_sampler_config;
+
+/* logits: f16 [vocab] on the device; context / suppress: host token id lists; *rng_state: the
+ * RuneRNG state (sampler.mojo:17-43), advanced only when the draw consumes a random number, as
+ * the reference does. Waits; *token receives the sampled id (0 for vocab <= 0, as :232-233). */
+int32_t aesir_sample_token(aesir_ctx *ctx, const void *logits, int64_t vocab, const aesir_sampler_config *cfg,
+                           const int64_t *context, int64_t n_context, const int64_t *suppress, int64_t n_suppress,
+                           uint64_t *rng_state, int64_t *token);
+/* RuneRNG.next_u64 (core/sampler.mojo:34-37) on a host state: the mixer advances the state itself.
+ * RuneRNG(seed) starts from seed, or from 0x9E3779B97F4A7C15 when seed is 0 (:25-29). */
+uint64_t aesir_rune_rng_next(uint64_t *state);
+
 /* ======================================================================= KV cache
  * KVCache (core/mimir_well.mojo:434-521): K and V each [num_layers][max_seq_len][hidden_dim]
  * f16, carved from the context's well. */

@@ -342,6 +342,169 @@ int64_t ao_greedy_sample_f16(const uint16_t *logits, int64_t n, const int64_t *s
     return best;
 }
 
+/* ---- full sampler stack, sampler.mojo:17-305 -------------------------------------------- */
+
+/* RuneRNG.next_float32, sampler.mojo:39-42: uniform in [0, 1) from the low 24 bits. */
+float ao_rune_rng_next_float32(uint64_t *state) {
+    uint64_t v = ao_rune_rng_next(state);
+    return (float)(v & 0xFFFFFFULL) / 16777216.0f;
+}
+
+/* f32 exp of the sampler stages. The reference calls Mojo's f32 exp; this restatement uses the
+ * correctly rounded value (exp in f64, rounded once), which the GPU sampler computes the same way. */
+static float exp_f32(float x) { return (float)exp((double)x); }
+
+typedef struct {
+    int64_t id;
+    float logit;
+} cand_t;
+
+/* Order of sort_candidates_descending (sampler.mojo:92-104), a stable insertion sort on the
+ * logit: descending logits, equal logits (-0 == +0) in their original order. Every sort of the
+ * stack starts from index order or from an already sorted prefix, so the original order is the
+ * id order and this total order gives the same permutation in O(n log n). */
+static int cand_cmp(const void *pa, const void *pb) {
+    const cand_t *a = (const cand_t *)pa, *b = (const cand_t *)pb;
+    if (a->logit > b->logit) return -1;
+    if (a->logit < b->logit) return 1;
+    return a->id < b->id ? -1 : (a->id > b->id ? 1 : 0);
+}
+
+/* Softmax of the (sorted) candidate prefix as apply_top_p / apply_min_p compute it (:127-138,
+ * :176-187): p = exp(l - l[0]) summed in order, then divided by the sum when it is positive. */
+static void stage_probs(const cand_t *c, int64_t n, float *probs) {
+    const float max_logit = c[0].logit;
+    float sum = 0.0f;
+    for (int64_t i = 0; i < n; i++) {
+        probs[i] = exp_f32(c[i].logit - max_logit);
+        sum += probs[i];
+    }
+    if (sum > 0.0f)
+        for (int64_t i = 0; i < n; i++) probs[i] /= sum;
+}
+
+int64_t ao_sample_candidates_f16(const uint16_t *logits, int64_t vocab, const ao_sampler_config *cfg,
+                                 const int64_t *context, int64_t n_context, const int64_t *suppress,
+                                 int64_t n_suppress, int64_t *ids_out, float *logits_out) {
+    if (vocab <= 0) return 0;
+    cand_t *c = (cand_t *)malloc((size_t)vocab * sizeof(cand_t));
+    int32_t *count = (int32_t *)calloc((size_t)vocab, sizeof(int32_t));
+    float *probs = (float *)malloc((size_t)vocab * sizeof(float));
+    for (int64_t i = 0; i < vocab; i++) {
+        c[i].id = i;
+        c[i].logit = sanitize_logit(H2F(logits[i]));
+    }
+    /* apply_token_mask (:197-211) */
+    for (int64_t s = 0; s < n_suppress; s++)
+        if (suppress[s] >= 0 && suppress[s] < vocab) c[suppress[s]].logit = -1e9f;
+    /* occurrences of each candidate id in the context (the presence / count loops of :59-76, :151-163) */
+    for (int64_t t = 0; t < n_context; t++)
+        if (context[t] >= 0 && context[t] < vocab) count[context[t]]++;
+    /* apply_repetition_penalty (:54-76) */
+    if (cfg->repetition_penalty != 1.0f && n_context > 0)
+        for (int64_t i = 0; i < vocab; i++)
+            if (count[i] > 0) {
+                if (c[i].logit < 0.0f) c[i].logit *= cfg->repetition_penalty;
+                else c[i].logit /= cfg->repetition_penalty;
+            }
+    /* apply_frequency_presence_penalty (:143-163) */
+    if (!(cfg->frequency_penalty == 0.0f && cfg->presence_penalty == 0.0f) && n_context > 0)
+        for (int64_t i = 0; i < vocab; i++)
+            if (count[i] > 0) {
+                const float freq_loss = (float)count[i] * cfg->frequency_penalty;
+                c[i].logit -= (freq_loss + cfg->presence_penalty);
+            }
+    /* apply_temperature (:79-88) */
+    if (cfg->temperature > 0.0f && cfg->temperature != 1.0f) {
+        const float inv_temp = 1.0f / cfg->temperature;
+        for (int64_t i = 0; i < vocab; i++) c[i].logit *= inv_temp;
+    }
+    int64_t n = vocab;
+    int sorted = 0;
+    /* apply_top_k (:107-116) */
+    if (cfg->top_k > 0 && cfg->top_k < n) {
+        qsort(c, (size_t)n, sizeof(cand_t), cand_cmp);
+        sorted = 1;
+        n = cfg->top_k;
+    }
+    /* apply_top_p (:119-147) */
+    if (cfg->top_p < 1.0f && n > 1) {
+        if (!sorted) qsort(c, (size_t)n, sizeof(cand_t), cand_cmp);
+        sorted = 1;
+        stage_probs(c, n, probs);
+        float cum = 0.0f;
+        int64_t cutoff = n - 1;
+        for (int64_t i = 0; i < n; i++) {
+            cum += probs[i];
+            if (cum >= cfg->top_p) {
+                cutoff = i;
+                break;
+            }
+        }
+        n = cutoff + 1;
+    }
+    /* apply_min_p (:166-194) */
+    if (cfg->min_p > 0.0f && cfg->min_p < 1.0f && n > 1) {
+        if (!sorted) qsort(c, (size_t)n, sizeof(cand_t), cand_cmp);
+        sorted = 1;
+        stage_probs(c, n, probs);
+        const float threshold = cfg->min_p * probs[0];
+        int64_t kept = 0;
+        while (kept < n && probs[kept] >= threshold) kept++;
+        if (kept > 0) n = kept;
+    }
+    for (int64_t i = 0; i < n; i++) {
+        ids_out[i] = c[i].id;
+        logits_out[i] = c[i].logit;
+    }
+    free(c);
+    free(count);
+    free(probs);
+    return n;
+}
+
+int64_t ao_sample_token_f16(const uint16_t *logits, int64_t vocab, const ao_sampler_config *cfg,
+                            const int64_t *context, int64_t n_context, const int64_t *suppress,
+                            int64_t n_suppress, uint64_t *rng_state) {
+    if (vocab <= 0) return 0;
+    /* greedy branch (:241-261) */
+    if (cfg->temperature <= 0.0f || cfg->top_k == 1) return ao_greedy_sample_f16(logits, vocab, suppress, n_suppress);
+    int64_t *ids = (int64_t *)malloc((size_t)vocab * sizeof(int64_t));
+    float *lg = (float *)malloc((size_t)vocab * sizeof(float));
+    float *ex = (float *)malloc((size_t)vocab * sizeof(float));
+    const int64_t n = ao_sample_candidates_f16(logits, vocab, cfg, context, n_context, suppress, n_suppress, ids, lg);
+    int64_t tok = 0;
+    if (n > 0) {
+        /* final draw (:284-305) */
+        float max_l = lg[0];
+        for (int64_t i = 1; i < n; i++)
+            if (lg[i] > max_l) max_l = lg[i];
+        float sum_e = 0.0f;
+        for (int64_t i = 0; i < n; i++) {
+            ex[i] = exp_f32(lg[i] - max_l);
+            sum_e += ex[i];
+        }
+        if (sum_e <= 0.0f) {
+            tok = ids[0];
+        } else {
+            const float r = ao_rune_rng_next_float32(rng_state) * sum_e;
+            float acc = 0.0f;
+            tok = ids[n - 1];
+            for (int64_t i = 0; i < n; i++) {
+                acc += ex[i];
+                if (r <= acc) {
+                    tok = ids[i];
+                    break;
+                }
+            }
+        }
+    }
+    free(ids);
+    free(lg);
+    free(ex);
+    return tok;
+}
+
 /* GGUF block_q8_0: { f16 d; int8 qs[32]; } packed, 34 bytes. */
 #define Q8_0_BLOCK_BYTES 34
 

@@ -54,6 +54,26 @@ void ao_mul_f16(uint16_t *up, const uint16_t *gate, int64_t size);
 void ao_residual_add_f16(uint16_t *x, const uint16_t *residual, int64_t size);
 int64_t ao_argmax_f16(const uint16_t *logits, int64_t n);
 int64_t ao_greedy_sample_f16(const uint16_t *logits, int64_t n, const int64_t *suppress, int64_t n_suppress);
+/* sample_token_from_logits (sampler.mojo:217-305). ao_sampler_config holds its parameters. */
+typedef struct {
+    float temperature;
+    int64_t top_k;
+    float top_p;
+    float min_p;
+    float repetition_penalty;
+    float frequency_penalty;
+    float presence_penalty;
+} ao_sampler_config;
+/* The candidate list after the mask, penalties, temperature and truncations (ids and f32
+ * logits in candidate order); returns its length. */
+int64_t ao_sample_candidates_f16(const uint16_t *logits, int64_t vocab, const ao_sampler_config *cfg,
+                                 const int64_t *context, int64_t n_context, const int64_t *suppress,
+                                 int64_t n_suppress, int64_t *ids_out, float *logits_out);
+/* The sampled token; advances *rng_state when the draw consumes a random number. */
+int64_t ao_sample_token_f16(const uint16_t *logits, int64_t vocab, const ao_sampler_config *cfg,
+                            const int64_t *context, int64_t n_context, const int64_t *suppress,
+                            int64_t n_suppress, uint64_t *rng_state);
+float ao_rune_rng_next_float32(uint64_t *state);
 int ao_gemm_q8_0(const uint16_t *A, int64_t a_rows, int64_t a_cols, const uint8_t *blocks, int64_t b_rows,
                  uint16_t *C, int64_t c_rows, int64_t c_cols);
 void ao_dequantize_q8_0(const uint8_t *blocks, uint16_t *out, int64_t n_blocks);

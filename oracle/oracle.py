@@ -73,6 +73,12 @@ def lib():
         L.ao_generate.argtypes = [P, P, P, I64, I64, I64, P, I64, P, P, P, P, P]
         L.ao_rune_rng_next.argtypes = [P]
         L.ao_rune_rng_next.restype = C.c_uint64
+        L.ao_rune_rng_next_float32.argtypes = [P]
+        L.ao_rune_rng_next_float32.restype = C.c_float
+        L.ao_sample_candidates_f16.argtypes = [P, I64, P, P, I64, P, I64, P, P]
+        L.ao_sample_candidates_f16.restype = I64
+        L.ao_sample_token_f16.argtypes = [P, I64, P, P, I64, P, I64, P]
+        L.ao_sample_token_f16.restype = I64
         L.ao_fill_normal_f16.argtypes = [P, I64, C.c_uint64, C.c_uint64, C.c_float, C.c_float]
         L.ao_fill_normal_f16.restype = None
         L.ao_fill_normal_f32.argtypes = [P, I64, C.c_uint64, C.c_uint64, C.c_float, C.c_float]
@@ -189,6 +195,53 @@ def greedy_sample_f16(logits, suppress=()) -> int:
     logits = _f16(logits)
     s = np.ascontiguousarray(np.array(list(suppress) or [0], dtype=np.int64))
     return int(lib().ao_greedy_sample_f16(_ptr(logits), logits.size, _ptr(s), len(suppress)))
+
+
+class SamplerConfig(C.Structure):
+    """Parameters of sample_token_from_logits (sampler.mojo:217-230)."""
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_int64), ("top_p", C.c_float), ("min_p", C.c_float),
+                ("repetition_penalty", C.c_float), ("frequency_penalty", C.c_float),
+                ("presence_penalty", C.c_float)]
+
+    def __init__(self, temperature=1.0, top_k=0, top_p=1.0, min_p=0.0, repetition_penalty=1.0,
+                 frequency_penalty=0.0, presence_penalty=0.0):
+        super().__init__(temperature, top_k, top_p, min_p, repetition_penalty, frequency_penalty, presence_penalty)
+
+
+def _i64(seq):
+    return np.ascontiguousarray(np.array(list(seq) or [0], dtype=np.int64))
+
+
+def rune_rng_state(seed: int) -> int:
+    """RuneRNG.__init__ (sampler.mojo:25-29): seed 0 maps to 0x9E3779B97F4A7C15."""
+    return seed if seed != 0 else 0x9E3779B97F4A7C15
+
+
+def rune_rng_next_float32(state: int):
+    st = C.c_uint64(state)
+    v = lib().ao_rune_rng_next_float32(C.byref(st))
+    return float(v), st.value
+
+
+def sample_candidates_f16(logits, cfg: SamplerConfig, context=(), suppress=()):
+    """Candidate ids and f32 logits after the mask, penalties, temperature and truncations."""
+    logits = _f16(logits)
+    ids = np.zeros(logits.size, np.int64)
+    lg = np.zeros(logits.size, np.float32)
+    c, sp = _i64(context), _i64(suppress)
+    n = lib().ao_sample_candidates_f16(_ptr(logits), logits.size, C.byref(cfg), _ptr(c), len(context), _ptr(sp),
+                                       len(suppress), _ptr(ids), _ptr(lg))
+    return ids[:n], lg[:n]
+
+
+def sample_token_f16(logits, cfg: SamplerConfig, rng_state: int, context=(), suppress=()):
+    """sample_token_from_logits: (token, new RuneRNG state)."""
+    logits = _f16(logits)
+    c, sp = _i64(context), _i64(suppress)
+    st = C.c_uint64(rng_state)
+    tok = lib().ao_sample_token_f16(_ptr(logits), logits.size, C.byref(cfg), _ptr(c), len(context), _ptr(sp),
+                                    len(suppress), C.byref(st))
+    return int(tok), st.value
 
 
 def gemm_q8_0(A, blocks, n_rows) -> np.ndarray:

@@ -98,6 +98,8 @@ _sig("aesir_model_logits", [P, P])
 _sig("aesir_decode_loop", [P, I64, I64, I64, I32, P, C.POINTER(F32)])
 _sig("aesir_model_kernel_times", [P, I64, I32, P, I32])
 _sig("aesir_prefill", [P, P, I64, I64, P])
+_sig("aesir_sample_token", [P, P, I64, P, P, I64, P, I64, P, P])
+_sig("aesir_rune_rng_next", [P], C.c_uint64)
 _sig("aesir_model_fill_kv_random", [P, I64, C.c_uint64, F32])
 _sig("aesir_generation_stop_reason", [I64, I64, I64, I64, P, I64, I64, I64])
 _sig("aesir_generate", [P, P, I64, C.POINTER(_GenConfig), P, C.POINTER(I64), C.POINTER(I32)])
@@ -295,6 +297,43 @@ def gemm_q8_0(ctx: Context, A: Tensor, blocks_ptr: int, b_rows: int, C_: Tensor)
 
 def q8_0_matvec_f32(ctx: Context, blocks_ptr: int, n_rows: int, k: int, x: Tensor, y: Tensor):
     _check(_L.aesir_q8_0_matvec_f32(ctx.h, blocks_ptr, n_rows, k, x.ptr, y.ptr))
+
+
+class SamplerConfig(C.Structure):
+    """sample_token_from_logits parameters (core/sampler.mojo:217-230); defaults leave every stage off
+    except the draw at temperature 1."""
+    _fields_ = [("temperature", F32), ("top_k", I64), ("top_p", F32), ("min_p", F32),
+                ("repetition_penalty", F32), ("frequency_penalty", F32), ("presence_penalty", F32)]
+
+    def __init__(self, temperature=1.0, top_k=0, top_p=1.0, min_p=0.0, repetition_penalty=1.0,
+                 frequency_penalty=0.0, presence_penalty=0.0):
+        super().__init__(temperature, top_k, top_p, min_p, repetition_penalty, frequency_penalty, presence_penalty)
+
+
+class RuneRNG:
+    """RuneRNG (core/sampler.mojo:17-43) on the host; its state feeds sample_token."""
+
+    def __init__(self, seed: int = 42):
+        self.state = seed if seed != 0 else 0x9E3779B97F4A7C15
+
+    def next_u64(self) -> int:
+        st = C.c_uint64(self.state)
+        v = _L.aesir_rune_rng_next(C.byref(st))
+        self.state = st.value
+        return int(v)
+
+
+def sample_token(ctx: Context, logits: Tensor, cfg: SamplerConfig, rng: RuneRNG, context_tokens=(),
+                 suppress_tokens=()) -> int:
+    """sample_token_from_logits on the device (logits: f16 device tensor of vocab entries)."""
+    c = np.ascontiguousarray(np.array(list(context_tokens) or [0], dtype=np.int64))
+    sp = np.ascontiguousarray(np.array(list(suppress_tokens) or [0], dtype=np.int64))
+    st = C.c_uint64(rng.state)
+    tok = I64()
+    _check(_L.aesir_sample_token(ctx.h, logits.ptr, logits.size, C.byref(cfg), c.ctypes.data, len(context_tokens),
+                                 sp.ctypes.data, len(suppress_tokens), C.byref(st), C.byref(tok)))
+    rng.state = st.value
+    return tok.value
 
 
 class KVCache:

@@ -36,7 +36,7 @@ CXXFLAGS = [
 ]
 
 SOURCES = ["ctx.hip", "gemv.hip", "attention.hip", "basic.hip", "q8_0.hip", "abi_ops.hip", "model.hip",
-           "prefill.hip", "gguf.hip"]
+           "prefill.hip", "gguf.hip", "sampler.hip"]
 
 
 def _compile(src: str) -> str:

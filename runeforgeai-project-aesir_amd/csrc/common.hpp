@@ -56,6 +56,8 @@ struct RopeTable {
     void *dev = nullptr;
 };
 
+struct SamplerWork;  // device workspace of aesir_sample_token (sampler.hip)
+
 // Device scratch owned by the context for the standalone kernel entry points.
 struct CtxScratch {
     void *base = nullptr;
@@ -84,6 +86,7 @@ struct aesir_ctx {
     aesir::CtxScratch scratch;
     std::vector<aesir::RopeTable> rope_tables;
     int64_t *pinned_i64 = nullptr;  // small pinned staging area (64 entries)
+    aesir::SamplerWork *sampler = nullptr;  // grown on the first aesir_sample_token call
 };
 
 struct aesir_kv {
@@ -99,6 +102,8 @@ namespace aesir {
 int32_t bind(aesir_ctx *ctx);
 // Returns (building if needed) a RoPE table covering positions [0, min_pos).
 int32_t rope_table(aesir_ctx *ctx, float theta, int64_t head_dim, int64_t min_pos, const void **table);
+// Frees the sampler workspace of a context.
+void sampler_release(aesir_ctx *ctx);
 // Bump allocation in bytes from the well (256-byte aligned).
 int32_t well_alloc_bytes(aesir_ctx *ctx, int64_t bytes, void **out);
 

@@ -476,3 +476,178 @@ def test_generate_equals_manual_forward_steps(oracle):
             break
         nxt, _ = m.forward(kv, cur, len(cur) - 1)
     assert toks == manual and reason == "length"
+
+
+# ---------------------------------------------------------------- sampler stack (sampler.mojo:17-305)
+
+def test_rune_rng_textbook_value(oracle):
+    """RuneRNG(0) starts from 0x9E3779B97F4A7C15, so its first output is the first SplitMix64 output
+    for seed 0 (0xE220A8397B1DCDAF, the published test value); equal seeds give equal streams
+    (tests/test_inference.mojo:161-166)."""
+    import ctypes as C
+
+    st = C.c_uint64(oracle.rune_rng_state(0))
+    assert oracle.lib().ao_rune_rng_next(C.byref(st)) == 0xE220A8397B1DCDAF
+    a, b = oracle.rune_rng_state(12345), oracle.rune_rng_state(12345)
+    for _ in range(10):
+        ua, a = oracle.rune_rng_next_float32(a)
+        ub, b = oracle.rune_rng_next_float32(b)
+        assert ua == ub and 0.0 <= ua < 1.0
+
+
+def test_sampler_stage_known_answers(oracle):
+    """The stage tests of tests/test_inference.mojo:168-223, through the candidate list."""
+    S = oracle.SamplerConfig
+    f16 = lambda v: np.array(v, np.float16)
+    ids, lg = oracle.sample_candidates_f16(f16([2.0, 2.0]), S(repetition_penalty=2.0), context=[0])
+    assert lg.tolist() == [1.0, 2.0]
+    ids, lg = oracle.sample_candidates_f16(f16([4.0]), S(temperature=2.0))
+    assert lg.tolist() == [2.0]
+    ids, lg = oracle.sample_candidates_f16(f16([1.0, 5.0, 3.0]), S(top_k=2))
+    assert ids.tolist() == [1, 2]
+    ids, lg = oracle.sample_candidates_f16(f16([10.0, 0.0, -10.0]), S(top_p=0.9))
+    assert ids.tolist() == [0]
+    ids, lg = oracle.sample_candidates_f16(f16([10.0, 10.0]), S(frequency_penalty=1.0, presence_penalty=0.5),
+                                           context=[0, 0])
+    assert lg.tolist() == [7.5, 10.0]
+    ids, lg = oracle.sample_candidates_f16(f16([10.0, 2.0, -5.0]), S(min_p=0.1))
+    assert ids.tolist() == [0]
+    # negative logits are multiplied by the repetition penalty (:70-71)
+    ids, lg = oracle.sample_candidates_f16(f16([-2.0, 1.0]), S(repetition_penalty=2.0), context=[0, 1])
+    assert lg.tolist() == [-4.0, 0.5]
+    # suppressed ids sit at -1e9; non-finite logits become -1e9 (:9-14, :197-211)
+    ids, lg = oracle.sample_candidates_f16(f16([1.0, np.inf, 3.0]), S(), suppress=[2])
+    assert lg.tolist() == [1.0, -1e9, -1e9]
+
+
+def _reference_stack(logits, cfg, context, suppress, u):
+    """Literal restatement of sample_token_from_logits for small vocabularies: f32 scalars, the
+    stable insertion sort of sort_candidates_descending, sequential sums; u is the draw's uniform."""
+    f = np.float32
+    ex = lambda x: f(math.exp(float(x)))
+    c = []
+    for i, x in enumerate(np.asarray(logits, np.float16).astype(np.float32)):
+        c.append([i, f(-1e9) if (np.isnan(x) or np.isinf(x)) else f(x)])
+    for cand in c:
+        if cand[0] in suppress:
+            cand[1] = f(-1e9)
+    if cfg["rp"] != 1.0 and context:
+        for cand in c:
+            if cand[0] in context:
+                cand[1] = cand[1] * f(cfg["rp"]) if cand[1] < 0 else cand[1] / f(cfg["rp"])
+    if not (cfg["fp"] == 0.0 and cfg["pp"] == 0.0) and context:
+        for cand in c:
+            n = context.count(cand[0])
+            if n > 0:
+                cand[1] = cand[1] - (f(n) * f(cfg["fp"]) + f(cfg["pp"]))
+    if cfg["t"] > 0 and cfg["t"] != 1.0:
+        inv = f(1.0) / f(cfg["t"])
+        for cand in c:
+            cand[1] = cand[1] * inv
+
+    def isort(c):
+        for i in range(1, len(c)):
+            key = c[i]
+            j = i - 1
+            while j >= 0 and c[j][1] < key[1]:
+                c[j + 1] = c[j]
+                j -= 1
+            c[j + 1] = key
+        return c
+
+    def probs(c):
+        mx = c[0][1]
+        p = [ex(x[1] - mx) for x in c]
+        s = f(0.0)
+        for v in p:
+            s = f(s + v)
+        return [f(v / s) for v in p] if s > 0 else p
+
+    if cfg["k"] > 0 and cfg["k"] < len(c):
+        c = isort(c)[: cfg["k"]]
+    if cfg["p"] < 1.0 and len(c) > 1:
+        c = isort(c)
+        cum, cut = f(0.0), len(c) - 1
+        for i, v in enumerate(probs(c)):
+            cum = f(cum + v)
+            if cum >= f(cfg["p"]):
+                cut = i
+                break
+        c = c[: cut + 1]
+    if 0.0 < cfg["m"] < 1.0 and len(c) > 1:
+        c = isort(c)
+        pr = probs(c)
+        th = f(cfg["m"]) * pr[0]
+        kept = []
+        for i, v in enumerate(pr):
+            if v >= th:
+                kept.append(c[i])
+            else:
+                break
+        c = kept or c
+    mx = max(x[1] for x in c)
+    e = [ex(x[1] - mx) for x in c]
+    s = f(0.0)
+    for v in e:
+        s = f(s + v)
+    if s <= 0:
+        return c[0][0]
+    r, acc = f(f(u) * s), f(0.0)
+    for i, v in enumerate(e):
+        acc = f(acc + v)
+        if r <= acc:
+            return c[i][0]
+    return c[-1][0]
+
+
+@pytest.mark.parametrize("cfgd", [
+    dict(t=0.8, k=0, p=1.0, m=0.0, rp=1.0, fp=0.0, pp=0.0),
+    dict(t=1.3, k=7, p=1.0, m=0.0, rp=1.3, fp=0.2, pp=0.1),
+    dict(t=0.7, k=0, p=0.8, m=0.0, rp=1.0, fp=0.0, pp=0.0),
+    dict(t=1.0, k=20, p=0.9, m=0.05, rp=1.1, fp=0.0, pp=0.5),
+    dict(t=2.0, k=0, p=1.0, m=0.2, rp=1.0, fp=0.3, pp=0.0),
+])
+def test_sampler_matches_literal_restatement(oracle, cfgd):
+    """Small vocabularies with many tied logits (values on a coarse grid) so the stable-sort order
+    matters; 40 draws per config from one RuneRNG stream."""
+    rng = np.random.default_rng(7)
+    cfg = oracle.SamplerConfig(temperature=cfgd["t"], top_k=cfgd["k"], top_p=cfgd["p"], min_p=cfgd["m"],
+                               repetition_penalty=cfgd["rp"], frequency_penalty=cfgd["fp"],
+                               presence_penalty=cfgd["pp"])
+    state = oracle.rune_rng_state(99)
+    for draw in range(40):
+        logits = (rng.integers(-8, 8, 48) * 0.5).astype(np.float16)
+        context = rng.integers(0, 48, 10).tolist()
+        suppress = rng.integers(0, 48, 2).tolist()
+        u, _ = oracle.rune_rng_next_float32(state)
+        want = _reference_stack(logits, cfgd, context, suppress, u)
+        got, state = oracle.sample_token_f16(logits, cfg, state, context, suppress)
+        assert got == want, (draw, got, want)
+
+
+def test_sampler_draw_frequencies(oracle):
+    """The draw is inverse-CDF sampling: over 20000 draws the empirical frequencies of an 8-token
+    vocabulary match softmax(logits / T) within 5 standard errors."""
+    logits = np.array([0.5, 1.5, -1.0, 2.0, 0.0, 1.0, -0.5, 0.25], np.float16)
+    T = 1.5
+    cfg = oracle.SamplerConfig(temperature=T)
+    p = np.exp(logits.astype(np.float64) / T)
+    p /= p.sum()
+    state, n = oracle.rune_rng_state(2024), 20000
+    counts = np.zeros(8)
+    for _ in range(n):
+        t, state = oracle.sample_token_f16(logits, cfg, state)
+        counts[t] += 1
+    se = np.sqrt(p * (1 - p) / n)
+    assert np.all(np.abs(counts / n - p) < 5 * se), (counts / n, p)
+
+
+def test_sampler_greedy_branch_and_rng_use(oracle):
+    """temperature <= 0 or top_k == 1 is the greedy branch and consumes no random number."""
+    x = np.array([1.0, np.inf, 2.0, np.nan, 2.0], np.float16)
+    st = oracle.rune_rng_state(5)
+    for cfg in (oracle.SamplerConfig(temperature=0.0), oracle.SamplerConfig(temperature=1.0, top_k=1)):
+        t, st2 = oracle.sample_token_f16(x, cfg, st, suppress=[2])
+        assert t == oracle.greedy_sample_f16(x, suppress=[2]) == 4 and st2 == st
+    t, st3 = oracle.sample_token_f16(x, oracle.SamplerConfig(temperature=1.0), st)
+    assert st3 != st

@@ -144,6 +144,52 @@ def prefill_bench(A, seed: int, n_prompt: int = 128, n_decode: int = 256, reps: 
             "decode_tok_s": round(n_decode / dec, 1) if n_decode > 0 else None, "first_tokens": [nxt] + toks[:3]}
 
 
+def q8_mat_bytes(rows: int, cols: int) -> int:
+    """Q8_0 matrix in HBM: int8 quants plus one f16 scale per 32 weights (34 bytes per block)."""
+    return rows * cols + rows * (cols // 32) * 2
+
+
+Q8_LAYER_BYTES = (q8_mat_bytes(DIM + 2 * KV_DIM, DIM) + q8_mat_bytes(DIM, DIM) + q8_mat_bytes(2 * FFN, DIM)
+                  + q8_mat_bytes(DIM, FFN) + 2 * 2 * DIM)
+Q8_TOKEN_WEIGHT_BYTES = LAYERS * Q8_LAYER_BYTES + q8_mat_bytes(VOCAB, DIM) + 2 * DIM + q8_mat_bytes(1, DIM)
+Q8_GATE_UP_BYTES = q8_mat_bytes(2 * FFN, DIM) + DIM * 2 + DIM * 2 + FFN * 2
+
+
+def q8_bench(A, seed: int, kv: int, steps: int, warmup: int, kernel_iters: int) -> dict:
+    """Batch-1 greedy decode of the Llama-3-8B shape with Q8_0 matrices (GGUF block_q8_0 data
+    repacked as int8 quants + f16 scales; random quants, scales for weights of std 0.02), KV cache
+    pre-filled to kv positions; same step structure as the F16 decode."""
+    ctx_len = kv + max(steps, warmup) + 64
+    well = int(Q8_TOKEN_WEIGHT_BYTES + q8_mat_bytes(VOCAB - 1, DIM) + 2 * LAYERS * ctx_len * KV_DIM * 2 + (512 << 20))
+    ctx = A.Context(well)
+    m = A.Model.create(ctx, A.ModelConfig(DIM, LAYERS, HEADS, KV_HEADS, FFN, VOCAB, ctx_len), A.GGML_Q8_0)
+    m.init_random(seed, 0.02, 0.0, 0.02)
+    m.fill_kv_random(kv, seed=seed + 1)
+    m.decode_loop(1, kv, warmup)
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    toks, event_ms = m.decode_loop(1, kv, steps)
+    ctx.synchronize()
+    wall = time.perf_counter() - t0
+    tok_s = steps / wall
+    mean_kv = kv + (steps - 1) / 2.0 + 1
+    step_bytes = Q8_TOKEN_WEIGHT_BYTES + KV_BYTES_PER_POS * mean_kv + KV_BYTES_PER_POS
+    kt = m.kernel_times(kv, iters=kernel_iters)
+    gu_ms = kt["gate_up_swiglu"]
+    m.close()
+    ctx.close()
+    return {"workload": f"llama3-8b-shape q8_0 batch-1 greedy decode, kv {kv}", "value": round(tok_s, 2),
+            "unit": "tok/s", "steps": steps, "ms_per_step": round(wall * 1e3 / steps, 4),
+            "dtype": "q8_0 weights (f16(q*d)), f16 activations, f32 accumulate",
+            "step_hbm": {"bytes_per_token": int(step_bytes), "achieved_gbs": round(step_bytes * tok_s / 1e9, 1),
+                         "frac": round(step_bytes * tok_s / 1e9 / HBM_PEAK_GBS, 4),
+                         "event_ms_per_step": round(event_ms / steps, 4)},
+            "gate_up_swiglu": {"avg_launch_ms": round(gu_ms, 5), "bytes_per_launch": Q8_GATE_UP_BYTES,
+                               "achieved_gbs": round(Q8_GATE_UP_BYTES / (gu_ms * 1e-3) / 1e9, 1),
+                               "frac": round(Q8_GATE_UP_BYTES / (gu_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+            "kernel_ms": {k: round(v, 5) for k, v in kt.items()}, "tokens_head": toks[:8]}
+
+
 def measured_traffic():
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary
     (FETCH_SIZE + WRITE_SIZE, each scaled by its copy-kernel calibration factor), or None."""
@@ -172,6 +218,8 @@ def main():
     ap.add_argument("--prefill-only", action="store_true", help="run only the TinyLlama prefill measurement")
     ap.add_argument("--prefill-decode-steps", type=int, default=256,
                     help="greedy decode steps after the prefill in --prefill-only runs (0: none)")
+    ap.add_argument("--no-q8", action="store_true", help="skip the Q8_0-weight decode measurement")
+    ap.add_argument("--q8-only", action="store_true", help="run only the Q8_0-weight decode measurement")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain 256 MiB device-to-device copy (the FETCH_SIZE / WRITE_SIZE calibration "
                          "of the HBM traffic figure) and exit")
@@ -189,6 +237,9 @@ def main():
 
     if args.prefill_only:
         print(json.dumps({"prefill": prefill_bench(A, args.seed, n_decode=args.prefill_decode_steps)}))
+        return
+    if args.q8_only:
+        print(json.dumps({"q8_0": q8_bench(A, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters)}))
         return
 
     ctx_len = args.kv + max(args.steps, args.warmup) + 64
@@ -250,6 +301,8 @@ def main():
     ctx.close()
     if not args.no_prefill:
         out["prefill"] = prefill_bench(A, args.seed)
+    if not args.no_q8:
+        out["q8_0"] = q8_bench(A, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.kv, args.cpu_reps)
         out["cpu_baseline"]["value"] = round(out["cpu_baseline"]["value"], 4)

@@ -40,6 +40,10 @@ extern "C" {
 /* GGML tensor type ids accepted by aesir_model_set_tensor (loader/gguf.mojo:17-19). */
 #define AESIR_GGML_F32 0
 #define AESIR_GGML_F16 1
+/* GGML block_q8_0 {f16 d; int8 qs[32]} (34 bytes per 32 weights). The reference dequantizes it in
+ * gemm_q8_0 (core/compute.mojo:1038-1065) but its loader rejects it (loader/gguf.mojo:450-463);
+ * here it is also a model weight type (aesir_model_create_typed, aesir_model_load_gguf). */
+#define AESIR_GGML_Q8_0 8
 
 /* GPURealmType.AMD_ROCM_HIP (core/mimir_well.mojo:99): the realm id this library serves. */
 #define AESIR_REALM_AMD_ROCM_HIP 1
@@ -201,24 +205,41 @@ typedef struct {
  * interleaved), norms, KV cache [layers][ctx_len][kv_dim] x2, decode workspace. The weights
  * start zeroed. Validates the GGUFModelConfig contract (loader/gguf.mojo:133-149). */
 int32_t aesir_model_create(aesir_ctx *ctx, const aesir_model_config *cfg, aesir_model **out);
+/* aesir_model_create with a weight type for the seven matrix kinds (token_embd, output, attn_q/k/v,
+ * attn_output, ffn_gate/up/down): AESIR_GGML_F16 (what aesir_model_create makes) or
+ * AESIR_GGML_Q8_0. A Q8_0 model keeps each matrix as int8 quants [rows][cols] plus f16 block
+ * scales [rows][cols/32] in HBM (same fused row order as F16); dim and ffn must be multiples of
+ * 32 (and at most 16384). Every weight is used as w = f16(f16(q) * d), gemm_q8_0's rule
+ * (core/compute.mojo:1062-1063), so a Q8_0 model computes what the F16 model holding the
+ * dequantized weights computes. Norm vectors stay f16. No reference counterpart as a model
+ * (the reference loader has no Q8_0 model path). */
+int32_t aesir_model_create_typed(aesir_ctx *ctx, const aesir_model_config *cfg, int32_t weight_type,
+                                 aesir_model **out);
+/* Weight type of the model's matrices (AESIR_GGML_F16 or AESIR_GGML_Q8_0). */
+int32_t aesir_model_weight_type(const aesir_model *model);
 int32_t aesir_model_destroy(aesir_model *model);
 int32_t aesir_model_get_config(const aesir_model *model, aesir_model_config *cfg);
 /* Uploads one tensor by its GGUF name ("token_embd.weight", "blk.N.attn_q.weight", ...),
  * host data in GGUF order (rows x cols, cols fastest). F32 tensors are rounded to f16 as
  * loader/gguf.mojo:486-493 does. Shape and type are checked against
- * _validate_required_tensors (loader/gguf.mojo:567-628) with its messages. */
+ * _validate_required_tensors (loader/gguf.mojo:567-628) with its messages. The matrices of a
+ * Q8_0 model take AESIR_GGML_Q8_0 data: rows x (cols/32) packed 34-byte blocks. */
 int32_t aesir_model_set_tensor(aesir_model *model, const char *name, const void *host_data, int64_t rows,
                                int64_t cols, int32_t ggml_type);
-/* Reads a tensor back in GGUF order as f16 (for verification). */
+/* Reads a tensor back in GGUF order as f16 (for verification); Q8_0 matrices come back
+ * dequantized, f16(q * d) per element. */
 int32_t aesir_model_get_tensor(aesir_model *model, const char *name, void *host_out, int64_t elements);
 /* Device-side seeded random init: every weight N(0, std), every norm N(norm_mean, norm_std),
  * rounded to f16; element i of tensor t uses the same counter-based Box-Muller stream as the
- * test oracle's generator. For models too large to build on the host. */
+ * test oracle's generator. For models too large to build on the host. Q8_0 matrices get
+ * quants uniform in [-127, 127] and block scales uniform in [0.5, 1.5) * std / 64 (weights of
+ * standard deviation near std). */
 int32_t aesir_model_init_random(aesir_model *model, uint64_t seed, float std, float norm_mean, float norm_std);
 /* GGUFSeer.mmap_and_load (loader/gguf.mojo:664-690) + AesirEngine.__init__'s layer setup
  * (aesir.mojo:237-296): parses a GGUF v3 Llama F16 file, enforces the reference loader
  * contract, creates the model (KV rows = ctx_len_override if > 0, else llama.context_length)
- * and uploads every tensor into HBM. */
+ * and uploads every tensor into HBM. Beyond the reference loader it also takes files whose
+ * seven matrix kinds are all Q8_0 (norms F32 or F16), giving a Q8_0 model. */
 int32_t aesir_model_load_gguf(aesir_ctx *ctx, const char *path, int64_t ctx_len_override, aesir_model **out);
 
 /* GGUFSeer.inspect_metadata (loader/gguf.mojo:649-662), extended to the tensor table: parses and

@@ -86,6 +86,8 @@ _sig("aesir_kv_append", [P, P, I64, I64, P, I64, P, I64])
 _sig("aesir_kv_k_slice", [P, I64, I64, C.POINTER(P)])
 _sig("aesir_kv_v_slice", [P, I64, I64, C.POINTER(P)])
 _sig("aesir_model_create", [P, C.POINTER(_ModelConfig), C.POINTER(P)])
+_sig("aesir_model_create_typed", [P, C.POINTER(_ModelConfig), I32, C.POINTER(P)])
+_sig("aesir_model_weight_type", [P])
 _sig("aesir_model_destroy", [P])
 _sig("aesir_model_get_config", [P, C.POINTER(_ModelConfig)])
 _sig("aesir_model_set_tensor", [P, C.c_char_p, P, I64, I64, I32])
@@ -385,9 +387,39 @@ class ModelConfig:
                             self.ctx_len, self.rms_eps, self.rope_theta, self.bos_token_id, self.eos_token_id)
 
 
+GGML_F32, GGML_F16, GGML_Q8_0 = 0, 1, 8
+
+
+class Q8_0Tensor:
+    """A rows x cols matrix as GGUF block_q8_0 data: rows * cols / 32 packed 34-byte blocks
+    {f16 d; int8 qs[32]} in row order (the bytes a GGUF file holds for a GGML type-8 tensor)."""
+
+    def __init__(self, blocks: np.ndarray, rows: int, cols: int):
+        if cols % 32:
+            raise ValueError("Q8_0 rows must be a multiple of 32 long")
+        self.blocks = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(rows * cols // 32, 34)
+        self.rows, self.cols = rows, cols
+
+    @classmethod
+    def from_parts(cls, d: np.ndarray, q: np.ndarray) -> "Q8_0Tensor":
+        """d: f16 scales [rows, cols/32]; q: int8 quants [rows, cols]."""
+        rows, cols = q.shape
+        nb = rows * cols // 32
+        blocks = np.empty((nb, 34), np.uint8)
+        blocks[:, :2] = np.ascontiguousarray(d, np.float16).reshape(nb).view(np.uint8).reshape(nb, 2)
+        blocks[:, 2:] = np.ascontiguousarray(q, np.int8).reshape(nb, 32).view(np.uint8)
+        return cls(blocks, rows, cols)
+
+    def dequantize(self) -> np.ndarray:
+        """f16(q * d) per element (the product is exact in f32, then one rounding)."""
+        d = self.blocks[:, :2].copy().view(np.float16).astype(np.float32)
+        q = self.blocks[:, 2:].copy().view(np.int8).astype(np.float32)
+        return (q * d).astype(np.float16).reshape(self.rows, self.cols)
+
+
 class Model:
-    """One Llama F16 model in HBM: forward_pass (core/inference.mojo:424-518) and the generation
-    loop (aesir.mojo:323-462)."""
+    """One Llama model in HBM (F16 or Q8_0 matrices): forward_pass (core/inference.mojo:424-518)
+    and the generation loop (aesir.mojo:323-462)."""
 
     def __init__(self, ctx: Context, handle: int):
         self.ctx, self.h = ctx, handle
@@ -397,11 +429,18 @@ class Model:
                                c.rope_theta, c.bos_token_id, c.eos_token_id)
 
     @classmethod
-    def create(cls, ctx: Context, cfg: ModelConfig) -> "Model":
+    def create(cls, ctx: Context, cfg: ModelConfig, weight_type: int = GGML_F16) -> "Model":
         h = P()
         c = cfg._c()
-        _check(_L.aesir_model_create(ctx.h, C.byref(c), C.byref(h)))
+        if weight_type == GGML_F16:
+            _check(_L.aesir_model_create(ctx.h, C.byref(c), C.byref(h)))
+        else:
+            _check(_L.aesir_model_create_typed(ctx.h, C.byref(c), weight_type, C.byref(h)))
         return cls(ctx, h.value)
+
+    @property
+    def weight_type(self) -> int:
+        return _L.aesir_model_weight_type(self.h)
 
     @classmethod
     def load_gguf(cls, ctx: Context, path: str, ctx_len: int = 0) -> "Model":
@@ -420,7 +459,11 @@ class Model:
         except Exception:
             pass
 
-    def set_tensor(self, name: str, data: np.ndarray):
+    def set_tensor(self, name: str, data):
+        if isinstance(data, Q8_0Tensor):
+            _check(_L.aesir_model_set_tensor(self.h, name.encode(), data.blocks.ctypes.data, data.rows, data.cols,
+                                             GGML_Q8_0))
+            return
         data = np.asarray(data)
         ggml = 0 if data.dtype == np.float32 else 1
         data = np.ascontiguousarray(data, dtype=np.float32 if ggml == 0 else np.float16)

@@ -173,6 +173,36 @@ int32_t launch_fill_normal(hipStream_t s, void *dst, int64_t n, int64_t cols, in
     return AESIR_OK;
 }
 
+// Q8_0 init: quant i (row i / cols, column i % cols) uniform in [-127, 127] (standard deviation
+// 73.3); block j's scale uniform in [0.5, 1.5) * std / 64, rounded to f16, so the weights have a
+// standard deviation near std. Counter streams as in fill_normal_kernel (quants from odd
+// counters, scales from even ones).
+__global__ __launch_bounds__(kEThreads) void fill_q8_0_kernel(int8_t *__restrict__ q, int64_t q_stride,
+                                                              h16 *__restrict__ d, int64_t d_stride, int64_t rows,
+                                                              int64_t cols, uint64_t base, double dscale) {
+    const int64_t nb = cols / 32, n = rows * cols;
+    for (int64_t i = (int64_t)blockIdx.x * kEThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kEThreads) {
+        const uint64_t a = mix64(base + (uint64_t)(2 * i + 1) * kGolden);
+        q[(i / cols) * q_stride + i % cols] = (int8_t)((int)((a >> 32) % 255u) - 127);
+        if (i % 32 == 0) {
+            const int64_t j = i / 32;
+            const uint64_t b = mix64(base + (uint64_t)(2 * j + 2) * kGolden);
+            const double u = (double)(b >> 40) * (1.0 / 16777216.0);
+            d[(j / nb) * d_stride + j % nb] = (h16)(float)((0.5 + u) * dscale);
+        }
+    }
+}
+
+int32_t launch_fill_q8_0(hipStream_t s, void *q, int64_t q_stride, void *d, int64_t d_stride, int64_t rows,
+                         int64_t cols, uint64_t seed, uint64_t stream, float std) {
+    if (cols % 32 != 0) return fail(AESIR_ERR_SHAPE, "fill_q8_0: columns must be a multiple of 32");
+    const uint64_t base = mix64(seed ^ mix64(stream + kGolden));
+    hipLaunchKernelGGL(fill_q8_0_kernel, dim3(grid_for(rows * cols, kEThreads * 8)), dim3(kEThreads), 0, s,
+                       (int8_t *)q, q_stride, (h16 *)d, d_stride, rows, cols, base, (double)std / 64.0);
+    AESIR_LAUNCH_CHECK("fill_q8_0_kernel");
+    return AESIR_OK;
+}
+
 __global__ __launch_bounds__(kEThreads) void f32_to_f16_kernel(const float *__restrict__ src, h16 *__restrict__ dst,
                                                                int64_t n) {
     for (int64_t i = (int64_t)blockIdx.x * kEThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kEThreads)

@@ -409,7 +409,7 @@ struct EpiLmHead {
     template <int ROWS>
     __device__ __forceinline__ void apply(int64_t n0, int64_t, int64_t N, const float *s, int tid, NoPre) const {
         if (tid < ROWS && n0 + tid < N) logits[n0 + tid] = (h16)s[tid];
-        if (tid == 0) parts[blockIdx.x] = group_scan<ROWS>(n0, N, s);
+        if (tid == 0 && n0 < N) parts[n0 / ROWS] = group_scan<ROWS>(n0, N, s);
     }
 };
 
@@ -455,6 +455,190 @@ __global__ __launch_bounds__(kFinishThreads) void argmax_finish_kernel(const Arg
             state->step = state->step + 1;
         }
     }
+}
+
+// ------------------------------------------------------------------ Q8_0 weights
+//
+// Q8_0 matrices are repacked in HBM as int8 quants [N][K] (rows 32-byte aligned) plus f16 block
+// scales [N][K / 32]. Thread t multiplies k = 16t + 4096i: one 16-byte quant load (half a block)
+// and one 2-byte scale per row and slab, so a wave streams contiguous 1 KiB of quants per row.
+// Dequantization reproduces gemm_q8_0 (compute.mojo:1038-1065) exactly: w = f16(f16(q) * d).
+// The int8 -> f16 conversion is exact through the exponent trick (byte ^ 0x80 placed under the
+// f16 exponent 0x64 reads 1152 + q; subtracting 1152 is exact), the scale product is a packed f16
+// multiply (one round to nearest even, as hmul), the dot product v_dot2_f32_f16.
+constexpr int kQSlab = kThreads * 16;  // k elements covered by one pass of the workgroup
+// Rows per group of the Q8_0 decode GEMVs, and row groups per workgroup. Measured on MI355X
+// (Llama-3-8B shapes, us per launch): 4 rows beat 8 and 16 on every GEMV; 2 groups per workgroup
+// take gate/up from 24.2 to 23.2 but slow the 4096-row GEMVs (QKV 7.7 -> 9.1, O 5.7 -> 6.2), and
+// 4 or 8 groups are slower still.
+constexpr int kQ8Rows = 4;
+
+// f16 values f16(q_j * d) of 16 quants, as two 8-element chunks.
+__device__ __forceinline__ void deq16(u32x4 q, h16 d, u32x4 &o0, u32x4 &o1) {
+    const unsigned qw[4] = {q.x, q.y, q.z, q.w};
+    unsigned o[8];
+    const h16x2 bias = {(h16)1152.0f, (h16)1152.0f}, dd = {d, d};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const unsigned w = qw[j] ^ 0x80808080u;
+        const h16x2 lo = as_h2(__builtin_amdgcn_perm(0x64646464u, w, 0x04010400u)) - bias;  // q0, q1
+        const h16x2 hi = as_h2(__builtin_amdgcn_perm(0x64646464u, w, 0x04030402u)) - bias;  // q2, q3
+        o[2 * j] = h2_bits(lo * dd);
+        o[2 * j + 1] = h2_bits(hi * dd);
+    }
+    o0 = u32x4{o[0], o[1], o[2], o[3]};
+    o1 = u32x4{o[4], o[5], o[6], o[7]};
+}
+
+// x source of a Q8_0 launch: x itself, or (layer 0) row token->token of the Q8_0 embedding table,
+// dequantized in registers, with workgroup 0 writing the row to xcopy (the residual stream).
+struct Q8XSrc {
+    const h16 *x;
+    const int8_t *eq;
+    const h16 *ed;
+    const DecodeState *token;
+    h16 *xcopy;
+};
+
+// The Q8_0 twin of gemv_fixed_kernel (NS = ceil(K / 4096) slabs, K % 32 == 0): x chunks stay in
+// registers, optionally RMS-normalized once per workgroup. A workgroup owns G consecutive groups
+// of ROWS rows; the weight requests run one (group, slab) step ahead of the dot products through a
+// register double buffer, so the next group's rows are in flight during a group's reduction and
+// epilogue, and x is loaded and normalized once for G groups.
+template <int ROWS, int NS, int G, bool NORM, class Epi>
+__global__ __launch_bounds__(kThreads) void gemv_q8_kernel(const int8_t *__restrict__ Wq, const h16 *__restrict__ Wd,
+                                                           int64_t N, int64_t K, Q8XSrc src,
+                                                           const h16 *__restrict__ nw, float eps, Epi epi) {
+    __shared__ float red[4 * ROWS];
+    __shared__ float sums[ROWS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t nbase = (int64_t)blockIdx.x * G * ROWS;
+    const int64_t k0 = (int64_t)tid * 16;
+    const int64_t KB = K / 32;
+    auto row = [&](int g, int r) -> int64_t {
+        const int64_t n = nbase + (int64_t)g * ROWS + r;
+        return n < N ? n : N - 1;
+    };
+    u32x4 xr[NS][2], nr[NS][2];
+    bool live[NS];
+    const bool embed = src.eq != nullptr;
+    const int64_t trow = embed ? src.token->token : 0;
+#pragma unroll
+    for (int i = 0; i < NS; i++) {
+        const int64_t k = k0 + (int64_t)i * kQSlab;
+        live[i] = k < K;  // false in a partial slab (and for every thread beyond K when K < 4096)
+        const int64_t kc = live[i] ? k : 0;
+        if (embed) {
+            xr[i][0] = ld16(src.eq + trow * K + kc);  // quants; dequantized below
+            xr[i][1].x = h_to_bits(src.ed[trow * KB + kc / 32]);
+        } else {
+            xr[i][0] = ld16(src.x + kc);
+            xr[i][1] = ld16(src.x + kc + 8);
+        }
+        if (NORM) {
+            nr[i][0] = ld16(nw + kc);
+            nr[i][1] = ld16(nw + kc + 8);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const int64_t kf = k0 < K ? k0 : 0;
+    u32x4 qb[2][ROWS];
+    h16 db[2][ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; r++) {
+        const int64_t n = row(0, r);
+        qb[0][r] = ld16_stream(Wq + n * K + kf);
+        db[0][r] = Wd[n * KB + kf / 32];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    using Pre = decltype(epi.template prefetch<ROWS>(0, 0, N, tid));
+    Pre pre[G];
+    pre[0] = epi.template prefetch<ROWS>(nbase, 0, N, tid);
+
+    float ss = 0.0f;
+    h16 *xcopy = (src.xcopy && blockIdx.x == 0) ? src.xcopy : nullptr;
+#pragma unroll
+    for (int i = 0; i < NS; i++) {
+        if (embed) deq16(xr[i][0], bits_to_h((uint16_t)xr[i][1].x), xr[i][0], xr[i][1]);
+        if (!live[i]) xr[i][0] = xr[i][1] = u32x4{0u, 0u, 0u, 0u};
+        if (xcopy && live[i]) {
+            st16(xcopy + k0 + (int64_t)i * kQSlab, xr[i][0]);
+            st16(xcopy + k0 + (int64_t)i * kQSlab + 8, xr[i][1]);
+        }
+        if (NORM) ss = sumsq8(xr[i][1], sumsq8(xr[i][0], ss));
+    }
+    if (NORM) {
+        ss = block_sum<kThreads / kWave>(ss, red);
+        const h16 inv = (h16)(1.0f / sqrtf(ss / (float)K + eps));
+#pragma unroll
+        for (int i = 0; i < NS; i++) {
+            xr[i][0] = norm8(xr[i][0], nr[i][0], inv);
+            xr[i][1] = norm8(xr[i][1], nr[i][1], inv);
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        float acc[ROWS];
+#pragma unroll
+        for (int r = 0; r < ROWS; r++) acc[r] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NS; i++) {
+            const int st = g * NS + i;
+            if (st + 1 < G * NS) {  // request step st + 1: (group gn, slab kn)
+                const int gn = (st + 1) / NS, in = (st + 1) % NS;
+                const int64_t k = k0 + (int64_t)in * kQSlab;
+                const int64_t kc = k < K ? k : kf;  // dead lanes of a partial slab re-read their first chunk
+#pragma unroll
+                for (int r = 0; r < ROWS; r++) {
+                    const int64_t n = row(gn, r);
+                    qb[(st + 1) & 1][r] = ld16_stream(Wq + n * K + kc);
+                    db[(st + 1) & 1][r] = Wd[n * KB + kc / 32];
+                }
+                if (in == 0) pre[gn] = epi.template prefetch<ROWS>(nbase + (int64_t)gn * ROWS, 0, N, tid);
+            }
+#pragma unroll
+            for (int r = 0; r < ROWS; r++) {
+                u32x4 w0, w1;
+                deq16(qb[st & 1][r], db[st & 1][r], w0, w1);
+                acc[r] = dot8(w1, xr[i][1], dot8(w0, xr[i][0], acc[r]));
+            }
+        }
+        wave_multi_sum<ROWS>(acc, lane);
+        constexpr int GW = kWave / ROWS;
+        if ((lane & (GW - 1)) == 0) red[wave * ROWS + lane / GW] = acc[0];
+        __syncthreads();
+        if (tid < ROWS) sums[tid] = (red[tid] + red[ROWS + tid]) + (red[2 * ROWS + tid] + red[3 * ROWS + tid]);
+        __syncthreads();
+        epi.template apply<ROWS>(nbase + (int64_t)g * ROWS, 0, N, sums, tid, pre[g]);
+    }
+}
+
+template <int ROWS, int G, bool NORM, class Epi>
+static int32_t gemv_q8_dispatch(hipStream_t s, const void *Wq, const void *Wd, int64_t N, int64_t K, const Q8XSrc &src,
+                                const void *nw, float eps, const Epi &epi, const char *name) {
+    const void *xp = src.eq ? (const void *)src.eq : (const void *)src.x;
+    if (K % 32 != 0 || ((uintptr_t)Wq & 15) || ((uintptr_t)xp & 15) || (NORM && ((uintptr_t)nw & 15)) ||
+        (src.xcopy && ((uintptr_t)src.xcopy & 15)))
+        return fail(AESIR_ERR_UNSUPPORTED, "%s: Q8_0 GEMV needs K %% 32 == 0 and 16-byte aligned rows", name);
+    const int64_t ns = (K + kQSlab - 1) / kQSlab;
+    const dim3 grid((unsigned)((N + ROWS * G - 1) / (ROWS * G)));
+    if (grid.x == 0) return AESIR_OK;
+    switch (ns) {
+#define AESIR_GEMV_Q8(NSV)                                                                                        \
+    case NSV:                                                                                                    \
+        hipLaunchKernelGGL((gemv_q8_kernel<ROWS, NSV, G, NORM, Epi>), grid, dim3(kThreads), 0, s,                 \
+                           (const int8_t *)Wq, (const h16 *)Wd, N, K, src, (const h16 *)nw, eps, epi);            \
+        break;
+        AESIR_GEMV_Q8(1)
+        AESIR_GEMV_Q8(2)
+        AESIR_GEMV_Q8(3)
+        AESIR_GEMV_Q8(4)
+#undef AESIR_GEMV_Q8
+        default:
+            return fail(AESIR_ERR_UNSUPPORTED, "%s: Q8_0 GEMV with K = %lld exceeds 16384", name, (long long)K);
+    }
+    AESIR_LAUNCH_CHECK(name);
+    return AESIR_OK;
 }
 
 // ------------------------------------------------------------------ launchers
@@ -530,19 +714,32 @@ int32_t launch_gemm_f16(aesir_ctx *ctx, const void *A, int64_t M, int64_t K, con
 int32_t launch_qkv_rope_kv(hipStream_t s, const QkvArgs &a) {
     EpiQkv e{(h16 *)a.q_out, (h16 *)a.k_cache, (h16 *)a.v_cache, (const h16x2 *)a.rope, a.state,
              a.dim, a.kvd, a.head_dim, a.max_seq};
+    if (a.w_scale) {  // Q8_0 weights (and, for layer 0, a Q8_0 embedding table)
+        const Q8XSrc src = a.embd ? Q8XSrc{nullptr, (const int8_t *)a.embd, (const h16 *)a.embd_scale, a.state, (h16 *)a.x}
+                                  : Q8XSrc{(const h16 *)a.x, nullptr, nullptr, nullptr, nullptr};
+        return gemv_q8_dispatch<kQ8Rows, 1, true>(s, a.w, a.w_scale, a.dim + 2 * a.kvd, a.dim, src, a.norm_w, a.eps, e,
+                                                  "gemv_q8_qkv_rope_kv");
+    }
     XSrc src = a.embd ? XSrc{(const h16 *)a.embd, a.dim, a.state, (h16 *)a.x} : XSrc{(const h16 *)a.x, 0, nullptr, nullptr};
     return gemv_dispatch<kRowsSmall, true>(s, a.w, a.dim + 2 * a.kvd, a.dim, src, 1, a.norm_w, a.eps, e, "gemv_qkv_rope_kv");
 }
 
-int32_t launch_gemv_residual(hipStream_t s, const void *w, int64_t N, int64_t K, const void *x_in, void *x) {
+int32_t launch_gemv_residual(hipStream_t s, const void *w, int64_t N, int64_t K, const void *x_in, void *x,
+                             const void *w_scale) {
     EpiResidual e{(h16 *)x};
+    if (w_scale)
+        return gemv_q8_dispatch<kQ8Rows, 1, false>(s, w, w_scale, N, K, Q8XSrc{(const h16 *)x_in, nullptr, nullptr, nullptr, nullptr},
+                                                   nullptr, 0.0f, e, "gemv_q8_residual");
     return gemv_dispatch<kRowsSmall, false>(s, w, N, K, XSrc{(const h16 *)x_in, 0, nullptr, nullptr}, 1, nullptr, 0.0f, e,
                                             "gemv_residual");
 }
 
 int32_t launch_gate_up_swiglu(hipStream_t s, const void *x, const void *norm_w, float eps, const void *w,
-                              int64_t ffn, int64_t dim, void *act) {
+                              int64_t ffn, int64_t dim, void *act, const void *w_scale) {
     EpiSwiglu e{(h16 *)act};
+    if (w_scale)
+        return gemv_q8_dispatch<kQ8Rows, 2, true>(s, w, w_scale, 2 * ffn, dim, Q8XSrc{(const h16 *)x, nullptr, nullptr, nullptr, nullptr},
+                                                  norm_w, eps, e, "gemv_q8_gate_up");
     return gemv_dispatch<kRowsSmall, true>(s, w, 2 * ffn, dim, XSrc{(const h16 *)x, 0, nullptr, nullptr}, 1, norm_w,
                                            eps, e, "gemv_gate_up_swiglu");
 }
@@ -551,6 +748,9 @@ int64_t lm_head_groups(int64_t vocab) { return (vocab + 7) / 8; }
 
 int32_t launch_lm_head(hipStream_t s, const LmHeadArgs &a) {
     EpiLmHead e{(h16 *)a.logits, (ArgPart *)a.partials};
+    if (a.w_scale)
+        return gemv_q8_dispatch<8, 1, true>(s, a.w, a.w_scale, a.vocab, a.dim, Q8XSrc{(const h16 *)a.x, nullptr, nullptr, nullptr, nullptr},
+                                         a.norm_w, a.eps, e, "gemv_q8_lm_head");
     return gemv_dispatch<8, true>(s, a.w, a.vocab, a.dim, XSrc{(const h16 *)a.x, 0, nullptr, nullptr}, 1, a.norm_w,
                                   a.eps, e, "gemv_lm_head");
 }

@@ -5,6 +5,8 @@
 // (message text included), then _validate_required_tensors. Where the reference aliases F16
 // tensors into the mmap, this loader uploads them once into the model's arena (Q/K/V
 // concatenated, gate/up interleaved); F32 norms are rounded to f16 as the reference does.
+// One extension: a file whose seven matrix kinds are all Q8_0 (GGML type 8) loads as a Q8_0 model
+// (the reference loader stops at "Real inference slice supports only F16 and F32 tensors").
 #include <fcntl.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
@@ -253,6 +255,11 @@ int32_t parse(Gguf &g, const char *path) {
         } else if (t.type == AESIR_GGML_F32) {
             if (n > g.size / 4) return fail(AESIR_ERR_FORMAT, "GGUF F32 tensor byte size overflows the file");
             bytes = n * 4;
+        } else if (t.type == AESIR_GGML_Q8_0) {  // beyond the reference loader: 34-byte blocks of 32
+            if (t.cols % 32 != 0)
+                return fail(AESIR_ERR_FORMAT, "GGUF Q8_0 tensor row length is not a multiple of 32: %s", t.name.c_str());
+            if (n / 32 > g.size / 34) return fail(AESIR_ERR_FORMAT, "GGUF Q8_0 tensor byte size overflows the file");
+            bytes = n / 32 * 34;
         } else {
             return fail(AESIR_ERR_FORMAT, "Real inference slice supports only F16 and F32 tensors");
         }
@@ -283,6 +290,13 @@ std::vector<std::string> required_tensors(const Gguf &g) {
     return required;
 }
 
+// Weight type of the matrices: Q8_0 when token_embd.weight is Q8_0 (then every matrix must be),
+// else F16 as the reference requires.
+uint32_t matrix_type(const Gguf &g) {
+    const GgufTensor &t = g.tensors[g.by_name.at("token_embd.weight")];
+    return t.type == AESIR_GGML_Q8_0 ? (uint32_t)AESIR_GGML_Q8_0 : (uint32_t)AESIR_GGML_F16;
+}
+
 // Expected (rows, cols, type) of a required tensor (loader/gguf.mojo:597-628).
 void expected_shape(const Gguf &g, const std::string &name, int64_t vocab, int64_t *rows, int64_t *cols, uint32_t *type) {
     const int64_t d = g.embedding_length, kvd = d / g.head_count * g.head_count_kv, f = g.feed_forward_length;
@@ -290,7 +304,7 @@ void expected_shape(const Gguf &g, const std::string &name, int64_t vocab, int64
         const size_t n = std::strlen(suf);
         return name.size() >= n && name.compare(name.size() - n, n, suf) == 0;
     };
-    *type = AESIR_GGML_F16;
+    *type = matrix_type(g);
     if (name == "token_embd.weight" || name == "output.weight") { *rows = vocab; *cols = d; }
     else if (ends("norm.weight")) { *rows = 1; *cols = d; *type = AESIR_GGML_F32; }
     else if (ends("attn_q.weight") || ends("attn_output.weight")) { *rows = d; *cols = d; }
@@ -356,7 +370,7 @@ extern "C" int32_t aesir_model_load_gguf(aesir_ctx *ctx, const char *path, int64
     aesir_model_config c{};
     fill_config(g, ctx_len_override, &c);
     aesir_model *m = nullptr;
-    AESIR_TRY(aesir_model_create(ctx, &c, &m));
+    AESIR_TRY(aesir_model_create_typed(ctx, &c, (int32_t)matrix_type(g), &m));
     for (auto &r : required) {
         const GgufTensor &t = g.tensors[g.by_name.at(r)];
         TensorRef ref;

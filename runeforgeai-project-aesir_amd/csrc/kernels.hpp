@@ -41,16 +41,21 @@ struct QkvArgs {
     int64_t max_seq;
     const void *rope;       // [n_pos][head_dim/2] (cos, sin) f16 pairs
     const DecodeState *state;
+    const void *w_scale;    // Q8_0 weights: f16 block scales [dim + 2*kvd][dim / 32] (w is then int8);
+                            // null for f16 weights
+    const void *embd_scale; // layer 0 of a Q8_0 model: token_embd block scales (embd is then int8)
 };
 int32_t launch_qkv_rope_kv(hipStream_t s, const QkvArgs &a);
 
 // x[n] = f16(f16(W x_in)[n] + x[n]) (O projection and down projection with the residual add).
-int32_t launch_gemv_residual(hipStream_t s, const void *w, int64_t N, int64_t K, const void *x_in, void *x);
+// w_scale non-null: W is Q8_0 (int8 quants [N][K] + f16 scales [N][K/32]).
+int32_t launch_gemv_residual(hipStream_t s, const void *w, int64_t N, int64_t K, const void *x_in, void *x,
+                             const void *w_scale = nullptr);
 
 // act[i] = f16(f16(up_i) * silu(f16(gate_i))) with W rows interleaved (2i gate, 2i+1 up),
 // after an RMSNorm prologue of x with norm_w.
 int32_t launch_gate_up_swiglu(hipStream_t s, const void *x, const void *norm_w, float eps, const void *w,
-                              int64_t ffn, int64_t dim, void *act);
+                              int64_t ffn, int64_t dim, void *act, const void *w_scale = nullptr);
 
 // lm_head with RMSNorm prologue and f16 logits, then the argmax of its per-workgroup partials
 // (second launch), which writes the decode state.
@@ -63,6 +68,7 @@ struct LmHeadArgs {
     void *partials; // [n_groups] (value, index)
     DecodeState *state;
     int64_t *ring;  // token ring (autoregressive loop), may be null
+    const void *w_scale;  // Q8_0 lm_head scales (w is then int8), or null
 };
 int32_t launch_lm_head_argmax(hipStream_t s, const LmHeadArgs &a);
 int32_t launch_lm_head(hipStream_t s, const LmHeadArgs &a);
@@ -105,6 +111,10 @@ int32_t launch_argmax(hipStream_t s, const void *logits, int64_t n, void *partia
                       int64_t *result);
 int32_t launch_fill_normal(hipStream_t s, void *dst, int64_t n, int64_t cols, int64_t dst_stride, uint64_t seed,
                            uint64_t stream, float mean, float std);
+// Q8_0 matrix init (quants [rows][cols] at q_stride bytes per row, f16 block scales at d_stride
+// elements per row): q uniform in [-127, 127], d uniform in [0.5, 1.5) * std / 64.
+int32_t launch_fill_q8_0(hipStream_t s, void *q, int64_t q_stride, void *d, int64_t d_stride, int64_t rows,
+                         int64_t cols, uint64_t seed, uint64_t stream, float std);
 int32_t launch_f32_to_f16(hipStream_t s, const float *src, void *dst, int64_t n);
 
 // ------------------------------------------------------------------ Q8_0 (q8_0.hip)

@@ -71,26 +71,38 @@ int32_t parse_tensor_name(const aesir_model *m, const char *name, TensorRef *ref
 }
 
 // Expected GGUF shape (rows, cols) and the device placement of a tensor: element (r, c) of the
-// GGUF tensor lives at base + r * row_stride + c.
+// GGUF tensor lives at base + r * row_stride + c (and its Q8_0 block scale at
+// scale + r * scale_stride + c / 32).
 TensorPlace place_tensor(const aesir_model *m, const TensorRef &ref) {
     const int64_t d = m->cfg.dim, kvd = m->kvd, f = m->cfg.ffn, V = m->cfg.vocab;
-    TensorPlace p{};
+    const bool q8 = m->wtype == AESIR_GGML_Q8_0;
+    const int es = q8 ? 1 : 2;
     const ModelLayer *L = ref.layer >= 0 ? &m->layers[ref.layer] : nullptr;
+    // matrix rows [r0, r0 + rows) of a fused tensor with `cols` columns, every `step`-th row
+    auto mat = [&](int64_t rows, int64_t cols, void *base, void *scale, int64_t r0, int64_t step) {
+        TensorPlace p{rows, cols, (char *)base + r0 * cols * es, step * cols, false, es, nullptr, 0};
+        if (q8) {
+            p.scale = (uint16_t *)scale + r0 * (cols / 32);
+            p.scale_stride = step * (cols / 32);
+        }
+        return p;
+    };
+    auto norm = [&](void *base) { return TensorPlace{1, d, base, d, true, 2, nullptr, 0}; };
     switch (ref.kind) {
-        case TensorKind::TokenEmbd: p = {V, d, m->tok_embd, d, false}; break;
-        case TensorKind::OutputNorm: p = {1, d, m->out_norm, d, true}; break;
-        case TensorKind::Output: p = {V, d, m->out_w, d, false}; break;
-        case TensorKind::AttnNorm: p = {1, d, L->attn_norm, d, true}; break;
-        case TensorKind::AttnQ: p = {d, d, L->wqkv, d, false}; break;
-        case TensorKind::AttnK: p = {kvd, d, (uint16_t *)L->wqkv + d * d, d, false}; break;
-        case TensorKind::AttnV: p = {kvd, d, (uint16_t *)L->wqkv + (d + kvd) * d, d, false}; break;
-        case TensorKind::AttnOut: p = {d, d, L->wo, d, false}; break;
-        case TensorKind::FfnNorm: p = {1, d, L->ffn_norm, d, true}; break;
-        case TensorKind::FfnGate: p = {f, d, L->wgu, 2 * d, false}; break;
-        case TensorKind::FfnUp: p = {f, d, (uint16_t *)L->wgu + d, 2 * d, false}; break;
-        case TensorKind::FfnDown: p = {d, f, L->wdown, f, false}; break;
+        case TensorKind::TokenEmbd: return mat(V, d, m->tok_embd, m->tok_embd_s, 0, 1);
+        case TensorKind::OutputNorm: return norm(m->out_norm);
+        case TensorKind::Output: return mat(V, d, m->out_w, m->out_w_s, 0, 1);
+        case TensorKind::AttnNorm: return norm(L->attn_norm);
+        case TensorKind::AttnQ: return mat(d, d, L->wqkv, L->sqkv, 0, 1);
+        case TensorKind::AttnK: return mat(kvd, d, L->wqkv, L->sqkv, d, 1);
+        case TensorKind::AttnV: return mat(kvd, d, L->wqkv, L->sqkv, d + kvd, 1);
+        case TensorKind::AttnOut: return mat(d, d, L->wo, L->so, 0, 1);
+        case TensorKind::FfnNorm: return norm(L->ffn_norm);
+        case TensorKind::FfnGate: return mat(f, d, L->wgu, L->sgu, 0, 2);  // gate i -> fused row 2i
+        case TensorKind::FfnUp: return mat(f, d, L->wgu, L->sgu, 1, 2);    // up i -> fused row 2i + 1
+        case TensorKind::FfnDown: return mat(d, f, L->wdown, L->sdown, 0, 1);
     }
-    return p;
+    return TensorPlace{};
 }
 
 static int64_t stream_id(const TensorRef &ref) {
@@ -143,9 +155,27 @@ int32_t model_upload(aesir_model *m, const TensorRef &ref, const void *host, int
     const std::string nm = tensor_name(ref);
     if (rows != p.rows || cols != p.cols)
         return fail(AESIR_ERR_FORMAT, "GGUF required tensor has an invalid shape: %s", nm.c_str());
+    hipStream_t s = m->ctx->stream;
+    if (p.esize == 1) {  // Q8_0 matrix: split the 34-byte blocks into quants and scales
+        if (type != AESIR_GGML_Q8_0)
+            return fail(AESIR_ERR_FORMAT, "GGUF required tensor has an invalid type: %s", nm.c_str());
+        const int64_t nb = cols / 32;
+        std::vector<int8_t> qs((size_t)(rows * cols));
+        std::vector<uint16_t> ds((size_t)(rows * nb));
+        const uint8_t *b = (const uint8_t *)host;
+        for (int64_t i = 0; i < rows * nb; i++, b += 34) {
+            std::memcpy(&ds[i], b, 2);
+            std::memcpy(&qs[i * 32], b + 2, 32);
+        }
+        AESIR_HIP_TRY(hipMemcpy2DAsync(p.base, (size_t)p.row_stride, qs.data(), (size_t)cols, (size_t)cols, (size_t)rows,
+                                       hipMemcpyHostToDevice, s));
+        AESIR_HIP_TRY(hipMemcpy2DAsync(p.scale, (size_t)p.scale_stride * 2, ds.data(), (size_t)nb * 2, (size_t)nb * 2,
+                                       (size_t)rows, hipMemcpyHostToDevice, s));
+        AESIR_HIP_TRY(hipStreamSynchronize(s));
+        return AESIR_OK;
+    }
     if (type != AESIR_GGML_F16 && !(p.is_norm && type == AESIR_GGML_F32))
         return fail(AESIR_ERR_FORMAT, "GGUF required tensor has an invalid type: %s", nm.c_str());
-    hipStream_t s = m->ctx->stream;
     std::vector<uint16_t> conv;
     const void *src = host;
     if (type == AESIR_GGML_F32) {  // loader/gguf.mojo:486-493: F32 -> f16 (round to nearest even)
@@ -167,7 +197,7 @@ static QkvArgs qkv_args(aesir_model *m, int64_t l) {
     const ModelLayer &L = m->layers[l];
     return QkvArgs{m->x, l == 0 ? m->tok_embd : nullptr, L.attn_norm, c.rms_eps, L.wqkv, c.dim, m->kvd, m->hd, m->q,
                    (uint16_t *)m->k_cache + l * c.ctx_len * m->kvd, (uint16_t *)m->v_cache + l * c.ctx_len * m->kvd,
-                   c.ctx_len, m->rope, m->state};
+                   c.ctx_len, m->rope, m->state, L.sqkv, l == 0 ? m->tok_embd_s : nullptr};
 }
 
 static AttnArgs attn_args(aesir_model *m, int64_t l) {
@@ -194,7 +224,7 @@ static AttnArgs attn_args(aesir_model *m, int64_t l) {
 LmHeadArgs lm_args(aesir_model *m, bool with_ring) {
     const aesir_model_config &c = m->cfg;
     return LmHeadArgs{m->x, m->out_norm, m->out_eps, m->out_w, c.vocab, c.dim, m->logits, m->lm_parts, m->state,
-                      with_ring ? m->ring : nullptr};
+                      with_ring ? m->ring : nullptr, m->out_w_s};
 }
 
 static int32_t enqueue_step(aesir_model *m, hipStream_t s) {
@@ -204,9 +234,9 @@ static int32_t enqueue_step(aesir_model *m, hipStream_t s) {
         const ModelLayer &L = m->layers[l];
         AESIR_TRY(launch_qkv_rope_kv(s, qkv_args(m, l)));  // layer 0 also performs the embedding lookup
         AESIR_TRY(launch_attention_decode(s, attn_args(m, l)));
-        AESIR_TRY(launch_gemv_residual(s, L.wo, d, d, m->attn, m->x));
-        AESIR_TRY(launch_gate_up_swiglu(s, m->x, L.ffn_norm, c.rms_eps, L.wgu, c.ffn, d, m->act));
-        AESIR_TRY(launch_gemv_residual(s, L.wdown, d, c.ffn, m->act, m->x));
+        AESIR_TRY(launch_gemv_residual(s, L.wo, d, d, m->attn, m->x, L.so));
+        AESIR_TRY(launch_gate_up_swiglu(s, m->x, L.ffn_norm, c.rms_eps, L.wgu, c.ffn, d, m->act, L.sgu));
+        AESIR_TRY(launch_gemv_residual(s, L.wdown, d, c.ffn, m->act, m->x, L.sdown));
     }
     return launch_lm_head_argmax(s, lm_args(m, true));
 }
@@ -257,6 +287,15 @@ static int32_t run_step(aesir_model *m, bool graph) {
     return enqueue_step(m, s);
 }
 
+int32_t model_step(aesir_model *m, int64_t token, int64_t pos, int64_t *next) {
+    AESIR_TRY(upload_state(m, token, pos, 0, m->ring_cap));
+    AESIR_TRY(run_step(m, true));
+    AESIR_HIP_TRY(hipMemcpyAsync(m->state_host, m->state, sizeof(DecodeState), hipMemcpyDeviceToHost, m->ctx->stream));
+    AESIR_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+    *next = m->state_host->next_token;
+    return AESIR_OK;
+}
+
 int32_t upload_state(aesir_model *m, int64_t token, int64_t pos, int64_t advance, int64_t ring_cap) {
     DecodeState *h = m->state_host;
     std::memset(h, 0, sizeof(DecodeState));
@@ -277,8 +316,17 @@ using namespace aesir;
 extern "C" {
 
 int32_t aesir_model_create(aesir_ctx *ctx, const aesir_model_config *cfg, aesir_model **out) {
+    return aesir_model_create_typed(ctx, cfg, AESIR_GGML_F16, out);
+}
+
+int32_t aesir_model_weight_type(const aesir_model *m) { return m ? m->wtype : -1; }
+
+int32_t aesir_model_create_typed(aesir_ctx *ctx, const aesir_model_config *cfg, int32_t weight_type,
+                                 aesir_model **out) {
     AESIR_TRY(bind(ctx));
     if (!cfg || !out) return fail(AESIR_ERR_INVALID, "aesir_model_create: null argument");
+    if (weight_type != AESIR_GGML_F16 && weight_type != AESIR_GGML_Q8_0)
+        return fail(AESIR_ERR_UNSUPPORTED, "model: weight type %d is not F16 or Q8_0", (int)weight_type);
     *out = nullptr;
     const aesir_model_config c = *cfg;
     // GGUFModelConfig.validate (loader/gguf.mojo:133-149)
@@ -293,10 +341,14 @@ int32_t aesir_model_create(aesir_ctx *ctx, const aesir_model_config *cfg, aesir_
     if (hd % 2 != 0) return fail(AESIR_ERR_INVALID, "apply_rope: head_dim must be positive and even");
     if (hd > 256 || c.n_heads / c.n_kv_heads > 16)
         return fail(AESIR_ERR_UNSUPPORTED, "model: head_dim <= 256 and <= 16 query heads per KV head are supported");
+    const bool q8 = weight_type == AESIR_GGML_Q8_0;
+    if (q8 && (c.dim % 32 != 0 || c.ffn % 32 != 0 || c.dim > 16384 || c.ffn > 16384))
+        return fail(AESIR_ERR_UNSUPPORTED, "model: Q8_0 weights need dim and ffn to be multiples of 32, at most 16384");
 
     auto *m = new aesir_model();
     m->ctx = ctx;
     m->cfg = c;
+    m->wtype = weight_type;
     m->hd = hd;
     m->kvd = hd * c.n_kv_heads;
     m->attn_scale = (float)(1.0 / std::pow((double)hd, 0.5));  // compute.mojo:1968
@@ -312,17 +364,22 @@ int32_t aesir_model_create(aesir_ctx *ctx, const aesir_model_config *cfg, aesir_
     auto take = [&](int64_t bytes, void **p) {
         if (rc == AESIR_OK) rc = carve(ctx, bytes, p);
     };
-    take(V * d * 2, &m->tok_embd);
+    // a matrix of rows x cols: f16, or int8 quants plus f16 block scales (Q8_0)
+    auto matrix = [&](int64_t rows, int64_t cols, void **w, void **scale) {
+        take(rows * cols * (q8 ? 1 : 2), w);
+        if (q8) take(rows * (cols / 32) * 2, scale);
+    };
+    matrix(V, d, &m->tok_embd, &m->tok_embd_s);
     take(d * 2, &m->out_norm);
-    take(V * d * 2, &m->out_w);
+    matrix(V, d, &m->out_w, &m->out_w_s);
     m->layers.resize((size_t)c.n_layers);
     for (auto &L : m->layers) {
         take(d * 2, &L.attn_norm);
-        take((d + 2 * kvd) * d * 2, &L.wqkv);
-        take(d * d * 2, &L.wo);
+        matrix(d + 2 * kvd, d, &L.wqkv, &L.sqkv);
+        matrix(d, d, &L.wo, &L.so);
         take(d * 2, &L.ffn_norm);
-        take(2 * f * d * 2, &L.wgu);
-        take(d * f * 2, &L.wdown);
+        matrix(2 * f, d, &L.wgu, &L.sgu);
+        matrix(d, f, &L.wdown, &L.sdown);
     }
     take(c.n_layers * c.ctx_len * kvd * 2, &m->k_cache);
     take(c.n_layers * c.ctx_len * kvd * 2, &m->v_cache);
@@ -407,9 +464,23 @@ int32_t aesir_model_get_tensor(aesir_model *m, const char *name, void *host_out,
     AESIR_TRY(parse_tensor_name(m, name, &ref));
     const TensorPlace p = place_tensor(m, ref);
     if (elements < p.rows * p.cols) return fail(AESIR_ERR_SHAPE, "aesir_model_get_tensor: output too small");
+    hipStream_t s = m->ctx->stream;
+    if (p.esize == 1) {  // Q8_0: dequantize f16(q * d); the product is exact in f32, so one rounding
+        const int64_t nb = p.cols / 32;
+        std::vector<int8_t> qs((size_t)(p.rows * p.cols));
+        std::vector<uint16_t> ds((size_t)(p.rows * nb));
+        AESIR_HIP_TRY(hipMemcpy2DAsync(qs.data(), (size_t)p.cols, p.base, (size_t)p.row_stride, (size_t)p.cols,
+                                       (size_t)p.rows, hipMemcpyDeviceToHost, s));
+        AESIR_HIP_TRY(hipMemcpy2DAsync(ds.data(), (size_t)nb * 2, p.scale, (size_t)p.scale_stride * 2, (size_t)nb * 2,
+                                       (size_t)p.rows, hipMemcpyDeviceToHost, s));
+        AESIR_HIP_TRY(hipStreamSynchronize(s));
+        uint16_t *o = (uint16_t *)host_out;
+        for (int64_t i = 0; i < p.rows * p.cols; i++) o[i] = f32_to_f16_bits((float)qs[i] * f16_bits_to_f32(ds[i / 32]));
+        return AESIR_OK;
+    }
     AESIR_HIP_TRY(hipMemcpy2DAsync(host_out, (size_t)p.cols * 2, p.base, (size_t)p.row_stride * 2, (size_t)p.cols * 2,
-                                   (size_t)p.rows, hipMemcpyDeviceToHost, m->ctx->stream));
-    AESIR_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+                                   (size_t)p.rows, hipMemcpyDeviceToHost, s));
+    AESIR_HIP_TRY(hipStreamSynchronize(s));
     return AESIR_OK;
 }
 
@@ -418,6 +489,11 @@ int32_t aesir_model_init_random(aesir_model *m, uint64_t seed, float std, float 
     AESIR_TRY(bind(m->ctx));
     for (const TensorRef &ref : all_tensors(m)) {
         const TensorPlace p = place_tensor(m, ref);
+        if (p.esize == 1) {
+            AESIR_TRY(launch_fill_q8_0(m->ctx->stream, p.base, p.row_stride, p.scale, p.scale_stride, p.rows, p.cols,
+                                       seed, (uint64_t)stream_id(ref), std));
+            continue;
+        }
         AESIR_TRY(launch_fill_normal(m->ctx->stream, p.base, p.rows * p.cols, p.cols, p.row_stride, seed,
                                      (uint64_t)stream_id(ref), p.is_norm ? norm_mean : 0.0f,
                                      p.is_norm ? norm_std : std));
@@ -440,12 +516,7 @@ int32_t aesir_forward_pass(aesir_model *m, const int64_t *tokens, int64_t n_toke
     const int64_t tok = tokens[idx];
     if (tok < 0 || tok >= m->cfg.vocab) return fail(AESIR_ERR_INVALID, "Prompt token ID is outside the embedding vocabulary");
     AESIR_TRY(ensure_rope(m, start_pos + 1));
-    AESIR_TRY(upload_state(m, tok, start_pos, 0, m->ring_cap));
-    AESIR_TRY(run_step(m, true));
-    AESIR_HIP_TRY(hipMemcpyAsync(m->state_host, m->state, sizeof(DecodeState), hipMemcpyDeviceToHost, m->ctx->stream));
-    AESIR_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
-    *next_token = m->state_host->next_token;
-    return AESIR_OK;
+    return model_step(m, tok, start_pos, next_token);
 }
 
 int32_t aesir_model_logits(aesir_model *m, void *host_out) {
@@ -511,9 +582,9 @@ int32_t aesir_model_kernel_times(aesir_model *m, int64_t pos, int32_t iters, flo
             switch (cls) {
                 case 0: return launch_qkv_rope_kv(s, qkv_args(m, l));
                 case 1: return launch_attention_decode(s, attn_args(m, l));
-                case 2: return launch_gemv_residual(s, L.wo, d, d, m->attn, m->x);
-                case 3: return launch_gate_up_swiglu(s, m->x, L.ffn_norm, c.rms_eps, L.wgu, c.ffn, d, m->act);
-                case 4: return launch_gemv_residual(s, L.wdown, d, c.ffn, m->act, m->x);
+                case 2: return launch_gemv_residual(s, L.wo, d, d, m->attn, m->x, L.so);
+                case 3: return launch_gate_up_swiglu(s, m->x, L.ffn_norm, c.rms_eps, L.wgu, c.ffn, d, m->act, L.sgu);
+                case 4: return launch_gemv_residual(s, L.wdown, d, c.ffn, m->act, m->x, L.sdown);
                 case 5: return launch_lm_head(s, lm_args(m, false));
                 default: return launch_argmax_finish(s, m->lm_parts, lm_head_groups(c.vocab), m->state, nullptr, nullptr);
             }

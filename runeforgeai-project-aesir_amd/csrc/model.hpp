@@ -12,6 +12,8 @@ namespace aesir {
 // Per-layer device tensors. Q, K and V rows are concatenated ([dim + 2 kvd][dim]) so one GEMV
 // produces q|k|v; gate and up rows are interleaved (row 2i = gate i, row 2i+1 = up i) so the
 // SwiGLU pair of an output lands in one workgroup.
+// Q8_0 models store every matrix as int8 quants in the same row order plus f16 block scales
+// [rows][cols / 32] (the s* pointers; null for F16 models).
 struct ModelLayer {
     void *attn_norm = nullptr;  // [dim]
     void *wqkv = nullptr;       // [dim + 2 kvd][dim]
@@ -19,6 +21,7 @@ struct ModelLayer {
     void *ffn_norm = nullptr;   // [dim]
     void *wgu = nullptr;        // [2 ffn][dim]
     void *wdown = nullptr;      // [dim][ffn]
+    void *sqkv = nullptr, *so = nullptr, *sgu = nullptr, *sdown = nullptr;
 };
 
 enum class TensorKind : int {
@@ -41,12 +44,17 @@ struct TensorRef {
     int layer;  // -1 for global tensors
 };
 
-// GGUF shape and device placement: element (r, c) at base + r * row_stride + c (f16 elements).
+// GGUF shape and device placement: element (r, c) at base + r * row_stride + c (elements of
+// esize bytes: 2 for f16, 1 for Q8_0 quants); a Q8_0 matrix's block scale (r, c / 32) at
+// scale + r * scale_stride + c / 32 (f16).
 struct TensorPlace {
     int64_t rows, cols;
     void *base;
     int64_t row_stride;
     bool is_norm;
+    int esize = 2;
+    void *scale = nullptr;
+    int64_t scale_stride = 0;
 };
 
 }  // namespace aesir
@@ -57,7 +65,9 @@ struct aesir_model {
     int64_t hd = 0, kvd = 0;
     float attn_scale = 0.0f, out_eps = 1e-5f;
     int64_t well_start = 0;
+    int32_t wtype = AESIR_GGML_F16;  // matrices: AESIR_GGML_F16 or AESIR_GGML_Q8_0
     void *tok_embd = nullptr, *out_norm = nullptr, *out_w = nullptr;
+    void *tok_embd_s = nullptr, *out_w_s = nullptr;  // Q8_0 block scales
     std::vector<aesir::ModelLayer> layers;
     void *k_cache = nullptr, *v_cache = nullptr;  // [n_layers][ctx_len][kvd]
     void *x = nullptr, *q = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr;
@@ -98,5 +108,7 @@ int64_t prefill_part_floats(int64_t rows, int64_t dim, int64_t qkv_n, int64_t ff
 int32_t ensure_rope(aesir_model *m, int64_t max_pos);
 int32_t upload_state(aesir_model *m, int64_t token, int64_t pos, int64_t advance, int64_t ring_cap);
 LmHeadArgs lm_args(aesir_model *m, bool with_ring);
+// One decode step of `token` at `pos` (graph replay when enabled); waits and returns the greedy token.
+int32_t model_step(aesir_model *m, int64_t token, int64_t pos, int64_t *next);
 
 }  // namespace aesir

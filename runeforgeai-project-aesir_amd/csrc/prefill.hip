@@ -443,6 +443,10 @@ int32_t model_prefill(aesir_model *m, const int64_t *tokens, int64_t n, int64_t 
         if (tokens[i] < 0 || tokens[i] >= c.vocab)
             return fail(AESIR_ERR_INVALID, "Prompt token ID is outside the embedding vocabulary");
     AESIR_TRY(ensure_rope(m, start_pos + n));
+    if (m->wtype != AESIR_GGML_F16) {  // Q8_0 weights: the reference's prefill, one decode step per position
+        for (int64_t i = 0; i < n; i++) AESIR_TRY(model_step(m, tokens[i], start_pos + i, next));
+        return AESIR_OK;
+    }
     for (int64_t r0 = 0; r0 < n; r0 += m->pf_rows) {
         const int64_t rows = n - r0 < m->pf_rows ? n - r0 : m->pf_rows;
         AESIR_TRY(prefill_chunk(m, tokens + r0, start_pos + r0, rows));

@@ -73,22 +73,27 @@ def llama_metadata(cfg, vocab: int, eos: int = 2, bos: int = 1, freq_base: float
 
 def write_gguf(path: str, metadata: list, tensors: dict, alignment: int = 32, version: int = 3,
                magic: int = 0x46554747):
-    """tensors: name -> numpy array (float16 -> GGML F16, float32 -> GGML F32), 1-D or 2-D."""
+    """tensors: name -> numpy array (float16 -> GGML F16, float32 -> GGML F32), 1-D or 2-D, or an
+    object with .blocks (uint8 [rows * cols / 32, 34]), .rows and .cols -> GGML Q8_0 (type 8)."""
     head = bytearray()
     head += struct.pack("<IIQQ", magic, version, len(tensors), len(metadata))
     for key, vtype, value in metadata:
         _kv(head, key, vtype, value)
     offs, blobs, cur = [], [], 0
     for name, arr in tensors.items():
-        arr = np.ascontiguousarray(arr)
-        ttype = 0 if arr.dtype == np.float32 else 1
         _s(head, name)
-        if arr.ndim == 1:
-            head += struct.pack("<I", 1) + struct.pack("<Q", arr.shape[0])
+        if hasattr(arr, "blocks"):
+            head += struct.pack("<I", 2) + struct.pack("<QQ", arr.cols, arr.rows)
+            ttype, raw = 8, np.ascontiguousarray(arr.blocks, np.uint8).tobytes()
         else:
-            head += struct.pack("<I", 2) + struct.pack("<QQ", arr.shape[1], arr.shape[0])
+            arr = np.ascontiguousarray(arr)
+            ttype = 0 if arr.dtype == np.float32 else 1
+            if arr.ndim == 1:
+                head += struct.pack("<I", 1) + struct.pack("<Q", arr.shape[0])
+            else:
+                head += struct.pack("<I", 2) + struct.pack("<QQ", arr.shape[1], arr.shape[0])
+            raw = arr.tobytes()
         head += struct.pack("<I", ttype) + struct.pack("<Q", cur)
-        raw = arr.tobytes()
         offs.append(cur)
         blobs.append(raw)
         cur += len(raw)

@@ -102,7 +102,8 @@ def test_gguf_freq_base_recorded_not_applied(A, oracle, tiny_gguf):
     ("rope_dim", "GGUF RoPE dimension does not match attention head size"),
     ("alignment", "GGUF alignment must be a power of two up to 4096"),
     ("eos", "Tokenizer eos_token_id is out of bounds"),
-    ("q8", "Real inference slice supports only F16 and F32 tensors"),
+    ("q4", "Real inference slice supports only F16 and F32 tensors"),
+    ("q8_mixed", "GGUF required tensor has an invalid type: output.weight"),
 ])
 def test_gguf_contract_errors(A, tiny_gguf, mutation, message):
     """loader/gguf.mojo:405-628 error paths, with the reference's message text."""
@@ -132,19 +133,27 @@ def test_gguf_contract_errors(A, tiny_gguf, mutation, message):
         md.append(("general.alignment", T_UINT32, 48))
     elif mutation == "eos":
         md[13] = ("tokenizer.ggml.eos_token_id", T_UINT32, 9999)
+    if mutation == "q8_mixed":
+        # Q8_0 token_embd with F16 layer matrices: the Q8_0 extension needs every matrix in Q8_0
+        from aesir_hip import Q8_0Tensor
+
+        e = tensors["token_embd.weight"]
+        d = np.full((e.shape[0], e.shape[1] // 32), 0.001, np.float16)
+        q = np.zeros(e.shape, np.int8)
+        tensors["token_embd.weight"] = Q8_0Tensor.from_parts(d, q)
     path = make(md=md, tensors=tensors, **kw)
     if mutation == "truncated":
         size = os.path.getsize(path)
         with open(path, "r+b") as f:
             f.truncate(size - 100)
-    if mutation == "q8":
-        # rewrite the type field of the first tensor to GGML Q8_0 (8)
+    if mutation == "q4":
+        # rewrite the type field of the first tensor to GGML Q4_0 (2), which neither loader takes
         raw = bytearray(open(path, "rb").read())
         name = b"token_embd.weight"
         i = raw.index(name) + len(name)
         ndim = int.from_bytes(raw[i:i + 4], "little")
         tpos = i + 4 + 8 * ndim
-        raw[tpos:tpos + 4] = (8).to_bytes(4, "little")
+        raw[tpos:tpos + 4] = (2).to_bytes(4, "little")
         open(path, "wb").write(bytes(raw))
     with pytest.raises(A.AesirError, match=re.escape(message)):
         A.gguf_inspect(path)
@@ -162,3 +171,41 @@ def test_gguf_duplicate_key(A, tiny_gguf):
 def test_gguf_missing_file(A, tmp_path):
     with pytest.raises(A.AesirError, match="Failed to open GGUF model"):
         A.gguf_inspect(str(tmp_path / "nope.gguf"))
+
+
+def test_q8_0_tensor_pack_matches_oracle_dequantize(A, oracle):
+    """Q8_0Tensor packs GGUF block_q8_0 bytes; its dequantize equals the oracle's
+    dequantize_q8_0 (compute.mojo:343-353) bit for bit."""
+    rng = np.random.default_rng(3)
+    q = rng.integers(-127, 128, size=(6, 96), dtype=np.int8)
+    d = rng.uniform(0.001, 0.02, (6, 3)).astype(np.float16)
+    t = A.Q8_0Tensor.from_parts(d, q)
+    assert t.blocks.shape == (18, 34)
+    assert np.array_equal(t.blocks[4, :2].view(np.float16), d.reshape(-1)[4:5])
+    assert np.array_equal(t.blocks[4, 2:].view(np.int8), q.reshape(-1, 32)[4])
+    ref = oracle.dequantize_q8_0(t.blocks, 18).reshape(6, 96)
+    assert np.array_equal(t.dequantize().view(np.uint16), ref.view(np.uint16))
+
+
+def test_gguf_inspect_q8_0_file(A, oracle, tmp_path):
+    """A file whose matrices are all Q8_0 (norms F32) passes the loader contract."""
+    from gguf_tools import llama_metadata, write_gguf
+
+    cfg = oracle.Config(dim=64, n_layers=2, n_heads=4, n_kv_heads=2, ffn=96, vocab=128, ctx_len=64)
+    tensors = {}
+    for name, (r, c) in oracle.tensor_shapes(cfg).items():
+        if name.endswith("norm.weight"):
+            tensors[name] = np.ones(c, np.float32)
+        else:
+            tensors[name] = A.Q8_0Tensor.from_parts(np.full((r, c // 32), 0.01, np.float16), np.ones((r, c), np.int8))
+    path = str(tmp_path / "q8.gguf")
+    write_gguf(path, llama_metadata(cfg, cfg.vocab), tensors)
+    c, _ = A.gguf_inspect(path)
+    assert (c.dim, c.n_layers, c.ffn, c.vocab) == (64, 2, 96, 128)
+    # a Q8_0 tensor whose rows are not whole blocks is rejected while mapping the tensor table
+    from types import SimpleNamespace
+
+    tensors["blk.0.ffn_down.weight"] = SimpleNamespace(blocks=np.zeros((160, 34), np.uint8), rows=64, cols=80)
+    write_gguf(path, llama_metadata(cfg, cfg.vocab), tensors)
+    with pytest.raises(A.AesirError, match="Q8_0 tensor row length is not a multiple of 32: blk.0.ffn_down.weight"):
+        A.gguf_inspect(path)

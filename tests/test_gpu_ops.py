@@ -238,6 +238,31 @@ def test_attention_repeated_calls_reuse_merge_counters(A, ctx):
         assert within_tol(out[0], f64_attention(q, K, V, S, hd, nq, nkv), atol=2e-3, rtol=2e-3), S
 
 
+@pytest.mark.parametrize("S,hd,nq,nkv", [(2048, 128, 32, 8), (3000, 64, 16, 4), (130, 128, 8, 8)])
+def test_attention_merge_sees_every_partial(A, ctx, S, hd, nq, nkv):
+    """The split merge reads partials that the split workgroups wrote into the context's shared
+    partial buffer. Two inputs alternate 60 times through the same buffers: every result must
+    equal that input's first result bit for bit (a partial left over from the other input would
+    change it), and the first results match f64."""
+    cases = []
+    for _ in range(2):
+        q = RNG.standard_normal((1, nq * hd)).astype(np.float16)
+        K = RNG.standard_normal((S, nkv * hd)).astype(np.float16)
+        V = RNG.standard_normal((S, nkv * hd)).astype(np.float16)
+        cases.append((q, K, V, ctx.from_numpy(q), ctx.from_numpy(K), ctx.from_numpy(V)))
+    out = ctx.tensor(1, nq * hd)
+    first = []
+    for i in range(120):
+        q, K, V, dq, dK, dV = cases[i % 2]
+        A.flash_attention_gqa(ctx, dq, dK, dV, out, S, hd, nq, nkv)
+        got = out.numpy()
+        if i < 2:
+            assert within_tol(got[0], f64_attention(q, K, V, S, hd, nq, nkv), atol=2e-3, rtol=2e-3)
+            first.append(got.copy())
+        else:
+            assert np.array_equal(got.view(np.uint16), first[i % 2].view(np.uint16)), i
+
+
 def test_attention_no_op_cases(A, ctx):
     """compute.mojo:1961-1966: output untouched."""
     q = ctx.from_numpy(np.full((1, 8), 0.5, np.float16))
@@ -392,7 +417,14 @@ def test_gemm_q8_0_vs_oracle(A, ctx, oracle, N, K):
     A.gemm_q8_0(ctx, ctx.from_numpy(a), upload_bytes(ctx, blocks), N, c)
     got = c.numpy()
     ref = oracle.gemm_q8_0(a, blocks, N)
-    assert np.max(ulp_diff(got, ref)) <= 1
+    # Beyond 1 ulp only where the result is small enough that f32 summation-order noise (bounded
+    # by 2^-17 of the sum of |products|) exceeds an f16 ulp.
+    W = oracle.dequantize_q8_0(blocks, N * K // 32).reshape(N, K).astype(np.float64)
+    noise = 2.0 ** -17 * (np.abs(a.astype(np.float64)) @ np.abs(W).T)
+    d = ulp_diff(got, ref)
+    bad = (d > 1) & (np.abs(got.astype(np.float64) - ref.astype(np.float64)) > noise)
+    assert not bad.any(), (d.max(), np.argwhere(bad)[:4])
+    assert (d > 0).mean() < 0.1
 
 
 @pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336)])

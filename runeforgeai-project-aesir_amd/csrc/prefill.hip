@@ -7,11 +7,11 @@
 //   A (activations) and B (weights) are both K-contiguous, so every MFMA operand fragment is one
 //   16-byte row load: lane l holds row (l % 16) and k = 8 (l / 16) .. +7 of its 16 x 32 slice, the
 //   same k order for A and B. A workgroup is 4 waves over 64 adjacent output columns (16 weight
-//   rows per wave) and a 128-row M tile. Each 64-wide K chunk of A is copied once per workgroup
-//   into a double-buffered LDS tile (rows padded to 144 bytes) and every wave reads its A
-//   fragments from there with ds_read_b128, while it streams its own weight rows from HBM
-//   exactly once, one chunk ahead of the MFMAs. Each wave keeps 8 accumulator tiles (rows
-//   16i + 4 (l / 16) + e, column l % 16 in lane l).
+//   rows per wave) and a 128-row M tile. Each 64-wide K chunk of A and of the workgroup's weight
+//   rows is copied straight from memory into an LDS stage (buffer loads with the LDS destination,
+//   no register staging, weight lines fetched whole), and every wave reads its fragments with
+//   ds_read_b128. Each wave keeps 8 accumulator tiles (rows 16i + 4 (l / 16) + e, column l % 16
+//   in lane l).
 //   Small-N GEMMs also split K over grid.z to put enough weight bytes in flight; their f32
 //   partials are summed in a fixed order by the epilogue kernel (deterministic, no atomics).
 //   At M = 128 the GEMM is HBM-bound (128 flop/byte against MI355X's 312 flop/byte ridge).
@@ -57,96 +57,114 @@ __device__ __forceinline__ void gemm_epilogue(h16 *C, int64_t ldc, int64_t M, in
     }
 }
 
-// grid (N / 64, ceil(M / 128), splits). With one split the epilogue is applied here; otherwise
-// split z writes its f32 partial to P[z][M][N] for gemm_reduce_kernel. Requires K % 64 == 0 and
-// 16-byte aligned rows (checked by the launcher).
-constexpr int kGemmKC = 64;           // k per LDS chunk (two MFMA k-steps)
-constexpr int kGemmLdsRow = kGemmKC + 8;  // padded LDS row (halves): 144 bytes, no bank conflicts
+constexpr int kGemmKC = 64;  // k per chunk (two MFMA k-steps)
+
+// grid (N / 64, ceil(M / 128), splits): a 4-wave workgroup owns 64 output columns (16 per wave)
+// and a 128-row M tile. With one split the epilogue is applied here; otherwise split z writes its
+// f32 partial to P[z][M][N] for gemm_reduce_kernel. Requires K % 64 == 0 and 16-byte aligned rows
+// (checked by the launcher). Each 64-wide K chunk
+// of A (128 rows x 128 B) and of the workgroup's 64 weight rows (64 x 128 B) is copied by
+// buffer_load_dwordx4 ... lds straight into one of S LDS stages: a wave instruction moves 8 whole
+// 128-byte row segments (lane l: row l / 8, 16-byte granule l % 8), so every weight line is
+// fetched whole by one instruction, and nothing passes through registers. Granule p of row r
+// holds k-granule p ^ ((r >> 1) & 7), which spreads the 16 rows of an MFMA fragment read over
+// all LDS banks. S - 1 chunks are in flight ahead of the MFMAs; the waits are explicit vmcnt
+// counts (each wave issues 6 copies per chunk) followed by a workgroup barrier.
+constexpr int kDmaRowBytes = 128;                      // one chunk of one row
+constexpr int kDmaStageA = kGemmMT * kDmaRowBytes;      // 16 KB
+constexpr int kDmaStage = kDmaStageA + kGemmNT * kDmaRowBytes;  // + 8 KB of weights
+constexpr int kDmaCopies = kGemmMT / 8 / kGemmWaves + kGemmNT / 8 / kGemmWaves;  // per wave per chunk (6)
+// LDS stages. Measured on MI355X (TinyLlama prefill GEMMs, us per GEMM + reduce): 2 stages
+// (48 KB, three workgroups per CU) and 3 (72 KB, two) are equal and beat 4 or 5 (one workgroup
+// per CU: gate/up 22.6 -> 31.4 and 32.4).
+constexpr int kDmaStages = 2;
+
+__device__ __forceinline__ int dma_swz(int row) { return (row >> 1) & 7; }
+
+// s_waitcnt immediate that waits until at most n vector-memory operations are outstanding
+// (gfx9 encoding: vmcnt bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima).
+constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
 template <int EPI>
 __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(const h16 *__restrict__ A, int64_t M, int64_t K,
-                                                                 const h16 *__restrict__ B, int64_t N,
-                                                                 h16 *__restrict__ C, int64_t ldc,
-                                                                 float *__restrict__ P) {
-    __shared__ __align__(16) h16 as[2][kGemmMT][kGemmLdsRow];
+                                                                const h16 *__restrict__ B, int64_t N,
+                                                                h16 *__restrict__ C, int64_t ldc,
+                                                                float *__restrict__ P) {
+    constexpr int S = kDmaStages;
+    extern __shared__ __align__(16) uint8_t lds[];  // S stages of kDmaStage bytes
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t m0 = (int64_t)blockIdx.y * kGemmMT;
-    const int64_t n0 = (int64_t)blockIdx.x * kGemmNT + wave * kGemmNW;
+    const int64_t nb = (int64_t)blockIdx.x * kGemmNT;
     const int r = lane & 15, g = lane >> 4;
     const int64_t nkc = K / kGemmKC, splits = gridDim.z, z = blockIdx.z;
     const int64_t c0 = nkc * z / splits, c1 = nkc * (z + 1) / splits;
-    // Buffer loads: one V# per operand (range = the whole matrix, so rows past M or N read 0),
-    // a 32-bit per-lane byte offset, the k offset as a uniform SGPR offset.
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void *)A, 0, (int)(M * K * 2), kBufferDword3);
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void *)B, 0, (int)(N * K * 2), kBufferDword3);
-    // A chunk staging: thread t copies row t / 2, k-halves 32 (t % 2) .. +31 (four 16-byte loads)
-    const int arow = tid >> 1, acol = (tid & 1) * 32;
-    const int aoff = (int)(((m0 + arow) * K + acol) * 2);
-    const int boff = (int)(((n0 + r) * K + 8 * g) * 2);
+    // copy instruction j of this wave: A rows 32 wave + 8 j + lane / 8 (j < 4), weight rows
+    // 16 wave + 8 j + lane / 8 (j < 2); the per-lane byte offset holds the row and granule, the
+    // chunk's k offset goes in the uniform soffset
+    const int drow = lane >> 3, dp = lane & 7;
+    int aoff[4], boff[2];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int row = 32 * wave + 8 * j + drow;
+        aoff[j] = (int)((m0 + row) * K * 2) + ((dp ^ dma_swz(row)) << 4);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int row = 16 * wave + 8 * j + drow;
+        boff[j] = (int)((nb + row) * K * 2) + ((dp ^ dma_swz(row)) << 4);
+    }
+    auto issue = [&](int64_t c, int stage) {
+        c = c < c1 ? c : c1 - 1;  // past the range: re-read the last chunk into a free stage
+        const int kb = (int)(c * kDmaRowBytes);
+        uint8_t *sa = lds + stage * kDmaStage;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                ra, (__attribute__((address_space(3))) void *)(sa + (32 * wave + 8 * j) * kDmaRowBytes), 16, aoff[j],
+                kb, 0, 0);
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rb, (__attribute__((address_space(3))) void *)(sa + kDmaStageA + (16 * wave + 8 * j) * kDmaRowBytes),
+                16, boff[j], kb, 0, 0);
+    };
 
     f32x4 acc[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     if (c0 < c1) {
-        // Pipeline: chunk c computes from LDS buffer (c - c0) % 2 and weight slot (c - c0) % 4
-        // while A(c + 2) (two register sets by chunk parity) and the weights of chunk c + 3 (a
-        // four-slot ring) are in flight; at its end A(c + 1), requested a chunk earlier, goes to
-        // the other LDS buffer. Requests are unconditional (past the range they re-read the last
-        // chunk) so the compiler's wait counts stay exact.
-        u32x4 ax[4], ay[4], b0[2], b1[2], b2[2], b3[2];
-        auto load_a = [&](u32x4 (&av)[4], int64_t c) {
-            c = c < c1 ? c : c1 - 1;
-            const int kb = (int)(c * kGemmKC * 2);
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-                av[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, aoff + 16 * j, kb, 0));
-        };
-        auto load_b = [&](u32x4 (&bv)[2], int64_t c) {
-            c = c < c1 ? c : c1 - 1;
-            const int kb = (int)(c * kGemmKC * 2);
+        for (int j = 0; j < S - 1; j++) issue(c0 + j, j);
+        const int brow = 16 * wave + r;
+        for (int64_t c = c0; c < c1; c++) {
+            const int t = (int)(c - c0);
+            __builtin_amdgcn_s_waitcnt(vm_wait(kDmaCopies * (S - 2)));  // this wave's copies of chunk c landed
+            __builtin_amdgcn_s_barrier();                                // ... and every wave's
+            issue(c + S - 1, (t + S - 1) % S);  // into the stage chunk c - 1 used
+            const uint8_t *sa = lds + (t % S) * kDmaStage, *sb = sa + kDmaStageA;
+            u32x4 bf[2], a[2][8];  // every fragment of the chunk is requested before the first MFMA
 #pragma unroll
-            for (int j = 0; j < 2; j++)
-                bv[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, boff, kb + 64 * j, 0));
-        };
-        auto store_a = [&](const u32x4 (&av)[4], int buf) {
+            for (int q = 0; q < 2; q++) {
+                bf[q] = ld16(sb + brow * kDmaRowBytes + (((4 * q + g) ^ dma_swz(brow)) << 4));
 #pragma unroll
-            for (int j = 0; j < 4; j++) st16(&as[buf][arow][acol + 8 * j], av[j]);
-        };
-        auto chunk = [&](int64_t c, int buf, const u32x4 (&bcur)[2], u32x4 (&bnext)[2], u32x4 (&afree)[4],
-                         const u32x4 (&anext)[4]) {
-            load_a(afree, c + 2);
-            load_b(bnext, c + 3);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                u32x4 a[8];
-#pragma unroll
-                for (int i = 0; i < 8; i++) a[i] = ld16(&as[buf][16 * i + r][32 * j + 8 * g]);
-#pragma unroll
-                for (int i = 0; i < 8; i++) acc[i] = mfma16x16x32(a[i], bcur[j], acc[i]);
+                for (int i = 0; i < 8; i++) {
+                    const int row = 16 * i + r;
+                    a[q][i] = ld16(sa + row * kDmaRowBytes + (((4 * q + g) ^ dma_swz(row)) << 4));
+                }
             }
             __builtin_amdgcn_sched_barrier(0);
-            store_a(anext, buf ^ 1);  // A(c + 1); past the range a copy nothing reads
-            __syncthreads();
-        };
-        load_a(ax, c0);
-        load_b(b0, c0);
-        load_a(ay, c0 + 1);
-        load_b(b1, c0 + 1);
-        load_b(b2, c0 + 2);
-        store_a(ax, 0);
-        __syncthreads();
-        for (int64_t c = c0; c < c1; c += 4) {
-            chunk(c, 0, b0, b3, ax, ay);
-            if (c + 1 >= c1) break;
-            chunk(c + 1, 1, b1, b0, ay, ax);
-            if (c + 2 >= c1) break;
-            chunk(c + 2, 0, b2, b1, ax, ay);
-            if (c + 3 >= c1) break;
-            chunk(c + 3, 1, b3, b2, ay, ax);
+#pragma unroll
+            for (int q = 0; q < 2; q++)
+#pragma unroll
+                for (int i = 0; i < 8; i++) acc[i] = mfma16x16x32(a[q][i], bf[q], acc[i]);
+            __builtin_amdgcn_sched_barrier(0);
         }
+        __builtin_amdgcn_s_waitcnt(vm_wait(0));  // no copy may land in LDS after the workgroup ends
     }
 
-    const int64_t n = n0 + r;
+    const int64_t n = nb + 16 * wave + r;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
 #pragma unroll
@@ -214,7 +232,7 @@ static int32_t launch_mfma(hipStream_t s, const void *A, int64_t M, int64_t K, c
     while (splits > 1 && splits * M * N > part_floats) splits--;
     if (EPI == kEpiSwiglu && (N & 1)) return fail(AESIR_ERR_INVALID, "%s: odd gate/up column count", name);
     hipLaunchKernelGGL(gemm_mfma_kernel<EPI>, dim3((unsigned)gx, (unsigned)gy, (unsigned)splits), dim3(kGemmThreads),
-                       0, s, (const h16 *)A, M, K, (const h16 *)B, N, (h16 *)C, ldc, part);
+                       kDmaStages * kDmaStage, s, (const h16 *)A, M, K, (const h16 *)B, N, (h16 *)C, ldc, part);
     AESIR_LAUNCH_CHECK(name);
     if (splits > 1) {
         const int64_t blocks = (M * N + 255) / 256;

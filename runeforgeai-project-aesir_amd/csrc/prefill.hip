@@ -223,9 +223,12 @@ int64_t prefill_part_floats(int64_t rows, int64_t dim, int64_t qkv_n, int64_t ff
     return most;
 }
 
+// With `defer` set, a split GEMM leaves its f32 partials in `part` for a fused row kernel of the
+// caller instead of launching gemm_reduce_kernel; *splits_out receives the split count.
 template <int EPI>
 static int32_t launch_mfma(hipStream_t s, const void *A, int64_t M, int64_t K, const void *B, int64_t N, void *C,
-                           int64_t ldc, float *part, int64_t part_floats, const char *name) {
+                           int64_t ldc, float *part, int64_t part_floats, const char *name, bool defer = false,
+                           int64_t *splits_out = nullptr) {
     const int64_t gx = (N + kGemmNT - 1) / kGemmNT, gy = (M + kGemmMT - 1) / kGemmMT;
     if (gx > 2147483647 || gy > 65535) return fail(AESIR_ERR_UNSUPPORTED, "%s: GEMM grid too large", name);
     int64_t splits = gemm_splits(M, K, N);
@@ -234,7 +237,8 @@ static int32_t launch_mfma(hipStream_t s, const void *A, int64_t M, int64_t K, c
     hipLaunchKernelGGL(gemm_mfma_kernel<EPI>, dim3((unsigned)gx, (unsigned)gy, (unsigned)splits), dim3(kGemmThreads),
                        kDmaStages * kDmaStage, s, (const h16 *)A, M, K, (const h16 *)B, N, (h16 *)C, ldc, part);
     AESIR_LAUNCH_CHECK(name);
-    if (splits > 1) {
+    if (splits_out) *splits_out = splits;
+    if (splits > 1 && !defer) {
         const int64_t blocks = (M * N + 255) / 256;
         hipLaunchKernelGGL(gemm_reduce_kernel<EPI>, dim3((unsigned)blocks), dim3(256), 0, s, (const float *)part, splits,
                            M, N, (h16 *)C, ldc);
@@ -289,6 +293,78 @@ __global__ __launch_bounds__(kPThreads) void qkv_post_rows_kernel(const h16 *__r
     for (int64_t j = threadIdx.x; j < pairs + kvd / 2; j += kPThreads) {
         const int64_t col = 2 * j;
         const h16 a = row[col], b = row[col + 1];
+        if (j < pairs) {
+            const int64_t c = col < dim ? col : col - dim;
+            const h16x2 cs = rope[pos * (hd / 2) + ((c % hd) >> 1)];
+            h16 *dst = col < dim ? Q + r * dim + c : kc + slot * kvd + c;
+            dst[0] = hsub(hmul(a, cs.x), hmul(b, cs.y));
+            dst[1] = hadd(hmul(a, cs.y), hmul(b, cs.x));
+        } else {
+            h16 *dst = vc + slot * kvd + (col - dim - kvd);
+            dst[0] = a;
+            dst[1] = b;
+        }
+    }
+}
+
+// Split-GEMM tails fused with the row kernel that follows them (one workgroup per row; the
+// partials are summed in split order exactly as gemm_reduce_kernel does).
+//   reduce_residual_norm_rows_kernel: X[m] = f16(f16(sum_z P[z][m]) + X[m]) (the residual
+//     epilogue), then Xn[m] = rmsnorm(X[m]) with weight w (compute.mojo:2178-2204).
+//   reduce_qkv_post_rows_kernel: QKV[m] = f16(sum_z P[z][m]) (the store epilogue) fed straight
+//     into qkv_post_rows_kernel's RoPE and KV append.
+constexpr int kRowVec = 8;  // columns per thread and pass (N % 8 == 0)
+__global__ __launch_bounds__(kPThreads) void reduce_residual_norm_rows_kernel(const float *__restrict__ P,
+                                                                              int64_t splits, int64_t M, int64_t N,
+                                                                              h16 *__restrict__ X, h16 *__restrict__ Xn,
+                                                                              const h16 *__restrict__ w, float eps) {
+    __shared__ float red[kPThreads / kWave];
+    const int64_t m = blockIdx.x;
+    h16 *x = X + m * N;
+    float ss = 0.0f;
+    for (int64_t c0 = (int64_t)threadIdx.x * kRowVec; c0 < N; c0 += (int64_t)kPThreads * kRowVec) {
+        float v[kRowVec];
+#pragma unroll
+        for (int e = 0; e < kRowVec; e++) v[e] = 0.0f;
+        for (int64_t z = 0; z < splits; z++) {
+            const float *p = P + (z * M + m) * N + c0;
+            const f32x4 a = *reinterpret_cast<const f32x4 *>(p), b = *reinterpret_cast<const f32x4 *>(p + 4);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                v[e] += a[e];
+                v[4 + e] += b[e];
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < kRowVec; e++) {
+            const h16 xv = hadd((h16)v[e], x[c0 + e]);
+            x[c0 + e] = xv;
+            const float f = (float)xv;
+            ss = fmaf(f, f, ss);
+        }
+    }
+    ss = block_sum<kPThreads / kWave>(ss, red);
+    const h16 inv = (h16)(1.0f / sqrtf(ss / (float)N + eps));
+    h16 *y = Xn + m * N;
+    for (int64_t c0 = (int64_t)threadIdx.x * kRowVec; c0 < N; c0 += (int64_t)kPThreads * kRowVec)
+#pragma unroll
+        for (int e = 0; e < kRowVec; e++) y[c0 + e] = hmul(hmul(x[c0 + e], inv), w[c0 + e]);
+}
+
+__global__ __launch_bounds__(kPThreads) void reduce_qkv_post_rows_kernel(
+    const float *__restrict__ P, int64_t splits, int64_t M, int64_t dim, int64_t kvd, int64_t hd, int64_t p0,
+    int64_t max_seq, const h16x2 *__restrict__ rope, h16 *__restrict__ Q, h16 *__restrict__ kc, h16 *__restrict__ vc) {
+    const int64_t r = blockIdx.x, pos = p0 + r, slot = pos % max_seq;
+    const int64_t N = dim + 2 * kvd, pairs = (dim + kvd) / 2;
+    for (int64_t j = threadIdx.x; j < N / 2; j += kPThreads) {
+        const int64_t col = 2 * j;
+        float2 v = {0.0f, 0.0f};
+        for (int64_t z = 0; z < splits; z++) {
+            const float2 t = *reinterpret_cast<const float2 *>(P + (z * M + r) * N + col);
+            v.x += t.x;
+            v.y += t.y;
+        }
+        const h16 a = (h16)v.x, b = (h16)v.y;
         if (j < pairs) {
             const int64_t c = col < dim ? col : col - dim;
             const h16x2 cs = rope[pos * (hd / 2) + ((c % hd) >> 1)];
@@ -405,18 +481,50 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
     const int64_t pr = m->pf_rows;
     const bool mfma = mfma_shape_ok(Xn, pr, d, L0(m), qkv_n) && mfma_shape_ok(Xn, pr, d, L0(m), d) &&
                       mfma_shape_ok(Xn, pr, d, L0(m), 2 * f) && mfma_shape_ok(Xn, pr, f, L0(m), d);
+    const bool rowvec = d % kRowVec == 0;  // fused residual + norm rows need whole 8-column groups
+    bool xn_ready = false;                 // Xn already holds this layer's attention-norm rows
+    auto norm_rows = [&](const void *w) -> int32_t {
+        hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3((unsigned)n), dim3(kPThreads), 0, s, X, Xn, d, (const h16 *)w,
+                           c.rms_eps);
+        AESIR_LAUNCH_CHECK("rmsnorm_rows_kernel");
+        return AESIR_OK;
+    };
+    // residual GEMM into X, then X -> Xn normalized with `next_norm` (if any), fused when split
+    auto residual_gemm = [&](const h16 *in, int64_t K, const void *w, const void *next_norm, const char *name) -> int32_t {
+        int64_t splits = 1;
+        AESIR_TRY(launch_mfma<kEpiResidual>(s, in, n, K, w, d, X, d, m->pf_part, m->pf_part_floats, name,
+                                            next_norm && rowvec, &splits));
+        if (!next_norm) return AESIR_OK;
+        if (splits > 1 && rowvec) {
+            hipLaunchKernelGGL(reduce_residual_norm_rows_kernel, dim3((unsigned)n), dim3(kPThreads), 0, s,
+                               (const float *)m->pf_part, splits, n, d, X, Xn, (const h16 *)next_norm, c.rms_eps);
+            AESIR_LAUNCH_CHECK("reduce_residual_norm_rows_kernel");
+            return AESIR_OK;
+        }
+        return norm_rows(next_norm);
+    };
     for (int64_t l = 0; l < c.n_layers; l++) {
         const ModelLayer &L = m->layers[l];
         h16 *kc = (h16 *)m->k_cache + l * c.ctx_len * kvd, *vc = (h16 *)m->v_cache + l * c.ctx_len * kvd;
         // attention block (inference.mojo:166-232)
-        hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3((unsigned)n), dim3(kPThreads), 0, s, X, Xn, d,
-                           (const h16 *)L.attn_norm, c.rms_eps);
-        AESIR_LAUNCH_CHECK("rmsnorm_rows_kernel");
-        if (mfma) AESIR_TRY(launch_mfma<kEpiStore>(s, Xn, n, d, L.wqkv, qkv_n, QKV, qkv_n, m->pf_part, m->pf_part_floats, "gemm_mfma_qkv"));
-        else AESIR_TRY(launch_gemm_f16(m->ctx, Xn, n, d, L.wqkv, qkv_n, QKV));
-        hipLaunchKernelGGL(qkv_post_rows_kernel, dim3((unsigned)n), dim3(kPThreads), 0, s, QKV, d, kvd, hd, p0,
-                           c.ctx_len, (const h16x2 *)m->rope, Q, kc, vc);
-        AESIR_LAUNCH_CHECK("qkv_post_rows_kernel");
+        if (!xn_ready) AESIR_TRY(norm_rows(L.attn_norm));
+        xn_ready = false;
+        int64_t qkv_splits = 1;
+        if (mfma)
+            AESIR_TRY(launch_mfma<kEpiStore>(s, Xn, n, d, L.wqkv, qkv_n, QKV, qkv_n, m->pf_part, m->pf_part_floats,
+                                             "gemm_mfma_qkv", true, &qkv_splits));
+        else
+            AESIR_TRY(launch_gemm_f16(m->ctx, Xn, n, d, L.wqkv, qkv_n, QKV));
+        if (qkv_splits > 1) {
+            hipLaunchKernelGGL(reduce_qkv_post_rows_kernel, dim3((unsigned)n), dim3(kPThreads), 0, s,
+                               (const float *)m->pf_part, qkv_splits, n, d, kvd, hd, p0, c.ctx_len,
+                               (const h16x2 *)m->rope, Q, kc, vc);
+            AESIR_LAUNCH_CHECK("reduce_qkv_post_rows_kernel");
+        } else {
+            hipLaunchKernelGGL(qkv_post_rows_kernel, dim3((unsigned)n), dim3(kPThreads), 0, s, QKV, d, kvd, hd, p0,
+                               c.ctx_len, (const h16x2 *)m->rope, Q, kc, vc);
+            AESIR_LAUNCH_CHECK("qkv_post_rows_kernel");
+        }
         if (hd % 8 == 0)  // rows of K are then 16-byte aligned (kvd and the cache base are)
             hipLaunchKernelGGL(prefill_attention_kernel<true>, dim3((unsigned)n, (unsigned)c.n_heads), dim3(kWave), 0,
                                s, Q, kc, vc, ATT, d, kvd, hd, c.n_heads / c.n_kv_heads, p0, c.ctx_len, m->attn_scale);
@@ -424,21 +532,22 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
             hipLaunchKernelGGL(prefill_attention_kernel<false>, dim3((unsigned)n, (unsigned)c.n_heads), dim3(kWave), 0,
                                s, Q, kc, vc, ATT, d, kvd, hd, c.n_heads / c.n_kv_heads, p0, c.ctx_len, m->attn_scale);
         AESIR_LAUNCH_CHECK("prefill_attention_kernel");
+        // O projection + residual, then the feed-forward norm (inference.mojo:227-241)
         if (mfma) {
-            AESIR_TRY(launch_mfma<kEpiResidual>(s, ATT, n, d, L.wo, d, X, d, m->pf_part, m->pf_part_floats, "gemm_mfma_o_residual"));
+            AESIR_TRY(residual_gemm(ATT, d, L.wo, L.ffn_norm, "gemm_mfma_o_residual"));
         } else {
             AESIR_TRY(launch_gemm_f16(m->ctx, ATT, n, d, L.wo, d, Xn));
             AESIR_TRY(launch_residual_add(s, X, Xn, n * d));
+            AESIR_TRY(norm_rows(L.ffn_norm));
         }
-        // feed-forward block (inference.mojo:235-273)
-        hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3((unsigned)n), dim3(kPThreads), 0, s, X, Xn, d,
-                           (const h16 *)L.ffn_norm, c.rms_eps);
-        AESIR_LAUNCH_CHECK("rmsnorm_rows_kernel");
+        // feed-forward block (inference.mojo:235-273); the down projection's tail also produces
+        // the next layer's attention-norm rows
         if (mfma) {
             AESIR_TRY(launch_mfma<kEpiSwiglu>(s, Xn, n, d, L.wgu, 2 * f, ACT, f, m->pf_part, m->pf_part_floats,
                                                 "gemm_mfma_gate_up_swiglu"));
-            AESIR_TRY(launch_mfma<kEpiResidual>(s, ACT, n, f, L.wdown, d, X, d, m->pf_part, m->pf_part_floats,
-                                                  "gemm_mfma_down_residual"));
+            const void *next_norm = l + 1 < c.n_layers ? m->layers[l + 1].attn_norm : nullptr;
+            AESIR_TRY(residual_gemm(ACT, f, L.wdown, next_norm, "gemm_mfma_down_residual"));
+            xn_ready = next_norm != nullptr;
         } else {
             // interleaved gate/up rows -> [n][2f] products, then the SwiGLU over the pairs
             AESIR_TRY(launch_gemm_f16(m->ctx, Xn, n, d, L.wgu, 2 * f, m->pf_gu));

@@ -108,15 +108,18 @@ TL = dict(dim=2048, layers=22, heads=32, kv_heads=4, ffn=5632, vocab=32000)
 TL_KVD = TL["dim"] // TL["heads"] * TL["kv_heads"]
 TL_GEMM_PARAMS = TL["layers"] * ((TL["dim"] + 2 * TL_KVD) * TL["dim"] + TL["dim"] ** 2 + 3 * TL["ffn"] * TL["dim"])
 TL_WEIGHT_BYTES = 2 * (TL_GEMM_PARAMS + TL["layers"] * 2 * TL["dim"] + TL["vocab"] * TL["dim"] + 2 * TL["dim"])
+# Q8_0: 34 bytes per 32 weights for every matrix a prefill streams, f16 norms
+TL_Q8_WEIGHT_BYTES = (TL_GEMM_PARAMS + TL["vocab"] * TL["dim"]) * 34 // 32 + 2 * (TL["layers"] * 2 * TL["dim"] + 2 * TL["dim"])
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense f16
 
 
-def prefill_bench(A, seed: int, n_prompt: int = 128, n_decode: int = 256, reps: int = 5) -> dict:
+def prefill_bench(A, seed: int, n_prompt: int = 128, n_decode: int = 256, reps: int = 5, q8: bool = False) -> dict:
     """Batched prefill of n_prompt positions on the TinyLlama shape (MFMA GEMMs; wall time of the
-    blocking aesir_prefill call, host launches included), then n_decode graph-replayed greedy steps."""
+    blocking aesir_prefill call, host launches included), then n_decode graph-replayed greedy steps.
+    q8: the same with Q8_0 matrices (weights for the GEMMs dequantized per fragment)."""
     ctx = A.Context(TL_WEIGHT_BYTES + (1 << 30))
     m = A.Model.create(ctx, A.ModelConfig(TL["dim"], TL["layers"], TL["heads"], TL["kv_heads"], TL["ffn"],
-                                          TL["vocab"], n_prompt + n_decode + 64))
+                                          TL["vocab"], n_prompt + n_decode + 64), A.GGML_Q8_0 if q8 else A.GGML_F16)
     m.init_random(seed, 0.02, 0.0, 0.02)
     rng = np.random.default_rng(seed)
     prompt = rng.integers(0, TL["vocab"], n_prompt).tolist()
@@ -136,11 +139,12 @@ def prefill_bench(A, seed: int, n_prompt: int = 128, n_decode: int = 256, reps: 
     flops = 2.0 * TL_GEMM_PARAMS * n_prompt
     m.close()
     ctx.close()
-    return {"workload": f"tinyllama-1.1b shape f16: {n_prompt}-token batched prefill, then {n_decode} greedy decode steps",
+    return {"workload": f"tinyllama-1.1b shape {'q8_0' if q8 else 'f16'}: {n_prompt}-token batched prefill, then "
+                        f"{n_decode} greedy decode steps",
             "prefill_ms": round(best * 1e3, 3), "prefill_tok_s": round(n_prompt / best, 1),
             "gemm_tflops": round(flops / best / 1e12, 2),
             "mfma_frac": round(flops / best / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
-            "weight_gbs": round(TL_WEIGHT_BYTES / best / 1e9, 1),
+            "weight_gbs": round((TL_Q8_WEIGHT_BYTES if q8 else TL_WEIGHT_BYTES) / best / 1e9, 1),
             "decode_tok_s": round(n_decode / dec, 1) if n_decode > 0 else None, "first_tokens": [nxt] + toks[:3]}
 
 
@@ -239,7 +243,9 @@ def main():
         print(json.dumps({"prefill": prefill_bench(A, args.seed, n_decode=args.prefill_decode_steps)}))
         return
     if args.q8_only:
-        print(json.dumps({"q8_0": q8_bench(A, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters)}))
+        q = q8_bench(A, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters)
+        q["prefill"] = prefill_bench(A, args.seed, n_decode=64, q8=True)
+        print(json.dumps({"q8_0": q}))
         return
 
     ctx_len = args.kv + max(args.steps, args.warmup) + 64
@@ -303,6 +309,7 @@ def main():
         out["prefill"] = prefill_bench(A, args.seed)
     if not args.no_q8:
         out["q8_0"] = q8_bench(A, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters)
+        out["q8_0"]["prefill"] = prefill_bench(A, args.seed, n_decode=64, q8=True)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.kv, args.cpu_reps)
         out["cpu_baseline"]["value"] = round(out["cpu_baseline"]["value"], 4)

@@ -61,6 +61,8 @@ int32_t aesir_abi_version(void);
  * Replaces MimirWell.__init__ (core/mimir_well.mojo:533-541), which allocates and zeroes a host
  * pool; here the pool is device memory, zeroed at creation. */
 int32_t aesir_ctx_create(int32_t device, int64_t well_bytes, aesir_ctx **out);
+/* Fails (AESIR_ERR_INVALID, context left intact) while a model created on it is alive: models hold
+ * pointers into the context, so destroy them first. */
 int32_t aesir_ctx_destroy(aesir_ctx *ctx);
 int32_t aesir_ctx_synchronize(aesir_ctx *ctx);
 /* The context's hipStream_t, for callers that interleave their own work. */

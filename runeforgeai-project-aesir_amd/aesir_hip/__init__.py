@@ -12,6 +12,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+import weakref
 from dataclasses import dataclass
 
 import numpy as np
@@ -184,10 +185,13 @@ class Context:
         h = P()
         _check(_L.aesir_ctx_create(device, int(well_bytes), C.byref(h)))
         self.h = h.value
+        self._models = weakref.WeakSet()  # models hold pointers into the context: closed first
 
     def close(self):
         if self.h:
-            _L.aesir_ctx_destroy(self.h)
+            for m in list(self._models):
+                m.close()
+            _check(_L.aesir_ctx_destroy(self.h))
             self.h = None
 
     def __enter__(self):
@@ -423,6 +427,7 @@ class Model:
 
     def __init__(self, ctx: Context, handle: int):
         self.ctx, self.h = ctx, handle
+        ctx._models.add(self)
         c = _ModelConfig()
         _check(_L.aesir_model_get_config(self.h, C.byref(c)))
         self.cfg = ModelConfig(c.dim, c.n_layers, c.n_heads, c.n_kv_heads, c.ffn, c.vocab, c.ctx_len, c.rms_eps,

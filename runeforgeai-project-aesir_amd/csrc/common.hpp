@@ -83,6 +83,7 @@ struct aesir_ctx {
     char arch[64] = {0};
     hipEvent_t ev_start = nullptr, ev_stop = nullptr;
     bool timer_running = false;
+    int64_t live_models = 0;  // models created on this context and not yet destroyed
     aesir::CtxScratch scratch;
     std::vector<aesir::RopeTable> rope_tables;
     int64_t *pinned_i64 = nullptr;  // small pinned staging area (64 entries)

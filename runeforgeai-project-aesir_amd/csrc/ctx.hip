@@ -160,6 +160,9 @@ int32_t aesir_ctx_create(int32_t device, int64_t well_bytes, aesir_ctx **out) {
 
 int32_t aesir_ctx_destroy(aesir_ctx *ctx) {
     if (!ctx) return AESIR_OK;
+    if (ctx->live_models > 0)  // a model keeps pointers into this context
+        return fail(AESIR_ERR_INVALID, "aesir_ctx_destroy: %lld model(s) still alive; destroy them first",
+                    (long long)ctx->live_models);
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     for (auto &t : ctx->rope_tables) (void)hipFree(t.dev);

@@ -49,6 +49,17 @@ __device__ __forceinline__ h16x2 as_h2(unsigned int u) { return __builtin_bit_ca
 __device__ __forceinline__ unsigned int h2_bits(h16x2 h) { return __builtin_bit_cast(unsigned int, h); }
 
 // acc + sum of the 8 f16 products of two 16-byte vectors (v_dot2_f32_f16, f32 accumulate).
+// f16(q_j * d) of the four int8 quants in w (byte j = quant j), as two f16 pairs (quants 0, 1 and
+// 2, 3). int8 -> f16 is exact through the exponent trick (byte ^ 0x80 placed under the f16
+// exponent of 1024 reads 1152 + q; subtracting 1152 is exact); the packed f16 multiply by d
+// rounds once, as the f16 product f16(q) * d does.
+__device__ __forceinline__ void dequant_q8x4(unsigned w, h16 d, unsigned &lo, unsigned &hi) {
+    const unsigned u = w ^ 0x80808080u;
+    const h16x2 bias = {(h16)1152.0f, (h16)1152.0f}, dd = {d, d};
+    lo = h2_bits((as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias) * dd);
+    hi = h2_bits((as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias) * dd);
+}
+
 __device__ __forceinline__ float dot8(u32x4 a, u32x4 b, float acc) {
     acc = __builtin_amdgcn_fdot2(as_h2(a.x), as_h2(b.x), acc, false);
     acc = __builtin_amdgcn_fdot2(as_h2(a.y), as_h2(b.y), acc, false);

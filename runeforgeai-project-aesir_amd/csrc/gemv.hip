@@ -473,10 +473,8 @@ __global__ __launch_bounds__(kFinishThreads) void argmax_finish_kernel(const Arg
 // Q8_0 matrices are repacked in HBM as int8 quants [N][K] (rows 32-byte aligned) plus f16 block
 // scales [N][K / 32]. Thread t multiplies k = 16t + 4096i: one 16-byte quant load (half a block)
 // and one 2-byte scale per row and slab, so a wave streams contiguous 1 KiB of quants per row.
-// Dequantization reproduces gemm_q8_0 (compute.mojo:1038-1065) exactly: w = f16(f16(q) * d).
-// The int8 -> f16 conversion is exact through the exponent trick (byte ^ 0x80 placed under the
-// f16 exponent 0x64 reads 1152 + q; subtracting 1152 is exact), the scale product is a packed f16
-// multiply (one round to nearest even, as hmul), the dot product v_dot2_f32_f16.
+// Dequantization (dequant_q8x4) reproduces gemm_q8_0 (compute.mojo:1038-1065) exactly:
+// w = f16(f16(q) * d); the dot product is v_dot2_f32_f16.
 constexpr int kQSlab = kThreads * 16;  // k elements covered by one pass of the workgroup
 // Rows per group of the Q8_0 decode GEMVs, and row groups per workgroup. Measured on MI355X
 // (Llama-3-8B shapes, us per launch): 4 rows beat 8 and 16 on every GEMV; 2 groups per workgroup
@@ -486,17 +484,11 @@ constexpr int kQ8Rows = 4;
 
 // f16 values f16(q_j * d) of 16 quants, as two 8-element chunks.
 __device__ __forceinline__ void deq16(u32x4 q, h16 d, u32x4 &o0, u32x4 &o1) {
-    const unsigned qw[4] = {q.x, q.y, q.z, q.w};
     unsigned o[8];
-    const h16x2 bias = {(h16)1152.0f, (h16)1152.0f}, dd = {d, d};
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const unsigned w = qw[j] ^ 0x80808080u;
-        const h16x2 lo = as_h2(__builtin_amdgcn_perm(0x64646464u, w, 0x04010400u)) - bias;  // q0, q1
-        const h16x2 hi = as_h2(__builtin_amdgcn_perm(0x64646464u, w, 0x04030402u)) - bias;  // q2, q3
-        o[2 * j] = h2_bits(lo * dd);
-        o[2 * j + 1] = h2_bits(hi * dd);
-    }
+    dequant_q8x4(q.x, d, o[0], o[1]);
+    dequant_q8x4(q.y, d, o[2], o[3]);
+    dequant_q8x4(q.z, d, o[4], o[5]);
+    dequant_q8x4(q.w, d, o[6], o[7]);
     o0 = u32x4{o[0], o[1], o[2], o[3]};
     o1 = u32x4{o[4], o[5], o[6], o[7]};
 }

@@ -425,6 +425,7 @@ int32_t aesir_model_create_typed(aesir_ctx *ctx, const aesir_model_config *cfg, 
     if (const char *e = std::getenv("AESIR_NO_GRAPH")) m->use_graph = e[0] == '0';
     if ((rc = ensure_rope(m, c.ctx_len)) != AESIR_OK) return fail_cleanup(rc);
     if (hipStreamSynchronize(ctx->stream) != hipSuccess) return fail_cleanup(fail(AESIR_ERR_HIP, "sync failed"));
+    ctx->live_models++;
     *out = m;
     return AESIR_OK;
 }
@@ -438,6 +439,7 @@ int32_t aesir_model_destroy(aesir_model *m) {
         (void)hipGraphDestroy(m->graph);
     }
     if (m->state_host) (void)hipHostFree(m->state_host);
+    m->ctx->live_models--;
     delete m;
     return AESIR_OK;
 }

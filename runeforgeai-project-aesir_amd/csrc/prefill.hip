@@ -74,24 +74,36 @@ constexpr int kDmaRowBytes = 128;                      // one chunk of one row
 constexpr int kDmaStageA = kGemmMT * kDmaRowBytes;      // 16 KB
 constexpr int kDmaStage = kDmaStageA + kGemmNT * kDmaRowBytes;  // + 8 KB of weights
 constexpr int kDmaCopies = kGemmMT / 8 / kGemmWaves + kGemmNT / 8 / kGemmWaves;  // per wave per chunk (6)
+// Q8_0 weights: a chunk of a weight row is 64 int8 quants (64 B) plus its two f16 block scales.
+constexpr int kDmaQRowBytes = 64;
+constexpr int kDmaStageQ = kDmaStageA + kGemmNT * kDmaQRowBytes + kGemmNT * 4;  // A + quants + scales
 // LDS stages. Measured on MI355X (TinyLlama prefill GEMMs, us per GEMM + reduce): 2 stages
 // (48 KB, three workgroups per CU) and 3 (72 KB, two) are equal and beat 4 or 5 (one workgroup
 // per CU: gate/up 22.6 -> 31.4 and 32.4).
 constexpr int kDmaStages = 2;
 
 __device__ __forceinline__ int dma_swz(int row) { return (row >> 1) & 7; }
+__device__ __forceinline__ int dma_swz_q(int row) { return (row >> 2) & 3; }  // 4 granules per quant row
 
 // s_waitcnt immediate that waits until at most n vector-memory operations are outstanding
 // (gfx9 encoding: vmcnt bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima).
 constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
-template <int EPI>
+// Q8: B is Q8_0 (int8 quants [N][K] + f16 block scales Bs [N][K / 32]). A chunk's 64 weight rows
+// are 64-byte quant segments (one copy per wave: 16 rows x 4 granules, granule p of row r holding
+// k-granule p ^ ((r >> 2) & 3)) plus the rows' two scales (one dword copy, wave 0). Each B
+// fragment is dequantized from LDS as f16(q * d) (dequant_q8x4, gemm_q8_0's rounding), so the
+// product equals the f16 GEMM with the dequantized weights. With 2 stages every wait is a full
+// drain, so the waves' different copy counts need no bookkeeping.
+template <int EPI, bool Q8>
 __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(const h16 *__restrict__ A, int64_t M, int64_t K,
-                                                                const h16 *__restrict__ B, int64_t N,
+                                                                const void *__restrict__ B, int64_t N,
                                                                 h16 *__restrict__ C, int64_t ldc,
-                                                                float *__restrict__ P) {
+                                                                float *__restrict__ P, const h16 *__restrict__ Bs) {
     constexpr int S = kDmaStages;
-    extern __shared__ __align__(16) uint8_t lds[];  // S stages of kDmaStage bytes
+    constexpr int kStage = Q8 ? kDmaStageQ : kDmaStage;
+    static_assert(!Q8 || S == 2, "the Q8_0 copies rely on full-drain waits");
+    extern __shared__ __align__(16) uint8_t lds[];  // S stages of kStage bytes
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t m0 = (int64_t)blockIdx.y * kGemmMT;
     const int64_t nb = (int64_t)blockIdx.x * kGemmNT;
@@ -99,7 +111,11 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(const h16 *__re
     const int64_t nkc = K / kGemmKC, splits = gridDim.z, z = blockIdx.z;
     const int64_t c0 = nkc * z / splits, c1 = nkc * (z + 1) / splits;
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void *)A, 0, (int)(M * K * 2), kBufferDword3);
-    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void *)B, 0, (int)(N * K * 2), kBufferDword3);
+    const __amdgpu_buffer_rsrc_t rb =
+        __builtin_amdgcn_make_buffer_rsrc((void *)B, 0, (int)(N * K * (Q8 ? 1 : 2)), kBufferDword3);
+    const int64_t KB = K / 32;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)Bs, 0, Q8 ? (int)(N * KB * 2) : 0, kBufferDword3);
     // copy instruction j of this wave: A rows 32 wave + 8 j + lane / 8 (j < 4), weight rows
     // 16 wave + 8 j + lane / 8 (j < 2); the per-lane byte offset holds the row and granule, the
     // chunk's k offset goes in the uniform soffset
@@ -115,20 +131,33 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(const h16 *__re
         const int row = 16 * wave + 8 * j + drow;
         boff[j] = (int)((nb + row) * K * 2) + ((dp ^ dma_swz(row)) << 4);
     }
+    const int qrow = 16 * wave + (lane >> 2), qp = lane & 3;  // Q8: quant copy lane -> (row, granule)
+    const int qoff = (int)((nb + qrow) * K) + ((qp ^ dma_swz_q(qrow)) << 4);
+    const int soff = (int)((nb + lane) * KB * 2);              // Q8: scale copy lane -> row
     auto issue = [&](int64_t c, int stage) {
         c = c < c1 ? c : c1 - 1;  // past the range: re-read the last chunk into a free stage
         const int kb = (int)(c * kDmaRowBytes);
-        uint8_t *sa = lds + stage * kDmaStage;
+        uint8_t *sa = lds + stage * kStage;
 #pragma unroll
         for (int j = 0; j < 4; j++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 ra, (__attribute__((address_space(3))) void *)(sa + (32 * wave + 8 * j) * kDmaRowBytes), 16, aoff[j],
                 kb, 0, 0);
-#pragma unroll
-        for (int j = 0; j < 2; j++)
+        if (Q8) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rb, (__attribute__((address_space(3))) void *)(sa + kDmaStageA + (16 * wave + 8 * j) * kDmaRowBytes),
-                16, boff[j], kb, 0, 0);
+                rb, (__attribute__((address_space(3))) void *)(sa + kDmaStageA + 16 * wave * kDmaQRowBytes), 16, qoff,
+                (int)(c * kDmaQRowBytes), 0, 0);
+            if (wave == 0)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rs, (__attribute__((address_space(3))) void *)(sa + kDmaStageA + kGemmNT * kDmaQRowBytes), 4, soff,
+                    (int)(c * 4), 0, 0);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rb, (__attribute__((address_space(3))) void *)(sa + kDmaStageA + (16 * wave + 8 * j) * kDmaRowBytes),
+                    16, boff[j], kb, 0, 0);
+        }
     };
 
     f32x4 acc[8];
@@ -143,11 +172,19 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(const h16 *__re
             __builtin_amdgcn_s_waitcnt(vm_wait(kDmaCopies * (S - 2)));  // this wave's copies of chunk c landed
             __builtin_amdgcn_s_barrier();                                // ... and every wave's
             issue(c + S - 1, (t + S - 1) % S);  // into the stage chunk c - 1 used
-            const uint8_t *sa = lds + (t % S) * kDmaStage, *sb = sa + kDmaStageA;
+            const uint8_t *sa = lds + (t % S) * kStage, *sb = sa + kDmaStageA;
             u32x4 bf[2], a[2][8];  // every fragment of the chunk is requested before the first MFMA
+            uint2 bq[2];
+            h16 bd[2];
 #pragma unroll
             for (int q = 0; q < 2; q++) {
-                bf[q] = ld16(sb + brow * kDmaRowBytes + (((4 * q + g) ^ dma_swz(brow)) << 4));
+                if (Q8) {  // k 32q + 8g .. +7: half g & 1 of granule 2q + g / 2
+                    bq[q] = *reinterpret_cast<const uint2 *>(
+                        sb + brow * kDmaQRowBytes + (((2 * q + (g >> 1)) ^ dma_swz_q(brow)) << 4) + 8 * (g & 1));
+                    bd[q] = reinterpret_cast<const h16 *>(sb + kGemmNT * kDmaQRowBytes)[2 * brow + q];
+                } else {
+                    bf[q] = ld16(sb + brow * kDmaRowBytes + (((4 * q + g) ^ dma_swz(brow)) << 4));
+                }
 #pragma unroll
                 for (int i = 0; i < 8; i++) {
                     const int row = 16 * i + r;
@@ -155,6 +192,15 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(const h16 *__re
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
+            if (Q8) {
+#pragma unroll
+                for (int q = 0; q < 2; q++) {
+                    unsigned w[4];
+                    dequant_q8x4(bq[q].x, bd[q], w[0], w[1]);
+                    dequant_q8x4(bq[q].y, bd[q], w[2], w[3]);
+                    bf[q] = u32x4{w[0], w[1], w[2], w[3]};
+                }
+            }
 #pragma unroll
             for (int q = 0; q < 2; q++)
 #pragma unroll
@@ -197,7 +243,7 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const float *__restric
 
 // The kernel addresses each operand through a buffer resource with a 32-bit byte range.
 static bool mfma_shape_ok(const void *A, int64_t M, int64_t K, const void *B, int64_t N) {
-    const int64_t lim = (int64_t)1 << 31;
+    const int64_t lim = (int64_t)1 << 31;  // (Q8_0 quant rows are half as long: the f16 bound covers them)
     return K % 64 == 0 && ((uintptr_t)A & 15) == 0 && ((uintptr_t)B & 15) == 0 && (M + kGemmMT) * K * 2 < lim &&
            (N + kGemmNT) * K * 2 < lim;
 }
@@ -225,17 +271,23 @@ int64_t prefill_part_floats(int64_t rows, int64_t dim, int64_t qkv_n, int64_t ff
 
 // With `defer` set, a split GEMM leaves its f32 partials in `part` for a fused row kernel of the
 // caller instead of launching gemm_reduce_kernel; *splits_out receives the split count.
+// Bs non-null: B is Q8_0 quants with these f16 block scales.
 template <int EPI>
 static int32_t launch_mfma(hipStream_t s, const void *A, int64_t M, int64_t K, const void *B, int64_t N, void *C,
                            int64_t ldc, float *part, int64_t part_floats, const char *name, bool defer = false,
-                           int64_t *splits_out = nullptr) {
+                           int64_t *splits_out = nullptr, const void *Bs = nullptr) {
     const int64_t gx = (N + kGemmNT - 1) / kGemmNT, gy = (M + kGemmMT - 1) / kGemmMT;
     if (gx > 2147483647 || gy > 65535) return fail(AESIR_ERR_UNSUPPORTED, "%s: GEMM grid too large", name);
     int64_t splits = gemm_splits(M, K, N);
     while (splits > 1 && splits * M * N > part_floats) splits--;
     if (EPI == kEpiSwiglu && (N & 1)) return fail(AESIR_ERR_INVALID, "%s: odd gate/up column count", name);
-    hipLaunchKernelGGL(gemm_mfma_kernel<EPI>, dim3((unsigned)gx, (unsigned)gy, (unsigned)splits), dim3(kGemmThreads),
-                       kDmaStages * kDmaStage, s, (const h16 *)A, M, K, (const h16 *)B, N, (h16 *)C, ldc, part);
+    const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)splits);
+    if (Bs)
+        hipLaunchKernelGGL((gemm_mfma_kernel<EPI, true>), grid, dim3(kGemmThreads), kDmaStages * kDmaStageQ, s,
+                           (const h16 *)A, M, K, B, N, (h16 *)C, ldc, part, (const h16 *)Bs);
+    else
+        hipLaunchKernelGGL((gemm_mfma_kernel<EPI, false>), grid, dim3(kGemmThreads), kDmaStages * kDmaStage, s,
+                           (const h16 *)A, M, K, B, N, (h16 *)C, ldc, part, (const h16 *)nullptr);
     AESIR_LAUNCH_CHECK(name);
     if (splits_out) *splits_out = splits;
     if (splits > 1 && !defer) {
@@ -270,6 +322,19 @@ __global__ __launch_bounds__(kPThreads) void rmsnorm_rows_kernel(const h16 *__re
     ss = block_sum<kPThreads / kWave>(ss, red);
     const h16 inv = (h16)(1.0f / sqrtf(ss / (float)cols + eps));
     for (int64_t c = threadIdx.x; c < cols; c += kPThreads) y[c] = hmul(hmul(x[c], inv), w[c]);
+}
+
+// X[r] = token_embd[tokens[r]] (inference.mojo:452-467), one workgroup per row; the Q8_0 table
+// variant writes f16(q * d) (the product is exact in f32, so one rounding, as f16(q) * d).
+__global__ __launch_bounds__(kPThreads) void embed_rows_q8_kernel(const int8_t *__restrict__ q,
+                                                                  const h16 *__restrict__ dsc, int64_t dim,
+                                                                  const int64_t *__restrict__ tokens,
+                                                                  h16 *__restrict__ X) {
+    const int64_t t = tokens[blockIdx.x];
+    const int8_t *src = q + t * dim;
+    const h16 *ds = dsc + t * (dim / 32);
+    h16 *dst = X + (int64_t)blockIdx.x * dim;
+    for (int64_t c = threadIdx.x; c < dim; c += kPThreads) dst[c] = (h16)((float)src[c] * (float)ds[c / 32]);
 }
 
 // X[r] = token_embd[tokens[r]] (inference.mojo:452-467), one workgroup per row.
@@ -464,6 +529,15 @@ static int32_t launch_swiglu_pairs(hipStream_t s, const void *gu, void *act, int
 
 static const void *L0(const aesir_model *m) { return m->layers[0].wqkv; }
 
+// Every GEMM of a layer runs on the matrix cores when all four shapes qualify (arena buffers and
+// weights are 256-byte aligned).
+static bool prefill_mfma_ok(const aesir_model *m) {
+    const int64_t d = m->cfg.dim, f = m->cfg.ffn, pr = m->pf_rows, qkv_n = d + 2 * m->kvd;
+    const void *X = m->pf_xn;
+    return mfma_shape_ok(X, pr, d, L0(m), qkv_n) && mfma_shape_ok(X, pr, d, L0(m), d) &&
+           mfma_shape_ok(X, pr, d, L0(m), 2 * f) && mfma_shape_ok(X, pr, f, L0(m), d);
+}
+
 // Runs positions [p0, p0 + n) of tokens through every layer (n <= the model's prefill rows).
 static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t p0, int64_t n) {
     const aesir_model_config &c = m->cfg;
@@ -473,14 +547,16 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
     h16 *X = (h16 *)m->pf_x, *Xn = (h16 *)m->pf_xn, *QKV = (h16 *)m->pf_qkv, *Q = (h16 *)m->pf_q;
     h16 *ATT = (h16 *)m->pf_att, *ACT = (h16 *)m->pf_act;
     AESIR_HIP_TRY(hipMemcpyAsync(m->pf_tokens, tokens_host, (size_t)n * sizeof(int64_t), hipMemcpyHostToDevice, s));
-    hipLaunchKernelGGL(embed_rows_kernel, dim3((unsigned)n), dim3(kPThreads), 0, s, (const h16 *)m->tok_embd, d,
-                       (const int64_t *)m->pf_tokens, X);
+    if (m->tok_embd_s)
+        hipLaunchKernelGGL(embed_rows_q8_kernel, dim3((unsigned)n), dim3(kPThreads), 0, s, (const int8_t *)m->tok_embd,
+                           (const h16 *)m->tok_embd_s, d, (const int64_t *)m->pf_tokens, X);
+    else
+        hipLaunchKernelGGL(embed_rows_kernel, dim3((unsigned)n), dim3(kPThreads), 0, s, (const h16 *)m->tok_embd, d,
+                           (const int64_t *)m->pf_tokens, X);
     AESIR_LAUNCH_CHECK("embed_rows_kernel");
-    // every GEMM of the layer on the matrix cores when all four shapes qualify (arena buffers
-    // and weights are 256-byte aligned)
-    const int64_t pr = m->pf_rows;
-    const bool mfma = mfma_shape_ok(Xn, pr, d, L0(m), qkv_n) && mfma_shape_ok(Xn, pr, d, L0(m), d) &&
-                      mfma_shape_ok(Xn, pr, d, L0(m), 2 * f) && mfma_shape_ok(Xn, pr, f, L0(m), d);
+    const bool mfma = prefill_mfma_ok(m);
+    if (!mfma && m->wtype != AESIR_GGML_F16)
+        return fail(AESIR_ERR_UNSUPPORTED, "prefill: Q8_0 weights need the MFMA GEMM shapes (K %% 64 == 0)");
     const bool rowvec = d % kRowVec == 0;  // fused residual + norm rows need whole 8-column groups
     bool xn_ready = false;                 // Xn already holds this layer's attention-norm rows
     auto norm_rows = [&](const void *w) -> int32_t {
@@ -490,10 +566,11 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
         return AESIR_OK;
     };
     // residual GEMM into X, then X -> Xn normalized with `next_norm` (if any), fused when split
-    auto residual_gemm = [&](const h16 *in, int64_t K, const void *w, const void *next_norm, const char *name) -> int32_t {
+    auto residual_gemm = [&](const h16 *in, int64_t K, const void *w, const void *ws, const void *next_norm,
+                             const char *name) -> int32_t {
         int64_t splits = 1;
         AESIR_TRY(launch_mfma<kEpiResidual>(s, in, n, K, w, d, X, d, m->pf_part, m->pf_part_floats, name,
-                                            next_norm && rowvec, &splits));
+                                            next_norm && rowvec, &splits, ws));
         if (!next_norm) return AESIR_OK;
         if (splits > 1 && rowvec) {
             hipLaunchKernelGGL(reduce_residual_norm_rows_kernel, dim3((unsigned)n), dim3(kPThreads), 0, s,
@@ -512,7 +589,7 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
         int64_t qkv_splits = 1;
         if (mfma)
             AESIR_TRY(launch_mfma<kEpiStore>(s, Xn, n, d, L.wqkv, qkv_n, QKV, qkv_n, m->pf_part, m->pf_part_floats,
-                                             "gemm_mfma_qkv", true, &qkv_splits));
+                                             "gemm_mfma_qkv", true, &qkv_splits, L.sqkv));
         else
             AESIR_TRY(launch_gemm_f16(m->ctx, Xn, n, d, L.wqkv, qkv_n, QKV));
         if (qkv_splits > 1) {
@@ -534,7 +611,7 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
         AESIR_LAUNCH_CHECK("prefill_attention_kernel");
         // O projection + residual, then the feed-forward norm (inference.mojo:227-241)
         if (mfma) {
-            AESIR_TRY(residual_gemm(ATT, d, L.wo, L.ffn_norm, "gemm_mfma_o_residual"));
+            AESIR_TRY(residual_gemm(ATT, d, L.wo, L.so, L.ffn_norm, "gemm_mfma_o_residual"));
         } else {
             AESIR_TRY(launch_gemm_f16(m->ctx, ATT, n, d, L.wo, d, Xn));
             AESIR_TRY(launch_residual_add(s, X, Xn, n * d));
@@ -544,9 +621,9 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
         // the next layer's attention-norm rows
         if (mfma) {
             AESIR_TRY(launch_mfma<kEpiSwiglu>(s, Xn, n, d, L.wgu, 2 * f, ACT, f, m->pf_part, m->pf_part_floats,
-                                                "gemm_mfma_gate_up_swiglu"));
+                                                "gemm_mfma_gate_up_swiglu", false, nullptr, L.sgu));
             const void *next_norm = l + 1 < c.n_layers ? m->layers[l + 1].attn_norm : nullptr;
-            AESIR_TRY(residual_gemm(ACT, f, L.wdown, next_norm, "gemm_mfma_down_residual"));
+            AESIR_TRY(residual_gemm(ACT, f, L.wdown, L.sdown, next_norm, "gemm_mfma_down_residual"));
             xn_ready = next_norm != nullptr;
         } else {
             // interleaved gate/up rows -> [n][2f] products, then the SwiGLU over the pairs
@@ -570,7 +647,9 @@ int32_t model_prefill(aesir_model *m, const int64_t *tokens, int64_t n, int64_t 
         if (tokens[i] < 0 || tokens[i] >= c.vocab)
             return fail(AESIR_ERR_INVALID, "Prompt token ID is outside the embedding vocabulary");
     AESIR_TRY(ensure_rope(m, start_pos + n));
-    if (m->wtype != AESIR_GGML_F16) {  // Q8_0 weights: the reference's prefill, one decode step per position
+    if (m->wtype != AESIR_GGML_F16 && !prefill_mfma_ok(m)) {
+        // Q8_0 weights in shapes the MFMA GEMM does not tile: the reference's prefill, one decode
+        // step per position
         for (int64_t i = 0; i < n; i++) AESIR_TRY(model_step(m, tokens[i], start_pos + i, next));
         return AESIR_OK;
     }

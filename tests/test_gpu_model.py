@@ -228,3 +228,14 @@ def test_llama3_8b_shape_properties(A, oracle):
         assert g == e == host
         print("llama3-8b shape: 8 graph steps in", ms, "ms", flush=True)
         m.close()
+
+
+def test_context_refuses_destroy_while_models_live(A):
+    """A model holds pointers into its context: aesir_ctx_destroy refuses while one is alive, and
+    Context.close() destroys the context's models first."""
+    c = A.Context(64 << 20)
+    m = A.Model.create(c, A.ModelConfig(64, 1, 4, 4, 64, 64, 16))
+    assert A._L.aesir_ctx_destroy(c.h) != 0
+    assert "still alive" in A._L.aesir_last_error().decode()
+    c.close()
+    assert m.h is None and c.h is None

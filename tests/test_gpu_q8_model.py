@@ -8,8 +8,8 @@ dequantized weights: identical greedy tokens, logits within max-abs 2e-2 / rel 1
 - shapes where K < 4096 (idle threads), K = 4096 and partial last slabs (K = 5632, 14336), the
   Q8_0 embedding row fused into layer 0, and the Q8_0 lm_head with its argmax;
 - a GGUF v3 file with Q8_0 matrices loads into the same model as set_tensor builds;
-- graph replay equals eager launches; the batched-prefill entry point on a Q8_0 model equals the
-  per-position forward; device init draws quants and scales in their stated ranges.
+- graph replay equals eager launches; the batched prefill (Q8_0 MFMA GEMMs) equals the
+  per-position oracle; device init draws quants and scales in their stated ranges.
 """
 import numpy as np
 import pytest
@@ -173,7 +173,7 @@ def test_q8_gguf_load_matches_set_tensor(A, ctx, oracle, tmp_path):
 
 def test_q8_graph_eager_prefill_agree(A, ctx, oracle):
     """Device-autoregressive decode (graph and eager) continues the host-driven stream; the
-    prefill entry point (per-position steps for Q8_0) returns the same next token."""
+    batched prefill returns the same next token."""
     cfg = Q8_TL
     tensors, _ = q8_weights(A, oracle, cfg, 31)
     m = q8_model(A, ctx, cfg, tensors)
@@ -190,6 +190,36 @@ def test_q8_graph_eager_prefill_agree(A, ctx, oracle):
     assert list(e_toks) == host[1:]
     for mm in (m, m2, m3):
         mm.close()
+
+
+@pytest.mark.parametrize("shape,n_prompt,split", [("small", 40, 0), ("small", 200, 77), ("tinyllama", 100, 0)])
+def test_q8_batched_prefill_matches_per_position(A, ctx, oracle, shape, n_prompt, split):
+    """aesir_prefill on a Q8_0 model runs the Q8_0 MFMA GEMMs (quants and scales copied into LDS,
+    dequantized per fragment): the next token, logits within tolerance and the greedy steps that
+    read the prefilled cache equal the per-position oracle on the dequantized weights. 200
+    positions = two 128-row chunks; `split` > 0 prefills the prompt in two calls (start_pos > 0)."""
+    cfg = dict(Q8_SMALL if shape == "small" else Q8_TL)
+    cfg["ctx_len"] = max(cfg["ctx_len"], n_prompt + 8)
+    tensors, deq = q8_weights(A, oracle, cfg, 41)
+    om = oracle.Model(oracle.Config(**cfg), deq)
+    prompt = oracle.prompt_tokens(n_prompt, cfg["vocab"], 13)
+    want, wl = oracle_stream(om, prompt, 3)
+    m = q8_model(A, ctx, cfg, tensors)
+    if split:
+        m.prefill(prompt[:split])
+        got = m.prefill(prompt[split:], start_pos=split)
+    else:
+        got = m.prefill(prompt)
+    assert within_tol(m.logits(), wl[0])
+    assert got == want[0]
+    cur = list(prompt) + [got]
+    follow = [got]
+    for _ in range(2):
+        nxt = m.forward_pass(cur, len(cur) - 1)
+        cur.append(nxt)
+        follow.append(nxt)
+    assert follow == want
+    m.close()
 
 
 def test_q8_init_random_ranges(A, ctx):

@@ -7,7 +7,7 @@
 //   A (activations) and B (weights) are both K-contiguous, so every MFMA operand fragment is one
 //   16-byte row load: lane l holds row (l % 16) and k = 8 (l / 16) .. +7 of its 16 x 32 slice, the
 //   same k order for A and B. A workgroup is 4 waves over 64 adjacent output columns (16 weight
-//   rows per wave) and a 128-row M tile. Each 64-wide K chunk of A and of the workgroup's weight
+//   rows per wave) and a 32-row M tile. Each 64-wide K chunk of A and of the workgroup's weight
 //   rows is copied straight from memory into an LDS stage (buffer loads with the LDS destination,
 //   no register staging, weight lines fetched whole), and every wave reads its fragments with
 //   ds_read_b128. Each wave keeps 8 accumulator tiles (rows 16i + 4 (l / 16) + e, column l % 16
@@ -27,7 +27,14 @@ namespace aesir {
 
 typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int kGemmMT = 128;  // rows of A per workgroup tile
+// Rows of A per workgroup tile and the workgroup count the K splits aim for. Measured on MI355X
+// (TinyLlama 128-token prefill, ms): M tile 128 / 256 workgroups 2.39; 64 / 256 2.31; 64 / 512
+// 2.23; 32 / 512 2.22; 32 / 1024 2.37. Smaller tiles re-read the weights from L2 (one HBM read)
+// but copy less of A per workgroup and fit more workgroups per CU.
+constexpr int kGemmMT = 32;
+constexpr int kGemmWgTarget = 512;
+constexpr int kGemmMF = kGemmMT / 16;   // MFMA row fragments per wave
+constexpr int kGemmAJ = kGemmMT / 8 / 4;  // A copy instructions per wave per chunk
 constexpr int kGemmWaves = 4;
 constexpr int kGemmNW = 16;   // output columns per wave
 constexpr int kGemmNT = kGemmWaves * kGemmNW;
@@ -60,10 +67,10 @@ __device__ __forceinline__ void gemm_epilogue(h16 *C, int64_t ldc, int64_t M, in
 constexpr int kGemmKC = 64;  // k per chunk (two MFMA k-steps)
 
 // grid (N / 64, ceil(M / 128), splits): a 4-wave workgroup owns 64 output columns (16 per wave)
-// and a 128-row M tile. With one split the epilogue is applied here; otherwise split z writes its
+// and a kGemmMT-row M tile. With one split the epilogue is applied here; otherwise split z writes its
 // f32 partial to P[z][M][N] for gemm_reduce_kernel. Requires K % 64 == 0 and 16-byte aligned rows
 // (checked by the launcher). Each 64-wide K chunk
-// of A (128 rows x 128 B) and of the workgroup's 64 weight rows (64 x 128 B) is copied by
+// of A (kGemmMT rows x 128 B) and of the workgroup's 64 weight rows (64 x 128 B) is copied by
 // buffer_load_dwordx4 ... lds straight into one of S LDS stages: a wave instruction moves 8 whole
 // 128-byte row segments (lane l: row l / 8, 16-byte granule l % 8), so every weight line is
 // fetched whole by one instruction, and nothing passes through registers. Granule p of row r
@@ -71,15 +78,15 @@ constexpr int kGemmKC = 64;  // k per chunk (two MFMA k-steps)
 // all LDS banks. S - 1 chunks are in flight ahead of the MFMAs; the waits are explicit vmcnt
 // counts (each wave issues 6 copies per chunk) followed by a workgroup barrier.
 constexpr int kDmaRowBytes = 128;                      // one chunk of one row
-constexpr int kDmaStageA = kGemmMT * kDmaRowBytes;      // 16 KB
+constexpr int kDmaStageA = kGemmMT * kDmaRowBytes;      // 4 KB
 constexpr int kDmaStage = kDmaStageA + kGemmNT * kDmaRowBytes;  // + 8 KB of weights
 constexpr int kDmaCopies = kGemmMT / 8 / kGemmWaves + kGemmNT / 8 / kGemmWaves;  // per wave per chunk (6)
 // Q8_0 weights: a chunk of a weight row is 64 int8 quants (64 B) plus its two f16 block scales.
 constexpr int kDmaQRowBytes = 64;
 constexpr int kDmaStageQ = kDmaStageA + kGemmNT * kDmaQRowBytes + kGemmNT * 4;  // A + quants + scales
-// LDS stages. Measured on MI355X (TinyLlama prefill GEMMs, us per GEMM + reduce): 2 stages
-// (48 KB, three workgroups per CU) and 3 (72 KB, two) are equal and beat 4 or 5 (one workgroup
-// per CU: gate/up 22.6 -> 31.4 and 32.4).
+// LDS stages. Measured on MI355X with a 128-row M tile (TinyLlama prefill GEMMs, us per GEMM +
+// reduce): 2 stages (48 KB, three workgroups per CU) and 3 (72 KB, two) are equal and beat 4 or 5
+// (one workgroup per CU: gate/up 22.6 -> 31.4 and 32.4). With the 32-row tile a stage is 12 KB.
 constexpr int kDmaStages = 2;
 
 __device__ __forceinline__ int dma_swz(int row) { return (row >> 1) & 7; }
@@ -116,14 +123,14 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(const h16 *__re
     const int64_t KB = K / 32;
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc((void *)Bs, 0, Q8 ? (int)(N * KB * 2) : 0, kBufferDword3);
-    // copy instruction j of this wave: A rows 32 wave + 8 j + lane / 8 (j < 4), weight rows
+    // copy instruction j of this wave: A rows 8 kGemmAJ wave + 8 j + lane / 8 (j < kGemmAJ), weight rows
     // 16 wave + 8 j + lane / 8 (j < 2); the per-lane byte offset holds the row and granule, the
     // chunk's k offset goes in the uniform soffset
     const int drow = lane >> 3, dp = lane & 7;
-    int aoff[4], boff[2];
+    int aoff[kGemmAJ], boff[2];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int row = 32 * wave + 8 * j + drow;
+    for (int j = 0; j < kGemmAJ; j++) {
+        const int row = 8 * kGemmAJ * wave + 8 * j + drow;
         aoff[j] = (int)((m0 + row) * K * 2) + ((dp ^ dma_swz(row)) << 4);
     }
 #pragma unroll
@@ -139,9 +146,9 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(const h16 *__re
         const int kb = (int)(c * kDmaRowBytes);
         uint8_t *sa = lds + stage * kStage;
 #pragma unroll
-        for (int j = 0; j < 4; j++)
+        for (int j = 0; j < kGemmAJ; j++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                ra, (__attribute__((address_space(3))) void *)(sa + (32 * wave + 8 * j) * kDmaRowBytes), 16, aoff[j],
+                ra, (__attribute__((address_space(3))) void *)(sa + (8 * kGemmAJ * wave + 8 * j) * kDmaRowBytes), 16, aoff[j],
                 kb, 0, 0);
         if (Q8) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -160,9 +167,9 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(const h16 *__re
         }
     };
 
-    f32x4 acc[8];
+    f32x4 acc[kGemmMF];
 #pragma unroll
-    for (int i = 0; i < 8; i++) acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < kGemmMF; i++) acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     if (c0 < c1) {
 #pragma unroll
         for (int j = 0; j < S - 1; j++) issue(c0 + j, j);
@@ -173,7 +180,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(const h16 *__re
             __builtin_amdgcn_s_barrier();                                // ... and every wave's
             issue(c + S - 1, (t + S - 1) % S);  // into the stage chunk c - 1 used
             const uint8_t *sa = lds + (t % S) * kStage, *sb = sa + kDmaStageA;
-            u32x4 bf[2], a[2][8];  // every fragment of the chunk is requested before the first MFMA
+            u32x4 bf[2], a[2][kGemmMF];  // every fragment of the chunk is requested before the first MFMA
             uint2 bq[2];
             h16 bd[2];
 #pragma unroll
@@ -186,7 +193,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(const h16 *__re
                     bf[q] = ld16(sb + brow * kDmaRowBytes + (((4 * q + g) ^ dma_swz(brow)) << 4));
                 }
 #pragma unroll
-                for (int i = 0; i < 8; i++) {
+                for (int i = 0; i < kGemmMF; i++) {
                     const int row = 16 * i + r;
                     a[q][i] = ld16(sa + row * kDmaRowBytes + (((4 * q + g) ^ dma_swz(row)) << 4));
                 }
@@ -204,7 +211,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(const h16 *__re
 #pragma unroll
             for (int q = 0; q < 2; q++)
 #pragma unroll
-                for (int i = 0; i < 8; i++) acc[i] = mfma16x16x32(a[q][i], bf[q], acc[i]);
+                for (int i = 0; i < kGemmMF; i++) acc[i] = mfma16x16x32(a[q][i], bf[q], acc[i]);
             __builtin_amdgcn_sched_barrier(0);
         }
         __builtin_amdgcn_s_waitcnt(vm_wait(0));  // no copy may land in LDS after the workgroup ends
@@ -212,7 +219,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(const h16 *__re
 
     const int64_t n = nb + 16 * wave + r;
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
+    for (int i = 0; i < kGemmMF; i++) {
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const int64_t m = m0 + 16 * i + 4 * g + e;
@@ -248,11 +255,11 @@ static bool mfma_shape_ok(const void *A, int64_t M, int64_t K, const void *B, in
            (N + kGemmNT) * K * 2 < lim;
 }
 
-// K splits for a GEMM: enough workgroups to keep the chip's memory pipes full (about 256
-// workgroups, 1024 waves) while every split keeps at least 8 k-steps.
+// K splits for a GEMM: enough workgroups to keep the chip's memory pipes full (about
+// kGemmWgTarget) while every split keeps at least 8 k-steps.
 static int64_t gemm_splits(int64_t M, int64_t K, int64_t N) {
     const int64_t tiles = ((N + kGemmNT - 1) / kGemmNT) * ((M + kGemmMT - 1) / kGemmMT);
-    int64_t s = (256 + tiles - 1) / tiles;
+    int64_t s = (kGemmWgTarget + tiles - 1) / tiles;
     const int64_t max_s = K / 256;  // at least four 64-wide chunks per split
     if (s > max_s) s = max_s;
     return s < 1 ? 1 : s;
@@ -421,7 +428,8 @@ __global__ __launch_bounds__(kPThreads) void reduce_qkv_post_rows_kernel(
     int64_t max_seq, const h16x2 *__restrict__ rope, h16 *__restrict__ Q, h16 *__restrict__ kc, h16 *__restrict__ vc) {
     const int64_t r = blockIdx.x, pos = p0 + r, slot = pos % max_seq;
     const int64_t N = dim + 2 * kvd, pairs = (dim + kvd) / 2;
-    for (int64_t j = threadIdx.x; j < N / 2; j += kPThreads) {
+    // grid.y workgroups share a row's pairs, so every thread sums one pair's partials
+    for (int64_t j = (int64_t)blockIdx.y * kPThreads + threadIdx.x; j < N / 2; j += (int64_t)gridDim.y * kPThreads) {
         const int64_t col = 2 * j;
         float2 v = {0.0f, 0.0f};
         for (int64_t z = 0; z < splits; z++) {
@@ -593,7 +601,8 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
         else
             AESIR_TRY(launch_gemm_f16(m->ctx, Xn, n, d, L.wqkv, qkv_n, QKV));
         if (qkv_splits > 1) {
-            hipLaunchKernelGGL(reduce_qkv_post_rows_kernel, dim3((unsigned)n), dim3(kPThreads), 0, s,
+            hipLaunchKernelGGL(reduce_qkv_post_rows_kernel,
+                               dim3((unsigned)n, (unsigned)((qkv_n / 2 + kPThreads - 1) / kPThreads)), dim3(kPThreads), 0, s,
                                (const float *)m->pf_part, qkv_splits, n, d, kvd, hd, p0, c.ctx_len,
                                (const h16x2 *)m->rope, Q, kc, vc);
             AESIR_LAUNCH_CHECK("reduce_qkv_post_rows_kernel");

@@ -517,6 +517,101 @@ __global__ __launch_bounds__(kWave) void prefill_attention_kernel(const h16 *__r
     }
 }
 
+// The same attention for KV groups of 8 query heads (head_dim 64 or 128) or 4 (head_dim 128), one workgroup per
+// (row, KV head): the G query heads that share a KV head are computed together, so each K/V row
+// is loaded once per workgroup (whole 16-byte row segments) into LDS tiles of 128 positions
+// instead of once per head and lane. Per tile: thread (head h, slot u) scores positions u,
+// u + 256/G, ... (dot8 over the head dims in the same order as above), the G heads' f32 online
+// softmax runs over their 256/G-thread groups, and thread (h, dim pair) accumulates P V from LDS.
+constexpr int kAttTile = 128;
+template <int HD, int G>
+__global__ __launch_bounds__(kPThreads) void prefill_attention_tile_kernel(
+    const h16 *__restrict__ Q, const h16 *__restrict__ kc, const h16 *__restrict__ vc, h16 *__restrict__ out,
+    int64_t dim, int64_t kvd, int64_t p0, int64_t max_seq, float scale) {
+    constexpr int TPH = kPThreads / G;        // threads per head (32 or 64)
+    constexpr int NP = kAttTile / TPH;         // positions per thread per tile
+    constexpr int NDP = HD / 2 / TPH;          // dim pairs per thread
+    constexpr int KR = HD + 8;                 // padded K row (halves)
+    constexpr int CH = HD / 8;                 // 16-byte chunks per row
+    static_assert(NP >= 1 && NDP >= 1 && TPH <= kWave, "shape");
+    __shared__ __align__(16) h16 ks[kAttTile][KR];
+    __shared__ __align__(16) h16 vs[kAttTile][HD];
+    __shared__ float ps[G][kAttTile];
+    const int tid = threadIdx.x, h = tid / TPH, u = tid % TPH;
+    const int64_t r = blockIdx.x, g = blockIdx.y;
+    const int64_t pos = p0 + r;
+    const int64_t S = pos + 1 < max_seq ? pos + 1 : max_seq;
+    const int64_t head = g * G + h;
+    u32x4 qr[CH];
+    {
+        const h16 *q = Q + r * dim + head * HD;
+#pragma unroll
+        for (int c = 0; c < CH; c++) qr[c] = ld16(q + 8 * c);
+    }
+    const h16 *Kg = kc + g * HD, *Vg = vc + g * HD;
+    float m = -INFINITY, l = 0.0f, acc[NDP][2];
+#pragma unroll
+    for (int j = 0; j < NDP; j++) acc[j][0] = acc[j][1] = 0.0f;
+    for (int64_t t0 = 0; t0 < S; t0 += kAttTile) {
+        const int n = (int)(S - t0 < kAttTile ? S - t0 : kAttTile);
+        __syncthreads();  // the previous tile's K, V and P are no longer read
+        for (int e = tid; e < kAttTile * CH; e += kPThreads) {
+            const int row = e / CH, c = e % CH;
+            const int64_t p = t0 + (row < n ? row : 0);
+            st16(&ks[row][8 * c], ld16(Kg + p * kvd + 8 * c));
+            st16(&vs[row][8 * c], ld16(Vg + p * kvd + 8 * c));
+        }
+        __syncthreads();
+        float sc[NP];
+        float mt = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < NP; j++) {
+            const int row = u + j * TPH;
+            float d = 0.0f;
+#pragma unroll
+            for (int c = 0; c < CH; c++) d = dot8(ld16(&ks[row][8 * c]), qr[c], d);
+            sc[j] = row < n ? d * scale : -INFINITY;
+            mt = fmaxf(mt, sc[j]);
+        }
+#pragma unroll
+        for (int o = TPH / 2; o > 0; o >>= 1) mt = fmaxf(mt, __shfl_xor(mt, o, kWave));
+        const float mn = fmaxf(m, mt);
+        float lt = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NP; j++) {
+            const float pr = u + j * TPH < n ? expf(sc[j] - mn) : 0.0f;
+            ps[h][u + j * TPH] = pr;
+            lt += pr;
+        }
+#pragma unroll
+        for (int o = TPH / 2; o > 0; o >>= 1) lt += __shfl_xor(lt, o, kWave);
+        const float al = expf(m - mn);  // 0 on the first tile
+        l = l * al + lt;
+        m = mn;
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < NDP; j++) {
+            const int dp = 2 * (u + j * TPH);
+            float a0 = acc[j][0] * al, a1 = acc[j][1] * al;
+            for (int t = 0; t < n; t++) {
+                const float pr = ps[h][t];
+                const h16x2 v = *reinterpret_cast<const h16x2 *>(&vs[t][dp]);
+                a0 = fmaf(pr, (float)v.x, a0);
+                a1 = fmaf(pr, (float)v.y, a1);
+            }
+            acc[j][0] = a0;
+            acc[j][1] = a1;
+        }
+    }
+    h16 *o = out + r * dim + head * HD;
+#pragma unroll
+    for (int j = 0; j < NDP; j++) {
+        const int dp = 2 * (u + j * TPH);
+        o[dp] = (h16)(acc[j][0] / l);
+        o[dp + 1] = (h16)(acc[j][1] / l);
+    }
+}
+
 // act[i] = f16(up * silu(gate)) over interleaved [gate, up] pairs gu[2i], gu[2i + 1]
 // (inference.mojo:257-260 on the gate/up GEMM rows as this build lays them out).
 __global__ __launch_bounds__(kPThreads) void swiglu_pairs_kernel(const h16 *__restrict__ gu, h16 *__restrict__ act,
@@ -611,6 +706,17 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
                                c.ctx_len, (const h16x2 *)m->rope, Q, kc, vc);
             AESIR_LAUNCH_CHECK("qkv_post_rows_kernel");
         }
+        const int64_t G = c.n_heads / c.n_kv_heads;
+        const dim3 tgrid((unsigned)n, (unsigned)c.n_kv_heads);
+#define AESIR_PF_ATT(HDV, GV)                                                                                      \
+    if (hd == HDV && G == GV)                                                                                     \
+        hipLaunchKernelGGL((prefill_attention_tile_kernel<HDV, GV>), tgrid, dim3(kPThreads), 0, s, Q, kc, vc, ATT, d, \
+                           kvd, p0, c.ctx_len, m->attn_scale);                                                   \
+    else
+        AESIR_PF_ATT(64, 8)
+        AESIR_PF_ATT(128, 8)
+        AESIR_PF_ATT(128, 4)
+#undef AESIR_PF_ATT
         if (hd % 8 == 0)  // rows of K are then 16-byte aligned (kvd and the cache base are)
             hipLaunchKernelGGL(prefill_attention_kernel<true>, dim3((unsigned)n, (unsigned)c.n_heads), dim3(kWave), 0,
                                s, Q, kc, vc, ATT, d, kvd, hd, c.n_heads / c.n_kv_heads, p0, c.ctx_len, m->attn_scale);

@@ -8,8 +8,8 @@
   (aesir.mojo:358-374, one forward_pass per position): the same next token, logits within
   max-abs 2e-2 / rel 1e-2, and the greedy decode that follows reads the K/V cache the prefill
   wrote and continues with the oracle's tokens. Covered: the tiny model (non-MFMA shapes: ffn 172),
-  prompts longer than one 128-row chunk, continuation at start_pos > 0, and the TinyLlama shape
-  (MFMA GEMMs with the store, residual and SwiGLU epilogues).
+  prompts longer than one 128-row chunk, continuation at start_pos > 0, the TinyLlama shape
+  (MFMA GEMMs with the store, residual and SwiGLU epilogues) and the GQA-grouped attention tiles.
 """
 import numpy as np
 import pytest
@@ -153,6 +153,31 @@ def test_prefill_tinyllama_shape_mfma(A, ctx, oracle):
     first, ologits, follow = oracle_prefill(om, prompt, 3)
     m = gpu_model(A, ctx, cfg, w)
     got = m.prefill(prompt)
+    assert within_tol(m.logits(), ologits)
+    assert got == first
+    assert gpu_follow(m, prompt, got, 3) == follow
+    m.close()
+
+
+@pytest.mark.parametrize("dim,heads,kv,n_prompt,split", [(512, 8, 1, 300, 0), (512, 4, 1, 150, 0),
+                                                        (1024, 8, 1, 140, 70)])
+def test_prefill_grouped_attention_tiles(A, ctx, oracle, dim, heads, kv, n_prompt, split):
+    """The GQA-grouped prefill attention (one workgroup per row and KV head, 128-position LDS
+    tiles): head_dim 64 with 8 query heads per KV head, head_dim 128 with 4 and with 8; prompts
+    longer than one tile (300 positions: three tiles for the last rows) and a continuation at
+    start_pos 70. Next token, logits and the following greedy steps equal the per-position oracle."""
+    cfg = oracle.Config(dim=dim, n_layers=2, n_heads=heads, n_kv_heads=kv, ffn=2 * dim, vocab=512,
+                        ctx_len=n_prompt + 16)
+    w = oracle.synthetic_weights(cfg, 77)
+    om = oracle.Model(cfg, w)
+    prompt = oracle.prompt_tokens(n_prompt, cfg.vocab, 3)
+    first, ologits, follow = oracle_prefill(om, prompt, 3)
+    m = gpu_model(A, ctx, cfg, w)
+    if split:
+        m.prefill(prompt[:split])
+        got = m.prefill(prompt[split:], start_pos=split)
+    else:
+        got = m.prefill(prompt)
     assert within_tol(m.logits(), ologits)
     assert got == first
     assert gpu_follow(m, prompt, got, 3) == follow

@@ -84,10 +84,10 @@ constexpr int kDmaCopies = kGemmMT / 8 / kGemmWaves + kGemmNT / 8 / kGemmWaves; 
 // Q8_0 weights: a chunk of a weight row is 64 int8 quants (64 B) plus its two f16 block scales.
 constexpr int kDmaQRowBytes = 64;
 constexpr int kDmaStageQ = kDmaStageA + kGemmNT * kDmaQRowBytes + kGemmNT * 4;  // A + quants + scales
-// LDS stages. Measured on MI355X with a 128-row M tile (TinyLlama prefill GEMMs, us per GEMM +
-// reduce): 2 stages (48 KB, three workgroups per CU) and 3 (72 KB, two) are equal and beat 4 or 5
-// (one workgroup per CU: gate/up 22.6 -> 31.4 and 32.4). With the 32-row tile a stage is 12 KB.
-constexpr int kDmaStages = 2;
+// LDS stages (S - 1 chunks in flight). Measured on MI355X, TinyLlama 128-token prefill with the
+// 32-row tile (12 KB stages): 2 stages 1.88 ms, 3 stages 1.74, 4 1.76, 6 1.89.
+constexpr int kDmaStages = 3;                  // f16 weights
+constexpr int kDmaStagesQ = 2;                 // Q8_0 weights (full-drain waits)
 
 __device__ __forceinline__ int dma_swz(int row) { return (row >> 1) & 7; }
 __device__ __forceinline__ int dma_swz_q(int row) { return (row >> 2) & 3; }  // 4 granules per quant row
@@ -107,7 +107,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(const h16 *__re
                                                                 const void *__restrict__ B, int64_t N,
                                                                 h16 *__restrict__ C, int64_t ldc,
                                                                 float *__restrict__ P, const h16 *__restrict__ Bs) {
-    constexpr int S = kDmaStages;
+    constexpr int S = Q8 ? kDmaStagesQ : kDmaStages;
     constexpr int kStage = Q8 ? kDmaStageQ : kDmaStage;
     static_assert(!Q8 || S == 2, "the Q8_0 copies rely on full-drain waits");
     extern __shared__ __align__(16) uint8_t lds[];  // S stages of kStage bytes
@@ -290,7 +290,7 @@ static int32_t launch_mfma(hipStream_t s, const void *A, int64_t M, int64_t K, c
     if (EPI == kEpiSwiglu && (N & 1)) return fail(AESIR_ERR_INVALID, "%s: odd gate/up column count", name);
     const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)splits);
     if (Bs)
-        hipLaunchKernelGGL((gemm_mfma_kernel<EPI, true>), grid, dim3(kGemmThreads), kDmaStages * kDmaStageQ, s,
+        hipLaunchKernelGGL((gemm_mfma_kernel<EPI, true>), grid, dim3(kGemmThreads), kDmaStagesQ * kDmaStageQ, s,
                            (const h16 *)A, M, K, B, N, (h16 *)C, ldc, part, (const h16 *)Bs);
     else
         hipLaunchKernelGGL((gemm_mfma_kernel<EPI, false>), grid, dim3(kGemmThreads), kDmaStages * kDmaStage, s,

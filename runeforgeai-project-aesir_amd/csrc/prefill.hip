@@ -80,14 +80,13 @@ constexpr int kGemmKC = 64;  // k per chunk (two MFMA k-steps)
 constexpr int kDmaRowBytes = 128;                      // one chunk of one row
 constexpr int kDmaStageA = kGemmMT * kDmaRowBytes;      // 4 KB
 constexpr int kDmaStage = kDmaStageA + kGemmNT * kDmaRowBytes;  // + 8 KB of weights
-constexpr int kDmaCopies = kGemmMT / 8 / kGemmWaves + kGemmNT / 8 / kGemmWaves;  // per wave per chunk (6)
 // Q8_0 weights: a chunk of a weight row is 64 int8 quants (64 B) plus its two f16 block scales.
 constexpr int kDmaQRowBytes = 64;
 constexpr int kDmaStageQ = kDmaStageA + kGemmNT * kDmaQRowBytes + kGemmNT * 4;  // A + quants + scales
 // LDS stages (S - 1 chunks in flight). Measured on MI355X, TinyLlama 128-token prefill with the
 // 32-row tile (12 KB stages): 2 stages 1.88 ms, 3 stages 1.74, 4 1.76, 6 1.89.
 constexpr int kDmaStages = 3;                  // f16 weights
-constexpr int kDmaStagesQ = 2;                 // Q8_0 weights (full-drain waits)
+constexpr int kDmaStagesQ = 2;  // Q8_0 weights: 2 stages 1.94-1.97 ms, 3 stages 1.98-1.99, 4 stages 2.01 (TinyLlama)
 
 __device__ __forceinline__ int dma_swz(int row) { return (row >> 1) & 7; }
 __device__ __forceinline__ int dma_swz_q(int row) { return (row >> 2) & 3; }  // 4 granules per quant row
@@ -100,8 +99,8 @@ constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (
 // are 64-byte quant segments (one copy per wave: 16 rows x 4 granules, granule p of row r holding
 // k-granule p ^ ((r >> 2) & 3)) plus the rows' two scales (one dword copy, wave 0). Each B
 // fragment is dequantized from LDS as f16(q * d) (dequant_q8x4, gemm_q8_0's rounding), so the
-// product equals the f16 GEMM with the dequantized weights. With 2 stages every wait is a full
-// drain, so the waves' different copy counts need no bookkeeping.
+// product equals the f16 GEMM with the dequantized weights. Wave 0 issues one more copy per chunk
+// than the others, and its wait count says so.
 template <int EPI, bool Q8>
 __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(const h16 *__restrict__ A, int64_t M, int64_t K,
                                                                 const void *__restrict__ B, int64_t N,
@@ -109,7 +108,10 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(const h16 *__re
                                                                 float *__restrict__ P, const h16 *__restrict__ Bs) {
     constexpr int S = Q8 ? kDmaStagesQ : kDmaStages;
     constexpr int kStage = Q8 ? kDmaStageQ : kDmaStage;
-    static_assert(!Q8 || S == 2, "the Q8_0 copies rely on full-drain waits");
+    // copies per wave per chunk: A rows, then f16 weight rows, or Q8_0 quant rows (+ the scale
+    // dword copy, issued by wave 0 only)
+    constexpr int kCopiesF16 = kGemmAJ + kGemmNT / 8 / kGemmWaves;
+    constexpr int kCopiesQ8 = kGemmAJ + 1;
     extern __shared__ __align__(16) uint8_t lds[];  // S stages of kStage bytes
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t m0 = (int64_t)blockIdx.y * kGemmMT;
@@ -176,7 +178,13 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(const h16 *__re
         const int brow = 16 * wave + r;
         for (int64_t c = c0; c < c1; c++) {
             const int t = (int)(c - c0);
-            __builtin_amdgcn_s_waitcnt(vm_wait(kDmaCopies * (S - 2)));  // this wave's copies of chunk c landed
+            // this wave's copies of chunk c landed (S - 2 later chunks may still be in flight)
+            if (!Q8)
+                __builtin_amdgcn_s_waitcnt(vm_wait(kCopiesF16 * (S - 2)));
+            else if (wave == 0)
+                __builtin_amdgcn_s_waitcnt(vm_wait((kCopiesQ8 + 1) * (S - 2)));
+            else
+                __builtin_amdgcn_s_waitcnt(vm_wait(kCopiesQ8 * (S - 2)));
             __builtin_amdgcn_s_barrier();                                // ... and every wave's
             issue(c + S - 1, (t + S - 1) % S);  // into the stage chunk c - 1 used
             const uint8_t *sa = lds + (t % S) * kStage, *sb = sa + kDmaStageA;

@@ -194,6 +194,31 @@ def q8_bench(A, seed: int, kv: int, steps: int, warmup: int, kernel_iters: int) 
             "kernel_ms": {k: round(v, 5) for k, v in kt.items()}, "tokens_head": toks[:8]}
 
 
+def sampler_bench(A, seed: int, reps: int = 50) -> dict:
+    """aesir_sample_token (sample_token_from_logits on the device) over Llama-3's 128256 f16 logits
+    with 256 context tokens: wall time per blocking call (host round trip included) for the greedy
+    branch, a top-k 40 / top-p 0.95 / temperature 0.8 / repetition 1.1 draw, and a full-vocabulary
+    temperature-1 draw."""
+    rng = np.random.default_rng(seed)
+    ctx = A.Context(64 << 20)
+    logits = ctx.from_numpy((rng.standard_normal((1, VOCAB)) * 2.0).astype(np.float16))
+    context = rng.integers(0, VOCAB, 256).tolist()
+    cfgs = {"greedy_us": A.SamplerConfig(temperature=0.0),
+            "topk_topp_us": A.SamplerConfig(temperature=0.8, top_k=40, top_p=0.95, repetition_penalty=1.1),
+            "full_vocab_us": A.SamplerConfig(temperature=1.0)}
+    out = {"workload": f"sample_token_from_logits over {VOCAB} f16 logits, 256 context tokens"}
+    r = A.RuneRNG(seed)
+    for name, cfg in cfgs.items():
+        for _ in range(3):
+            A.sample_token(ctx, logits, cfg, r, context)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            A.sample_token(ctx, logits, cfg, r, context)
+        out[name] = round((time.perf_counter() - t0) / reps * 1e6, 1)
+    ctx.close()
+    return out
+
+
 def measured_traffic():
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary
     (FETCH_SIZE + WRITE_SIZE, each scaled by its copy-kernel calibration factor), or None."""
@@ -307,6 +332,7 @@ def main():
     ctx.close()
     if not args.no_prefill:
         out["prefill"] = prefill_bench(A, args.seed)
+    out["sampler"] = sampler_bench(A, args.seed)
     if not args.no_q8:
         out["q8_0"] = q8_bench(A, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters)
         out["q8_0"]["prefill"] = prefill_bench(A, args.seed, n_decode=64, q8=True)

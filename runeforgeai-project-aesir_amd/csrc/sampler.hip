@@ -8,9 +8,10 @@
 //             (descending logit key, index). Equal logits (-0 == +0) keep index order, which is the
 //             order the reference's stable insertion sort (:92-104) produces; every later stage of
 //             the stack sees an already sorted prefix, so one sort serves all of them
-//   tail      one workgroup: the exps in parallel, then the f32 running sums of apply_top_p,
-//             apply_min_p and the final draw sequentially in candidate order (f32 addition is not
-//             associative; the sums must follow the reference's order to choose the same token)
+//   tail      one workgroup: the exps in parallel, one LDS tile at a time, and the f32 running sums
+//             of apply_top_p, apply_min_p and the final draw in thread 0 in candidate order (f32
+//             addition is not associative; the sums must follow the reference's order to choose
+//             the same token)
 //   greedy    temperature <= 0 or top_k == 1: the first maximum of the sanitized, masked logits
 //
 // The random number comes from RuneRNG on the host (one draw per sampled token, consumed only
@@ -100,12 +101,13 @@ __global__ __launch_bounds__(1024) void sampler_greedy_kernel(const h16 *__restr
     __shared__ float bv[1024];
     __shared__ int64_t bi[1024];
     const int tid = threadIdx.x;
-    const int64_t per = (V + 1023) / 1024;
     float best = -INFINITY;
     int64_t besti = -1;
-    for (int64_t i = (int64_t)tid * per; i < (int64_t)(tid + 1) * per && i < V; i++) {
+    // strided (coalesced) scan; each thread sees its indices in increasing order, so strict '>'
+    // keeps its first maximum, and the tree below resolves equal values to the lower index
+    for (int64_t i = tid; i < V; i += 1024) {
         float v = sanitize_logit((float)logits[i]);
-        if (mask[i]) v = -1e9f;
+        if (mask && mask[i]) v = -1e9f;
         if (besti < 0 || v > best) {
             best = v;
             besti = i;
@@ -133,58 +135,146 @@ __global__ __launch_bounds__(1024) void sampler_greedy_kernel(const h16 *__restr
 }
 
 // Truncations and the draw over the candidate list: value i is vals[order ? order[i] : i].
+// Every running f32 sum of the reference is evaluated in candidate order by thread 0: the
+// workgroup computes a tile of kSeqTile exps in parallel into LDS, thread 0 consumes the tile in
+// index order, and the next tile follows.
+constexpr int kSeqTile = 8192;
 __global__ __launch_bounds__(kTailThreads) void sampler_tail_kernel(const float *__restrict__ vals,
                                                                     const int32_t *__restrict__ order, int64_t V,
-                                                                    SampleParams p, float *__restrict__ ex,
-                                                                    int64_t *out) {
+                                                                    SampleParams p, int64_t *out) {
+    __shared__ __align__(16) float tile[kSeqTile];
     __shared__ float red[kTailThreads];
     __shared__ int64_t n_sh;
+    __shared__ float f_sh;
     const int tid = threadIdx.x;
     auto val = [&](int64_t i) -> float { return vals[order ? order[i] : i]; };
     int64_t n = V;
     if (p.top_k > 0 && p.top_k < n) n = p.top_k;  // apply_top_k (:107-116)
 
-    // exps of the sorted prefix relative to its first (largest) logit, as apply_top_p / apply_min_p
-    auto prefix_exps = [&](int64_t m) {
-        const float mx = val(0);
-        for (int64_t i = tid; i < m; i += kTailThreads) ex[i] = exp_f32(val(i) - mx);
+    // Ordered passes over e_i = exp_f32(val(i) - mx), i in [0, m), one LDS tile at a time.
+    auto fill = [&](int64_t t0, int cnt, float mx) {
+        for (int e = tid; e < cnt; e += kTailThreads) tile[e] = exp_f32(val(t0 + e) - mx);
         __syncthreads();
     };
-    if (p.top_p < 1.0f && n > 1) {  // apply_top_p (:119-147)
-        prefix_exps(n);
-        if (tid == 0) {
-            float sum = 0.0f;
-            for (int64_t i = 0; i < n; i++) sum += ex[i];
-            float cum = 0.0f;
-            int64_t cutoff = n - 1;
-            for (int64_t i = 0; i < n; i++) {
-                const float pr = sum > 0.0f ? ex[i] / sum : ex[i];
-                cum += pr;
-                if (cum >= p.top_p) {
-                    cutoff = i;
+    // sum_i e_i in index order (thread 0), broadcast
+    auto seq_sum = [&](int64_t m, float mx) -> float {
+        float sum = 0.0f;
+        for (int64_t t0 = 0; t0 < m; t0 += kSeqTile) {
+            const int cnt = (int)(m - t0 < kSeqTile ? m - t0 : kSeqTile);
+            fill(t0, cnt, mx);
+            if (tid == 0) {
+                // 16 values per block, the next block's LDS reads issued before this block's adds
+                const int nb = cnt / 16;
+                f32x4 cur[4], nxt[4];
+                if (nb > 0)
+#pragma unroll
+                    for (int q = 0; q < 4; q++) cur[q] = *reinterpret_cast<const f32x4 *>(&tile[4 * q]);
+                for (int b = 0; b < nb; b++) {
+                    const int nbase = b + 1 < nb ? 16 * (b + 1) : 16 * b;
+#pragma unroll
+                    for (int q = 0; q < 4; q++) nxt[q] = *reinterpret_cast<const f32x4 *>(&tile[nbase + 4 * q]);
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        sum += cur[q][0];
+                        sum += cur[q][1];
+                        sum += cur[q][2];
+                        sum += cur[q][3];
+                    }
+#pragma unroll
+                    for (int q = 0; q < 4; q++) cur[q] = nxt[q];
+                }
+                for (int e = 16 * nb; e < cnt; e++) sum += tile[e];
+            }
+            __syncthreads();
+        }
+        if (tid == 0) f_sh = sum;
+        __syncthreads();
+        const float r = f_sh;
+        __syncthreads();
+        return r;
+    };
+    // First i with target <= acc_i, acc_i = acc_{i-1} + term(e_i) in f32 (thread 0), or m. The
+    // terms are >= 0, so acc never decreases: a block of 16 is added first and rescanned term by
+    // term only when the target falls inside it.
+    auto seq_reach = [&](int64_t m, float mx, float target, auto term) -> int64_t {
+        float acc = 0.0f;
+        int64_t hit = m;
+        for (int64_t t0 = 0; t0 < m; t0 += kSeqTile) {
+            const int cnt = (int)(m - t0 < kSeqTile ? m - t0 : kSeqTile);
+            fill(t0, cnt, mx);
+            if (tid == 0) {
+                for (int b = 0; b < cnt && hit == m; b += 16) {
+                    const int be = b + 16 < cnt ? b + 16 : cnt;
+                    float a = acc;
+                    if (be - b == 16) {
+                        f32x4 v[4];
+#pragma unroll
+                        for (int q = 0; q < 4; q++) v[q] = *reinterpret_cast<const f32x4 *>(&tile[b + 4 * q]);
+#pragma unroll
+                        for (int q = 0; q < 4; q++)
+#pragma unroll
+                            for (int u = 0; u < 4; u++) a += term(v[q][u]);
+                    } else {
+                        for (int e = b; e < be; e++) a += term(tile[e]);
+                    }
+                    if (target <= a) {  // the crossing is in this block
+                        for (int e = b; e < be; e++) {
+                            acc += term(tile[e]);
+                            if (target <= acc) {
+                                hit = t0 + e;
+                                break;
+                            }
+                        }
+                    } else {
+                        acc = a;
+                    }
+                }
+                n_sh = hit;
+            }
+            __syncthreads();
+            hit = n_sh;
+            __syncthreads();
+            if (hit < m) break;
+        }
+        return hit;
+    };
+
+    if (p.top_p < 1.0f && n > 1) {  // apply_top_p (:119-147): exps relative to the first (largest) logit
+        const float mx = val(0);
+        const float sum = seq_sum(n, mx);
+        const int64_t cut = seq_reach(n, mx, p.top_p, [&](float e) { return sum > 0.0f ? e / sum : e; });
+        n = cut < n ? cut + 1 : n;
+    }
+    if (p.min_p > 0.0f && p.min_p < 1.0f && n > 1) {  // apply_min_p (:166-194)
+        const float mx = val(0);
+        const float sum = seq_sum(n, mx);
+        const float e0 = exp_f32(0.0f);  // the first candidate's exp (val(0) - mx = 0)
+        const float p0 = sum > 0.0f ? e0 / sum : e0;
+        const float threshold = p.min_p * p0;
+        // kept = the first index whose probability falls below the threshold (each test is
+        // independent of the others, so the tile is searched in parallel)
+        int64_t kept = n;
+        for (int64_t t0 = 0; t0 < n && kept == n; t0 += kSeqTile) {
+            const int cnt = (int)(n - t0 < kSeqTile ? n - t0 : kSeqTile);
+            fill(t0, cnt, mx);
+            int first = cnt;
+            for (int e = tid; e < cnt; e += kTailThreads) {
+                const float pr = sum > 0.0f ? tile[e] / sum : tile[e];
+                if (!(pr >= threshold)) {
+                    first = e;
                     break;
                 }
             }
-            n_sh = cutoff + 1;
+            red[tid] = (float)first;  // exact: indices < 2^24
+            __syncthreads();
+            for (int st = kTailThreads / 2; st > 0; st >>= 1) {
+                if (tid < st) red[tid] = fminf(red[tid], red[tid + st]);
+                __syncthreads();
+            }
+            if ((int)red[0] < cnt) kept = t0 + (int)red[0];
+            __syncthreads();
         }
-        __syncthreads();
-        n = n_sh;
-        __syncthreads();
-    }
-    if (p.min_p > 0.0f && p.min_p < 1.0f && n > 1) {  // apply_min_p (:166-194)
-        prefix_exps(n);
-        if (tid == 0) {
-            float sum = 0.0f;
-            for (int64_t i = 0; i < n; i++) sum += ex[i];
-            const float p0 = sum > 0.0f ? ex[0] / sum : ex[0];
-            const float threshold = p.min_p * p0;
-            int64_t kept = 0;
-            while (kept < n && (sum > 0.0f ? ex[kept] / sum : ex[kept]) >= threshold) kept++;
-            n_sh = kept > 0 ? kept : n;
-        }
-        __syncthreads();
-        n = n_sh;
-        __syncthreads();
+        n = kept > 0 ? kept : n;
     }
 
     // final draw (:284-305): max over the candidates, exps, sequential sum, inverse CDF
@@ -197,29 +287,23 @@ __global__ __launch_bounds__(kTailThreads) void sampler_tail_kernel(const float 
         __syncthreads();
     }
     mx = red[0];
-    for (int64_t i = tid; i < n; i += kTailThreads) ex[i] = exp_f32(val(i) - mx);
     __syncthreads();
-    if (tid != 0) return;
-    float sum_e = 0.0f;
-    for (int64_t i = 0; i < n; i++) sum_e += ex[i];
+    const float sum_e = seq_sum(n, mx);
     const int64_t first = order ? order[0] : 0;
     if (!(sum_e > 0.0f)) {
-        out[0] = first;
-        out[1] = 0;
+        if (tid == 0) {
+            out[0] = first;
+            out[1] = 0;
+        }
         return;
     }
     const float r = p.u * sum_e;
-    float acc = 0.0f;
-    int64_t pick = n - 1;
-    for (int64_t i = 0; i < n; i++) {
-        acc += ex[i];
-        if (r <= acc) {
-            pick = i;
-            break;
-        }
+    int64_t pick = seq_reach(n, mx, r, [](float e) { return e; });
+    if (pick >= n) pick = n - 1;
+    if (tid == 0) {
+        out[0] = order ? order[pick] : pick;
+        out[1] = 1;
     }
-    out[0] = order ? order[pick] : pick;
-    out[1] = 1;
 }
 
 // Device workspace of the sampler, grown on demand (never inside a captured graph).
@@ -227,7 +311,7 @@ struct SamplerWork {
     int64_t cap_v = 0, cap_ctx = 0;
     int32_t *counts = nullptr;
     uint8_t *mask = nullptr;
-    float *vals = nullptr, *ex = nullptr;
+    float *vals = nullptr;
     uint32_t *keys = nullptr, *keys_out = nullptr;
     int32_t *idx = nullptr, *idx_out = nullptr;
     int64_t *lists = nullptr;  // context tokens then suppress ids
@@ -237,7 +321,7 @@ struct SamplerWork {
 };
 
 static void free_work(SamplerWork *w) {
-    void *ps[] = {w->counts, w->mask, w->vals, w->ex, w->keys, w->keys_out, w->idx, w->idx_out, w->lists,
+    void *ps[] = {w->counts, w->mask, w->vals, w->keys, w->keys_out, w->idx, w->idx_out, w->lists,
                   w->result, w->sort_tmp};
     for (void *p : ps)
         if (p) (void)hipFree(p);
@@ -267,7 +351,6 @@ static int32_t ensure_work(aesir_ctx *ctx, int64_t V, int64_t n_lists) {
         AESIR_HIP_TRY(hipMalloc((void **)&w->counts, (size_t)V * 4));
         AESIR_HIP_TRY(hipMalloc((void **)&w->mask, (size_t)V));
         AESIR_HIP_TRY(hipMalloc((void **)&w->vals, (size_t)V * 4));
-        AESIR_HIP_TRY(hipMalloc((void **)&w->ex, (size_t)V * 4));
         AESIR_HIP_TRY(hipMalloc((void **)&w->keys, (size_t)V * 4));
         AESIR_HIP_TRY(hipMalloc((void **)&w->keys_out, (size_t)V * 4));
         AESIR_HIP_TRY(hipMalloc((void **)&w->idx, (size_t)V * 4));
@@ -325,6 +408,16 @@ int32_t aesir_sample_token(aesir_ctx *ctx, const void *logits, int64_t vocab, co
     AESIR_TRY(ensure_work(ctx, vocab, n_lists));
     SamplerWork *w = ctx->sampler;
     hipStream_t s = ctx->stream;
+    const bool greedy = cfg->temperature <= 0.0f || cfg->top_k == 1;  // sampler.mojo:235
+    if (greedy && n_suppress == 0) {  // the greedy branch reads no penalty state: argmax of the logits
+        hipLaunchKernelGGL(sampler_greedy_kernel, dim3(1), dim3(1024), 0, s, (const h16 *)logits, vocab,
+                           (const uint8_t *)nullptr, w->result);
+        AESIR_LAUNCH_CHECK("sampler_greedy_kernel");
+        AESIR_HIP_TRY(hipMemcpyAsync(ctx->pinned_i64, w->result, 16, hipMemcpyDeviceToHost, s));
+        AESIR_HIP_TRY(hipStreamSynchronize(s));
+        *token = ctx->pinned_i64[0];
+        return AESIR_OK;
+    }
     if (n_context > 0)
         AESIR_HIP_TRY(hipMemcpyAsync(w->lists, context, (size_t)n_context * 8, hipMemcpyHostToDevice, s));
     if (n_suppress > 0)
@@ -339,7 +432,6 @@ int32_t aesir_sample_token(aesir_ctx *ctx, const void *logits, int64_t vocab, co
         AESIR_LAUNCH_CHECK("sampler_mark_kernel");
     }
     uint64_t st = *rng_state;
-    const bool greedy = cfg->temperature <= 0.0f || cfg->top_k == 1;  // sampler.mojo:235
     if (greedy) {
         hipLaunchKernelGGL(sampler_greedy_kernel, dim3(1), dim3(1024), 0, s, (const h16 *)logits, vocab, w->mask,
                            w->result);
@@ -371,7 +463,7 @@ int32_t aesir_sample_token(aesir_ctx *ctx, const void *logits, int64_t vocab, co
                                                     (unsigned)vocab, 0, 32, s));
         }
         hipLaunchKernelGGL(sampler_tail_kernel, dim3(1), dim3(kTailThreads), 0, s, w->vals,
-                           p.sort ? (const int32_t *)w->idx_out : nullptr, vocab, p, w->ex, w->result);
+                           p.sort ? (const int32_t *)w->idx_out : nullptr, vocab, p, w->result);
         AESIR_LAUNCH_CHECK("sampler_tail_kernel");
         st = peek;
     }

@@ -471,11 +471,10 @@ __global__ __launch_bounds__(kFinishThreads) void argmax_finish_kernel(const Arg
 // ------------------------------------------------------------------ Q8_0 weights
 //
 // Q8_0 matrices are repacked in HBM as int8 quants [N][K] (rows 32-byte aligned) plus f16 block
-// scales [N][K / 32]. Thread t multiplies k = 16t + 4096i: one 16-byte quant load (half a block)
-// and one 2-byte scale per row and slab, so a wave streams contiguous 1 KiB of quants per row.
+// scales [N][K / 32]. Per row and slab a thread makes one 16- or 8-byte quant load and one 2-byte
+// scale load, so a wave streams contiguous 1 KiB or 512 B of quants per row.
 // Dequantization (dequant_q8x4) reproduces gemm_q8_0 (compute.mojo:1038-1065) exactly:
 // w = f16(f16(q) * d); the dot product is v_dot2_f32_f16.
-constexpr int kQSlab = kThreads * 16;  // k elements covered by one pass of the workgroup
 // Rows per group of the Q8_0 decode GEMVs, and row groups per workgroup. Measured on MI355X
 // (Llama-3-8B shapes, us per launch): 4 rows beat 8 and 16 on every GEMV; 2 groups per workgroup
 // take gate/up from 24.2 to 23.2 but slow the 4096-row GEMVs (QKV 7.7 -> 9.1, O 5.7 -> 6.2), and
@@ -503,60 +502,90 @@ struct Q8XSrc {
     h16 *xcopy;
 };
 
-// The Q8_0 twin of gemv_fixed_kernel (NS = ceil(K / 4096) slabs, K % 32 == 0): x chunks stay in
-// registers, optionally RMS-normalized once per workgroup. A workgroup owns G consecutive groups
-// of ROWS rows; the weight requests run one (group, slab) step ahead of the dot products through a
-// register double buffer, so the next group's rows are in flight during a group's reduction and
-// epilogue, and x is loaded and normalized once for G groups.
-template <int ROWS, int NS, int G, bool NORM, class Epi>
+// The Q8_0 twin of gemv_fixed_kernel (K % 32 == 0): thread t multiplies QW quants per row and
+// slab (k = QW t + 256 QW i, NS slabs; QW = 16 loads half a block per row, QW = 8 a quarter, so
+// K = 2048 or 14336 need no idle lanes). x chunks stay in registers, optionally RMS-normalized
+// once per workgroup. A workgroup owns G consecutive groups of ROWS rows; the weight requests run
+// D (group, slab) steps ahead of the dot products through a register ring, so the next group's
+// rows are in flight during a group's reduction and epilogue, and x is loaded and normalized once
+// for G groups.
+template <int QW>
+struct QVec;  // QW quants of one row
+template <>
+struct QVec<16> {
+    u32x4 v;
+    __device__ __forceinline__ static QVec load(const int8_t *p) { return QVec{ld16_stream(p)}; }
+};
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+template <>
+struct QVec<8> {
+    u32x2 v;
+    __device__ __forceinline__ static QVec load(const int8_t *p) {
+        return QVec{__builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(p))};
+    }
+};
+// f16(q * d) of the QW quants as QW / 8 chunks of 8 f16
+__device__ __forceinline__ void deq(const QVec<16> &q, h16 d, u32x4 (&o)[2]) { deq16(q.v, d, o[0], o[1]); }
+__device__ __forceinline__ void deq(const QVec<8> &q, h16 d, u32x4 (&o)[1]) {
+    unsigned w[4];
+    dequant_q8x4(q.v.x, d, w[0], w[1]);
+    dequant_q8x4(q.v.y, d, w[2], w[3]);
+    o[0] = u32x4{w[0], w[1], w[2], w[3]};
+}
+
+template <int ROWS, int NS, int G, int QW, bool NORM, class Epi>
 __global__ __launch_bounds__(kThreads) void gemv_q8_kernel(const int8_t *__restrict__ Wq, const h16 *__restrict__ Wd,
                                                            int64_t N, int64_t K, Q8XSrc src,
                                                            const h16 *__restrict__ nw, float eps, Epi epi) {
+    constexpr int XC = QW / 8;                  // 8-element x chunks per slab
+    constexpr int64_t SLAB = (int64_t)kThreads * QW;
     __shared__ float red[4 * ROWS];
     __shared__ float sums[ROWS];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t nbase = (int64_t)blockIdx.x * G * ROWS;
-    const int64_t k0 = (int64_t)tid * 16;
+    const int64_t k0 = (int64_t)tid * QW;
     const int64_t KB = K / 32;
     auto row = [&](int g, int r) -> int64_t {
         const int64_t n = nbase + (int64_t)g * ROWS + r;
         return n < N ? n : N - 1;
     };
-    u32x4 xr[NS][2], nr[NS][2];
+    u32x4 xr[NS][XC], nr[NS][XC];
     bool live[NS];
+    QVec<QW> eqv[NS];
+    h16 edv[NS];
     const bool embed = src.eq != nullptr;
     const int64_t trow = embed ? src.token->token : 0;
 #pragma unroll
     for (int i = 0; i < NS; i++) {
-        const int64_t k = k0 + (int64_t)i * kQSlab;
-        live[i] = k < K;  // false in a partial slab (and for every thread beyond K when K < 4096)
+        const int64_t k = k0 + (int64_t)i * SLAB;
+        live[i] = k < K;  // false in a partial slab (and for every thread beyond K when K < SLAB)
         const int64_t kc = live[i] ? k : 0;
-        if (embed) {
-            xr[i][0] = ld16(src.eq + trow * K + kc);  // quants; dequantized below
-            xr[i][1].x = h_to_bits(src.ed[trow * KB + kc / 32]);
+        if (embed) {  // quants and scale of the embedding row; dequantized below
+            eqv[i] = QVec<QW>::load(src.eq + trow * K + kc);
+            edv[i] = src.ed[trow * KB + kc / 32];
         } else {
-            xr[i][0] = ld16(src.x + kc);
-            xr[i][1] = ld16(src.x + kc + 8);
+#pragma unroll
+            for (int c = 0; c < XC; c++) xr[i][c] = ld16(src.x + kc + 8 * c);
         }
         if (NORM) {
-            nr[i][0] = ld16(nw + kc);
-            nr[i][1] = ld16(nw + kc + 8);
+#pragma unroll
+            for (int c = 0; c < XC; c++) nr[i][c] = ld16(nw + kc + 8 * c);
         }
     }
     __builtin_amdgcn_sched_barrier(0);
     const int64_t kf = k0 < K ? k0 : 0;
     // step st = (group st / NS, slab st % NS); D steps in flight through a register ring
     constexpr int T = G * NS, D = T < kGemvDepth ? T : kGemvDepth;
-    u32x4 qb[D][ROWS];
+    QVec<QW> qb[D][ROWS];
     h16 db[D][ROWS];
     auto request = [&](int st) {
         const int g = st / NS, i = st % NS;
-        const int64_t k = k0 + (int64_t)i * kQSlab;
+        const int64_t k = k0 + (int64_t)i * SLAB;
         const int64_t kc = k < K ? k : kf;  // dead lanes of a partial slab re-read their first chunk
 #pragma unroll
         for (int r = 0; r < ROWS; r++) {
             const int64_t n = row(g, r);
-            qb[st % D][r] = ld16_stream(Wq + n * K + kc);
+            qb[st % D][r] = QVec<QW>::load(Wq + n * K + kc);
             db[st % D][r] = Wd[n * KB + kc / 32];
         }
     };
@@ -573,22 +602,21 @@ __global__ __launch_bounds__(kThreads) void gemv_q8_kernel(const int8_t *__restr
     h16 *xcopy = (src.xcopy && blockIdx.x == 0) ? src.xcopy : nullptr;
 #pragma unroll
     for (int i = 0; i < NS; i++) {
-        if (embed) deq16(xr[i][0], bits_to_h((uint16_t)xr[i][1].x), xr[i][0], xr[i][1]);
-        if (!live[i]) xr[i][0] = xr[i][1] = u32x4{0u, 0u, 0u, 0u};
-        if (xcopy && live[i]) {
-            st16(xcopy + k0 + (int64_t)i * kQSlab, xr[i][0]);
-            st16(xcopy + k0 + (int64_t)i * kQSlab + 8, xr[i][1]);
+        if (embed) deq(eqv[i], edv[i], xr[i]);
+#pragma unroll
+        for (int c = 0; c < XC; c++) {
+            if (!live[i]) xr[i][c] = u32x4{0u, 0u, 0u, 0u};
+            if (xcopy && live[i]) st16(xcopy + k0 + (int64_t)i * SLAB + 8 * c, xr[i][c]);
+            if (NORM) ss = sumsq8(xr[i][c], ss);
         }
-        if (NORM) ss = sumsq8(xr[i][1], sumsq8(xr[i][0], ss));
     }
     if (NORM) {
         ss = block_sum<kThreads / kWave>(ss, red);
         const h16 inv = (h16)(1.0f / sqrtf(ss / (float)K + eps));
 #pragma unroll
-        for (int i = 0; i < NS; i++) {
-            xr[i][0] = norm8(xr[i][0], nr[i][0], inv);
-            xr[i][1] = norm8(xr[i][1], nr[i][1], inv);
-        }
+        for (int i = 0; i < NS; i++)
+#pragma unroll
+            for (int c = 0; c < XC; c++) xr[i][c] = norm8(xr[i][c], nr[i][c], inv);
     }
 #pragma unroll
     for (int g = 0; g < G; g++) {
@@ -600,9 +628,10 @@ __global__ __launch_bounds__(kThreads) void gemv_q8_kernel(const int8_t *__restr
             const int st = g * NS + i;
 #pragma unroll
             for (int r = 0; r < ROWS; r++) {
-                u32x4 w0, w1;
-                deq16(qb[st % D][r], db[st % D][r], w0, w1);
-                acc[r] = dot8(w1, xr[i][1], dot8(w0, xr[i][0], acc[r]));
+                u32x4 w[XC];
+                deq(qb[st % D][r], db[st % D][r], w);
+#pragma unroll
+                for (int c = 0; c < XC; c++) acc[r] = dot8(w[c], xr[i][c], acc[r]);
             }
             if (st + D < T) {
                 request(st + D);
@@ -627,23 +656,42 @@ static int32_t gemv_q8_dispatch(hipStream_t s, const void *Wq, const void *Wd, i
     if (K % 32 != 0 || ((uintptr_t)Wq & 15) || ((uintptr_t)xp & 15) || (NORM && ((uintptr_t)nw & 15)) ||
         (src.xcopy && ((uintptr_t)src.xcopy & 15)))
         return fail(AESIR_ERR_UNSUPPORTED, "%s: Q8_0 GEMV needs K %% 32 == 0 and 16-byte aligned rows", name);
-    const int64_t ns = (K + kQSlab - 1) / kQSlab;
     const dim3 grid((unsigned)((N + ROWS * G - 1) / (ROWS * G)));
     if (grid.x == 0) return AESIR_OK;
-    switch (ns) {
-#define AESIR_GEMV_Q8(NSV)                                                                                        \
-    case NSV:                                                                                                    \
-        hipLaunchKernelGGL((gemv_q8_kernel<ROWS, NSV, G, NORM, Epi>), grid, dim3(kThreads), 0, s,                 \
-                           (const int8_t *)Wq, (const h16 *)Wd, N, K, src, (const h16 *)nw, eps, epi);            \
+    // 8 quants per thread below K = 4096 (a 4096-wide slab would leave half the lanes idle at K =
+    // 2048), else 16. Measured on MI355X: TinyLlama Q8_0 decode 1316 -> 1399 tok/s with 8; at
+    // K = 14336 8-quant slabs (7 whole ones) lose to 16-quant ones (3.5): 17.4 against 14.2 us.
+    const bool qw8 = K < 4096;
+    const int64_t ns = qw8 ? (K + 2047) / 2048 : (K + 4095) / 4096;
+#define AESIR_GEMV_Q8(QWV, NSV)                                                                            \
+    case NSV:                                                                                             \
+        hipLaunchKernelGGL((gemv_q8_kernel<ROWS, NSV, G, QWV, NORM, Epi>), grid, dim3(kThreads), 0, s,    \
+                           (const int8_t *)Wq, (const h16 *)Wd, N, K, src, (const h16 *)nw, eps, epi);    \
         break;
-        AESIR_GEMV_Q8(1)
-        AESIR_GEMV_Q8(2)
-        AESIR_GEMV_Q8(3)
-        AESIR_GEMV_Q8(4)
-#undef AESIR_GEMV_Q8
-        default:
-            return fail(AESIR_ERR_UNSUPPORTED, "%s: Q8_0 GEMV with K = %lld exceeds 16384", name, (long long)K);
+    if (qw8) {
+        switch (ns) {
+            AESIR_GEMV_Q8(8, 1)
+            AESIR_GEMV_Q8(8, 2)
+            AESIR_GEMV_Q8(8, 3)
+            AESIR_GEMV_Q8(8, 4)
+            AESIR_GEMV_Q8(8, 5)
+            AESIR_GEMV_Q8(8, 6)
+            AESIR_GEMV_Q8(8, 7)
+            AESIR_GEMV_Q8(8, 8)
+            default:
+                return fail(AESIR_ERR_UNSUPPORTED, "%s: Q8_0 GEMV with K = %lld exceeds 16384", name, (long long)K);
+        }
+    } else {
+        switch (ns) {
+            AESIR_GEMV_Q8(16, 1)
+            AESIR_GEMV_Q8(16, 2)
+            AESIR_GEMV_Q8(16, 3)
+            AESIR_GEMV_Q8(16, 4)
+            default:
+                return fail(AESIR_ERR_UNSUPPORTED, "%s: Q8_0 GEMV with K = %lld exceeds 16384", name, (long long)K);
+        }
     }
+#undef AESIR_GEMV_Q8
     AESIR_LAUNCH_CHECK(name);
     return AESIR_OK;
 }

@@ -206,6 +206,37 @@ def test_tinyllama_shape_two_layers(A, ctx, oracle):
 
 
 @pytest.mark.timeout(300)
+@pytest.mark.parametrize("shape", ["tinyllama", "llama3"])
+def test_long_prompt_decode_shapes(A, ctx, oracle, shape):
+    """Decode at head_dim 64 and 128 over 150 positions, so attention runs with 1, 2 and 3 splits
+    of 64 positions (the split merge and its single-split shortcut). Logits within tolerance and
+    identical argmax at every position, then graph-replayed decode steps."""
+    if shape == "tinyllama":
+        cfg = oracle.Config(dim=2048, n_layers=2, n_heads=32, n_kv_heads=4, ffn=5632, vocab=32000, ctx_len=256)
+    else:
+        cfg = oracle.Config(dim=4096, n_layers=1, n_heads=32, n_kv_heads=8, ffn=14336, vocab=4096, ctx_len=256,
+                            theta=500000.0)
+    w = oracle.synthetic_weights(cfg, 33)
+    om = oracle.Model(cfg, w)
+    m = gpu_model(A, ctx, cfg, w)
+    toks = oracle.prompt_tokens(150, cfg.vocab, 5)
+    okv = om.new_kv()
+    for p in range(len(toks)):
+        want, ol = om.forward(okv, toks, p)
+        got = m.forward_pass(toks, p)
+        assert got == want, p
+        if p in (0, 63, 64, 65, 127, 128, 149):
+            assert within_tol(m.logits(), ol), p
+    cur = list(toks) + [got]
+    g, _ = m.decode_loop(got, len(toks), 4, use_graph=True)
+    for t in g:
+        want, _ = om.forward(okv, cur, len(cur) - 1)
+        assert t == want
+        cur.append(t)
+    m.close()
+
+
+@pytest.mark.timeout(300)
 def test_llama3_8b_shape_properties(A, oracle):
     """Config 4 at full size on the device (random init, ~15 GB): graph == eager == forward_pass."""
     cfg = oracle.LLAMA3_8B

@@ -353,8 +353,7 @@ __global__ __launch_bounds__(kAThreads) void attn_fast_kernel(AttnArgs a) {
             for (int h = 0; h < GH; h++) {
                 float d = dot8(kr[i][0], qr[h][0], 0.0f);
                 d = dot8(kr[i][1], qr[h][1], d);
-#pragma unroll
-                for (int o = 1; o < TPP; o <<= 1) d += __shfl_xor(d, o, kWave);
+                d = group_sum<TPP>(d);
                 if (sc_c == 0) sc[h][sp + i * RPP] = d * a.scale;
             }
         }

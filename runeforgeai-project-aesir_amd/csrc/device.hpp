@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 namespace aesir {
 
@@ -69,40 +70,115 @@ __device__ __forceinline__ float dot8(u32x4 a, u32x4 b, float acc) {
 }
 
 // ------------------------------------------------------------------ reductions
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+// Cross-lane steps without LDS: DPP row patterns for partners within a 16-lane row, and gfx950's
+// v_permlane16_swap / v_permlane32_swap for partners 16 and 32 lanes away. Every step combines a
+// lane with a partner whose position in the reduction tree is symmetric (x ^ 1, x ^ 2, 7 - x in
+// each 8-lane half, 15 - x in each row, x ^ 16, x ^ 32), so after the steps of a group every lane
+// of the group holds the same value. The patterns read every lane of the group: call them with
+// the whole wave active.
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // 7 - x within each 8-lane half row
+constexpr int kDppMirror = 0x140;     // 15 - x within each 16-lane row
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+
+// (value of a in the lower lane of each pair, value of b in the upper lane), for lane pairs
+// (x, x + 16) in every 32 lanes (D = 16) or (x, x + 32) (D = 32); the sum of the two results is
+// a(lower) + a(upper) in lower lanes and b(lower) + b(upper) in upper lanes.
+template <int D>
+__device__ __forceinline__ float swap_pair_sum(float a, float b) {
+    const unsigned ua = __builtin_bit_cast(unsigned, a), ub = __builtin_bit_cast(unsigned, b);
+    if constexpr (D == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(ua, ub, false, false);
+        return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(ua, ub, false, false);
+        return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+    }
+}
+template <int D>
+__device__ __forceinline__ float swap_pair_max(float v) {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    if constexpr (D == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        return fmaxf(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        return fmaxf(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
+    }
+}
+
+// Sum / max over aligned groups of L lanes (L = 1, 2, 4, ..., 64); every lane of a group gets it.
+template <int L>
+__device__ __forceinline__ float group_sum(float v) {
+    if constexpr (L >= 2) v += dpp_f<kDppXor1>(v);
+    if constexpr (L >= 4) v += dpp_f<kDppXor2>(v);
+    if constexpr (L >= 8) v += dpp_f<kDppHalfMirror>(v);
+    if constexpr (L >= 16) v += dpp_f<kDppMirror>(v);
+    if constexpr (L >= 32) v = swap_pair_sum<16>(v, v);
+    if constexpr (L >= 64) v = swap_pair_sum<32>(v, v);
     return v;
 }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+template <int L>
+__device__ __forceinline__ float group_max(float v) {
+    if constexpr (L >= 2) v = fmaxf(v, dpp_f<kDppXor1>(v));
+    if constexpr (L >= 4) v = fmaxf(v, dpp_f<kDppXor2>(v));
+    if constexpr (L >= 8) v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+    if constexpr (L >= 16) v = fmaxf(v, dpp_f<kDppMirror>(v));
+    if constexpr (L >= 32) v = swap_pair_max<16>(v);
+    if constexpr (L >= 64) v = swap_pair_max<32>(v);
     return v;
 }
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<kWave>(v); }
+__device__ __forceinline__ float wave_max(float v) { return group_max<kWave>(v); }
 
 // Reduces R per-lane partial sums across the wave by recursive halving: after the call, every
 // lane holds the full wave sum of row (lane / (64 / R)) in v[0]. R is a power of two <= 64.
+// Halving steps pair lanes 32 apart, then 16, 8 (15 - x), 4 (7 - x), 2, 1; at each step the
+// lane whose partner bit is set keeps the upper half of its live rows.
 template <int R>
 __device__ __forceinline__ float wave_multi_sum(float (&v)[R], int lane) {
     int live = R;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
+    auto halve_swap = [&](auto dist) {
+        constexpr int D = decltype(dist)::value;
         if (live > 1) {
             const int half = live >> 1;
-            const bool upper = (lane & o) != 0;
+#pragma unroll
+            for (int r = 0; r < R / 2; r++)
+                if (r < half) v[r] = swap_pair_sum<D>(v[r], v[r + half]);
+            live = half;
+        } else {
+            v[0] = swap_pair_sum<D>(v[0], v[0]);
+        }
+    };
+    halve_swap(std::integral_constant<int, 32>{});
+    halve_swap(std::integral_constant<int, 16>{});
+    auto halve_dpp = [&](auto ctrl, int bit) {
+        constexpr int C = decltype(ctrl)::value;
+        if (live > 1) {
+            const int half = live >> 1;
+            const bool upper = (lane & bit) != 0;
 #pragma unroll
             for (int r = 0; r < R / 2; r++) {
                 if (r < half) {
-                    float keep = upper ? v[r + half] : v[r];
-                    float give = upper ? v[r] : v[r + half];
-                    v[r] = keep + __shfl_xor(give, o, kWave);
+                    const float keep = upper ? v[r + half] : v[r];
+                    const float give = upper ? v[r] : v[r + half];
+                    v[r] = keep + dpp_f<C>(give);
                 }
             }
             live = half;
         } else {
-            v[0] += __shfl_xor(v[0], o, kWave);
+            v[0] += dpp_f<C>(v[0]);
         }
-    }
+    };
+    halve_dpp(std::integral_constant<int, kDppMirror>{}, 8);
+    halve_dpp(std::integral_constant<int, kDppHalfMirror>{}, 4);
+    halve_dpp(std::integral_constant<int, kDppXor2>{}, 2);
+    halve_dpp(std::integral_constant<int, kDppXor1>{}, 1);
     return v[0];
 }
 

@@ -233,7 +233,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(const h16 *__re
             const int64_t m = m0 + 16 * i + 4 * g + e;
             const float v = acc[i][e];
             if (splits == 1) {
-                const float partner = __shfl_xor(v, 1, kWave);  // lane r ^ 1 holds column n ^ 1
+                const float partner = dpp_f<kDppXor1>(v);  // lane r ^ 1 holds column n ^ 1
                 gemm_epilogue<EPI>(C, ldc, M, N, m, n, v, partner);
             } else if (m < M && n < N) {
                 P[(z * M + m) * N + n] = v;
@@ -252,7 +252,7 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const float *__restric
     const int64_t oc = o < total ? o : total - 1;  // tail threads repeat the last output, store nothing
     float v = 0.0f;
     for (int64_t z = 0; z < splits; z++) v += P[z * total + oc];
-    const float partner = __shfl_xor(v, 1, kWave);  // N even for SwiGLU: o ^ 1 is column n ^ 1
+    const float partner = dpp_f<kDppXor1>(v);  // N even for SwiGLU: o ^ 1 is column n ^ 1
     if (o < total) gemm_epilogue<EPI>(C, ldc, M, N, oc / N, oc % N, v, partner);
 }
 
@@ -581,8 +581,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_attention_tile_kernel(
             sc[j] = row < n ? d * scale : -INFINITY;
             mt = fmaxf(mt, sc[j]);
         }
-#pragma unroll
-        for (int o = TPH / 2; o > 0; o >>= 1) mt = fmaxf(mt, __shfl_xor(mt, o, kWave));
+        mt = group_max<TPH>(mt);
         const float mn = fmaxf(m, mt);
         float lt = 0.0f;
 #pragma unroll
@@ -591,8 +590,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_attention_tile_kernel(
             ps[h][u + j * TPH] = pr;
             lt += pr;
         }
-#pragma unroll
-        for (int o = TPH / 2; o > 0; o >>= 1) lt += __shfl_xor(lt, o, kWave);
+        lt = group_sum<TPH>(lt);
         const float al = expf(m - mn);  // 0 on the first tile
         l = l * al + lt;
         m = mn;

@@ -400,10 +400,25 @@ __global__ __launch_bounds__(kAThreads) void attn_fast_kernel(AttnArgs a) {
 #pragma unroll
             for (int i = 0; i < NVL; i++) vr[i] = vn[i];
         }
-        __syncthreads();  // sc and vs are rewritten by the next round
+        if (more) __syncthreads();  // sc and vs are rewritten by the next round
     }
 
-    // combine the PV position groups, then write the partial (or the output for one split)
+    // Write the partial (or the output for one split). With one PV position group and one head
+    // per wave (head_dim 128, 4 heads per workgroup), thread t's head is its wave's, whose
+    // running max and sum are already in its registers.
+    if constexpr (PVS == 1 && HD / 2 == kWave && GH == kAThreads / kWave) {
+        if (nsplit == 1) {
+            h16 *out = reinterpret_cast<h16 *>(a.out) + (head0 + ph) * HD + pd;
+            out[0] = (h16)(acc0 / l_w);
+            out[1] = (h16)(acc1 / l_w);
+        } else {
+            float *pp = a.part + ((head0 + ph) * a.max_split + split) * (HD + 2);
+            *reinterpret_cast<float2 *>(pp + 2 + pd) = float2{acc0, acc1};
+            if (pd == 0) *reinterpret_cast<float2 *>(pp) = float2{m_w, l_w};
+        }
+        return;
+    }
+    // otherwise combine the PV position groups through LDS first
     if (wave < GH && lane == 0) {
         mrun[wave] = m_w;
         lrun[wave] = l_w;
@@ -430,15 +445,16 @@ __global__ __launch_bounds__(kAThreads) void attn_fast_kernel(AttnArgs a) {
 
 // Merge of the split partials, one workgroup per query head: w_s = exp(m_s - max m),
 // out = f16(sum_s w_s acc_s / sum_s w_s l_s). Thread t owns dim pair t % (HD/2) over the splits
-// s = t / (HD/2) (mod NG); its first accumulator loads are issued before the weights are known.
+// s = t / (HD/2) (mod NG). The (m, l) pair of split t and the accumulators of the first 64
+// splits (the decode step's maximum) are requested together, so a merge costs one round trip.
 template <int HD>
 __global__ __launch_bounds__(kAThreads) void attn_fast_merge_kernel(AttnArgs a) {
     constexpr int NDP = HD / 2;
     constexpr int NG = kAThreads / NDP;
-    constexpr int kPre = 8;
+    constexpr int kPre = 64 / NG;
     constexpr int kW = kAThreads / kWave;
     __shared__ float wsh[kMaxFastSplit];
-    __shared__ float red[kW];
+    __shared__ float redm[kW], reds[kW];
     __shared__ float2 gx[NG][NDP];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t S = decode_seq_len(a);
@@ -449,6 +465,8 @@ __global__ __launch_bounds__(kAThreads) void attn_fast_merge_kernel(AttnArgs a) 
     const float *base = a.part + h * a.max_split * (HD + 2);
     const int dp = tid % NDP, sg = tid / NDP;
 
+    const float2 ml = tid < nsplit ? *reinterpret_cast<const float2 *>(base + (int64_t)tid * (HD + 2))
+                                   : float2{-INFINITY, 0.0f};
     float2 pre[kPre];
 #pragma unroll
     for (int j = 0; j < kPre; j++) {
@@ -456,23 +474,32 @@ __global__ __launch_bounds__(kAThreads) void attn_fast_merge_kernel(AttnArgs a) 
         pre[j] = s < nsplit ? *reinterpret_cast<const float2 *>(base + (int64_t)s * (HD + 2) + 2 + 2 * dp)
                             : float2{0.0f, 0.0f};
     }
-    float mloc = -INFINITY;
-    for (int s = tid; s < nsplit; s += kAThreads) mloc = fmaxf(mloc, base[(int64_t)s * (HD + 2)]);
+    float mloc = ml.x;
+    for (int s = tid + kAThreads; s < nsplit; s += kAThreads) mloc = fmaxf(mloc, base[(int64_t)s * (HD + 2)]);
     mloc = wave_max(mloc);
-    if (lane == 0) red[wave] = mloc;
+    if (lane == 0) redm[wave] = mloc;
     __syncthreads();
-    float M = red[0];
+    float M = redm[0];
 #pragma unroll
-    for (int w = 1; w < kW; w++) M = fmaxf(M, red[w]);
-    __syncthreads();
+    for (int w = 1; w < kW; w++) M = fmaxf(M, redm[w]);
     float lsum = 0.0f;
-    for (int s = tid; s < nsplit; s += kAThreads) {
-        const float2 ml = *reinterpret_cast<const float2 *>(base + (int64_t)s * (HD + 2));
+    if (tid < nsplit) {
         const float e = expf(ml.x - M);
-        wsh[s] = e;
-        lsum = fmaf(ml.y, e, lsum);
+        wsh[tid] = e;
+        lsum = ml.y * e;
     }
-    const float L = block_sum<kW>(lsum, red);  // also publishes wsh
+    for (int s = tid + kAThreads; s < nsplit; s += kAThreads) {
+        const float2 m2 = *reinterpret_cast<const float2 *>(base + (int64_t)s * (HD + 2));
+        const float e = expf(m2.x - M);
+        wsh[s] = e;
+        lsum = fmaf(m2.y, e, lsum);
+    }
+    lsum = wave_sum(lsum);
+    if (lane == 0) reds[wave] = lsum;
+    __syncthreads();  // also publishes wsh
+    float L = reds[0];
+#pragma unroll
+    for (int w = 1; w < kW; w++) L += reds[w];
     float x0 = 0.0f, x1 = 0.0f;
 #pragma unroll
     for (int j = 0; j < kPre; j++) {
@@ -482,7 +509,7 @@ __global__ __launch_bounds__(kAThreads) void attn_fast_merge_kernel(AttnArgs a) 
             x1 = fmaf(pre[j].y, wsh[s], x1);
         }
     }
-    for (int s0 = sg + NG * kPre; s0 < nsplit; s0 += NG * kPre) {  // kPre loads in flight per batch
+    for (int s0 = sg + NG * kPre; s0 < nsplit; s0 += NG * kPre) {  // more than 64 splits: kPre loads per batch
         float2 v[kPre];
 #pragma unroll
         for (int j = 0; j < kPre; j++) {

@@ -183,7 +183,9 @@ __device__ __forceinline__ float wave_multi_sum(float (&v)[R], int lane) {
 }
 
 // Workgroup-wide sum for blockDim.x == 64 * NW; `red` is shared scratch of >= NW floats.
-template <int NW>
+// REUSE = false: the caller never writes `red` again, so the barrier that would protect it from
+// the next use is left out.
+template <int NW, bool REUSE = true>
 __device__ __forceinline__ float block_sum(float v, float *red) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     v = wave_sum(v);
@@ -192,7 +194,7 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
     float s = 0.0f;
 #pragma unroll
     for (int w = 0; w < NW; w++) s += red[w];
-    __syncthreads();
+    if (REUSE) __syncthreads();
     return s;
 }
 

@@ -18,6 +18,16 @@ namespace aesir {
 constexpr int kThreads = 256;
 constexpr int kSlab = kThreads * 8;  // k elements covered by one pass of the workgroup
 
+// Row sums of a ROWS-row workgroup: red[w * ROWS + r] holds wave w's sum of row r; each
+// epilogue thread adds up the rows it needs (same order for every reader).
+template <int ROWS>
+struct RowSums {
+    const float *red;
+    __device__ __forceinline__ float operator[](int r) const {
+        return (red[r] + red[ROWS + r]) + (red[2 * ROWS + r] + red[3 * ROWS + r]);
+    }
+};
+
 __device__ __forceinline__ u32x4 gather8(const h16 *p, int64_t k, int64_t K) {
     uint16_t t[8];
 #pragma unroll
@@ -141,7 +151,6 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const h16 *__restrict__ 
     extern __shared__ __align__(16) unsigned char smem_raw[];
     h16 *xs = reinterpret_cast<h16 *>(smem_raw);
     __shared__ float red[4 * ROWS];
-    __shared__ float sums[ROWS];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t n0 = (int64_t)blockIdx.x * ROWS;
     const int64_t m = blockIdx.y;
@@ -200,9 +209,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const h16 *__restrict__ 
     constexpr int G = kWave / ROWS;
     if ((lane & (G - 1)) == 0) red[wave * ROWS + lane / G] = acc[0];
     __syncthreads();
-    if (tid < ROWS) sums[tid] = (red[tid] + red[ROWS + tid]) + (red[2 * ROWS + tid] + red[3 * ROWS + tid]);
-    __syncthreads();
-    epi.template apply<ROWS>(n0, m, N, sums, tid, pre);
+    epi.template apply<ROWS>(n0, m, N, RowSums<ROWS>{red}, tid, pre);
 }
 
 // Fixed-shape fast path (K % 8 == 0, 16-byte aligned, NS = ceil(K / 2048) slabs known at
@@ -221,7 +228,7 @@ __global__ __launch_bounds__(kThreads) void gemv_fixed_kernel(const h16 *__restr
                                                               XSrc src, const h16 *__restrict__ nw, float eps,
                                                               Epi epi) {
     __shared__ float red[4 * ROWS];
-    __shared__ float sums[ROWS];
+    __shared__ float nred[4];  // RMSNorm sum of squares
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t n0 = (int64_t)blockIdx.x * ROWS;
     const int64_t m = blockIdx.y;
@@ -262,7 +269,7 @@ __global__ __launch_bounds__(kThreads) void gemv_fixed_kernel(const h16 *__restr
         if (NORM) ss = sumsq8(xr[i], ss);
     }
     if (NORM) {
-        ss = block_sum<kThreads / kWave>(ss, red);
+        ss = block_sum<kThreads / kWave, false>(ss, nred);
         const h16 inv = (h16)(1.0f / sqrtf(ss / (float)K + eps));
 #pragma unroll
         for (int i = 0; i < NS; i++) xr[i] = norm8(xr[i], nr[i], inv);  // zero chunks stay zero
@@ -287,9 +294,7 @@ __global__ __launch_bounds__(kThreads) void gemv_fixed_kernel(const h16 *__restr
     constexpr int G = kWave / ROWS;
     if ((lane & (G - 1)) == 0) red[wave * ROWS + lane / G] = acc[0];
     __syncthreads();
-    if (tid < ROWS) sums[tid] = (red[tid] + red[ROWS + tid]) + (red[2 * ROWS + tid] + red[3 * ROWS + tid]);
-    __syncthreads();
-    epi.template apply<ROWS>(n0, m, N, sums, tid, pre);
+    epi.template apply<ROWS>(n0, m, N, RowSums<ROWS>{red}, tid, pre);
 }
 
 // ------------------------------------------------------------------ epilogues
@@ -304,8 +309,8 @@ struct EpiStore {
     int64_t ldy;
     template <int ROWS>
     __device__ __forceinline__ NoPre prefetch(int64_t, int64_t, int64_t, int) const { return {}; }
-    template <int ROWS>
-    __device__ __forceinline__ void apply(int64_t n0, int64_t m, int64_t N, const float *s, int tid, NoPre) const {
+    template <int ROWS, class S>
+    __device__ __forceinline__ void apply(int64_t n0, int64_t m, int64_t N, const S &s, int tid, NoPre) const {
         if (tid < ROWS && n0 + tid < N) y[m * ldy + n0 + tid] = (h16)s[tid];
     }
 };
@@ -317,8 +322,8 @@ struct EpiResidual {
     __device__ __forceinline__ h16 prefetch(int64_t n0, int64_t, int64_t N, int tid) const {
         return (tid < ROWS && n0 + tid < N) ? x[n0 + tid] : (h16)0.0f;  // only this workgroup writes it
     }
-    template <int ROWS>
-    __device__ __forceinline__ void apply(int64_t n0, int64_t, int64_t N, const float *s, int tid, h16 old) const {
+    template <int ROWS, class S>
+    __device__ __forceinline__ void apply(int64_t n0, int64_t, int64_t N, const S &s, int tid, h16 old) const {
         if (tid < ROWS && n0 + tid < N) x[n0 + tid] = hadd((h16)s[tid], old);
     }
 };
@@ -346,8 +351,8 @@ struct EpiQkv {
         }
         return p;
     }
-    template <int ROWS>
-    __device__ __forceinline__ void apply(int64_t n0, int64_t, int64_t N, const float *s, int tid, const Pre &pre) const {
+    template <int ROWS, class S>
+    __device__ __forceinline__ void apply(int64_t n0, int64_t, int64_t N, const S &s, int tid, const Pre &pre) const {
         static_assert(ROWS % 2 == 0, "pairs must stay in one workgroup");
         if (tid >= ROWS / 2) return;
         const int64_t n = n0 + 2 * tid;
@@ -376,8 +381,8 @@ struct EpiSwiglu {
     h16 *act;
     template <int ROWS>
     __device__ __forceinline__ NoPre prefetch(int64_t, int64_t, int64_t, int) const { return {}; }
-    template <int ROWS>
-    __device__ __forceinline__ void apply(int64_t n0, int64_t, int64_t N, const float *s, int tid, NoPre) const {
+    template <int ROWS, class S>
+    __device__ __forceinline__ void apply(int64_t n0, int64_t, int64_t N, const S &s, int tid, NoPre) const {
         if (tid >= ROWS / 2 || n0 + 2 * tid >= N) return;
         const h16 g = (h16)s[2 * tid], u = (h16)s[2 * tid + 1];
         act[n0 / 2 + tid] = hmul(u, silu_h(g));
@@ -396,8 +401,8 @@ constexpr float kArgmaxFloor = -10000.0f;  // f16(-10000) is exact (inference.mo
 __device__ __forceinline__ ArgPart arg_combine(ArgPart a, ArgPart b) { return b.v > a.v ? b : a; }
 
 // Per-group scan of the ROWS logits of one workgroup in ascending order.
-template <int ROWS>
-__device__ __forceinline__ ArgPart group_scan(int64_t n0, int64_t N, const float *s) {
+template <int ROWS, class S>
+__device__ __forceinline__ ArgPart group_scan(int64_t n0, int64_t N, const S &s) {
     float cv = kArgmaxFloor;
     int32_t ci = -1;
     for (int r = 0; r < ROWS && n0 + r < N; r++) {
@@ -417,8 +422,8 @@ struct EpiLmHead {
     ArgPart *parts;
     template <int ROWS>
     __device__ __forceinline__ NoPre prefetch(int64_t, int64_t, int64_t, int) const { return {}; }
-    template <int ROWS>
-    __device__ __forceinline__ void apply(int64_t n0, int64_t, int64_t N, const float *s, int tid, NoPre) const {
+    template <int ROWS, class S>
+    __device__ __forceinline__ void apply(int64_t n0, int64_t, int64_t N, const S &s, int tid, NoPre) const {
         if (tid < ROWS && n0 + tid < N) logits[n0 + tid] = (h16)s[tid];
         if (tid == 0 && n0 < N) parts[n0 / ROWS] = group_scan<ROWS>(n0, N, s);
     }
@@ -539,8 +544,8 @@ __global__ __launch_bounds__(kThreads) void gemv_q8_kernel(const int8_t *__restr
                                                            const h16 *__restrict__ nw, float eps, Epi epi) {
     constexpr int XC = QW / 8;                  // 8-element x chunks per slab
     constexpr int64_t SLAB = (int64_t)kThreads * QW;
-    __shared__ float red[4 * ROWS];
-    __shared__ float sums[ROWS];
+    __shared__ float red[G > 1 ? 2 : 1][4 * ROWS];  // alternating per row group: one barrier per group
+    __shared__ float nred[4];                      // RMSNorm sum of squares
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t nbase = (int64_t)blockIdx.x * G * ROWS;
     const int64_t k0 = (int64_t)tid * QW;
@@ -611,7 +616,7 @@ __global__ __launch_bounds__(kThreads) void gemv_q8_kernel(const int8_t *__restr
         }
     }
     if (NORM) {
-        ss = block_sum<kThreads / kWave>(ss, red);
+        ss = block_sum<kThreads / kWave, false>(ss, nred);
         const h16 inv = (h16)(1.0f / sqrtf(ss / (float)K + eps));
 #pragma unroll
         for (int i = 0; i < NS; i++)
@@ -641,11 +646,10 @@ __global__ __launch_bounds__(kThreads) void gemv_q8_kernel(const int8_t *__restr
         }
         wave_multi_sum<ROWS>(acc, lane);
         constexpr int GW = kWave / ROWS;
-        if ((lane & (GW - 1)) == 0) red[wave * ROWS + lane / GW] = acc[0];
+        float *rg = red[g & (G > 1 ? 1 : 0)];  // group g + 2 rewrites it only after group g + 1's barrier
+        if ((lane & (GW - 1)) == 0) rg[wave * ROWS + lane / GW] = acc[0];
         __syncthreads();
-        if (tid < ROWS) sums[tid] = (red[tid] + red[ROWS + tid]) + (red[2 * ROWS + tid] + red[3 * ROWS + tid]);
-        __syncthreads();
-        epi.template apply<ROWS>(nbase + (int64_t)g * ROWS, 0, N, sums, tid, pre[g]);
+        epi.template apply<ROWS>(nbase + (int64_t)g * ROWS, 0, N, RowSums<ROWS>{rg}, tid, pre[g]);
     }
 }
 

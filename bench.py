@@ -219,6 +219,85 @@ def sampler_bench(A, seed: int, reps: int = 50) -> dict:
     return out
 
 
+def kv_sweep_bench(A, seed: int, kvs=(512, 8192, 32768), steps: int = 64, warmup: int = 8) -> dict:
+    """The F16 decode of the headline at the other KV lengths of the Llama-3-8B config (one model
+    whose cache is pre-filled to the longest length; each point decodes from that position)."""
+    ctx_len = max(kvs) + steps + warmup + 64
+    model_bytes = TOKEN_WEIGHT_BYTES - 2 * DIM + 2 * VOCAB * DIM
+    ctx = A.Context(int(model_bytes + 2 * LAYERS * ctx_len * KV_DIM * 2 + (512 << 20)))
+    m = A.Model.create(ctx, A.ModelConfig(DIM, LAYERS, HEADS, KV_HEADS, FFN, VOCAB, ctx_len))
+    m.init_random(seed, 0.02, 0.0, 0.02)
+    m.fill_kv_random(max(kvs) + steps + warmup, seed=seed + 1)
+    out = {"workload": "llama3-8b-shape f16 batch-1 greedy decode (graph), KV pre-filled N(0,1)"}
+    for kv in kvs:
+        m.decode_loop(1, kv, warmup)
+        ctx.synchronize()
+        t0 = time.perf_counter()
+        m.decode_loop(1, kv, steps)
+        ctx.synchronize()
+        wall = time.perf_counter() - t0
+        tok_s = steps / wall
+        step_bytes = TOKEN_WEIGHT_BYTES + KV_BYTES_PER_POS * (kv + (steps - 1) / 2.0 + 1) + KV_BYTES_PER_POS
+        out[f"kv{kv}"] = {"tok_s": round(tok_s, 2), "ms_per_step": round(wall * 1e3 / steps, 4),
+                          "bytes_per_token": int(step_bytes), "achieved_gbs": round(step_bytes * tok_s / 1e9, 1),
+                          "frac": round(step_bytes * tok_s / 1e9 / HBM_PEAK_GBS, 4)}
+    m.close()
+    ctx.close()
+    return out
+
+
+def micro_bench(A, seed: int, iters: int = 64, copies: int = 16) -> dict:
+    """The kernel micro-suite and the Q8_0 matvec (config 5) through the C-ABI
+    ops. Weight-sized operands rotate through `copies` buffers (more than the 256 MB MALL) so every
+    call reads HBM; time per call is HIP-event time over `iters` back-to-back calls on the context
+    stream (argmax returns its index to the host, so its figure is a blocking round trip)."""
+    rng = np.random.default_rng(seed)
+    ctx = A.Context(int(copies * (DIM * DIM * 2 + 1_835_008 * 34) + (512 << 20)))
+    out = {}
+
+    def timed(fn, n=iters):
+        fn(0)
+        ctx.synchronize()
+        ctx.timer_start()
+        for i in range(n):
+            fn(i)
+        return ctx.timer_stop() / n
+
+    def rate(name, us, nbytes):
+        out[name] = {"us": round(us, 2), "bytes": int(nbytes), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                     "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+    w = (rng.standard_normal((DIM, DIM)) * 0.02).astype(np.float16)
+    ws = [ctx.from_numpy(w) for _ in range(copies)]
+    x = ctx.from_numpy(rng.standard_normal((1, DIM)).astype(np.float16))
+    y = ctx.tensor(1, DIM)
+    rate("gemv_4096x4096", timed(lambda i: A.gemm_f16(ctx, x, ws[i % copies], y)) * 1e3, DIM * DIM * 2 + 4 * DIM)
+    nw = ctx.from_numpy((1.0 + 0.02 * rng.standard_normal(DIM)).astype(np.float16))
+    for rows in (1, 64):
+        t = ctx.from_numpy(rng.standard_normal((rows, DIM)).astype(np.float16))
+        rate(f"rmsnorm_{rows}x4096", timed(lambda i: A.rmsnorm(ctx, t, nw, 1e-5)) * 1e3, 2 * rows * DIM * 2 + DIM * 2)
+    q = ctx.from_numpy(rng.standard_normal((4096, HEADS * 128)).astype(np.float16))
+    k = ctx.from_numpy(rng.standard_normal((4096, KV_HEADS * 128)).astype(np.float16))
+    rate("rope_q4096x4096_k4096x1024", timed(lambda i: A.apply_rope(ctx, q, k, 0, 128, 10000.0)) * 1e3,
+         2 * 2 * 4096 * (HEADS + KV_HEADS) * 128)
+    lg = ctx.from_numpy(rng.standard_normal((1, VOCAB)).astype(np.float16))
+    rate("argmax_128256_blocking", timed(lambda i: A.argmax(ctx, lg)) * 1e3, VOCAB * 2)
+    off = ctx.offset
+    for n, kk in ((14336, 4096), (4096, 14336)):
+        ctx.synchronize()
+        ctx.reset(off)
+        qq = rng.integers(-127, 128, size=(n, kk), dtype=np.int8)
+        dd = rng.uniform(0.001, 0.02, size=(n, kk // 32)).astype(np.float16)
+        blocks = A.Q8_0Tensor.from_parts(dd, qq).blocks.reshape(1, -1)
+        bufs = [ctx.tensor(1, blocks.size, np.uint8).upload(blocks) for _ in range(copies)]
+        xf = ctx.from_numpy(rng.standard_normal((1, kk)).astype(np.float32), np.float32)
+        yf = ctx.tensor(1, n, np.float32)
+        rate(f"q8_0_matvec_{n}x{kk}", timed(lambda i: A.q8_0_matvec_f32(ctx, bufs[i % copies].ptr, n, kk, xf, yf)) * 1e3,
+             blocks.size + 4 * kk + 4 * n)
+    ctx.close()
+    return out
+
+
 def measured_traffic():
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary
     (FETCH_SIZE + WRITE_SIZE, each scaled by its copy-kernel calibration factor), or None."""
@@ -248,6 +327,8 @@ def main():
     ap.add_argument("--prefill-decode-steps", type=int, default=256,
                     help="greedy decode steps after the prefill in --prefill-only runs (0: none)")
     ap.add_argument("--no-q8", action="store_true", help="skip the Q8_0-weight decode measurement")
+    ap.add_argument("--no-sweep", action="store_true", help="skip the decode at KV 512 / 8192 / 32768")
+    ap.add_argument("--no-micro", action="store_true", help="skip the kernel micro-suite and the Q8_0 matvec")
     ap.add_argument("--q8-only", action="store_true", help="run only the Q8_0-weight decode measurement")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain 256 MiB device-to-device copy (the FETCH_SIZE / WRITE_SIZE calibration "
@@ -330,6 +411,10 @@ def main():
     }
     m.close()
     ctx.close()
+    if not args.no_sweep:
+        out["kv_sweep"] = kv_sweep_bench(A, args.seed)
+    if not args.no_micro:
+        out["micro"] = micro_bench(A, args.seed)
     if not args.no_prefill:
         out["prefill"] = prefill_bench(A, args.seed)
     out["sampler"] = sampler_bench(A, args.seed)

@@ -342,17 +342,16 @@ __global__ __launch_bounds__(kAThreads) void attn_fast_kernel(AttnArgs a) {
     }
     float m_w = -INFINITY, l_w = 0.0f;  // running softmax state of head `wave` (waves < GH)
     float acc0 = 0.0f, acc1 = 0.0f;
-    for (int64_t t0 = p0; t0 < p1; t0 += kRound) {
+    // One round: scores, V to LDS, online softmax, P V. The caller owns the barrier that lets the
+    // next round rewrite sc and vs.
+    auto round = [&](int64_t t0, const u32x4 (&kc)[NSP][2], const u32x4 (&vc)[NVL]) {
         const int n_here = (int)(p1 - t0 < kRound ? p1 - t0 : kRound);
-        const bool more = t0 + kRound < p1;  // uniform
-        if (more) load_round(t0 + kRound, kn, vn);  // next round in flight during this one
-        // scores
 #pragma unroll
         for (int i = 0; i < NSP; i++) {
 #pragma unroll
             for (int h = 0; h < GH; h++) {
-                float d = dot8(kr[i][0], qr[h][0], 0.0f);
-                d = dot8(kr[i][1], qr[h][1], d);
+                float d = dot8(kc[i][0], qr[h][0], 0.0f);
+                d = dot8(kc[i][1], qr[h][1], d);
                 d = group_sum<TPP>(d);
                 if (sc_c == 0) sc[h][sp + i * RPP] = d * a.scale;
             }
@@ -360,7 +359,7 @@ __global__ __launch_bounds__(kAThreads) void attn_fast_kernel(AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < NVL; i++) {
             const int e = tid + i * kAThreads, r = e / VCH, c = e % VCH;
-            st16(&vs[r][8 * c], vr[i]);
+            st16(&vs[r][8 * c], vc[i]);
         }
         __syncthreads();
         // online softmax of head `wave` over the round (one position per lane)
@@ -376,32 +375,36 @@ __global__ __launch_bounds__(kAThreads) void attn_fast_kernel(AttnArgs a) {
         }
         __syncthreads();
         // P V over this thread's positions of the round (probabilities are 0 beyond n_here)
-        {
-            const float al = alpha[ph];
-            acc0 *= al;
-            acc1 *= al;
+        const float al = alpha[ph];
+        acc0 *= al;
+        acc1 *= al;
 #pragma unroll
-            for (int j = 0; j < NPOS; j += 4) {
-                const f32x4 w = *reinterpret_cast<const f32x4 *>(&sc[ph][pg * NPOS + j]);
+        for (int j = 0; j < NPOS; j += 4) {
+            const f32x4 w = *reinterpret_cast<const f32x4 *>(&sc[ph][pg * NPOS + j]);
 #pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    const h16x2 v = *reinterpret_cast<const h16x2 *>(&vs[pg * NPOS + j + u][pd]);
-                    acc0 = fmaf(w[u], (float)v.x, acc0);
-                    acc1 = fmaf(w[u], (float)v.y, acc1);
-                }
+            for (int u = 0; u < 4; u++) {
+                const h16x2 v = *reinterpret_cast<const h16x2 *>(&vs[pg * NPOS + j + u][pd]);
+                acc0 = fmaf(w[u], (float)v.x, acc0);
+                acc1 = fmaf(w[u], (float)v.y, acc1);
             }
         }
-        if (more) {
+    };
+    // Rounds with a successor request it before computing (unconditionally, so the compiler's wait
+    // counts stay exact and the successor's loads overlap this round); the last round follows.
+    int64_t t0 = p0;
+    for (; t0 + kRound < p1; t0 += kRound) {
+        load_round(t0 + kRound, kn, vn);
+        round(t0, kr, vr);
 #pragma unroll
-            for (int i = 0; i < NSP; i++) {
-                kr[i][0] = kn[i][0];
-                kr[i][1] = kn[i][1];
-            }
-#pragma unroll
-            for (int i = 0; i < NVL; i++) vr[i] = vn[i];
+        for (int i = 0; i < NSP; i++) {
+            kr[i][0] = kn[i][0];
+            kr[i][1] = kn[i][1];
         }
-        if (more) __syncthreads();  // sc and vs are rewritten by the next round
+#pragma unroll
+        for (int i = 0; i < NVL; i++) vr[i] = vn[i];
+        __syncthreads();  // sc and vs are rewritten by the next round
     }
+    round(t0, kr, vr);
 
     // Write the partial (or the output for one split). With one PV position group and one head
     // per wave (head_dim 128, 4 heads per workgroup), thread t's head is its wave's, whose

@@ -409,8 +409,11 @@ def upload_bytes(ctx, raw: np.ndarray) -> int:
     return t.ptr
 
 
-@pytest.mark.parametrize("N,K", [(48, 256), (64, 4096), (33, 96)])
+@pytest.mark.parametrize("N,K", [(48, 256), (64, 4096), (33, 96), (50, 512), (37, 16384), (5, 32768)])
 def test_gemm_q8_0_vs_oracle(A, ctx, oracle, N, K):
+    """Rows of K / 32 blocks with (K / 32) % 8 == 0 are staged through LDS, 4, 2 or 1 rows per
+    workgroup by row length (K = 256 .. 14336: 4; 16384: 2; 32768: 1), including a last workgroup
+    with fewer rows (N = 50, 37, 5); K = 96 takes the per-lane block-pair kernel."""
     blocks, d, q = make_q8_0(N, K, RNG)
     a = RNG.standard_normal((1, K)).astype(np.float16)
     c = ctx.tensor(1, N)
@@ -427,7 +430,7 @@ def test_gemm_q8_0_vs_oracle(A, ctx, oracle, N, K):
     assert (d > 0).mean() < 0.1
 
 
-@pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336)])
+@pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336), (37, 16384), (29, 96)])
 def test_q8_0_matvec_f32_closed_form(A, ctx, N, K):
     """Config 5: fp32 dequantize-then-matvec of the same blocks (closed form, f64)."""
     blocks, d, q = make_q8_0(N, K, RNG)

@@ -60,8 +60,41 @@ __global__ __launch_bounds__(kEThreads) void rope_kernel(h16 *__restrict__ Q, in
     }
 }
 
+// Vector form for head_dim % 8 == 0 and 16-byte aligned rows: one thread per 8 elements (4 pairs,
+// one 16-byte load and store) and the pairs' 4 (cos, sin) entries in one 16-byte table load; grid
+// (column chunks, row). Same per-pair f16 arithmetic as rope_kernel.
+__global__ __launch_bounds__(kEThreads) void rope_vec_kernel(h16 *__restrict__ Q, int64_t q_cols, h16 *__restrict__ K,
+                                                             int64_t k_cols, int64_t start_pos, int64_t hd,
+                                                             const h16x2 *__restrict__ table) {
+    const int64_t r = blockIdx.y;
+    const int cq = (int)(q_cols / 8), ck = (int)(k_cols / 8);
+    const h16x2 *trow = table + (start_pos + r) * (hd / 2);
+    for (int c = blockIdx.x * kEThreads + threadIdx.x; c < cq + ck; c += gridDim.x * kEThreads) {
+        h16 *p = c < cq ? Q + r * q_cols + 8 * (int64_t)c : K + r * k_cols + 8 * (int64_t)(c - cq);
+        const int col = c < cq ? 8 * c : 8 * (c - cq);
+        const u32x4 v = ld16(p);
+        const u32x4 t = ld16(trow + ((col % hd) >> 1));
+        u32x4 o;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const h16x2 ab = as_h2(v[j]), cs = as_h2(t[j]);
+            const h16x2 rot = {hsub(hmul(ab.x, cs.x), hmul(ab.y, cs.y)), hadd(hmul(ab.x, cs.y), hmul(ab.y, cs.x))};
+            o[j] = h2_bits(rot);
+        }
+        st16(p, o);
+    }
+}
+
 int32_t launch_rope(hipStream_t s, void *Q, int64_t q_rows, int64_t q_cols, void *K, int64_t k_cols,
                     int64_t start_pos, int64_t head_dim, const void *table) {
+    if (head_dim % 8 == 0 && q_cols % 8 == 0 && k_cols % 8 == 0 && q_rows <= 65535 && q_cols + k_cols < (1LL << 31) &&
+        (((uintptr_t)Q | (uintptr_t)K | (uintptr_t)table) & 15) == 0) {
+        const int64_t chunks = (q_cols + k_cols) / 8;
+        hipLaunchKernelGGL(rope_vec_kernel, dim3(grid_for(chunks, kEThreads), (unsigned)q_rows), dim3(kEThreads), 0, s,
+                           (h16 *)Q, q_cols, (h16 *)K, k_cols, start_pos, head_dim, (const h16x2 *)table);
+        AESIR_LAUNCH_CHECK("rope_vec_kernel");
+        return AESIR_OK;
+    }
     const int64_t total = q_rows * (q_cols / 2 + k_cols / 2);
     hipLaunchKernelGGL(rope_kernel, dim3(grid_for(total, kEThreads)), dim3(kEThreads), 0, s, (h16 *)Q, q_rows,
                        q_cols, (h16 *)K, k_cols, start_pos, head_dim, (const h16x2 *)table);

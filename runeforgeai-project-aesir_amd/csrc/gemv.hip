@@ -766,8 +766,8 @@ constexpr int kRowsSmall = 4;
 int32_t launch_gemm_f16(aesir_ctx *ctx, const void *A, int64_t M, int64_t K, const void *B, int64_t N, void *C) {
     if (M > 65535) return fail(AESIR_ERR_UNSUPPORTED, "gemm_f16: more than 65535 rows of A");
     EpiStore e{(h16 *)C, N};
-    return gemv_dispatch<8, false>(ctx->stream, B, N, K, XSrc{(const h16 *)A, K, nullptr, nullptr}, M, nullptr, 0.0f, e,
-                                   "gemv_store");
+    return gemv_dispatch<kRowsSmall, false>(ctx->stream, B, N, K, XSrc{(const h16 *)A, K, nullptr, nullptr}, M, nullptr,
+                                            0.0f, e, "gemv_store");
 }
 
 int32_t launch_qkv_rope_kv(hipStream_t s, const QkvArgs &a) {

@@ -394,56 +394,112 @@ __global__ __launch_bounds__(kPThreads) void qkv_post_rows_kernel(const h16 *__r
 //   reduce_qkv_post_rows_kernel: QKV[m] = f16(sum_z P[z][m]) (the store epilogue) fed straight
 //     into qkv_post_rows_kernel's RoPE and KV append.
 constexpr int kRowVec = 8;  // columns per thread and pass (N % 8 == 0)
+constexpr int kRowPasses = 2;  // rows up to 2 x 2048 columns keep their values in registers
+// SPL > 0: the launch has exactly SPL splits, and every split's partials are requested before the
+// first sum (one memory round trip instead of SPL); SPL = 0: any count, summed as loaded. Both
+// add the splits in split order.
+template <int SPL>
 __global__ __launch_bounds__(kPThreads) void reduce_residual_norm_rows_kernel(const float *__restrict__ P,
-                                                                              int64_t splits, int64_t M, int64_t N,
+                                                                              int64_t splits_rt, int64_t M, int64_t N,
                                                                               h16 *__restrict__ X, h16 *__restrict__ Xn,
                                                                               const h16 *__restrict__ w, float eps) {
     __shared__ float red[kPThreads / kWave];
+    const int64_t splits = SPL > 0 ? SPL : splits_rt;
     const int64_t m = blockIdx.x;
     h16 *x = X + m * N;
+    h16 *y = Xn + m * N;
+    const bool keep = N <= (int64_t)kRowPasses * kPThreads * kRowVec;
+    u32x4 xk0 = {0u, 0u, 0u, 0u}, xk1 = xk0;  // this thread's residual values of passes 0 and 1 (keep)
     float ss = 0.0f;
-    for (int64_t c0 = (int64_t)threadIdx.x * kRowVec; c0 < N; c0 += (int64_t)kPThreads * kRowVec) {
+    int pass = 0;
+    for (int64_t c0 = (int64_t)threadIdx.x * kRowVec; c0 < N; c0 += (int64_t)kPThreads * kRowVec, pass++) {
+        const u32x4 xo = ld16(x + c0);
         float v[kRowVec];
 #pragma unroll
         for (int e = 0; e < kRowVec; e++) v[e] = 0.0f;
-        for (int64_t z = 0; z < splits; z++) {
-            const float *p = P + (z * M + m) * N + c0;
-            const f32x4 a = *reinterpret_cast<const f32x4 *>(p), b = *reinterpret_cast<const f32x4 *>(p + 4);
+        if (SPL > 0) {
+            f32x4 a[SPL > 0 ? SPL : 1], b[SPL > 0 ? SPL : 1];
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                v[e] += a[e];
-                v[4 + e] += b[e];
+            for (int z = 0; z < SPL; z++) {
+                const float *p = P + (z * M + m) * N + c0;
+                a[z] = *reinterpret_cast<const f32x4 *>(p);
+                b[z] = *reinterpret_cast<const f32x4 *>(p + 4);
+            }
+#pragma unroll
+            for (int z = 0; z < SPL; z++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    v[e] += a[z][e];
+                    v[4 + e] += b[z][e];
+                }
+        } else {
+            for (int64_t z = 0; z < splits; z++) {
+                const float *p = P + (z * M + m) * N + c0;
+                const f32x4 a = *reinterpret_cast<const f32x4 *>(p), b = *reinterpret_cast<const f32x4 *>(p + 4);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    v[e] += a[e];
+                    v[4 + e] += b[e];
+                }
             }
         }
+        u32x4 xn;
 #pragma unroll
-        for (int e = 0; e < kRowVec; e++) {
-            const h16 xv = hadd((h16)v[e], x[c0 + e]);
-            x[c0 + e] = xv;
-            const float f = (float)xv;
-            ss = fmaf(f, f, ss);
+        for (int e = 0; e < kRowVec; e += 2) {
+            const h16x2 old = as_h2(xo[e / 2]);
+            const h16x2 nv = {hadd((h16)v[e], old.x), hadd((h16)v[e + 1], old.y)};
+            xn[e / 2] = h2_bits(nv);
+            const float f0 = (float)nv.x, f1 = (float)nv.y;
+            ss = fmaf(f0, f0, ss);
+            ss = fmaf(f1, f1, ss);
         }
+        st16(x + c0, xn);
+        if (pass == 0) xk0 = xn;
+        else xk1 = xn;
     }
-    ss = block_sum<kPThreads / kWave>(ss, red);
+    ss = block_sum<kPThreads / kWave, false>(ss, red);
     const h16 inv = (h16)(1.0f / sqrtf(ss / (float)N + eps));
-    h16 *y = Xn + m * N;
-    for (int64_t c0 = (int64_t)threadIdx.x * kRowVec; c0 < N; c0 += (int64_t)kPThreads * kRowVec)
+    pass = 0;
+    for (int64_t c0 = (int64_t)threadIdx.x * kRowVec; c0 < N; c0 += (int64_t)kPThreads * kRowVec, pass++) {
+        const u32x4 xv = !keep ? ld16(x + c0) : pass == 0 ? xk0 : xk1;
+        const u32x4 wv = ld16(w + c0);
+        u32x4 o;
 #pragma unroll
-        for (int e = 0; e < kRowVec; e++) y[c0 + e] = hmul(hmul(x[c0 + e], inv), w[c0 + e]);
+        for (int e = 0; e < 4; e++) {
+            const h16x2 a = as_h2(xv[e]), ww = as_h2(wv[e]);
+            const h16x2 r = {hmul(hmul(a.x, inv), ww.x), hmul(hmul(a.y, inv), ww.y)};
+            o[e] = h2_bits(r);
+        }
+        st16(y + c0, o);
+    }
 }
 
+template <int SPL>
 __global__ __launch_bounds__(kPThreads) void reduce_qkv_post_rows_kernel(
-    const float *__restrict__ P, int64_t splits, int64_t M, int64_t dim, int64_t kvd, int64_t hd, int64_t p0,
+    const float *__restrict__ P, int64_t splits_rt, int64_t M, int64_t dim, int64_t kvd, int64_t hd, int64_t p0,
     int64_t max_seq, const h16x2 *__restrict__ rope, h16 *__restrict__ Q, h16 *__restrict__ kc, h16 *__restrict__ vc) {
+    const int64_t splits = SPL > 0 ? SPL : splits_rt;
     const int64_t r = blockIdx.x, pos = p0 + r, slot = pos % max_seq;
     const int64_t N = dim + 2 * kvd, pairs = (dim + kvd) / 2;
     // grid.y workgroups share a row's pairs, so every thread sums one pair's partials
     for (int64_t j = (int64_t)blockIdx.y * kPThreads + threadIdx.x; j < N / 2; j += (int64_t)gridDim.y * kPThreads) {
         const int64_t col = 2 * j;
         float2 v = {0.0f, 0.0f};
-        for (int64_t z = 0; z < splits; z++) {
-            const float2 t = *reinterpret_cast<const float2 *>(P + (z * M + r) * N + col);
-            v.x += t.x;
-            v.y += t.y;
+        if (SPL > 0) {
+            float2 t[SPL > 0 ? SPL : 1];
+#pragma unroll
+            for (int z = 0; z < SPL; z++) t[z] = *reinterpret_cast<const float2 *>(P + (z * M + r) * N + col);
+#pragma unroll
+            for (int z = 0; z < SPL; z++) {
+                v.x += t[z].x;
+                v.y += t[z].y;
+            }
+        } else {
+            for (int64_t z = 0; z < splits; z++) {
+                const float2 t = *reinterpret_cast<const float2 *>(P + (z * M + r) * N + col);
+                v.x += t.x;
+                v.y += t.y;
+            }
         }
         const h16 a = (h16)v.x, b = (h16)v.y;
         if (j < pairs) {
@@ -682,8 +738,20 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
                                             next_norm && rowvec, &splits, ws));
         if (!next_norm) return AESIR_OK;
         if (splits > 1 && rowvec) {
-            hipLaunchKernelGGL(reduce_residual_norm_rows_kernel, dim3((unsigned)n), dim3(kPThreads), 0, s,
-                               (const float *)m->pf_part, splits, n, d, X, Xn, (const h16 *)next_norm, c.rms_eps);
+#define AESIR_RRN(SV)                                                                                           \
+    hipLaunchKernelGGL(reduce_residual_norm_rows_kernel<SV>, dim3((unsigned)n), dim3(kPThreads), 0, s,            \
+                       (const float *)m->pf_part, splits, n, d, X, Xn, (const h16 *)next_norm, c.rms_eps)
+            switch (splits) {
+                case 2: AESIR_RRN(2); break;
+                case 3: AESIR_RRN(3); break;
+                case 4: AESIR_RRN(4); break;
+                case 5: AESIR_RRN(5); break;
+                case 6: AESIR_RRN(6); break;
+                case 7: AESIR_RRN(7); break;
+                case 8: AESIR_RRN(8); break;
+                default: AESIR_RRN(0); break;
+            }
+#undef AESIR_RRN
             AESIR_LAUNCH_CHECK("reduce_residual_norm_rows_kernel");
             return AESIR_OK;
         }
@@ -702,10 +770,21 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
         else
             AESIR_TRY(launch_gemm_f16(m->ctx, Xn, n, d, L.wqkv, qkv_n, QKV));
         if (qkv_splits > 1) {
-            hipLaunchKernelGGL(reduce_qkv_post_rows_kernel,
-                               dim3((unsigned)n, (unsigned)((qkv_n / 2 + kPThreads - 1) / kPThreads)), dim3(kPThreads), 0, s,
-                               (const float *)m->pf_part, qkv_splits, n, d, kvd, hd, p0, c.ctx_len,
-                               (const h16x2 *)m->rope, Q, kc, vc);
+            const dim3 qgrid((unsigned)n, (unsigned)((qkv_n / 2 + kPThreads - 1) / kPThreads));
+#define AESIR_RQP(SV)                                                                                           \
+    hipLaunchKernelGGL(reduce_qkv_post_rows_kernel<SV>, qgrid, dim3(kPThreads), 0, s, (const float *)m->pf_part, \
+                       qkv_splits, n, d, kvd, hd, p0, c.ctx_len, (const h16x2 *)m->rope, Q, kc, vc)
+            switch (qkv_splits) {
+                case 2: AESIR_RQP(2); break;
+                case 3: AESIR_RQP(3); break;
+                case 4: AESIR_RQP(4); break;
+                case 5: AESIR_RQP(5); break;
+                case 6: AESIR_RQP(6); break;
+                case 7: AESIR_RQP(7); break;
+                case 8: AESIR_RQP(8); break;
+                default: AESIR_RQP(0); break;
+            }
+#undef AESIR_RQP
             AESIR_LAUNCH_CHECK("reduce_qkv_post_rows_kernel");
         } else {
             hipLaunchKernelGGL(qkv_post_rows_kernel, dim3((unsigned)n), dim3(kPThreads), 0, s, QKV, d, kvd, hd, p0,

@@ -13,6 +13,7 @@ typedef _Float16 h16;
 typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kWave = 64;
 
@@ -67,6 +68,14 @@ __device__ __forceinline__ float dot8(u32x4 a, u32x4 b, float acc) {
     acc = __builtin_amdgcn_fdot2(as_h2(a.z), as_h2(b.z), acc, false);
     acc = __builtin_amdgcn_fdot2(as_h2(a.w), as_h2(b.w), acc, false);
     return acc;
+}
+
+// D = A B + C on one 16 x 16 x 32 f16 tile (v_mfma_f32_16x16x32_f16). Lane l holds A row l % 16
+// and B column l % 16, each with k = 8 (l / 16) .. + 7 (8 halves), and D rows 4 (l / 16) + e,
+// column l % 16, in element e.
+__device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h16x8, a), __builtin_bit_cast(h16x8, b), c, 0, 0,
+                                                  0);
 }
 
 // ------------------------------------------------------------------ reductions

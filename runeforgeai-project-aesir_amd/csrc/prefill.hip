@@ -25,7 +25,6 @@
 
 namespace aesir {
 
-typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
 
 // Rows of A per workgroup tile and the workgroup count the K splits aim for. Measured on MI355X
 // (TinyLlama 128-token prefill, ms): M tile 128 / 256 workgroups 2.39; 64 / 256 2.31; 64 / 512
@@ -45,10 +44,6 @@ enum GemmEpi : int { kEpiStore = 0, kEpiResidual = 1, kEpiSwiglu = 2 };
 // Third dword of a raw buffer resource (V#) on gfx9-family GPUs, gfx950 included.
 constexpr int kBufferDword3 = 0x00020000;
 
-__device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h16x8, a), __builtin_bit_cast(h16x8, b), c, 0, 0,
-                                                  0);
-}
 
 // Applies the epilogue to output (m, n) with f32 value v; `partner` is the value of column n ^ 1
 // in the same row (used by kEpiSwiglu: 2i gate, 2i + 1 up -> C[m][i] = f16(up * silu(gate))).

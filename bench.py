@@ -43,22 +43,31 @@ def token_bytes(kv_len: int) -> int:
 GATE_UP_BYTES = 2 * FFN * DIM * 2 + DIM * 2 + DIM * 2 + FFN * 2
 
 
+CPU_LAYERS = (4, 20)  # the two forward depths the CPU baseline times
+
+
 def cpu_baseline(kv_len: int, reps: int) -> dict:
     """Times the CPU oracle (single-threaded C restatement of the reference path) on a bounded
-    sample: forward passes with 1 and with 2 Llama-3-8B-shape layers plus the lm_head at KV
-    length kv_len; per-layer and head costs are taken from the difference and scaled to 32 layers."""
+    sample of about 10 s: forward passes with 4 and with 20 Llama-3-8B-shape layers plus the
+    lm_head at KV length kv_len; per-layer and head costs are taken from the difference and scaled
+    to 32 layers. The layers share one set of weight arrays (each layer still streams its 436 MB
+    from DRAM, far beyond the CPU caches)."""
     from oracle import oracle as O
 
-    cfg = O.Config(dim=DIM, n_layers=2, n_heads=HEADS, n_kv_heads=KV_HEADS, ffn=FFN, vocab=VOCAB,
+    lo, hi = CPU_LAYERS
+    cfg = O.Config(dim=DIM, n_layers=hi, n_heads=HEADS, n_kv_heads=KV_HEADS, ffn=FFN, vocab=VOCAB,
                    ctx_len=kv_len + 8)
     rng = np.random.default_rng(5)
     block = (rng.standard_normal(1 << 24, dtype=np.float32) * 0.02).astype(np.float16)
-    weights = {}
+    weights, shared = {}, {}
     for name, (r, c) in O.tensor_shapes(cfg).items():
         if name == "token_embd.weight":
             weights[name] = np.zeros((r, c), np.float16)  # only one row is read
-        else:
-            weights[name] = np.resize(block, r * c).reshape(r, c)
+            continue
+        key = name.split(".", 2)[2] if name.startswith("blk.") else name
+        if key not in shared:
+            shared[key] = np.resize(block, r * c).reshape(r, c)
+        weights[name] = shared[key]
     m = O.Model(cfg, weights)
     kv = m.new_kv()
     kv.k[:] = np.resize(block, kv.k.size).reshape(kv.k.shape) * np.float16(50)
@@ -74,13 +83,13 @@ def cpu_baseline(kv_len: int, reps: int) -> dict:
             best = min(best, time.perf_counter() - t0)
         return best
 
-    t1, t2 = timed(1), timed(2)
-    per_layer = max(t2 - t1, 1e-9)
-    head = max(t1 - per_layer, 0.0)
+    t_lo, t_hi = timed(lo), timed(hi)
+    per_layer = max((t_hi - t_lo) / (hi - lo), 1e-9)
+    head = max(t_lo - lo * per_layer, 0.0)
     sec_per_token = LAYERS * per_layer + head
     return {"value": 1.0 / sec_per_token, "unit": "tok/s", "cores": 1, "kind": "port",
             "sample": (f"C oracle (restatement of the reference CPU path, single thread), Llama-3-8B-shape "
-                       f"forward at KV {kv_len} with 1 and 2 layers + lm_head, best of {reps}; "
+                       f"forward at KV {kv_len} with {lo} and {hi} layers + lm_head, best of {reps}; "
                        f"{per_layer * 1e3:.1f} ms/layer, {head * 1e3:.1f} ms head, scaled to 32 layers"),
             "simd": bool(O.lib().ao_simd_enabled())}
 

@@ -256,7 +256,8 @@ def kv_sweep_bench(A, seed: int, kvs=(512, 8192, 32768), steps: int = 64, warmup
 
 
 def micro_bench(A, seed: int, iters: int = 64, copies: int = 16) -> dict:
-    """The kernel micro-suite and the Q8_0 matvec (config 5) through the C-ABI
+    """The kernel micro-suite (GEMV 4096 x 4096, RMSNorm, RoPE, argmax) and the Q8_0 GGUF-block matvec on the
+    Llama-3-8B FFN shapes, through the C-ABI
     ops. Weight-sized operands rotate through `copies` buffers (more than the 256 MB MALL) so every
     call reads HBM; time per call is HIP-event time over `iters` back-to-back calls on the context
     stream (argmax returns its index to the host, so its figure is a blocking round trip)."""

@@ -6,6 +6,7 @@
 // otherwise single blocks with 2-byte loads. Two activation types:
 //   - f16 A (reference semantics): w = f16(f16(q) * d) per element, products summed in f32.
 //   - f32 x (block matvec): y = sum over blocks of d * sum(q * x), all in f32.
+#include <atomic>
 #include <type_traits>
 
 #include "device.hpp"
@@ -177,6 +178,192 @@ __global__ __launch_bounds__(kQThreads) void q8_0_staged_kernel(const uint8_t *_
     }
 }
 
+// f32 matvec on rows of nb = 64, 128, 256, 448 or 512 blocks: x as integer digits, persistent
+// workgroups with an LDS ring.
+//   - Thread t owns block column b = t % nb of a row phase ph = t / nb (PH = 64 NW / nb phases).
+//     It holds its 32 x values as a fixed-point integer v = rint(x * 2^(21 - e)), e = ilogb of the
+//     block's largest |x| (|v| <= 2^22, rounding error <= 2^-22 of that largest |x|), split into
+//     three signed 8-bit digits v = d0 + 2^8 d1 + 2^16 d2 packed four to a dword (24 registers).
+//   - Per row the block's 32 quants meet each digit in 8 v_dot4_i32_i8 (exact integer sums); the
+//     three sums are recombined in f32 (exact up to the final rounding), scaled by 2^(e - 21)
+//     (v_ldexp) and by the block scale d. A block whose x holds an inf or NaN takes the plain f32
+//     product instead, so such inputs propagate as in the f32 formula.
+//   - Workgroup g handles row groups g, g + G, ... of R = PH RT rows; each group's contiguous byte
+//     span is copied by 16-byte buffer loads with the LDS destination into one of S stages, S - 1
+//     groups ahead of the one being summed (every wave issues P one-kilobyte copies per group, the
+//     range check zero-fills past the matrix, so the vmcnt waits are exact counts).
+constexpr int kCus = 256;  // MI355X compute units (the persistent grid's size unit)
+constexpr int q8_vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+template <int NW, int PH, int RT, int S, int P>
+__global__ __launch_bounds__(NW * 64) void q8_0_digits_kernel(const uint8_t *__restrict__ blocks, int64_t N,
+                                                              int64_t rowbytes, const float *__restrict__ x,
+                                                              float *__restrict__ y) {
+    extern __shared__ __align__(16) uint8_t ring[];
+    constexpr int T = NW * 64, NB = T / PH, R = PH * RT, WPP = NW / PH;
+    constexpr int kStage = P * NW * 1024, kYs = 16;
+    __shared__ float red[NW * RT];
+    __shared__ float ys[kYs * R];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int b = tid % NB, ph = tid / NB;
+    const int64_t ng = (N + R - 1) / R;
+    const float *xb = x + 32 * b;
+    int dg[3][8];
+    int ex;
+    bool plain;
+    {
+        float xv[32];
+#pragma unroll
+        for (int i = 0; i < 32; i += 4) *reinterpret_cast<u32x4 *>(&xv[i]) = ld16(xb + i);
+        float m = 0.0f;
+        plain = false;
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            m = fmaxf(m, fabsf(xv[i]));
+            plain |= !(fabsf(xv[i]) <= 3.402823466e38f);  // inf or NaN
+        }
+        ex = m > 0.0f && !plain ? ilogbf(m) : 0;
+#pragma unroll
+        for (int w = 0; w < 8; w++) {
+            unsigned p[3] = {0u, 0u, 0u};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int v = plain ? 0 : (int)rintf(ldexpf(xv[4 * w + k], 21 - ex));
+                const int d0 = (int)(int8_t)(v & 0xff);
+                const int r1 = (v - d0) >> 8;
+                const int d1 = (int)(int8_t)(r1 & 0xff);
+                const int d2 = (r1 - d1) >> 8;
+                p[0] |= (unsigned)(d0 & 0xff) << (8 * k);
+                p[1] |= (unsigned)(d1 & 0xff) << (8 * k);
+                p[2] |= (unsigned)(d2 & 0xff) << (8 * k);
+            }
+            dg[0][w] = (int)p[0];
+            dg[1][w] = (int)p[1];
+            dg[2][w] = (int)p[2];
+        }
+    }
+    // the digits are in registers before the first copy is issued (no x load left in flight)
+#pragma unroll
+    for (int w = 0; w < 8; w++) asm volatile("" : "+v"(dg[0][w]), "+v"(dg[1][w]), "+v"(dg[2][w]));
+    auto issue = [&](int64_t g, int stage) {
+        int64_t rows = N - g * R;
+        rows = rows < 0 ? 0 : rows > R ? R : rows;
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(blocks + (rows > 0 ? g * R * rowbytes : 0)), 0, (int)(rows * rowbytes), 0x00020000);
+#pragma unroll
+        for (int j = 0; j < P; j++) {
+            const int c0 = (j * NW + wave) * kWave;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rs, (__attribute__((address_space(3))) void *)(ring + stage * kStage + c0 * 16), 16, (c0 + lane) * 16, 0,
+                0, 0);
+        }
+    };
+    const int64_t g0 = blockIdx.x, gs = gridDim.x;
+#pragma unroll
+    for (int s = 0; s < S - 1; s++) issue(g0 + s * gs, s);
+    const int bo = 34 * b, sh = bo & 3;
+    // Row results wait in LDS and go out kYs groups at a time: a global store in the loop would
+    // make the next group's vmcnt wait include its write acknowledgement.
+    auto flush = [&](int cnt, int64_t g_end) {
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_s_barrier();
+        for (int i = tid; i < cnt * R; i += T) {
+            const int64_t n = (g_end - (int64_t)(cnt - 1 - i / R) * gs) * R + i % R;
+            if (n < N) y[n] = ys[i];
+        }
+    };
+    int stage = 0, it = 0;
+    int64_t last = g0;
+    for (int64_t g = g0; g < ng; g += gs) {
+        issue(g + (S - 1) * gs, stage == 0 ? S - 1 : stage - 1);  // the stage summed one group ago
+        __builtin_amdgcn_s_waitcnt(q8_vm_wait((S - 1) * P));       // this wave's copies of group g ...
+        __builtin_amdgcn_s_barrier();                              // ... and every other wave's
+        const uint32_t *st = reinterpret_cast<const uint32_t *>(ring + stage * kStage);
+        float acc[RT];
+        auto block_words = [&](int rr, uint32_t (&w)[9]) {  // block b of row ph + PH rr, from its first byte
+            const int wi = ((ph + PH * rr) * (int)rowbytes + bo) >> 2;
+#pragma unroll
+            for (int i = 0; i < 9; i++) w[i] = st[wi + i];
+#pragma unroll
+            for (int i = 0; i < 8; i++) w[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], sh);
+            w[8] = w[8] >> (8 * sh);
+        };
+        if (!plain) {
+#pragma unroll
+            for (int rr = 0; rr < RT; rr++) {
+                uint32_t w[9];
+                block_words(rr, w);
+                int s0 = 0, s1 = 0, s2 = 0;
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const int q = (int)__builtin_amdgcn_alignbyte(w[i + 1], w[i], 2);  // quants 4i .. 4i + 3
+                    s0 = __builtin_amdgcn_sdot4(q, dg[0][i], s0, false);
+                    s1 = __builtin_amdgcn_sdot4(q, dg[1][i], s1, false);
+                    s2 = __builtin_amdgcn_sdot4(q, dg[2][i], s2, false);
+                }
+                const float v = fmaf((float)s2, 65536.0f, fmaf((float)s1, 256.0f, (float)s0));
+                acc[rr] = ldexpf((float)bits_to_h((uint16_t)(w[0] & 0xffff)) * v, ex - 21);
+            }
+        } else {
+#pragma unroll
+            for (int rr = 0; rr < RT; rr++) {
+                uint32_t w[9];
+                block_words(rr, w);
+                float v = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 32; i++) {
+                    const int bb = 2 + i;
+                    v = fmaf((float)(int8_t)((w[bb >> 2] >> (8 * (bb & 3))) & 0xff), xb[i], v);
+                }
+                acc[rr] = (float)bits_to_h((uint16_t)(w[0] & 0xffff)) * v;
+            }
+        }
+        wave_multi_sum<RT>(acc, lane);
+        constexpr int GW = kWave / RT;
+        if ((lane & (GW - 1)) == 0) red[wave * RT + lane / GW] = acc[0];
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the row sums are in LDS
+        __builtin_amdgcn_s_barrier();
+        if (tid < R) {  // row g R + tid: phase tid % PH, waves of that phase
+            const int p = tid % PH, ri = tid / PH;
+            float v = 0.0f;
+#pragma unroll
+            for (int w = 0; w < WPP; w++) v += red[(p * WPP + w) * RT + ri];
+            ys[(it % kYs) * R + tid] = v;
+        }
+        stage = stage + 1 == S ? 0 : stage + 1;
+        if (++it % kYs == 0) flush(kYs, g);
+        last = g;
+    }
+    __builtin_amdgcn_s_waitcnt(q8_vm_wait(0));  // no copy may land in LDS after the workgroup ends
+    if (it % kYs) flush(it % kYs, last);
+}
+
+template <int NW, int PH, int RT, int S, int P>
+static int32_t launch_digits(hipStream_t s, const void *blocks, int64_t N, int64_t rowbytes, const float *x, float *y,
+                             int wg_per_cu) {
+    constexpr int R = PH * RT;
+    static_assert(P * NW * 1024 >= 0, "stage size");
+    if ((int64_t)R * rowbytes + 16 > (int64_t)P * NW * 1024) return fail(AESIR_ERR_INVALID, "q8_0_matvec: stage too small");
+    const unsigned lds = (unsigned)(S * P * NW * 1024);
+    const void *fn = reinterpret_cast<const void *>(q8_0_digits_kernel<NW, PH, RT, S, P>);
+    static std::atomic<uint64_t> lds_set{0};  // devices (bit per ordinal < 64) whose LDS limit is raised
+    if (lds > 65536) {
+        int dev = 0;
+        AESIR_HIP_TRY(hipGetDevice(&dev));
+        const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
+        if (!bit || !(lds_set.load(std::memory_order_relaxed) & bit)) {
+            AESIR_HIP_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+            lds_set.fetch_or(bit, std::memory_order_relaxed);
+        }
+    }
+    const int64_t ng = (N + R - 1) / R;
+    const int64_t grid = ng < (int64_t)kCus * wg_per_cu ? ng : (int64_t)kCus * wg_per_cu;
+    hipLaunchKernelGGL((q8_0_digits_kernel<NW, PH, RT, S, P>), dim3((unsigned)grid), dim3(NW * 64), lds, s,
+                       (const uint8_t *)blocks, N, rowbytes, x, y);
+    AESIR_LAUNCH_CHECK("q8_0_digits_kernel");
+    return AESIR_OK;
+}
+
 template <bool F32X>
 static int32_t q8_dispatch(hipStream_t s, const void *blocks, int64_t M, int64_t N, int64_t K, const void *x, void *y) {
     const int64_t nb = K / 32, rowbytes = nb * 34;
@@ -219,6 +406,20 @@ int32_t launch_gemm_q8_0(hipStream_t s, const void *A, int64_t M, int64_t K, con
 
 int32_t launch_q8_0_matvec_f32(hipStream_t s, const void *blocks, int64_t N, int64_t K, const float *x, float *y) {
     if (((uintptr_t)blocks & 1) != 0) return fail(AESIR_ERR_INVALID, "q8_0_matvec: blocks must be 2-byte aligned");
+    const int64_t nb = K / 32, rowbytes = nb * 34;
+    // Digit kernel shapes (rows of 64 .. 512 blocks, one thread per block column). Stage sizes and
+    // workgroups per CU measured on MI355X at 14336 x 4096 (2 per CU, 2 stages: 13.8 us against 17.5
+    // for the staged kernel) and 4096 x 14336 (1 per CU, 3 stages: 14.8 us against 19.6).
+    if (K % 32 == 0 && ((uintptr_t)blocks & 15) == 0 && ((uintptr_t)x & 15) == 0 && N * rowbytes < ((int64_t)1 << 31)) {
+        switch (nb) {
+            case 64: return launch_digits<4, 4, 2, 2, 5>(s, blocks, N, rowbytes, x, y, 2);     // 8 rows, 17 KB
+            case 128: return launch_digits<4, 2, 4, 2, 9>(s, blocks, N, rowbytes, x, y, 2);    // 8 rows, 34 KB
+            case 256: return launch_digits<4, 1, 4, 2, 9>(s, blocks, N, rowbytes, x, y, 2);    // 4 rows, 34 KB
+            case 448: return launch_digits<7, 1, 2, 3, 5>(s, blocks, N, rowbytes, x, y, 1);    // 2 rows, 30 KB
+            case 512: return launch_digits<8, 1, 2, 2, 5>(s, blocks, N, rowbytes, x, y, 1);    // 2 rows, 34 KB
+            default: break;
+        }
+    }
     return q8_dispatch<true>(s, blocks, 1, N, K, x, y);
 }
 

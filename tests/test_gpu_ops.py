@@ -430,9 +430,12 @@ def test_gemm_q8_0_vs_oracle(A, ctx, oracle, N, K):
     assert (d > 0).mean() < 0.1
 
 
-@pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336), (37, 16384), (29, 96)])
+@pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336), (37, 16384), (29, 96), (4100, 2048), (2050, 8192),
+                                 (600, 16384), (3, 14336), (50, 512)])
 def test_q8_0_matvec_f32_closed_form(A, ctx, N, K):
-    """Config 5: fp32 dequantize-then-matvec of the same blocks (closed form, f64)."""
+    """Config 5: fp32 dequantize-then-matvec of the same blocks (closed form, f64). Rows of 64, 128,
+    256, 448 and 512 blocks take the integer-digit kernel (more row groups than workgroups, and a
+    last group with fewer rows: 4100, 2050, 600); 16 and 3 blocks the staged and pair kernels."""
     blocks, d, q = make_q8_0(N, K, RNG)
     x = RNG.standard_normal(K).astype(np.float32)
     y = ctx.tensor(1, N, np.float32)
@@ -443,3 +446,26 @@ def test_q8_0_matvec_f32_closed_form(A, ctx, N, K):
     # f32 arithmetic: error bounded by 2^-17 of the sum of |products|
     noise = 2.0 ** -17 * (np.abs(W) @ np.abs(x.astype(np.float64)))
     assert np.all(np.abs(got - ref) <= noise)
+
+
+@pytest.mark.parametrize("K", [4096, 14336])
+def test_q8_0_matvec_f32_non_finite_x(A, ctx, K):
+    """An inf in x reaches every row as in the f32 formula (+-inf, or NaN where 0 * inf or inf - inf
+    occurs); the other blocks of the row keep their digit path."""
+    N = 96
+    blocks, d, q = make_q8_0(N, K, RNG)
+    x = RNG.standard_normal(K).astype(np.float32)
+    x[5] = np.inf
+    x[K - 40] = -np.inf
+    y = ctx.tensor(1, N, np.float32)
+    A.q8_0_matvec_f32(ctx, upload_bytes(ctx, blocks), N, K, ctx.from_numpy(x, np.float32), y)
+    W = (q.astype(np.float64) * d.astype(np.float64)[:, None]).reshape(N, K)
+    with np.errstate(invalid="ignore"):
+        ref = W @ x.astype(np.float64)
+    got = y.numpy()[0].astype(np.float64)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(np.isposinf(got), np.isposinf(ref))
+    assert np.array_equal(np.isneginf(got), np.isneginf(ref))
+    x[5] = np.nan
+    A.q8_0_matvec_f32(ctx, upload_bytes(ctx, blocks), N, K, ctx.from_numpy(x, np.float32), y)
+    assert np.isnan(y.numpy()).all()

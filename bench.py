@@ -168,20 +168,21 @@ Q8_TOKEN_WEIGHT_BYTES = LAYERS * Q8_LAYER_BYTES + q8_mat_bytes(VOCAB, DIM) + 2 *
 Q8_GATE_UP_BYTES = q8_mat_bytes(2 * FFN, DIM) + DIM * 2 + DIM * 2 + FFN * 2
 
 
-def q8_bench(A, seed: int, kv: int, steps: int, warmup: int, kernel_iters: int) -> dict:
+def q8_bench(A, seed: int, kv: int, steps: int, warmup: int, kernel_iters: int, use_graph: bool = True) -> dict:
     """Batch-1 greedy decode of the Llama-3-8B shape with Q8_0 matrices (GGUF block_q8_0 data
     repacked as int8 quants + f16 scales; random quants, scales for weights of std 0.02), KV cache
-    pre-filled to kv positions; same step structure as the F16 decode."""
+    pre-filled to kv positions; same step structure as the F16 decode (graph replay unless
+    use_graph is False)."""
     ctx_len = kv + max(steps, warmup) + 64
     well = int(Q8_TOKEN_WEIGHT_BYTES + q8_mat_bytes(VOCAB - 1, DIM) + 2 * LAYERS * ctx_len * KV_DIM * 2 + (512 << 20))
     ctx = A.Context(well)
     m = A.Model.create(ctx, A.ModelConfig(DIM, LAYERS, HEADS, KV_HEADS, FFN, VOCAB, ctx_len), A.GGML_Q8_0)
     m.init_random(seed, 0.02, 0.0, 0.02)
     m.fill_kv_random(kv, seed=seed + 1)
-    m.decode_loop(1, kv, warmup)
+    m.decode_loop(1, kv, warmup, use_graph=use_graph)
     ctx.synchronize()
     t0 = time.perf_counter()
-    toks, event_ms = m.decode_loop(1, kv, steps)
+    toks, event_ms = m.decode_loop(1, kv, steps, use_graph=use_graph)
     ctx.synchronize()
     wall = time.perf_counter() - t0
     tok_s = steps / wall
@@ -359,7 +360,7 @@ def main():
         print(json.dumps({"prefill": prefill_bench(A, args.seed, n_decode=args.prefill_decode_steps)}))
         return
     if args.q8_only:
-        q = q8_bench(A, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters)
+        q = q8_bench(A, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters, not args.eager)
         q["prefill"] = prefill_bench(A, args.seed, n_decode=64, q8=True)
         print(json.dumps({"q8_0": q}))
         return
@@ -429,7 +430,7 @@ def main():
         out["prefill"] = prefill_bench(A, args.seed)
     out["sampler"] = sampler_bench(A, args.seed)
     if not args.no_q8:
-        out["q8_0"] = q8_bench(A, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters)
+        out["q8_0"] = q8_bench(A, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters, use_graph)
         out["q8_0"]["prefill"] = prefill_bench(A, args.seed, n_decode=64, q8=True)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.kv, args.cpu_reps)

@@ -238,55 +238,62 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(const h16 *__re
     }
 }
 
-// Wide-tile variant for GEMMs with many output columns (the gate/up projection): a 128 x 64 tile
-// per workgroup of 8 waves (4 x 2, each 32 x 32), 128-wide K chunks (four MFMA k-steps per
-// chunk), 3 LDS stages of 48 KB, no K split. Per chunk a wave copies 6 KB: every copy
+// Wide-tile kernel for M > 64 and K % 128 == 0: the whole 128-position chunk in one M tile,
+// NT = 64 or 32 columns per workgroup of 8 waves (4 x 2, each 32 x NT / 2), 128-wide K chunks
+// (four MFMA k-steps per chunk), 3 LDS stages of (128 + NT) 256-byte rows. Every copy
 // instruction moves 4 whole 256-byte row chunks (lane l: row l / 16, granule l % 16), granule p
 // of row r holding k-granule p ^ (r & 15), so the 16 rows of a fragment read hit distinct banks.
-// With the whole 128-position chunk in one M tile every weight row is copied once (the 32 x 64
-// kernel copies it once per 32 rows), A once per 64 columns, and each barrier covers four times
-// the bytes. Measured on MI355X (M = 128, weights cold), against the 32 x 64 kernel:
-//   gate/up 11264 x 2048: 17.3 us against 22.5 (64 x 128 tiles: 18.3; hipBLASLt MT64x128x128: 18.9)
-//   gate/up 28672 x 4096: 64 us against 134 (64 x 128 tiles: 82)
-// Narrow GEMMs (2048 - 2560 columns: 16 - 20 tiles) stay on the split 32 x 64 kernel.
-constexpr int kWideMT = 128, kWideNT = 64, kWideWM = 4, kWideWN = 2, kWideKC = 128, kWideS = 3;
+// Every weight row is copied once (the 32 x 64 kernel copies it once per 32 rows) and each
+// barrier covers 3 - 4 times the bytes. K splits over grid.z write f32 partials like the 32 x 64
+// kernel's, for the same reduce and row kernels.
+// Measured on MI355X (M = 128, weights cold, us; against the split 32 x 64 kernel):
+//   11264 x 2048 (gate/up)  17.3 against 22.5   28672 x 4096  64 against 134
+//   2560 x 2048 (QKV)       10.3 against 11.8    6144 x 4096  21.3 against 27.1
+//   2048 x 2048 (O)          9.5 against  9.6    4096 x 4096  15.3 against 19.3
+//   2048 x 5632 (down)      13.8 against 15.9    4096 x 14336 34.1 against 56.5
+// (hipBLASLt's pick for 11264 x 2048, MT64x128x128: 18.9.)
+constexpr int kWideMT = 128, kWideWM = 4, kWideWN = 2, kWideKC = 128, kWideS = 3;
 constexpr int kWideThreads = kWideWM * kWideWN * kWave;
-constexpr int kWideRB = kWideKC * 2;                                // bytes of one row chunk
-constexpr int kWideStage = (kWideMT + kWideNT) * kWideRB;           // 48 KB
-constexpr int kWideCopies = (kWideMT + kWideNT) / 4 / (kWideWM * kWideWN);  // per wave per chunk
-constexpr int kWideMinTiles = 128;  // fewer tiles than this: the split 32 x 64 kernel fills the chip better
-static_assert(kWideCopies * 4 * kWideWM * kWideWN == kWideMT + kWideNT, "whole copy instructions per wave");
+constexpr int kWideRB = kWideKC * 2;  // bytes of one row chunk
+constexpr int kWideMaxSplits = 8;     // fused row kernels take up to 8 split partials
+constexpr int kWideWgTarget = 256;    // the split count doubles while tiles x splits stays within this
 
-template <int EPI>
-__global__ __launch_bounds__(kWideThreads) void gemm_wide_kernel(const h16 *__restrict__ A, int64_t M, int64_t K,
-                                                                 const h16 *__restrict__ B, int64_t N,
-                                                                 h16 *__restrict__ C, int64_t ldc) {
-    constexpr int MF = kWideMT / kWideWM / 16, NF = kWideNT / kWideWN / 16, KQ = kWideKC / 32;
-    extern __shared__ __align__(16) uint8_t lds[];  // kWideS stages of kWideStage bytes
+__host__ __device__ constexpr int wide_stage_bytes(int nt) { return (kWideMT + nt) * kWideRB; }
+
+template <int EPI, int NT>
+__device__ __forceinline__ void gemm_wide_body(const h16 *__restrict__ A, int64_t M, int64_t K,
+                                               const h16 *__restrict__ B, int64_t N, h16 *__restrict__ C,
+                                               int64_t ldc, float *__restrict__ P) {
+    constexpr int kStage = wide_stage_bytes(NT);
+    constexpr int kCopies = (kWideMT + NT) / 4 / (kWideWM * kWideWN);  // per wave per chunk
+    static_assert(kCopies * 4 * kWideWM * kWideWN == kWideMT + NT, "whole copy instructions per wave");
+    constexpr int MF = kWideMT / kWideWM / 16, NF = NT / kWideWN / 16, KQ = kWideKC / 32;
+    extern __shared__ __align__(16) uint8_t lds[];  // kWideS stages of kStage bytes
     // wave index as a scalar, so that each copy's operand choice (A or weights) is a scalar select
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / kWideWN, wn = wave % kWideWN;
-    const int64_t m0 = (int64_t)blockIdx.y * kWideMT, n0 = (int64_t)blockIdx.x * kWideNT;
+    const int64_t m0 = (int64_t)blockIdx.y * kWideMT, n0 = (int64_t)blockIdx.x * NT;
     const int r = lane & 15, g = lane >> 4;
-    const int64_t nkc = K / kWideKC;
+    const int64_t nkc = K / kWideKC, splits = gridDim.z, z = blockIdx.z;
+    const int64_t c0 = nkc * z / splits, c1 = nkc * (z + 1) / splits;
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void *)A, 0, (int)(M * K * 2), kBufferDword3);
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void *)B, 0, (int)(N * K * 2), kBufferDword3);
-    // copy j of this wave: stage rows 4 (kWideCopies wave + j) .. + 3 (A rows first, then weights)
-    int off[kWideCopies], ldsrow[kWideCopies];
-    bool isa[kWideCopies];
+    // copy j of this wave: stage rows 4 (kCopies wave + j) .. + 3 (A rows first, then weights)
+    int off[kCopies], ldsrow[kCopies];
+    bool isa[kCopies];
 #pragma unroll
-    for (int j = 0; j < kWideCopies; j++) {
-        const int row0 = 4 * (kWideCopies * wave + j), row = row0 + (lane >> 4);
+    for (int j = 0; j < kCopies; j++) {
+        const int row0 = 4 * (kCopies * wave + j), row = row0 + (lane >> 4);
         isa[j] = row0 < kWideMT;
         ldsrow[j] = row0;
         const int64_t grow = isa[j] ? m0 + row : n0 + row - kWideMT;
         off[j] = (int)(grow * K * 2) + (((lane & 15) ^ (row & 15)) << 4);
     }
     auto issue = [&](int64_t c, int stage) {
-        c = c < nkc ? c : nkc - 1;  // past the end: re-read the last chunk into a free stage
-        uint8_t *sa = lds + stage * kWideStage;
+        c = c < c1 ? c : c1 - 1;  // past the split's end: re-read its last chunk into a free stage
+        uint8_t *sa = lds + stage * kStage;
 #pragma unroll
-        for (int j = 0; j < kWideCopies; j++)
+        for (int j = 0; j < kCopies; j++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(isa[j] ? ra : rb,
                                                      (__attribute__((address_space(3))) void *)(sa + ldsrow[j] * kWideRB),
                                                      16, off[j], (int)(c * kWideRB), 0, 0);
@@ -297,13 +304,13 @@ __global__ __launch_bounds__(kWideThreads) void gemm_wide_kernel(const h16 *__re
 #pragma unroll
         for (int j = 0; j < NF; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int j = 0; j < kWideS - 1; j++) issue(j, j);
-    for (int64_t c = 0; c < nkc; c++) {
-        const int t = (int)(c % kWideS);
-        __builtin_amdgcn_s_waitcnt(vm_wait(kWideCopies * (kWideS - 2)));  // this wave's copies of chunk c ...
-        __builtin_amdgcn_s_barrier();                                     // ... and every wave's
-        issue(c + kWideS - 1, (t + kWideS - 1) % kWideS);                 // into the stage chunk c - 1 used
-        const uint8_t *sa = lds + t * kWideStage, *sb = sa + kWideMT * kWideRB;
+    for (int j = 0; j < kWideS - 1; j++) issue(c0 + j, j);
+    for (int64_t c = c0; c < c1; c++) {
+        const int t = (int)((c - c0) % kWideS);
+        __builtin_amdgcn_s_waitcnt(vm_wait(kCopies * (kWideS - 2)));  // this wave's copies of chunk c ...
+        __builtin_amdgcn_s_barrier();                                 // ... and every wave's
+        issue(c + kWideS - 1, (t + kWideS - 1) % kWideS);             // into the stage chunk c - 1 used
+        const uint8_t *sa = lds + t * kStage, *sb = sa + kWideMT * kWideRB;
         u32x4 a[KQ][MF], b[KQ][NF];
 #pragma unroll
         for (int q = 0; q < KQ; q++) {
@@ -314,7 +321,7 @@ __global__ __launch_bounds__(kWideThreads) void gemm_wide_kernel(const h16 *__re
             }
 #pragma unroll
             for (int j = 0; j < NF; j++) {
-                const int row = wn * (kWideNT / kWideWN) + 16 * j + r;
+                const int row = wn * (NT / kWideWN) + 16 * j + r;
                 b[q][j] = ld16(sb + row * kWideRB + (((4 * q + g) ^ ((row + kWideMT) & 15)) << 4));
             }
         }
@@ -335,11 +342,75 @@ __global__ __launch_bounds__(kWideThreads) void gemm_wide_kernel(const h16 *__re
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const int64_t m = m0 + wm * (kWideMT / kWideWM) + 16 * i + 4 * g + e;
-                const int64_t n = n0 + wn * (kWideNT / kWideWN) + 16 * j + r;
+                const int64_t n = n0 + wn * (NT / kWideWN) + 16 * j + r;
                 const float v = acc[i][j][e];
-                const float partner = dpp_f<kDppXor1>(v);  // lane r ^ 1 holds column n ^ 1
-                gemm_epilogue<EPI>(C, ldc, M, N, m, n, v, partner);
+                if (splits == 1) {
+                    const float partner = dpp_f<kDppXor1>(v);  // lane r ^ 1 holds column n ^ 1
+                    gemm_epilogue<EPI>(C, ldc, M, N, m, n, v, partner);
+                } else if (m < M && n < N) {
+                    P[(z * M + m) * N + n] = v;
+                }
             }
+}
+
+// One kernel per (epilogue, tile width); the template body above is shared.
+#define AESIR_WIDE_KERNEL(EPIV, NTV)                                                                             \
+    __global__ __launch_bounds__(kWideThreads) void gemm_wide_kernel_##EPIV##_##NTV(                            \
+        const h16 *__restrict__ A, int64_t M, int64_t K, const h16 *__restrict__ B, int64_t N, h16 *__restrict__ C, \
+        int64_t ldc, float *__restrict__ P) {                                                                    \
+        gemm_wide_body<EPIV, NTV>(A, M, K, B, N, C, ldc, P);                                                    \
+    }
+AESIR_WIDE_KERNEL(0, 64)
+AESIR_WIDE_KERNEL(0, 32)
+AESIR_WIDE_KERNEL(1, 64)
+AESIR_WIDE_KERNEL(1, 32)
+AESIR_WIDE_KERNEL(2, 64)
+AESIR_WIDE_KERNEL(2, 32)
+#undef AESIR_WIDE_KERNEL
+
+typedef void (*WideKernelFn)(const h16 *, int64_t, int64_t, const h16 *, int64_t, h16 *, int64_t, float *);
+template <int EPI, int NT>
+static WideKernelFn wide_kernel() {
+    if constexpr (EPI == kEpiStore) return NT == 64 ? gemm_wide_kernel_0_64 : gemm_wide_kernel_0_32;
+    else if constexpr (EPI == kEpiResidual) return NT == 64 ? gemm_wide_kernel_1_64 : gemm_wide_kernel_1_32;
+    else return NT == 64 ? gemm_wide_kernel_2_64 : gemm_wide_kernel_2_32;
+}
+
+// Tile width and K splits of the wide-tile kernel for an f16 GEMM, or nt = 0 when the 32 x 64
+// kernel serves it (Q8_0 weights, M <= 64, K % 128 != 0, or a 32-bit byte range exceeded).
+// NT = 64 from 4096 columns up, 32 below; the split count doubles while it divides the K chunks
+// evenly, leaves at least 4 chunks per split and keeps tiles x splits within kWideWgTarget.
+struct WidePlan {
+    int nt;
+    int64_t splits;
+};
+static WidePlan wide_plan(int64_t M, int64_t K, int64_t N, bool q8) {
+    const int64_t lim = (int64_t)1 << 31;
+    if (q8 || M <= 64 || K % kWideKC != 0 || (M + kWideMT) * K * 2 >= lim || (N + 64) * K * 2 >= lim) return {0, 1};
+    const int nt = N >= 4096 ? 64 : 32;
+    const int64_t tiles = ((N + nt - 1) / nt) * ((M + kWideMT - 1) / kWideMT), nkc = K / kWideKC;
+    int64_t s = 1;
+    while (2 * s <= kWideMaxSplits && tiles * 2 * s <= kWideWgTarget && nkc % (2 * s) == 0 && nkc / (2 * s) >= 4) s *= 2;
+    return {nt, s};
+}
+
+template <int EPI, int NT>
+static int32_t launch_wide(hipStream_t s, const void *A, int64_t M, int64_t K, const void *B, int64_t N, void *C,
+                           int64_t ldc, float *part, int64_t splits) {
+    static std::atomic<uint64_t> lds_set{0};  // devices (bit per ordinal < 64) whose LDS limit is raised
+    constexpr int lds = kWideS * wide_stage_bytes(NT);
+    int dev = 0;
+    AESIR_HIP_TRY(hipGetDevice(&dev));
+    const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
+    if (!bit || !(lds_set.load(std::memory_order_relaxed) & bit)) {
+        AESIR_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(wide_kernel<EPI, NT>()),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, lds));
+        lds_set.fetch_or(bit, std::memory_order_relaxed);
+    }
+    const dim3 grid((unsigned)((N + NT - 1) / NT), (unsigned)((M + kWideMT - 1) / kWideMT), (unsigned)splits);
+    hipLaunchKernelGGL((wide_kernel<EPI, NT>()), grid, dim3(kWideThreads), lds, s, (const h16 *)A, M, K,
+                       (const h16 *)B, N, (h16 *)C, ldc, part);
+    return AESIR_OK;
 }
 
 // Sums the split partials of each output in split order and applies the epilogue; one thread
@@ -378,8 +449,9 @@ int64_t prefill_part_floats(int64_t rows, int64_t dim, int64_t qkv_n, int64_t ff
     int64_t most = 0;
     for (auto &kn : shapes) {
         if (kn[0] % 64 != 0) continue;
-        const int64_t need = gemm_splits(rows, kn[0], kn[1]) * rows * kn[1];
-        if (gemm_splits(rows, kn[0], kn[1]) > 1 && need > most) most = need;
+        const WidePlan wp = wide_plan(rows, kn[0], kn[1], false);
+        const int64_t sp = wp.nt ? wp.splits : gemm_splits(rows, kn[0], kn[1]);
+        if (sp > 1 && sp * rows * kn[1] > most) most = sp * rows * kn[1];
     }
     return most;
 }
@@ -394,22 +466,21 @@ static int32_t launch_mfma(hipStream_t s, const void *A, int64_t M, int64_t K, c
     const int64_t gx = (N + kGemmNT - 1) / kGemmNT, gy = (M + kGemmMT - 1) / kGemmMT;
     if (gx > 2147483647 || gy > 65535) return fail(AESIR_ERR_UNSUPPORTED, "%s: GEMM grid too large", name);
     if (EPI == kEpiSwiglu && (N & 1)) return fail(AESIR_ERR_INVALID, "%s: odd gate/up column count", name);
-    const int64_t wx = (N + kWideNT - 1) / kWideNT, wy = (M + kWideMT - 1) / kWideMT;
-    if (!Bs && K % kWideKC == 0 && wx * wy >= kWideMinTiles && (N + kWideNT) * K * 2 < ((int64_t)1 << 31) &&
-        (M + kWideMT) * K * 2 < ((int64_t)1 << 31)) {
-        static std::atomic<uint64_t> lds_set{0};  // devices (bit per ordinal < 64) whose LDS limit is raised
-        int dev = 0;
-        AESIR_HIP_TRY(hipGetDevice(&dev));
-        const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
-        if (!bit || !(lds_set.load(std::memory_order_relaxed) & bit)) {
-            AESIR_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_wide_kernel<EPI>),
-                                              hipFuncAttributeMaxDynamicSharedMemorySize, kWideS * kWideStage));
-            lds_set.fetch_or(bit, std::memory_order_relaxed);
-        }
-        hipLaunchKernelGGL((gemm_wide_kernel<EPI>), dim3((unsigned)wx, (unsigned)wy), dim3(kWideThreads),
-                           kWideS * kWideStage, s, (const h16 *)A, M, K, (const h16 *)B, N, (h16 *)C, ldc);
+    if (const WidePlan wp = wide_plan(M, K, N, Bs != nullptr); wp.nt) {
+        int64_t splits = wp.splits;
+        while (splits > 1 && splits * M * N > part_floats) splits /= 2;
+        if (wp.nt == 64)
+            AESIR_TRY((launch_wide<EPI, 64>(s, A, M, K, B, N, C, ldc, part, splits)));
+        else
+            AESIR_TRY((launch_wide<EPI, 32>(s, A, M, K, B, N, C, ldc, part, splits)));
         AESIR_LAUNCH_CHECK(name);
-        if (splits_out) *splits_out = 1;
+        if (splits_out) *splits_out = splits;
+        if (splits > 1 && !defer) {
+            const int64_t blocks = (M * N + 255) / 256;
+            hipLaunchKernelGGL(gemm_reduce_kernel<EPI>, dim3((unsigned)blocks), dim3(256), 0, s, (const float *)part,
+                               splits, M, N, (h16 *)C, ldc);
+            AESIR_LAUNCH_CHECK("gemm_reduce_kernel");
+        }
         return AESIR_OK;
     }
     int64_t splits = gemm_splits(M, K, N);

@@ -14,6 +14,8 @@
 //   in lane l).
 //   Small-N GEMMs also split K over grid.z to put enough weight bytes in flight; their f32
 //   partials are summed in a fixed order by the epilogue kernel (deterministic, no atomics).
+//   Chunks of more than 64 positions use the wide-tile kernel below (the whole chunk in one
+//   128-row M tile, 8 waves, 128-wide K chunks) instead; this 32-row kernel serves shorter chunks.
 //   At M = 128 the GEMM is HBM-bound (128 flop/byte against MI355X's 312 flop/byte ridge).
 #include <atomic>
 #include <cmath>
@@ -258,45 +260,88 @@ constexpr int kWideRB = kWideKC * 2;  // bytes of one row chunk
 constexpr int kWideMaxSplits = 8;     // fused row kernels take up to 8 split partials
 constexpr int kWideWgTarget = 256;    // the split count doubles while tiles x splits stays within this
 
-__host__ __device__ constexpr int wide_stage_bytes(int nt) { return (kWideMT + nt) * kWideRB; }
+// Q8_0 weights (q8): a chunk's weight rows are 128-byte quant segments (8 rows per copy
+// instruction: lane l row l / 8, granule l % 8, granule p of row r holding k-granule p ^ ((r >> 1)
+// & 7)) plus the rows' four f16 block scales (4-byte copies, two lanes per row); every B fragment
+// is dequantized to f16(q * d) by dequant_q8x4, as in the 32 x 64 kernel.
+__host__ __device__ constexpr int wide_stage_bytes(int nt, bool q8) {
+    return q8 ? kWideMT * kWideRB + nt * kWideKC + nt * 8 : (kWideMT + nt) * kWideRB;
+}
+__device__ __forceinline__ int wide_qswz(int row) { return (row >> 1) & 7; }
 
-template <int EPI, int NT>
+template <int EPI, int NT, bool Q8>
 __device__ __forceinline__ void gemm_wide_body(const h16 *__restrict__ A, int64_t M, int64_t K,
-                                               const h16 *__restrict__ B, int64_t N, h16 *__restrict__ C,
-                                               int64_t ldc, float *__restrict__ P) {
-    constexpr int kStage = wide_stage_bytes(NT);
-    constexpr int kCopies = (kWideMT + NT) / 4 / (kWideWM * kWideWN);  // per wave per chunk
-    static_assert(kCopies * 4 * kWideWM * kWideWN == kWideMT + NT, "whole copy instructions per wave");
+                                               const void *__restrict__ B, int64_t N, h16 *__restrict__ C,
+                                               int64_t ldc, float *__restrict__ P, const h16 *__restrict__ Bs) {
+    constexpr int kW = kWideWM * kWideWN;
+    constexpr int kStage = wide_stage_bytes(NT, Q8);
+    // f16: (128 + NT) / 4 copies of four 256-byte rows, the same count for every wave
+    constexpr int kCopies = (kWideMT + NT) / 4 / kW;
+    static_assert(Q8 || kCopies * 4 * kW == kWideMT + NT, "whole copy instructions per wave");
+    // Q8_0: 128 / 4 A copies (4 per wave), NT / 8 quant copies (waves 0 .. NT / 8 - 1) and NT / 32
+    // scale copies (waves (NT / 8 + s) % 8)
+    constexpr int kAq = kWideMT / 4 / kW, kQq = NT / 8, kSq = NT / 32;
+    static_assert(kAq * 4 * kW == kWideMT && kQq <= kW && kSq <= kW, "Q8_0 copy plan");
     constexpr int MF = kWideMT / kWideWM / 16, NF = NT / kWideWN / 16, KQ = kWideKC / 32;
     extern __shared__ __align__(16) uint8_t lds[];  // kWideS stages of kStage bytes
-    // wave index as a scalar, so that each copy's operand choice (A or weights) is a scalar select
+    // wave index as a scalar, so that each copy's operand choice is a scalar select
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / kWideWN, wn = wave % kWideWN;
     const int64_t m0 = (int64_t)blockIdx.y * kWideMT, n0 = (int64_t)blockIdx.x * NT;
     const int r = lane & 15, g = lane >> 4;
     const int64_t nkc = K / kWideKC, splits = gridDim.z, z = blockIdx.z;
     const int64_t c0 = nkc * z / splits, c1 = nkc * (z + 1) / splits;
+    const int64_t KB = K / 32;
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void *)A, 0, (int)(M * K * 2), kBufferDword3);
-    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void *)B, 0, (int)(N * K * 2), kBufferDword3);
-    // copy j of this wave: stage rows 4 (kCopies wave + j) .. + 3 (A rows first, then weights)
-    int off[kCopies], ldsrow[kCopies];
-    bool isa[kCopies];
+    const __amdgpu_buffer_rsrc_t rb =
+        __builtin_amdgcn_make_buffer_rsrc((void *)B, 0, (int)(N * K * (Q8 ? 1 : 2)), kBufferDword3);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)Bs, 0, Q8 ? (int)(N * KB * 2) : 0, kBufferDword3);
+    // f16 copy j of this wave: stage rows 4 (kCopies wave + j) .. + 3 (A rows first, then weights);
+    // Q8_0: A copy j rows 4 (kAq wave + j) .. + 3
+    constexpr int kAC = Q8 ? kAq : kCopies;
+    int off[kAC], ldsrow[kAC];
+    bool isa[kAC];
 #pragma unroll
-    for (int j = 0; j < kCopies; j++) {
-        const int row0 = 4 * (kCopies * wave + j), row = row0 + (lane >> 4);
+    for (int j = 0; j < kAC; j++) {
+        const int row0 = 4 * (kAC * wave + j), row = row0 + (lane >> 4);
         isa[j] = row0 < kWideMT;
         ldsrow[j] = row0;
         const int64_t grow = isa[j] ? m0 + row : n0 + row - kWideMT;
         off[j] = (int)(grow * K * 2) + (((lane & 15) ^ (row & 15)) << 4);
     }
+    const bool has_q = Q8 && wave < kQq;  // this wave's quant copy: rows 8 wave + lane / 8
+    const int qrow = 8 * wave + (lane >> 3);
+    const int qoff = (int)((n0 + qrow) * K) + (((lane & 7) ^ wide_qswz(qrow)) << 4);
+    const int sidx = (wave - kQq + kW) % kW;  // this wave's scale copy (if sidx < kSq): rows 32 sidx + lane / 2
+    const bool has_s = Q8 && sidx < kSq;
+    const int soff = (int)((n0 + 32 * sidx + (lane >> 1)) * KB * 2) + 4 * (lane & 1);
+    const int ncopy = Q8 ? kAq + (has_q ? 1 : 0) + (has_s ? 1 : 0) : kCopies;  // wave-uniform
     auto issue = [&](int64_t c, int stage) {
         c = c < c1 ? c : c1 - 1;  // past the split's end: re-read its last chunk into a free stage
         uint8_t *sa = lds + stage * kStage;
 #pragma unroll
-        for (int j = 0; j < kCopies; j++)
+        for (int j = 0; j < kAC; j++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(isa[j] ? ra : rb,
                                                      (__attribute__((address_space(3))) void *)(sa + ldsrow[j] * kWideRB),
                                                      16, off[j], (int)(c * kWideRB), 0, 0);
+        if (Q8) {
+            uint8_t *sq = sa + kWideMT * kWideRB;
+            if (has_q)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rb, (__attribute__((address_space(3))) void *)(sq + 8 * wave * kWideKC), 16, qoff,
+                    (int)(c * kWideKC), 0, 0);
+            if (has_s)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rs, (__attribute__((address_space(3))) void *)(sq + NT * kWideKC + 32 * sidx * 8), 4, soff,
+                    (int)(c * 8), 0, 0);
+        }
+    };
+    // wait until only the copies of the next chunk are in flight (wave-uniform count)
+    auto wait_chunk = [&]() {
+        if (!Q8 || ncopy == kAq) __builtin_amdgcn_s_waitcnt(vm_wait(kAC * (kWideS - 2)));
+        else if (ncopy == kAq + 1) __builtin_amdgcn_s_waitcnt(vm_wait((kAq + 1) * (kWideS - 2)));
+        else __builtin_amdgcn_s_waitcnt(vm_wait((kAq + 2) * (kWideS - 2)));
     };
     f32x4 acc[MF][NF];
 #pragma unroll
@@ -307,11 +352,13 @@ __device__ __forceinline__ void gemm_wide_body(const h16 *__restrict__ A, int64_
     for (int j = 0; j < kWideS - 1; j++) issue(c0 + j, j);
     for (int64_t c = c0; c < c1; c++) {
         const int t = (int)((c - c0) % kWideS);
-        __builtin_amdgcn_s_waitcnt(vm_wait(kCopies * (kWideS - 2)));  // this wave's copies of chunk c ...
-        __builtin_amdgcn_s_barrier();                                 // ... and every wave's
-        issue(c + kWideS - 1, (t + kWideS - 1) % kWideS);             // into the stage chunk c - 1 used
+        wait_chunk();                                      // this wave's copies of chunk c ...
+        __builtin_amdgcn_s_barrier();                      // ... and every wave's
+        issue(c + kWideS - 1, (t + kWideS - 1) % kWideS);  // into the stage chunk c - 1 used
         const uint8_t *sa = lds + t * kStage, *sb = sa + kWideMT * kWideRB;
         u32x4 a[KQ][MF], b[KQ][NF];
+        uint2 bq[KQ][NF];
+        h16 bd[KQ][NF];
 #pragma unroll
         for (int q = 0; q < KQ; q++) {
 #pragma unroll
@@ -322,10 +369,27 @@ __device__ __forceinline__ void gemm_wide_body(const h16 *__restrict__ A, int64_
 #pragma unroll
             for (int j = 0; j < NF; j++) {
                 const int row = wn * (NT / kWideWN) + 16 * j + r;
-                b[q][j] = ld16(sb + row * kWideRB + (((4 * q + g) ^ ((row + kWideMT) & 15)) << 4));
+                if (Q8) {  // k 32 q + 8 g .. + 7: half g & 1 of granule 2 q + g / 2; block q of the chunk
+                    bq[q][j] = *reinterpret_cast<const uint2 *>(sb + row * kWideKC +
+                                                                (((2 * q + (g >> 1)) ^ wide_qswz(row)) << 4) + 8 * (g & 1));
+                    bd[q][j] = reinterpret_cast<const h16 *>(sb + NT * kWideKC + row * 8)[q];
+                } else {
+                    b[q][j] = ld16(sb + row * kWideRB + (((4 * q + g) ^ ((row + kWideMT) & 15)) << 4));
+                }
             }
         }
         __builtin_amdgcn_sched_barrier(0);
+        if (Q8) {
+#pragma unroll
+            for (int q = 0; q < KQ; q++)
+#pragma unroll
+                for (int j = 0; j < NF; j++) {
+                    unsigned w[4];
+                    dequant_q8x4(bq[q][j].x, bd[q][j], w[0], w[1]);
+                    dequant_q8x4(bq[q][j].y, bd[q][j], w[2], w[3]);
+                    b[q][j] = u32x4{w[0], w[1], w[2], w[3]};
+                }
+        }
 #pragma unroll
         for (int q = 0; q < KQ; q++)
 #pragma unroll
@@ -353,40 +417,53 @@ __device__ __forceinline__ void gemm_wide_body(const h16 *__restrict__ A, int64_
             }
 }
 
-// One kernel per (epilogue, tile width); the template body above is shared.
-#define AESIR_WIDE_KERNEL(EPIV, NTV)                                                                             \
-    __global__ __launch_bounds__(kWideThreads) void gemm_wide_kernel_##EPIV##_##NTV(                            \
-        const h16 *__restrict__ A, int64_t M, int64_t K, const h16 *__restrict__ B, int64_t N, h16 *__restrict__ C, \
-        int64_t ldc, float *__restrict__ P) {                                                                    \
-        gemm_wide_body<EPIV, NTV>(A, M, K, B, N, C, ldc, P);                                                    \
+// One kernel per (epilogue, tile width, weight type); the template body above is shared.
+#define AESIR_WIDE_KERNEL(EPIV, NTV, Q8V, SUF)                                                                   \
+    __global__ __launch_bounds__(kWideThreads) void gemm_wide_kernel_##EPIV##_##NTV##SUF(                       \
+        const h16 *__restrict__ A, int64_t M, int64_t K, const void *__restrict__ B, int64_t N, h16 *__restrict__ C, \
+        int64_t ldc, float *__restrict__ P, const h16 *__restrict__ Bs) {                                         \
+        gemm_wide_body<EPIV, NTV, Q8V>(A, M, K, B, N, C, ldc, P, Bs);                                           \
     }
-AESIR_WIDE_KERNEL(0, 64)
-AESIR_WIDE_KERNEL(0, 32)
-AESIR_WIDE_KERNEL(1, 64)
-AESIR_WIDE_KERNEL(1, 32)
-AESIR_WIDE_KERNEL(2, 64)
-AESIR_WIDE_KERNEL(2, 32)
+AESIR_WIDE_KERNEL(0, 64, false, )
+AESIR_WIDE_KERNEL(0, 32, false, )
+AESIR_WIDE_KERNEL(1, 64, false, )
+AESIR_WIDE_KERNEL(1, 32, false, )
+AESIR_WIDE_KERNEL(2, 64, false, )
+AESIR_WIDE_KERNEL(2, 32, false, )
+AESIR_WIDE_KERNEL(0, 64, true, _q8)
+AESIR_WIDE_KERNEL(0, 32, true, _q8)
+AESIR_WIDE_KERNEL(1, 64, true, _q8)
+AESIR_WIDE_KERNEL(1, 32, true, _q8)
+AESIR_WIDE_KERNEL(2, 64, true, _q8)
+AESIR_WIDE_KERNEL(2, 32, true, _q8)
 #undef AESIR_WIDE_KERNEL
 
-typedef void (*WideKernelFn)(const h16 *, int64_t, int64_t, const h16 *, int64_t, h16 *, int64_t, float *);
-template <int EPI, int NT>
+typedef void (*WideKernelFn)(const h16 *, int64_t, int64_t, const void *, int64_t, h16 *, int64_t, float *,
+                             const h16 *);
+template <int EPI, int NT, bool Q8>
 static WideKernelFn wide_kernel() {
-    if constexpr (EPI == kEpiStore) return NT == 64 ? gemm_wide_kernel_0_64 : gemm_wide_kernel_0_32;
-    else if constexpr (EPI == kEpiResidual) return NT == 64 ? gemm_wide_kernel_1_64 : gemm_wide_kernel_1_32;
-    else return NT == 64 ? gemm_wide_kernel_2_64 : gemm_wide_kernel_2_32;
+    if constexpr (Q8) {
+        if constexpr (EPI == kEpiStore) return NT == 64 ? gemm_wide_kernel_0_64_q8 : gemm_wide_kernel_0_32_q8;
+        else if constexpr (EPI == kEpiResidual) return NT == 64 ? gemm_wide_kernel_1_64_q8 : gemm_wide_kernel_1_32_q8;
+        else return NT == 64 ? gemm_wide_kernel_2_64_q8 : gemm_wide_kernel_2_32_q8;
+    } else {
+        if constexpr (EPI == kEpiStore) return NT == 64 ? gemm_wide_kernel_0_64 : gemm_wide_kernel_0_32;
+        else if constexpr (EPI == kEpiResidual) return NT == 64 ? gemm_wide_kernel_1_64 : gemm_wide_kernel_1_32;
+        else return NT == 64 ? gemm_wide_kernel_2_64 : gemm_wide_kernel_2_32;
+    }
 }
 
-// Tile width and K splits of the wide-tile kernel for an f16 GEMM, or nt = 0 when the 32 x 64
-// kernel serves it (Q8_0 weights, M <= 64, K % 128 != 0, or a 32-bit byte range exceeded).
-// NT = 64 from 4096 columns up, 32 below; the split count doubles while it divides the K chunks
-// evenly, leaves at least 4 chunks per split and keeps tiles x splits within kWideWgTarget.
+// Tile width and K splits of the wide-tile kernel, or nt = 0 when the 32 x 64 kernel serves the
+// GEMM (M <= 64, K % 128 != 0, or a 32-bit byte range exceeded). NT = 64 from 4096 columns up, 32
+// below; the split count doubles while it divides the K chunks evenly, leaves at least 4 chunks per
+// split and keeps tiles x splits within kWideWgTarget.
 struct WidePlan {
     int nt;
     int64_t splits;
 };
-static WidePlan wide_plan(int64_t M, int64_t K, int64_t N, bool q8) {
+static WidePlan wide_plan(int64_t M, int64_t K, int64_t N) {
     const int64_t lim = (int64_t)1 << 31;
-    if (q8 || M <= 64 || K % kWideKC != 0 || (M + kWideMT) * K * 2 >= lim || (N + 64) * K * 2 >= lim) return {0, 1};
+    if (M <= 64 || K % kWideKC != 0 || (M + kWideMT) * K * 2 >= lim || (N + 64) * K * 2 >= lim) return {0, 1};
     const int nt = N >= 4096 ? 64 : 32;
     const int64_t tiles = ((N + nt - 1) / nt) * ((M + kWideMT - 1) / kWideMT), nkc = K / kWideKC;
     int64_t s = 1;
@@ -394,22 +471,22 @@ static WidePlan wide_plan(int64_t M, int64_t K, int64_t N, bool q8) {
     return {nt, s};
 }
 
-template <int EPI, int NT>
+template <int EPI, int NT, bool Q8>
 static int32_t launch_wide(hipStream_t s, const void *A, int64_t M, int64_t K, const void *B, int64_t N, void *C,
-                           int64_t ldc, float *part, int64_t splits) {
+                           int64_t ldc, float *part, int64_t splits, const void *Bs) {
     static std::atomic<uint64_t> lds_set{0};  // devices (bit per ordinal < 64) whose LDS limit is raised
-    constexpr int lds = kWideS * wide_stage_bytes(NT);
+    constexpr int lds = kWideS * wide_stage_bytes(NT, Q8);
     int dev = 0;
     AESIR_HIP_TRY(hipGetDevice(&dev));
     const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
     if (!bit || !(lds_set.load(std::memory_order_relaxed) & bit)) {
-        AESIR_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(wide_kernel<EPI, NT>()),
+        AESIR_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(wide_kernel<EPI, NT, Q8>()),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, lds));
         lds_set.fetch_or(bit, std::memory_order_relaxed);
     }
     const dim3 grid((unsigned)((N + NT - 1) / NT), (unsigned)((M + kWideMT - 1) / kWideMT), (unsigned)splits);
-    hipLaunchKernelGGL((wide_kernel<EPI, NT>()), grid, dim3(kWideThreads), lds, s, (const h16 *)A, M, K,
-                       (const h16 *)B, N, (h16 *)C, ldc, part);
+    hipLaunchKernelGGL((wide_kernel<EPI, NT, Q8>()), grid, dim3(kWideThreads), lds, s, (const h16 *)A, M, K, B, N,
+                       (h16 *)C, ldc, part, (const h16 *)Bs);
     return AESIR_OK;
 }
 
@@ -449,7 +526,7 @@ int64_t prefill_part_floats(int64_t rows, int64_t dim, int64_t qkv_n, int64_t ff
     int64_t most = 0;
     for (auto &kn : shapes) {
         if (kn[0] % 64 != 0) continue;
-        const WidePlan wp = wide_plan(rows, kn[0], kn[1], false);
+        const WidePlan wp = wide_plan(rows, kn[0], kn[1]);
         const int64_t sp = wp.nt ? wp.splits : gemm_splits(rows, kn[0], kn[1]);
         if (sp > 1 && sp * rows * kn[1] > most) most = sp * rows * kn[1];
     }
@@ -466,13 +543,17 @@ static int32_t launch_mfma(hipStream_t s, const void *A, int64_t M, int64_t K, c
     const int64_t gx = (N + kGemmNT - 1) / kGemmNT, gy = (M + kGemmMT - 1) / kGemmMT;
     if (gx > 2147483647 || gy > 65535) return fail(AESIR_ERR_UNSUPPORTED, "%s: GEMM grid too large", name);
     if (EPI == kEpiSwiglu && (N & 1)) return fail(AESIR_ERR_INVALID, "%s: odd gate/up column count", name);
-    if (const WidePlan wp = wide_plan(M, K, N, Bs != nullptr); wp.nt) {
+    if (const WidePlan wp = wide_plan(M, K, N); wp.nt) {
         int64_t splits = wp.splits;
         while (splits > 1 && splits * M * N > part_floats) splits /= 2;
-        if (wp.nt == 64)
-            AESIR_TRY((launch_wide<EPI, 64>(s, A, M, K, B, N, C, ldc, part, splits)));
+        if (wp.nt == 64 && Bs)
+            AESIR_TRY((launch_wide<EPI, 64, true>(s, A, M, K, B, N, C, ldc, part, splits, Bs)));
+        else if (Bs)
+            AESIR_TRY((launch_wide<EPI, 32, true>(s, A, M, K, B, N, C, ldc, part, splits, Bs)));
+        else if (wp.nt == 64)
+            AESIR_TRY((launch_wide<EPI, 64, false>(s, A, M, K, B, N, C, ldc, part, splits, nullptr)));
         else
-            AESIR_TRY((launch_wide<EPI, 32>(s, A, M, K, B, N, C, ldc, part, splits)));
+            AESIR_TRY((launch_wide<EPI, 32, false>(s, A, M, K, B, N, C, ldc, part, splits, nullptr)));
         AESIR_LAUNCH_CHECK(name);
         if (splits_out) *splits_out = splits;
         if (splits > 1 && !defer) {

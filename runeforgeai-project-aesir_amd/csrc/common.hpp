@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
@@ -39,6 +40,19 @@ void clear_error();
         if (_e != hipSuccess)                                                                      \
             return ::aesir::fail(AESIR_ERR_HIP, "launch of %s failed: %s", name, hipGetErrorString(_e)); \
     } while (0)
+
+// Raises a kernel's dynamic LDS limit to `bytes` (above the 64 KB default) once per device: HIP
+// keeps the attribute per function and device. `done` is the caller's static bitmask for that
+// kernel (bit d = device ordinal d < 64; higher ordinals set the attribute on every call).
+inline int32_t raise_lds_limit(const void *fn, int bytes, std::atomic<uint64_t> &done) {
+    int dev = 0;
+    AESIR_HIP_TRY(hipGetDevice(&dev));
+    const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
+    if (bit && (done.load(std::memory_order_relaxed) & bit)) return AESIR_OK;
+    AESIR_HIP_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
+    done.fetch_or(bit, std::memory_order_relaxed);
+    return AESIR_OK;
+}
 
 // ------------------------------------------------------------------ f16 on the host
 

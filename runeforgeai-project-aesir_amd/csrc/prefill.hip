@@ -17,7 +17,6 @@
 //   Chunks of more than 64 positions use the wide-tile kernel below (the whole chunk in one
 //   128-row M tile, 8 waves, 128-wide K chunks) instead; this 32-row kernel serves shorter chunks.
 //   At M = 128 the GEMM is HBM-bound (128 flop/byte against MI355X's 312 flop/byte ridge).
-#include <atomic>
 #include <cmath>
 #include <vector>
 
@@ -474,16 +473,9 @@ static WidePlan wide_plan(int64_t M, int64_t K, int64_t N) {
 template <int EPI, int NT, bool Q8>
 static int32_t launch_wide(hipStream_t s, const void *A, int64_t M, int64_t K, const void *B, int64_t N, void *C,
                            int64_t ldc, float *part, int64_t splits, const void *Bs) {
-    static std::atomic<uint64_t> lds_set{0};  // devices (bit per ordinal < 64) whose LDS limit is raised
+    static std::atomic<uint64_t> lds_set{0};
     constexpr int lds = kWideS * wide_stage_bytes(NT, Q8);
-    int dev = 0;
-    AESIR_HIP_TRY(hipGetDevice(&dev));
-    const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
-    if (!bit || !(lds_set.load(std::memory_order_relaxed) & bit)) {
-        AESIR_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(wide_kernel<EPI, NT, Q8>()),
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, lds));
-        lds_set.fetch_or(bit, std::memory_order_relaxed);
-    }
+    AESIR_TRY(raise_lds_limit(reinterpret_cast<const void *>(wide_kernel<EPI, NT, Q8>()), lds, lds_set));
     const dim3 grid((unsigned)((N + NT - 1) / NT), (unsigned)((M + kWideMT - 1) / kWideMT), (unsigned)splits);
     hipLaunchKernelGGL((wide_kernel<EPI, NT, Q8>()), grid, dim3(kWideThreads), lds, s, (const h16 *)A, M, K, B, N,
                        (h16 *)C, ldc, part, (const h16 *)Bs);

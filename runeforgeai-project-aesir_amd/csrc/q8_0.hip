@@ -6,7 +6,6 @@
 // otherwise single blocks with 2-byte loads. Two activation types:
 //   - f16 A (reference semantics): w = f16(f16(q) * d) per element, products summed in f32.
 //   - f32 x (block matvec): y = sum over blocks of d * sum(q * x), all in f32.
-#include <atomic>
 #include <type_traits>
 
 #include "device.hpp"
@@ -346,16 +345,8 @@ static int32_t launch_digits(hipStream_t s, const void *blocks, int64_t N, int64
     if ((int64_t)R * rowbytes + 16 > (int64_t)P * NW * 1024) return fail(AESIR_ERR_INVALID, "q8_0_matvec: stage too small");
     const unsigned lds = (unsigned)(S * P * NW * 1024);
     const void *fn = reinterpret_cast<const void *>(q8_0_digits_kernel<NW, PH, RT, S, P>);
-    static std::atomic<uint64_t> lds_set{0};  // devices (bit per ordinal < 64) whose LDS limit is raised
-    if (lds > 65536) {
-        int dev = 0;
-        AESIR_HIP_TRY(hipGetDevice(&dev));
-        const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
-        if (!bit || !(lds_set.load(std::memory_order_relaxed) & bit)) {
-            AESIR_HIP_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-            lds_set.fetch_or(bit, std::memory_order_relaxed);
-        }
-    }
+    static std::atomic<uint64_t> lds_set{0};
+    if (lds > 65536) AESIR_TRY(raise_lds_limit(fn, (int)lds, lds_set));
     const int64_t ng = (N + R - 1) / R;
     const int64_t grid = ng < (int64_t)kCus * wg_per_cu ? ng : (int64_t)kCus * wg_per_cu;
     hipLaunchKernelGGL((q8_0_digits_kernel<NW, PH, RT, S, P>), dim3((unsigned)grid), dim3(NW * 64), lds, s,

@@ -28,10 +28,13 @@
 namespace aesir {
 
 
-// Rows of A per workgroup tile and the workgroup count the K splits aim for. Measured on MI355X
-// (TinyLlama 128-token prefill, ms): M tile 128 / 256 workgroups 2.39; 64 / 256 2.31; 64 / 512
-// 2.23; 32 / 512 2.22; 32 / 1024 2.37. Smaller tiles re-read the weights from L2 (one HBM read)
-// but copy less of A per workgroup and fit more workgroups per CU.
+// Rows of A per workgroup tile and the workgroup count the K splits aim for in this 4-wave kernel
+// with 64-wide K chunks. Measured on MI355X (TinyLlama 128-token prefill, ms, when this kernel
+// served every chunk): M tile 128 / 256 workgroups 2.39; 64 / 256 2.31; 64 / 512 2.23; 32 / 512
+// 2.22; 32 / 1024 2.37. Smaller tiles re-read the weights from L2 (one HBM read) but copy less of
+// A per workgroup and fit more workgroups per CU. (The 8-wave wide-tile kernel below, with
+// 128-wide chunks, does better with the whole 128-row chunk in one tile; this kernel now serves
+// chunks of 64 rows or fewer.)
 constexpr int kGemmMT = 32;
 constexpr int kGemmWgTarget = 512;
 constexpr int kGemmMF = kGemmMT / 16;   // MFMA row fragments per wave

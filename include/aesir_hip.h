@@ -259,6 +259,14 @@ int32_t aesir_gguf_inspect(const char *path, aesir_model_config *cfg, float *rop
  * and argmax. Waits; *next_token is the greedy token. */
 int32_t aesir_forward_pass(aesir_model *model, const int64_t *tokens, int64_t n_tokens, int64_t start_pos,
                            int64_t *next_token);
+/* The forward_pass overload without an explicit KVCache (core/inference.mojo:521-547): a fresh
+ * cache of llama.context_length rows, then tokens[n_tokens - 1] evaluated at position
+ * start_pos = n_tokens - 1 (0 for an empty list, which returns token 0). The reference carves the
+ * new cache from never-used, zeroed well memory; here the model's own cache serves as that fresh
+ * cache: rows [0, min(start_pos, ctx_len)) of every layer are cleared first (earlier contents
+ * are lost). Waits; *next_token is the greedy token. */
+int32_t aesir_forward_pass_no_cache(aesir_model *model, const int64_t *tokens, int64_t n_tokens,
+                                    int64_t *next_token);
 /* Batched prefill: the same result as forward_pass at each position start_pos .. start_pos +
  * n_tokens - 1 in turn (the per-position prefill loop of _run_generation, aesir.mojo:358-374),
  * computed with all positions of a 128-row chunk going through each layer together: MFMA f16

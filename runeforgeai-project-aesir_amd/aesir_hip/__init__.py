@@ -97,6 +97,7 @@ _sig("aesir_model_init_random", [P, C.c_uint64, F32, F32, F32])
 _sig("aesir_model_load_gguf", [P, C.c_char_p, I64, C.POINTER(P)])
 _sig("aesir_gguf_inspect", [C.c_char_p, C.POINTER(_ModelConfig), C.POINTER(F32)])
 _sig("aesir_forward_pass", [P, P, I64, I64, C.POINTER(I64)])
+_sig("aesir_forward_pass_no_cache", [P, P, I64, C.POINTER(I64)])
 _sig("aesir_model_logits", [P, P])
 _sig("aesir_decode_loop", [P, I64, I64, I64, I32, P, C.POINTER(F32)])
 _sig("aesir_model_kernel_times", [P, I64, I32, P, I32])
@@ -491,6 +492,14 @@ class Model:
         t = np.ascontiguousarray(np.array(tokens, dtype=np.int64))
         out = I64()
         _check(_L.aesir_forward_pass(self.h, t.ctypes.data if t.size else None, t.size, start_pos, C.byref(out)))
+        return out.value
+
+    def forward_pass_no_cache(self, tokens) -> int:
+        """forward_pass without an explicit KVCache (core/inference.mojo:521-547): the last token at
+        position len(tokens) - 1 over a fresh (zeroed) cache; the model's cache is cleared first."""
+        t = np.ascontiguousarray(np.array(tokens, dtype=np.int64))
+        out = I64()
+        _check(_L.aesir_forward_pass_no_cache(self.h, t.ctypes.data if t.size else None, t.size, C.byref(out)))
         return out.value
 
     def prefill(self, tokens, start_pos: int = 0) -> int:

@@ -54,6 +54,43 @@ inline int32_t raise_lds_limit(const void *fn, int bytes, std::atomic<uint64_t> 
     return AESIR_OK;
 }
 
+// ------------------------------------------------------------------ checked sizes
+
+// a * b, or -1 when an operand is negative or the product overflows int64 (sizes derived from
+// file metadata must never wrap).
+inline int64_t mul_checked(int64_t a, int64_t b) {
+    int64_t r;
+    if (a < 0 || b < 0 || __builtin_mul_overflow(a, b, &r)) return -1;
+    return r;
+}
+inline int64_t mul_checked(int64_t a, int64_t b, int64_t c) { return a < 0 || b < 0 ? -1 : mul_checked(mul_checked(a, b), c); }
+inline int64_t mul_checked(int64_t a, int64_t b, int64_t c, int64_t d) {
+    return mul_checked(mul_checked(a, b, c), d);
+}
+
+// GGML block geometry: elements per block and bytes per block of a tensor type (0 if the type
+// is not one this library stores).
+struct GgmlBlock {
+    int64_t elems, bytes;
+};
+inline GgmlBlock ggml_block(int64_t type) {
+    switch (type) {
+        case AESIR_GGML_F32: return {1, 4};
+        case AESIR_GGML_F16: return {1, 2};
+        case AESIR_GGML_Q8_0: return {32, 34};
+        default: return {0, 0};
+    }
+}
+// Bytes of a rows x cols tensor of a GGML type: -1 for an unknown type, -2 when cols is not a
+// multiple of the block, -3 on overflow.
+inline int64_t ggml_tensor_bytes(int64_t type, int64_t rows, int64_t cols) {
+    const GgmlBlock b = ggml_block(type);
+    if (b.elems == 0) return -1;
+    if (cols % b.elems != 0) return -2;
+    const int64_t r = mul_checked(rows, cols / b.elems, b.bytes);
+    return r < 0 ? -3 : r;
+}
+
 // ------------------------------------------------------------------ f16 on the host
 
 uint16_t f32_to_f16_bits(float f);  // round to nearest even

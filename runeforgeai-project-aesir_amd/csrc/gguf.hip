@@ -247,24 +247,17 @@ int32_t parse(Gguf &g, const char *path) {
     AESIR_TRY(g.need(data_offset, 0));
     for (auto &t : raw) {  // _map_tensor (loader/gguf.mojo:465-499)
         if (g.by_name.count(t.name)) return fail(AESIR_ERR_FORMAT, "GGUF contains a duplicate tensor name: %s", t.name.c_str());
-        const int64_t n = t.rows * t.cols;
-        int64_t bytes;
-        if (t.type == AESIR_GGML_F16) {
-            if (n > g.size / 2) return fail(AESIR_ERR_FORMAT, "GGUF F16 tensor byte size overflows the file");
-            bytes = n * 2;
-        } else if (t.type == AESIR_GGML_F32) {
-            if (n > g.size / 4) return fail(AESIR_ERR_FORMAT, "GGUF F32 tensor byte size overflows the file");
-            bytes = n * 4;
-        } else if (t.type == AESIR_GGML_Q8_0) {  // beyond the reference loader: 34-byte blocks of 32
-            if (t.cols % 32 != 0)
-                return fail(AESIR_ERR_FORMAT, "GGUF Q8_0 tensor row length is not a multiple of 32: %s", t.name.c_str());
-            if (n / 32 > g.size / 34) return fail(AESIR_ERR_FORMAT, "GGUF Q8_0 tensor byte size overflows the file");
-            bytes = n / 32 * 34;
-        } else {
-            return fail(AESIR_ERR_FORMAT, "Real inference slice supports only F16 and F32 tensors");
-        }
+        // F16 and F32 as the reference loader; the block types beyond it (Q8_0) by their GGML
+        // block geometry. Every size product is overflow-checked before any range check.
+        const int64_t bytes = ggml_tensor_bytes(t.type, t.rows, t.cols);
+        if (bytes == -1) return fail(AESIR_ERR_FORMAT, "Real inference slice supports only F16 and F32 tensors");
+        if (bytes == -2)
+            return fail(AESIR_ERR_FORMAT, "GGUF tensor row length is not a multiple of its block size: %s", t.name.c_str());
+        if (bytes < 0 || bytes > g.size)
+            return fail(AESIR_ERR_FORMAT, "GGUF tensor byte size overflows the file: %s", t.name.c_str());
         if (t.offset < 0 || t.offset % g.alignment != 0)
             return fail(AESIR_ERR_FORMAT, "GGUF tensor offset is not correctly aligned: %s", t.name.c_str());
+        if (t.offset > g.size) return fail(AESIR_ERR_FORMAT, "GGUF is truncated or contains an out-of-range offset");
         t.offset += data_offset;
         AESIR_TRY(g.need(t.offset, bytes));
         g.by_name[t.name] = g.tensors.size();

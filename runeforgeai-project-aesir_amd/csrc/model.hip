@@ -336,6 +336,10 @@ int32_t aesir_model_create_typed(aesir_ctx *ctx, const aesir_model_config *cfg, 
     if (c.dim % c.n_heads != 0) return fail(AESIR_ERR_FORMAT, "GGUF embedding length is not divisible by head count");
     if (c.n_heads % c.n_kv_heads != 0) return fail(AESIR_ERR_FORMAT, "GGUF query heads are not divisible by KV heads");
     if (c.vocab <= 0) return fail(AESIR_ERR_FORMAT, "GGUF vocabulary is empty");
+    // Dimensions up to 2^31 keep every sum below exact; every product is checked where it is formed.
+    const int64_t lim = (int64_t)1 << 31;
+    if (c.dim > lim || c.ffn > lim || c.vocab > lim || c.ctx_len > lim || c.n_layers > lim)
+        return fail(AESIR_ERR_FORMAT, "model: a dimension exceeds 2^31");
     if (!(c.rms_eps > 0.0f)) return fail(AESIR_ERR_INVALID, "rmsnorm: epsilon must be positive");
     const int64_t hd = c.dim / c.n_heads;
     if (hd % 2 != 0) return fail(AESIR_ERR_INVALID, "apply_rope: head_dim must be positive and even");
@@ -361,13 +365,16 @@ int32_t aesir_model_create_typed(aesir_ctx *ctx, const aesir_model_config *cfg, 
         return rc;
     };
     int32_t rc = AESIR_OK;
+    // Every size below is a checked product (mul_checked is -1 on overflow): a config read from
+    // a file must not wrap into a small allocation.
     auto take = [&](int64_t bytes, void **p) {
+        if (rc == AESIR_OK && bytes < 0) rc = fail(AESIR_ERR_FORMAT, "model: a tensor size overflows int64");
         if (rc == AESIR_OK) rc = carve(ctx, bytes, p);
     };
     // a matrix of rows x cols: f16, or int8 quants plus f16 block scales (Q8_0)
     auto matrix = [&](int64_t rows, int64_t cols, void **w, void **scale) {
-        take(rows * cols * (q8 ? 1 : 2), w);
-        if (q8) take(rows * (cols / 32) * 2, scale);
+        take(mul_checked(rows, cols, q8 ? 1 : 2), w);
+        if (q8) take(mul_checked(rows, cols / 32, 2), scale);
     };
     matrix(V, d, &m->tok_embd, &m->tok_embd_s);
     take(d * 2, &m->out_norm);
@@ -381,8 +388,8 @@ int32_t aesir_model_create_typed(aesir_ctx *ctx, const aesir_model_config *cfg, 
         matrix(2 * f, d, &L.wgu, &L.sgu);
         matrix(d, f, &L.wdown, &L.sdown);
     }
-    take(c.n_layers * c.ctx_len * kvd * 2, &m->k_cache);
-    take(c.n_layers * c.ctx_len * kvd * 2, &m->v_cache);
+    take(mul_checked(c.n_layers, c.ctx_len, kvd, 2), &m->k_cache);
+    take(mul_checked(c.n_layers, c.ctx_len, kvd, 2), &m->v_cache);
     take(d * 2, &m->x);
     take(d * 2, &m->q);
     take(d * 2, &m->attn);
@@ -519,6 +526,26 @@ int32_t aesir_forward_pass(aesir_model *m, const int64_t *tokens, int64_t n_toke
     if (tok < 0 || tok >= m->cfg.vocab) return fail(AESIR_ERR_INVALID, "Prompt token ID is outside the embedding vocabulary");
     AESIR_TRY(ensure_rope(m, start_pos + 1));
     return model_step(m, tok, start_pos, next_token);
+}
+
+int32_t aesir_forward_pass_no_cache(aesir_model *m, const int64_t *tokens, int64_t n_tokens, int64_t *next_token) {
+    if (!m || !next_token) return fail(AESIR_ERR_INVALID, "forward_pass: null argument");
+    AESIR_TRY(bind(m->ctx));
+    if (n_tokens <= 0) {  // start_pos 0 over an empty list: inference.mojo:446-447
+        *next_token = 0;
+        return AESIR_OK;
+    }
+    // inference.mojo:543-546: a new KVCache carved from never-used (zeroed) well memory, then
+    // the last token at position len - 1. The rows that attention reads besides the one this
+    // step appends are rows [0, min(start_pos, ctx_len)) of every layer: clear them.
+    const int64_t start_pos = n_tokens - 1;
+    const int64_t rows = start_pos < m->cfg.ctx_len ? start_pos : m->cfg.ctx_len;
+    if (rows > 0) {
+        const size_t pitch = (size_t)(m->cfg.ctx_len * m->kvd * 2), width = (size_t)(rows * m->kvd * 2);
+        AESIR_HIP_TRY(hipMemset2DAsync(m->k_cache, pitch, 0, width, (size_t)m->cfg.n_layers, m->ctx->stream));
+        AESIR_HIP_TRY(hipMemset2DAsync(m->v_cache, pitch, 0, width, (size_t)m->cfg.n_layers, m->ctx->stream));
+    }
+    return aesir_forward_pass(m, tokens, n_tokens, start_pos, next_token);
 }
 
 int32_t aesir_model_logits(aesir_model *m, void *host_out) {

@@ -102,8 +102,10 @@ def test_gguf_freq_base_recorded_not_applied(A, oracle, tiny_gguf):
     ("rope_dim", "GGUF RoPE dimension does not match attention head size"),
     ("alignment", "GGUF alignment must be a power of two up to 4096"),
     ("eos", "Tokenizer eos_token_id is out of bounds"),
-    ("q4", "Real inference slice supports only F16 and F32 tensors"),
+    ("q4_1", "Real inference slice supports only F16 and F32 tensors"),
     ("q8_mixed", "GGUF required tensor has an invalid type: output.weight"),
+    ("overflow", "GGUF tensor byte size overflows the file: token_embd.weight"),
+    ("huge", "GGUF tensor byte size overflows the file: token_embd.weight"),
 ])
 def test_gguf_contract_errors(A, tiny_gguf, mutation, message):
     """loader/gguf.mojo:405-628 error paths, with the reference's message text."""
@@ -146,14 +148,21 @@ def test_gguf_contract_errors(A, tiny_gguf, mutation, message):
         size = os.path.getsize(path)
         with open(path, "r+b") as f:
             f.truncate(size - 100)
-    if mutation == "q4":
-        # rewrite the type field of the first tensor to GGML Q4_0 (2), which neither loader takes
+    if mutation in ("q4_1", "overflow", "huge"):
+        # q4_1: rewrite the type field of the first tensor to GGML Q4_1 (3), which neither loader
+        # takes; overflow: dims whose element count wraps int64 (2^33 x 2^31); huge: dims whose
+        # byte size fits int64 but exceeds the file (2^20 x 2^20)
         raw = bytearray(open(path, "rb").read())
         name = b"token_embd.weight"
         i = raw.index(name) + len(name)
         ndim = int.from_bytes(raw[i:i + 4], "little")
         tpos = i + 4 + 8 * ndim
-        raw[tpos:tpos + 4] = (2).to_bytes(4, "little")
+        if mutation == "q4_1":
+            raw[tpos:tpos + 4] = (3).to_bytes(4, "little")
+        else:
+            ne0, ne1 = (1 << 33, 1 << 31) if mutation == "overflow" else (1 << 20, 1 << 20)
+            raw[i + 4:i + 12] = ne0.to_bytes(8, "little")
+            raw[i + 12:i + 20] = ne1.to_bytes(8, "little")
         open(path, "wb").write(bytes(raw))
     with pytest.raises(A.AesirError, match=re.escape(message)):
         A.gguf_inspect(path)
@@ -207,5 +216,5 @@ def test_gguf_inspect_q8_0_file(A, oracle, tmp_path):
 
     tensors["blk.0.ffn_down.weight"] = SimpleNamespace(blocks=np.zeros((160, 34), np.uint8), rows=64, cols=80)
     write_gguf(path, llama_metadata(cfg, cfg.vocab), tensors)
-    with pytest.raises(A.AesirError, match="Q8_0 tensor row length is not a multiple of 32: blk.0.ffn_down.weight"):
+    with pytest.raises(A.AesirError, match="GGUF tensor row length is not a multiple of its block size: blk.0.ffn_down.weight"):
         A.gguf_inspect(path)

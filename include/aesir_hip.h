@@ -124,6 +124,21 @@ int32_t aesir_attn_gqa_decode(aesir_ctx *ctx, const void *query, int64_t query_r
                               int64_t output_rows, int64_t seq_len, int64_t head_dim, int64_t nq,
                               int64_t nkv);
 
+/* Allocation-free variant of aesir_attn_gqa_decode; it has no counterpart in the reference. It is
+ * for callers that cannot allocate device memory: code under HIP graph capture, tight serving
+ * loops and harnesses that forbid hipMalloc. It takes no context: work is enqueued on `stream`
+ * (a hipStream_t; NULL is the null stream) of the calling thread's current device. Same
+ * arguments, checks and results as aesir_attn_gqa_decode, with the split partials held in a
+ * static 4 MiB device array per GPU (2^20 floats: nq * splits * (head_dim + 2) must fit; the
+ * split count is halved until it does, and sizes that do not fit with one split are rejected
+ * with AESIR_ERR_UNSUPPORTED). It calls no allocator. All calls on one GPU share that array:
+ * calls that overlap on one GPU (two streams, or two host threads) race and must be ordered by
+ * the caller. */
+int32_t aesir_attn_gqa_decode_static(void *stream, const void *query, int64_t query_rows, const void *keys,
+                                     int64_t keys_cols, const void *values, int64_t values_cols, void *output,
+                                     int64_t output_rows, int64_t seq_len, int64_t head_dim, int64_t nq,
+                                     int64_t nkv);
+
 /* silu (core/compute.mojo:2113-2126), in place; size <= 0 is a no-op. */
 int32_t aesir_silu_f16(aesir_ctx *ctx, void *T, int64_t size);
 /* SwiGLU as TransformerBlock.forward does it (core/inference.mojo:258-260): silu(gate) in

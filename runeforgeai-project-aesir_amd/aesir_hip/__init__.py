@@ -74,6 +74,7 @@ _sig("aesir_gemm_f16", [P, P, I64, I64, P, I64, I64, P, I64, I64])
 _sig("aesir_rmsnorm_f16", [P, P, I64, I64, P, I64, F32])
 _sig("aesir_rope_f16", [P, P, I64, I64, P, I64, I64, I64, I64, F32])
 _sig("aesir_attn_gqa_decode", [P, P, I64, P, I64, P, I64, P, I64, I64, I64, I64, I64])
+_sig("aesir_attn_gqa_decode_static", [P, P, I64, P, I64, P, I64, P, I64, I64, I64, I64, I64])
 _sig("aesir_silu_f16", [P, P, I64])
 _sig("aesir_swiglu_f16", [P, P, P, I64])
 _sig("aesir_residual_add_f16", [P, P, P, I64])

@@ -3,6 +3,7 @@
 // Each validates exactly as the reference function does, with the reference's message text,
 // then enqueues the gfx950 kernel on the context stream.
 #include <cmath>
+#include <mutex>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -51,14 +52,20 @@ int32_t aesir_rope_f16(aesir_ctx *ctx, void *Q, int64_t q_rows, int64_t q_cols, 
     return launch_rope(ctx->stream, Q, q_rows, q_cols, K, k_cols, start_pos, head_dim, table);
 }
 
-int32_t aesir_attn_gqa_decode(aesir_ctx *ctx, const void *query, int64_t query_rows, const void *keys,
-                              int64_t keys_cols, const void *values, int64_t values_cols, void *output,
-                              int64_t output_rows, int64_t seq_len, int64_t head_dim, int64_t nq, int64_t nkv) {
-    AESIR_TRY(bind(ctx));
-    // compute.mojo:1961-1966: silent no-ops
+}  // extern "C"
+
+// Validation and argument set-up shared by the two attention entry points. *skip is set for the
+// inputs on which the reference returns silently (compute.mojo:1961-1966); the split count is
+// halved until the partials fit `part_cap` floats.
+static int32_t attn_args_for_call(const void *query, int64_t query_rows, const void *keys, int64_t keys_cols,
+                                  const void *values, int64_t values_cols, void *output, int64_t output_rows,
+                                  int64_t seq_len, int64_t head_dim, int64_t nq, int64_t nkv, int64_t part_cap,
+                                  const char *scratch_name, AttnArgs *out, bool *skip) {
+    *skip = true;
     if (seq_len <= 0 || query_rows != 1 || output_rows != 1) return AESIR_OK;
     if (nq <= 0 || nkv <= 0 || head_dim <= 0) return AESIR_OK;
     if (nq % nkv != 0) return AESIR_OK;
+    *skip = false;
     if (!query || !keys || !values || !output) return fail(AESIR_ERR_INVALID, "flash_attention_gqa: null tensor pointer");
     if (nkv * head_dim > keys_cols || nkv * head_dim > values_cols)
         return fail(AESIR_ERR_SHAPE, "flash_attention_gqa: key/value rows narrower than kv_heads * head_dim");
@@ -77,14 +84,77 @@ int32_t aesir_attn_gqa_decode(aesir_ctx *ctx, const void *query, int64_t query_r
     a.state = nullptr;
     a.max_seq = seq_len;
     int64_t max_split = attention_split_count(head_dim, seq_len);
-    while (max_split > 1 && attention_partial_floats(nq, head_dim, max_split) > ctx->scratch.attn_part_floats)
-        max_split >>= 1;
-    if (attention_partial_floats(nq, head_dim, max_split) > ctx->scratch.attn_part_floats)
-        return fail(AESIR_ERR_UNSUPPORTED, "flash_attention_gqa: %lld heads x %lld dims exceed the context scratch",
-                    (long long)nq, (long long)head_dim);
+    while (max_split > 1 && attention_partial_floats(nq, head_dim, max_split) > part_cap) max_split >>= 1;
+    if (attention_partial_floats(nq, head_dim, max_split) > part_cap)
+        return fail(AESIR_ERR_UNSUPPORTED, "flash_attention_gqa: %lld heads x %lld dims exceed the %s of %lld floats",
+                    (long long)nq, (long long)head_dim, scratch_name, (long long)part_cap);
     a.max_split = max_split;
+    *out = a;
+    return AESIR_OK;
+}
+
+// ------------------------------------------------------------------ allocation-free attention
+//
+// Scratch of aesir_attn_gqa_decode_static: the split partials (m, l, acc) live in this
+// file-scope array, one copy per GPU for the life of the process, so that entry point calls no
+// allocator. Host code never passes `scratch` itself (in host code it names a host-side stand-in):
+// the device address of each GPU's copy comes from hipGetSymbolAddress, taken once per device on
+// that device's first call, and only that address reaches kernels.
+constexpr int64_t kStaticAttnFloats = (int64_t)1 << 20;  // 4 MiB per GPU
+static __device__ __align__(256) float scratch[kStaticAttnFloats];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+float *g_scratch_ptr[kMaxScratchDevices];  // device address of `scratch`, by device ordinal
+}  // namespace
+
+static int32_t static_attn_scratch(float **out) {
+    int dev = 0;
+    AESIR_HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxScratchDevices)
+        return fail(AESIR_ERR_UNSUPPORTED, "flash_attention_gqa (static): device ordinal %d exceeds %d", dev,
+                    kMaxScratchDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(AESIR_ERR_HIP, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(e));
+        g_scratch_ptr[dev] = (float *)p;
+    }
+    *out = g_scratch_ptr[dev];
+    return AESIR_OK;
+}
+
+extern "C" {
+
+int32_t aesir_attn_gqa_decode(aesir_ctx *ctx, const void *query, int64_t query_rows, const void *keys,
+                              int64_t keys_cols, const void *values, int64_t values_cols, void *output,
+                              int64_t output_rows, int64_t seq_len, int64_t head_dim, int64_t nq, int64_t nkv) {
+    AESIR_TRY(bind(ctx));
+    AttnArgs a{};
+    bool skip = true;
+    AESIR_TRY(attn_args_for_call(query, query_rows, keys, keys_cols, values, values_cols, output, output_rows, seq_len,
+                                 head_dim, nq, nkv, ctx->scratch.attn_part_floats, "context scratch", &a, &skip));
+    if (skip) return AESIR_OK;
     a.part = ctx->scratch.attn_part;
     return launch_attention_decode(ctx->stream, a);
+}
+
+int32_t aesir_attn_gqa_decode_static(void *stream, const void *query, int64_t query_rows, const void *keys,
+                                     int64_t keys_cols, const void *values, int64_t values_cols, void *output,
+                                     int64_t output_rows, int64_t seq_len, int64_t head_dim, int64_t nq, int64_t nkv) {
+    clear_error();
+    AttnArgs a{};
+    bool skip = true;
+    AESIR_TRY(attn_args_for_call(query, query_rows, keys, keys_cols, values, values_cols, output, output_rows, seq_len,
+                                 head_dim, nq, nkv, kStaticAttnFloats, "static scratch", &a, &skip));
+    if (skip) return AESIR_OK;
+    float *part = nullptr;
+    AESIR_TRY(static_attn_scratch(&part));
+    a.part = part;
+    return launch_attention_decode((hipStream_t)stream, a);
 }
 
 int32_t aesir_silu_f16(aesir_ctx *ctx, void *T, int64_t size) {

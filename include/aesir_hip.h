@@ -159,10 +159,11 @@ int32_t aesir_argmax_f16(aesir_ctx *ctx, const void *logits, int64_t n, int64_t 
  * w = f16(f16(q) * d); C = f16(sum f32(A) * f32(w)). a_cols must be a multiple of 32. */
 int32_t aesir_gemm_q8_0(aesir_ctx *ctx, const void *A, int64_t a_rows, int64_t a_cols, const void *blocks,
                         int64_t b_rows, void *C, int64_t c_rows, int64_t c_cols);
-/* Q8_0 block matvec with f32 activations and f32 output: y[n] = sum_k x[k] * d*q, to f32
- * accuracy (within 2^-17 of sum_k |x[k] * d*q| of the exact sum; rows of 64-512 blocks use exact
- * integer dot products on x held as 22-bit fixed point per block). An inf or NaN in x propagates
- * as in the f32 formula. */
+/* Q8_0 block matvec with f32 activations and f32 output: y[n] = sum_k x[k] * d*q. Rows of
+ * 64-512 blocks use exact integer dot products on x held as 30-bit fixed point per block: each
+ * block's value is within 2^-30 * max|x_blk| * sum|d*q| of the exact block dot product (plus one
+ * f32 rounding), and the block values are summed in f32. Other shapes use the f32 formula. An inf
+ * or NaN in x propagates as in the f32 formula. */
 int32_t aesir_q8_0_matvec_f32(aesir_ctx *ctx, const void *blocks, int64_t n_rows, int64_t k, const float *x,
                               float *y);
 

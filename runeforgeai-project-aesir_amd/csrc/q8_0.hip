@@ -180,12 +180,15 @@ __global__ __launch_bounds__(kQThreads) void q8_0_staged_kernel(const uint8_t *_
 // f32 matvec on rows of nb = 64, 128, 256, 448 or 512 blocks: x as integer digits, persistent
 // workgroups with an LDS ring.
 //   - Thread t owns block column b = t % nb of a row phase ph = t / nb (PH = 64 NW / nb phases).
-//     It holds its 32 x values as a fixed-point integer v = rint(x * 2^(21 - e)), e = ilogb of the
-//     block's largest |x| (|v| <= 2^22, rounding error <= 2^-22 of that largest |x|), split into
-//     three signed 8-bit digits v = d0 + 2^8 d1 + 2^16 d2 packed four to a dword (24 registers).
-//   - Per row the block's 32 quants meet each digit in 8 v_dot4_i32_i8 (exact integer sums); the
-//     three sums are recombined in f32 (exact up to the final rounding), scaled by 2^(e - 21)
-//     (v_ldexp) and by the block scale d. A block whose x holds an inf or NaN takes the plain f32
+//     It holds its 32 x values as a fixed-point integer v = rint(x * 2^(29 - e)), e = ilogb of the
+//     block's largest |x| (|v| <= 2^30, rounding error <= 2^(e - 30) <= 2^-30 of that largest
+//     |x|), split into four signed 8-bit digits v = d0 + 2^8 d1 + 2^16 d2 + 2^24 d3 packed four to
+//     a dword (32 registers).
+//   - Per row the block's 32 quants meet each digit in 8 v_dot4_i32_i8 (exact integer sums, each
+//     below 2^20 in magnitude); the four sums are recombined exactly in f64 (below 2^44), then
+//     multiplied by the block scale d and by 2^(e - 29) and rounded to f32. So a block's value is
+//     within 2^-30 * max|x_blk| * sum|d q| (plus one f32 rounding) of the exact block dot product;
+//     the block values are summed in f32. A block whose x holds an inf or NaN takes the plain f32
 //     product instead, so such inputs propagate as in the f32 formula.
 //   - Workgroup g handles row groups g, g + G, ... of R = PH RT rows; each group's contiguous byte
 //     span is copied by 16-byte buffer loads with the LDS destination into one of S stages, S - 1
@@ -207,7 +210,7 @@ __global__ __launch_bounds__(NW * 64) void q8_0_digits_kernel(const uint8_t *__r
     const int b = tid % NB, ph = tid / NB;
     const int64_t ng = (N + R - 1) / R;
     const float *xb = x + 32 * b;
-    int dg[3][8];
+    int dg[4][8];
     int ex;
     bool plain;
     {
@@ -224,26 +227,28 @@ __global__ __launch_bounds__(NW * 64) void q8_0_digits_kernel(const uint8_t *__r
         ex = m > 0.0f && !plain ? ilogbf(m) : 0;
 #pragma unroll
         for (int w = 0; w < 8; w++) {
-            unsigned p[3] = {0u, 0u, 0u};
+            unsigned p[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                const int v = plain ? 0 : (int)rintf(ldexpf(xv[4 * w + k], 21 - ex));
+                const int v = plain ? 0 : (int)rintf(ldexpf(xv[4 * w + k], 29 - ex));  // |v| <= 2^30
                 const int d0 = (int)(int8_t)(v & 0xff);
                 const int r1 = (v - d0) >> 8;
                 const int d1 = (int)(int8_t)(r1 & 0xff);
-                const int d2 = (r1 - d1) >> 8;
+                const int r2 = (r1 - d1) >> 8;
+                const int d2 = (int)(int8_t)(r2 & 0xff);
+                const int d3 = (r2 - d2) >> 8;  // |d3| <= 64
                 p[0] |= (unsigned)(d0 & 0xff) << (8 * k);
                 p[1] |= (unsigned)(d1 & 0xff) << (8 * k);
                 p[2] |= (unsigned)(d2 & 0xff) << (8 * k);
+                p[3] |= (unsigned)(d3 & 0xff) << (8 * k);
             }
-            dg[0][w] = (int)p[0];
-            dg[1][w] = (int)p[1];
-            dg[2][w] = (int)p[2];
+#pragma unroll
+            for (int j = 0; j < 4; j++) dg[j][w] = (int)p[j];
         }
     }
     // the digits are in registers before the first copy is issued (no x load left in flight)
 #pragma unroll
-    for (int w = 0; w < 8; w++) asm volatile("" : "+v"(dg[0][w]), "+v"(dg[1][w]), "+v"(dg[2][w]));
+    for (int w = 0; w < 8; w++) asm volatile("" : "+v"(dg[0][w]), "+v"(dg[1][w]), "+v"(dg[2][w]), "+v"(dg[3][w]));
     auto issue = [&](int64_t g, int stage) {
         int64_t rows = N - g * R;
         rows = rows < 0 ? 0 : rows > R ? R : rows;
@@ -292,16 +297,18 @@ __global__ __launch_bounds__(NW * 64) void q8_0_digits_kernel(const uint8_t *__r
             for (int rr = 0; rr < RT; rr++) {
                 uint32_t w[9];
                 block_words(rr, w);
-                int s0 = 0, s1 = 0, s2 = 0;
+                int s0 = 0, s1 = 0, s2 = 0, s3 = 0;
 #pragma unroll
                 for (int i = 0; i < 8; i++) {
                     const int q = (int)__builtin_amdgcn_alignbyte(w[i + 1], w[i], 2);  // quants 4i .. 4i + 3
                     s0 = __builtin_amdgcn_sdot4(q, dg[0][i], s0, false);
                     s1 = __builtin_amdgcn_sdot4(q, dg[1][i], s1, false);
                     s2 = __builtin_amdgcn_sdot4(q, dg[2][i], s2, false);
+                    s3 = __builtin_amdgcn_sdot4(q, dg[3][i], s3, false);
                 }
-                const float v = fmaf((float)s2, 65536.0f, fmaf((float)s1, 256.0f, (float)s0));
-                acc[rr] = ldexpf((float)bits_to_h((uint16_t)(w[0] & 0xffff)) * v, ex - 21);
+                // exact in f64: |s_j| < 2^20, the sum < 2^44
+                const double v = fma((double)s3, 16777216.0, fma((double)s2, 65536.0, fma((double)s1, 256.0, (double)s0)));
+                acc[rr] = (float)ldexp(v * (double)bits_to_h((uint16_t)(w[0] & 0xffff)), ex - 29);
             }
         } else {
 #pragma unroll

@@ -448,6 +448,33 @@ def test_q8_0_matvec_f32_closed_form(A, ctx, N, K):
     assert np.all(np.abs(got - ref) <= noise)
 
 
+@pytest.mark.parametrize("K", [2048, 4096, 14336, 16384])
+def test_q8_0_matvec_f32_outlier_blocks(A, ctx, K):
+    """Activations with outlier channels: every block holds 1000 beside N(0, 1e-3) values and the
+    outlier's quant is 0, so the small values carry the dot product. The GPU equals the sum of the
+    emulated digit-kernel block values (q8_digits.py) up to f32 summation over blocks, and stays
+    within the stated bound of the exact f64 result: 2^-30 * max|x_blk| * sum|d q| per block plus
+    f32 rounding and summation."""
+    from q8_digits import block_bound, block_values
+
+    N, nb = 96, K // 32
+    blocks, d, q = make_q8_0(N, K, RNG)
+    x = (RNG.standard_normal(K) * 1e-3).astype(np.float32)
+    x[::32] = 1000.0
+    q = q.reshape(N, nb, 32).copy()
+    q[:, :, 0] = 0
+    blocks[:, 2:] = q.reshape(-1, 32).view(np.uint8)
+    y = ctx.tensor(1, N, np.float32)
+    A.q8_0_matvec_f32(ctx, upload_bytes(ctx, blocks), N, K, ctx.from_numpy(x, np.float32), y)
+    got = y.numpy()[0].astype(np.float64)
+    dd = d.reshape(N, nb)
+    emu = block_values(x.reshape(nb, 32), q, dd).astype(np.float64)
+    sum_noise = 2.0 ** -20 * np.abs(emu).sum(axis=1)
+    assert np.all(np.abs(got - emu.sum(axis=1)) <= sum_noise)
+    exact = (q.astype(np.float64) * dd.astype(np.float64)[:, :, None]).reshape(N, K) @ x.astype(np.float64)
+    assert np.all(np.abs(got - exact) <= block_bound(x.reshape(nb, 32), q, dd).sum(axis=1) + sum_noise)
+
+
 @pytest.mark.parametrize("K", [4096, 14336])
 def test_q8_0_matvec_f32_non_finite_x(A, ctx, K):
     """An inf in x reaches every row as in the f32 formula (+-inf, or NaN where 0 * inf or inf - inf

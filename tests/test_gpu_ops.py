@@ -228,10 +228,10 @@ def test_attention_peaked_scores(A, ctx, oracle):
     assert within_tol(out[0], f64_attention(q, K, V, 3000, 128, 32, 8), atol=2e-3, rtol=2e-3)
 
 
-def test_attention_repeated_calls_reuse_merge_counters(A, ctx):
-    """The split merge of the head_dim 64/128 path finds its last workgroup with device counters that
-    the merging workgroup resets; back-to-back calls with shrinking and growing split counts must
-    all merge."""
+def test_attention_repeated_calls_varying_split_counts(A, ctx):
+    """Back-to-back calls with shrinking and growing split counts (32, 1, 1, 11, 32, 1 splits of
+    the head_dim 128 path) reuse the same partial buffer: each call's merge must read only its own
+    splits' partials, and the single-split calls write the output without a merge."""
     hd, nq, nkv = 128, 32, 8
     for S in (2048, 40, 1, 700, 2048, 33):
         q, K, V, out = attn_case(ctx, A, S, hd, nq, nkv)

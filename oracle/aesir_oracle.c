@@ -542,6 +542,129 @@ int ao_gemm_q8_0(const uint16_t *A, int64_t a_rows, int64_t a_cols, const uint8_
     return AO_OK;
 }
 
+/* ------------------------------------------------------------------ 4-bit and K-quant blocks */
+
+/* GGUF block_q4_0 { f16 d; uint8 qs[16]; } packed, 18 bytes: byte i holds element i in its low
+ * nibble and element i + 16 in its high nibble. The reference's BlockQ4_0 (compute.mojo:22-31)
+ * names the same two fields in that order. */
+#define Q4_0_BLOCK_BYTES 18
+
+/* dequantize_q4_0, compute.mojo:266-280: w = f16((f16(q) - 8) * d). q - 8 is exact in f16, so
+ * the single rounding is that of the product (evaluated exactly in f32, rounded once). */
+static inline uint16_t q4_0_weight(const uint8_t *blk, int i) {
+    uint16_t d;
+    memcpy(&d, blk, 2);
+    const int q = i < 16 ? (blk[2 + i] & 0x0F) : (blk[2 + i - 16] >> 4);
+    return F2H((float)(q - 8) * H2F(d));
+}
+
+void ao_dequantize_q4_0(const uint8_t *blocks, uint16_t *out, int64_t n_blocks) {
+    for (int64_t b = 0; b < n_blocks; b++)
+        for (int i = 0; i < 32; i++) out[b * 32 + i] = q4_0_weight(blocks + b * Q4_0_BLOCK_BYTES, i);
+}
+
+/* gemm_q4_0, compute.mojo:876-912: per block, the 16 lower and the 16 upper products are each
+ * reduced by the 16-lane reduce_add and added to an f32 sum in that order; C = f16(sum). */
+int ao_gemm_q4_0(const uint16_t *A, int64_t a_rows, int64_t a_cols, const uint8_t *blocks, int64_t b_rows,
+                 uint16_t *C, int64_t c_rows, int64_t c_cols) {
+    if (a_rows <= 0 || a_cols <= 0 || b_rows <= 0)
+        return ao_fail(AO_ERR_INVALID, "gemm_q4_0: matrix dimensions must be positive");
+    if (a_cols % 32 != 0) return ao_fail(AO_ERR_SHAPE, "gemm_q4_0: inner dimension must be a multiple of 32");
+    if (c_rows != a_rows || c_cols != b_rows) return ao_fail(AO_ERR_SHAPE, "gemm_q4_0: output matrix shape mismatch");
+    const int64_t K = a_cols, bpr = K / 32;
+    uint16_t w[32];
+    for (int64_t row = 0; row < a_rows; row++) {
+        for (int64_t n = 0; n < b_rows; n++) {
+            float sum = 0.0f;
+            for (int64_t b = 0; b < bpr; b++) {
+                const uint8_t *blk = blocks + (n * bpr + b) * Q4_0_BLOCK_BYTES;
+                for (int i = 0; i < 32; i++) w[i] = q4_0_weight(blk, i);
+                sum += chunk16_dot_scalar(A + row * K + b * 32, w);
+                sum += chunk16_dot_scalar(A + row * K + b * 32 + 16, w + 16);
+            }
+            C[row * b_rows + n] = F2H(sum);
+        }
+    }
+    return AO_OK;
+}
+
+/* GGML's K-quant super-blocks of 256 weights, as GGUF files store them (GGML type 12 = Q4_K and
+ * 14 = Q6_K, the ids the reference loader maps at loader/gguf.mojo:20-30). The reference's own
+ * BlockQ4_K / BlockQ6_K (compute.mojo:86-100, 183-199) are different, synthetic layouts; these
+ * functions restate GGML's published block format (ggml-quants dequantize_row_q4_K /
+ * dequantize_row_q6_K, unchanged since GGUF v3) in f32, which is what the library's K-quant
+ * GEMVs accumulate against. */
+#define Q4_K_BLOCK_BYTES 144
+#define Q6_K_BLOCK_BYTES 210
+
+/* 6-bit scale and min of sub-block j (0..7) of a Q4_K super-block. */
+static void q4_k_scale_min(const uint8_t *sc, int j, int *scale, int *min) {
+    if (j < 4) {
+        *scale = sc[j] & 63;
+        *min = sc[j + 4] & 63;
+    } else {
+        *scale = (sc[j + 4] & 0x0F) | ((sc[j - 4] >> 6) << 4);
+        *min = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4);
+    }
+}
+
+/* block_q4_K { f16 d; f16 dmin; uint8 scales[12]; uint8 qs[128]; }: weight 64 g + l (l < 32)
+ * is the low nibble of qs[32 g + l] (sub-block 2 g), weight 64 g + 32 + l its high nibble
+ * (sub-block 2 g + 1); w = (d * sc) * q - dmin * m in f32 (both products exact, one rounding). */
+void ao_dequantize_q4_k(const uint8_t *blocks, float *out, int64_t n_blocks) {
+    for (int64_t b = 0; b < n_blocks; b++) {
+        const uint8_t *blk = blocks + b * Q4_K_BLOCK_BYTES;
+        uint16_t dh, mh;
+        memcpy(&dh, blk, 2);
+        memcpy(&mh, blk + 2, 2);
+        const float d = H2F(dh), dmin = H2F(mh);
+        const uint8_t *sc = blk + 4, *qs = blk + 16;
+        float *y = out + b * 256;
+        for (int g = 0; g < 4; g++) {
+            int s0, m0, s1, m1;
+            q4_k_scale_min(sc, 2 * g, &s0, &m0);
+            q4_k_scale_min(sc, 2 * g + 1, &s1, &m1);
+            const float d0 = d * (float)s0, n0 = dmin * (float)m0, d1 = d * (float)s1, n1 = dmin * (float)m1;
+            for (int l = 0; l < 32; l++) {
+                y[64 * g + l] = d0 * (float)(qs[32 * g + l] & 0x0F) - n0;
+                y[64 * g + 32 + l] = d1 * (float)(qs[32 * g + l] >> 4) - n1;
+            }
+        }
+    }
+}
+
+/* block_q6_K { uint8 ql[128]; uint8 qh[64]; int8 scales[16]; f16 d; }: for half h (ql + 64 h,
+ * qh + 32 h, scales + 8 h) and l < 32, the 6-bit values
+ *   q1 = (ql[l] & 15) | (((qh[l] >> 0) & 3) << 4)       -> weight 128 h + l,      scale[l / 16]
+ *   q2 = (ql[l + 32] & 15) | (((qh[l] >> 2) & 3) << 4)  -> weight 128 h + l + 32, scale[l / 16 + 2]
+ *   q3 = (ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)       -> weight 128 h + l + 64, scale[l / 16 + 4]
+ *   q4 = (ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)  -> weight 128 h + l + 96, scale[l / 16 + 6]
+ * and w = (d * scale) * (q - 32) in f32 (d * scale exact, one rounding). */
+void ao_dequantize_q6_k(const uint8_t *blocks, float *out, int64_t n_blocks) {
+    for (int64_t b = 0; b < n_blocks; b++) {
+        const uint8_t *blk = blocks + b * Q6_K_BLOCK_BYTES;
+        uint16_t dh;
+        memcpy(&dh, blk + 208, 2);
+        const float d = H2F(dh);
+        float *y = out + b * 256;
+        for (int h = 0; h < 2; h++) {
+            const uint8_t *ql = blk + 64 * h, *qh = blk + 128 + 32 * h;
+            const int8_t *sc = (const int8_t *)(blk + 192 + 8 * h);
+            for (int l = 0; l < 32; l++) {
+                const int is = l / 16;
+                const int q1 = ((ql[l] & 15) | (((qh[l] >> 0) & 3) << 4)) - 32;
+                const int q2 = ((ql[l + 32] & 15) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                const int q3 = ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                const int q4 = ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                y[128 * h + l] = (d * (float)sc[is]) * (float)q1;
+                y[128 * h + l + 32] = (d * (float)sc[is + 2]) * (float)q2;
+                y[128 * h + l + 64] = (d * (float)sc[is + 4]) * (float)q3;
+                y[128 * h + l + 96] = (d * (float)sc[is + 6]) * (float)q4;
+            }
+        }
+    }
+}
+
 /* ------------------------------------------------------------------ KV cache */
 
 /* KVCache.append, mimir_well.mojo:488-501 */

@@ -77,6 +77,14 @@ float ao_rune_rng_next_float32(uint64_t *state);
 int ao_gemm_q8_0(const uint16_t *A, int64_t a_rows, int64_t a_cols, const uint8_t *blocks, int64_t b_rows,
                  uint16_t *C, int64_t c_rows, int64_t c_cols);
 void ao_dequantize_q8_0(const uint8_t *blocks, uint16_t *out, int64_t n_blocks);
+/* gemm_q4_0 / dequantize_q4_0 (compute.mojo:876-912, 266-280) on GGUF block_q4_0 (18 bytes). */
+int ao_gemm_q4_0(const uint16_t *A, int64_t a_rows, int64_t a_cols, const uint8_t *blocks, int64_t b_rows,
+                 uint16_t *C, int64_t c_rows, int64_t c_cols);
+void ao_dequantize_q4_0(const uint8_t *blocks, uint16_t *out, int64_t n_blocks);
+/* GGML block_q4_K (144 bytes) / block_q6_K (210 bytes) super-blocks of 256 weights, dequantized
+ * to f32 (GGML's published format; see aesir_oracle.c). */
+void ao_dequantize_q4_k(const uint8_t *blocks, float *out, int64_t n_blocks);
+void ao_dequantize_q6_k(const uint8_t *blocks, float *out, int64_t n_blocks);
 
 /* ---- KV cache (mimir_well.mojo:434-521) over caller-owned buffers ---- */
 typedef struct {

@@ -63,6 +63,13 @@ def lib():
         L.ao_gemm_q8_0.argtypes = [P, I64, I64, P, I64, P, I64, I64]
         L.ao_dequantize_q8_0.argtypes = [P, P, I64]
         L.ao_dequantize_q8_0.restype = None
+        L.ao_gemm_q4_0.argtypes = [P, I64, I64, P, I64, P, I64, I64]
+        L.ao_dequantize_q4_0.argtypes = [P, P, I64]
+        L.ao_dequantize_q4_0.restype = None
+        L.ao_dequantize_q4_k.argtypes = [P, P, I64]
+        L.ao_dequantize_q4_k.restype = None
+        L.ao_dequantize_q6_k.argtypes = [P, P, I64]
+        L.ao_dequantize_q6_k.restype = None
         L.ao_kv_append.argtypes = [P, I64, I64, P, I64, P, I64]
         L.ao_kv_slice.argtypes = [P, I64, I64, P, P]
         L.ao_forward_scratch_elems.argtypes = [P]
@@ -251,6 +258,38 @@ def gemm_q8_0(A, blocks, n_rows) -> np.ndarray:
     _check(lib().ao_gemm_q8_0(_ptr(A), A.shape[0], A.shape[1], _ptr(blocks), n_rows, _ptr(Cm),
                               A.shape[0], n_rows))
     return Cm
+
+
+def gemm_q4_0(A, blocks, n_rows) -> np.ndarray:
+    A = _f16(A)
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    Cm = np.zeros((A.shape[0], n_rows), dtype=np.float16)
+    _check(lib().ao_gemm_q4_0(_ptr(A), A.shape[0], A.shape[1], _ptr(blocks), n_rows, _ptr(Cm),
+                              A.shape[0], n_rows))
+    return Cm
+
+
+def dequantize_q4_0(blocks, n_blocks) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    out = np.zeros(n_blocks * 32, dtype=np.float16)
+    lib().ao_dequantize_q4_0(_ptr(blocks), _ptr(out), n_blocks)
+    return out
+
+
+def dequantize_q4_k(blocks, n_blocks) -> np.ndarray:
+    """GGML block_q4_K super-blocks (144 bytes) -> f32 weights."""
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    out = np.zeros(n_blocks * 256, dtype=np.float32)
+    lib().ao_dequantize_q4_k(_ptr(blocks), _ptr(out), n_blocks)
+    return out
+
+
+def dequantize_q6_k(blocks, n_blocks) -> np.ndarray:
+    """GGML block_q6_K super-blocks (210 bytes) -> f32 weights."""
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    out = np.zeros(n_blocks * 256, dtype=np.float32)
+    lib().ao_dequantize_q6_k(_ptr(blocks), _ptr(out), n_blocks)
+    return out
 
 
 def dequantize_q8_0(blocks, n_blocks) -> np.ndarray:

@@ -393,18 +393,29 @@ class ModelConfig:
                             self.ctx_len, self.rms_eps, self.rope_theta, self.bos_token_id, self.eos_token_id)
 
 
-GGML_F32, GGML_F16, GGML_Q8_0 = 0, 1, 8
+GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 0, 1, 2, 8, 12, 14
 
 
-class Q8_0Tensor:
-    """A rows x cols matrix as GGUF block_q8_0 data: rows * cols / 32 packed 34-byte blocks
-    {f16 d; int8 qs[32]} in row order (the bytes a GGUF file holds for a GGML type-8 tensor)."""
+class QuantTensor:
+    """A rows x cols matrix as the packed GGML blocks of one quantized type, in row order (the
+    bytes a GGUF file holds for the tensor). Subclasses fix the type's block geometry."""
+
+    ggml_type = -1
+    block_elems = 0
+    block_bytes = 0
 
     def __init__(self, blocks: np.ndarray, rows: int, cols: int):
-        if cols % 32:
-            raise ValueError("Q8_0 rows must be a multiple of 32 long")
-        self.blocks = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(rows * cols // 32, 34)
+        if cols % self.block_elems:
+            raise ValueError(f"{type(self).__name__} rows must be a multiple of {self.block_elems} long")
+        nb = rows * cols // self.block_elems
+        self.blocks = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(nb, self.block_bytes)
         self.rows, self.cols = rows, cols
+
+
+class Q8_0Tensor(QuantTensor):
+    """GGUF block_q8_0: rows * cols / 32 packed 34-byte blocks {f16 d; int8 qs[32]} (GGML type 8)."""
+
+    ggml_type, block_elems, block_bytes = 8, 32, 34
 
     @classmethod
     def from_parts(cls, d: np.ndarray, q: np.ndarray) -> "Q8_0Tensor":
@@ -421,6 +432,84 @@ class Q8_0Tensor:
         d = self.blocks[:, :2].copy().view(np.float16).astype(np.float32)
         q = self.blocks[:, 2:].copy().view(np.int8).astype(np.float32)
         return (q * d).astype(np.float16).reshape(self.rows, self.cols)
+
+
+class Q4_0Tensor(QuantTensor):
+    """GGUF block_q4_0: 18-byte blocks {f16 d; uint8 qs[16]} of 32 weights (GGML type 2); byte i
+    holds element i in its low nibble and element i + 16 in its high nibble."""
+
+    ggml_type, block_elems, block_bytes = 2, 32, 18
+
+    @classmethod
+    def from_parts(cls, d: np.ndarray, q: np.ndarray) -> "Q4_0Tensor":
+        """d: f16 scales [rows, cols/32]; q: 4-bit values 0..15 [rows, cols]."""
+        rows, cols = q.shape
+        nb = rows * cols // 32
+        qb = np.ascontiguousarray(q, np.uint8).reshape(nb, 32) & 15
+        blocks = np.empty((nb, 18), np.uint8)
+        blocks[:, :2] = np.ascontiguousarray(d, np.float16).reshape(nb).view(np.uint8).reshape(nb, 2)
+        blocks[:, 2:] = qb[:, :16] | (qb[:, 16:] << 4)
+        return cls(blocks, rows, cols)
+
+    def dequantize(self) -> np.ndarray:
+        """dequantize_q4_0 (core/compute.mojo:266-280): f16((q - 8) * d), one rounding."""
+        d = self.blocks[:, :2].copy().view(np.float16).astype(np.float32)
+        qs = self.blocks[:, 2:]
+        q = np.concatenate([qs & 15, qs >> 4], axis=1).astype(np.float32) - 8.0
+        return (q * d).astype(np.float16).reshape(self.rows, self.cols)
+
+
+class Q4_KTensor(QuantTensor):
+    """GGUF block_q4_K: 144-byte super-blocks of 256 weights (GGML type 12):
+    {f16 d; f16 dmin; uint8 scales[12]; uint8 qs[128]}, eight sub-blocks of 32 with a 6-bit scale
+    and a 6-bit min each; w = d * scale * q - dmin * min."""
+
+    ggml_type, block_elems, block_bytes = 12, 256, 144
+
+    @classmethod
+    def from_parts(cls, d, dmin, scales, mins, q) -> "Q4_KTensor":
+        """d, dmin: f16 [rows, cols/256]; scales, mins: 0..63 [rows, cols/256, 8]; q: 0..15 [rows, cols]."""
+        rows, cols = q.shape
+        nb = rows * cols // 256
+        sc = np.ascontiguousarray(scales, np.uint8).reshape(nb, 8) & 63
+        mn = np.ascontiguousarray(mins, np.uint8).reshape(nb, 8) & 63
+        packed = np.zeros((nb, 12), np.uint8)
+        packed[:, 0:4] = sc[:, 0:4] | ((sc[:, 4:8] >> 4) << 6)
+        packed[:, 4:8] = mn[:, 0:4] | ((mn[:, 4:8] >> 4) << 6)
+        packed[:, 8:12] = (sc[:, 4:8] & 15) | ((mn[:, 4:8] & 15) << 4)
+        qb = np.ascontiguousarray(q, np.uint8).reshape(nb, 4, 64) & 15
+        qs = (qb[:, :, :32] | (qb[:, :, 32:] << 4)).reshape(nb, 128)
+        blocks = np.empty((nb, 144), np.uint8)
+        blocks[:, 0:2] = np.ascontiguousarray(d, np.float16).reshape(nb).view(np.uint8).reshape(nb, 2)
+        blocks[:, 2:4] = np.ascontiguousarray(dmin, np.float16).reshape(nb).view(np.uint8).reshape(nb, 2)
+        blocks[:, 4:16] = packed
+        blocks[:, 16:] = qs
+        return cls(blocks, rows, cols)
+
+
+class Q6_KTensor(QuantTensor):
+    """GGUF block_q6_K: 210-byte super-blocks of 256 weights (GGML type 14):
+    {uint8 ql[128]; uint8 qh[64]; int8 scales[16]; f16 d}, sixteen sub-blocks of 16 with an int8
+    scale each; w = d * scale * (q - 32) for 6-bit q."""
+
+    ggml_type, block_elems, block_bytes = 14, 256, 210
+
+    @classmethod
+    def from_parts(cls, d, scales, q) -> "Q6_KTensor":
+        """d: f16 [rows, cols/256]; scales: int8 [rows, cols/256, 16]; q: 0..63 [rows, cols]."""
+        rows, cols = q.shape
+        nb = rows * cols // 256
+        qv = (np.ascontiguousarray(q, np.uint8) & 63).reshape(nb, 2, 4, 32)  # [block, half, group, l]
+        ql = np.empty((nb, 2, 64), np.uint8)
+        ql[:, :, :32] = (qv[:, :, 0] & 15) | ((qv[:, :, 2] & 15) << 4)
+        ql[:, :, 32:] = (qv[:, :, 1] & 15) | ((qv[:, :, 3] & 15) << 4)
+        qh = (qv[:, :, 0] >> 4) | ((qv[:, :, 1] >> 4) << 2) | ((qv[:, :, 2] >> 4) << 4) | ((qv[:, :, 3] >> 4) << 6)
+        blocks = np.empty((nb, 210), np.uint8)
+        blocks[:, 0:128] = ql.reshape(nb, 128)
+        blocks[:, 128:192] = qh.reshape(nb, 64)
+        blocks[:, 192:208] = np.ascontiguousarray(scales, np.int8).reshape(nb, 16).view(np.uint8)
+        blocks[:, 208:210] = np.ascontiguousarray(d, np.float16).reshape(nb).view(np.uint8).reshape(nb, 2)
+        return cls(blocks, rows, cols)
 
 
 class Model:
@@ -467,9 +556,9 @@ class Model:
             pass
 
     def set_tensor(self, name: str, data):
-        if isinstance(data, Q8_0Tensor):
+        if isinstance(data, QuantTensor):
             _check(_L.aesir_model_set_tensor(self.h, name.encode(), data.blocks.ctypes.data, data.rows, data.cols,
-                                             GGML_Q8_0))
+                                             data.ggml_type))
             return
         data = np.asarray(data)
         ggml = 0 if data.dtype == np.float32 else 1

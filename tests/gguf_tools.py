@@ -74,7 +74,7 @@ def llama_metadata(cfg, vocab: int, eos: int = 2, bos: int = 1, freq_base: float
 def write_gguf(path: str, metadata: list, tensors: dict, alignment: int = 32, version: int = 3,
                magic: int = 0x46554747):
     """tensors: name -> numpy array (float16 -> GGML F16, float32 -> GGML F32), 1-D or 2-D, or an
-    object with .blocks (uint8 [rows * cols / 32, 34]), .rows and .cols -> GGML Q8_0 (type 8)."""
+    object with .blocks (uint8, the packed GGML blocks), .rows, .cols and .ggml_type (8 = Q8_0 if absent)."""
     head = bytearray()
     head += struct.pack("<IIQQ", magic, version, len(tensors), len(metadata))
     for key, vtype, value in metadata:
@@ -84,7 +84,7 @@ def write_gguf(path: str, metadata: list, tensors: dict, alignment: int = 32, ve
         _s(head, name)
         if hasattr(arr, "blocks"):
             head += struct.pack("<I", 2) + struct.pack("<QQ", arr.cols, arr.rows)
-            ttype, raw = 8, np.ascontiguousarray(arr.blocks, np.uint8).tobytes()
+            ttype, raw = getattr(arr, "ggml_type", 8), np.ascontiguousarray(arr.blocks, np.uint8).tobytes()
         else:
             arr = np.ascontiguousarray(arr)
             ttype = 0 if arr.dtype == np.float32 else 1

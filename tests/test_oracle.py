@@ -651,3 +651,139 @@ def test_sampler_greedy_branch_and_rng_use(oracle):
         assert t == oracle.greedy_sample_f16(x, suppress=[2]) == 4 and st2 == st
     t, st3 = oracle.sample_token_f16(x, oracle.SamplerConfig(temperature=1.0), st)
     assert st3 != st
+
+
+# ---------------------------------------------------------------- Q4_0 / Q4_K / Q6_K blocks
+
+def test_q4_0_reference_kat(oracle):
+    """tests/test_legacy_quantization.mojo:6-46: scale 0.5, every qs byte 0x91 -> the 16 lower
+    weights (1 - 8) * 0.5 = -3.5, the 16 upper (9 - 8) * 0.5 = 0.5; A = ones gives -48, equal to
+    gemm_f16 on the dequantized weights."""
+    blk = np.zeros((1, 18), np.uint8)
+    blk[0, :2] = np.array([0.5], np.float16).view(np.uint8)
+    blk[0, 2:] = 0x91
+    w = oracle.dequantize_q4_0(blk, 1)
+    assert np.array_equal(w[:16], np.full(16, -3.5, np.float16)) and np.array_equal(w[16:], np.full(16, 0.5, np.float16))
+    a = np.ones((1, 32), np.float16)
+    c = oracle.gemm_q4_0(a, blk, 1)
+    assert c[0, 0] == np.float16(-48.0)
+    assert c[0, 0] == oracle.gemm_f16(a, w.reshape(1, 32))[0, 0]
+
+
+def test_q4_0_pack_dequant_and_gemm(oracle):
+    """Q4_0Tensor packs GGUF block_q4_0; the oracle's dequantize equals f16((q - 8) * d) from the
+    parts; gemm_q4_0 is within 1 f16 ulp of f64 on the dequantized weights, and errors match."""
+    import aesir_hip as A
+
+    rng = np.random.default_rng(4)
+    rows, cols = 7, 96
+    q = rng.integers(0, 16, (rows, cols)).astype(np.uint8)
+    d = rng.uniform(0.001, 0.05, (rows, cols // 32)).astype(np.float16)
+    t = A.Q4_0Tensor.from_parts(d, q)
+    assert t.blocks.shape == (rows * cols // 32, 18)
+    ref = ((q.astype(np.float32) - 8) * np.repeat(d.astype(np.float32), 32, axis=1)).astype(np.float16)
+    got = oracle.dequantize_q4_0(t.blocks, rows * cols // 32).reshape(rows, cols)
+    assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+    assert np.array_equal(t.dequantize().view(np.uint16), ref.view(np.uint16))
+    x = rng.standard_normal((3, cols)).astype(np.float16)
+    c = oracle.gemm_q4_0(x, t.blocks, rows)
+    exact = x.astype(np.float64) @ ref.astype(np.float64).T
+    assert np.all(np.abs(c.astype(np.float64) - exact) <= np.abs(np.spacing(c.astype(np.float16))).astype(np.float64) + 1e-6)
+    with pytest.raises(oracle.OracleError, match="inner dimension must be a multiple of 32"):
+        oracle.gemm_q4_0(np.ones((1, 40), np.float16), t.blocks, 1)
+
+
+def _q4_k_literal_block():
+    """One block_q4_K built byte by byte from GGML's layout: d = 0.5, dmin = 0.25, sub-block
+    scales [1, 2, 3, 4, 45, 33, 63, 16] and mins [0, 5, 10, 15, 19, 63, 1, 32] (the last four
+    need the high-bit packing), qs[32 g + l] = (l % 16) | ((15 - l % 16) << 4)."""
+    sc = [1, 2, 3, 4, 45, 33, 63, 16]
+    mn = [0, 5, 10, 15, 19, 63, 1, 32]
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = np.array([0.5], np.float16).view(np.uint8)
+    blk[2:4] = np.array([0.25], np.float16).view(np.uint8)
+    # scales[12], worked out by hand: j < 4 low 6 bits, high 2 bits carry bits 4-5 of j + 4;
+    # bytes 8..11 hold the low nibbles of scale / min j + 4
+    blk[4:16] = [0x81, 0x82, 0xC3, 0x44, 0x40, 0xC5, 0x0A, 0x8F, 0x3D, 0xF1, 0x1F, 0x00]
+    l = np.arange(32)
+    for g in range(4):
+        blk[16 + 32 * g:16 + 32 * g + 32] = (l % 16) | ((15 - l % 16) << 4)
+    want = np.zeros(256, np.float64)
+    for g in range(4):
+        want[64 * g + l] = 0.5 * sc[2 * g] * (l % 16) - 0.25 * mn[2 * g]
+        want[64 * g + 32 + l] = 0.5 * sc[2 * g + 1] * (15 - l % 16) - 0.25 * mn[2 * g + 1]
+    return blk, sc, mn, want
+
+
+def test_q4_k_literal_block(oracle):
+    """GGML block_q4_K decoded from a hand-built block: every weight equals d * scale * q -
+    dmin * min of its sub-block (e.g. weight 163, sub-block 5: 0.5 * 33 * 12 - 0.25 * 63 = 182.25);
+    the host packer produces the same 144 bytes."""
+    import aesir_hip as A
+
+    blk, sc, mn, want = _q4_k_literal_block()
+    got = oracle.dequantize_q4_k(blk.reshape(1, 144), 1)
+    assert got[163] == np.float32(182.25)
+    assert np.array_equal(got, want.astype(np.float32))
+    q = np.zeros(256, np.uint8)
+    for g in range(4):
+        q[64 * g:64 * g + 32] = np.arange(32) % 16
+        q[64 * g + 32:64 * g + 64] = 15 - np.arange(32) % 16
+    t = A.Q4_KTensor.from_parts(np.array([[0.5]], np.float16), np.array([[0.25]], np.float16),
+                                np.array(sc, np.uint8).reshape(1, 1, 8), np.array(mn, np.uint8).reshape(1, 1, 8),
+                                q.reshape(1, 256))
+    assert np.array_equal(t.blocks[0], blk)
+
+
+def test_q6_k_literal_block(oracle):
+    """GGML block_q6_K from a hand-built block: 6-bit q_i = (7 i + 3) % 64 placed in ql / qh by the
+    format's loops, scales (-1)^j (j + 1), d = 0.125; weight i = 0.125 * scale[i // 16] * (q_i - 32)
+    (weight 128 h + 32 grp + l uses scale 8 h + 2 grp + l // 16 = i // 16). The host packer produces
+    the same 210 bytes."""
+    import aesir_hip as A
+
+    qv = (7 * np.arange(256) + 3) % 64
+    sc = np.array([(j + 1) * (-1) ** j for j in range(16)], np.int8)
+    blk = np.zeros(210, np.uint8)
+    for h in range(2):
+        for l in range(32):
+            b = 128 * h
+            blk[64 * h + l] = (qv[b + l] & 15) | ((qv[b + 64 + l] & 15) << 4)
+            blk[64 * h + 32 + l] = (qv[b + 32 + l] & 15) | ((qv[b + 96 + l] & 15) << 4)
+            blk[128 + 32 * h + l] = ((qv[b + l] >> 4) | ((qv[b + 32 + l] >> 4) << 2) | ((qv[b + 64 + l] >> 4) << 4)
+                                     | ((qv[b + 96 + l] >> 4) << 6))
+    blk[192:208] = sc.view(np.uint8)
+    blk[208:210] = np.array([0.125], np.float16).view(np.uint8)
+    want = (0.125 * sc[np.arange(256) // 16].astype(np.float64) * (qv - 32)).astype(np.float32)
+    assert np.array_equal(oracle.dequantize_q6_k(blk.reshape(1, 210), 1), want)
+    t = A.Q6_KTensor.from_parts(np.array([[0.125]], np.float16), sc.reshape(1, 1, 16), qv.astype(np.uint8).reshape(1, 256))
+    assert np.array_equal(t.blocks[0], blk)
+
+
+def test_k_quant_random_blocks_match_the_formula(oracle):
+    """Random super-blocks through the packers: the oracle's f32 dequantization is within one f32
+    rounding of the f64 formula from the parts (Q4_K: d sc q - dmin m; Q6_K: d sc (q - 32))."""
+    import aesir_hip as A
+
+    rng = np.random.default_rng(8)
+    rows, cols = 5, 512
+    nsb = cols // 256
+    d = rng.uniform(1e-4, 0.01, (rows, nsb)).astype(np.float16)
+    dmin = rng.uniform(1e-4, 0.01, (rows, nsb)).astype(np.float16)
+    sc = rng.integers(0, 64, (rows, nsb, 8)).astype(np.uint8)
+    mn = rng.integers(0, 64, (rows, nsb, 8)).astype(np.uint8)
+    q = rng.integers(0, 16, (rows, cols)).astype(np.uint8)
+    t = A.Q4_KTensor.from_parts(d, dmin, sc, mn, q)
+    got = oracle.dequantize_q4_k(t.blocks, rows * nsb).reshape(rows, cols).astype(np.float64)
+    sub = np.arange(cols) // 32
+    ds = d.astype(np.float64)[:, sub // 8] * sc.astype(np.float64).reshape(rows, -1)[:, sub]
+    ms = dmin.astype(np.float64)[:, sub // 8] * mn.astype(np.float64).reshape(rows, -1)[:, sub]
+    want = ds * q - ms
+    assert np.all(np.abs(got - want) <= 2.0 ** -24 * (np.abs(ds * q) + np.abs(ms)))
+    s6 = rng.integers(-128, 128, (rows, nsb, 16)).astype(np.int8)
+    q6 = rng.integers(0, 64, (rows, cols)).astype(np.uint8)
+    t6 = A.Q6_KTensor.from_parts(d, s6, q6)
+    got6 = oracle.dequantize_q6_k(t6.blocks, rows * nsb).reshape(rows, cols).astype(np.float64)
+    sub16 = np.arange(cols) // 16
+    want6 = d.astype(np.float64)[:, sub16 // 16] * s6.astype(np.float64).reshape(rows, -1)[:, sub16] * (q6.astype(np.float64) - 32)
+    assert np.all(np.abs(got6 - want6) <= 2.0 ** -24 * np.abs(want6))

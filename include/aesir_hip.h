@@ -44,6 +44,18 @@ extern "C" {
  * gemm_q8_0 (core/compute.mojo:1038-1065) but its loader rejects it (loader/gguf.mojo:450-463);
  * here it is also a model weight type (aesir_model_create_typed, aesir_model_load_gguf). */
 #define AESIR_GGML_Q8_0 8
+/* GGML block_q4_0 {f16 d; uint8 qs[16]} (18 bytes per 32 weights; byte i: element i in the low
+ * nibble, element i + 16 in the high nibble). The reference's gemm_q4_0 / dequantize_q4_0
+ * (core/compute.mojo:876-912, 266-280) fix the arithmetic: w = f16(f16(q - 8) * d). */
+#define AESIR_GGML_Q4_0 2
+/* GGML's K-quant super-blocks of 256 weights as GGUF files hold them (the ids the reference loader
+ * names at loader/gguf.mojo:20-30; its own BlockQ4_K / BlockQ6_K are different, synthetic
+ * layouts): block_q4_K {f16 d; f16 dmin; uint8 scales[12]; uint8 qs[128]} (144 bytes),
+ * w = d * sc * q - dmin * m with 6-bit sc, m per 32 weights; block_q6_K {uint8 ql[128];
+ * uint8 qh[64]; int8 scales[16]; f16 d} (210 bytes), w = d * sc * (q - 32) with 6-bit q. The
+ * library evaluates these weights in f32, as GGML defines them. */
+#define AESIR_GGML_Q4_K 12
+#define AESIR_GGML_Q6_K 14
 
 /* GPURealmType.AMD_ROCM_HIP (core/mimir_well.mojo:99): the realm id this library serves. */
 #define AESIR_REALM_AMD_ROCM_HIP 1
@@ -159,6 +171,18 @@ int32_t aesir_argmax_f16(aesir_ctx *ctx, const void *logits, int64_t n, int64_t 
  * w = f16(f16(q) * d); C = f16(sum f32(A) * f32(w)). a_cols must be a multiple of 32. */
 int32_t aesir_gemm_q8_0(aesir_ctx *ctx, const void *A, int64_t a_rows, int64_t a_cols, const void *blocks,
                         int64_t b_rows, void *C, int64_t c_rows, int64_t c_cols);
+/* The reference's quantized branch of gemm_f16 (core/compute.mojo:1763-1800) over packed GGUF
+ * blocks of ggml_type: B is b_rows x a_cols weights, C[m, n] = f16(sum_k A[m, k] w[n, k]).
+ * AESIR_GGML_Q4_0 follows gemm_q4_0 (:876-912, w = f16(f16(q - 8) * d)); AESIR_GGML_Q8_0 is
+ * aesir_gemm_q8_0; AESIR_GGML_Q4_K / AESIR_GGML_Q6_K use GGML's f32 weights (the reference's
+ * gemm_q4_k_m / gemm_q6_k read synthetic block layouts that no GGUF file holds). Raises
+ * "gemm_q4_0: matrix dimensions must be positive", "...: inner dimension must be a multiple of
+ * 32" (256 for the K-quants), "...: output matrix shape mismatch". The blocks are repacked into
+ * the library's record layout in free well space for the duration of the call (about the size
+ * of the blocks; with a_rows >= 16 also an f16 copy of the weights for the matrix cores, whose
+ * K-quant weights are then rounded to f16). */
+int32_t aesir_gemm_quant(aesir_ctx *ctx, const void *A, int64_t a_rows, int64_t a_cols, const void *blocks,
+                         int32_t ggml_type, int64_t b_rows, void *C, int64_t c_rows, int64_t c_cols);
 /* Q8_0 block matvec with f32 activations and f32 output: y[n] = sum_k x[k] * d*q. Rows of
  * 64-512 blocks use exact integer dot products on x held as 30-bit fixed point per block: each
  * block's value is within 2^-30 * max|x_blk| * sum|d*q| of the exact block dot product (plus one

@@ -81,6 +81,7 @@ _sig("aesir_residual_add_f16", [P, P, P, I64])
 _sig("aesir_embed_f16", [P, P, I64, I64, I64, P])
 _sig("aesir_argmax_f16", [P, P, I64, C.POINTER(I64)])
 _sig("aesir_gemm_q8_0", [P, P, I64, I64, P, I64, P, I64, I64])
+_sig("aesir_gemm_quant", [P, P, I64, I64, P, I32, I64, P, I64, I64])
 _sig("aesir_q8_0_matvec_f32", [P, P, I64, I64, P, P])
 _sig("aesir_kv_create", [P, I64, I64, I64, C.POINTER(P)])
 _sig("aesir_kv_destroy", [P])
@@ -301,6 +302,11 @@ def argmax(ctx: Context, logits: Tensor) -> int:
 
 def gemm_q8_0(ctx: Context, A: Tensor, blocks_ptr: int, b_rows: int, C_: Tensor):
     _check(_L.aesir_gemm_q8_0(ctx.h, A.ptr, A.rows, A.cols, blocks_ptr, b_rows, C_.ptr, C_.rows, C_.cols))
+
+
+def gemm_quant(ctx: Context, A: Tensor, blocks_ptr: int, ggml_type: int, b_rows: int, C_: Tensor):
+    """gemm_f16's quantized branch (core/compute.mojo:1763-1800) over packed GGUF blocks on the device."""
+    _check(_L.aesir_gemm_quant(ctx.h, A.ptr, A.rows, A.cols, blocks_ptr, ggml_type, b_rows, C_.ptr, C_.rows, C_.cols))
 
 
 def q8_0_matvec_f32(ctx: Context, blocks_ptr: int, n_rows: int, k: int, x: Tensor, y: Tensor):

@@ -35,7 +35,7 @@ CXXFLAGS = [
     f"-I{CSRC}",
 ]
 
-SOURCES = ["ctx.hip", "gemv.hip", "attention.hip", "basic.hip", "q8_0.hip", "abi_ops.hip", "model.hip",
+SOURCES = ["ctx.hip", "gemv.hip", "quant.hip", "attention.hip", "basic.hip", "q8_0.hip", "abi_ops.hip", "model.hip",
            "prefill.hip", "gguf.hip", "sampler.hip"]
 
 

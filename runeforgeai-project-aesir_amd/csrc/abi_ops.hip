@@ -214,6 +214,48 @@ int32_t aesir_gemm_q8_0(aesir_ctx *ctx, const void *A, int64_t a_rows, int64_t a
     return launch_gemm_q8_0(ctx->stream, A, a_rows, a_cols, blocks, b_rows, C);
 }
 
+int32_t aesir_gemm_quant(aesir_ctx *ctx, const void *A, int64_t a_rows, int64_t a_cols, const void *blocks,
+                         int32_t ggml_type, int64_t b_rows, void *C, int64_t c_rows, int64_t c_cols) {
+    AESIR_TRY(bind(ctx));
+    if (ggml_type == AESIR_GGML_Q8_0) return aesir_gemm_q8_0(ctx, A, a_rows, a_cols, blocks, b_rows, C, c_rows, c_cols);
+    const char *nm = ggml_type == AESIR_GGML_Q4_0 ? "gemm_q4_0" : ggml_type == AESIR_GGML_Q4_K ? "gemm_q4_k" : "gemm_q6_k";
+    if (!qf_type(ggml_type)) return fail(AESIR_ERR_UNSUPPORTED, "gemm_quant: GGML type %d is not Q4_0, Q8_0, Q4_K or Q6_K", (int)ggml_type);
+    // compute.mojo:877-882 (gemm_q4_0's checks; the K-quant twins raise the same)
+    if (a_rows <= 0 || a_cols <= 0 || b_rows <= 0) return fail(AESIR_ERR_INVALID, "%s: matrix dimensions must be positive", nm);
+    const int64_t blk = ggml_type == AESIR_GGML_Q4_0 ? 32 : 256;
+    if (a_cols % blk != 0)
+        return fail(AESIR_ERR_SHAPE, "%s: inner dimension must be a multiple of %lld", nm, (long long)blk);
+    if (c_rows != a_rows || c_cols != b_rows) return fail(AESIR_ERR_SHAPE, "%s: output matrix shape mismatch", nm);
+    if (!A || !blocks || !C) return fail(AESIR_ERR_INVALID, "%s: null tensor pointer", nm);
+    // The blocks are repacked into records in free well space for this call; the space is
+    // released after enqueueing (later work on the stream runs after this call's kernels).
+    const int64_t K = a_cols, N = b_rows, mark = ctx->well_offset;
+    QFMat w;
+    w.type = ggml_type;
+    void *planes[4] = {nullptr, nullptr, nullptr, nullptr};
+    int32_t rc = AESIR_OK;
+    for (int plane = 0; plane < 4 && rc == AESIR_OK; plane++) {
+        const int64_t rb = qf_plane_row_bytes(ggml_type, plane, K);
+        if (rb > 0) rc = well_alloc_bytes(ctx, mul_checked(N, rb), &planes[plane]);
+    }
+    w.nib = planes[0];
+    w.hb = planes[1];
+    w.s0 = planes[2];
+    w.s1 = planes[3];
+    if (rc == AESIR_OK) rc = launch_qf_repack(ctx->stream, ggml_type, blocks, N, K, w, 1);
+    if (rc == AESIR_OK && a_rows >= 16) {  // matrix cores on an f16 copy of the weights
+        void *wf = nullptr;
+        rc = well_alloc_bytes(ctx, mul_checked(N, K, 2), &wf);
+        if (rc == AESIR_OK) rc = launch_qf_dequant(ctx->stream, w, N, K, 1, nullptr, wf, K);
+        if (rc == AESIR_OK) rc = launch_gemm_f16_mfma(ctx, A, a_rows, K, wf, N, C);
+    } else {
+        for (int64_t r = 0; r < a_rows && rc == AESIR_OK; r++)
+            rc = launch_qf_gemv_store(ctx->stream, w, N, K, (const uint16_t *)A + r * K, (uint16_t *)C + r * N);
+    }
+    ctx->well_offset = mark;
+    return rc;
+}
+
 int32_t aesir_q8_0_matvec_f32(aesir_ctx *ctx, const void *blocks, int64_t n_rows, int64_t k, const float *x, float *y) {
     AESIR_TRY(bind(ctx));
     if (n_rows <= 0 || k <= 0) return fail(AESIR_ERR_INVALID, "q8_0_matvec: matrix dimensions must be positive");

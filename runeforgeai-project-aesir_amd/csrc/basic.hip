@@ -174,13 +174,6 @@ int32_t launch_kv_append(hipStream_t s, void *kc, void *vc, const void *k, const
 // ------------------------------------------------------------------ seeded init
 // Counter-based normal: element i of stream (seed, stream) from two SplitMix64-mixer outputs
 // (the RuneRNG mixer of sampler.mojo:34-37) and Box-Muller in f64, rounded to f32 then f16.
-__host__ __device__ __forceinline__ uint64_t mix64(uint64_t z) {
-    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
-    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
-    return z ^ (z >> 31);
-}
-
-constexpr uint64_t kGolden = 0x9E3779B97F4A7C15ULL;
 
 // Element i (row i / cols, column i % cols) lands at dst[(i / cols) * dst_stride + i % cols], so a
 // tensor can be generated straight into an interleaved layout.

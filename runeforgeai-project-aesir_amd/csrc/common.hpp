@@ -78,6 +78,9 @@ inline GgmlBlock ggml_block(int64_t type) {
         case AESIR_GGML_F32: return {1, 4};
         case AESIR_GGML_F16: return {1, 2};
         case AESIR_GGML_Q8_0: return {32, 34};
+        case AESIR_GGML_Q4_0: return {32, 18};
+        case AESIR_GGML_Q4_K: return {256, 144};
+        case AESIR_GGML_Q6_K: return {256, 210};
         default: return {0, 0};
     }
 }

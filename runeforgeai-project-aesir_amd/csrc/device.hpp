@@ -39,6 +39,15 @@ __device__ __forceinline__ h16 silu_h(h16 x) {
     return hmul(x, sig);
 }
 
+// ------------------------------------------------------------------ counter-based generator
+// SplitMix64's finalizer; synthetic weights draw element i of a stream from mix64(base + i * kGolden).
+__host__ __device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    return z ^ (z >> 31);
+}
+constexpr uint64_t kGolden = 0x9E3779B97F4A7C15ULL;
+
 // ------------------------------------------------------------------ vector loads
 __device__ __forceinline__ u32x4 ld16(const void *p) { return *reinterpret_cast<const u32x4 *>(p); }
 // Streaming weight load: non-temporal hint so single-use weights do not evict reused data.

@@ -5,8 +5,10 @@
 // (message text included), then _validate_required_tensors. Where the reference aliases F16
 // tensors into the mmap, this loader uploads them once into the model's arena (Q/K/V
 // concatenated, gate/up interleaved); F32 norms are rounded to f16 as the reference does.
-// One extension: a file whose seven matrix kinds are all Q8_0 (GGML type 8) loads as a Q8_0 model
-// (the reference loader stops at "Real inference slice supports only F16 and F32 tensors").
+// One extension: a file whose seven matrix kinds all share one block type, Q8_0, Q4_0, Q4_K or
+// Q6_K (GGML types 8, 2, 12, 14), loads as a model of that weight type (the reference loader stops
+// at "Real inference slice supports only F16 and F32 tensors"). Files that mix block types
+// between matrices are refused with "GGUF required tensor has an invalid type".
 #include <fcntl.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
@@ -247,7 +249,7 @@ int32_t parse(Gguf &g, const char *path) {
     AESIR_TRY(g.need(data_offset, 0));
     for (auto &t : raw) {  // _map_tensor (loader/gguf.mojo:465-499)
         if (g.by_name.count(t.name)) return fail(AESIR_ERR_FORMAT, "GGUF contains a duplicate tensor name: %s", t.name.c_str());
-        // F16 and F32 as the reference loader; the block types beyond it (Q8_0) by their GGML
+        // F16 and F32 as the reference loader; the block types beyond it (Q8_0, Q4_0, Q4_K, Q6_K) by their GGML
         // block geometry. Every size product is overflow-checked before any range check.
         const int64_t bytes = ggml_tensor_bytes(t.type, t.rows, t.cols);
         if (bytes == -1) return fail(AESIR_ERR_FORMAT, "Real inference slice supports only F16 and F32 tensors");
@@ -283,11 +285,14 @@ std::vector<std::string> required_tensors(const Gguf &g) {
     return required;
 }
 
-// Weight type of the matrices: Q8_0 when token_embd.weight is Q8_0 (then every matrix must be),
-// else F16 as the reference requires.
+// Weight type of the matrices: token_embd.weight's type when it is one of the block types this
+// library adds (Q8_0, Q4_0, Q4_K, Q6_K; then every matrix must have it), else F16 as the
+// reference requires.
 uint32_t matrix_type(const Gguf &g) {
     const GgufTensor &t = g.tensors[g.by_name.at("token_embd.weight")];
-    return t.type == AESIR_GGML_Q8_0 ? (uint32_t)AESIR_GGML_Q8_0 : (uint32_t)AESIR_GGML_F16;
+    const bool block = t.type == AESIR_GGML_Q8_0 || t.type == AESIR_GGML_Q4_0 || t.type == AESIR_GGML_Q4_K ||
+                       t.type == AESIR_GGML_Q6_K;
+    return block ? t.type : (uint32_t)AESIR_GGML_F16;
 }
 
 // Expected (rows, cols, type) of a required tensor (loader/gguf.mojo:597-628).

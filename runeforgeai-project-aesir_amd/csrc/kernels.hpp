@@ -27,6 +27,49 @@ int32_t launch_gemm_f16(aesir_ctx *ctx, const void *A, int64_t M, int64_t K, con
 int32_t launch_gemm_f16_mfma(aesir_ctx *ctx, const void *A, int64_t M, int64_t K, const void *B, int64_t N,
                              void *C);
 
+// A Q4_0, Q4_K or Q6_K matrix [N][K] in HBM (quant.hip), repacked from its GGUF blocks into
+// records of 16 weights: record r of a row holds weights 16 r .. 16 r + 15.
+//   nib  8 bytes per record: byte j holds weight 16 r + j in its low nibble and 16 r + 8 + j in
+//        its high nibble (Q6_K: the low 4 of the 6 bits);
+//   hb   Q6_K only, 4 bytes per record: the high 2 bits of weight 16 r + i at bit
+//        16 ((i >> 1) & 1) + 2 (2 (i >> 2) + (i & 1));
+//   s0   Q4_0: f16 d per 32 weights; Q4_K: (scale, min) bytes per 32 weights, 6-bit values
+//        unpacked; Q6_K: int8 scale per 16 weights;
+//   s1   Q4_K: (d, dmin) f16 pair per 256 weights; Q6_K: f16 d per 256 weights.
+// Plane rows are `step` logical rows apart (step 2 for the interleaved gate/up rows).
+struct QFMat {
+    int32_t type = 0;
+    const void *nib = nullptr, *hb = nullptr, *s0 = nullptr, *s1 = nullptr;
+};
+// Bytes of one row of each plane (0 if the type has no such plane). plane: 0 nib, 1 hb, 2 s0, 3 s1.
+__host__ __device__ inline int64_t qf_plane_row_bytes(int32_t type, int plane, int64_t K) {
+    switch (plane) {
+        case 0: return K / 2;
+        case 1: return type == AESIR_GGML_Q6_K ? K / 4 : 0;
+        case 2: return type == AESIR_GGML_Q6_K ? K / 16 : K / 32 * 2;
+        case 3: return type == AESIR_GGML_Q4_K ? K / 256 * 4 : type == AESIR_GGML_Q6_K ? K / 256 * 2 : 0;
+        default: return 0;
+    }
+}
+// True for the types this layout serves.
+bool qf_type(int32_t type);
+// GGUF blocks (rows x K, packed, device memory) -> planes of rows 0.. of `dst` (rows `step` apart).
+int32_t launch_qf_repack(hipStream_t s, int32_t type, const void *blocks, int64_t rows, int64_t K, const QFMat &dst,
+                         int64_t step);
+// Planes -> f16 [rows][K] (out_stride elements per output row); `row_ids` (device, may be null)
+// selects the source rows (embedding lookups), else rows 0 .. rows - 1.
+int32_t launch_qf_dequant(hipStream_t s, const QFMat &w, int64_t rows, int64_t K, int64_t step,
+                          const int64_t *row_ids, void *out, int64_t out_stride);
+// Seeded synthetic planes: weights of standard deviation near `std`, mean near 0.
+int32_t launch_qf_fill_random(hipStream_t s, const QFMat &w, int64_t rows, int64_t K, int64_t step, uint64_t seed,
+                              uint64_t stream, float std);
+// y[n] = f16(sum_k x[k] w[n, k]) for one row of x (the per-op GEMV of a repacked matrix).
+int32_t launch_qf_gemv_store(hipStream_t s, const QFMat &w, int64_t N, int64_t K, const void *x, void *y);
+// Decode-step GEMVs of repacked matrices with the fused epilogues (see the F16 launchers).
+int32_t launch_qf_gemv_residual(hipStream_t s, const QFMat &w, int64_t N, int64_t K, const void *x_in, void *x);
+int32_t launch_qf_gate_up_swiglu(hipStream_t s, const void *x, const void *norm_w, float eps, const QFMat &w,
+                                 int64_t ffn, int64_t dim, void *act);
+
 // Fused decode-step GEMVs. All pointers are device pointers inside the model's arena.
 struct QkvArgs {
     const void *x;          // residual stream [dim] (pre-norm)
@@ -44,6 +87,8 @@ struct QkvArgs {
     const void *w_scale;    // Q8_0 weights: f16 block scales [dim + 2*kvd][dim / 32] (w is then int8);
                             // null for f16 weights
     const void *embd_scale; // layer 0 of a Q8_0 model: token_embd block scales (embd is then int8)
+    QFMat wq;               // Q4_0 / Q4_K / Q6_K models: the QKV matrix (w and w_scale unused)
+    QFMat eq;               // layer 0 of such a model: token_embd (embd unused)
 };
 int32_t launch_qkv_rope_kv(hipStream_t s, const QkvArgs &a);
 
@@ -69,6 +114,7 @@ struct LmHeadArgs {
     DecodeState *state;
     int64_t *ring;  // token ring (autoregressive loop), may be null
     const void *w_scale;  // Q8_0 lm_head scales (w is then int8), or null
+    QFMat wq;             // Q4_0 / Q4_K / Q6_K lm_head (w and w_scale unused)
 };
 int32_t launch_lm_head_argmax(hipStream_t s, const LmHeadArgs &a);
 int32_t launch_lm_head(hipStream_t s, const LmHeadArgs &a);

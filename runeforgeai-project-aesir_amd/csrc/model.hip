@@ -75,11 +75,23 @@ int32_t parse_tensor_name(const aesir_model *m, const char *name, TensorRef *ref
 // scale + r * scale_stride + c / 32).
 TensorPlace place_tensor(const aesir_model *m, const TensorRef &ref) {
     const int64_t d = m->cfg.dim, kvd = m->kvd, f = m->cfg.ffn, V = m->cfg.vocab;
-    const bool q8 = m->wtype == AESIR_GGML_Q8_0;
+    const bool q8 = m->wtype == AESIR_GGML_Q8_0, qf = qf_type(m->wtype);
     const int es = q8 ? 1 : 2;
     const ModelLayer *L = ref.layer >= 0 ? &m->layers[ref.layer] : nullptr;
     // matrix rows [r0, r0 + rows) of a fused tensor with `cols` columns, every `step`-th row
-    auto mat = [&](int64_t rows, int64_t cols, void *base, void *scale, int64_t r0, int64_t step) {
+    auto mat = [&](int64_t rows, int64_t cols, void *base, void *scale, void *s1, void *hb, int64_t r0,
+                   int64_t step) {
+        if (qf) {
+            auto at = [&](void *p, int plane) {
+                return p ? (void *)((char *)p + r0 * qf_plane_row_bytes(m->wtype, plane, cols)) : nullptr;
+            };
+            TensorPlace p{rows, cols, at(base, 0), 0, false, 0, at(scale, 2), 0};
+            p.qtype = m->wtype;
+            p.s1 = at(s1, 3);
+            p.hb = at(hb, 1);
+            p.step = step;
+            return p;
+        }
         TensorPlace p{rows, cols, (char *)base + r0 * cols * es, step * cols, false, es, nullptr, 0};
         if (q8) {
             p.scale = (uint16_t *)scale + r0 * (cols / 32);
@@ -89,20 +101,40 @@ TensorPlace place_tensor(const aesir_model *m, const TensorRef &ref) {
     };
     auto norm = [&](void *base) { return TensorPlace{1, d, base, d, true, 2, nullptr, 0}; };
     switch (ref.kind) {
-        case TensorKind::TokenEmbd: return mat(V, d, m->tok_embd, m->tok_embd_s, 0, 1);
+        case TensorKind::TokenEmbd: return mat(V, d, m->tok_embd, m->tok_embd_s, m->tok_embd_s1, m->tok_embd_hb, 0, 1);
         case TensorKind::OutputNorm: return norm(m->out_norm);
-        case TensorKind::Output: return mat(V, d, m->out_w, m->out_w_s, 0, 1);
+        case TensorKind::Output: return mat(V, d, m->out_w, m->out_w_s, m->out_w_s1, m->out_w_hb, 0, 1);
         case TensorKind::AttnNorm: return norm(L->attn_norm);
-        case TensorKind::AttnQ: return mat(d, d, L->wqkv, L->sqkv, 0, 1);
-        case TensorKind::AttnK: return mat(kvd, d, L->wqkv, L->sqkv, d, 1);
-        case TensorKind::AttnV: return mat(kvd, d, L->wqkv, L->sqkv, d + kvd, 1);
-        case TensorKind::AttnOut: return mat(d, d, L->wo, L->so, 0, 1);
+        case TensorKind::AttnQ: return mat(d, d, L->wqkv, L->sqkv, L->qkv_s1, L->qkv_hb, 0, 1);
+        case TensorKind::AttnK: return mat(kvd, d, L->wqkv, L->sqkv, L->qkv_s1, L->qkv_hb, d, 1);
+        case TensorKind::AttnV: return mat(kvd, d, L->wqkv, L->sqkv, L->qkv_s1, L->qkv_hb, d + kvd, 1);
+        case TensorKind::AttnOut: return mat(d, d, L->wo, L->so, L->o_s1, L->o_hb, 0, 1);
         case TensorKind::FfnNorm: return norm(L->ffn_norm);
-        case TensorKind::FfnGate: return mat(f, d, L->wgu, L->sgu, 0, 2);  // gate i -> fused row 2i
-        case TensorKind::FfnUp: return mat(f, d, L->wgu, L->sgu, 1, 2);    // up i -> fused row 2i + 1
-        case TensorKind::FfnDown: return mat(d, f, L->wdown, L->sdown, 0, 1);
+        case TensorKind::FfnGate: return mat(f, d, L->wgu, L->sgu, L->gu_s1, L->gu_hb, 0, 2);  // gate i -> fused row 2i
+        case TensorKind::FfnUp: return mat(f, d, L->wgu, L->sgu, L->gu_s1, L->gu_hb, 1, 2);    // up i -> fused row 2i + 1
+        case TensorKind::FfnDown: return mat(d, f, L->wdown, L->sdown, L->down_s1, L->down_hb, 0, 1);
     }
     return TensorPlace{};
+}
+
+QFMat model_qf(const aesir_model *m, const void *w, const void *s0, const void *s1, const void *hb) {
+    QFMat q;
+    q.type = m->wtype;
+    q.nib = w;
+    q.s0 = s0;
+    q.s1 = s1;
+    q.hb = hb;
+    return q;
+}
+
+static QFMat place_qf(const TensorPlace &p) {
+    QFMat q;
+    q.type = p.qtype;
+    q.nib = p.base;
+    q.s0 = p.scale;
+    q.s1 = p.s1;
+    q.hb = p.hb;
+    return q;
 }
 
 static int64_t stream_id(const TensorRef &ref) {
@@ -156,6 +188,21 @@ int32_t model_upload(aesir_model *m, const TensorRef &ref, const void *host, int
     if (rows != p.rows || cols != p.cols)
         return fail(AESIR_ERR_FORMAT, "GGUF required tensor has an invalid shape: %s", nm.c_str());
     hipStream_t s = m->ctx->stream;
+    if (p.esize == 0) {  // Q4_0 / Q4_K / Q6_K matrix: repack the GGUF blocks on the device
+        if (type != p.qtype)
+            return fail(AESIR_ERR_FORMAT, "GGUF required tensor has an invalid type: %s", nm.c_str());
+        const int64_t bytes = ggml_tensor_bytes(type, rows, cols);
+        if (bytes <= 0) return fail(AESIR_ERR_FORMAT, "GGUF required tensor has an invalid shape: %s", nm.c_str());
+        void *staging = nullptr;
+        AESIR_HIP_TRY(hipMalloc(&staging, (size_t)bytes));
+        int32_t rc = AESIR_OK;
+        if (hipMemcpyAsync(staging, host, (size_t)bytes, hipMemcpyHostToDevice, s) != hipSuccess)
+            rc = fail(AESIR_ERR_HIP, "hipMemcpyAsync of %s failed", nm.c_str());
+        if (rc == AESIR_OK) rc = launch_qf_repack(s, type, staging, rows, cols, place_qf(p), p.step);
+        if (hipStreamSynchronize(s) != hipSuccess && rc == AESIR_OK) rc = fail(AESIR_ERR_HIP, "repack of %s failed", nm.c_str());
+        (void)hipFree(staging);
+        return rc;
+    }
     if (p.esize == 1) {  // Q8_0 matrix: split the 34-byte blocks into quants and scales
         if (type != AESIR_GGML_Q8_0)
             return fail(AESIR_ERR_FORMAT, "GGUF required tensor has an invalid type: %s", nm.c_str());
@@ -195,9 +242,35 @@ int32_t model_upload(aesir_model *m, const TensorRef &ref, const void *host, int
 static QkvArgs qkv_args(aesir_model *m, int64_t l) {
     const aesir_model_config &c = m->cfg;
     const ModelLayer &L = m->layers[l];
-    return QkvArgs{m->x, l == 0 ? m->tok_embd : nullptr, L.attn_norm, c.rms_eps, L.wqkv, c.dim, m->kvd, m->hd, m->q,
-                   (uint16_t *)m->k_cache + l * c.ctx_len * m->kvd, (uint16_t *)m->v_cache + l * c.ctx_len * m->kvd,
-                   c.ctx_len, m->rope, m->state, L.sqkv, l == 0 ? m->tok_embd_s : nullptr};
+    QkvArgs a{m->x, l == 0 ? m->tok_embd : nullptr, L.attn_norm, c.rms_eps, L.wqkv, c.dim, m->kvd, m->hd, m->q,
+              (uint16_t *)m->k_cache + l * c.ctx_len * m->kvd, (uint16_t *)m->v_cache + l * c.ctx_len * m->kvd,
+              c.ctx_len, m->rope, m->state, L.sqkv, l == 0 ? m->tok_embd_s : nullptr};
+    if (qf_type(m->wtype)) {
+        a.wq = model_qf(m, L.wqkv, L.sqkv, L.qkv_s1, L.qkv_hb);
+        if (l == 0) a.eq = model_qf(m, m->tok_embd, m->tok_embd_s, m->tok_embd_s1, m->tok_embd_hb);
+    }
+    return a;
+}
+
+// O and down projections with the residual add, and the gate/up GEMV with SwiGLU, for every
+// weight type.
+static int32_t launch_o_residual(aesir_model *m, hipStream_t s, const ModelLayer &L) {
+    const int64_t d = m->cfg.dim;
+    if (qf_type(m->wtype)) return launch_qf_gemv_residual(s, model_qf(m, L.wo, L.so, L.o_s1, L.o_hb), d, d, m->attn, m->x);
+    return launch_gemv_residual(s, L.wo, d, d, m->attn, m->x, L.so);
+}
+static int32_t launch_down_residual(aesir_model *m, hipStream_t s, const ModelLayer &L) {
+    const int64_t d = m->cfg.dim, f = m->cfg.ffn;
+    if (qf_type(m->wtype))
+        return launch_qf_gemv_residual(s, model_qf(m, L.wdown, L.sdown, L.down_s1, L.down_hb), d, f, m->act, m->x);
+    return launch_gemv_residual(s, L.wdown, d, f, m->act, m->x, L.sdown);
+}
+static int32_t launch_gate_up(aesir_model *m, hipStream_t s, const ModelLayer &L) {
+    const aesir_model_config &c = m->cfg;
+    if (qf_type(m->wtype))
+        return launch_qf_gate_up_swiglu(s, m->x, L.ffn_norm, c.rms_eps, model_qf(m, L.wgu, L.sgu, L.gu_s1, L.gu_hb), c.ffn,
+                                        c.dim, m->act);
+    return launch_gate_up_swiglu(s, m->x, L.ffn_norm, c.rms_eps, L.wgu, c.ffn, c.dim, m->act, L.sgu);
 }
 
 static AttnArgs attn_args(aesir_model *m, int64_t l) {
@@ -223,8 +296,10 @@ static AttnArgs attn_args(aesir_model *m, int64_t l) {
 
 LmHeadArgs lm_args(aesir_model *m, bool with_ring) {
     const aesir_model_config &c = m->cfg;
-    return LmHeadArgs{m->x, m->out_norm, m->out_eps, m->out_w, c.vocab, c.dim, m->logits, m->lm_parts, m->state,
-                      with_ring ? m->ring : nullptr, m->out_w_s};
+    LmHeadArgs a{m->x, m->out_norm, m->out_eps, m->out_w, c.vocab, c.dim, m->logits, m->lm_parts, m->state,
+                 with_ring ? m->ring : nullptr, m->out_w_s};
+    if (qf_type(m->wtype)) a.wq = model_qf(m, m->out_w, m->out_w_s, m->out_w_s1, m->out_w_hb);
+    return a;
 }
 
 static int32_t enqueue_step(aesir_model *m, hipStream_t s) {
@@ -234,9 +309,9 @@ static int32_t enqueue_step(aesir_model *m, hipStream_t s) {
         const ModelLayer &L = m->layers[l];
         AESIR_TRY(launch_qkv_rope_kv(s, qkv_args(m, l)));  // layer 0 also performs the embedding lookup
         AESIR_TRY(launch_attention_decode(s, attn_args(m, l)));
-        AESIR_TRY(launch_gemv_residual(s, L.wo, d, d, m->attn, m->x, L.so));
-        AESIR_TRY(launch_gate_up_swiglu(s, m->x, L.ffn_norm, c.rms_eps, L.wgu, c.ffn, d, m->act, L.sgu));
-        AESIR_TRY(launch_gemv_residual(s, L.wdown, d, c.ffn, m->act, m->x, L.sdown));
+        AESIR_TRY(launch_o_residual(m, s, L));
+        AESIR_TRY(launch_gate_up(m, s, L));
+        AESIR_TRY(launch_down_residual(m, s, L));
     }
     return launch_lm_head_argmax(s, lm_args(m, true));
 }
@@ -325,8 +400,8 @@ int32_t aesir_model_create_typed(aesir_ctx *ctx, const aesir_model_config *cfg, 
                                  aesir_model **out) {
     AESIR_TRY(bind(ctx));
     if (!cfg || !out) return fail(AESIR_ERR_INVALID, "aesir_model_create: null argument");
-    if (weight_type != AESIR_GGML_F16 && weight_type != AESIR_GGML_Q8_0)
-        return fail(AESIR_ERR_UNSUPPORTED, "model: weight type %d is not F16 or Q8_0", (int)weight_type);
+    if (weight_type != AESIR_GGML_F16 && weight_type != AESIR_GGML_Q8_0 && !qf_type(weight_type))
+        return fail(AESIR_ERR_UNSUPPORTED, "model: weight type %d is not F16, Q8_0, Q4_0, Q4_K or Q6_K", (int)weight_type);
     *out = nullptr;
     const aesir_model_config c = *cfg;
     // GGUFModelConfig.validate (loader/gguf.mojo:133-149)
@@ -345,9 +420,16 @@ int32_t aesir_model_create_typed(aesir_ctx *ctx, const aesir_model_config *cfg, 
     if (hd % 2 != 0) return fail(AESIR_ERR_INVALID, "apply_rope: head_dim must be positive and even");
     if (hd > 256 || c.n_heads / c.n_kv_heads > 16)
         return fail(AESIR_ERR_UNSUPPORTED, "model: head_dim <= 256 and <= 16 query heads per KV head are supported");
-    const bool q8 = weight_type == AESIR_GGML_Q8_0;
+    const bool q8 = weight_type == AESIR_GGML_Q8_0, qf = qf_type(weight_type);
     if (q8 && (c.dim % 32 != 0 || c.ffn % 32 != 0 || c.dim > 16384 || c.ffn > 16384))
         return fail(AESIR_ERR_UNSUPPORTED, "model: Q8_0 weights need dim and ffn to be multiples of 32, at most 16384");
+    if (qf) {
+        const int64_t blk = weight_type == AESIR_GGML_Q4_0 ? 32 : 256;
+        if (c.dim % blk != 0 || c.ffn % blk != 0 || c.dim > 28672 || c.ffn > 28672)
+            return fail(AESIR_ERR_UNSUPPORTED, "model: %s weights need dim and ffn to be multiples of %lld, at most 28672",
+                        weight_type == AESIR_GGML_Q4_0 ? "Q4_0" : weight_type == AESIR_GGML_Q4_K ? "Q4_K" : "Q6_K",
+                        (long long)blk);
+    }
 
     auto *m = new aesir_model();
     m->ctx = ctx;
@@ -371,22 +453,35 @@ int32_t aesir_model_create_typed(aesir_ctx *ctx, const aesir_model_config *cfg, 
         if (rc == AESIR_OK && bytes < 0) rc = fail(AESIR_ERR_FORMAT, "model: a tensor size overflows int64");
         if (rc == AESIR_OK) rc = carve(ctx, bytes, p);
     };
-    // a matrix of rows x cols: f16, or int8 quants plus f16 block scales (Q8_0)
-    auto matrix = [&](int64_t rows, int64_t cols, void **w, void **scale) {
+    // a matrix of rows x cols: f16, int8 quants plus f16 block scales (Q8_0), or the record
+    // planes of a 4-bit type (nibbles, then s0, s1 and hb where the type has them)
+    auto matrix = [&](int64_t rows, int64_t cols, void **w, void **scale, void **s1, void **hb) {
+        if (qf) {
+            for (int plane = 0; plane < 4; plane++) {
+                const int64_t rb = qf_plane_row_bytes(weight_type, plane, cols);
+                if (rb > 0) take(mul_checked(rows, rb), plane == 0 ? w : plane == 1 ? hb : plane == 2 ? scale : s1);
+            }
+            return;
+        }
         take(mul_checked(rows, cols, q8 ? 1 : 2), w);
         if (q8) take(mul_checked(rows, cols / 32, 2), scale);
     };
-    matrix(V, d, &m->tok_embd, &m->tok_embd_s);
+    matrix(V, d, &m->tok_embd, &m->tok_embd_s, &m->tok_embd_s1, &m->tok_embd_hb);
     take(d * 2, &m->out_norm);
-    matrix(V, d, &m->out_w, &m->out_w_s);
+    matrix(V, d, &m->out_w, &m->out_w_s, &m->out_w_s1, &m->out_w_hb);
     m->layers.resize((size_t)c.n_layers);
     for (auto &L : m->layers) {
         take(d * 2, &L.attn_norm);
-        matrix(d + 2 * kvd, d, &L.wqkv, &L.sqkv);
-        matrix(d, d, &L.wo, &L.so);
+        matrix(d + 2 * kvd, d, &L.wqkv, &L.sqkv, &L.qkv_s1, &L.qkv_hb);
+        matrix(d, d, &L.wo, &L.so, &L.o_s1, &L.o_hb);
         take(d * 2, &L.ffn_norm);
-        matrix(2 * f, d, &L.wgu, &L.sgu);
-        matrix(d, f, &L.wdown, &L.sdown);
+        matrix(2 * f, d, &L.wgu, &L.sgu, &L.gu_s1, &L.gu_hb);
+        matrix(d, f, &L.wdown, &L.sdown, &L.down_s1, &L.down_hb);
+    }
+    if (qf) {  // f16 copy of the largest layer matrix for the prefill GEMMs
+        int64_t big = (d + 2 * kvd) * d;
+        if (2 * f * d > big) big = 2 * f * d;
+        take(mul_checked(big, 2), &m->pf_wdeq);
     }
     take(mul_checked(c.n_layers, c.ctx_len, kvd, 2), &m->k_cache);
     take(mul_checked(c.n_layers, c.ctx_len, kvd, 2), &m->v_cache);
@@ -474,6 +569,16 @@ int32_t aesir_model_get_tensor(aesir_model *m, const char *name, void *host_out,
     const TensorPlace p = place_tensor(m, ref);
     if (elements < p.rows * p.cols) return fail(AESIR_ERR_SHAPE, "aesir_model_get_tensor: output too small");
     hipStream_t s = m->ctx->stream;
+    if (p.esize == 0) {  // 4-bit types: dequantize on the device (qf_deq16's f16 values)
+        void *tmp = nullptr;
+        AESIR_HIP_TRY(hipMalloc(&tmp, (size_t)(p.rows * p.cols * 2)));
+        int32_t rc = launch_qf_dequant(s, place_qf(p), p.rows, p.cols, p.step, nullptr, tmp, p.cols);
+        if (rc == AESIR_OK && hipMemcpyAsync(host_out, tmp, (size_t)(p.rows * p.cols * 2), hipMemcpyDeviceToHost, s) != hipSuccess)
+            rc = fail(AESIR_ERR_HIP, "hipMemcpyAsync of the dequantized tensor failed");
+        if (hipStreamSynchronize(s) != hipSuccess && rc == AESIR_OK) rc = fail(AESIR_ERR_HIP, "dequantization failed");
+        (void)hipFree(tmp);
+        return rc;
+    }
     if (p.esize == 1) {  // Q8_0: dequantize f16(q * d); the product is exact in f32, so one rounding
         const int64_t nb = p.cols / 32;
         std::vector<int8_t> qs((size_t)(p.rows * p.cols));
@@ -498,6 +603,11 @@ int32_t aesir_model_init_random(aesir_model *m, uint64_t seed, float std, float 
     AESIR_TRY(bind(m->ctx));
     for (const TensorRef &ref : all_tensors(m)) {
         const TensorPlace p = place_tensor(m, ref);
+        if (p.esize == 0) {
+            AESIR_TRY(launch_qf_fill_random(m->ctx->stream, place_qf(p), p.rows, p.cols, p.step, seed,
+                                            (uint64_t)stream_id(ref), std));
+            continue;
+        }
         if (p.esize == 1) {
             AESIR_TRY(launch_fill_q8_0(m->ctx->stream, p.base, p.row_stride, p.scale, p.scale_stride, p.rows, p.cols,
                                        seed, (uint64_t)stream_id(ref), std));
@@ -611,9 +721,9 @@ int32_t aesir_model_kernel_times(aesir_model *m, int64_t pos, int32_t iters, flo
             switch (cls) {
                 case 0: return launch_qkv_rope_kv(s, qkv_args(m, l));
                 case 1: return launch_attention_decode(s, attn_args(m, l));
-                case 2: return launch_gemv_residual(s, L.wo, d, d, m->attn, m->x, L.so);
-                case 3: return launch_gate_up_swiglu(s, m->x, L.ffn_norm, c.rms_eps, L.wgu, c.ffn, d, m->act, L.sgu);
-                case 4: return launch_gemv_residual(s, L.wdown, d, c.ffn, m->act, m->x, L.sdown);
+                case 2: return launch_o_residual(m, s, L);
+                case 3: return launch_gate_up(m, s, L);
+                case 4: return launch_down_residual(m, s, L);
                 case 5: return launch_lm_head(s, lm_args(m, false));
                 default: return launch_argmax_finish(s, m->lm_parts, lm_head_groups(c.vocab), m->state, nullptr, nullptr);
             }

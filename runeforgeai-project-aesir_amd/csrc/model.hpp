@@ -22,6 +22,10 @@ struct ModelLayer {
     void *wgu = nullptr;        // [2 ffn][dim]
     void *wdown = nullptr;      // [dim][ffn]
     void *sqkv = nullptr, *so = nullptr, *sgu = nullptr, *sdown = nullptr;
+    // Q4_0 / Q4_K / Q6_K models: w* hold the nibble records and s* the s0 planes (QFMat); the
+    // s1 and hb planes are here (null where the type has none)
+    void *qkv_s1 = nullptr, *qkv_hb = nullptr, *o_s1 = nullptr, *o_hb = nullptr;
+    void *gu_s1 = nullptr, *gu_hb = nullptr, *down_s1 = nullptr, *down_hb = nullptr;
 };
 
 enum class TensorKind : int {
@@ -46,7 +50,8 @@ struct TensorRef {
 
 // GGUF shape and device placement: element (r, c) at base + r * row_stride + c (elements of
 // esize bytes: 2 for f16, 1 for Q8_0 quants); a Q8_0 matrix's block scale (r, c / 32) at
-// scale + r * scale_stride + c / 32 (f16).
+// scale + r * scale_stride + c / 32 (f16). For Q4_0 / Q4_K / Q6_K matrices (esize 0), row r of
+// the tensor is plane row r * step of the QFMat {qtype, base, hb, scale, s1}.
 struct TensorPlace {
     int64_t rows, cols;
     void *base;
@@ -55,6 +60,9 @@ struct TensorPlace {
     int esize = 2;
     void *scale = nullptr;
     int64_t scale_stride = 0;
+    int32_t qtype = 0;
+    void *s1 = nullptr, *hb = nullptr;
+    int64_t step = 1;
 };
 
 }  // namespace aesir
@@ -67,7 +75,9 @@ struct aesir_model {
     int64_t well_start = 0;
     int32_t wtype = AESIR_GGML_F16;  // matrices: AESIR_GGML_F16 or AESIR_GGML_Q8_0
     void *tok_embd = nullptr, *out_norm = nullptr, *out_w = nullptr;
-    void *tok_embd_s = nullptr, *out_w_s = nullptr;  // Q8_0 block scales
+    void *tok_embd_s = nullptr, *out_w_s = nullptr;  // Q8_0 block scales; s0 planes of 4-bit types
+    void *tok_embd_s1 = nullptr, *tok_embd_hb = nullptr, *out_w_s1 = nullptr, *out_w_hb = nullptr;
+    void *pf_wdeq = nullptr;  // 4-bit types: f16 copy of the matrix a prefill GEMM is reading
     std::vector<aesir::ModelLayer> layers;
     void *k_cache = nullptr, *v_cache = nullptr;  // [n_layers][ctx_len][kvd]
     void *x = nullptr, *q = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr;
@@ -99,6 +109,8 @@ TensorPlace place_tensor(const aesir_model *m, const TensorRef &ref);
 std::vector<TensorRef> all_tensors(const aesir_model *m);
 std::string tensor_name(const TensorRef &ref);
 int32_t model_upload(aesir_model *m, const TensorRef &ref, const void *host, int64_t rows, int64_t cols, int32_t type);
+// QFMat of one matrix of a Q4_0 / Q4_K / Q6_K model.
+QFMat model_qf(const aesir_model *m, const void *w, const void *s0, const void *s1, const void *hb);
 // Batched prefill of tokens[0..n) at positions start_pos.., in chunks of pf_rows rows; *next is the
 // greedy token after the last position.
 int32_t model_prefill(aesir_model *m, const int64_t *tokens, int64_t n, int64_t start_pos, int64_t *next);

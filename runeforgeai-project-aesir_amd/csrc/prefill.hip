@@ -977,7 +977,11 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
     h16 *X = (h16 *)m->pf_x, *Xn = (h16 *)m->pf_xn, *QKV = (h16 *)m->pf_qkv, *Q = (h16 *)m->pf_q;
     h16 *ATT = (h16 *)m->pf_att, *ACT = (h16 *)m->pf_act;
     AESIR_HIP_TRY(hipMemcpyAsync(m->pf_tokens, tokens_host, (size_t)n * sizeof(int64_t), hipMemcpyHostToDevice, s));
-    if (m->tok_embd_s)
+    const bool qf = qf_type(m->wtype);
+    if (qf)
+        AESIR_TRY(launch_qf_dequant(s, model_qf(m, m->tok_embd, m->tok_embd_s, m->tok_embd_s1, m->tok_embd_hb), n, d, 1,
+                                    (const int64_t *)m->pf_tokens, X, d));
+    else if (m->tok_embd_s)
         hipLaunchKernelGGL(embed_rows_q8_kernel, dim3((unsigned)n), dim3(kPThreads), 0, s, (const int8_t *)m->tok_embd,
                            (const h16 *)m->tok_embd_s, d, (const int64_t *)m->pf_tokens, X);
     else
@@ -986,7 +990,22 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
     AESIR_LAUNCH_CHECK("embed_rows_kernel");
     const bool mfma = prefill_mfma_ok(m);
     if (!mfma && m->wtype != AESIR_GGML_F16)
-        return fail(AESIR_ERR_UNSUPPORTED, "prefill: Q8_0 weights need the MFMA GEMM shapes (K %% 64 == 0)");
+        return fail(AESIR_ERR_UNSUPPORTED, "prefill: quantized weights need the MFMA GEMM shapes (K %% 64 == 0)");
+    // 4-bit types: each GEMM reads an f16 copy of its matrix, dequantized just before it (the
+    // prefill is not bound by weight bytes at 128 rows; the decode GEMVs read the records)
+    struct W {
+        const void *w, *s;
+    };
+    auto wmat = [&](const void *w, const void *s0, const void *s1, const void *hb, int64_t rows, int64_t K,
+                    W *out) -> int32_t {
+        if (!qf) {
+            *out = W{w, s0};
+            return AESIR_OK;
+        }
+        AESIR_TRY(launch_qf_dequant(s, model_qf(m, w, s0, s1, hb), rows, K, 1, nullptr, m->pf_wdeq, K));
+        *out = W{m->pf_wdeq, nullptr};
+        return AESIR_OK;
+    };
     const bool rowvec = d % kRowVec == 0;  // fused residual + norm rows need whole 8-column groups
     bool xn_ready = false;                 // Xn already holds this layer's attention-norm rows
     auto norm_rows = [&](const void *w) -> int32_t {
@@ -1029,9 +1048,11 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
         if (!xn_ready) AESIR_TRY(norm_rows(L.attn_norm));
         xn_ready = false;
         int64_t qkv_splits = 1;
+        W wq;
+        AESIR_TRY(wmat(L.wqkv, L.sqkv, L.qkv_s1, L.qkv_hb, qkv_n, d, &wq));
         if (mfma)
-            AESIR_TRY(launch_mfma<kEpiStore>(s, Xn, n, d, L.wqkv, qkv_n, QKV, qkv_n, m->pf_part, m->pf_part_floats,
-                                             "gemm_mfma_qkv", true, &qkv_splits, L.sqkv));
+            AESIR_TRY(launch_mfma<kEpiStore>(s, Xn, n, d, wq.w, qkv_n, QKV, qkv_n, m->pf_part, m->pf_part_floats,
+                                             "gemm_mfma_qkv", true, &qkv_splits, wq.s));
         else
             AESIR_TRY(launch_gemm_f16(m->ctx, Xn, n, d, L.wqkv, qkv_n, QKV));
         if (qkv_splits > 1) {
@@ -1076,7 +1097,9 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
         AESIR_LAUNCH_CHECK("prefill_attention_kernel");
         // O projection + residual, then the feed-forward norm (inference.mojo:227-241)
         if (mfma) {
-            AESIR_TRY(residual_gemm(ATT, d, L.wo, L.so, L.ffn_norm, "gemm_mfma_o_residual"));
+            W wo;
+            AESIR_TRY(wmat(L.wo, L.so, L.o_s1, L.o_hb, d, d, &wo));
+            AESIR_TRY(residual_gemm(ATT, d, wo.w, wo.s, L.ffn_norm, "gemm_mfma_o_residual"));
         } else {
             AESIR_TRY(launch_gemm_f16(m->ctx, ATT, n, d, L.wo, d, Xn));
             AESIR_TRY(launch_residual_add(s, X, Xn, n * d));
@@ -1085,10 +1108,13 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
         // feed-forward block (inference.mojo:235-273); the down projection's tail also produces
         // the next layer's attention-norm rows
         if (mfma) {
-            AESIR_TRY(launch_mfma<kEpiSwiglu>(s, Xn, n, d, L.wgu, 2 * f, ACT, f, m->pf_part, m->pf_part_floats,
-                                                "gemm_mfma_gate_up_swiglu", false, nullptr, L.sgu));
+            W wgu, wdn;
+            AESIR_TRY(wmat(L.wgu, L.sgu, L.gu_s1, L.gu_hb, 2 * f, d, &wgu));
+            AESIR_TRY(launch_mfma<kEpiSwiglu>(s, Xn, n, d, wgu.w, 2 * f, ACT, f, m->pf_part, m->pf_part_floats,
+                                                "gemm_mfma_gate_up_swiglu", false, nullptr, wgu.s));
             const void *next_norm = l + 1 < c.n_layers ? m->layers[l + 1].attn_norm : nullptr;
-            AESIR_TRY(residual_gemm(ACT, f, L.wdown, L.sdown, next_norm, "gemm_mfma_down_residual"));
+            AESIR_TRY(wmat(L.wdown, L.sdown, L.down_s1, L.down_hb, d, f, &wdn));
+            AESIR_TRY(residual_gemm(ACT, f, wdn.w, wdn.s, next_norm, "gemm_mfma_down_residual"));
             xn_ready = next_norm != nullptr;
         } else {
             // interleaved gate/up rows -> [n][2f] products, then the SwiGLU over the pairs

@@ -218,3 +218,37 @@ def test_gguf_inspect_q8_0_file(A, oracle, tmp_path):
     write_gguf(path, llama_metadata(cfg, cfg.vocab), tensors)
     with pytest.raises(A.AesirError, match="GGUF tensor row length is not a multiple of its block size: blk.0.ffn_down.weight"):
         A.gguf_inspect(path)
+
+
+@pytest.mark.parametrize("kind", ["q4_0", "q4_k", "q6_k"])
+def test_gguf_inspect_4bit_files(A, oracle, tmp_path, kind):
+    """Files whose matrices are all Q4_0, Q4_K or Q6_K (norms F32) pass the loader contract; a file
+    that mixes block types between matrices is refused with the reference's type message."""
+    from gguf_tools import llama_metadata, write_gguf
+
+    cfg = oracle.Config(dim=256, n_layers=1, n_heads=4, n_kv_heads=2, ffn=512, vocab=64, ctx_len=32)
+    rng = np.random.default_rng(1)
+
+    def tensor(k, r, c):
+        if k == "q4_0":
+            return A.Q4_0Tensor.from_parts(np.full((r, c // 32), 0.01, np.float16), rng.integers(0, 16, (r, c)).astype(np.uint8))
+        if k == "q4_k":
+            n = c // 256
+            return A.Q4_KTensor.from_parts(np.full((r, n), 0.001, np.float16), np.full((r, n), 0.001, np.float16),
+                                           np.ones((r, n, 8), np.uint8), np.ones((r, n, 8), np.uint8),
+                                           rng.integers(0, 16, (r, c)).astype(np.uint8))
+        return A.Q6_KTensor.from_parts(np.full((r, c // 256), 0.001, np.float16), np.ones((r, c // 256, 16), np.int8),
+                                       rng.integers(0, 64, (r, c)).astype(np.uint8))
+
+    tensors = {}
+    for name, (r, c) in oracle.tensor_shapes(cfg).items():
+        tensors[name] = np.ones(c, np.float32) if name.endswith("norm.weight") else tensor(kind, r, c)
+    path = str(tmp_path / "q.gguf")
+    write_gguf(path, llama_metadata(cfg, cfg.vocab), tensors)
+    c, _ = A.gguf_inspect(path)
+    assert (c.dim, c.ffn, c.vocab) == (256, 512, 64)
+    other = "q6_k" if kind != "q6_k" else "q4_k"
+    tensors["blk.0.attn_v.weight"] = tensor(other, cfg.kv_dim, cfg.dim)
+    write_gguf(path, llama_metadata(cfg, cfg.vocab), tensors)
+    with pytest.raises(A.AesirError, match="GGUF required tensor has an invalid type: blk.0.attn_v.weight"):
+        A.gguf_inspect(path)

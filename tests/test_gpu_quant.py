@@ -1,0 +1,258 @@
+"""GPU parity of the Q4_0, Q4_K and Q6_K weight paths (repacked records, decode GEMVs with the fused
+epilogues, batched prefill, GGUF loading) against the CPU oracle.
+
+- aesir_gemm_quant on packed GGUF blocks: Q4_0 within 1 f16 ulp of the oracle's gemm_q4_0
+  (core/compute.mojo:876-912; beyond 1 ulp only where f32 summation noise exceeds it); Q4_K / Q6_K
+  against f64 on the oracle's f32 dequantization (GGML's weights) within one f16 rounding plus
+  f32 summation noise; 16 or more rows of A take the matrix cores on f16-rounded weights and are
+  held to f64 on those.
+- Models: the F16 oracle holding the weights the model reads back (get_tensor). Q4_0's weights
+  are exactly those f16 values, so tokens are identical; the K-quant GEMVs use GGML's f32 weights,
+  which differ from the read-back f16 values by one f16 rounding, so logits are held to the
+  forward-pass tolerance and a token may differ only at a near tie of the oracle's logits.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+RNG = np.random.default_rng(4321)
+
+
+@pytest.fixture(scope="module")
+def A():
+    import aesir_hip
+
+    return aesir_hip
+
+
+@pytest.fixture(scope="module")
+def ctx(A):
+    c = A.Context(3 << 30)
+    yield c
+    c.close()
+
+
+@pytest.fixture(autouse=True)
+def well_scope(ctx):
+    off = ctx.offset
+    yield
+    ctx.synchronize()
+    ctx.reset(off)
+
+
+TYPES = {"q4_0": 2, "q4_k": 12, "q6_k": 14}
+
+
+def random_tensor(A, kind, rows, cols, rng, std=0.02):
+    """Packed GGUF blocks of a rows x cols matrix with weights of standard deviation near std."""
+    if kind == "q4_0":
+        d = (rng.uniform(0.5, 1.5, (rows, cols // 32)) * std / 4.6).astype(np.float16)
+        return A.Q4_0Tensor.from_parts(d, rng.integers(0, 16, (rows, cols)).astype(np.uint8))
+    nsb = cols // 256
+    if kind == "q4_k":
+        sc = rng.integers(1, 64, (rows, nsb, 8)).astype(np.uint8)
+        mn = rng.integers(0, 64, (rows, nsb, 8)).astype(np.uint8)
+        d = (rng.uniform(0.5, 1.5, (rows, nsb)) * std / (32 * 4.6)).astype(np.float16)
+        dmin = (d.astype(np.float32) * rng.uniform(0.5, 1.0, (rows, nsb))).astype(np.float16)
+        return A.Q4_KTensor.from_parts(d, dmin, sc, mn, rng.integers(0, 16, (rows, cols)).astype(np.uint8))
+    sc = rng.integers(-127, 128, (rows, nsb, 16)).astype(np.int8)
+    d = (rng.uniform(0.5, 1.5, (rows, nsb)) * std / (64 * 18.5)).astype(np.float16)
+    return A.Q6_KTensor.from_parts(d, sc, rng.integers(0, 64, (rows, cols)).astype(np.uint8))
+
+
+def f32_weights(oracle, kind, t):
+    nb = t.blocks.shape[0]
+    if kind == "q4_0":
+        return oracle.dequantize_q4_0(t.blocks, nb).astype(np.float32).reshape(t.rows, t.cols)
+    if kind == "q4_k":
+        return oracle.dequantize_q4_k(t.blocks, nb).reshape(t.rows, t.cols)
+    return oracle.dequantize_q6_k(t.blocks, nb).reshape(t.rows, t.cols)
+
+
+def upload_bytes(ctx, raw):
+    raw = np.ascontiguousarray(raw, np.uint8).reshape(-1)
+    t = ctx.tensor(1, (raw.size + 1) // 2)
+    buf = np.zeros(t.size * 2, np.uint8)
+    buf[: raw.size] = raw
+    t.upload(buf.view(np.float16))
+    return t.ptr
+
+
+def ulp_diff(a, b):
+    ai = np.asarray(a, np.float16).view(np.int16).astype(np.int32)
+    bi = np.asarray(b, np.float16).view(np.int16).astype(np.int32)
+    ai = np.where(ai < 0, -32768 - ai, ai)
+    bi = np.where(bi < 0, -32768 - bi, bi)
+    return np.abs(ai - bi)
+
+
+@pytest.mark.parametrize("kind", list(TYPES))
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 64), (1, 14336, 40), (3, 2048, 100), (1, 5632, 33), (1, 28672, 8),
+                                   (20, 4096, 48)])
+def test_gemm_quant_vs_oracle(A, ctx, oracle, kind, M, K, N):
+    t = random_tensor(A, kind, N, K, RNG)
+    x = RNG.standard_normal((M, K)).astype(np.float16)
+    c = ctx.tensor(M, N)
+    A.gemm_quant(ctx, ctx.from_numpy(x), upload_bytes(ctx, t.blocks), TYPES[kind], N, c)
+    got = c.numpy().astype(np.float64)
+    W = f32_weights(oracle, kind, t).astype(np.float64)
+    if M >= 16:
+        W = W.astype(np.float16).astype(np.float64)  # the matrix cores read f16 weights
+    xd = x.astype(np.float64)
+    noise = 2.0 ** -17 * (np.abs(xd) @ np.abs(W).T)
+    if kind == "q4_0" and M < 16:
+        ref = oracle.gemm_q4_0(x, t.blocks, N)
+        d = ulp_diff(got.astype(np.float16), ref)
+        bad = (d > 1) & (np.abs(got - ref.astype(np.float64)) > noise)
+        assert not bad.any(), d.max()
+        assert (d > 0).mean() < 0.02
+        return
+    exact = xd @ W.T
+    tol = np.abs(np.spacing(exact.astype(np.float16))).astype(np.float64) + noise
+    assert np.all(np.abs(got - exact) <= tol), np.max(np.abs(got - exact) / tol)
+
+
+def test_gemm_quant_errors(A, ctx):
+    a = ctx.tensor(1, 96)
+    c = ctx.tensor(1, 2)
+    with pytest.raises(A.AesirError, match="gemm_q4_0: inner dimension must be a multiple of 32"):
+        A.gemm_quant(ctx, ctx.tensor(1, 40), a.ptr, 2, 2, c)
+    with pytest.raises(A.AesirError, match="gemm_q4_k: inner dimension must be a multiple of 256"):
+        A.gemm_quant(ctx, a, a.ptr, 12, 2, c)
+    with pytest.raises(A.AesirError, match="gemm_q6_k: output matrix shape mismatch"):
+        A.gemm_quant(ctx, ctx.tensor(1, 256), a.ptr, 14, 3, c)
+    with pytest.raises(A.AesirError, match="is not Q4_0, Q8_0, Q4_K or Q6_K"):
+        A.gemm_quant(ctx, a, a.ptr, 3, 2, c)
+
+
+def quant_weights(A, oracle, cfg, kind, rng):
+    w = {}
+    for name, (r, c) in oracle.tensor_shapes(cfg).items():
+        if name.endswith("norm.weight"):
+            w[name] = (1.0 + 0.05 * rng.standard_normal(c)).astype(np.float16)
+        else:
+            w[name] = random_tensor(A, kind, r, c, rng)
+    return w
+
+
+def same_token(got, want, ref_logits):
+    if got == want:
+        return True
+    a, b = float(ref_logits[got]), float(ref_logits[want])
+    return abs(a - b) <= 2 * float(np.spacing(np.float16(max(abs(a), abs(b)))))
+
+
+def within_tol(got, ref, atol=2e-2, rtol=1e-2):
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    return bool(np.all(np.abs(got - ref) <= atol + rtol * np.abs(ref)))
+
+
+def quant_model(A, ctx, oracle, cfg, kind, seed):
+    rng = np.random.default_rng(seed)
+    m = A.Model.create(ctx, A.ModelConfig(cfg.dim, cfg.n_layers, cfg.n_heads, cfg.n_kv_heads, cfg.ffn, cfg.vocab,
+                                          cfg.ctx_len, cfg.eps, cfg.theta, 1, -1), TYPES[kind])
+    m.set_weights(quant_weights(A, oracle, cfg, kind, rng))
+    back = {name: m.get_tensor(name, shape) for name, shape in oracle.tensor_shapes(cfg).items()}
+    return m, oracle.Model(cfg, back)
+
+
+SMALL = dict(dim=256, n_layers=2, n_heads=4, n_kv_heads=2, ffn=512, vocab=300, ctx_len=160)
+
+
+@pytest.mark.parametrize("kind", list(TYPES))
+def test_quant_model_stream_matches_dequantized_oracle(A, ctx, oracle, kind):
+    """Per-position forward passes, then graph-replayed decode, against the F16 oracle on the
+    read-back weights; graph replay == eager launches == the host loop."""
+    cfg = oracle.Config(**SMALL)
+    m, om = quant_model(A, ctx, oracle, cfg, kind, 5)
+    prompt = oracle.prompt_tokens(12, cfg.vocab, 3)
+    okv = om.new_kv()
+    cur = list(prompt)
+    for p in range(len(prompt) + 20):
+        want, ol = om.forward(okv, cur, p)
+        got = m.forward_pass(cur, p)
+        assert within_tol(m.logits(), ol), (kind, p)
+        if kind == "q4_0":
+            assert got == want, p
+        else:
+            assert same_token(got, want, ol), (p, got, want)
+        if p >= len(prompt) - 1:
+            cur.append(got)
+    nxt = cur[len(prompt)]
+    g, _ = m.decode_loop(nxt, len(prompt), 16, use_graph=True)
+    e, _ = m.decode_loop(nxt, len(prompt), 16, use_graph=False)
+    host = []
+    c2 = list(prompt) + [nxt]
+    for _ in range(16):
+        host.append(m.forward_pass(c2, len(c2) - 1))
+        c2.append(host[-1])
+    assert g == e == host
+    m.close()
+
+
+@pytest.mark.parametrize("kind", list(TYPES))
+def test_quant_batched_prefill_matches_per_position(A, ctx, oracle, kind):
+    """aesir_prefill of a 140-token prompt (two chunks, matrix cores on f16 copies of the weights)
+    against the per-position oracle: next token (near ties allowed) and logits within tolerance."""
+    cfg = oracle.Config(**SMALL)
+    m, om = quant_model(A, ctx, oracle, cfg, kind, 6)
+    prompt = oracle.prompt_tokens(140, cfg.vocab, 4)
+    okv = om.new_kv()
+    for p in range(len(prompt)):
+        want, ol = om.forward(okv, prompt, p)
+    got = m.prefill(prompt, 0)
+    assert within_tol(m.logits(), ol)
+    assert same_token(got, want, ol), (got, want)
+    m.close()
+
+
+@pytest.mark.parametrize("kind", list(TYPES))
+def test_quant_gguf_file_loads_like_set_tensor(A, ctx, oracle, kind, tmp_path):
+    """A GGUF file whose matrices are all of the type (norms F32) loads into the same model."""
+    from gguf_tools import llama_metadata, write_gguf
+
+    cfg = oracle.Config(**SMALL)
+    rng = np.random.default_rng(7)
+    w = quant_weights(A, oracle, cfg, kind, rng)
+    tensors = {k: (v.astype(np.float32) if k.endswith("norm.weight") else v) for k, v in w.items()}
+    path = str(tmp_path / f"{kind}.gguf")
+    write_gguf(path, llama_metadata(cfg, cfg.vocab), tensors)
+    mf = A.Model.load_gguf(ctx, path, cfg.ctx_len)
+    assert mf.weight_type == TYPES[kind]
+    ms = A.Model.create(ctx, A.ModelConfig(cfg.dim, cfg.n_layers, cfg.n_heads, cfg.n_kv_heads, cfg.ffn, cfg.vocab,
+                                           cfg.ctx_len, cfg.eps, cfg.theta, 1, 2), TYPES[kind])
+    ms.set_weights(w)
+    prompt = oracle.prompt_tokens(6, cfg.vocab, 8)
+    a, _ = mf.generate(prompt, 8)
+    b, _ = ms.generate(prompt, 8)
+    assert a == b
+    name = "blk.1.ffn_down.weight"
+    assert np.array_equal(mf.get_tensor(name, (cfg.dim, cfg.ffn)), ms.get_tensor(name, (cfg.dim, cfg.ffn)))
+    mf.close()
+    ms.close()
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("kind", list(TYPES))
+def test_quant_llama3_8b_shape_properties(A, oracle, kind):
+    """Llama-3-8B shape with device-initialized weights of the type: graph == eager == forward_pass
+    for 6 steps from KV 2048, finite logits, and the read-back of a matrix within its weight range."""
+    cfg = oracle.LLAMA3_8B
+    with A.Context(14 << 30) as big:
+        m = A.Model.create(big, A.ModelConfig(cfg.dim, cfg.n_layers, cfg.n_heads, cfg.n_kv_heads, cfg.ffn, cfg.vocab,
+                                              2048 + 16), TYPES[kind])
+        m.init_random(11)
+        m.fill_kv_random(2048, seed=2)
+        g, _ = m.decode_loop(77, 2048, 6, use_graph=True)
+        e, _ = m.decode_loop(77, 2048, 6, use_graph=False)
+        cur = [0] * 2048 + [77]
+        host = []
+        for _ in range(6):
+            host.append(m.forward_pass(cur, len(cur) - 1))
+            assert np.all(np.isfinite(m.logits().astype(np.float32)))
+            cur.append(host[-1])
+        assert g == e == host
+        wd = m.get_tensor("blk.0.ffn_down.weight", (cfg.dim, cfg.ffn)).astype(np.float32)
+        assert np.isfinite(wd).all() and 0.01 < wd.std() < 0.04, wd.std()
+        m.close()

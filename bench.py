@@ -206,6 +206,66 @@ def q8_bench(A, seed: int, kv: int, steps: int, warmup: int, kernel_iters: int, 
             "kernel_ms": {k: round(v, 5) for k, v in kt.items()}, "tokens_head": toks[:8]}
 
 
+# Q4_0 / Q4_K / Q6_K matrices in HBM (records of 16 weights): 4-bit nibbles, Q6_K's 2-bit high
+# plane, and the per-block scale planes.
+QF_TYPES = {"q4_0": 2, "q4_k": 12, "q6_k": 14}
+
+
+def qf_mat_bytes(kind: str, rows: int, cols: int) -> int:
+    per_row = cols // 2
+    if kind == "q4_0":
+        per_row += cols // 32 * 2
+    elif kind == "q4_k":
+        per_row += cols // 32 * 2 + cols // 256 * 4
+    else:
+        per_row += cols // 4 + cols // 16 + cols // 256 * 2
+    return rows * per_row
+
+
+def qf_token_bytes(kind: str) -> int:
+    layer = (qf_mat_bytes(kind, DIM + 2 * KV_DIM, DIM) + qf_mat_bytes(kind, DIM, DIM) + qf_mat_bytes(kind, 2 * FFN, DIM)
+             + qf_mat_bytes(kind, DIM, FFN) + 2 * 2 * DIM)
+    return LAYERS * layer + qf_mat_bytes(kind, VOCAB, DIM) + 2 * DIM + qf_mat_bytes(kind, 1, DIM)
+
+
+def quant_bench(A, kind: str, seed: int, kv: int, steps: int, warmup: int, kernel_iters: int,
+                use_graph: bool = True) -> dict:
+    """Batch-1 greedy decode of the Llama-3-8B shape with Q4_0, Q4_K or Q6_K matrices (random
+    records and scales for weights of std 0.02), KV cache pre-filled to kv positions; same step
+    structure and timing as the F16 decode."""
+    ctx_len = kv + max(steps, warmup) + 64
+    well = int(qf_token_bytes(kind) + qf_mat_bytes(kind, VOCAB, DIM) + 2 * LAYERS * ctx_len * KV_DIM * 2
+               + 2 * 2 * FFN * DIM + (512 << 20))
+    ctx = A.Context(well)
+    m = A.Model.create(ctx, A.ModelConfig(DIM, LAYERS, HEADS, KV_HEADS, FFN, VOCAB, ctx_len), QF_TYPES[kind])
+    m.init_random(seed, 0.02, 0.0, 0.02)
+    m.fill_kv_random(kv, seed=seed + 1)
+    m.decode_loop(1, kv, warmup, use_graph=use_graph)
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    toks, event_ms = m.decode_loop(1, kv, steps, use_graph=use_graph)
+    ctx.synchronize()
+    wall = time.perf_counter() - t0
+    tok_s = steps / wall
+    mean_kv = kv + (steps - 1) / 2.0 + 1
+    step_bytes = qf_token_bytes(kind) + KV_BYTES_PER_POS * mean_kv + KV_BYTES_PER_POS
+    kt = m.kernel_times(kv, iters=kernel_iters)
+    gu_ms = kt["gate_up_swiglu"]
+    gu_bytes = qf_mat_bytes(kind, 2 * FFN, DIM) + DIM * 2 + DIM * 2 + FFN * 2
+    m.close()
+    ctx.close()
+    return {"workload": f"llama3-8b-shape {kind} batch-1 greedy decode, kv {kv}", "value": round(tok_s, 2),
+            "unit": "tok/s", "steps": steps, "ms_per_step": round(wall * 1e3 / steps, 4),
+            "dtype": f"{kind} weights, f16 activations, f32 accumulate",
+            "step_hbm": {"bytes_per_token": int(step_bytes), "achieved_gbs": round(step_bytes * tok_s / 1e9, 1),
+                         "frac": round(step_bytes * tok_s / 1e9 / HBM_PEAK_GBS, 4),
+                         "event_ms_per_step": round(event_ms / steps, 4)},
+            "gate_up_swiglu": {"avg_launch_ms": round(gu_ms, 5), "bytes_per_launch": gu_bytes,
+                               "achieved_gbs": round(gu_bytes / (gu_ms * 1e-3) / 1e9, 1),
+                               "frac": round(gu_bytes / (gu_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+            "kernel_ms": {k: round(v, 5) for k, v in kt.items()}, "tokens_head": toks[:8]}
+
+
 def sampler_bench(A, seed: int, reps: int = 50) -> dict:
     """aesir_sample_token (sample_token_from_logits on the device) over Llama-3's 128256 f16 logits
     with 256 context tokens: wall time per blocking call (host round trip included) for the greedy
@@ -343,6 +403,8 @@ def main():
     ap.add_argument("--no-sweep", action="store_true", help="skip the decode at KV 512 / 8192 / 32768")
     ap.add_argument("--no-micro", action="store_true", help="skip the kernel micro-suite and the Q8_0 matvec")
     ap.add_argument("--q8-only", action="store_true", help="run only the Q8_0-weight decode measurement")
+    ap.add_argument("--no-quant", action="store_true", help="skip the Q4_0 / Q4_K / Q6_K decode measurements")
+    ap.add_argument("--quant-only", action="store_true", help="run only the Q4_0 / Q4_K / Q6_K decode measurements")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain 256 MiB device-to-device copy (the FETCH_SIZE / WRITE_SIZE calibration "
                          "of the HBM traffic figure) and exit")
@@ -360,6 +422,10 @@ def main():
 
     if args.prefill_only:
         print(json.dumps({"prefill": prefill_bench(A, args.seed, n_decode=args.prefill_decode_steps)}))
+        return
+    if args.quant_only:
+        print(json.dumps({"quant": {k: quant_bench(A, k, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters,
+                                                   not args.eager) for k in QF_TYPES}}))
         return
     if args.q8_only:
         q = q8_bench(A, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters, not args.eager)
@@ -434,6 +500,9 @@ def main():
     if not args.no_q8:
         out["q8_0"] = q8_bench(A, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters, use_graph)
         out["q8_0"]["prefill"] = prefill_bench(A, args.seed, n_decode=64, q8=True)
+    if not args.no_quant:
+        out["quant"] = {k: quant_bench(A, k, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters, use_graph)
+                        for k in QF_TYPES}
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.kv, args.cpu_reps)
         out["cpu_baseline"]["value"] = round(out["cpu_baseline"]["value"], 4)

@@ -349,7 +349,6 @@ struct QVec<16> {
     u32x4 v;
     __device__ __forceinline__ static QVec load(const int8_t *p) { return QVec{ld16_stream(p)}; }
 };
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 template <>
 struct QVec<8> {
     u32x2 v;

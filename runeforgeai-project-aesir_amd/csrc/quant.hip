@@ -40,7 +40,6 @@ constexpr int kQfGroupsFfn = 2;
 constexpr int kQfDepth = 2;
 constexpr int kQfMaxSlabs[3] = {4, 2, 3};
 
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 bool qf_type(int32_t t) { return t == AESIR_GGML_Q4_0 || t == AESIR_GGML_Q4_K || t == AESIR_GGML_Q6_K; }
 

@@ -251,16 +251,21 @@ typedef struct {
  * start zeroed. Validates the GGUFModelConfig contract (loader/gguf.mojo:133-149). */
 int32_t aesir_model_create(aesir_ctx *ctx, const aesir_model_config *cfg, aesir_model **out);
 /* aesir_model_create with a weight type for the seven matrix kinds (token_embd, output, attn_q/k/v,
- * attn_output, ffn_gate/up/down): AESIR_GGML_F16 (what aesir_model_create makes) or
- * AESIR_GGML_Q8_0. A Q8_0 model keeps each matrix as int8 quants [rows][cols] plus f16 block
- * scales [rows][cols/32] in HBM (same fused row order as F16); dim and ffn must be multiples of
- * 32 (and at most 16384). Every weight is used as w = f16(f16(q) * d), gemm_q8_0's rule
- * (core/compute.mojo:1062-1063), so a Q8_0 model computes what the F16 model holding the
- * dequantized weights computes. Norm vectors stay f16. No reference counterpart as a model
- * (the reference loader has no Q8_0 model path). */
+ * attn_output, ffn_gate/up/down): AESIR_GGML_F16 (what aesir_model_create makes), AESIR_GGML_Q8_0,
+ * AESIR_GGML_Q4_0, AESIR_GGML_Q4_K or AESIR_GGML_Q6_K. A Q8_0 model keeps each matrix as int8
+ * quants [rows][cols] plus f16 block scales [rows][cols/32] in HBM (same fused row order as F16);
+ * dim and ffn must be multiples of 32 (and at most 16384). Every weight is used as
+ * w = f16(f16(q) * d), gemm_q8_0's rule (core/compute.mojo:1062-1063), so a Q8_0 model computes
+ * what the F16 model holding the dequantized weights computes. A Q4_0 / Q4_K / Q6_K model keeps
+ * each matrix repacked into 16-weight records (nibble plane, per-block scale planes, Q6_K
+ * high-bit plane); dim and ffn must be multiples of 32 (Q4_0) or 256 (K-quants), at most 28672.
+ * Q4_0 weights are w = f16(f16(q - 8) * d) (gemm_q4_0, core/compute.mojo:876-912); Q4_K and Q6_K
+ * weights are GGML's f32 values (d * sc) * q - dmin * m and (d * sc) * (q - 32). Norm vectors
+ * stay f16. No reference counterpart as a model (the reference loader has no quantized model
+ * path, loader/gguf.mojo:450-463). */
 int32_t aesir_model_create_typed(aesir_ctx *ctx, const aesir_model_config *cfg, int32_t weight_type,
                                  aesir_model **out);
-/* Weight type of the model's matrices (AESIR_GGML_F16 or AESIR_GGML_Q8_0). */
+/* Weight type of the model's matrices (AESIR_GGML_F16, _Q8_0, _Q4_0, _Q4_K or _Q6_K). */
 int32_t aesir_model_weight_type(const aesir_model *model);
 int32_t aesir_model_destroy(aesir_model *model);
 int32_t aesir_model_get_config(const aesir_model *model, aesir_model_config *cfg);
@@ -268,23 +273,27 @@ int32_t aesir_model_get_config(const aesir_model *model, aesir_model_config *cfg
  * host data in GGUF order (rows x cols, cols fastest). F32 tensors are rounded to f16 as
  * loader/gguf.mojo:486-493 does. Shape and type are checked against
  * _validate_required_tensors (loader/gguf.mojo:567-628) with its messages. The matrices of a
- * Q8_0 model take AESIR_GGML_Q8_0 data: rows x (cols/32) packed 34-byte blocks. */
+ * quantized model take data of the model's type as GGUF packs it: rows x (cols/32) blocks of 34
+ * (Q8_0) or 18 (Q4_0) bytes, rows x (cols/256) blocks of 144 (Q4_K) or 210 (Q6_K) bytes. */
 int32_t aesir_model_set_tensor(aesir_model *model, const char *name, const void *host_data, int64_t rows,
                                int64_t cols, int32_t ggml_type);
-/* Reads a tensor back in GGUF order as f16 (for verification); Q8_0 matrices come back
- * dequantized, f16(q * d) per element. */
+/* Reads a tensor back in GGUF order as f16 (for verification); quantized matrices come back
+ * dequantized: f16(q * d) (Q8_0), f16(f16(q - 8) * d) (Q4_0), GGML's f32 weight rounded once to
+ * f16 (Q4_K, Q6_K). */
 int32_t aesir_model_get_tensor(aesir_model *model, const char *name, void *host_out, int64_t elements);
 /* Device-side seeded random init: every weight N(0, std), every norm N(norm_mean, norm_std),
  * rounded to f16; element i of tensor t uses the same counter-based Box-Muller stream as the
  * test oracle's generator. For models too large to build on the host. Q8_0 matrices get
  * quants uniform in [-127, 127] and block scales uniform in [0.5, 1.5) * std / 64 (weights of
- * standard deviation near std). */
+ * standard deviation near std); Q4_0 / Q4_K / Q6_K matrices get uniform nibbles (and high bits)
+ * with scales chosen for a standard deviation near std. */
 int32_t aesir_model_init_random(aesir_model *model, uint64_t seed, float std, float norm_mean, float norm_std);
 /* GGUFSeer.mmap_and_load (loader/gguf.mojo:664-690) + AesirEngine.__init__'s layer setup
  * (aesir.mojo:237-296): parses a GGUF v3 Llama F16 file, enforces the reference loader
  * contract, creates the model (KV rows = ctx_len_override if > 0, else llama.context_length)
  * and uploads every tensor into HBM. Beyond the reference loader it also takes files whose
- * seven matrix kinds are all Q8_0 (norms F32 or F16), giving a Q8_0 model. */
+ * seven matrix kinds all share one of Q8_0, Q4_0, Q4_K or Q6_K (norms F32 or F16), giving a model
+ * of that weight type; matrices of mixed types are refused. */
 int32_t aesir_model_load_gguf(aesir_ctx *ctx, const char *path, int64_t ctx_len_override, aesir_model **out);
 
 /* GGUFSeer.inspect_metadata (loader/gguf.mojo:649-662), extended to the tensor table: parses and

@@ -279,8 +279,12 @@ __device__ __forceinline__ int64_t split_chunk(int64_t S, int64_t max_split) {
     return (chunk + kRound - 1) / kRound * kRound;
 }
 
-template <int HD, int GH>
-__global__ __launch_bounds__(kAThreads) void attn_fast_kernel(AttnArgs a) {
+// NG > 1 (short views, one split): NG groups of 256 threads share the workgroup; group q takes
+// rounds q, q + NG, ... of the view (every group runs the same number of loop iterations, the
+// surplus ones masked), and the groups' (m, l, acc) are combined in LDS before the output is
+// written, so no merge launch follows.
+template <int HD, int GH, int NG>
+__global__ __launch_bounds__(kAThreads * NG) void attn_fast_kernel(AttnArgs a) {
     constexpr int TPP = HD / 16;              // score threads per K row (16 dims each)
     constexpr int RPP = kAThreads / TPP;      // K rows per score pass
     constexpr int NSP = kRound / RPP;         // score passes per round (2 for HD 128, 1 for HD 64)
@@ -290,12 +294,20 @@ __global__ __launch_bounds__(kAThreads) void attn_fast_kernel(AttnArgs a) {
     constexpr int PVS = kAThreads / kItems;   // PV position groups (1, 2, 4 or 8)
     constexpr int NPOS = kRound / PVS;        // positions per thread per round in the PV pass
     static_assert(NSP * RPP == kRound && NVL * kAThreads == kRound * VCH && kItems * PVS == kAThreads, "shape");
-    __shared__ __align__(16) float sc[GH][kRound];  // scores, then probabilities
-    __shared__ __align__(16) h16 vs[kRound][HD];
-    __shared__ float alpha[GH], mrun[GH], lrun[GH];
-    __shared__ float2 pvx[PVS > 1 ? PVS - 1 : 1][kItems];
+    __shared__ __align__(16) float scs[NG][GH][kRound];  // scores, then probabilities
+    __shared__ __align__(16) h16 vss[NG][kRound][HD];
+    __shared__ float alphas[NG][GH], mruns[NG][GH], lruns[NG][GH];
+    __shared__ float2 pvxs[NG][PVS > 1 ? PVS - 1 : 1][kItems];
+    __shared__ float2 gacc[NG > 1 ? NG - 1 : 1][kItems];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x % kAThreads, grp = threadIdx.x / kAThreads;  // thread in its group
+    const int lane = tid & 63, wave = tid >> 6;
+    auto &sc = scs[grp];
+    auto &vs = vss[grp];
+    auto &alpha = alphas[grp];
+    auto &mrun = mruns[grp];
+    auto &lrun = lruns[grp];
+    auto &pvx = pvxs[grp];
     const int64_t G = a.nq / a.nkv;
     const int g = blockIdx.y, hg = blockIdx.z;
     const int split = blockIdx.x;
@@ -315,6 +327,8 @@ __global__ __launch_bounds__(kAThreads) void attn_fast_kernel(AttnArgs a) {
 
     // K/V requests of one round (rows past p1 re-read row t0 and are masked)
     auto load_round = [&](int64_t t0, u32x4 (&kr)[NSP][2], u32x4 (&vr)[NVL]) {
+        if constexpr (NG > 1)
+            if (t0 >= p1) t0 = p0;  // a group's surplus round re-reads the first round (masked)
         const int n = (int)(p1 - t0 < kRound ? p1 - t0 : kRound);
 #pragma unroll
         for (int i = 0; i < NSP; i++) {
@@ -329,8 +343,11 @@ __global__ __launch_bounds__(kAThreads) void attn_fast_kernel(AttnArgs a) {
             vr[i] = ld16(Vb + (t0 + (r < n ? r : 0)) * a.v_stride + 8 * c);
         }
     };
+    const int nrounds = (int)((p1 - p0 + kRound - 1) / kRound);
+    const int iters = (nrounds + NG - 1) / NG;  // loop iterations of every group
+    auto round_t0 = [&](int j) { return p0 + (int64_t)kRound * (grp + NG * j); };
     u32x4 kr[NSP][2], vr[NVL], kn[NSP][2], vn[NVL];
-    load_round(p0, kr, vr);
+    load_round(NG > 1 ? round_t0(0) : p0, kr, vr);
     u32x4 qr[GH][2];
     {
         const h16 *qb = reinterpret_cast<const h16 *>(a.q) + head0 * HD + 16 * sc_c;
@@ -345,7 +362,7 @@ __global__ __launch_bounds__(kAThreads) void attn_fast_kernel(AttnArgs a) {
     // One round: scores, V to LDS, online softmax, P V. The caller owns the barrier that lets the
     // next round rewrite sc and vs.
     auto round = [&](int64_t t0, const u32x4 (&kc)[NSP][2], const u32x4 (&vc)[NVL]) {
-        const int n_here = (int)(p1 - t0 < kRound ? p1 - t0 : kRound);
+        const int n_here = NG > 1 && t0 >= p1 ? 0 : (int)(p1 - t0 < kRound ? p1 - t0 : kRound);  // 0: surplus round
 #pragma unroll
         for (int i = 0; i < NSP; i++) {
 #pragma unroll
@@ -363,7 +380,7 @@ __global__ __launch_bounds__(kAThreads) void attn_fast_kernel(AttnArgs a) {
         }
         __syncthreads();
         // online softmax of head `wave` over the round (one position per lane)
-        if (wave < GH) {
+        if (wave < GH && (NG == 1 || n_here > 0)) {
             const float s = lane < n_here ? sc[wave][lane] : -INFINITY;
             const float mn = fmaxf(m_w, wave_max(s));
             const float pr = lane < n_here ? expf(s - mn) : 0.0f;
@@ -375,6 +392,7 @@ __global__ __launch_bounds__(kAThreads) void attn_fast_kernel(AttnArgs a) {
         }
         __syncthreads();
         // P V over this thread's positions of the round (probabilities are 0 beyond n_here)
+        if (NG > 1 && n_here == 0) return;
         const float al = alpha[ph];
         acc0 *= al;
         acc1 *= al;
@@ -391,20 +409,76 @@ __global__ __launch_bounds__(kAThreads) void attn_fast_kernel(AttnArgs a) {
     };
     // Rounds with a successor request it before computing (unconditionally, so the compiler's wait
     // counts stay exact and the successor's loads overlap this round); the last round follows.
-    int64_t t0 = p0;
-    for (; t0 + kRound < p1; t0 += kRound) {
-        load_round(t0 + kRound, kn, vn);
-        round(t0, kr, vr);
+    if constexpr (NG == 1) {
+        int64_t t0 = p0;
+        for (; t0 + kRound < p1; t0 += kRound) {
+            load_round(t0 + kRound, kn, vn);
+            round(t0, kr, vr);
 #pragma unroll
-        for (int i = 0; i < NSP; i++) {
-            kr[i][0] = kn[i][0];
-            kr[i][1] = kn[i][1];
+            for (int i = 0; i < NSP; i++) {
+                kr[i][0] = kn[i][0];
+                kr[i][1] = kn[i][1];
+            }
+#pragma unroll
+            for (int i = 0; i < NVL; i++) vr[i] = vn[i];
+            __syncthreads();  // sc and vs are rewritten by the next round
         }
+        round(t0, kr, vr);
+    } else {
+        int j = 0;
+        for (; j + 1 < iters; j++) {
+            load_round(round_t0(j + 1), kn, vn);
+            round(round_t0(j), kr, vr);
 #pragma unroll
-        for (int i = 0; i < NVL; i++) vr[i] = vn[i];
-        __syncthreads();  // sc and vs are rewritten by the next round
+            for (int i = 0; i < NSP; i++) {
+                kr[i][0] = kn[i][0];
+                kr[i][1] = kn[i][1];
+            }
+#pragma unroll
+            for (int i = 0; i < NVL; i++) vr[i] = vn[i];
+            __syncthreads();
+        }
+        round(round_t0(j), kr, vr);
     }
-    round(t0, kr, vr);
+
+    if constexpr (NG > 1) {  // combine the groups (one split: the output is written here)
+        if (wave < GH && lane == 0) {
+            mrun[wave] = m_w;
+            lrun[wave] = l_w;
+        }
+        if (PVS > 1 && pg > 0) pvx[pg - 1][item] = float2{acc0, acc1};
+        __syncthreads();
+        if (pg == 0) {
+#pragma unroll
+            for (int q = 0; q < PVS - 1; q++) {
+                const float2 o = pvx[q][item];
+                acc0 += o.x;
+                acc1 += o.y;
+            }
+            if (grp > 0) gacc[grp - 1][item] = float2{acc0, acc1};
+        }
+        __syncthreads();
+        if (grp == 0 && pg == 0) {
+            float M = mruns[0][ph];
+#pragma unroll
+            for (int q = 1; q < NG; q++) M = fmaxf(M, mruns[q][ph]);  // group 0 always has a round
+            float L = lruns[0][ph] * expf(mruns[0][ph] - M);
+            acc0 *= expf(mruns[0][ph] - M);
+            acc1 *= expf(mruns[0][ph] - M);
+#pragma unroll
+            for (int q = 1; q < NG; q++) {
+                const float e = expf(mruns[q][ph] - M);  // 0 for a group without rounds
+                const float2 o = gacc[q - 1][item];
+                L = fmaf(lruns[q][ph], e, L);
+                acc0 = fmaf(o.x, e, acc0);
+                acc1 = fmaf(o.y, e, acc1);
+            }
+            h16 *out = reinterpret_cast<h16 *>(a.out) + (head0 + ph) * HD + pd;
+            out[0] = (h16)(acc0 / L);
+            out[1] = (h16)(acc1 / L);
+        }
+        return;
+    }
 
     // Write the partial (or the output for one split). With one PV position group and one head
     // per wave (head_dim 128, 4 heads per workgroup), thread t's head is its wave's, whose
@@ -552,9 +626,15 @@ static int fast_group(const AttnArgs &a) {
     return G % 4 == 0 ? 4 : G % 2 == 0 ? 2 : 1;
 }
 
-// Split count: one 64-position round per split up to 64 splits (more splits cost more in the
-// merge than they gain in parallelism on MI355X; longer views give each split several rounds).
+// Views of at most this many positions run as one split: one workgroup per head group with
+// kSingleGroups(hd) groups of 256 threads taking two rounds each at most, and no merge launch.
+static int64_t single_split_max(int64_t hd) { return hd == 64 ? 8 * kRound : hd == 128 ? 4 * kRound : 0; }
+
+// Split count: one split for short views (above); otherwise one 64-position round per split up
+// to 64 splits (more splits cost more in the merge than they gain in parallelism on MI355X;
+// longer views give each split several rounds).
 int64_t attention_split_count(int64_t hd, int64_t max_positions) {
+    if (max_positions <= single_split_max(hd)) return 1;
     const bool fast = hd == 64 || hd == 128;
     const int64_t per = fast ? kRound : kTile;
     const int64_t cap = fast ? 64 : kMaxSplit;
@@ -576,10 +656,26 @@ int32_t launch_attention_decode(hipStream_t s, const AttnArgs &a) {
         return fail(AESIR_ERR_UNSUPPORTED, "attention: query group x head_dim too large");
     if (a.max_split < 1 || a.max_split > kMaxFastSplit) return fail(AESIR_ERR_INVALID, "attention: bad split count");
     if (a.hd / 2 > kMergeThreads * 64) return fail(AESIR_ERR_UNSUPPORTED, "attention: head_dim too large for the merge");
+    if (const int gh = fast_group(a); gh && a.max_split == 1) {
+        // one split: NG groups per workgroup (4 for head_dim 64 with 2 heads per workgroup, 2
+        // for head_dim 128 with up to 4, whose registers allow only 2 groups), no merge
+        const int gs = a.hd == 64 && gh > 2 ? 2 : gh;
+        const dim3 grid(1u, (unsigned)a.nkv, (unsigned)(G / gs));
+#define AESIR_ATTN_ONE(HDV, GHV, NGV)                                                          \
+    if (a.hd == HDV && gs == GHV) hipLaunchKernelGGL((attn_fast_kernel<HDV, GHV, NGV>), grid, dim3(kAThreads * NGV), 0, s, a);
+        AESIR_ATTN_ONE(128, 4, 2)
+        AESIR_ATTN_ONE(128, 2, 2)
+        AESIR_ATTN_ONE(128, 1, 2)
+        AESIR_ATTN_ONE(64, 2, 4)
+        AESIR_ATTN_ONE(64, 1, 4)
+#undef AESIR_ATTN_ONE
+        AESIR_LAUNCH_CHECK("attn_fast_kernel (one split)");
+        return AESIR_OK;
+    }
     if (const int gh = fast_group(a)) {
         const dim3 grid((unsigned)a.max_split, (unsigned)a.nkv, (unsigned)(G / gh));
 #define AESIR_ATTN_FAST(HDV, GHV)                                                              \
-    if (a.hd == HDV && gh == GHV) hipLaunchKernelGGL((attn_fast_kernel<HDV, GHV>), grid, dim3(kAThreads), 0, s, a);
+    if (a.hd == HDV && gh == GHV) hipLaunchKernelGGL((attn_fast_kernel<HDV, GHV, 1>), grid, dim3(kAThreads), 0, s, a);
         AESIR_ATTN_FAST(128, 4)
         AESIR_ATTN_FAST(128, 2)
         AESIR_ATTN_FAST(128, 1)

@@ -665,6 +665,77 @@ void ao_dequantize_q6_k(const uint8_t *blocks, float *out, int64_t n_blocks) {
     }
 }
 
+/* Correctly rounded binary64 -> binary16: round to odd into f32 (24 significant bits, more than
+ * the 11 + 2 that f16 needs), then round to nearest even into f16; the sticky odd bit makes the
+ * two roundings equal one (Boldo and Melquiond, "When double rounding is odd", 2005). */
+static uint16_t ao_f64_to_f16(double x) {
+    float f = (float)x;
+    if ((double)f != x) {
+        if (fabs((double)f) > fabs(x)) f = nextafterf(f, 0.0f); /* toward zero */
+        uint32_t b;
+        memcpy(&b, &f, 4);
+        b |= 1u;
+        memcpy(&f, &b, 4);
+    }
+    return F2H(f);
+}
+
+/* The library's f16 K-quant weights (quant.hip): the block's scale products rounded to f16, then
+ * one rounding of the weight, in the f16 arithmetic of the reference's dequantize_q4_k_m
+ * (compute.mojo:245-262, q * scale + min) and dequantize_q6_k_block (compute.mojo:508-527):
+ *   Q4_K  w = f16(a q - b), a = f16(d sc), b = f16(dmin m)   (a fused multiply-add: one rounding)
+ *   Q6_K  w = f16(a (q - 32)), a = f16(d sc)
+ * d sc and dmin m are exact in f32 (11 x 8 bits), so F2H rounds them once; a q - b is exact in f64
+ * (at most 43 significant bits across the f16 exponent range) and ao_f64_to_f16 rounds it once;
+ * a (q - 32) is exact in f32. Block fields and weight order as ao_dequantize_q4_k / _q6_k. */
+void ao_dequantize_q4_k_f16(const uint8_t *blocks, uint16_t *out, int64_t n_blocks) {
+    for (int64_t b = 0; b < n_blocks; b++) {
+        const uint8_t *blk = blocks + b * Q4_K_BLOCK_BYTES;
+        uint16_t dh, mh;
+        memcpy(&dh, blk, 2);
+        memcpy(&mh, blk + 2, 2);
+        const float d = H2F(dh), dmin = H2F(mh);
+        const uint8_t *sc = blk + 4, *qs = blk + 16;
+        uint16_t *y = out + b * 256;
+        for (int g = 0; g < 4; g++) {
+            int s0, m0, s1, m1;
+            q4_k_scale_min(sc, 2 * g, &s0, &m0);
+            q4_k_scale_min(sc, 2 * g + 1, &s1, &m1);
+            const double a0 = H2F(F2H(d * (float)s0)), b0 = H2F(F2H(dmin * (float)m0));
+            const double a1 = H2F(F2H(d * (float)s1)), b1 = H2F(F2H(dmin * (float)m1));
+            for (int l = 0; l < 32; l++) {
+                y[64 * g + l] = ao_f64_to_f16(a0 * (double)(qs[32 * g + l] & 0x0F) - b0);
+                y[64 * g + 32 + l] = ao_f64_to_f16(a1 * (double)(qs[32 * g + l] >> 4) - b1);
+            }
+        }
+    }
+}
+
+void ao_dequantize_q6_k_f16(const uint8_t *blocks, uint16_t *out, int64_t n_blocks) {
+    for (int64_t b = 0; b < n_blocks; b++) {
+        const uint8_t *blk = blocks + b * Q6_K_BLOCK_BYTES;
+        uint16_t dh;
+        memcpy(&dh, blk + 208, 2);
+        const float d = H2F(dh);
+        uint16_t *y = out + b * 256;
+        for (int h = 0; h < 2; h++) {
+            const uint8_t *ql = blk + 64 * h, *qh = blk + 128 + 32 * h;
+            const int8_t *sc = (const int8_t *)(blk + 192 + 8 * h);
+            for (int l = 0; l < 32; l++) {
+                const int is = l / 16;
+                const int q[4] = {((ql[l] & 15) | (((qh[l] >> 0) & 3) << 4)) - 32,
+                                  ((ql[l + 32] & 15) | (((qh[l] >> 2) & 3) << 4)) - 32,
+                                  ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32,
+                                  ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32};
+                for (int j = 0; j < 4; j++) {
+                    const float a = H2F(F2H(d * (float)sc[is + 2 * j]));
+                    y[128 * h + 32 * j + l] = F2H(a * (float)q[j]);
+                }
+            }
+        }
+    }
+}
+
 /* ------------------------------------------------------------------ KV cache */
 
 /* KVCache.append, mimir_well.mojo:488-501 */

@@ -85,6 +85,8 @@ void ao_dequantize_q4_0(const uint8_t *blocks, uint16_t *out, int64_t n_blocks);
  * to f32 (GGML's published format; see aesir_oracle.c). */
 void ao_dequantize_q4_k(const uint8_t *blocks, float *out, int64_t n_blocks);
 void ao_dequantize_q6_k(const uint8_t *blocks, float *out, int64_t n_blocks);
+void ao_dequantize_q4_k_f16(const uint8_t *blocks, uint16_t *out, int64_t n_blocks);
+void ao_dequantize_q6_k_f16(const uint8_t *blocks, uint16_t *out, int64_t n_blocks);
 
 /* ---- KV cache (mimir_well.mojo:434-521) over caller-owned buffers ---- */
 typedef struct {

@@ -70,6 +70,10 @@ def lib():
         L.ao_dequantize_q4_k.restype = None
         L.ao_dequantize_q6_k.argtypes = [P, P, I64]
         L.ao_dequantize_q6_k.restype = None
+        L.ao_dequantize_q4_k_f16.argtypes = [P, P, I64]
+        L.ao_dequantize_q4_k_f16.restype = None
+        L.ao_dequantize_q6_k_f16.argtypes = [P, P, I64]
+        L.ao_dequantize_q6_k_f16.restype = None
         L.ao_kv_append.argtypes = [P, I64, I64, P, I64, P, I64]
         L.ao_kv_slice.argtypes = [P, I64, I64, P, P]
         L.ao_forward_scratch_elems.argtypes = [P]
@@ -289,6 +293,22 @@ def dequantize_q6_k(blocks, n_blocks) -> np.ndarray:
     blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
     out = np.zeros(n_blocks * 256, dtype=np.float32)
     lib().ao_dequantize_q6_k(_ptr(blocks), _ptr(out), n_blocks)
+    return out
+
+
+def dequantize_q4_k_f16(blocks, n_blocks) -> np.ndarray:
+    """GGML block_q4_K super-blocks -> the library's f16 weights f16(f16(d sc) q - f16(dmin m))."""
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    out = np.zeros(n_blocks * 256, dtype=np.float16)
+    lib().ao_dequantize_q4_k_f16(_ptr(blocks), _ptr(out), n_blocks)
+    return out
+
+
+def dequantize_q6_k_f16(blocks, n_blocks) -> np.ndarray:
+    """GGML block_q6_K super-blocks -> the library's f16 weights f16(f16(d sc) (q - 32))."""
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    out = np.zeros(n_blocks * 256, dtype=np.float16)
+    lib().ao_dequantize_q6_k_f16(_ptr(blocks), _ptr(out), n_blocks)
     return out
 
 

@@ -227,30 +227,33 @@ int32_t aesir_gemm_quant(aesir_ctx *ctx, const void *A, int64_t a_rows, int64_t 
         return fail(AESIR_ERR_SHAPE, "%s: inner dimension must be a multiple of %lld", nm, (long long)blk);
     if (c_rows != a_rows || c_cols != b_rows) return fail(AESIR_ERR_SHAPE, "%s: output matrix shape mismatch", nm);
     if (!A || !blocks || !C) return fail(AESIR_ERR_INVALID, "%s: null tensor pointer", nm);
-    // The blocks are repacked into records in free well space for this call; the space is
-    // released after enqueueing (later work on the stream runs after this call's kernels).
+    // Fewer than 16 rows of A on whole 128-weight segments: the blocks are repacked into tiled
+    // records and each row runs the decode GEMV. Otherwise the blocks are dequantized to f16 (the
+    // same values) for the F16 GEMM, on the matrix cores from 16 rows. Both take free well space
+    // for this call, released after enqueueing (later work on the stream runs after these kernels).
     const int64_t K = a_cols, N = b_rows, mark = ctx->well_offset;
-    QFMat w;
-    w.type = ggml_type;
-    void *planes[4] = {nullptr, nullptr, nullptr, nullptr};
     int32_t rc = AESIR_OK;
-    for (int plane = 0; plane < 4 && rc == AESIR_OK; plane++) {
-        const int64_t rb = qf_plane_row_bytes(ggml_type, plane, K);
-        if (rb > 0) rc = well_alloc_bytes(ctx, mul_checked(N, rb), &planes[plane]);
-    }
-    w.nib = planes[0];
-    w.hb = planes[1];
-    w.s0 = planes[2];
-    w.s1 = planes[3];
-    if (rc == AESIR_OK) rc = launch_qf_repack(ctx->stream, ggml_type, blocks, N, K, w, 1);
-    if (rc == AESIR_OK && a_rows >= 16) {  // matrix cores on an f16 copy of the weights
-        void *wf = nullptr;
-        rc = well_alloc_bytes(ctx, mul_checked(N, K, 2), &wf);
-        if (rc == AESIR_OK) rc = launch_qf_dequant(ctx->stream, w, N, K, 1, nullptr, wf, K);
-        if (rc == AESIR_OK) rc = launch_gemm_f16_mfma(ctx, A, a_rows, K, wf, N, C);
-    } else {
+    if (a_rows < 16 && qf_gemv_ok(K)) {
+        QFMat w;
+        w.type = ggml_type;
+        void *planes[4] = {nullptr, nullptr, nullptr, nullptr};
+        for (int plane = 0; plane < 4 && rc == AESIR_OK; plane++) {
+            const int64_t rb = qf_plane_row_bytes(ggml_type, plane, K);
+            if (rb > 0) rc = well_alloc_bytes(ctx, mul_checked(qf_rows_alloc(N), rb), &planes[plane]);
+        }
+        w.nib = planes[0];
+        w.hb = planes[1];
+        w.s0 = planes[2];
+        w.s1 = planes[3];
+        if (rc == AESIR_OK) rc = launch_qf_repack(ctx->stream, ggml_type, blocks, N, K, w, 1);
         for (int64_t r = 0; r < a_rows && rc == AESIR_OK; r++)
             rc = launch_qf_gemv_store(ctx->stream, w, N, K, (const uint16_t *)A + r * K, (uint16_t *)C + r * N);
+    } else {
+        void *wf = nullptr;
+        rc = well_alloc_bytes(ctx, mul_checked(N, K, 2), &wf);
+        if (rc == AESIR_OK) rc = launch_gguf_dequant(ctx->stream, ggml_type, blocks, N, K, wf);
+        if (rc == AESIR_OK)
+            rc = a_rows >= 16 ? launch_gemm_f16_mfma(ctx, A, a_rows, K, wf, N, C) : launch_gemm_f16(ctx, A, a_rows, K, wf, N, C);
     }
     ctx->well_offset = mark;
     return rc;

@@ -31,15 +31,23 @@ int32_t launch_gemm_f16_mfma(aesir_ctx *ctx, const void *A, int64_t M, int64_t K
 // records of 16 weights: record r of a row holds weights 16 r .. 16 r + 15.
 //   nib  8 bytes per record: byte j holds weight 16 r + j in its low nibble and 16 r + 8 + j in
 //        its high nibble (Q6_K: the low 4 of the 6 bits);
-//   hb   Q6_K only, 4 bytes per record: the high 2 bits of weight 16 r + i at bit
-//        16 ((i >> 1) & 1) + 2 (2 (i >> 2) + (i & 1));
+//   hb   Q6_K only, 4 bytes per record: the high 2 bits of the record's weights (bit layout in
+//        quant.hip, qf_hb_pos);
 //   s0   Q4_0: f16 d per 32 weights; Q4_K: (scale, min) bytes per 32 weights, 6-bit values
 //        unpacked; Q6_K: int8 scale per 16 weights;
 //   s1   Q4_K: (d, dmin) f16 pair per 256 weights; Q6_K: f16 d per 256 weights.
-// Plane rows are `step` logical rows apart (step 2 for the interleaved gate/up rows).
+// The nib, hb and s0 planes are tiled for the matrix-core GEMV: rows in blocks of 16 and records
+// in segments of 8 (128 weights, K a multiple of 128); tile (row block, segment) stores, for
+// record pair q = (record % 8) / 2 and row i of the block, the pair's 16 nibble bytes (8 hb bytes,
+// 2 s0 bytes) at [q][i], so that lane l of a wave reading 16 (8, 2) bytes at l times that size
+// gets row l % 16 and record pair l / 16: the A-operand layout of v_mfma_f32_16x16x32_f16. s1 is
+// [row block][K / 256][row % 16] (the 16 rows' entries of a super-block together). Planes hold
+// qf_rows_alloc(N) rows (whole row blocks). Logical row r of a fused sub-matrix is plane row
+// row0 + r * step (step 2 for the interleaved gate/up rows).
 struct QFMat {
     int32_t type = 0;
     const void *nib = nullptr, *hb = nullptr, *s0 = nullptr, *s1 = nullptr;
+    int64_t row0 = 0;
 };
 // Bytes of one row of each plane (0 if the type has no such plane). plane: 0 nib, 1 hb, 2 s0, 3 s1.
 __host__ __device__ inline int64_t qf_plane_row_bytes(int32_t type, int plane, int64_t K) {
@@ -51,18 +59,43 @@ __host__ __device__ inline int64_t qf_plane_row_bytes(int32_t type, int plane, i
         default: return 0;
     }
 }
+// Plane rows allocated for an N-row matrix (whole 16-row blocks).
+__host__ __device__ inline int64_t qf_rows_alloc(int64_t N) { return (N + 15) / 16 * 16; }
+// Tile of (plane row r, record rec) and the byte offsets of the record's planes.
+__host__ __device__ inline int64_t qf_tile(int64_t r, int64_t rec, int64_t K) { return (r >> 4) * (K >> 7) + (rec >> 3); }
+__host__ __device__ inline int64_t qf_nib_off(int64_t r, int64_t rec, int64_t K) {
+    return qf_tile(r, rec, K) * 1024 + ((rec & 7) >> 1) * 256 + (r & 15) * 16 + (rec & 1) * 8;
+}
+__host__ __device__ inline int64_t qf_hbw_off(int64_t r, int64_t rec, int64_t K) {
+    return qf_tile(r, rec, K) * 512 + ((rec & 7) >> 1) * 128 + (r & 15) * 8 + (rec & 1) * 4;
+}
+// s0 entry of the record's pair (Q4_0 d, Q4_K scale | min << 8); Q6_K's byte of the record is at
+// + (rec & 1)
+__host__ __device__ inline int64_t qf_s0_off(int64_t r, int64_t rec, int64_t K) {
+    return qf_tile(r, rec, K) * 128 + ((rec & 7) >> 1) * 32 + (r & 15) * 2;
+}
+__host__ __device__ inline int64_t qf_s1_off(int64_t r, int64_t rec, int64_t K, int esize) {
+    return (((r >> 4) * (K >> 8) + (rec >> 4)) * 16 + (r & 15)) * esize;
+}
 // True for the types this layout serves.
 bool qf_type(int32_t type);
-// GGUF blocks (rows x K, packed, device memory) -> planes of rows 0.. of `dst` (rows `step` apart).
+// GGUF blocks (rows x K, packed, device memory) -> planes of rows dst.row0 + r * step.
 int32_t launch_qf_repack(hipStream_t s, int32_t type, const void *blocks, int64_t rows, int64_t K, const QFMat &dst,
                          int64_t step);
 // Planes -> f16 [rows][K] (out_stride elements per output row); `row_ids` (device, may be null)
-// selects the source rows (embedding lookups), else rows 0 .. rows - 1.
+// selects the source rows (embedding lookups), else rows 0 .. rows - 1 (of w.row0, `step` apart).
 int32_t launch_qf_dequant(hipStream_t s, const QFMat &w, int64_t rows, int64_t K, int64_t step,
                           const int64_t *row_ids, void *out, int64_t out_stride);
 // Seeded synthetic planes: weights of standard deviation near `std`, mean near 0.
 int32_t launch_qf_fill_random(hipStream_t s, const QFMat &w, int64_t rows, int64_t K, int64_t step, uint64_t seed,
                               uint64_t stream, float std);
+// GGUF blocks (rows x K, packed, device memory) -> f16 [rows][K] straight from the blocks, the
+// same f16 values as launch_qf_dequant (the per-op GEMMs of 16 or more rows, and of row lengths
+// the GEMV does not take).
+int32_t launch_gguf_dequant(hipStream_t s, int32_t type, const void *blocks, int64_t rows, int64_t K, void *out);
+// The decode GEMV stages x in LDS (2 K bytes) and works on whole 128-weight segments.
+constexpr int64_t kQfGemvMaxK = 28672;
+bool qf_gemv_ok(int64_t K);
 // y[n] = f16(sum_k x[k] w[n, k]) for one row of x (the per-op GEMV of a repacked matrix).
 int32_t launch_qf_gemv_store(hipStream_t s, const QFMat &w, int64_t N, int64_t K, const void *x, void *y);
 // Decode-step GEMVs of repacked matrices with the fused epilogues (see the F16 launchers).

@@ -72,7 +72,7 @@ int32_t parse_tensor_name(const aesir_model *m, const char *name, TensorRef *ref
 
 // Expected GGUF shape (rows, cols) and the device placement of a tensor: element (r, c) of the
 // GGUF tensor lives at base + r * row_stride + c (and its Q8_0 block scale at
-// scale + r * scale_stride + c / 32).
+// scale + r * scale_stride + c / 32); a 4-bit tensor's row r is plane row row0 + r * step.
 TensorPlace place_tensor(const aesir_model *m, const TensorRef &ref) {
     const int64_t d = m->cfg.dim, kvd = m->kvd, f = m->cfg.ffn, V = m->cfg.vocab;
     const bool q8 = m->wtype == AESIR_GGML_Q8_0, qf = qf_type(m->wtype);
@@ -82,14 +82,12 @@ TensorPlace place_tensor(const aesir_model *m, const TensorRef &ref) {
     auto mat = [&](int64_t rows, int64_t cols, void *base, void *scale, void *s1, void *hb, int64_t r0,
                    int64_t step) {
         if (qf) {
-            auto at = [&](void *p, int plane) {
-                return p ? (void *)((char *)p + r0 * qf_plane_row_bytes(m->wtype, plane, cols)) : nullptr;
-            };
-            TensorPlace p{rows, cols, at(base, 0), 0, false, 0, at(scale, 2), 0};
+            TensorPlace p{rows, cols, base, 0, false, 0, scale, 0};
             p.qtype = m->wtype;
-            p.s1 = at(s1, 3);
-            p.hb = at(hb, 1);
+            p.s1 = s1;
+            p.hb = hb;
             p.step = step;
+            p.row0 = r0;
             return p;
         }
         TensorPlace p{rows, cols, (char *)base + r0 * cols * es, step * cols, false, es, nullptr, 0};
@@ -134,6 +132,7 @@ static QFMat place_qf(const TensorPlace &p) {
     q.s0 = p.scale;
     q.s1 = p.s1;
     q.hb = p.hb;
+    q.row0 = p.row0;
     return q;
 }
 
@@ -424,8 +423,9 @@ int32_t aesir_model_create_typed(aesir_ctx *ctx, const aesir_model_config *cfg, 
     if (q8 && (c.dim % 32 != 0 || c.ffn % 32 != 0 || c.dim > 16384 || c.ffn > 16384))
         return fail(AESIR_ERR_UNSUPPORTED, "model: Q8_0 weights need dim and ffn to be multiples of 32, at most 16384");
     if (qf) {
-        const int64_t blk = weight_type == AESIR_GGML_Q4_0 ? 32 : 256;
-        if (c.dim % blk != 0 || c.ffn % blk != 0 || c.dim > 28672 || c.ffn > 28672)
+        // whole 128-weight segments of the repacked planes; K-quant super-blocks of 256
+        const int64_t blk = weight_type == AESIR_GGML_Q4_0 ? 128 : 256;
+        if (c.dim % blk != 0 || c.ffn % blk != 0 || c.dim > kQfGemvMaxK || c.ffn > kQfGemvMaxK)
             return fail(AESIR_ERR_UNSUPPORTED, "model: %s weights need dim and ffn to be multiples of %lld, at most 28672",
                         weight_type == AESIR_GGML_Q4_0 ? "Q4_0" : weight_type == AESIR_GGML_Q4_K ? "Q4_K" : "Q6_K",
                         (long long)blk);
@@ -459,7 +459,7 @@ int32_t aesir_model_create_typed(aesir_ctx *ctx, const aesir_model_config *cfg, 
         if (qf) {
             for (int plane = 0; plane < 4; plane++) {
                 const int64_t rb = qf_plane_row_bytes(weight_type, plane, cols);
-                if (rb > 0) take(mul_checked(rows, rb), plane == 0 ? w : plane == 1 ? hb : plane == 2 ? scale : s1);
+                if (rb > 0) take(mul_checked(qf_rows_alloc(rows), rb), plane == 0 ? w : plane == 1 ? hb : plane == 2 ? scale : s1);
             }
             return;
         }

@@ -51,7 +51,7 @@ struct TensorRef {
 // GGUF shape and device placement: element (r, c) at base + r * row_stride + c (elements of
 // esize bytes: 2 for f16, 1 for Q8_0 quants); a Q8_0 matrix's block scale (r, c / 32) at
 // scale + r * scale_stride + c / 32 (f16). For Q4_0 / Q4_K / Q6_K matrices (esize 0), row r of
-// the tensor is plane row r * step of the QFMat {qtype, base, hb, scale, s1}.
+// the tensor is plane row row0 + r * step of the QFMat {qtype, base, hb, scale, s1, row0}.
 struct TensorPlace {
     int64_t rows, cols;
     void *base;
@@ -63,6 +63,7 @@ struct TensorPlace {
     int32_t qtype = 0;
     void *s1 = nullptr, *hb = nullptr;
     int64_t step = 1;
+    int64_t row0 = 0;  // 4-bit types: plane row of the tensor's row 0
 };
 
 }  // namespace aesir

@@ -7,20 +7,21 @@
 // 8 nibble bytes per record, byte j holding weights j and 8 + j, so that masking a record word
 // with 0x000F000F or 0x00F000F0 and OR-ing 0x64006400 yields the f16 pair (1024 + q_a, 1024 +
 // q_b) or (1024 + 16 q_a, 1024 + 16 q_b) for weights (a, a + 2); plus small planes of per-block
-// scales and, for Q6_K, one word of high bits per record. A decode GEMV lane multiplies one
-// 32-weight chunk (two records, one 16-byte load) per row and slab, with x held in registers in
-// the matching pair order.
+// scales and, for Q6_K, one word of high bits per record. The planes are tiled in 16-row x
+// 128-weight tiles, so that lane l of a wave reading 16 bytes at 16 l gets two records of row
+// l % 16: the A operand of v_mfma_f32_16x16x32_f16 for four matrix-core steps once dequantized.
+// The decode GEMV dequantizes in registers and multiplies on the matrix cores.
 //
-// Arithmetic per type:
-//   Q4_0  w = f16(f16(q - 8) * d), the reference's dequantize_q4_0 (compute.mojo:266-280): the
-//         pair q - 8 is exact in f16, the packed f16 multiply by d rounds once; then f32
-//         v_dot2_f32_f16 accumulation as in the F16 path.
-//   Q4_K  w = (d * sc) * q - dmin * m, GGML's value in f32. Per 32-weight sub-block: S = sum x q
-//         with q exact in f16, X = sum x; contribution (d sc) S - (dmin m) X in f32.
-//   Q6_K  w = (d * sc) * (q - 32): per record S = sum x (q - 32) with the 6-bit value exact in
-//         f16, contribution (d sc) S in f32.
-// The K-quant dot products therefore use the f32 weights GGML defines, not f16-rounded ones.
-#include <atomic>
+// Weights (the f16 values that the GEMV, the dequantization for the prefill GEMMs and the
+// read-back all produce, bit for bit):
+//   Q4_0  w = f16(f16(q - 8) * d), the reference's dequantize_q4_0 (compute.mojo:266-280): q - 8
+//         is exact in f16, the product rounds once.
+//   Q4_K  w = f16(a q - b), one fused multiply-add in f16, with a = f16(d * sc) and
+//         b = f16(dmin * m) from GGML's block fields: the f16 arithmetic of the reference's
+//         dequantize_q4_k_m (compute.mojo:245-262, q * scale + min in f16).
+//   Q6_K  w = f16(a (q - 32)) with a = f16(d * sc), f16 products as in the reference's
+//         dequantize_q6_k_block (compute.mojo:508-527).
+// Products with x accumulate in f32 (the matrix cores, as in the F16 path's MFMA GEMMs).
 #include <type_traits>
 
 #include "device.hpp"
@@ -30,16 +31,8 @@
 namespace aesir {
 
 constexpr int kRec = 16;                  // weights per record
+constexpr int kSeg = 128;                 // weights per tile row (8 records)
 constexpr unsigned kMagic = 0x64006400u;  // f16 1024 in both halves
-// Decode GEMV shape: rows per group (the epilogue's unit), groups per workgroup (the gate/up
-// projection runs two), weight requests in flight per lane (in (group, slab) steps), and the
-// most slabs instantiated for 1, 2 and 4 sub-groups (K <= 32768, 8192, 6144).
-constexpr int kQfGroupRows = 8;
-constexpr int kQfGroups = 1;
-constexpr int kQfGroupsFfn = 2;
-constexpr int kQfDepth = 2;
-constexpr int kQfMaxSlabs[3] = {4, 2, 3};
-
 
 bool qf_type(int32_t t) { return t == AESIR_GGML_Q4_0 || t == AESIR_GGML_Q4_K || t == AESIR_GGML_Q6_K; }
 
@@ -54,6 +47,18 @@ __host__ __device__ __forceinline__ int qf_hb_pos(int i) {
     const int a = i & ~2, f = (a & 1) | (((a >> 2) & 1) << 1) | (((a >> 3) & 1) << 2);
     return qf_hb_off(f) + 16 * ((i >> 1) & 1);
 }
+
+// ------------------------------------------------------------------ weight arithmetic
+
+// Scales of the f16 weight rules from the block fields (correctly rounded f16 products of exact
+// operands): Q4_K (f16(d sc), f16(dmin m)), Q6_K f16(d sc).
+__device__ __forceinline__ h16x2 q4k_scales(h16x2 d_dmin, h16x2 sc_m) { return d_dmin * sc_m; }
+__device__ __forceinline__ h16 q6k_scale(h16 d, int sc) { return hmul(d, (h16)(float)sc); }
+// Weight pairs from exact f16 pairs of quantized values: Q4_0 q - 8 (times d), Q4_K q (a q - b,
+// one fused rounding), Q6_K q - 32 (times a).
+__device__ __forceinline__ h16x2 q4_0_w2(h16x2 q8, h16x2 dd) { return q8 * dd; }
+__device__ __forceinline__ h16x2 q4k_w2(h16x2 q, h16x2 aa, h16x2 nbb) { return __builtin_elementwise_fma(q, aa, nbb); }
+__device__ __forceinline__ h16x2 q6k_w2(h16x2 q32, h16x2 aa) { return q32 * aa; }
 
 // ------------------------------------------------------------------ one record
 
@@ -78,20 +83,21 @@ struct QRec<AESIR_GGML_Q6_K> {
     h16 d;
 };
 
-// Record `rec` of plane row `prow` (the row index in plane rows, i.e. already scaled by step).
+// Record `rec` of plane row `prow`.
 template <int T>
 __device__ __forceinline__ QRec<T> qf_load(const QFMat &w, int64_t prow, int64_t rec, int64_t K) {
     QRec<T> q;
-    q.nib = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>((const uint8_t *)w.nib + prow * (K / 2)) + rec);
+    q.nib = *reinterpret_cast<const u32x2 *>((const uint8_t *)w.nib + qf_nib_off(prow, rec, K));
+    const uint8_t *s0 = (const uint8_t *)w.s0 + qf_s0_off(prow, rec, K);
     if constexpr (T == AESIR_GGML_Q4_0) {
-        q.d = reinterpret_cast<const h16 *>(w.s0)[prow * (K / 32) + rec / 2];
+        q.d = *reinterpret_cast<const h16 *>(s0);
     } else if constexpr (T == AESIR_GGML_Q4_K) {
-        q.scm = reinterpret_cast<const uint16_t *>(w.s0)[prow * (K / 32) + rec / 2];
-        q.dd = reinterpret_cast<const uint32_t *>(w.s1)[prow * (K / 256) + rec / 16];
+        q.scm = *reinterpret_cast<const uint16_t *>(s0);
+        q.dd = *reinterpret_cast<const uint32_t *>((const uint8_t *)w.s1 + qf_s1_off(prow, rec, K, 4));
     } else {
-        q.hb = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(w.hb) + prow * (K / 16) + rec);
-        q.sc = reinterpret_cast<const int8_t *>(w.s0)[prow * (K / 16) + rec];
-        q.d = reinterpret_cast<const h16 *>(w.s1)[prow * (K / 256) + rec / 16];
+        q.hb = *reinterpret_cast<const uint32_t *>((const uint8_t *)w.hb + qf_hbw_off(prow, rec, K));
+        q.sc = *reinterpret_cast<const int8_t *>(s0 + (rec & 1));
+        q.d = *reinterpret_cast<const h16 *>((const uint8_t *)w.s1 + qf_s1_off(prow, rec, K, 2));
     }
     return q;
 }
@@ -105,18 +111,6 @@ __device__ __forceinline__ unsigned qf_pair(u32x2 nib, int f) {
 __device__ __forceinline__ unsigned qf_hb_pair(unsigned hb, int f) {
     const int s = 4 - qf_hb_off(f);
     return (s >= 0 ? hb << s : hb >> -s) & 0x00300030u;
-}
-
-// x of one record in pair order: xp[f] = (x[a_f], x[a_f + 2]) from the natural chunks x[0..7],
-// x[8..15].
-__device__ __forceinline__ void qf_perm_x(const u32x4 (&x)[2], unsigned (&xp)[8]) {
-#pragma unroll
-    for (int c = 0; c < 2; c++) {
-        xp[4 * c + 0] = __builtin_amdgcn_perm(x[c].y, x[c].x, 0x05040100u);
-        xp[4 * c + 1] = __builtin_amdgcn_perm(x[c].y, x[c].x, 0x07060302u);
-        xp[4 * c + 2] = __builtin_amdgcn_perm(x[c].w, x[c].z, 0x05040100u);
-        xp[4 * c + 3] = __builtin_amdgcn_perm(x[c].w, x[c].z, 0x07060302u);
-    }
 }
 
 // Exact f16 pairs of the record's quantized values, pair order: Q4_0 q - 8, Q4_K q, Q6_K q - 32.
@@ -134,33 +128,8 @@ __device__ __forceinline__ h16x2 qf_qpair(const QRec<T> &q, int f) {
     }
 }
 
-// The record's 16 weights as f16 in natural order (o[0]: weights 0..7, o[1]: 8..15):
-// Q4_0 f16((q - 8) d); Q4_K f16((d sc) q - dmin m); Q6_K f16((d sc) (q - 32)) with the products
-// in f32 (GGML's f32 value, then one rounding to f16).
-template <int T>
-__device__ __forceinline__ void qf_deq16(const QRec<T> &q, u32x4 (&o)[2]) {
-    unsigned wp[8];
-#pragma unroll
-    for (int f = 0; f < 8; f++) {
-        const h16x2 v = qf_qpair(q, f);
-        if constexpr (T == AESIR_GGML_Q4_0) {
-            const h16x2 dd = {q.d, q.d};
-            wp[f] = h2_bits(v * dd);
-        } else if constexpr (T == AESIR_GGML_Q4_K) {
-            const float d = (float)bits_to_h((uint16_t)(q.dd & 0xffffu)), dm = (float)bits_to_h((uint16_t)(q.dd >> 16));
-            const float a = d * (float)(q.scm & 0xffu), b = dm * (float)(q.scm >> 8);
-            h16x2 r;
-            r.x = (h16)(a * (float)v.x - b);
-            r.y = (h16)(a * (float)v.y - b);
-            wp[f] = h2_bits(r);
-        } else {
-            const float a = (float)q.d * (float)q.sc;
-            h16x2 r;
-            r.x = (h16)(a * (float)v.x);
-            r.y = (h16)(a * (float)v.y);
-            wp[f] = h2_bits(r);
-        }
-    }
+// Natural-order weights from pair-order pairs: o[0] holds weights 0..7, o[1] 8..15.
+__device__ __forceinline__ void qf_unpair(const unsigned (&wp)[8], u32x4 (&o)[2]) {
 #pragma unroll
     for (int c = 0; c < 2; c++) {
         o[c].x = __builtin_amdgcn_perm(wp[4 * c + 1], wp[4 * c + 0], 0x05040100u);
@@ -170,9 +139,35 @@ __device__ __forceinline__ void qf_deq16(const QRec<T> &q, u32x4 (&o)[2]) {
     }
 }
 
+// The record's 16 f16 weights in natural order.
+template <int T>
+__device__ __forceinline__ void qf_deq16(const QRec<T> &q, u32x4 (&o)[2]) {
+    unsigned wp[8];
+    h16x2 aa, nbb;
+    if constexpr (T == AESIR_GGML_Q4_0) {
+        aa = h16x2{q.d, q.d};
+    } else if constexpr (T == AESIR_GGML_Q4_K) {
+        const h16x2 sm = {(h16)(float)(q.scm & 0xffu), (h16)(float)(q.scm >> 8)};
+        const h16x2 ab = q4k_scales(as_h2(q.dd), sm);
+        aa = h16x2{ab.x, ab.x};
+        nbb = h16x2{-ab.y, -ab.y};
+    } else {
+        const h16 a = q6k_scale(q.d, q.sc);
+        aa = h16x2{a, a};
+    }
+#pragma unroll
+    for (int f = 0; f < 8; f++) {
+        const h16x2 v = qf_qpair(q, f);
+        if constexpr (T == AESIR_GGML_Q4_0) wp[f] = h2_bits(q4_0_w2(v, aa));
+        else if constexpr (T == AESIR_GGML_Q4_K) wp[f] = h2_bits(q4k_w2(v, aa, nbb));
+        else wp[f] = h2_bits(q6k_w2(v, aa));
+    }
+    qf_unpair(wp, o);
+}
+
 // ------------------------------------------------------------------ repacking
 
-// GGUF source of weight e of a row: its 4- or 6-bit value and block metadata.
+// GGUF source of weight e of a row: its 4- or 6-bit value.
 template <int T>
 __device__ __forceinline__ int gguf_q(const uint8_t *row, int64_t e) {
     if constexpr (T == AESIR_GGML_Q4_0) {
@@ -204,8 +199,8 @@ __device__ __forceinline__ void q4k_scale_min(const uint8_t *sc, int j, int &s, 
     }
 }
 
-__device__ __forceinline__ uint8_t *plane_row(const void *p, int32_t type, int plane, int64_t prow, int64_t K) {
-    return (uint8_t *)p + prow * qf_plane_row_bytes(type, plane, K);
+__device__ __forceinline__ int64_t gguf_row_bytes(int T, int64_t K) {
+    return T == AESIR_GGML_Q4_0 ? K / 32 * 18 : T == AESIR_GGML_Q4_K ? K / 256 * 144 : K / 256 * 210;
 }
 
 // One thread per record: GGUF blocks -> nibble record (+ hb word) and, from the record that
@@ -217,9 +212,8 @@ __global__ __launch_bounds__(256) void qf_repack_kernel(const uint8_t *__restric
     const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (gid >= rows * recs) return;
     const int64_t r = gid / recs, rec = gid % recs, k = rec * kRec;
-    const int64_t bpr = T == AESIR_GGML_Q4_0 ? K / 32 * 18 : T == AESIR_GGML_Q4_K ? K / 256 * 144 : K / 256 * 210;
-    const uint8_t *src = blocks + r * bpr;
-    const int64_t prow = r * step;
+    const uint8_t *src = blocks + r * gguf_row_bytes(T, K);
+    const int64_t prow = dst.row0 + r * step;
     int q[kRec];
 #pragma unroll
     for (int i = 0; i < kRec; i++) q[i] = gguf_q<T>(src, k + i);
@@ -229,29 +223,30 @@ __global__ __launch_bounds__(256) void qf_repack_kernel(const uint8_t *__restric
     if constexpr (T == AESIR_GGML_Q6_K) {
 #pragma unroll
         for (int i = 0; i < kRec; i++) hb |= (unsigned)(q[i] >> 4) << qf_hb_pos(i);
-        reinterpret_cast<uint32_t *>(plane_row(dst.hb, T, 1, prow, K))[rec] = hb;
+        *reinterpret_cast<uint32_t *>((uint8_t *)dst.hb + qf_hbw_off(prow, rec, K)) = hb;
     }
-    reinterpret_cast<u32x2 *>(plane_row(dst.nib, T, 0, prow, K))[rec] = u32x2{nib[0], nib[1]};
+    *reinterpret_cast<u32x2 *>((uint8_t *)dst.nib + qf_nib_off(prow, rec, K)) = u32x2{nib[0], nib[1]};
+    uint8_t *s0 = (uint8_t *)dst.s0 + qf_s0_off(prow, rec, K);
     if constexpr (T == AESIR_GGML_Q4_0) {
         if (rec % 2 == 0) {
             const uint8_t *blk = src + (k / 32) * 18;
-            reinterpret_cast<uint16_t *>(plane_row(dst.s0, T, 2, prow, K))[k / 32] = (uint16_t)(blk[0] | (blk[1] << 8));
+            *reinterpret_cast<uint16_t *>(s0) = (uint16_t)(blk[0] | (blk[1] << 8));
         }
     } else if constexpr (T == AESIR_GGML_Q4_K) {
         const uint8_t *blk = src + (k / 256) * 144;
         if (rec % 2 == 0) {
             int s, m;
             q4k_scale_min(blk + 4, (int)((k % 256) / 32), s, m);
-            reinterpret_cast<uint16_t *>(plane_row(dst.s0, T, 2, prow, K))[k / 32] = (uint16_t)(s | (m << 8));
+            *reinterpret_cast<uint16_t *>(s0) = (uint16_t)(s | (m << 8));
         }
         if (rec % 16 == 0)
-            reinterpret_cast<uint32_t *>(plane_row(dst.s1, T, 3, prow, K))[k / 256] =
+            *reinterpret_cast<uint32_t *>((uint8_t *)dst.s1 + qf_s1_off(prow, rec, K, 4)) =
                 (uint32_t)blk[0] | ((uint32_t)blk[1] << 8) | ((uint32_t)blk[2] << 16) | ((uint32_t)blk[3] << 24);
     } else {
         const uint8_t *blk = src + (k / 256) * 210;
-        reinterpret_cast<int8_t *>(plane_row(dst.s0, T, 2, prow, K))[k / 16] = (int8_t)blk[192 + (k % 256) / 16];
+        s0[rec & 1] = blk[192 + (k % 256) / 16];
         if (rec % 16 == 0)
-            reinterpret_cast<uint16_t *>(plane_row(dst.s1, T, 3, prow, K))[k / 256] =
+            *reinterpret_cast<uint16_t *>((uint8_t *)dst.s1 + qf_s1_off(prow, rec, K, 2)) =
                 (uint16_t)(blk[208] | (blk[209] << 8));
     }
 }
@@ -267,45 +262,92 @@ __global__ __launch_bounds__(256) void qf_dequant_kernel(QFMat w, int64_t rows, 
     const int64_t r = gid / recs, rec = gid % recs;
     const int64_t src_row = row_ids ? row_ids[r] : r;
     u32x4 o[2];
-    qf_deq16<T>(qf_load<T>(w, src_row * step, rec, K), o);
+    qf_deq16<T>(qf_load<T>(w, w.row0 + src_row * step, rec, K), o);
     h16 *dst = out + r * out_stride + rec * kRec;
     st16(dst, o[0]);
     st16(dst + 8, o[1]);
 }
 
+// One thread per record: GGUF blocks -> f16 weights straight from the blocks, with the same
+// weight rules (and instructions) as qf_deq16.
+template <int T>
+__global__ __launch_bounds__(256) void gguf_dequant_kernel(const uint8_t *__restrict__ blocks, int64_t rows, int64_t K,
+                                                           h16 *__restrict__ out) {
+    const int64_t recs = K / kRec;
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (gid >= rows * recs) return;
+    const int64_t r = gid / recs, rec = gid % recs, k = rec * kRec;
+    const uint8_t *src = blocks + r * gguf_row_bytes(T, K);
+    h16x2 aa, nbb;
+    if constexpr (T == AESIR_GGML_Q4_0) {
+        const uint8_t *blk = src + (k / 32) * 18;
+        const h16 d = bits_to_h((uint16_t)(blk[0] | (blk[1] << 8)));
+        aa = h16x2{d, d};
+    } else if constexpr (T == AESIR_GGML_Q4_K) {
+        const uint8_t *blk = src + (k / 256) * 144;
+        int s, m;
+        q4k_scale_min(blk + 4, (int)((k % 256) / 32), s, m);
+        const h16x2 dd = {bits_to_h((uint16_t)(blk[0] | (blk[1] << 8))), bits_to_h((uint16_t)(blk[2] | (blk[3] << 8)))};
+        const h16x2 ab = q4k_scales(dd, h16x2{(h16)(float)s, (h16)(float)m});
+        aa = h16x2{ab.x, ab.x};
+        nbb = h16x2{-ab.y, -ab.y};
+    } else {
+        const uint8_t *blk = src + (k / 256) * 210;
+        const h16 a = q6k_scale(bits_to_h((uint16_t)(blk[208] | (blk[209] << 8))), (int8_t)blk[192 + (k % 256) / 16]);
+        aa = h16x2{a, a};
+    }
+    unsigned wp[8];  // natural pairs (2 i, 2 i + 1)
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int q0 = gguf_q<T>(src, k + 2 * i), q1 = gguf_q<T>(src, k + 2 * i + 1);
+        if constexpr (T == AESIR_GGML_Q4_0)
+            wp[i] = h2_bits(q4_0_w2(h16x2{(h16)(float)(q0 - 8), (h16)(float)(q1 - 8)}, aa));
+        else if constexpr (T == AESIR_GGML_Q4_K)
+            wp[i] = h2_bits(q4k_w2(h16x2{(h16)(float)q0, (h16)(float)q1}, aa, nbb));
+        else
+            wp[i] = h2_bits(q6k_w2(h16x2{(h16)(float)(q0 - 32), (h16)(float)(q1 - 32)}, aa));
+    }
+    h16 *dst = out + r * K + k;
+    st16(dst, u32x4{wp[0], wp[1], wp[2], wp[3]});
+    st16(dst + 8, u32x4{wp[4], wp[5], wp[6], wp[7]});
+}
+
 // One thread per record: uniform random values; scales chosen so that the weights have a
-// standard deviation near `std` and a mean near 0.
+// standard deviation near `std` and a mean near 0. The values depend on (row, record) only, not
+// on where the planes put them.
 template <int T>
 __global__ __launch_bounds__(256) void qf_fill_kernel(QFMat w, int64_t rows, int64_t K, int64_t step, uint64_t base,
                                                       float std) {
     const int64_t recs = K / kRec;
     const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (gid >= rows * recs) return;
-    const int64_t r = gid / recs, rec = gid % recs, prow = r * step;
+    const int64_t r = gid / recs, rec = gid % recs, prow = w.row0 + r * step;
     const uint64_t a = mix64(base + (uint64_t)(2 * gid + 1) * kGolden);
     const uint64_t b = mix64(base + (uint64_t)(2 * gid + 2) * kGolden);
-    reinterpret_cast<u32x2 *>(plane_row(w.nib, T, 0, prow, K))[rec] = u32x2{(unsigned)a, (unsigned)(a >> 32)};
+    *reinterpret_cast<u32x2 *>((uint8_t *)w.nib + qf_nib_off(prow, rec, K)) = u32x2{(unsigned)a, (unsigned)(a >> 32)};
+    uint8_t *s0 = (uint8_t *)w.s0 + qf_s0_off(prow, rec, K);
     const float u = (float)(b >> 40) * (1.0f / 16777216.0f);  // [0, 1)
     if constexpr (T == AESIR_GGML_Q4_0) {
         // q - 8 uniform on [-8, 7]: standard deviation 4.61
-        if (rec % 2 == 0) reinterpret_cast<h16 *>(plane_row(w.s0, T, 2, prow, K))[rec / 2] = (h16)((0.5f + u) * std / 4.61f);
+        if (rec % 2 == 0) *reinterpret_cast<h16 *>(s0) = (h16)((0.5f + u) * std / 4.61f);
     } else if constexpr (T == AESIR_GGML_Q4_K) {
         // sc in [4, 8], m = round(7.5 sc), dmin = d: w = d sc (q - 7.5) nearly, q uniform on [0, 15]
         if (rec % 2 == 0) {
             const int s = 4 + (int)((b >> 8) % 5), m = (int)(7.5f * (float)s + 0.5f);
-            reinterpret_cast<uint16_t *>(plane_row(w.s0, T, 2, prow, K))[rec / 2] = (uint16_t)(s | (m << 8));
+            *reinterpret_cast<uint16_t *>(s0) = (uint16_t)(s | (m << 8));
         }
         if (rec % 16 == 0) {
             const h16 d = (h16)((0.5f + u) * std / (6.0f * 4.61f));
             const uint32_t dv = h_to_bits(d);
-            reinterpret_cast<uint32_t *>(plane_row(w.s1, T, 3, prow, K))[rec / 16] = dv | (dv << 16);
+            *reinterpret_cast<uint32_t *>((uint8_t *)w.s1 + qf_s1_off(prow, rec, K, 4)) = dv | (dv << 16);
         }
     } else {
         // q - 32 uniform on [-32, 31]: standard deviation 18.5; sc in [16, 47]
-        reinterpret_cast<uint32_t *>(plane_row(w.hb, T, 1, prow, K))[rec] = (uint32_t)(b >> 8);
-        reinterpret_cast<int8_t *>(plane_row(w.s0, T, 2, prow, K))[rec] = (int8_t)(16 + (int)((b >> 4) % 32));
+        *reinterpret_cast<uint32_t *>((uint8_t *)w.hb + qf_hbw_off(prow, rec, K)) = (uint32_t)(b >> 8);
+        s0[rec & 1] = (uint8_t)(16 + (int)((b >> 4) % 32));
         if (rec % 16 == 0)
-            reinterpret_cast<h16 *>(plane_row(w.s1, T, 3, prow, K))[rec / 16] = (h16)((0.5f + u) * std / (32.0f * 18.5f));
+            *reinterpret_cast<h16 *>((uint8_t *)w.s1 + qf_s1_off(prow, rec, K, 2)) =
+                (h16)((0.5f + u) * std / (32.0f * 18.5f));
     }
 }
 
@@ -320,9 +362,18 @@ static int32_t qf_check(int32_t type, int64_t K, const char *name) {
     return AESIR_OK;
 }
 
+// The tiled planes need whole 128-weight segments.
+static int32_t qf_check_planes(int32_t type, int64_t K, const char *name) {
+    AESIR_TRY(qf_check(type, K, name));
+    if (K % kSeg != 0)
+        return fail(AESIR_ERR_UNSUPPORTED, "%s: repacked planes need a row length that is a multiple of 128 (got %lld)",
+                    name, (long long)K);
+    return AESIR_OK;
+}
+
 int32_t launch_qf_repack(hipStream_t s, int32_t type, const void *blocks, int64_t rows, int64_t K, const QFMat &dst,
                          int64_t step) {
-    AESIR_TRY(qf_check(type, K, "repack"));
+    AESIR_TRY(qf_check_planes(type, K, "repack"));
     if (rows <= 0) return AESIR_OK;
     const unsigned g = rec_grid(rows, K);
     if (type == AESIR_GGML_Q4_0)
@@ -337,7 +388,7 @@ int32_t launch_qf_repack(hipStream_t s, int32_t type, const void *blocks, int64_
 
 int32_t launch_qf_dequant(hipStream_t s, const QFMat &w, int64_t rows, int64_t K, int64_t step,
                           const int64_t *row_ids, void *out, int64_t out_stride) {
-    AESIR_TRY(qf_check(w.type, K, "dequant"));
+    AESIR_TRY(qf_check_planes(w.type, K, "dequant"));
     if (rows <= 0) return AESIR_OK;
     const unsigned g = rec_grid(rows, K);
     if (w.type == AESIR_GGML_Q4_0)
@@ -350,9 +401,23 @@ int32_t launch_qf_dequant(hipStream_t s, const QFMat &w, int64_t rows, int64_t K
     return AESIR_OK;
 }
 
+int32_t launch_gguf_dequant(hipStream_t s, int32_t type, const void *blocks, int64_t rows, int64_t K, void *out) {
+    AESIR_TRY(qf_check(type, K, "gguf_dequant"));
+    if (rows <= 0) return AESIR_OK;
+    const unsigned g = rec_grid(rows, K);
+    if (type == AESIR_GGML_Q4_0)
+        hipLaunchKernelGGL(gguf_dequant_kernel<AESIR_GGML_Q4_0>, dim3(g), dim3(256), 0, s, (const uint8_t *)blocks, rows, K, (h16 *)out);
+    else if (type == AESIR_GGML_Q4_K)
+        hipLaunchKernelGGL(gguf_dequant_kernel<AESIR_GGML_Q4_K>, dim3(g), dim3(256), 0, s, (const uint8_t *)blocks, rows, K, (h16 *)out);
+    else
+        hipLaunchKernelGGL(gguf_dequant_kernel<AESIR_GGML_Q6_K>, dim3(g), dim3(256), 0, s, (const uint8_t *)blocks, rows, K, (h16 *)out);
+    AESIR_LAUNCH_CHECK("gguf_dequant_kernel");
+    return AESIR_OK;
+}
+
 int32_t launch_qf_fill_random(hipStream_t s, const QFMat &w, int64_t rows, int64_t K, int64_t step, uint64_t seed,
                               uint64_t stream, float std) {
-    AESIR_TRY(qf_check(w.type, K, "fill"));
+    AESIR_TRY(qf_check_planes(w.type, K, "fill"));
     if (rows <= 0) return AESIR_OK;
     const uint64_t base = mix64(seed ^ mix64(stream + kGolden));
     const unsigned g = rec_grid(rows, K);
@@ -366,12 +431,22 @@ int32_t launch_qf_fill_random(hipStream_t s, const QFMat &w, int64_t rows, int64
     return AESIR_OK;
 }
 
-// ------------------------------------------------------------------ decode GEMV
+// ------------------------------------------------------------------ decode GEMV (matrix cores)
 
-// A lane of the decode GEMV owns one 32-weight chunk of a row per slab: two records, i.e. one
-// 16-byte nibble load (c = chunk index, k = 32 c). Q4_0 chunks are GGML blocks and Q4_K chunks
-// are sub-blocks, so each needs one scale entry per row.
-constexpr int kChunk = 32;
+// Work of a workgroup: 16-row blocks blockIdx.x, + gridDim.x, ... (one block per workgroup when
+// the blocks are few, 256 persistent workgroups looping over them when there are many); wave w
+// multiplies a block's tiles of segments w, w + NW, ..., in rounds of qf_round() tiles whose loads
+// are issued together, the next round's (of this block or the next) while the current one
+// computes. Each lane dequantizes its 32 weights of a tile (two records of row lane % 16) into
+// four A operands, and x, staged once per workgroup in LDS in the matching pair order, is the B
+// operand, the same in all 16 columns, so every column of the 16 x 16 accumulator holds the row
+// sums. Per tile and lane: one 16-byte nibble load, 4 matrix-core steps, and the dequantization
+// (Q4_0 / Q4_K 52, Q6_K 76 VALU instructions). Q6_K tiles hold twice the registers (high-bit
+// words, wider dequantization), so their rounds are half as long.
+template <int T>
+constexpr int qf_round() {
+    return T == AESIR_GGML_Q6_K ? 2 : 4;
+}
 
 // Register-held constants: the and-or and packed-f16 forms below take a mask or bias from a
 // register (one VOP3 instruction holds at most one literal), which the compiler does not arrange
@@ -395,153 +470,134 @@ struct QfRegs {
     }
 };
 
-// One row's chunk as loaded.
+// One lane's share of a tile as loaded.
 template <int T>
-struct QChunk;
+struct QTile;
 template <>
-struct QChunk<AESIR_GGML_Q4_0> {
+struct QTile<AESIR_GGML_Q4_0> {
     u32x4 nib;
-    unsigned d;  // f16 scale in the low half
+    unsigned s0;  // f16 d in the low half
 };
 template <>
-struct QChunk<AESIR_GGML_Q4_K> {
+struct QTile<AESIR_GGML_Q4_K> {
     u32x4 nib;
-    unsigned scm;  // scale | min << 8
-    unsigned dd;   // f16 d | f16 dmin << 16
+    unsigned s0;  // scale | min << 8
+    unsigned s1;  // f16 d | f16 dmin << 16
 };
 template <>
-struct QChunk<AESIR_GGML_Q6_K> {
+struct QTile<AESIR_GGML_Q6_K> {
     u32x4 nib;
-    u32x2 hb;      // high-bit words of the two records
-    unsigned sc2;  // int8 scales of the two records
-    unsigned d;    // f16 super-block scale in the low half
+    u32x2 hb;     // high-bit words of the two records
+    unsigned s0;  // int8 scales of the two records
+    unsigned s1;  // f16 super-block d in the low half
 };
 
-// Buffer resources of a matrix's planes (range-checked loads with the row offset in an SGPR).
+// Buffer resources of a matrix's planes (range-checked loads, tile offsets in SGPRs).
 struct QfRsrc {
     __amdgpu_buffer_rsrc_t nib, hb, s0, s1;
-    int nb, hbb, s0b, s1b;  // bytes per row of each plane
 };
 
-__device__ __forceinline__ QfRsrc qf_rsrc(const QFMat &w, int32_t type, int64_t N, int64_t K) {
+__device__ __forceinline__ QfRsrc qf_rsrc(const QFMat &w, int32_t type, int64_t prows, int64_t K) {
     QfRsrc r;
-    r.nb = (int)qf_plane_row_bytes(type, 0, K);
-    r.hbb = type == AESIR_GGML_Q6_K ? (int)qf_plane_row_bytes(type, 1, K) : 0;
-    r.s0b = (int)qf_plane_row_bytes(type, 2, K);
-    r.s1b = type == AESIR_GGML_Q4_0 ? 0 : (int)qf_plane_row_bytes(type, 3, K);
-    r.nib = __builtin_amdgcn_make_buffer_rsrc((void *)w.nib, 0, (int)(N * r.nb), 0x00020000);
-    r.hb = __builtin_amdgcn_make_buffer_rsrc((void *)w.hb, 0, (int)(N * r.hbb), 0x00020000);
-    r.s0 = __builtin_amdgcn_make_buffer_rsrc((void *)w.s0, 0, (int)(N * r.s0b), 0x00020000);
-    r.s1 = __builtin_amdgcn_make_buffer_rsrc((void *)w.s1, 0, (int)(N * r.s1b), 0x00020000);
+    r.nib = __builtin_amdgcn_make_buffer_rsrc((void *)w.nib, 0, (int)(prows * qf_plane_row_bytes(type, 0, K)), 0x00020000);
+    r.hb = __builtin_amdgcn_make_buffer_rsrc((void *)w.hb, 0, (int)(prows * qf_plane_row_bytes(type, 1, K)), 0x00020000);
+    r.s0 = __builtin_amdgcn_make_buffer_rsrc((void *)w.s0, 0, (int)(prows * qf_plane_row_bytes(type, 2, K)), 0x00020000);
+    r.s1 = __builtin_amdgcn_make_buffer_rsrc((void *)w.s1, 0, (int)(prows * qf_plane_row_bytes(type, 3, K)), 0x00020000);
     return r;
 }
 
-// Chunk c of plane row n (n wave-uniform: the row offsets go in SGPRs).
+// Tile `tile` (wave-uniform); s1v / s1s: the lane's and the tile's byte offsets in the s1 plane.
 template <int T>
-__device__ __forceinline__ QChunk<T> qf_chunk_load(const QfRsrc &r, int n, int c) {
-    QChunk<T> q;
-    q.nib = __builtin_amdgcn_raw_buffer_load_b128(r.nib, c * 16, n * r.nb, 2);
-    if constexpr (T == AESIR_GGML_Q4_0) {
-        q.d = __builtin_amdgcn_raw_buffer_load_b16(r.s0, c * 2, n * r.s0b, 0);
-    } else if constexpr (T == AESIR_GGML_Q4_K) {
-        q.scm = __builtin_amdgcn_raw_buffer_load_b16(r.s0, c * 2, n * r.s0b, 0);
-        q.dd = __builtin_amdgcn_raw_buffer_load_b32(r.s1, (c >> 3) * 4, n * r.s1b, 0);
-    } else {
-        q.hb = __builtin_amdgcn_raw_buffer_load_b64(r.hb, c * 8, n * r.hbb, 2);
-        q.sc2 = __builtin_amdgcn_raw_buffer_load_b16(r.s0, c * 2, n * r.s0b, 0);
-        q.d = __builtin_amdgcn_raw_buffer_load_b16(r.s1, (c >> 3) * 2, n * r.s1b, 0);
+__device__ __forceinline__ QTile<T> qf_tile_load(const QfRsrc &r, int tile, int lane, int s1v, int s1s) {
+    QTile<T> q;
+    q.nib = __builtin_amdgcn_raw_buffer_load_b128(r.nib, lane * 16, tile * 1024, 2);
+    q.s0 = __builtin_amdgcn_raw_buffer_load_b16(r.s0, lane * 2, tile * 128, 0);
+    if constexpr (T == AESIR_GGML_Q4_K) q.s1 = __builtin_amdgcn_raw_buffer_load_b32(r.s1, s1v, s1s, 0);
+    if constexpr (T == AESIR_GGML_Q6_K) {
+        q.hb = __builtin_amdgcn_raw_buffer_load_b64(r.hb, lane * 8, tile * 512, 2);
+        q.s1 = __builtin_amdgcn_raw_buffer_load_b16(r.s1, s1v, s1s, 0);
     }
     return q;
 }
 
-// acc + this chunk's share of the row's dot product. xp: the chunk's x in pair order (record j
-// pair f at xp[8 j + f]); X: sum of the chunk's 32 x values (Q4_K).
-//
-// Nibble pairs come out of a word v of record bytes as (v & 0x000F000F) | magic = 1024 + q for
-// the low nibbles of bytes 0 and 2 and (v & 0x00F000F0) | magic = 1024 + 16 q for the high ones;
-// v >> 8 gives bytes 1 and 3. Word 0 of a record yields pairs f = 0, 1 (low) and 4, 5 (high),
-// word 1 pairs 2, 3 and 6, 7. All values are exact in f16: Q4_0 turns them into q - 8 (adding
-// -1032, or times 1/16 plus -72), Q4_K/Q6_K keep separate sums for the 16-scaled pairs and scale
-// by 1/16 in f32.
+// The four A operands of a lane's tile share: operand j from nibble word j (record j / 2, bytes
+// 4 (j % 2) .. + 3), as the pairs (v & lo), (v >> 8 & lo), (v & hi), (v >> 8 & hi), i.e. the
+// weights {0, 2, 1, 3, 8, 10, 9, 11} + 4 (j % 2) of the record. Values exact in f16 until the
+// weight rule's single rounding: Q4_0 turns 1024 + q into q - 8 by adding -1032 and 1024 + 16 q
+// by (.) / 16 - 72; Q4_K into q by -1024 and (.) / 16 - 64; Q6_K into q - 32 by -1056 and
+// (.) / 16 - 96, its high bits OR-ed in from the record's hb word (shifted by 4, 2, -4, -6 for
+// the four pair positions of the record).
 template <int T>
-__device__ __forceinline__ float qf_chunk_dot(const QChunk<T> &q, const unsigned (&xp)[16], float X, float acc,
-                                              const QfRegs &k) {
+__device__ __forceinline__ void qf_tile_a(const QTile<T> &q, const QfRegs &k, u32x4 (&a)[4]) {
     const unsigned nw[4] = {q.nib.x, q.nib.y, q.nib.z, q.nib.w};
+    const h16x2 s16 = {(h16)0.0625f, (h16)0.0625f};
     if constexpr (T == AESIR_GGML_Q4_0) {
-        const h16 d = bits_to_h((uint16_t)(q.d & 0xffffu));
+        const h16 d = bits_to_h((uint16_t)(q.s0 & 0xffffu));
         const h16x2 dd = {d, d};
-        const h16x2 blo = {(h16)-1032.0f, (h16)-1032.0f}, s16 = {(h16)0.0625f, (h16)0.0625f},
-                    bhi = {(h16)-72.0f, (h16)-72.0f};
+        const h16x2 blo = {(h16)-1032.0f, (h16)-1032.0f}, bhi = {(h16)-72.0f, (h16)-72.0f};
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const unsigned v = nw[j], t = v >> 8;
-            const unsigned *x = xp + 8 * (j >> 1) + 2 * (j & 1);
-            acc = __builtin_amdgcn_fdot2((as_h2((v & k.lo) | k.magic) + blo) * dd, as_h2(x[0]), acc, false);
-            acc = __builtin_amdgcn_fdot2((as_h2((t & k.lo) | k.magic) + blo) * dd, as_h2(x[1]), acc, false);
-            acc = __builtin_amdgcn_fdot2(__builtin_elementwise_fma(as_h2((v & k.hi) | k.magic), s16, bhi) * dd,
-                                         as_h2(x[4]), acc, false);
-            acc = __builtin_amdgcn_fdot2(__builtin_elementwise_fma(as_h2((t & k.hi) | k.magic), s16, bhi) * dd,
-                                         as_h2(x[5]), acc, false);
+            a[j].x = h2_bits(q4_0_w2(as_h2((v & k.lo) | k.magic) + blo, dd));
+            a[j].y = h2_bits(q4_0_w2(as_h2((t & k.lo) | k.magic) + blo, dd));
+            a[j].z = h2_bits(q4_0_w2(__builtin_elementwise_fma(as_h2((v & k.hi) | k.magic), s16, bhi), dd));
+            a[j].w = h2_bits(q4_0_w2(__builtin_elementwise_fma(as_h2((t & k.hi) | k.magic), s16, bhi), dd));
         }
-        return acc;
     } else if constexpr (T == AESIR_GGML_Q4_K) {
-        const h16x2 b = {(h16)-1024.0f, (h16)-1024.0f};
-        float slo = 0.0f, shi = 0.0f;
+        const h16x2 b1024 = {(h16)-1024.0f, (h16)-1024.0f}, bhi = {(h16)-64.0f, (h16)-64.0f};
+        // (scale, min) bytes into the low byte of each half, then exact through the 1024 exponent
+        const h16x2 sm = as_h2(__builtin_amdgcn_perm(0u, q.s0, 0x0c010c00u) | k.magic) + b1024;
+        const h16x2 ab = q4k_scales(as_h2(q.s1), sm);
+        const h16x2 aa = {ab.x, ab.x}, nbb = {-ab.y, -ab.y};
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const unsigned v = nw[j], t = v >> 8;
-            const unsigned *x = xp + 8 * (j >> 1) + 2 * (j & 1);
-            slo = __builtin_amdgcn_fdot2(as_h2((v & k.lo) | k.magic) + b, as_h2(x[0]), slo, false);
-            slo = __builtin_amdgcn_fdot2(as_h2((t & k.lo) | k.magic) + b, as_h2(x[1]), slo, false);
-            shi = __builtin_amdgcn_fdot2(as_h2((v & k.hi) | k.magic) + b, as_h2(x[4]), shi, false);
-            shi = __builtin_amdgcn_fdot2(as_h2((t & k.hi) | k.magic) + b, as_h2(x[5]), shi, false);
+            a[j].x = h2_bits(q4k_w2(as_h2((v & k.lo) | k.magic) + b1024, aa, nbb));
+            a[j].y = h2_bits(q4k_w2(as_h2((t & k.lo) | k.magic) + b1024, aa, nbb));
+            a[j].z = h2_bits(q4k_w2(__builtin_elementwise_fma(as_h2((v & k.hi) | k.magic), s16, bhi), aa, nbb));
+            a[j].w = h2_bits(q4k_w2(__builtin_elementwise_fma(as_h2((t & k.hi) | k.magic), s16, bhi), aa, nbb));
         }
-        const float S = fmaf(shi, 0.0625f, slo);
-        const float d = (float)bits_to_h((uint16_t)(q.dd & 0xffffu)), dm = (float)bits_to_h((uint16_t)(q.dd >> 16));
-        const float a = d * (float)(q.scm & 0xffu), bb = dm * (float)((q.scm >> 8) & 0xffu);
-        return acc + (a * S - bb * X);
     } else {
-        // High bits: record word h holds pair f's two 2-bit fields at o + 4 (f >> 2) and 16 above,
-        // o = {0, 2, 8, 10}[f & 3]; h shifted by 4 - o puts the low pairs' fields at bits 4 and
-        // 20 and the high pairs' at bits 8 and 24, next to their nibbles.
-        const h16x2 blo = {(h16)-1056.0f, (h16)-1056.0f}, bhi = {(h16)-1536.0f, (h16)-1536.0f};
-        const float d = (float)bits_to_h((uint16_t)(q.d & 0xffffu));
+        const h16x2 blo = {(h16)-1056.0f, (h16)-1056.0f}, bhi = {(h16)-96.0f, (h16)-96.0f};
+        const h16x2 b1152 = {(h16)-1152.0f, (h16)-1152.0f};
+        // int8 scales of the two records: byte ^ 0x80 under the 1024 exponent reads 1152 + sc
+        const h16x2 sc = as_h2(__builtin_amdgcn_perm(0u, q.s0 ^ 0x8080u, 0x0c010c00u) | k.magic) + b1152;
+        const h16 d = bits_to_h((uint16_t)(q.s1 & 0xffffu));
+        const h16x2 a01 = h16x2{d, d} * sc;  // (f16(d sc0), f16(d sc1))
         const unsigned hw[2] = {q.hb.x, q.hb.y};
 #pragma unroll
         for (int r = 0; r < 2; r++) {
+            const h16x2 aa = r == 0 ? h16x2{a01.x, a01.x} : h16x2{a01.y, a01.y};
             const unsigned h = hw[r];
-            const unsigned hs[4] = {h << 4, h << 2, h >> 4, h >> 6};
-            float slo = 0.0f, shi = 0.0f;
 #pragma unroll
-            for (int w = 0; w < 2; w++) {
-                const unsigned v = nw[2 * r + w], t = v >> 8;
-                const unsigned ha = hs[2 * w], hb = hs[2 * w + 1];
-                const unsigned *x = xp + 8 * r + 2 * w;
-                slo = __builtin_amdgcn_fdot2(as_h2((ha & k.hlo) | ((v & k.lo) | k.magic)) + blo, as_h2(x[0]), slo, false);
-                slo = __builtin_amdgcn_fdot2(as_h2((hb & k.hlo) | ((t & k.lo) | k.magic)) + blo, as_h2(x[1]), slo, false);
-                shi = __builtin_amdgcn_fdot2(as_h2((ha & k.hhi) | ((v & k.hi) | k.magic)) + bhi, as_h2(x[4]), shi, false);
-                shi = __builtin_amdgcn_fdot2(as_h2((hb & k.hhi) | ((t & k.hi) | k.magic)) + bhi, as_h2(x[5]), shi, false);
+            for (int wd = 0; wd < 2; wd++) {
+                const int j = 2 * r + wd;
+                const unsigned v = nw[j], t = v >> 8;
+                const unsigned ha = wd == 0 ? h << 4 : h >> 4, hb = wd == 0 ? h << 2 : h >> 6;
+                a[j].x = h2_bits(q6k_w2(as_h2((ha & k.hlo) | ((v & k.lo) | k.magic)) + blo, aa));
+                a[j].y = h2_bits(q6k_w2(as_h2((hb & k.hlo) | ((t & k.lo) | k.magic)) + blo, aa));
+                a[j].z = h2_bits(q6k_w2(__builtin_elementwise_fma(as_h2((ha & k.hhi) | ((v & k.hi) | k.magic)), s16, bhi), aa));
+                a[j].w = h2_bits(q6k_w2(__builtin_elementwise_fma(as_h2((hb & k.hhi) | ((t & k.hi) | k.magic)), s16, bhi), aa));
             }
-            const float sc = (float)(int8_t)((q.sc2 >> (8 * r)) & 0xffu);
-            acc += (d * sc) * fmaf(shi, 0.0625f, slo);
         }
-        return acc;
     }
 }
 
-// Row sums of a workgroup group of RT rows reduced by P waves each: red[w * RT + r].
-template <int RT, int P>
-struct QfRowSums {
-    const float *red;
-    __device__ __forceinline__ float operator[](int r) const {
-        if constexpr (P == 4) return (red[r] + red[RT + r]) + (red[2 * RT + r] + red[3 * RT + r]);
-        if constexpr (P == 2) return red[r] + red[RT + r];
-        return red[r];
+// x of one record (natural order, x[0]: elements 0..7, x[1]: 8..15) -> the B operands of its two
+// nibble words: o[0] = elements {0, 2, 1, 3, 8, 10, 9, 11}, o[1] = the same + 4.
+__device__ __forceinline__ void qf_perm_rec(const u32x4 (&x)[2], u32x4 (&o)[2]) {
+    const unsigned e[8] = {x[0].x, x[0].y, x[0].z, x[0].w, x[1].x, x[1].y, x[1].z, x[1].w};
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        o[c].x = __builtin_amdgcn_perm(e[2 * c + 1], e[2 * c], 0x05040100u);
+        o[c].y = __builtin_amdgcn_perm(e[2 * c + 1], e[2 * c], 0x07060302u);
+        o[c].z = __builtin_amdgcn_perm(e[2 * c + 5], e[2 * c + 4], 0x05040100u);
+        o[c].w = __builtin_amdgcn_perm(e[2 * c + 5], e[2 * c + 4], 0x07060302u);
     }
-};
+}
 
 // x source: x itself, or (layer 0) row token->token of the repacked embedding table, dequantized
-// in registers, with workgroup 0 writing the row to xcopy (the residual stream).
+// in the workgroup, with workgroup 0 writing the row to xcopy (the residual stream).
 struct QFXSrc {
     const h16 *x;
     QFMat emb;
@@ -549,253 +605,277 @@ struct QFXSrc {
     h16 *xcopy;
 };
 
-// The 256 threads form H sub-groups of LPR = 256 / H lanes; sub-group h multiplies rows
-// h ROWS .. h ROWS + ROWS - 1 of each RT = H ROWS-row group, lane p taking chunk p + LPR i of
-// slab i (NS slabs cover K). A workgroup runs G groups. x stays in registers (RMS-normalized once,
-// then put in pair order); the chunk requests run D (group, slab) steps ahead through a register
-// ring; each group ends in a wave reduction, one LDS exchange and the fused epilogue.
-template <int T, int ROWS, int H, int NS, int G, bool NORM, class Epi>
-__global__ __launch_bounds__(kThreads) void gemv_qf_kernel(QFMat w, int64_t N, int64_t K, QFXSrc src,
-                                                           const h16 *__restrict__ nw, float eps, Epi epi) {
-    constexpr int LPR = kThreads / H, WPS = LPR / kWave, RT = H * ROWS;
-    __shared__ float red[G > 1 ? 2 : 1][WPS * RT];
-    __shared__ float nred[4];
+// x records per thread held in registers while the first tiles load (larger K stages x in a loop
+// after the tile requests).
+constexpr int kQfXRegs = 1;
+
+template <int T, int NW, int SP, bool NORM, class Epi>
+__global__ __launch_bounds__(NW * kWave) void gemv_qf_kernel(QFMat w, int64_t N, int64_t K, QFXSrc src,
+                                                             const h16 *__restrict__ nw, float eps, Epi epi) {
+    constexpr int NT = NW * kWave, XR = kQfXRegs;
+    // the lm_head keeps one argmax partial per 8 logits: its epilogue runs per 8 rows
+    constexpr int ER = std::is_same<Epi, EpiLmHead>::value ? 8 : 16;
+    static_assert(NW >= 16 / ER, "one epilogue wave per row group");
+    extern __shared__ __align__(16) uint8_t lds[];  // x (2 K bytes), the row partials (2 x NW x 16), the norm scratch
+    float *red = reinterpret_cast<float *>(lds + 2 * K);
+    float *nred = red + 2 * NW * 16;  // NW floats, then 16 for the final row sums
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int h = wave / WPS, p = tid % LPR;
-    const int64_t nbase = (int64_t)blockIdx.x * G * RT;
-    const int chunks = (int)(K / kChunk);
-    const QfRsrc rs = qf_rsrc(w, T, N, K);
-    auto row = [&](int g, int r) -> int {  // plane row of row r of sub-group h in group g (clamped)
-        const int64_t n = nbase + (int64_t)g * RT + h * ROWS + r;
-        return (int)(n < N ? n : N - 1);
-    };
-    u32x4 xr[NS][4], nr[NS][4];
-    bool live[NS];
+    const int nseg = (int)(K / kSeg), nrec = (int)(K / kRec);
+    const int blocks = (int)((N + 15) / 16);
+    const int pb0 = (int)(w.row0 / 16);  // plane row block of row 0
+    const QfRsrc rs = qf_rsrc(w, T, w.row0 + (int64_t)blocks * 16, K);
+    constexpr int es1 = T == AESIR_GGML_Q4_K ? 4 : 2;
+    const int sbr = (int)(K / 256);  // s1 entries per row
+    const int s1v = (lane & 15) * es1;
+    // steps of this workgroup: (block k, round r), r < R, for its nb blocks
+    const int R = (nseg + NW * SP - 1) / (NW * SP);
+    const int nb = (blocks - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int steps = nb * R;
+    if (nb <= 0) return;  // a grid larger than the blocks (never launched so)
+
+    // x: record r of x itself, or of row token->token of the embedding table (dequantized)
     const bool embed = src.emb.nib != nullptr;
-    const int64_t trow = embed ? src.token->token : 0;
-#pragma unroll
-    for (int i = 0; i < NS; i++) {
-        const int c = p + LPR * i;
-        live[i] = c < chunks;
-        const int64_t k = live[i] ? (int64_t)c * kChunk : 0;
+    const int64_t erow = embed ? src.emb.row0 + src.token->token : 0;
+    h16 *xcopy = (src.xcopy && blockIdx.x == 0) ? src.xcopy : nullptr;
+    auto getx = [&](int r, u32x4(&x)[2]) {
         if (embed) {
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                u32x4 o[2];
-                qf_deq16<T>(qf_load<T>(src.emb, trow, k / kRec + j, K), o);
-                xr[i][2 * j] = o[0];
-                xr[i][2 * j + 1] = o[1];
-            }
+            qf_deq16<T>(qf_load<T>(src.emb, erow, r, K), x);
         } else {
-#pragma unroll
-            for (int q = 0; q < 4; q++) xr[i][q] = ld16(src.x + k + 8 * q);
+            x[0] = ld16(src.x + (int64_t)r * kRec);
+            x[1] = ld16(src.x + (int64_t)r * kRec + 8);
         }
-        if (NORM)
-#pragma unroll
-            for (int q = 0; q < 4; q++) nr[i][q] = ld16(nw + k + 8 * q);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    constexpr int TT = G * NS, D = TT < kQfDepth ? TT : kQfDepth;
-    QChunk<T> qb[D][ROWS];
-    auto request = [&](int st) {
-        const int g = st / NS, i = st % NS;
-        const int c = p + LPR * i;
-        const int cc = c < chunks ? c : 0;  // dead lanes of a partial slab re-read chunk 0
-#pragma unroll
-        for (int r = 0; r < ROWS; r++) qb[st % D][r] = qf_chunk_load<T>(rs, row(g, r), cc);
     };
+    // Every load below is issued on all paths (a surplus thread or slot re-reads a valid, cached
+    // address): the waits the compiler places before each use then count only the loads issued
+    // after it, so the next round's tiles stay in flight while the current one computes.
+    const bool xfast = nrec <= XR * NT;
+    u32x4 xr[XR][2], nr[XR][2];
+    if (xfast) {
 #pragma unroll
-    for (int st = 0; st < D; st++) request(st);
-    __builtin_amdgcn_sched_barrier(0);
-    using Pre = decltype(epi.template prefetch<RT>(0, 0, N, tid));
-    Pre pre[G];
-#pragma unroll
-    for (int g = 0; g < G; g++)
-        if (g * NS < D) pre[g] = epi.template prefetch<RT>(nbase + (int64_t)g * RT, 0, N, tid);
-
-    float ss = 0.0f;
-    const bool first = h == 0;  // sub-group 0 holds one copy of x
-    h16 *xcopy = (src.xcopy && blockIdx.x == 0 && first) ? src.xcopy : nullptr;
-#pragma unroll
-    for (int i = 0; i < NS; i++) {
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            if (!live[i]) xr[i][q] = u32x4{0u, 0u, 0u, 0u};
-            if (xcopy && live[i]) st16(xcopy + (int64_t)(p + LPR * i) * kChunk + 8 * q, xr[i][q]);
-            if (NORM && first) ss = sumsq8(xr[i][q], ss);
-        }
-    }
-    if (NORM) {
-        ss = block_sum<kThreads / kWave, false>(ss, nred);
-        const h16 inv = (h16)(1.0f / sqrtf(ss / (float)K + eps));
-#pragma unroll
-        for (int i = 0; i < NS; i++)
-#pragma unroll
-            for (int q = 0; q < 4; q++) xr[i][q] = norm8(xr[i][q], nr[i][q], inv);
-    }
-    unsigned xp[NS][16];
-    float X[NS];
-#pragma unroll
-    for (int i = 0; i < NS; i++) {
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            unsigned part[8];
-            const u32x4 pr[2] = {xr[i][2 * j], xr[i][2 * j + 1]};
-            qf_perm_x(pr, part);
-#pragma unroll
-            for (int f = 0; f < 8; f++) xp[i][8 * j + f] = part[f];
-        }
-        X[i] = 0.0f;
-        if constexpr (T == AESIR_GGML_Q4_K) {
-            const h16x2 one = {(h16)1.0f, (h16)1.0f};
-#pragma unroll
-            for (int f = 0; f < 16; f++) X[i] = __builtin_amdgcn_fdot2(as_h2(xp[i][f]), one, X[i], false);
-        }
-    }
-    const QfRegs kr = QfRegs::make();
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-        float acc[ROWS];
-#pragma unroll
-        for (int r = 0; r < ROWS; r++) acc[r] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < NS; i++) {
-            const int st = g * NS + i;
-#pragma unroll
-            for (int r = 0; r < ROWS; r++) acc[r] = qf_chunk_dot<T>(qb[st % D][r], xp[i], X[i], acc[r], kr);
-            if (st + D < TT) {
-                request(st + D);
-                const int gn = (st + D) / NS;
-                if ((st + D) % NS == 0) pre[gn] = epi.template prefetch<RT>(nbase + (int64_t)gn * RT, 0, N, tid);
+        for (int j = 0; j < XR; j++) {
+            const int r = tid + NT * j < nrec ? tid + NT * j : nrec - 1;
+            getx(r, xr[j]);
+            if (NORM) {
+                nr[j][0] = ld16(nw + (int64_t)r * kRec);
+                nr[j][1] = ld16(nw + (int64_t)r * kRec + 8);
             }
         }
-        wave_multi_sum<ROWS>(acc, lane);
-        constexpr int GW = kWave / ROWS;
-        float *rg = red[g & (G > 1 ? 1 : 0)];
-        if ((lane & (GW - 1)) == 0) rg[(wave % WPS) * RT + h * ROWS + lane / GW] = acc[0];
-        __syncthreads();
-        epi.template apply<RT>(nbase + (int64_t)g * RT, 0, N, QfRowSums<RT, WPS>{rg}, tid, pre[g]);
     }
-}
 
-// Sub-group count for a row length: the fewest lanes left idle by the last slab, then the fewer
-// slabs. Returns 0 when no instantiated shape covers K.
-static int qf_pick_h(int64_t K) {
-    int best = 0;
-    int64_t best_waste = INT64_MAX, best_ns = 0;
-    for (int h : {1, 2, 4}) {
-        const int64_t slab = (int64_t)(kThreads / h) * kChunk, ns = (K + slab - 1) / slab;
-        if (ns > kQfMaxSlabs[h == 1 ? 0 : h == 2 ? 1 : 2]) continue;
-        const int64_t waste = ns * slab - K;
-        if (waste < best_waste || (waste == best_waste && ns < best_ns)) {
-            best = h;
-            best_waste = waste;
-            best_ns = ns;
+    QTile<T> tl[2][SP];
+    auto issue = [&](int st, QTile<T>(&buf)[SP]) {
+        const int pb = pb0 + (int)blockIdx.x + (st / R) * (int)gridDim.x, first = wave + NW * SP * (st % R);
+#pragma unroll
+        for (int i = 0; i < SP; i++) {
+            const int sg = first + NW * i < nseg ? first + NW * i : nseg - 1;  // a surplus slot: the last segment
+            buf[i] = qf_tile_load<T>(rs, pb * nseg + sg, lane, s1v, (pb * sbr + sg / 2) * 16 * es1);
+        }
+    };
+    issue(0, tl[0]);
+    // the epilogue operands of this wave's rows (ER rows at en(k)) of the current and next block
+    const bool ewave = wave < 16 / ER;
+    auto en = [&](int k) { return (int64_t)((int)blockIdx.x + k * (int)gridDim.x) * 16 + wave * ER; };
+    using Pre = decltype(epi.template prefetch<ER>(0, 0, N, 0));
+    Pre pre = epi.template prefetch<ER>(en(0), 0, N, ewave ? lane : kWave);
+
+    // stage x: record r at lds + 32 r in the B-operand order, RMS-normalized when NORM
+    h16 inv = (h16)1.0f;
+    if (xfast) {
+        if (NORM) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int j = 0; j < XR; j++)
+                if (tid + NT * j < nrec) ss = sumsq8(xr[j][1], sumsq8(xr[j][0], ss));
+            ss = block_sum<NW, false>(ss, nred);
+            inv = (h16)(1.0f / sqrtf(ss / (float)K + eps));
+        }
+#pragma unroll
+        for (int j = 0; j < XR; j++) {
+            const int r = tid + NT * j;
+            if (r < nrec) {
+                u32x4 o[2];
+                if (xcopy) {
+                    st16(xcopy + (int64_t)r * kRec, xr[j][0]);
+                    st16(xcopy + (int64_t)r * kRec + 8, xr[j][1]);
+                }
+                if (NORM) {
+                    xr[j][0] = norm8(xr[j][0], nr[j][0], inv);
+                    xr[j][1] = norm8(xr[j][1], nr[j][1], inv);
+                }
+                qf_perm_rec(xr[j], o);
+                st16(lds + 32 * r, o[0]);
+                st16(lds + 32 * r + 16, o[1]);
+            }
+        }
+    } else {
+        if (NORM) {
+            float ss = 0.0f;
+            for (int r = tid; r < nrec; r += NT) {
+                u32x4 x[2];
+                getx(r, x);
+                ss = sumsq8(x[1], sumsq8(x[0], ss));
+            }
+            ss = block_sum<NW, false>(ss, nred);
+            inv = (h16)(1.0f / sqrtf(ss / (float)K + eps));
+        }
+        for (int r = tid; r < nrec; r += NT) {
+            u32x4 x[2], o[2];
+            getx(r, x);
+            if (xcopy) {
+                st16(xcopy + (int64_t)r * kRec, x[0]);
+                st16(xcopy + (int64_t)r * kRec + 8, x[1]);
+            }
+            if (NORM) {
+                x[0] = norm8(x[0], ld16(nw + (int64_t)r * kRec), inv);
+                x[1] = norm8(x[1], ld16(nw + (int64_t)r * kRec + 8), inv);
+            }
+            qf_perm_rec(x, o);
+            st16(lds + 32 * r, o[0]);
+            st16(lds + 32 * r + 16, o[1]);
         }
     }
-    return best;
-}
+    __syncthreads();
 
-template <int T, int ROWS, int H, int G, bool NORM, class Epi>
-static int32_t gemv_qf_launch_h(hipStream_t s, const QFMat &w, int64_t N, int64_t K, const QFXSrc &src, const void *nw,
-                                float eps, const Epi &epi, int64_t ns) {
-    const dim3 grid((unsigned)((N + (int64_t)H * ROWS * G - 1) / ((int64_t)H * ROWS * G)));
-    switch (ns) {
-#define AESIR_QF_NS(NSV)                                                                                          \
-    case NSV:                                                                                                    \
-        if constexpr (NSV <= kQfMaxSlabs[H == 1 ? 0 : H == 2 ? 1 : 2]) {                                        \
-            hipLaunchKernelGGL((gemv_qf_kernel<T, ROWS, H, NSV, G, NORM, Epi>), grid, dim3(kThreads), 0, s, w, N, K, \
-                               src, (const h16 *)nw, eps, epi);                                                  \
-            return AESIR_OK;                                                                                     \
-        }                                                                                                        \
-        break;
-        AESIR_QF_NS(1)
-        AESIR_QF_NS(2)
-        AESIR_QF_NS(3)
-        AESIR_QF_NS(4)
-#undef AESIR_QF_NS
-        default: break;
+    const QfRegs kr = QfRegs::make();
+    f32x4 acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+    float *fin = nred + NW;  // the block's final row sums, each ER-row part written and read by its epilogue wave
+    // step st: request step st + 1 into nxt (PF), multiply the tiles of cur, and after a block's
+    // last round reduce its row sums over the waves and run its epilogue
+    auto step = [&](auto pf, int st, const QTile<T>(&cur)[SP], QTile<T>(&nxt)[SP]) {
+        const int k = st / R, r = st % R;
+        if constexpr (decltype(pf)::value) issue(st + 1, nxt);
+        const int first = wave + NW * SP * r;
+#pragma unroll
+        for (int i = 0; i < SP; i++) {
+            const int sg = first + NW * i;
+            if (sg < nseg) {
+                const uint8_t *xs = lds + sg * 256 + (lane >> 4) * 64;  // records 8 sg + 2 (lane / 16), + 1
+                const u32x4 bx[4] = {ld16(xs), ld16(xs + 16), ld16(xs + 32), ld16(xs + 48)};
+                u32x4 a[4];
+                qf_tile_a<T>(cur[i], kr, a);
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[j & 1] = mfma16x16x32(a[j], bx[j], acc[j & 1]);
+            }
+        }
+        if (r == R - 1) {
+            float *rb = red + (k & 1) * (NW * 16);
+            if ((lane & 15) == 0) {  // rows 4 (lane / 16) + e, the same in every column
+                const f32x4 v = acc[0] + acc[1];
+#pragma unroll
+                for (int e = 0; e < 4; e++) rb[wave * 16 + 4 * (lane >> 4) + e] = v[e];
+            }
+            acc[0] = acc[1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            __syncthreads();
+            const Pre now = pre;
+            if (k + 1 < nb) pre = epi.template prefetch<ER>(en(k + 1), 0, N, ewave ? lane : kWave);
+            if (ewave) {
+                if (lane < ER) {  // lane: row wave * ER + lane, summed over the waves in one order
+                    float v = rb[wave * ER + lane];
+#pragma unroll
+                    for (int w2 = 1; w2 < NW; w2++) v += rb[w2 * 16 + wave * ER + lane];
+                    fin[wave * ER + lane] = v;
+                }
+                epi.template apply<ER>(en(k), 0, N, fin + wave * ER, lane, now);
+            }
+        }
+    };
+    // the last step requests nothing (no step follows it)
+    using Pf = std::true_type;
+    using NoPf = std::false_type;
+    int st = 0;
+    for (; st + 2 < steps; st += 2) {
+        step(Pf{}, st, tl[0], tl[1]);
+        step(Pf{}, st + 1, tl[1], tl[0]);
     }
-    return fail(AESIR_ERR_UNSUPPORTED, "quantized GEMV: K = %lld exceeds %lld", (long long)K,
-                (long long)(kThreads * kChunk * kQfMaxSlabs[0]));
+    if (steps - st == 2) {
+        step(Pf{}, st, tl[0], tl[1]);
+        step(NoPf{}, st + 1, tl[1], tl[0]);
+    } else {
+        step(NoPf{}, st, tl[0], tl[1]);
+    }
 }
 
-// RT: rows per group of the workgroup, split over the H sub-groups.
-template <int RT, int G, bool NORM, class Epi, int T>
-static int32_t gemv_qf_launch_t(hipStream_t s, const QFMat &w, int64_t N, int64_t K, const QFXSrc &src, const void *nw,
-                                float eps, const Epi &epi) {
-    const int h = qf_pick_h(K);
-    if (h == 0)
-        return fail(AESIR_ERR_UNSUPPORTED, "quantized GEMV: K = %lld exceeds %lld", (long long)K,
-                    (long long)(kThreads * kChunk * kQfMaxSlabs[0]));
-    const int64_t slab = (int64_t)(kThreads / h) * kChunk, ns = (K + slab - 1) / slab;
-    // one sub-group: half the rows per group (register budget of the long-K slabs), except for the
-    // lm_head, whose argmax partials are per RT rows
-    constexpr int R1 = std::is_same<Epi, EpiLmHead>::value ? RT : RT / 2;
-    if (h == 1) return gemv_qf_launch_h<T, R1, 1, G, NORM, Epi>(s, w, N, K, src, nw, eps, epi, ns);
-    if (h == 2) return gemv_qf_launch_h<T, RT / 2, 2, G, NORM, Epi>(s, w, N, K, src, nw, eps, epi, ns);
-    return gemv_qf_launch_h<T, RT / 4, 4, G, NORM, Epi>(s, w, N, K, src, nw, eps, epi, ns);
+// Waves, round length and workgroups (measured on MI355X over the Llama-3-8B shapes): 8 waves with
+// rounds of half the register budget's tiles; from 1024 blocks on, persistent workgroups (512,
+// or 1024 from 4096 blocks, i.e. 3.5 to 8 blocks each), otherwise one block per workgroup.
+struct QfShape {
+    int nw, sp;
+    int64_t grid;
+};
+static QfShape qf_shape(int64_t blocks, int round) {
+    const int64_t grid = blocks < 1024 ? blocks : blocks < 4096 ? 512 : 1024;
+    return {8, round / 2, grid};
 }
 
-template <int RT, int G, bool NORM, class Epi>
+template <bool NORM, class Epi, int T>
+static void gemv_qf_launch_t(hipStream_t s, const QFMat &w, int64_t N, int64_t K, const QFXSrc &src, const void *nwt,
+                             float eps, const Epi &epi) {
+    constexpr int RD = qf_round<T>();
+    const QfShape sh = qf_shape((N + 15) / 16, RD);
+    const size_t lds = (size_t)(2 * K) + ((size_t)sh.nw * (2 * 16 + 1) + 16) * sizeof(float);
+    hipLaunchKernelGGL((gemv_qf_kernel<T, 8, RD / 2, NORM, Epi>), dim3((unsigned)sh.grid), dim3(8 * kWave), lds, s, w, N, K,
+                       src, (const h16 *)nwt, eps, epi);
+}
+
+bool qf_gemv_ok(int64_t K) { return K > 0 && K % kSeg == 0 && K <= kQfGemvMaxK; }
+
+template <bool NORM, class Epi>
 static int32_t gemv_qf_dispatch(hipStream_t s, const QFMat &w, int64_t N, int64_t K, const QFXSrc &src, const void *nw,
                                 float eps, const Epi &epi, const char *name) {
-    static_assert(RT % 4 == 0, "groups split over up to four sub-groups");
     AESIR_TRY(qf_check(w.type, K, name));
+    if (!qf_gemv_ok(K))
+        return fail(AESIR_ERR_UNSUPPORTED, "%s: quantized GEMV needs a row length that is a multiple of 128, at most %lld (got %lld)",
+                    name, (long long)kQfGemvMaxK, (long long)K);
+    if (w.row0 % 16 != 0) return fail(AESIR_ERR_INVALID, "%s: quantized GEMV needs a matrix starting on a 16-row block", name);
     if (src.emb.nib && src.emb.type != w.type) return fail(AESIR_ERR_INVALID, "%s: embedding type differs", name);
     const void *xp = src.emb.nib ? (const void *)src.emb.nib : (const void *)src.x;
     if (((uintptr_t)w.nib & 15) || ((uintptr_t)xp & 15) || (NORM && ((uintptr_t)nw & 15)) ||
         (src.xcopy && ((uintptr_t)src.xcopy & 15)))
         return fail(AESIR_ERR_UNSUPPORTED, "%s: quantized GEMV needs 16-byte aligned operands", name);
-    // plane offsets are 32-bit in the buffer loads
     if (N <= 0) return AESIR_OK;
-    if (mul_checked(N, qf_plane_row_bytes(w.type, 0, K)) > INT32_MAX)
+    // plane offsets are 32-bit in the buffer loads
+    if (mul_checked(w.row0 + qf_rows_alloc(N), qf_plane_row_bytes(w.type, 0, K)) > INT32_MAX)
         return fail(AESIR_ERR_UNSUPPORTED, "%s: matrix of %lld x %lld exceeds 2 GiB of 4-bit weights", name, (long long)N,
                     (long long)K);
-    int32_t rc;
     if (w.type == AESIR_GGML_Q4_0)
-        rc = gemv_qf_launch_t<RT, G, NORM, Epi, AESIR_GGML_Q4_0>(s, w, N, K, src, nw, eps, epi);
+        gemv_qf_launch_t<NORM, Epi, AESIR_GGML_Q4_0>(s, w, N, K, src, nw, eps, epi);
     else if (w.type == AESIR_GGML_Q4_K)
-        rc = gemv_qf_launch_t<RT, G, NORM, Epi, AESIR_GGML_Q4_K>(s, w, N, K, src, nw, eps, epi);
+        gemv_qf_launch_t<NORM, Epi, AESIR_GGML_Q4_K>(s, w, N, K, src, nw, eps, epi);
     else
-        rc = gemv_qf_launch_t<RT, G, NORM, Epi, AESIR_GGML_Q6_K>(s, w, N, K, src, nw, eps, epi);
-    AESIR_TRY(rc);
+        gemv_qf_launch_t<NORM, Epi, AESIR_GGML_Q6_K>(s, w, N, K, src, nw, eps, epi);
     AESIR_LAUNCH_CHECK(name);
     return AESIR_OK;
 }
 
 int32_t launch_qf_gemv_store(hipStream_t s, const QFMat &w, int64_t N, int64_t K, const void *x, void *y) {
     EpiStore e{(h16 *)y, N};
-    return gemv_qf_dispatch<kQfGroupRows, kQfGroups, false>(s, w, N, K, QFXSrc{(const h16 *)x, QFMat{}, nullptr, nullptr},
-                                                          nullptr, 0.0f, e, "gemv_qf_store");
+    return gemv_qf_dispatch<false>(s, w, N, K, QFXSrc{(const h16 *)x, QFMat{}, nullptr, nullptr}, nullptr, 0.0f, e,
+                                   "gemv_qf_store");
 }
 
 int32_t launch_qf_gemv_residual(hipStream_t s, const QFMat &w, int64_t N, int64_t K, const void *x_in, void *x) {
     EpiResidual e{(h16 *)x};
-    return gemv_qf_dispatch<kQfGroupRows, kQfGroups, false>(s, w, N, K, QFXSrc{(const h16 *)x_in, QFMat{}, nullptr, nullptr},
-                                                          nullptr, 0.0f, e, "gemv_qf_residual");
+    return gemv_qf_dispatch<false>(s, w, N, K, QFXSrc{(const h16 *)x_in, QFMat{}, nullptr, nullptr}, nullptr, 0.0f, e,
+                                   "gemv_qf_residual");
 }
 
 int32_t launch_qf_gate_up_swiglu(hipStream_t s, const void *x, const void *norm_w, float eps, const QFMat &w,
                                  int64_t ffn, int64_t dim, void *act) {
     EpiSwiglu e{(h16 *)act};
-    return gemv_qf_dispatch<kQfGroupRows, kQfGroupsFfn, true>(s, w, 2 * ffn, dim,
-                                                            QFXSrc{(const h16 *)x, QFMat{}, nullptr, nullptr}, norm_w,
-                                                            eps, e, "gemv_qf_gate_up");
+    return gemv_qf_dispatch<true>(s, w, 2 * ffn, dim, QFXSrc{(const h16 *)x, QFMat{}, nullptr, nullptr}, norm_w, eps, e,
+                                  "gemv_qf_gate_up");
 }
 
 int32_t launch_qf_qkv_rope_kv(hipStream_t s, const QkvArgs &a, const EpiQkv &e) {
     const QFXSrc src = a.eq.nib ? QFXSrc{nullptr, a.eq, a.state, (h16 *)a.x}
                                 : QFXSrc{(const h16 *)a.x, QFMat{}, nullptr, nullptr};
-    return gemv_qf_dispatch<kQfGroupRows, kQfGroups, true>(s, a.wq, a.dim + 2 * a.kvd, a.dim, src, a.norm_w, a.eps, e,
-                                                         "gemv_qf_qkv_rope_kv");
+    return gemv_qf_dispatch<true>(s, a.wq, a.dim + 2 * a.kvd, a.dim, src, a.norm_w, a.eps, e, "gemv_qf_qkv_rope_kv");
 }
 
-// 8 rows per group: one argmax partial per 8 logits (lm_head_groups).
 int32_t launch_qf_lm_head(hipStream_t s, const LmHeadArgs &a, const EpiLmHead &e) {
-    return gemv_qf_dispatch<8, 1, true>(s, a.wq, a.vocab, a.dim, QFXSrc{(const h16 *)a.x, QFMat{}, nullptr, nullptr},
-                                        a.norm_w, a.eps, e, "gemv_qf_lm_head");
+    return gemv_qf_dispatch<true>(s, a.wq, a.vocab, a.dim, QFXSrc{(const h16 *)a.x, QFMat{}, nullptr, nullptr},
+                                  a.norm_w, a.eps, e, "gemv_qf_lm_head");
 }
 
 }  // namespace aesir

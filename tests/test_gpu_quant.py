@@ -1,15 +1,16 @@
-"""GPU parity of the Q4_0, Q4_K and Q6_K weight paths (repacked records, decode GEMVs with the fused
-epilogues, batched prefill, GGUF loading) against the CPU oracle.
+"""GPU parity of the Q4_0, Q4_K and Q6_K weight paths (tiled records, the matrix-core decode GEMV
+with the fused epilogues, batched prefill, GGUF loading) against the CPU oracle.
 
 - aesir_gemm_quant on packed GGUF blocks: Q4_0 within 1 f16 ulp of the oracle's gemm_q4_0
   (core/compute.mojo:876-912; beyond 1 ulp only where f32 summation noise exceeds it); Q4_K / Q6_K
-  against f64 on the oracle's f32 dequantization (GGML's weights) within one f16 rounding plus
-  f32 summation noise; 16 or more rows of A take the matrix cores on f16-rounded weights and are
-  held to f64 on those.
-- Models: the F16 oracle holding the weights the model reads back (get_tensor). Q4_0's weights
-  are exactly those f16 values, so tokens are identical; the K-quant GEMVs use GGML's f32 weights,
-  which differ from the read-back f16 values by one f16 rounding, so logits are held to the
-  forward-pass tolerance and a token may differ only at a near tie of the oracle's logits.
+  against f64 on the oracle's f16 weights (ao_dequantize_q4_k_f16 / _q6_k_f16, the rule every
+  kernel of the library applies) within one f16 rounding of the output plus f32 summation noise.
+  16 or more rows of A, and Q4_0 rows whose length is not a multiple of 128, take the F16 GEMM on
+  the same f16 weights and are held to f64 on those.
+- Models: the F16 oracle holding the weights the model reads back (get_tensor), which are the
+  f16 weights the GEMVs and the prefill multiply for all three types; Q4_0 tokens are identical,
+  K-quant tokens may differ only at a near tie of the oracle's logits, and logits are held to the
+  forward-pass tolerance.
 """
 import numpy as np
 import pytest
@@ -61,13 +62,16 @@ def random_tensor(A, kind, rows, cols, rng, std=0.02):
     return A.Q6_KTensor.from_parts(d, sc, rng.integers(0, 64, (rows, cols)).astype(np.uint8))
 
 
-def f32_weights(oracle, kind, t):
+def lib_weights(oracle, kind, t):
+    """The f16 weights the library multiplies, as f64."""
     nb = t.blocks.shape[0]
     if kind == "q4_0":
-        return oracle.dequantize_q4_0(t.blocks, nb).astype(np.float32).reshape(t.rows, t.cols)
-    if kind == "q4_k":
-        return oracle.dequantize_q4_k(t.blocks, nb).reshape(t.rows, t.cols)
-    return oracle.dequantize_q6_k(t.blocks, nb).reshape(t.rows, t.cols)
+        w = oracle.dequantize_q4_0(t.blocks, nb)
+    elif kind == "q4_k":
+        w = oracle.dequantize_q4_k_f16(t.blocks, nb)
+    else:
+        w = oracle.dequantize_q6_k_f16(t.blocks, nb)
+    return w.astype(np.float64).reshape(t.rows, t.cols)
 
 
 def upload_bytes(ctx, raw):
@@ -89,16 +93,14 @@ def ulp_diff(a, b):
 
 @pytest.mark.parametrize("kind", list(TYPES))
 @pytest.mark.parametrize("M,K,N", [(1, 4096, 64), (1, 14336, 40), (3, 2048, 100), (1, 5632, 33), (1, 28672, 8),
-                                   (20, 4096, 48)])
+                                   (20, 4096, 48), (1, 512, 16400), (2, 1536, 18000)])
 def test_gemm_quant_vs_oracle(A, ctx, oracle, kind, M, K, N):
     t = random_tensor(A, kind, N, K, RNG)
     x = RNG.standard_normal((M, K)).astype(np.float16)
     c = ctx.tensor(M, N)
     A.gemm_quant(ctx, ctx.from_numpy(x), upload_bytes(ctx, t.blocks), TYPES[kind], N, c)
     got = c.numpy().astype(np.float64)
-    W = f32_weights(oracle, kind, t).astype(np.float64)
-    if M >= 16:
-        W = W.astype(np.float16).astype(np.float64)  # the matrix cores read f16 weights
+    W = lib_weights(oracle, kind, t)
     xd = x.astype(np.float64)
     noise = 2.0 ** -17 * (np.abs(xd) @ np.abs(W).T)
     if kind == "q4_0" and M < 16:
@@ -111,6 +113,23 @@ def test_gemm_quant_vs_oracle(A, ctx, oracle, kind, M, K, N):
     exact = xd @ W.T
     tol = np.abs(np.spacing(exact.astype(np.float16))).astype(np.float64) + noise
     assert np.all(np.abs(got - exact) <= tol), np.max(np.abs(got - exact) / tol)
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 160, 24), (3, 96, 40), (1, 28704, 17)])
+def test_gemm_q4_0_rows_off_the_tile_grid(A, ctx, oracle, M, K, N):
+    """Q4_0 rows whose length is not a multiple of 128 (or above the GEMV's 28672) take the f16
+    dequantization + F16 GEMM route: within 1 f16 ulp of the oracle's gemm_q4_0 where f32
+    summation noise does not exceed it."""
+    t = random_tensor(A, "q4_0", N, K, RNG)
+    x = RNG.standard_normal((M, K)).astype(np.float16)
+    c = ctx.tensor(M, N)
+    A.gemm_quant(ctx, ctx.from_numpy(x), upload_bytes(ctx, t.blocks), TYPES["q4_0"], N, c)
+    got = c.numpy()
+    ref = oracle.gemm_q4_0(x, t.blocks, N)
+    W = lib_weights(oracle, "q4_0", t)
+    noise = 2.0 ** -17 * (np.abs(x.astype(np.float64)) @ np.abs(W).T)
+    d = ulp_diff(got, ref)
+    assert not ((d > 1) & (np.abs(got.astype(np.float64) - ref.astype(np.float64)) > noise)).any(), d.max()
 
 
 def test_gemm_quant_errors(A, ctx):

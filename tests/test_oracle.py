@@ -760,6 +760,53 @@ def test_q6_k_literal_block(oracle):
     assert np.array_equal(t.blocks[0], blk)
 
 
+def test_k_quant_f16_weights(oracle):
+    """The library's f16 K-quant weights (Q4_K f16(a q - b), a = f16(d sc), b = f16(dmin m), one
+    fused rounding; Q6_K f16(a (q - 32))): on the literal blocks every product is exact, so they
+    equal GGML's f32 weights; on random blocks they equal numpy's own float64 -> float16 rounding
+    of the exact value, and stay within half an f16 ulp plus the scale roundings of GGML's f32
+    weights (|q| half-ulps of a, half an ulp of b)."""
+    import aesir_hip as A
+
+    blk, _, _, want = _q4_k_literal_block()
+    got = oracle.dequantize_q4_k_f16(blk.reshape(1, 144), 1)
+    assert got.dtype == np.float16 and np.array_equal(got.astype(np.float64), want)
+    qv = (7 * np.arange(256) + 3) % 64
+    sc = np.array([(j + 1) * (-1) ** j for j in range(16)], np.int8)
+    t6 = A.Q6_KTensor.from_parts(np.array([[0.125]], np.float16), sc.reshape(1, 1, 16), qv.astype(np.uint8).reshape(1, 256))
+    assert np.array_equal(oracle.dequantize_q6_k_f16(t6.blocks, 1), oracle.dequantize_q6_k(t6.blocks, 1).astype(np.float16))
+
+    rng = np.random.default_rng(18)
+    rows, cols = 6, 768
+    nsb = cols // 256
+    d = rng.uniform(1e-4, 0.01, (rows, nsb)).astype(np.float16)
+    dmin = rng.uniform(1e-4, 0.01, (rows, nsb)).astype(np.float16)
+    s4 = rng.integers(0, 64, (rows, nsb, 8)).astype(np.uint8)
+    m4 = rng.integers(0, 64, (rows, nsb, 8)).astype(np.uint8)
+    q = rng.integers(0, 16, (rows, cols)).astype(np.uint8)
+    t = A.Q4_KTensor.from_parts(d, dmin, s4, m4, q)
+    got = oracle.dequantize_q4_k_f16(t.blocks, rows * nsb).reshape(rows, cols)
+    sub = np.arange(cols) // 32
+    a = (d.astype(np.float32)[:, sub // 8] * s4.astype(np.float32).reshape(rows, -1)[:, sub]).astype(np.float16)
+    b = (dmin.astype(np.float32)[:, sub // 8] * m4.astype(np.float32).reshape(rows, -1)[:, sub]).astype(np.float16)
+    exact = a.astype(np.float64) * q - b.astype(np.float64)
+    assert np.array_equal(got.view(np.uint16), exact.astype(np.float16).view(np.uint16))
+    f32 = oracle.dequantize_q4_k(t.blocks, rows * nsb).reshape(rows, cols).astype(np.float64)
+    rel = 2.0 ** -11 * (1 + 2.0 ** -10)  # half an f16 ulp of a normal value, relative to the rounded value
+    bound = (np.abs(np.spacing(got)).astype(np.float64) / 2 + q * np.abs(a).astype(np.float64) * rel
+             + np.abs(b).astype(np.float64) * rel)
+    assert np.all(np.abs(got.astype(np.float64) - f32) <= bound)
+    assert not np.array_equal(got.astype(np.float64), f32)  # the f16 rule is not the f32 value
+    s6 = rng.integers(-128, 128, (rows, nsb, 16)).astype(np.int8)
+    q6 = rng.integers(0, 64, (rows, cols)).astype(np.uint8)
+    t6 = A.Q6_KTensor.from_parts(d, s6, q6)
+    got6 = oracle.dequantize_q6_k_f16(t6.blocks, rows * nsb).reshape(rows, cols)
+    sub16 = np.arange(cols) // 16
+    a6 = (d.astype(np.float32)[:, sub16 // 16] * s6.astype(np.float32).reshape(rows, -1)[:, sub16]).astype(np.float16)
+    want6 = (a6.astype(np.float64) * (q6.astype(np.float64) - 32)).astype(np.float16)
+    assert np.array_equal(got6.view(np.uint16), want6.view(np.uint16))
+
+
 def test_k_quant_random_blocks_match_the_formula(oracle):
     """Random super-blocks through the packers: the oracle's f32 dequantization is within one f32
     rounding of the f64 formula from the parts (Q4_K: d sc q - dmin m; Q6_K: d sc (q - 32))."""

@@ -174,13 +174,16 @@ int32_t aesir_gemm_q8_0(aesir_ctx *ctx, const void *A, int64_t a_rows, int64_t a
 /* The reference's quantized branch of gemm_f16 (core/compute.mojo:1763-1800) over packed GGUF
  * blocks of ggml_type: B is b_rows x a_cols weights, C[m, n] = f16(sum_k A[m, k] w[n, k]).
  * AESIR_GGML_Q4_0 follows gemm_q4_0 (:876-912, w = f16(f16(q - 8) * d)); AESIR_GGML_Q8_0 is
- * aesir_gemm_q8_0; AESIR_GGML_Q4_K / AESIR_GGML_Q6_K use GGML's f32 weights (the reference's
- * gemm_q4_k_m / gemm_q6_k read synthetic block layouts that no GGUF file holds). Raises
- * "gemm_q4_0: matrix dimensions must be positive", "...: inner dimension must be a multiple of
- * 32" (256 for the K-quants), "...: output matrix shape mismatch". The blocks are repacked into
- * the library's record layout in free well space for the duration of the call (about the size
- * of the blocks; with a_rows >= 16 also an f16 copy of the weights for the matrix cores, whose
- * K-quant weights are then rounded to f16). */
+ * aesir_gemm_q8_0; AESIR_GGML_Q4_K / AESIR_GGML_Q6_K read GGML's super-blocks with f16 weights
+ * in the f16 arithmetic of the reference's dequantize_q4_k_m / dequantize_q6_k_block
+ * (:245-262, :508-527): w = f16(f16(d * sc) * q - f16(dmin * m)) (one fused rounding) and
+ * w = f16(f16(d * sc) * (q - 32)) (the reference's gemm_q4_k_m / gemm_q6_k read synthetic block
+ * layouts that no GGUF file holds). Raises "gemm_q4_0: matrix dimensions must be positive",
+ * "...: inner dimension must be a multiple of 32" (256 for the K-quants), "...: output matrix
+ * shape mismatch". Takes free well space for the duration of the call: with a_rows < 16 and
+ * a_cols a multiple of 128 (at most 28672) the blocks are repacked into the library's tiled
+ * planes (about the size of the blocks) for the decode GEMV; otherwise an f16 copy of the
+ * weights (2 bytes per weight) for the F16 GEMM. */
 int32_t aesir_gemm_quant(aesir_ctx *ctx, const void *A, int64_t a_rows, int64_t a_cols, const void *blocks,
                          int32_t ggml_type, int64_t b_rows, void *C, int64_t c_rows, int64_t c_cols);
 /* Q8_0 block matvec with f32 activations and f32 output: y[n] = sum_k x[k] * d*q. Rows of
@@ -257,11 +260,11 @@ int32_t aesir_model_create(aesir_ctx *ctx, const aesir_model_config *cfg, aesir_
  * dim and ffn must be multiples of 32 (and at most 16384). Every weight is used as
  * w = f16(f16(q) * d), gemm_q8_0's rule (core/compute.mojo:1062-1063), so a Q8_0 model computes
  * what the F16 model holding the dequantized weights computes. A Q4_0 / Q4_K / Q6_K model keeps
- * each matrix repacked into 16-weight records (nibble plane, per-block scale planes, Q6_K
- * high-bit plane); dim and ffn must be multiples of 32 (Q4_0) or 256 (K-quants), at most 28672.
- * Q4_0 weights are w = f16(f16(q - 8) * d) (gemm_q4_0, core/compute.mojo:876-912); Q4_K and Q6_K
- * weights are GGML's f32 values (d * sc) * q - dmin * m and (d * sc) * (q - 32). Norm vectors
- * stay f16. No reference counterpart as a model (the reference loader has no quantized model
+ * each matrix repacked into 16-weight records in 16-row x 128-weight tiles (nibble plane,
+ * per-block scale planes, Q6_K high-bit plane); dim and ffn must be multiples of 128 (Q4_0) or
+ * 256 (K-quants), at most 28672. Q4_0 weights are w = f16(f16(q - 8) * d) (gemm_q4_0,
+ * core/compute.mojo:876-912); Q4_K and Q6_K weights are f16(f16(d * sc) * q - f16(dmin * m)) and
+ * f16(f16(d * sc) * (q - 32)), as aesir_gemm_quant. Norm vectors stay f16. No reference counterpart as a model (the reference loader has no quantized model
  * path, loader/gguf.mojo:450-463). */
 int32_t aesir_model_create_typed(aesir_ctx *ctx, const aesir_model_config *cfg, int32_t weight_type,
                                  aesir_model **out);
@@ -278,8 +281,8 @@ int32_t aesir_model_get_config(const aesir_model *model, aesir_model_config *cfg
 int32_t aesir_model_set_tensor(aesir_model *model, const char *name, const void *host_data, int64_t rows,
                                int64_t cols, int32_t ggml_type);
 /* Reads a tensor back in GGUF order as f16 (for verification); quantized matrices come back
- * dequantized: f16(q * d) (Q8_0), f16(f16(q - 8) * d) (Q4_0), GGML's f32 weight rounded once to
- * f16 (Q4_K, Q6_K). */
+ * dequantized to the f16 weights the model multiplies: f16(q * d) (Q8_0), f16(f16(q - 8) * d)
+ * (Q4_0), the K-quant rules of aesir_model_create_typed (Q4_K, Q6_K). */
 int32_t aesir_model_get_tensor(aesir_model *model, const char *name, void *host_out, int64_t elements);
 /* Device-side seeded random init: every weight N(0, std), every norm N(norm_mean, norm_std),
  * rounded to f16; element i of tensor t uses the same counter-based Box-Muller stream as the

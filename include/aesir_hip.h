@@ -268,8 +268,24 @@ int32_t aesir_model_create(aesir_ctx *ctx, const aesir_model_config *cfg, aesir_
  * path, loader/gguf.mojo:450-463). */
 int32_t aesir_model_create_typed(aesir_ctx *ctx, const aesir_model_config *cfg, int32_t weight_type,
                                  aesir_model **out);
-/* Weight type of the model's matrices (AESIR_GGML_F16, _Q8_0, _Q4_0, _Q4_K or _Q6_K). */
+/* aesir_model_create_typed with one type per matrix: tensor_types holds n_types = 2 + 7 * n_layers
+ * ids in the order token_embd, output, then per layer attn_q, attn_k, attn_v, attn_output,
+ * ffn_gate, ffn_up, ffn_down (each F16, Q8_0, Q4_0, Q4_K or Q6_K, with that type's dim / ffn
+ * constraints). Each matrix keeps its own type in HBM, except the two fused ones: a layer's
+ * Q/K/V (and its gate/up) matrix is stored in f16 when its parts differ in type, each part
+ * dequantized at upload by its type's rule. aesir_model_set_tensor then takes each tensor in its
+ * own type. This is the layout of GGUF files that mix types (Q4_K_M and the like). No reference
+ * counterpart (the reference loader takes F16 files only, loader/gguf.mojo:450-463). */
+int32_t aesir_model_create_mixed(aesir_ctx *ctx, const aesir_model_config *cfg, const int32_t *tensor_types,
+                                 int64_t n_types, aesir_model **out);
+/* aesir_model_weight_type's value for a model whose matrices differ in type. */
+#define AESIR_WEIGHT_MIXED (-2)
+/* Weight type of the model's matrices (AESIR_GGML_F16, _Q8_0, _Q4_0, _Q4_K or _Q6_K), or
+ * AESIR_WEIGHT_MIXED when they differ (aesir_model_tensor_type gives each). */
 int32_t aesir_model_weight_type(const aesir_model *model);
+/* GGML type that aesir_model_set_tensor takes for the named tensor (norms: AESIR_GGML_F16, which
+ * also takes F32); a negative error code for an unknown name. */
+int32_t aesir_model_tensor_type(aesir_model *model, const char *name);
 int32_t aesir_model_destroy(aesir_model *model);
 int32_t aesir_model_get_config(const aesir_model *model, aesir_model_config *cfg);
 /* Uploads one tensor by its GGUF name ("token_embd.weight", "blk.N.attn_q.weight", ...),

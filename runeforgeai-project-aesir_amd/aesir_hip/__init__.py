@@ -90,7 +90,9 @@ _sig("aesir_kv_k_slice", [P, I64, I64, C.POINTER(P)])
 _sig("aesir_kv_v_slice", [P, I64, I64, C.POINTER(P)])
 _sig("aesir_model_create", [P, C.POINTER(_ModelConfig), C.POINTER(P)])
 _sig("aesir_model_create_typed", [P, C.POINTER(_ModelConfig), I32, C.POINTER(P)])
+_sig("aesir_model_create_mixed", [P, C.POINTER(_ModelConfig), P, I64, C.POINTER(P)])
 _sig("aesir_model_weight_type", [P])
+_sig("aesir_model_tensor_type", [P, C.c_char_p])
 _sig("aesir_model_destroy", [P])
 _sig("aesir_model_get_config", [P, C.POINTER(_ModelConfig)])
 _sig("aesir_model_set_tensor", [P, C.c_char_p, P, I64, I64, I32])
@@ -400,6 +402,7 @@ class ModelConfig:
 
 
 GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 0, 1, 2, 8, 12, 14
+WEIGHT_MIXED = -2  # aesir_model_weight_type of a model whose matrices differ in type
 
 
 class QuantTensor:
@@ -540,9 +543,33 @@ class Model:
             _check(_L.aesir_model_create_typed(ctx.h, C.byref(c), weight_type, C.byref(h)))
         return cls(ctx, h.value)
 
+    @classmethod
+    def create_mixed(cls, ctx: Context, cfg: ModelConfig, types: dict) -> "Model":
+        """A model with one type per matrix (aesir_model_create_mixed): `types` maps GGUF tensor
+        names ("token_embd.weight", "blk.N.attn_v.weight", ...) to GGML types; matrices it does
+        not name are F16."""
+        names = ["token_embd.weight", "output.weight"] + [
+            f"blk.{l}.{b}.weight" for l in range(cfg.n_layers)
+            for b in ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")]
+        unknown = set(types) - set(names)
+        if unknown:
+            raise ValueError(f"not a model matrix: {sorted(unknown)[0]}")
+        t = np.array([types.get(n, GGML_F16) for n in names], np.int32)
+        h = P()
+        c = cfg._c()
+        _check(_L.aesir_model_create_mixed(ctx.h, C.byref(c), t.ctypes.data, t.size, C.byref(h)))
+        return cls(ctx, h.value)
+
     @property
     def weight_type(self) -> int:
         return _L.aesir_model_weight_type(self.h)
+
+    def tensor_type(self, name: str) -> int:
+        """GGML type that set_tensor takes for the named tensor."""
+        rc = _L.aesir_model_tensor_type(self.h, name.encode())
+        if rc < 0:
+            raise AesirError(rc, _L.aesir_last_error().decode())
+        return rc
 
     @classmethod
     def load_gguf(cls, ctx: Context, path: str, ctx_len: int = 0) -> "Model":

@@ -251,7 +251,7 @@ int32_t aesir_gemm_quant(aesir_ctx *ctx, const void *A, int64_t a_rows, int64_t 
     } else {
         void *wf = nullptr;
         rc = well_alloc_bytes(ctx, mul_checked(N, K, 2), &wf);
-        if (rc == AESIR_OK) rc = launch_gguf_dequant(ctx->stream, ggml_type, blocks, N, K, wf);
+        if (rc == AESIR_OK) rc = launch_gguf_dequant(ctx->stream, ggml_type, blocks, N, K, wf, K);
         if (rc == AESIR_OK)
             rc = a_rows >= 16 ? launch_gemm_f16_mfma(ctx, A, a_rows, K, wf, N, C) : launch_gemm_f16(ctx, A, a_rows, K, wf, N, C);
     }

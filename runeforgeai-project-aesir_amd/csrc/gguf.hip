@@ -5,10 +5,10 @@
 // (message text included), then _validate_required_tensors. Where the reference aliases F16
 // tensors into the mmap, this loader uploads them once into the model's arena (Q/K/V
 // concatenated, gate/up interleaved); F32 norms are rounded to f16 as the reference does.
-// One extension: a file whose seven matrix kinds all share one block type, Q8_0, Q4_0, Q4_K or
-// Q6_K (GGML types 8, 2, 12, 14), loads as a model of that weight type (the reference loader stops
-// at "Real inference slice supports only F16 and F32 tensors"). Files that mix block types
-// between matrices are refused with "GGUF required tensor has an invalid type".
+// One extension: each matrix may also have a block type, Q8_0, Q4_0, Q4_K or Q6_K (GGML types 8,
+// 2, 12, 14), matrix by matrix (files such as Q4_K_M mix them); the model keeps each matrix in
+// its own type (the reference loader stops at "Real inference slice supports only F16 and F32
+// tensors"). Any other matrix type is refused with "GGUF required tensor has an invalid type".
 #include <fcntl.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
@@ -285,26 +285,23 @@ std::vector<std::string> required_tensors(const Gguf &g) {
     return required;
 }
 
-// Weight type of the matrices: token_embd.weight's type when it is one of the block types this
-// library adds (Q8_0, Q4_0, Q4_K, Q6_K; then every matrix must have it), else F16 as the
-// reference requires.
-uint32_t matrix_type(const Gguf &g) {
-    const GgufTensor &t = g.tensors[g.by_name.at("token_embd.weight")];
-    const bool block = t.type == AESIR_GGML_Q8_0 || t.type == AESIR_GGML_Q4_0 || t.type == AESIR_GGML_Q4_K ||
-                       t.type == AESIR_GGML_Q6_K;
-    return block ? t.type : (uint32_t)AESIR_GGML_F16;
+// Types a matrix may have: F16 as the reference requires, and the block types this library adds
+// (Q8_0, Q4_0, Q4_K, Q6_K), each matrix its own (GGUF files mix them: Q4_K_M and the like).
+bool matrix_type_ok(uint32_t t) {
+    return t == AESIR_GGML_F16 || t == AESIR_GGML_Q8_0 || t == AESIR_GGML_Q4_0 || t == AESIR_GGML_Q4_K ||
+           t == AESIR_GGML_Q6_K;
 }
 
-// Expected (rows, cols, type) of a required tensor (loader/gguf.mojo:597-628).
-void expected_shape(const Gguf &g, const std::string &name, int64_t vocab, int64_t *rows, int64_t *cols, uint32_t *type) {
+// Expected (rows, cols) of a required tensor (loader/gguf.mojo:597-628); *norm for the F32 norms.
+void expected_shape(const Gguf &g, const std::string &name, int64_t vocab, int64_t *rows, int64_t *cols, bool *norm) {
     const int64_t d = g.embedding_length, kvd = d / g.head_count * g.head_count_kv, f = g.feed_forward_length;
     auto ends = [&](const char *suf) {
         const size_t n = std::strlen(suf);
         return name.size() >= n && name.compare(name.size() - n, n, suf) == 0;
     };
-    *type = matrix_type(g);
+    *norm = false;
     if (name == "token_embd.weight" || name == "output.weight") { *rows = vocab; *cols = d; }
-    else if (ends("norm.weight")) { *rows = 1; *cols = d; *type = AESIR_GGML_F32; }
+    else if (ends("norm.weight")) { *rows = 1; *cols = d; *norm = true; }
     else if (ends("attn_q.weight") || ends("attn_output.weight")) { *rows = d; *cols = d; }
     else if (ends("attn_k.weight") || ends("attn_v.weight")) { *rows = kvd; *cols = d; }
     else if (ends("ffn_gate.weight") || ends("ffn_up.weight")) { *rows = f; *cols = d; }
@@ -320,12 +317,28 @@ int32_t validate_required(const Gguf &g) {
     for (auto &r : required) {
         const GgufTensor &t = g.tensors[g.by_name.at(r)];
         int64_t rows, cols;
-        uint32_t type;
-        expected_shape(g, r, vocab, &rows, &cols, &type);
+        bool norm;
+        expected_shape(g, r, vocab, &rows, &cols, &norm);
         if (t.rows != rows || t.cols != cols) return fail(AESIR_ERR_FORMAT, "GGUF required tensor has an invalid shape: %s", r.c_str());
-        if (t.type != type) return fail(AESIR_ERR_FORMAT, "GGUF required tensor has an invalid type: %s", r.c_str());
+        if (norm ? t.type != AESIR_GGML_F32 : !matrix_type_ok(t.type))
+            return fail(AESIR_ERR_FORMAT, "GGUF required tensor has an invalid type: %s", r.c_str());
     }
     return AESIR_OK;
+}
+
+// The matrices' types in aesir_model_create_mixed's order.
+WeightTypes weight_types(const Gguf &g) {
+    auto type = [&](const std::string &n) { return (int32_t)g.tensors[g.by_name.at(n)].type; };
+    WeightTypes t;
+    t.embd = type("token_embd.weight");
+    t.out = type("output.weight");
+    for (int64_t l = 0; l < g.block_count; l++) {
+        const std::string b = "blk." + std::to_string(l) + ".";
+        t.layers.push_back(LayerTypes{type(b + "attn_q.weight"), type(b + "attn_k.weight"), type(b + "attn_v.weight"),
+                                      type(b + "attn_output.weight"), type(b + "ffn_gate.weight"),
+                                      type(b + "ffn_up.weight"), type(b + "ffn_down.weight")});
+    }
+    return t;
 }
 
 void fill_config(const Gguf &g, int64_t ctx_len_override, aesir_model_config *c) {
@@ -368,7 +381,7 @@ extern "C" int32_t aesir_model_load_gguf(aesir_ctx *ctx, const char *path, int64
     aesir_model_config c{};
     fill_config(g, ctx_len_override, &c);
     aesir_model *m = nullptr;
-    AESIR_TRY(aesir_model_create_typed(ctx, &c, (int32_t)matrix_type(g), &m));
+    AESIR_TRY(model_create(ctx, &c, weight_types(g), &m));
     for (auto &r : required) {
         const GgufTensor &t = g.tensors[g.by_name.at(r)];
         TensorRef ref;

@@ -11,6 +11,7 @@
 //              gate_up_swiglu            rmsnorm(x) -> [gate,up] GEMV -> f16(up * silu(gate))
 //              down + residual           x = f16(f16(Wdown act) + x)
 //   lm_head_argmax                       rmsnorm(x) -> logits -> greedy token (-> next step's state)
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <string>
@@ -75,53 +76,57 @@ int32_t parse_tensor_name(const aesir_model *m, const char *name, TensorRef *ref
 // scale + r * scale_stride + c / 32); a 4-bit tensor's row r is plane row row0 + r * step.
 TensorPlace place_tensor(const aesir_model *m, const TensorRef &ref) {
     const int64_t d = m->cfg.dim, kvd = m->kvd, f = m->cfg.ffn, V = m->cfg.vocab;
-    const bool q8 = m->wtype == AESIR_GGML_Q8_0, qf = qf_type(m->wtype);
-    const int es = q8 ? 1 : 2;
     const ModelLayer *L = ref.layer >= 0 ? &m->layers[ref.layer] : nullptr;
-    // matrix rows [r0, r0 + rows) of a fused tensor with `cols` columns, every `step`-th row
-    auto mat = [&](int64_t rows, int64_t cols, void *base, void *scale, void *s1, void *hb, int64_t r0,
-                   int64_t step) {
-        if (qf) {
-            TensorPlace p{rows, cols, base, 0, false, 0, scale, 0};
-            p.qtype = m->wtype;
-            p.s1 = s1;
-            p.hb = hb;
+    const LayerTypes *T = ref.layer >= 0 ? &m->types.layers[ref.layer] : nullptr;
+    // matrix rows [r0, r0 + rows) of a fused matrix w with `cols` columns, every `step`-th row,
+    // uploaded as in_type
+    auto mat = [&](int64_t rows, int64_t cols, const WMat &w, int64_t r0, int64_t step, int32_t in_type) {
+        if (qf_type(w.type)) {
+            TensorPlace p{rows, cols, w.w, 0, false, 0, w.s0, 0};
+            p.qtype = w.type;
+            p.s1 = w.s1;
+            p.hb = w.hb;
             p.step = step;
             p.row0 = r0;
+            p.in_type = in_type;
             return p;
         }
-        TensorPlace p{rows, cols, (char *)base + r0 * cols * es, step * cols, false, es, nullptr, 0};
+        const bool q8 = w.type == AESIR_GGML_Q8_0;
+        const int es = q8 ? 1 : 2;
+        TensorPlace p{rows, cols, (char *)w.w + r0 * cols * es, step * cols, false, es, nullptr, 0};
+        p.qtype = w.type;
+        p.in_type = in_type;
         if (q8) {
-            p.scale = (uint16_t *)scale + r0 * (cols / 32);
+            p.scale = (uint16_t *)w.s0 + r0 * (cols / 32);
             p.scale_stride = step * (cols / 32);
         }
         return p;
     };
     auto norm = [&](void *base) { return TensorPlace{1, d, base, d, true, 2, nullptr, 0}; };
     switch (ref.kind) {
-        case TensorKind::TokenEmbd: return mat(V, d, m->tok_embd, m->tok_embd_s, m->tok_embd_s1, m->tok_embd_hb, 0, 1);
+        case TensorKind::TokenEmbd: return mat(V, d, m->embd, 0, 1, m->types.embd);
         case TensorKind::OutputNorm: return norm(m->out_norm);
-        case TensorKind::Output: return mat(V, d, m->out_w, m->out_w_s, m->out_w_s1, m->out_w_hb, 0, 1);
+        case TensorKind::Output: return mat(V, d, m->out, 0, 1, m->types.out);
         case TensorKind::AttnNorm: return norm(L->attn_norm);
-        case TensorKind::AttnQ: return mat(d, d, L->wqkv, L->sqkv, L->qkv_s1, L->qkv_hb, 0, 1);
-        case TensorKind::AttnK: return mat(kvd, d, L->wqkv, L->sqkv, L->qkv_s1, L->qkv_hb, d, 1);
-        case TensorKind::AttnV: return mat(kvd, d, L->wqkv, L->sqkv, L->qkv_s1, L->qkv_hb, d + kvd, 1);
-        case TensorKind::AttnOut: return mat(d, d, L->wo, L->so, L->o_s1, L->o_hb, 0, 1);
+        case TensorKind::AttnQ: return mat(d, d, L->qkv, 0, 1, T->q);
+        case TensorKind::AttnK: return mat(kvd, d, L->qkv, d, 1, T->k);
+        case TensorKind::AttnV: return mat(kvd, d, L->qkv, d + kvd, 1, T->v);
+        case TensorKind::AttnOut: return mat(d, d, L->o, 0, 1, T->o);
         case TensorKind::FfnNorm: return norm(L->ffn_norm);
-        case TensorKind::FfnGate: return mat(f, d, L->wgu, L->sgu, L->gu_s1, L->gu_hb, 0, 2);  // gate i -> fused row 2i
-        case TensorKind::FfnUp: return mat(f, d, L->wgu, L->sgu, L->gu_s1, L->gu_hb, 1, 2);    // up i -> fused row 2i + 1
-        case TensorKind::FfnDown: return mat(d, f, L->wdown, L->sdown, L->down_s1, L->down_hb, 0, 1);
+        case TensorKind::FfnGate: return mat(f, d, L->gu, 0, 2, T->gate);  // gate i -> fused row 2i
+        case TensorKind::FfnUp: return mat(f, d, L->gu, 1, 2, T->up);      // up i -> fused row 2i + 1
+        case TensorKind::FfnDown: return mat(d, f, L->down, 0, 1, T->down);
     }
     return TensorPlace{};
 }
 
-QFMat model_qf(const aesir_model *m, const void *w, const void *s0, const void *s1, const void *hb) {
+QFMat wmat_qf(const WMat &w) {
     QFMat q;
-    q.type = m->wtype;
-    q.nib = w;
-    q.s0 = s0;
-    q.s1 = s1;
-    q.hb = hb;
+    q.type = w.type;
+    q.nib = w.w;
+    q.s0 = w.s0;
+    q.s1 = w.s1;
+    q.hb = w.hb;
     return q;
 }
 
@@ -187,9 +192,24 @@ int32_t model_upload(aesir_model *m, const TensorRef &ref, const void *host, int
     if (rows != p.rows || cols != p.cols)
         return fail(AESIR_ERR_FORMAT, "GGUF required tensor has an invalid shape: %s", nm.c_str());
     hipStream_t s = m->ctx->stream;
+    if (!p.is_norm && type != p.in_type)
+        return fail(AESIR_ERR_FORMAT, "GGUF required tensor has an invalid type: %s", nm.c_str());
+    if (p.esize == 2 && !p.is_norm && type != AESIR_GGML_F16) {
+        // a quantized part of an f16-stored fused matrix: its f16 weights, dequantized on the device
+        const int64_t bytes = ggml_tensor_bytes(type, rows, cols);
+        if (bytes <= 0) return fail(AESIR_ERR_FORMAT, "GGUF required tensor has an invalid shape: %s", nm.c_str());
+        void *staging = nullptr;
+        AESIR_HIP_TRY(hipMalloc(&staging, (size_t)bytes));
+        int32_t rc = AESIR_OK;
+        if (hipMemcpyAsync(staging, host, (size_t)bytes, hipMemcpyHostToDevice, s) != hipSuccess)
+            rc = fail(AESIR_ERR_HIP, "hipMemcpyAsync of %s failed", nm.c_str());
+        if (rc == AESIR_OK) rc = launch_gguf_dequant(s, type, staging, rows, cols, p.base, p.row_stride);
+        if (hipStreamSynchronize(s) != hipSuccess && rc == AESIR_OK)
+            rc = fail(AESIR_ERR_HIP, "dequantization of %s failed", nm.c_str());
+        (void)hipFree(staging);
+        return rc;
+    }
     if (p.esize == 0) {  // Q4_0 / Q4_K / Q6_K matrix: repack the GGUF blocks on the device
-        if (type != p.qtype)
-            return fail(AESIR_ERR_FORMAT, "GGUF required tensor has an invalid type: %s", nm.c_str());
         const int64_t bytes = ggml_tensor_bytes(type, rows, cols);
         if (bytes <= 0) return fail(AESIR_ERR_FORMAT, "GGUF required tensor has an invalid shape: %s", nm.c_str());
         void *staging = nullptr;
@@ -203,8 +223,6 @@ int32_t model_upload(aesir_model *m, const TensorRef &ref, const void *host, int
         return rc;
     }
     if (p.esize == 1) {  // Q8_0 matrix: split the 34-byte blocks into quants and scales
-        if (type != AESIR_GGML_Q8_0)
-            return fail(AESIR_ERR_FORMAT, "GGUF required tensor has an invalid type: %s", nm.c_str());
         const int64_t nb = cols / 32;
         std::vector<int8_t> qs((size_t)(rows * cols));
         std::vector<uint16_t> ds((size_t)(rows * nb));
@@ -238,38 +256,47 @@ int32_t model_upload(aesir_model *m, const TensorRef &ref, const void *host, int
 
 // ------------------------------------------------------------------ decode step
 
+// The layer-0 QKV GEMV performs the embedding lookup when the table has the QKV matrix's type;
+// otherwise the decode step looks the row up first (embed_lookup).
+static bool embd_fused(const aesir_model *m) { return m->embd.type == m->layers[0].qkv.type; }
+
 static QkvArgs qkv_args(aesir_model *m, int64_t l) {
     const aesir_model_config &c = m->cfg;
     const ModelLayer &L = m->layers[l];
-    QkvArgs a{m->x, l == 0 ? m->tok_embd : nullptr, L.attn_norm, c.rms_eps, L.wqkv, c.dim, m->kvd, m->hd, m->q,
+    const bool emb = l == 0 && embd_fused(m);
+    QkvArgs a{m->x, emb ? m->embd.w : nullptr, L.attn_norm, c.rms_eps, L.qkv.w, c.dim, m->kvd, m->hd, m->q,
               (uint16_t *)m->k_cache + l * c.ctx_len * m->kvd, (uint16_t *)m->v_cache + l * c.ctx_len * m->kvd,
-              c.ctx_len, m->rope, m->state, L.sqkv, l == 0 ? m->tok_embd_s : nullptr};
-    if (qf_type(m->wtype)) {
-        a.wq = model_qf(m, L.wqkv, L.sqkv, L.qkv_s1, L.qkv_hb);
-        if (l == 0) a.eq = model_qf(m, m->tok_embd, m->tok_embd_s, m->tok_embd_s1, m->tok_embd_hb);
+              c.ctx_len, m->rope, m->state, L.qkv.type == AESIR_GGML_Q8_0 ? L.qkv.s0 : nullptr,
+              emb && m->embd.type == AESIR_GGML_Q8_0 ? m->embd.s0 : nullptr};
+    if (qf_type(L.qkv.type)) {
+        a.wq = wmat_qf(L.qkv);
+        if (emb) a.eq = wmat_qf(m->embd);
     }
     return a;
 }
 
+static int32_t embed_lookup(aesir_model *m, hipStream_t s) {
+    return launch_embed_rows(s, m->embd, m->cfg.dim, &m->state->token, 1, m->x);
+}
+
 // O and down projections with the residual add, and the gate/up GEMV with SwiGLU, for every
 // weight type.
+static const void *q8_scales(const WMat &w) { return w.type == AESIR_GGML_Q8_0 ? w.s0 : nullptr; }
 static int32_t launch_o_residual(aesir_model *m, hipStream_t s, const ModelLayer &L) {
     const int64_t d = m->cfg.dim;
-    if (qf_type(m->wtype)) return launch_qf_gemv_residual(s, model_qf(m, L.wo, L.so, L.o_s1, L.o_hb), d, d, m->attn, m->x);
-    return launch_gemv_residual(s, L.wo, d, d, m->attn, m->x, L.so);
+    if (qf_type(L.o.type)) return launch_qf_gemv_residual(s, wmat_qf(L.o), d, d, m->attn, m->x);
+    return launch_gemv_residual(s, L.o.w, d, d, m->attn, m->x, q8_scales(L.o));
 }
 static int32_t launch_down_residual(aesir_model *m, hipStream_t s, const ModelLayer &L) {
     const int64_t d = m->cfg.dim, f = m->cfg.ffn;
-    if (qf_type(m->wtype))
-        return launch_qf_gemv_residual(s, model_qf(m, L.wdown, L.sdown, L.down_s1, L.down_hb), d, f, m->act, m->x);
-    return launch_gemv_residual(s, L.wdown, d, f, m->act, m->x, L.sdown);
+    if (qf_type(L.down.type)) return launch_qf_gemv_residual(s, wmat_qf(L.down), d, f, m->act, m->x);
+    return launch_gemv_residual(s, L.down.w, d, f, m->act, m->x, q8_scales(L.down));
 }
 static int32_t launch_gate_up(aesir_model *m, hipStream_t s, const ModelLayer &L) {
     const aesir_model_config &c = m->cfg;
-    if (qf_type(m->wtype))
-        return launch_qf_gate_up_swiglu(s, m->x, L.ffn_norm, c.rms_eps, model_qf(m, L.wgu, L.sgu, L.gu_s1, L.gu_hb), c.ffn,
-                                        c.dim, m->act);
-    return launch_gate_up_swiglu(s, m->x, L.ffn_norm, c.rms_eps, L.wgu, c.ffn, c.dim, m->act, L.sgu);
+    if (qf_type(L.gu.type))
+        return launch_qf_gate_up_swiglu(s, m->x, L.ffn_norm, c.rms_eps, wmat_qf(L.gu), c.ffn, c.dim, m->act);
+    return launch_gate_up_swiglu(s, m->x, L.ffn_norm, c.rms_eps, L.gu.w, c.ffn, c.dim, m->act, q8_scales(L.gu));
 }
 
 static AttnArgs attn_args(aesir_model *m, int64_t l) {
@@ -295,18 +322,19 @@ static AttnArgs attn_args(aesir_model *m, int64_t l) {
 
 LmHeadArgs lm_args(aesir_model *m, bool with_ring) {
     const aesir_model_config &c = m->cfg;
-    LmHeadArgs a{m->x, m->out_norm, m->out_eps, m->out_w, c.vocab, c.dim, m->logits, m->lm_parts, m->state,
-                 with_ring ? m->ring : nullptr, m->out_w_s};
-    if (qf_type(m->wtype)) a.wq = model_qf(m, m->out_w, m->out_w_s, m->out_w_s1, m->out_w_hb);
+    LmHeadArgs a{m->x, m->out_norm, m->out_eps, m->out.w, c.vocab, c.dim, m->logits, m->lm_parts, m->state,
+                 with_ring ? m->ring : nullptr, q8_scales(m->out)};
+    if (qf_type(m->out.type)) a.wq = wmat_qf(m->out);
     return a;
 }
 
 static int32_t enqueue_step(aesir_model *m, hipStream_t s) {
     const aesir_model_config &c = m->cfg;
     const int64_t d = c.dim;
+    if (!embd_fused(m)) AESIR_TRY(embed_lookup(m, s));
     for (int64_t l = 0; l < c.n_layers; l++) {
         const ModelLayer &L = m->layers[l];
-        AESIR_TRY(launch_qkv_rope_kv(s, qkv_args(m, l)));  // layer 0 also performs the embedding lookup
+        AESIR_TRY(launch_qkv_rope_kv(s, qkv_args(m, l)));  // layer 0 may also perform the embedding lookup
         AESIR_TRY(launch_attention_decode(s, attn_args(m, l)));
         AESIR_TRY(launch_o_residual(m, s, L));
         AESIR_TRY(launch_gate_up(m, s, L));
@@ -397,10 +425,44 @@ int32_t aesir_model_weight_type(const aesir_model *m) { return m ? m->wtype : -1
 
 int32_t aesir_model_create_typed(aesir_ctx *ctx, const aesir_model_config *cfg, int32_t weight_type,
                                  aesir_model **out) {
+    WeightTypes t;
+    t.embd = t.out = weight_type;
+    if (cfg && cfg->n_layers > 0 && cfg->n_layers <= ((int64_t)1 << 31))
+        t.layers.assign((size_t)cfg->n_layers, LayerTypes{weight_type, weight_type, weight_type, weight_type,
+                                                          weight_type, weight_type, weight_type});
+    return model_create(ctx, cfg, t, out);
+}
+
+int32_t aesir_model_create_mixed(aesir_ctx *ctx, const aesir_model_config *cfg, const int32_t *tensor_types,
+                                 int64_t n_types, aesir_model **out) {
+    if (!cfg || !tensor_types || !out) return fail(AESIR_ERR_INVALID, "aesir_model_create_mixed: null argument");
+    if (cfg->n_layers <= 0 || cfg->n_layers > ((int64_t)1 << 31) || n_types != 2 + 7 * cfg->n_layers)
+        return fail(AESIR_ERR_INVALID, "aesir_model_create_mixed: need 2 + 7 * n_layers tensor types");
+    WeightTypes t;
+    t.embd = tensor_types[0];
+    t.out = tensor_types[1];
+    t.layers.resize((size_t)cfg->n_layers);
+    for (int64_t l = 0; l < cfg->n_layers; l++) {
+        const int32_t *v = tensor_types + 2 + 7 * l;
+        t.layers[l] = LayerTypes{v[0], v[1], v[2], v[3], v[4], v[5], v[6]};
+    }
+    return model_create(ctx, cfg, t, out);
+}
+
+int32_t aesir_model_tensor_type(aesir_model *m, const char *name) {
+    if (!m || !name) return fail(AESIR_ERR_INVALID, "aesir_model_tensor_type: null argument");
+    TensorRef ref;
+    AESIR_TRY(parse_tensor_name(m, name, &ref));
+    return place_tensor(m, ref).in_type;
+}
+
+}  // extern "C"
+
+namespace aesir {
+
+int32_t model_create(aesir_ctx *ctx, const aesir_model_config *cfg, const WeightTypes &types, aesir_model **out) {
     AESIR_TRY(bind(ctx));
     if (!cfg || !out) return fail(AESIR_ERR_INVALID, "aesir_model_create: null argument");
-    if (weight_type != AESIR_GGML_F16 && weight_type != AESIR_GGML_Q8_0 && !qf_type(weight_type))
-        return fail(AESIR_ERR_UNSUPPORTED, "model: weight type %d is not F16, Q8_0, Q4_0, Q4_K or Q6_K", (int)weight_type);
     *out = nullptr;
     const aesir_model_config c = *cfg;
     // GGUFModelConfig.validate (loader/gguf.mojo:133-149)
@@ -419,22 +481,35 @@ int32_t aesir_model_create_typed(aesir_ctx *ctx, const aesir_model_config *cfg, 
     if (hd % 2 != 0) return fail(AESIR_ERR_INVALID, "apply_rope: head_dim must be positive and even");
     if (hd > 256 || c.n_heads / c.n_kv_heads > 16)
         return fail(AESIR_ERR_UNSUPPORTED, "model: head_dim <= 256 and <= 16 query heads per KV head are supported");
-    const bool q8 = weight_type == AESIR_GGML_Q8_0, qf = qf_type(weight_type);
-    if (q8 && (c.dim % 32 != 0 || c.ffn % 32 != 0 || c.dim > 16384 || c.ffn > 16384))
-        return fail(AESIR_ERR_UNSUPPORTED, "model: Q8_0 weights need dim and ffn to be multiples of 32, at most 16384");
-    if (qf) {
-        // whole 128-weight segments of the repacked planes; K-quant super-blocks of 256
-        const int64_t blk = weight_type == AESIR_GGML_Q4_0 ? 128 : 256;
-        if (c.dim % blk != 0 || c.ffn % blk != 0 || c.dim > kQfGemvMaxK || c.ffn > kQfGemvMaxK)
-            return fail(AESIR_ERR_UNSUPPORTED, "model: %s weights need dim and ffn to be multiples of %lld, at most 28672",
-                        weight_type == AESIR_GGML_Q4_0 ? "Q4_0" : weight_type == AESIR_GGML_Q4_K ? "Q4_K" : "Q6_K",
-                        (long long)blk);
+    if ((int64_t)types.layers.size() != c.n_layers)
+        return fail(AESIR_ERR_INVALID, "model: one set of weight types per layer is needed");
+    // every matrix type present, each checked once against dim and ffn
+    std::vector<int32_t> present{types.embd, types.out};
+    for (const LayerTypes &t : types.layers)
+        for (int32_t v : {t.q, t.k, t.v, t.o, t.gate, t.up, t.down}) present.push_back(v);
+    std::sort(present.begin(), present.end());
+    present.erase(std::unique(present.begin(), present.end()), present.end());
+    for (int32_t wt : present) {
+        if (wt != AESIR_GGML_F16 && wt != AESIR_GGML_Q8_0 && !qf_type(wt))
+            return fail(AESIR_ERR_UNSUPPORTED, "model: weight type %d is not F16, Q8_0, Q4_0, Q4_K or Q6_K", (int)wt);
+        if (wt == AESIR_GGML_Q8_0 && (c.dim % 32 != 0 || c.ffn % 32 != 0 || c.dim > 16384 || c.ffn > 16384))
+            return fail(AESIR_ERR_UNSUPPORTED, "model: Q8_0 weights need dim and ffn to be multiples of 32, at most 16384");
+        if (qf_type(wt)) {
+            // whole 128-weight segments of the repacked planes; K-quant super-blocks of 256
+            const int64_t blk = wt == AESIR_GGML_Q4_0 ? 128 : 256;
+            if (c.dim % blk != 0 || c.ffn % blk != 0 || c.dim > kQfGemvMaxK || c.ffn > kQfGemvMaxK)
+                return fail(AESIR_ERR_UNSUPPORTED,
+                            "model: %s weights need dim and ffn to be multiples of %lld, at most 28672",
+                            wt == AESIR_GGML_Q4_0 ? "Q4_0" : wt == AESIR_GGML_Q4_K ? "Q4_K" : "Q6_K", (long long)blk);
+        }
     }
 
     auto *m = new aesir_model();
     m->ctx = ctx;
     m->cfg = c;
-    m->wtype = weight_type;
+    m->types = types;
+    // the stored model type: the matrices' common type, else AESIR_WEIGHT_MIXED
+    m->wtype = present.size() == 1 ? present[0] : AESIR_WEIGHT_MIXED;
     m->hd = hd;
     m->kvd = hd * c.n_kv_heads;
     m->attn_scale = (float)(1.0 / std::pow((double)hd, 0.5));  // compute.mojo:1968
@@ -453,32 +528,49 @@ int32_t aesir_model_create_typed(aesir_ctx *ctx, const aesir_model_config *cfg, 
         if (rc == AESIR_OK && bytes < 0) rc = fail(AESIR_ERR_FORMAT, "model: a tensor size overflows int64");
         if (rc == AESIR_OK) rc = carve(ctx, bytes, p);
     };
-    // a matrix of rows x cols: f16, int8 quants plus f16 block scales (Q8_0), or the record
-    // planes of a 4-bit type (nibbles, then s0, s1 and hb where the type has them)
-    auto matrix = [&](int64_t rows, int64_t cols, void **w, void **scale, void **s1, void **hb) {
-        if (qf) {
+    // a matrix of rows x cols stored as `type`: f16, int8 quants plus f16 block scales (Q8_0), or
+    // the record planes of a 4-bit type (nibbles, then s0, s1 and hb where the type has them)
+    bool any_qf = false;
+    auto matrix = [&](int64_t rows, int64_t cols, int32_t type, WMat *w) {
+        w->type = type;
+        if (qf_type(type)) {
+            any_qf = true;
             for (int plane = 0; plane < 4; plane++) {
-                const int64_t rb = qf_plane_row_bytes(weight_type, plane, cols);
-                if (rb > 0) take(mul_checked(qf_rows_alloc(rows), rb), plane == 0 ? w : plane == 1 ? hb : plane == 2 ? scale : s1);
+                const int64_t rb = qf_plane_row_bytes(type, plane, cols);
+                if (rb > 0)
+                    take(mul_checked(qf_rows_alloc(rows), rb), plane == 0 ? &w->w : plane == 1 ? &w->hb : plane == 2 ? &w->s0 : &w->s1);
             }
             return;
         }
-        take(mul_checked(rows, cols, q8 ? 1 : 2), w);
-        if (q8) take(mul_checked(rows, cols / 32, 2), scale);
+        const bool q8 = type == AESIR_GGML_Q8_0;
+        take(mul_checked(rows, cols, q8 ? 1 : 2), &w->w);
+        if (q8) take(mul_checked(rows, cols / 32, 2), &w->s0);
     };
-    matrix(V, d, &m->tok_embd, &m->tok_embd_s, &m->tok_embd_s1, &m->tok_embd_hb);
+    // A fused matrix whose parts differ in type is stored in f16 (each part dequantized at upload).
+    auto fused = [](std::initializer_list<int32_t> parts) {
+        const int32_t t0 = *parts.begin();
+        for (int32_t t : parts)
+            if (t != t0) return (int32_t)AESIR_GGML_F16;
+        return t0;
+    };
+    matrix(V, d, types.embd, &m->embd);
     take(d * 2, &m->out_norm);
-    matrix(V, d, &m->out_w, &m->out_w_s, &m->out_w_s1, &m->out_w_hb);
+    matrix(V, d, types.out, &m->out);
     m->layers.resize((size_t)c.n_layers);
-    for (auto &L : m->layers) {
+    for (int64_t l = 0; l < c.n_layers; l++) {
+        ModelLayer &L = m->layers[l];
+        const LayerTypes &t = types.layers[l];
         take(d * 2, &L.attn_norm);
-        matrix(d + 2 * kvd, d, &L.wqkv, &L.sqkv, &L.qkv_s1, &L.qkv_hb);
-        matrix(d, d, &L.wo, &L.so, &L.o_s1, &L.o_hb);
+        matrix(d + 2 * kvd, d, fused({t.q, t.k, t.v}), &L.qkv);
+        matrix(d, d, t.o, &L.o);
         take(d * 2, &L.ffn_norm);
-        matrix(2 * f, d, &L.wgu, &L.sgu, &L.gu_s1, &L.gu_hb);
-        matrix(d, f, &L.wdown, &L.sdown, &L.down_s1, &L.down_hb);
+        matrix(2 * f, d, fused({t.gate, t.up}), &L.gu);
+        matrix(d, f, t.down, &L.down);
     }
-    if (qf) {  // f16 copy of the largest layer matrix for the prefill GEMMs
+    m->all_f16 = m->embd.type == AESIR_GGML_F16 && m->out.type == AESIR_GGML_F16;
+    for (const ModelLayer &L : m->layers)
+        for (const WMat *w : {&L.qkv, &L.o, &L.gu, &L.down}) m->all_f16 = m->all_f16 && w->type == AESIR_GGML_F16;
+    if (any_qf) {  // f16 copy of the largest layer matrix for the prefill GEMMs
         int64_t big = (d + 2 * kvd) * d;
         if (2 * f * d > big) big = 2 * f * d;
         take(mul_checked(big, 2), &m->pf_wdeq);
@@ -531,6 +623,10 @@ int32_t aesir_model_create_typed(aesir_ctx *ctx, const aesir_model_config *cfg, 
     *out = m;
     return AESIR_OK;
 }
+
+}  // namespace aesir
+
+extern "C" {
 
 int32_t aesir_model_destroy(aesir_model *m) {
     if (!m) return AESIR_OK;

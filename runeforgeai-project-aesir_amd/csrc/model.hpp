@@ -9,23 +9,35 @@
 
 namespace aesir {
 
+// One device matrix: f16 [rows][cols] (F16); int8 quants [rows][cols] plus f16 block scales
+// [rows][cols / 32] in s0 (Q8_0); or the tiled record planes of a 4-bit type (Q4_0 / Q4_K /
+// Q6_K: w the nibble plane, s0, s1 and hb as QFMat describes them, null where the type has none).
+struct WMat {
+    int32_t type = AESIR_GGML_F16;
+    void *w = nullptr, *s0 = nullptr, *s1 = nullptr, *hb = nullptr;
+};
+
 // Per-layer device tensors. Q, K and V rows are concatenated ([dim + 2 kvd][dim]) so one GEMV
 // produces q|k|v; gate and up rows are interleaved (row 2i = gate i, row 2i+1 = up i) so the
 // SwiGLU pair of an output lands in one workgroup.
-// Q8_0 models store every matrix as int8 quants in the same row order plus f16 block scales
-// [rows][cols / 32] (the s* pointers; null for F16 models).
 struct ModelLayer {
     void *attn_norm = nullptr;  // [dim]
-    void *wqkv = nullptr;       // [dim + 2 kvd][dim]
-    void *wo = nullptr;         // [dim][dim]
     void *ffn_norm = nullptr;   // [dim]
-    void *wgu = nullptr;        // [2 ffn][dim]
-    void *wdown = nullptr;      // [dim][ffn]
-    void *sqkv = nullptr, *so = nullptr, *sgu = nullptr, *sdown = nullptr;
-    // Q4_0 / Q4_K / Q6_K models: w* hold the nibble records and s* the s0 planes (QFMat); the
-    // s1 and hb planes are here (null where the type has none)
-    void *qkv_s1 = nullptr, *qkv_hb = nullptr, *o_s1 = nullptr, *o_hb = nullptr;
-    void *gu_s1 = nullptr, *gu_hb = nullptr, *down_s1 = nullptr, *down_hb = nullptr;
+    WMat qkv;                   // [dim + 2 kvd][dim]
+    WMat o;                     // [dim][dim]
+    WMat gu;                    // [2 ffn][dim]
+    WMat down;                  // [dim][ffn]
+};
+
+// GGML types of the model's matrices as the caller uploads them (one per GGUF tensor). A fused
+// matrix whose parts differ (Q, K, V; gate, up) is stored as f16, its parts dequantized at upload
+// to the f16 weights their own type defines, which are the values every path multiplies.
+struct LayerTypes {
+    int32_t q, k, v, o, gate, up, down;
+};
+struct WeightTypes {
+    int32_t embd = AESIR_GGML_F16, out = AESIR_GGML_F16;
+    std::vector<LayerTypes> layers;
 };
 
 enum class TensorKind : int {
@@ -52,6 +64,8 @@ struct TensorRef {
 // esize bytes: 2 for f16, 1 for Q8_0 quants); a Q8_0 matrix's block scale (r, c / 32) at
 // scale + r * scale_stride + c / 32 (f16). For Q4_0 / Q4_K / Q6_K matrices (esize 0), row r of
 // the tensor is plane row row0 + r * step of the QFMat {qtype, base, hb, scale, s1, row0}.
+// in_type is the GGML type the tensor is uploaded as (a quantized part of an f16-stored fused
+// matrix is dequantized into it).
 struct TensorPlace {
     int64_t rows, cols;
     void *base;
@@ -64,6 +78,7 @@ struct TensorPlace {
     void *s1 = nullptr, *hb = nullptr;
     int64_t step = 1;
     int64_t row0 = 0;  // 4-bit types: plane row of the tensor's row 0
+    int32_t in_type = AESIR_GGML_F16;
 };
 
 }  // namespace aesir
@@ -74,10 +89,13 @@ struct aesir_model {
     int64_t hd = 0, kvd = 0;
     float attn_scale = 0.0f, out_eps = 1e-5f;
     int64_t well_start = 0;
-    int32_t wtype = AESIR_GGML_F16;  // matrices: AESIR_GGML_F16 or AESIR_GGML_Q8_0
-    void *tok_embd = nullptr, *out_norm = nullptr, *out_w = nullptr;
-    void *tok_embd_s = nullptr, *out_w_s = nullptr;  // Q8_0 block scales; s0 planes of 4-bit types
-    void *tok_embd_s1 = nullptr, *tok_embd_hb = nullptr, *out_w_s1 = nullptr, *out_w_hb = nullptr;
+    // the model's weight type (aesir_model_weight_type): the type of every matrix, or
+    // AESIR_WEIGHT_MIXED for a model whose matrices differ
+    int32_t wtype = AESIR_GGML_F16;
+    aesir::WeightTypes types;  // per GGUF tensor
+    bool all_f16 = true;       // every matrix stored as f16
+    aesir::WMat embd, out;     // token_embd [vocab][dim], output [vocab][dim]
+    void *out_norm = nullptr;
     void *pf_wdeq = nullptr;  // 4-bit types: f16 copy of the matrix a prefill GEMM is reading
     std::vector<aesir::ModelLayer> layers;
     void *k_cache = nullptr, *v_cache = nullptr;  // [n_layers][ctx_len][kvd]
@@ -110,8 +128,13 @@ TensorPlace place_tensor(const aesir_model *m, const TensorRef &ref);
 std::vector<TensorRef> all_tensors(const aesir_model *m);
 std::string tensor_name(const TensorRef &ref);
 int32_t model_upload(aesir_model *m, const TensorRef &ref, const void *host, int64_t rows, int64_t cols, int32_t type);
-// QFMat of one matrix of a Q4_0 / Q4_K / Q6_K model.
-QFMat model_qf(const aesir_model *m, const void *w, const void *s0, const void *s1, const void *hb);
+// Creates a model whose GGUF tensors have the given types (every matrix type one of F16, Q8_0,
+// Q4_0, Q4_K, Q6_K).
+int32_t model_create(aesir_ctx *ctx, const aesir_model_config *cfg, const WeightTypes &types, aesir_model **out);
+// QFMat of a matrix stored as a Q4_0 / Q4_K / Q6_K type.
+QFMat wmat_qf(const WMat &w);
+// X[r] = the f16 embedding row tokens[r] of `e` (any matrix type), r < n (tokens on the device).
+int32_t launch_embed_rows(hipStream_t s, const WMat &e, int64_t dim, const int64_t *tokens, int64_t n, void *X);
 // Batched prefill of tokens[0..n) at positions start_pos.., in chunks of pf_rows rows; *next is the
 // greedy token after the last position.
 int32_t model_prefill(aesir_model *m, const int64_t *tokens, int64_t n, int64_t start_pos, int64_t *next);

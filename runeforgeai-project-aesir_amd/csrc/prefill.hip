@@ -625,6 +625,19 @@ __global__ __launch_bounds__(kPThreads) void embed_rows_kernel(const h16 *__rest
     for (int64_t c = threadIdx.x; c < dim; c += kPThreads) dst[c] = src[c];
 }
 
+int32_t launch_embed_rows(hipStream_t s, const WMat &e, int64_t dim, const int64_t *tokens, int64_t n, void *X) {
+    if (n <= 0) return AESIR_OK;
+    if (qf_type(e.type)) return launch_qf_dequant(s, wmat_qf(e), n, dim, 1, tokens, X, dim);
+    if (e.type == AESIR_GGML_Q8_0)
+        hipLaunchKernelGGL(embed_rows_q8_kernel, dim3((unsigned)n), dim3(kPThreads), 0, s, (const int8_t *)e.w,
+                           (const h16 *)e.s0, dim, tokens, (h16 *)X);
+    else
+        hipLaunchKernelGGL(embed_rows_kernel, dim3((unsigned)n), dim3(kPThreads), 0, s, (const h16 *)e.w, dim, tokens,
+                           (h16 *)X);
+    AESIR_LAUNCH_CHECK("embed_rows_kernel");
+    return AESIR_OK;
+}
+
 // Row r of QKV [M][dim + 2 kvd] at position p0 + r: RoPE on its Q and K pairs (apply_rope,
 // compute.mojo:2232-2244, cos/sin from the host-built table) into Q [M][dim] and the K cache slot,
 // V copied to the V cache slot (KVCache.append at pos % max_seq, mimir_well.mojo:488-501).
@@ -957,7 +970,7 @@ static int32_t launch_swiglu_pairs(hipStream_t s, const void *gu, void *act, int
 
 // ------------------------------------------------------------------ the batched pass
 
-static const void *L0(const aesir_model *m) { return m->layers[0].wqkv; }
+static const void *L0(const aesir_model *m) { return m->layers[0].qkv.w; }
 
 // Every GEMM of a layer runs on the matrix cores when all four shapes qualify (arena buffers and
 // weights are 256-byte aligned).
@@ -977,32 +990,21 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
     h16 *X = (h16 *)m->pf_x, *Xn = (h16 *)m->pf_xn, *QKV = (h16 *)m->pf_qkv, *Q = (h16 *)m->pf_q;
     h16 *ATT = (h16 *)m->pf_att, *ACT = (h16 *)m->pf_act;
     AESIR_HIP_TRY(hipMemcpyAsync(m->pf_tokens, tokens_host, (size_t)n * sizeof(int64_t), hipMemcpyHostToDevice, s));
-    const bool qf = qf_type(m->wtype);
-    if (qf)
-        AESIR_TRY(launch_qf_dequant(s, model_qf(m, m->tok_embd, m->tok_embd_s, m->tok_embd_s1, m->tok_embd_hb), n, d, 1,
-                                    (const int64_t *)m->pf_tokens, X, d));
-    else if (m->tok_embd_s)
-        hipLaunchKernelGGL(embed_rows_q8_kernel, dim3((unsigned)n), dim3(kPThreads), 0, s, (const int8_t *)m->tok_embd,
-                           (const h16 *)m->tok_embd_s, d, (const int64_t *)m->pf_tokens, X);
-    else
-        hipLaunchKernelGGL(embed_rows_kernel, dim3((unsigned)n), dim3(kPThreads), 0, s, (const h16 *)m->tok_embd, d,
-                           (const int64_t *)m->pf_tokens, X);
-    AESIR_LAUNCH_CHECK("embed_rows_kernel");
+    AESIR_TRY(launch_embed_rows(s, m->embd, d, (const int64_t *)m->pf_tokens, n, X));
     const bool mfma = prefill_mfma_ok(m);
-    if (!mfma && m->wtype != AESIR_GGML_F16)
+    if (!mfma && !m->all_f16)
         return fail(AESIR_ERR_UNSUPPORTED, "prefill: quantized weights need the MFMA GEMM shapes (K %% 64 == 0)");
     // 4-bit types: each GEMM reads an f16 copy of its matrix, dequantized just before it (the
     // prefill is not bound by weight bytes at 128 rows; the decode GEMVs read the records)
     struct W {
         const void *w, *s;
     };
-    auto wmat = [&](const void *w, const void *s0, const void *s1, const void *hb, int64_t rows, int64_t K,
-                    W *out) -> int32_t {
-        if (!qf) {
-            *out = W{w, s0};
+    auto wmat = [&](const WMat &w, int64_t rows, int64_t K, W *out) -> int32_t {
+        if (!qf_type(w.type)) {
+            *out = W{w.w, w.type == AESIR_GGML_Q8_0 ? w.s0 : nullptr};
             return AESIR_OK;
         }
-        AESIR_TRY(launch_qf_dequant(s, model_qf(m, w, s0, s1, hb), rows, K, 1, nullptr, m->pf_wdeq, K));
+        AESIR_TRY(launch_qf_dequant(s, wmat_qf(w), rows, K, 1, nullptr, m->pf_wdeq, K));
         *out = W{m->pf_wdeq, nullptr};
         return AESIR_OK;
     };
@@ -1049,12 +1051,12 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
         xn_ready = false;
         int64_t qkv_splits = 1;
         W wq;
-        AESIR_TRY(wmat(L.wqkv, L.sqkv, L.qkv_s1, L.qkv_hb, qkv_n, d, &wq));
+        AESIR_TRY(wmat(L.qkv, qkv_n, d, &wq));
         if (mfma)
             AESIR_TRY(launch_mfma<kEpiStore>(s, Xn, n, d, wq.w, qkv_n, QKV, qkv_n, m->pf_part, m->pf_part_floats,
                                              "gemm_mfma_qkv", true, &qkv_splits, wq.s));
         else
-            AESIR_TRY(launch_gemm_f16(m->ctx, Xn, n, d, L.wqkv, qkv_n, QKV));
+            AESIR_TRY(launch_gemm_f16(m->ctx, Xn, n, d, L.qkv.w, qkv_n, QKV));
         if (qkv_splits > 1) {
             const dim3 qgrid((unsigned)n, (unsigned)((qkv_n / 2 + kPThreads - 1) / kPThreads));
 #define AESIR_RQP(SV)                                                                                           \
@@ -1098,10 +1100,10 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
         // O projection + residual, then the feed-forward norm (inference.mojo:227-241)
         if (mfma) {
             W wo;
-            AESIR_TRY(wmat(L.wo, L.so, L.o_s1, L.o_hb, d, d, &wo));
+            AESIR_TRY(wmat(L.o, d, d, &wo));
             AESIR_TRY(residual_gemm(ATT, d, wo.w, wo.s, L.ffn_norm, "gemm_mfma_o_residual"));
         } else {
-            AESIR_TRY(launch_gemm_f16(m->ctx, ATT, n, d, L.wo, d, Xn));
+            AESIR_TRY(launch_gemm_f16(m->ctx, ATT, n, d, L.o.w, d, Xn));
             AESIR_TRY(launch_residual_add(s, X, Xn, n * d));
             AESIR_TRY(norm_rows(L.ffn_norm));
         }
@@ -1109,18 +1111,18 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
         // the next layer's attention-norm rows
         if (mfma) {
             W wgu, wdn;
-            AESIR_TRY(wmat(L.wgu, L.sgu, L.gu_s1, L.gu_hb, 2 * f, d, &wgu));
+            AESIR_TRY(wmat(L.gu, 2 * f, d, &wgu));
             AESIR_TRY(launch_mfma<kEpiSwiglu>(s, Xn, n, d, wgu.w, 2 * f, ACT, f, m->pf_part, m->pf_part_floats,
                                                 "gemm_mfma_gate_up_swiglu", false, nullptr, wgu.s));
             const void *next_norm = l + 1 < c.n_layers ? m->layers[l + 1].attn_norm : nullptr;
-            AESIR_TRY(wmat(L.wdown, L.sdown, L.down_s1, L.down_hb, d, f, &wdn));
+            AESIR_TRY(wmat(L.down, d, f, &wdn));
             AESIR_TRY(residual_gemm(ACT, f, wdn.w, wdn.s, next_norm, "gemm_mfma_down_residual"));
             xn_ready = next_norm != nullptr;
         } else {
             // interleaved gate/up rows -> [n][2f] products, then the SwiGLU over the pairs
-            AESIR_TRY(launch_gemm_f16(m->ctx, Xn, n, d, L.wgu, 2 * f, m->pf_gu));
+            AESIR_TRY(launch_gemm_f16(m->ctx, Xn, n, d, L.gu.w, 2 * f, m->pf_gu));
             AESIR_TRY(launch_swiglu_pairs(s, m->pf_gu, ACT, n * f));
-            AESIR_TRY(launch_gemm_f16(m->ctx, ACT, n, f, L.wdown, d, Xn));
+            AESIR_TRY(launch_gemm_f16(m->ctx, ACT, n, f, L.down.w, d, Xn));
             AESIR_TRY(launch_residual_add(s, X, Xn, n * d));
         }
     }
@@ -1138,8 +1140,8 @@ int32_t model_prefill(aesir_model *m, const int64_t *tokens, int64_t n, int64_t 
         if (tokens[i] < 0 || tokens[i] >= c.vocab)
             return fail(AESIR_ERR_INVALID, "Prompt token ID is outside the embedding vocabulary");
     AESIR_TRY(ensure_rope(m, start_pos + n));
-    if (m->wtype != AESIR_GGML_F16 && !prefill_mfma_ok(m)) {
-        // Q8_0 weights in shapes the MFMA GEMM does not tile: the reference's prefill, one decode
+    if (!m->all_f16 && !prefill_mfma_ok(m)) {
+        // quantized weights in shapes the MFMA GEMM does not tile: the reference's prefill, one decode
         // step per position
         for (int64_t i = 0; i < n; i++) AESIR_TRY(model_step(m, tokens[i], start_pos + i, next));
         return AESIR_OK;

@@ -174,6 +174,8 @@ __device__ __forceinline__ int gguf_q(const uint8_t *row, int64_t e) {
         const uint8_t *blk = row + (e / 32) * 18;
         const int i = (int)(e % 32);
         return i < 16 ? (blk[2 + i] & 15) : (blk[2 + i - 16] >> 4);
+    } else if constexpr (T == AESIR_GGML_Q8_0) {
+        return (int)(int8_t)row[(e / 32) * 34 + 2 + e % 32];
     } else if constexpr (T == AESIR_GGML_Q4_K) {
         const uint8_t *qs = row + (e / 256) * 144 + 16;
         const int i = (int)(e % 256), g = i / 64, l = i % 64;
@@ -200,7 +202,10 @@ __device__ __forceinline__ void q4k_scale_min(const uint8_t *sc, int j, int &s, 
 }
 
 __device__ __forceinline__ int64_t gguf_row_bytes(int T, int64_t K) {
-    return T == AESIR_GGML_Q4_0 ? K / 32 * 18 : T == AESIR_GGML_Q4_K ? K / 256 * 144 : K / 256 * 210;
+    return T == AESIR_GGML_Q4_0   ? K / 32 * 18
+           : T == AESIR_GGML_Q8_0 ? K / 32 * 34
+           : T == AESIR_GGML_Q4_K ? K / 256 * 144
+                                  : K / 256 * 210;
 }
 
 // One thread per record: GGUF blocks -> nibble record (+ hb word) and, from the record that
@@ -272,15 +277,15 @@ __global__ __launch_bounds__(256) void qf_dequant_kernel(QFMat w, int64_t rows, 
 // weight rules (and instructions) as qf_deq16.
 template <int T>
 __global__ __launch_bounds__(256) void gguf_dequant_kernel(const uint8_t *__restrict__ blocks, int64_t rows, int64_t K,
-                                                           h16 *__restrict__ out) {
+                                                           h16 *__restrict__ out, int64_t out_stride) {
     const int64_t recs = K / kRec;
     const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (gid >= rows * recs) return;
     const int64_t r = gid / recs, rec = gid % recs, k = rec * kRec;
     const uint8_t *src = blocks + r * gguf_row_bytes(T, K);
     h16x2 aa, nbb;
-    if constexpr (T == AESIR_GGML_Q4_0) {
-        const uint8_t *blk = src + (k / 32) * 18;
+    if constexpr (T == AESIR_GGML_Q4_0 || T == AESIR_GGML_Q8_0) {
+        const uint8_t *blk = src + (k / 32) * (T == AESIR_GGML_Q4_0 ? 18 : 34);
         const h16 d = bits_to_h((uint16_t)(blk[0] | (blk[1] << 8)));
         aa = h16x2{d, d};
     } else if constexpr (T == AESIR_GGML_Q4_K) {
@@ -302,12 +307,14 @@ __global__ __launch_bounds__(256) void gguf_dequant_kernel(const uint8_t *__rest
         const int q0 = gguf_q<T>(src, k + 2 * i), q1 = gguf_q<T>(src, k + 2 * i + 1);
         if constexpr (T == AESIR_GGML_Q4_0)
             wp[i] = h2_bits(q4_0_w2(h16x2{(h16)(float)(q0 - 8), (h16)(float)(q1 - 8)}, aa));
+        else if constexpr (T == AESIR_GGML_Q8_0)  // f16(f16(q) * d), as the Q8_0 GEMV
+            wp[i] = h2_bits(h16x2{(h16)((float)q0 * (float)aa.x), (h16)((float)q1 * (float)aa.x)});
         else if constexpr (T == AESIR_GGML_Q4_K)
             wp[i] = h2_bits(q4k_w2(h16x2{(h16)(float)q0, (h16)(float)q1}, aa, nbb));
         else
             wp[i] = h2_bits(q6k_w2(h16x2{(h16)(float)(q0 - 32), (h16)(float)(q1 - 32)}, aa));
     }
-    h16 *dst = out + r * K + k;
+    h16 *dst = out + r * out_stride + k;
     st16(dst, u32x4{wp[0], wp[1], wp[2], wp[3]});
     st16(dst + 8, u32x4{wp[4], wp[5], wp[6], wp[7]});
 }
@@ -401,16 +408,28 @@ int32_t launch_qf_dequant(hipStream_t s, const QFMat &w, int64_t rows, int64_t K
     return AESIR_OK;
 }
 
-int32_t launch_gguf_dequant(hipStream_t s, int32_t type, const void *blocks, int64_t rows, int64_t K, void *out) {
-    AESIR_TRY(qf_check(type, K, "gguf_dequant"));
+int32_t launch_gguf_dequant(hipStream_t s, int32_t type, const void *blocks, int64_t rows, int64_t K, void *out,
+                            int64_t out_stride) {
+    if (type == AESIR_GGML_Q8_0) {
+        if (K <= 0 || K % 32 != 0)
+            return fail(AESIR_ERR_SHAPE, "gguf_dequant: row length %lld is not a multiple of the 32-weight block", (long long)K);
+    } else {
+        AESIR_TRY(qf_check(type, K, "gguf_dequant"));
+    }
+    if (out_stride < K || out_stride % 8 != 0 || ((uintptr_t)out & 15) != 0)
+        return fail(AESIR_ERR_SHAPE, "gguf_dequant: output rows must be 16-byte aligned and hold K weights");
     if (rows <= 0) return AESIR_OK;
     const unsigned g = rec_grid(rows, K);
+    const uint8_t *b = (const uint8_t *)blocks;
+    h16 *o = (h16 *)out;
     if (type == AESIR_GGML_Q4_0)
-        hipLaunchKernelGGL(gguf_dequant_kernel<AESIR_GGML_Q4_0>, dim3(g), dim3(256), 0, s, (const uint8_t *)blocks, rows, K, (h16 *)out);
+        hipLaunchKernelGGL(gguf_dequant_kernel<AESIR_GGML_Q4_0>, dim3(g), dim3(256), 0, s, b, rows, K, o, out_stride);
+    else if (type == AESIR_GGML_Q8_0)
+        hipLaunchKernelGGL(gguf_dequant_kernel<AESIR_GGML_Q8_0>, dim3(g), dim3(256), 0, s, b, rows, K, o, out_stride);
     else if (type == AESIR_GGML_Q4_K)
-        hipLaunchKernelGGL(gguf_dequant_kernel<AESIR_GGML_Q4_K>, dim3(g), dim3(256), 0, s, (const uint8_t *)blocks, rows, K, (h16 *)out);
+        hipLaunchKernelGGL(gguf_dequant_kernel<AESIR_GGML_Q4_K>, dim3(g), dim3(256), 0, s, b, rows, K, o, out_stride);
     else
-        hipLaunchKernelGGL(gguf_dequant_kernel<AESIR_GGML_Q6_K>, dim3(g), dim3(256), 0, s, (const uint8_t *)blocks, rows, K, (h16 *)out);
+        hipLaunchKernelGGL(gguf_dequant_kernel<AESIR_GGML_Q6_K>, dim3(g), dim3(256), 0, s, b, rows, K, o, out_stride);
     AESIR_LAUNCH_CHECK("gguf_dequant_kernel");
     return AESIR_OK;
 }

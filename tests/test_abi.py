@@ -103,7 +103,7 @@ def test_gguf_freq_base_recorded_not_applied(A, oracle, tiny_gguf):
     ("alignment", "GGUF alignment must be a power of two up to 4096"),
     ("eos", "Tokenizer eos_token_id is out of bounds"),
     ("q4_1", "Real inference slice supports only F16 and F32 tensors"),
-    ("q8_mixed", "GGUF required tensor has an invalid type: output.weight"),
+    ("f32_matrix", "GGUF required tensor has an invalid type: output.weight"),
     ("overflow", "GGUF tensor byte size overflows the file: token_embd.weight"),
     ("huge", "GGUF tensor byte size overflows the file: token_embd.weight"),
 ])
@@ -135,14 +135,9 @@ def test_gguf_contract_errors(A, tiny_gguf, mutation, message):
         md.append(("general.alignment", T_UINT32, 48))
     elif mutation == "eos":
         md[13] = ("tokenizer.ggml.eos_token_id", T_UINT32, 9999)
-    if mutation == "q8_mixed":
-        # Q8_0 token_embd with F16 layer matrices: the Q8_0 extension needs every matrix in Q8_0
-        from aesir_hip import Q8_0Tensor
-
-        e = tensors["token_embd.weight"]
-        d = np.full((e.shape[0], e.shape[1] // 32), 0.001, np.float16)
-        q = np.zeros(e.shape, np.int8)
-        tensors["token_embd.weight"] = Q8_0Tensor.from_parts(d, q)
+    if mutation == "f32_matrix":
+        # a matrix in F32: matrices are F16 (or one of the block types), never F32
+        tensors["output.weight"] = tensors["output.weight"].astype(np.float32)
     path = make(md=md, tensors=tensors, **kw)
     if mutation == "truncated":
         size = os.path.getsize(path)
@@ -222,8 +217,9 @@ def test_gguf_inspect_q8_0_file(A, oracle, tmp_path):
 
 @pytest.mark.parametrize("kind", ["q4_0", "q4_k", "q6_k"])
 def test_gguf_inspect_4bit_files(A, oracle, tmp_path, kind):
-    """Files whose matrices are all Q4_0, Q4_K or Q6_K (norms F32) pass the loader contract; a file
-    that mixes block types between matrices is refused with the reference's type message."""
+    """Files whose matrices are all Q4_0, Q4_K or Q6_K (norms F32) pass the loader contract, and so
+    do files that mix block types between matrices; a matrix of a type outside the set (F32) is
+    refused with the reference's type message."""
     from gguf_tools import llama_metadata, write_gguf
 
     cfg = oracle.Config(dim=256, n_layers=1, n_heads=4, n_kv_heads=2, ffn=512, vocab=64, ctx_len=32)
@@ -249,6 +245,13 @@ def test_gguf_inspect_4bit_files(A, oracle, tmp_path, kind):
     assert (c.dim, c.ffn, c.vocab) == (256, 512, 64)
     other = "q6_k" if kind != "q6_k" else "q4_k"
     tensors["blk.0.attn_v.weight"] = tensor(other, cfg.kv_dim, cfg.dim)
+    tensors["blk.0.ffn_down.weight"] = A.Q8_0Tensor.from_parts(np.full((cfg.dim, cfg.ffn // 32), 0.01, np.float16),
+                                                               np.ones((cfg.dim, cfg.ffn), np.int8))
+    tensors["output.weight"] = np.zeros((cfg.vocab, cfg.dim), np.float16)
+    write_gguf(path, llama_metadata(cfg, cfg.vocab), tensors)
+    c, _ = A.gguf_inspect(path)
+    assert (c.dim, c.ffn, c.vocab) == (256, 512, 64)
+    tensors["blk.0.attn_v.weight"] = np.zeros((cfg.kv_dim, cfg.dim), np.float32)
     write_gguf(path, llama_metadata(cfg, cfg.vocab), tensors)
     with pytest.raises(A.AesirError, match="GGUF required tensor has an invalid type: blk.0.attn_v.weight"):
         A.gguf_inspect(path)

@@ -228,16 +228,66 @@ def qf_token_bytes(kind: str) -> int:
     return LAYERS * layer + qf_mat_bytes(kind, VOCAB, DIM) + 2 * DIM + qf_mat_bytes(kind, 1, DIM)
 
 
+# llama.cpp's Q4_K_M recipe for a Llama: Q4_K matrices, Q6_K for output and for attn_v / ffn_down of
+# the first and last eighth of the layers and every third layer between. A layer whose V is Q6_K
+# keeps its fused Q/K/V matrix in f16 (parts of one fused matrix share a storage type).
+def q4_k_m_more_bits(l: int) -> bool:
+    return l < LAYERS // 8 or l >= 7 * LAYERS // 8 or (l - LAYERS // 8) % 3 == 2
+
+
+def q4_k_m_types() -> dict:
+    t = {"token_embd.weight": 12, "output.weight": 14}
+    for l in range(LAYERS):
+        for b in ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"):
+            t[f"blk.{l}.{b}.weight"] = 14 if b in ("attn_v", "ffn_down") and q4_k_m_more_bits(l) else 12
+    return t
+
+
+def stored_mat_bytes(kind: str, rows: int, cols: int) -> int:
+    if kind == "f16":
+        return rows * cols * 2
+    return q8_mat_bytes(rows, cols) if kind == "q8_0" else qf_mat_bytes(kind, rows, cols)
+
+
+def layer_storage(kind: str, l: int) -> tuple:
+    """Stored types of layer l's (qkv, o, gate/up, down) matrices."""
+    if kind != "q4_k_m":
+        return (kind,) * 4
+    more = q4_k_m_more_bits(l)
+    return ("f16" if more else "q4_k", "q4_k", "q4_k", "q6_k" if more else "q4_k")
+
+
+def quant_token_bytes(kind: str) -> int:
+    """Algorithmic weight bytes of one decode token as stored: every matrix once, norms, one
+    embedding row."""
+    embd, out = ("q4_k", "q6_k") if kind == "q4_k_m" else (kind, kind)
+    total = stored_mat_bytes(out, VOCAB, DIM) + 2 * DIM + stored_mat_bytes(embd, 1, DIM)
+    for l in range(LAYERS):
+        qkv, o, gu, down = layer_storage(kind, l)
+        total += (stored_mat_bytes(qkv, DIM + 2 * KV_DIM, DIM) + stored_mat_bytes(o, DIM, DIM)
+                  + stored_mat_bytes(gu, 2 * FFN, DIM) + stored_mat_bytes(down, DIM, FFN) + 2 * 2 * DIM)
+    return total
+
+
+assert all(quant_token_bytes(k) == qf_token_bytes(k) for k in QF_TYPES)
+QUANT_KINDS = list(QF_TYPES) + ["q4_k_m"]
+
+
 def quant_bench(A, kind: str, seed: int, kv: int, steps: int, warmup: int, kernel_iters: int,
                 use_graph: bool = True) -> dict:
-    """Batch-1 greedy decode of the Llama-3-8B shape with Q4_0, Q4_K or Q6_K matrices (random
-    records and scales for weights of std 0.02), KV cache pre-filled to kv positions; same step
-    structure and timing as the F16 decode."""
+    """Batch-1 greedy decode of the Llama-3-8B shape with Q4_0, Q4_K or Q6_K matrices, or the
+    Q4_K_M mix of Q4_K and Q6_K (random records and scales for weights of std 0.02; f16 for the
+    fused matrices the mix stores so), KV cache pre-filled to kv positions; same step structure and
+    timing as the F16 decode."""
     ctx_len = kv + max(steps, warmup) + 64
-    well = int(qf_token_bytes(kind) + qf_mat_bytes(kind, VOCAB, DIM) + 2 * LAYERS * ctx_len * KV_DIM * 2
+    well = int(quant_token_bytes(kind) + stored_mat_bytes("q6_k", VOCAB, DIM) + 2 * LAYERS * ctx_len * KV_DIM * 2
                + 2 * 2 * FFN * DIM + (512 << 20))
     ctx = A.Context(well)
-    m = A.Model.create(ctx, A.ModelConfig(DIM, LAYERS, HEADS, KV_HEADS, FFN, VOCAB, ctx_len), QF_TYPES[kind])
+    cfg = A.ModelConfig(DIM, LAYERS, HEADS, KV_HEADS, FFN, VOCAB, ctx_len)
+    if kind == "q4_k_m":
+        m = A.Model.create_mixed(ctx, cfg, q4_k_m_types())
+    else:
+        m = A.Model.create(ctx, cfg, QF_TYPES[kind])
     m.init_random(seed, 0.02, 0.0, 0.02)
     m.fill_kv_random(kv, seed=seed + 1)
     m.decode_loop(1, kv, warmup, use_graph=use_graph)
@@ -248,15 +298,17 @@ def quant_bench(A, kind: str, seed: int, kv: int, steps: int, warmup: int, kerne
     wall = time.perf_counter() - t0
     tok_s = steps / wall
     mean_kv = kv + (steps - 1) / 2.0 + 1
-    step_bytes = qf_token_bytes(kind) + KV_BYTES_PER_POS * mean_kv + KV_BYTES_PER_POS
+    step_bytes = quant_token_bytes(kind) + KV_BYTES_PER_POS * mean_kv + KV_BYTES_PER_POS
     kt = m.kernel_times(kv, iters=kernel_iters)
     gu_ms = kt["gate_up_swiglu"]
-    gu_bytes = qf_mat_bytes(kind, 2 * FFN, DIM) + DIM * 2 + DIM * 2 + FFN * 2
+    gu_kind = layer_storage(kind, 0)[2]  # the same in every layer
+    gu_bytes = stored_mat_bytes(gu_kind, 2 * FFN, DIM) + DIM * 2 + DIM * 2 + FFN * 2
     m.close()
     ctx.close()
+    dtype = ("q4_k / q6_k weights (f16 Q/K/V where V is q6_k)" if kind == "q4_k_m" else f"{kind} weights")
     return {"workload": f"llama3-8b-shape {kind} batch-1 greedy decode, kv {kv}", "value": round(tok_s, 2),
             "unit": "tok/s", "steps": steps, "ms_per_step": round(wall * 1e3 / steps, 4),
-            "dtype": f"{kind} weights, f16 activations, f32 accumulate",
+            "dtype": f"{dtype}, f16 activations, f32 accumulate",
             "step_hbm": {"bytes_per_token": int(step_bytes), "achieved_gbs": round(step_bytes * tok_s / 1e9, 1),
                          "frac": round(step_bytes * tok_s / 1e9 / HBM_PEAK_GBS, 4),
                          "event_ms_per_step": round(event_ms / steps, 4)},
@@ -425,7 +477,7 @@ def main():
         return
     if args.quant_only:
         print(json.dumps({"quant": {k: quant_bench(A, k, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters,
-                                                   not args.eager) for k in QF_TYPES}}))
+                                                   not args.eager) for k in QUANT_KINDS}}))
         return
     if args.q8_only:
         q = q8_bench(A, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters, not args.eager)
@@ -502,7 +554,7 @@ def main():
         out["q8_0"]["prefill"] = prefill_bench(A, args.seed, n_decode=64, q8=True)
     if not args.no_quant:
         out["quant"] = {k: quant_bench(A, k, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters, use_graph)
-                        for k in QF_TYPES}
+                        for k in QUANT_KINDS}
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.kv, args.cpu_reps)
         out["cpu_baseline"]["value"] = round(out["cpu_baseline"]["value"], 4)

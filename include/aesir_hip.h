@@ -53,7 +53,8 @@ extern "C" {
  * layouts): block_q4_K {f16 d; f16 dmin; uint8 scales[12]; uint8 qs[128]} (144 bytes),
  * w = d * sc * q - dmin * m with 6-bit sc, m per 32 weights; block_q6_K {uint8 ql[128];
  * uint8 qh[64]; int8 scales[16]; f16 d} (210 bytes), w = d * sc * (q - 32) with 6-bit q. The
- * library evaluates these weights in f32, as GGML defines them. */
+ * library's weights are the f16 values of the reference's f16 dequantization arithmetic
+ * (aesir_gemm_quant). */
 #define AESIR_GGML_Q4_K 12
 #define AESIR_GGML_Q6_K 14
 
@@ -310,9 +311,11 @@ int32_t aesir_model_init_random(aesir_model *model, uint64_t seed, float std, fl
 /* GGUFSeer.mmap_and_load (loader/gguf.mojo:664-690) + AesirEngine.__init__'s layer setup
  * (aesir.mojo:237-296): parses a GGUF v3 Llama F16 file, enforces the reference loader
  * contract, creates the model (KV rows = ctx_len_override if > 0, else llama.context_length)
- * and uploads every tensor into HBM. Beyond the reference loader it also takes files whose
- * seven matrix kinds all share one of Q8_0, Q4_0, Q4_K or Q6_K (norms F32 or F16), giving a model
- * of that weight type; matrices of mixed types are refused. */
+ * and uploads every tensor into HBM. Beyond the reference loader each matrix may also be Q8_0,
+ * Q4_0, Q4_K or Q6_K, matrix by matrix (norms F32): a file whose matrices share one type gives a
+ * model of that weight type (aesir_model_create_typed), a file that mixes them (Q4_K_M and the
+ * like) the model aesir_model_create_mixed makes for its types. Other matrix types are refused
+ * with "GGUF required tensor has an invalid type". */
 int32_t aesir_model_load_gguf(aesir_ctx *ctx, const char *path, int64_t ctx_len_override, aesir_model **out);
 
 /* GGUFSeer.inspect_metadata (loader/gguf.mojo:649-662), extended to the tensor table: parses and

@@ -57,6 +57,20 @@ extern "C" {
  * (aesir_gemm_quant). */
 #define AESIR_GGML_Q4_K 12
 #define AESIR_GGML_Q6_K 14
+/* The reference's other GGUF-block formats (loader/gguf.mojo:21-29): block_q4_1 {f16 d; f16 m;
+ * uint8 qs[16]} (20 bytes / 32 weights), block_q5_0 {f16 d; uint8 qh[4]; uint8 qs[16]} (22),
+ * block_q5_1 {f16 d; f16 m; uint8 qh[4]; uint8 qs[16]} (24), the reference's BlockQ4_1 / BlockQ5_0 /
+ * BlockQ5_1 (core/compute.mojo:35-83), with its weights: Q4_1 w = f16(f16(q * d) + m), Q5_0
+ * w = f16((q - 16) * d), Q5_1 w = f16(f16(q * d) + m) for the 4- or 5-bit q (compute.mojo:282-340,
+ * each f16 operation rounded); and GGML's block_q2_K (84 bytes / 256 weights), block_q3_K (110)
+ * and block_q5_K (176), whose f16 weights follow the Q4_K / Q6_K rules: a = f16(d * sc),
+ * b = f16(dmin * m), w = f16(a * q - b) (Q2_K, Q5_K, one rounding) or f16(a * q) (Q3_K, signed q). */
+#define AESIR_GGML_Q4_1 3
+#define AESIR_GGML_Q5_0 6
+#define AESIR_GGML_Q5_1 7
+#define AESIR_GGML_Q2_K 10
+#define AESIR_GGML_Q3_K 11
+#define AESIR_GGML_Q5_K 13
 
 /* GPURealmType.AMD_ROCM_HIP (core/mimir_well.mojo:99): the realm id this library serves. */
 #define AESIR_REALM_AMD_ROCM_HIP 1

@@ -736,6 +736,183 @@ void ao_dequantize_q6_k_f16(const uint8_t *blocks, uint16_t *out, int64_t n_bloc
     }
 }
 
+/* ------------------------------------------------------------------ Q4_1, Q5_0, Q5_1 blocks */
+
+/* GGUF block_q4_1 { f16 d; f16 m; uint8 qs[16]; } (20 bytes), block_q5_0 { f16 d; uint8 qh[4];
+ * uint8 qs[16]; } (22) and block_q5_1 { f16 d; f16 m; uint8 qh[4]; uint8 qs[16]; } (24), packed.
+ * The reference's BlockQ4_1 / BlockQ5_0 / BlockQ5_1 (compute.mojo:35-83) hold the same fields in
+ * the same order. Element i < 16 is the low nibble of qs[i], element i + 16 its high nibble; for
+ * the 5-bit types bit i % 8 of qh[i / 8] is element i's fifth bit (compute.mojo:309-312). */
+#define Q4_1_BLOCK_BYTES 20
+#define Q5_0_BLOCK_BYTES 22
+#define Q5_1_BLOCK_BYTES 24
+
+static int legacy_block_bytes(int type) { return type == 3 ? Q4_1_BLOCK_BYTES : type == 6 ? Q5_0_BLOCK_BYTES : Q5_1_BLOCK_BYTES; }
+
+/* The 4- or 5-bit value of element i of a block of GGML type 3 (Q4_1), 6 (Q5_0) or 7 (Q5_1). */
+static int legacy_q(const uint8_t *blk, int type, int i) {
+    const uint8_t *qs = blk + (type == 3 ? 4 : type == 6 ? 6 : 8);
+    int q = i < 16 ? (qs[i] & 0x0F) : (qs[i - 16] >> 4);
+    if (type != 3) {
+        const uint8_t *qh = blk + (type == 6 ? 2 : 4);
+        q |= ((qh[i / 8] >> (i % 8)) & 1) << 4;
+    }
+    return q;
+}
+
+/* The reference's f16 weight of element i, every f16 operation rounded once:
+ *   Q4_1  w = f16(f16(q * d) + m)         dequantize_q4_1 / gemm_q4_1 (compute.mojo:282-296, 941-942)
+ *   Q5_0  w = f16((q + 16 h - 16) * d)    dequantize_q5_0 / gemm_q5_0 (compute.mojo:299-317, 985-986)
+ *   Q5_1  w = f16(f16(q5 * d) + m)        dequantize_q5_1 / gemm_q5_1 (compute.mojo:321-340, 1027-1028)
+ * q + 16 h - 16 and every f16 conversion of a small integer are exact; q * d is exact in f32
+ * (5 x 11 bits) and F2H rounds it once; the sum of two f16 values is exact in f64 (their exponents
+ * span at most 41 bits) and ao_f64_to_f16 rounds it once. */
+static uint16_t legacy_weight(const uint8_t *blk, int type, int i) {
+    uint16_t dh, mh = 0;
+    memcpy(&dh, blk, 2);
+    if (type != 6) memcpy(&mh, blk + 2, 2);
+    const int q = legacy_q(blk, type, i);
+    if (type == 6) return F2H((float)(q - 16) * H2F(dh));
+    const uint16_t prod = F2H((float)q * H2F(dh));
+    return ao_f64_to_f16((double)H2F(prod) + (double)H2F(mh));
+}
+
+int ao_dequantize_legacy(int type, const uint8_t *blocks, uint16_t *out, int64_t n_blocks) {
+    if (type != 3 && type != 6 && type != 7) return ao_fail(AO_ERR_INVALID, "dequantize: type is not Q4_1, Q5_0 or Q5_1");
+    const int bb = legacy_block_bytes(type);
+    for (int64_t b = 0; b < n_blocks; b++)
+        for (int i = 0; i < 32; i++) out[b * 32 + i] = legacy_weight(blocks + b * bb, type, i);
+    return AO_OK;
+}
+
+/* gemm_q4_1 (compute.mojo:914-951): per block, the 16 lower and the 16 upper products are each
+ * reduced by the 16-lane reduce_add and added to the f32 sum, as gemm_q4_0. gemm_q5_0 / gemm_q5_1
+ * (compute.mojo:953-993, 995-1036): per block and i < 16, sum += a_lo * w_lo + a_hi * w_hi (two
+ * f32 products, their f32 sum, then the running sum; no contraction). C = f16(sum). */
+int ao_gemm_legacy(int type, const uint16_t *A, int64_t a_rows, int64_t a_cols, const uint8_t *blocks, int64_t b_rows,
+                   uint16_t *C, int64_t c_rows, int64_t c_cols) {
+    if (type != 3 && type != 6 && type != 7) return ao_fail(AO_ERR_INVALID, "gemm: type is not Q4_1, Q5_0 or Q5_1");
+    if (a_rows <= 0 || a_cols <= 0 || b_rows <= 0) return ao_fail(AO_ERR_INVALID, "gemm: matrix dimensions must be positive");
+    if (a_cols % 32 != 0) return ao_fail(AO_ERR_SHAPE, "gemm: inner dimension must be a multiple of 32");
+    if (c_rows != a_rows || c_cols != b_rows) return ao_fail(AO_ERR_SHAPE, "gemm: output matrix shape mismatch");
+    const int64_t K = a_cols, bpr = K / 32;
+    const int bb = legacy_block_bytes(type);
+    uint16_t w[32];
+    for (int64_t row = 0; row < a_rows; row++) {
+        for (int64_t n = 0; n < b_rows; n++) {
+            float sum = 0.0f;
+            for (int64_t b = 0; b < bpr; b++) {
+                const uint8_t *blk = blocks + (n * bpr + b) * bb;
+                const uint16_t *a = A + row * K + b * 32;
+                for (int i = 0; i < 32; i++) w[i] = legacy_weight(blk, type, i);
+                if (type == 3) {
+                    sum += chunk16_dot_scalar(a, w);
+                    sum += chunk16_dot_scalar(a + 16, w + 16);
+                } else {
+                    for (int i = 0; i < 16; i++) {
+                        const float lo = H2F(a[i]) * H2F(w[i]), hi = H2F(a[16 + i]) * H2F(w[16 + i]);
+                        sum += lo + hi;
+                    }
+                }
+            }
+            C[row * b_rows + n] = F2H(sum);
+        }
+    }
+    return AO_OK;
+}
+
+/* ------------------------------------------------------------------ Q5_K, Q2_K, Q3_K super-blocks */
+
+/* GGML's other K-quant super-blocks of 256 weights as GGUF files hold them (types 13, 10, 11; the
+ * ids of loader/gguf.mojo:26-29). The reference's BlockQ5_K / BlockQ3_K (compute.mojo:131-162) are
+ * synthetic layouts and its BlockQ2_K (:164-181) has GGML's fields but dequantize_q2_k_block
+ * (:486-504) ignores the scales, so these restate GGML's published format (ggml-quants
+ * dequantize_row_q5_K / _q2_K / _q3_K, unchanged since GGUF v3):
+ *   block_q5_K { f16 d; f16 dmin; uint8 scales[12]; uint8 qh[32]; uint8 qs[128]; } (176 bytes):
+ *     Q4_K's scale packing and nibble order, plus bit 2 g (weight 64 g + l) or 2 g + 1 (weight
+ *     64 g + 32 + l) of qh[l] as the fifth bit; w = d sc q - dmin m.
+ *   block_q2_K { uint8 scales[16]; uint8 qs[64]; f16 d; f16 dmin; } (84 bytes): for half h, shift
+ *     j and l < 32, weight 128 h + 32 j + l is (qs[32 h + l] >> 2 j) & 3, with sub-block
+ *     is = 8 h + 2 j + l / 16 whose byte holds the 4-bit scale (low) and min (high);
+ *     w = d sc q - dmin m.
+ *   block_q3_K { uint8 hmask[32]; uint8 qs[64]; uint8 scales[12]; f16 d; } (110 bytes): the same
+ *     2-bit order as Q2_K, minus 4 unless bit 4 h + j of hmask[l] is set, with sixteen 6-bit
+ *     scales (low 4 bits: byte j of scales for j < 8, the high nibble of byte j - 8 above; high 2
+ *     bits: bits 2 (j / 4) of byte 8 + j % 4), less 32; w = d (sc - 32) q. */
+#define Q5_K_BLOCK_BYTES 176
+#define Q2_K_BLOCK_BYTES 84
+#define Q3_K_BLOCK_BYTES 110
+
+static int q3_k_scale(const uint8_t *sc, int j) {
+    const int lo = j < 8 ? (sc[j] & 0x0F) : (sc[j - 8] >> 4);
+    const int hi = (sc[8 + j % 4] >> (2 * (j / 4))) & 3;
+    return (lo | (hi << 4)) - 32;
+}
+
+/* (value, scale-or-a, min-or-b index) of weight i of a block: v is the quantized value as the
+ * rule multiplies it, s the sub-block's integer scale, m its integer min (0 for Q3_K). */
+static void kquant_fields(int type, const uint8_t *blk, int i, int *v, int *s, int *m, float *d, float *dmin) {
+    uint16_t dh = 0, mh = 0;
+    if (type == 13) {
+        memcpy(&dh, blk, 2);
+        memcpy(&mh, blk + 2, 2);
+        const uint8_t *qh = blk + 16, *qs = blk + 48;
+        const int g = i / 64, l = i % 64, hi = l >= 32, ll = l % 32;
+        *v = (hi ? (qs[32 * g + ll] >> 4) : (qs[32 * g + ll] & 0x0F)) | (((qh[ll] >> (2 * g + hi)) & 1) << 4);
+        q4_k_scale_min(blk + 4, 2 * g + hi, s, m);
+    } else {
+        const int h = i / 128, j = (i % 128) / 32, l = i % 32;
+        const int is = 8 * h + 2 * j + l / 16;
+        if (type == 10) {
+            memcpy(&dh, blk + 80, 2);
+            memcpy(&mh, blk + 82, 2);
+            *v = (blk[16 + 32 * h + l] >> (2 * j)) & 3;
+            *s = blk[is] & 0x0F;
+            *m = blk[is] >> 4;
+        } else {
+            memcpy(&dh, blk + 108, 2);
+            const int q = (blk[32 + 32 * h + l] >> (2 * j)) & 3;
+            *v = q - (((blk[l] >> (4 * h + j)) & 1) ? 0 : 4);
+            *s = q3_k_scale(blk + 96, is);
+            *m = 0;
+        }
+    }
+    *d = H2F(dh);
+    *dmin = H2F(mh);
+}
+
+static int kquant_block_bytes(int type) { return type == 13 ? Q5_K_BLOCK_BYTES : type == 10 ? Q2_K_BLOCK_BYTES : Q3_K_BLOCK_BYTES; }
+
+/* GGML's f32 weights: (d sc) q - (dmin m), d sc and dmin m exact in f32, one rounding. */
+int ao_dequantize_kquant(int type, const uint8_t *blocks, float *out, int64_t n_blocks) {
+    if (type != 10 && type != 11 && type != 13) return ao_fail(AO_ERR_INVALID, "dequantize: type is not Q2_K, Q3_K or Q5_K");
+    const int bb = kquant_block_bytes(type);
+    for (int64_t b = 0; b < n_blocks; b++)
+        for (int i = 0; i < 256; i++) {
+            int v, sc, m;
+            float d, dmin;
+            kquant_fields(type, blocks + b * bb, i, &v, &sc, &m, &d, &dmin);
+            out[b * 256 + i] = (d * (float)sc) * (float)v - dmin * (float)m;
+        }
+    return AO_OK;
+}
+
+/* The library's f16 weights, the form of the Q4_K / Q6_K rules: a = f16(d sc), b = f16(dmin m),
+ * w = f16(a q - b) with one rounding (Q5_K, Q2_K), w = f16(a q) (Q3_K). */
+int ao_dequantize_kquant_f16(int type, const uint8_t *blocks, uint16_t *out, int64_t n_blocks) {
+    if (type != 10 && type != 11 && type != 13) return ao_fail(AO_ERR_INVALID, "dequantize: type is not Q2_K, Q3_K or Q5_K");
+    const int bb = kquant_block_bytes(type);
+    for (int64_t b = 0; b < n_blocks; b++)
+        for (int i = 0; i < 256; i++) {
+            int v, sc, m;
+            float d, dmin;
+            kquant_fields(type, blocks + b * bb, i, &v, &sc, &m, &d, &dmin);
+            const double a = H2F(F2H(d * (float)sc)), bm = H2F(F2H(dmin * (float)m));
+            out[b * 256 + i] = ao_f64_to_f16(a * (double)v - bm);
+        }
+    return AO_OK;
+}
+
 /* ------------------------------------------------------------------ KV cache */
 
 /* KVCache.append, mimir_well.mojo:488-501 */

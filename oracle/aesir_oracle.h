@@ -87,6 +87,15 @@ void ao_dequantize_q4_k(const uint8_t *blocks, float *out, int64_t n_blocks);
 void ao_dequantize_q6_k(const uint8_t *blocks, float *out, int64_t n_blocks);
 void ao_dequantize_q4_k_f16(const uint8_t *blocks, uint16_t *out, int64_t n_blocks);
 void ao_dequantize_q6_k_f16(const uint8_t *blocks, uint16_t *out, int64_t n_blocks);
+/* GGUF block_q4_1 / block_q5_0 / block_q5_1 (GGML types 3, 6, 7; 20, 22, 24 bytes per 32 weights):
+ * dequantize_q4_1 / _q5_0 / _q5_1 and gemm_q4_1 / _q5_0 / _q5_1 (compute.mojo:282-340, 914-1036). */
+int ao_dequantize_legacy(int type, const uint8_t *blocks, uint16_t *out, int64_t n_blocks);
+int ao_gemm_legacy(int type, const uint16_t *A, int64_t a_rows, int64_t a_cols, const uint8_t *blocks, int64_t b_rows,
+                   uint16_t *C, int64_t c_rows, int64_t c_cols);
+/* GGML block_q2_K / block_q3_K / block_q5_K (types 10, 11, 13; 84, 110, 176 bytes per 256 weights)
+ * to GGML's f32 weights, and to the library's f16 weights. */
+int ao_dequantize_kquant(int type, const uint8_t *blocks, float *out, int64_t n_blocks);
+int ao_dequantize_kquant_f16(int type, const uint8_t *blocks, uint16_t *out, int64_t n_blocks);
 
 /* ---- KV cache (mimir_well.mojo:434-521) over caller-owned buffers ---- */
 typedef struct {

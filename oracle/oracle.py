@@ -74,6 +74,10 @@ def lib():
         L.ao_dequantize_q4_k_f16.restype = None
         L.ao_dequantize_q6_k_f16.argtypes = [P, P, I64]
         L.ao_dequantize_q6_k_f16.restype = None
+        L.ao_dequantize_legacy.argtypes = [C.c_int, P, P, I64]
+        L.ao_gemm_legacy.argtypes = [C.c_int, P, I64, I64, P, I64, P, I64, I64]
+        L.ao_dequantize_kquant.argtypes = [C.c_int, P, P, I64]
+        L.ao_dequantize_kquant_f16.argtypes = [C.c_int, P, P, I64]
         L.ao_kv_append.argtypes = [P, I64, I64, P, I64, P, I64]
         L.ao_kv_slice.argtypes = [P, I64, I64, P, P]
         L.ao_forward_scratch_elems.argtypes = [P]
@@ -316,6 +320,45 @@ def dequantize_q8_0(blocks, n_blocks) -> np.ndarray:
     blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
     out = np.zeros(n_blocks * 32, dtype=np.float16)
     lib().ao_dequantize_q8_0(_ptr(blocks), _ptr(out), n_blocks)
+    return out
+
+
+LEGACY_TYPES = {"q4_1": 3, "q5_0": 6, "q5_1": 7}
+KQUANT_TYPES = {"q2_k": 10, "q3_k": 11, "q5_k": 13}
+
+
+def dequantize_legacy(kind: str, blocks, n_blocks) -> np.ndarray:
+    """GGUF block_q4_1 / _q5_0 / _q5_1 -> the reference's f16 weights (dequantize_q4_1 / _q5_0 /
+    _q5_1, core/compute.mojo:282-340)."""
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    out = np.zeros(n_blocks * 32, dtype=np.float16)
+    _check(lib().ao_dequantize_legacy(LEGACY_TYPES[kind], _ptr(blocks), _ptr(out), n_blocks))
+    return out
+
+
+def gemm_legacy(kind: str, A, blocks, n_rows) -> np.ndarray:
+    """gemm_q4_1 / _q5_0 / _q5_1 (core/compute.mojo:914-1036) on GGUF blocks."""
+    A = _f16(A)
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    Cm = np.zeros((A.shape[0], n_rows), dtype=np.float16)
+    _check(lib().ao_gemm_legacy(LEGACY_TYPES[kind], _ptr(A), A.shape[0], A.shape[1], _ptr(blocks), n_rows, _ptr(Cm),
+                                A.shape[0], n_rows))
+    return Cm
+
+
+def dequantize_kquant(kind: str, blocks, n_blocks) -> np.ndarray:
+    """GGML block_q2_K / _q3_K / _q5_K super-blocks -> GGML's f32 weights."""
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    out = np.zeros(n_blocks * 256, dtype=np.float32)
+    _check(lib().ao_dequantize_kquant(KQUANT_TYPES[kind], _ptr(blocks), _ptr(out), n_blocks))
+    return out
+
+
+def dequantize_kquant_f16(kind: str, blocks, n_blocks) -> np.ndarray:
+    """GGML block_q2_K / _q3_K / _q5_K super-blocks -> the library's f16 weights."""
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    out = np.zeros(n_blocks * 256, dtype=np.float16)
+    _check(lib().ao_dequantize_kquant_f16(KQUANT_TYPES[kind], _ptr(blocks), _ptr(out), n_blocks))
     return out
 
 

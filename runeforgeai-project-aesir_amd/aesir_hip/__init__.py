@@ -402,6 +402,7 @@ class ModelConfig:
 
 
 GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 0, 1, 2, 8, 12, 14
+GGML_Q4_1, GGML_Q5_0, GGML_Q5_1, GGML_Q2_K, GGML_Q3_K, GGML_Q5_K = 3, 6, 7, 10, 11, 13
 WEIGHT_MIXED = -2  # aesir_model_weight_type of a model whose matrices differ in type
 
 
@@ -518,6 +519,153 @@ class Q6_KTensor(QuantTensor):
         blocks[:, 128:192] = qh.reshape(nb, 64)
         blocks[:, 192:208] = np.ascontiguousarray(scales, np.int8).reshape(nb, 16).view(np.uint8)
         blocks[:, 208:210] = np.ascontiguousarray(d, np.float16).reshape(nb).view(np.uint8).reshape(nb, 2)
+        return cls(blocks, rows, cols)
+
+
+def _f16_bytes(a, nb: int) -> np.ndarray:
+    return np.ascontiguousarray(a, np.float16).reshape(nb).view(np.uint8).reshape(nb, 2)
+
+
+def _legacy_qs(q: np.ndarray, nb: int) -> np.ndarray:
+    """16 nibble bytes per 32 weights: element i low, element i + 16 high."""
+    qb = np.ascontiguousarray(q, np.uint8).reshape(nb, 32) & 15
+    return qb[:, :16] | (qb[:, 16:] << 4)
+
+
+def _legacy_qh(q: np.ndarray, nb: int) -> np.ndarray:
+    """4 bytes per 32 weights: bit i % 8 of byte i / 8 is element i's fifth bit."""
+    hb = (np.ascontiguousarray(q, np.uint8).reshape(nb, 4, 8) >> 4) & 1
+    return (hb << np.arange(8, dtype=np.uint8)).sum(axis=2).astype(np.uint8)
+
+
+class Q4_1Tensor(QuantTensor):
+    """GGUF block_q4_1: 20-byte blocks {f16 d; f16 m; uint8 qs[16]} of 32 weights (GGML type 3, the
+    reference's BlockQ4_1); w = f16(f16(q d) + m)."""
+
+    ggml_type, block_elems, block_bytes = 3, 32, 20
+
+    @classmethod
+    def from_parts(cls, d, m, q) -> "Q4_1Tensor":
+        """d, m: f16 [rows, cols/32]; q: 0..15 [rows, cols]."""
+        rows, cols = q.shape
+        nb = rows * cols // 32
+        blocks = np.empty((nb, 20), np.uint8)
+        blocks[:, 0:2] = _f16_bytes(d, nb)
+        blocks[:, 2:4] = _f16_bytes(m, nb)
+        blocks[:, 4:] = _legacy_qs(q, nb)
+        return cls(blocks, rows, cols)
+
+
+class Q5_0Tensor(QuantTensor):
+    """GGUF block_q5_0: 22-byte blocks {f16 d; uint8 qh[4]; uint8 qs[16]} of 32 weights (GGML type
+    6, the reference's BlockQ5_0); w = f16((q - 16) d) for 5-bit q."""
+
+    ggml_type, block_elems, block_bytes = 6, 32, 22
+
+    @classmethod
+    def from_parts(cls, d, q) -> "Q5_0Tensor":
+        """d: f16 [rows, cols/32]; q: 0..31 [rows, cols]."""
+        rows, cols = q.shape
+        nb = rows * cols // 32
+        blocks = np.empty((nb, 22), np.uint8)
+        blocks[:, 0:2] = _f16_bytes(d, nb)
+        blocks[:, 2:6] = _legacy_qh(q, nb)
+        blocks[:, 6:] = _legacy_qs(q, nb)
+        return cls(blocks, rows, cols)
+
+
+class Q5_1Tensor(QuantTensor):
+    """GGUF block_q5_1: 24-byte blocks {f16 d; f16 m; uint8 qh[4]; uint8 qs[16]} of 32 weights (GGML
+    type 7, the reference's BlockQ5_1); w = f16(f16(q d) + m) for 5-bit q."""
+
+    ggml_type, block_elems, block_bytes = 7, 32, 24
+
+    @classmethod
+    def from_parts(cls, d, m, q) -> "Q5_1Tensor":
+        """d, m: f16 [rows, cols/32]; q: 0..31 [rows, cols]."""
+        rows, cols = q.shape
+        nb = rows * cols // 32
+        blocks = np.empty((nb, 24), np.uint8)
+        blocks[:, 0:2] = _f16_bytes(d, nb)
+        blocks[:, 2:4] = _f16_bytes(m, nb)
+        blocks[:, 4:8] = _legacy_qh(q, nb)
+        blocks[:, 8:] = _legacy_qs(q, nb)
+        return cls(blocks, rows, cols)
+
+
+class Q5_KTensor(QuantTensor):
+    """GGUF block_q5_K: 176-byte super-blocks of 256 weights (GGML type 13):
+    {f16 d; f16 dmin; uint8 scales[12]; uint8 qh[32]; uint8 qs[128]}, Q4_K's scales and nibble
+    order plus a fifth bit per weight; w = d * scale * q - dmin * min for 5-bit q."""
+
+    ggml_type, block_elems, block_bytes = 13, 256, 176
+
+    @classmethod
+    def from_parts(cls, d, dmin, scales, mins, q) -> "Q5_KTensor":
+        """d, dmin: f16 [rows, cols/256]; scales, mins: 0..63 [rows, cols/256, 8]; q: 0..31 [rows, cols]."""
+        rows, cols = q.shape
+        nb = rows * cols // 256
+        base = Q4_KTensor.from_parts(d, dmin, scales, mins, np.ascontiguousarray(q, np.uint8) & 15).blocks
+        hb = ((np.ascontiguousarray(q, np.uint8).reshape(nb, 8, 32) >> 4) & 1)  # [block, sub-block 2g + hi, l]
+        qh = (hb << np.arange(8, dtype=np.uint8)[None, :, None]).sum(axis=1).astype(np.uint8)
+        blocks = np.empty((nb, 176), np.uint8)
+        blocks[:, 0:16] = base[:, 0:16]
+        blocks[:, 16:48] = qh
+        blocks[:, 48:] = base[:, 16:]
+        return cls(blocks, rows, cols)
+
+
+class Q2_KTensor(QuantTensor):
+    """GGUF block_q2_K: 84-byte super-blocks of 256 weights (GGML type 10):
+    {uint8 scales[16]; uint8 qs[64]; f16 d; f16 dmin}, sixteen sub-blocks of 16 with a 4-bit scale
+    and min each; w = d * scale * q - dmin * min for 2-bit q."""
+
+    ggml_type, block_elems, block_bytes = 10, 256, 84
+
+    @classmethod
+    def from_parts(cls, d, dmin, scales, mins, q) -> "Q2_KTensor":
+        """d, dmin: f16 [rows, cols/256]; scales, mins: 0..15 [rows, cols/256, 16]; q: 0..3 [rows, cols]."""
+        rows, cols = q.shape
+        nb = rows * cols // 256
+        qv = (np.ascontiguousarray(q, np.uint8) & 3).reshape(nb, 2, 4, 32)  # [block, half, shift, l]
+        qs = (qv << (2 * np.arange(4, dtype=np.uint8))[None, None, :, None]).sum(axis=2).astype(np.uint8)
+        blocks = np.empty((nb, 84), np.uint8)
+        blocks[:, 0:16] = ((np.ascontiguousarray(scales, np.uint8) & 15)
+                           | ((np.ascontiguousarray(mins, np.uint8) & 15) << 4)).reshape(nb, 16)
+        blocks[:, 16:80] = qs.reshape(nb, 64)
+        blocks[:, 80:82] = _f16_bytes(d, nb)
+        blocks[:, 82:84] = _f16_bytes(dmin, nb)
+        return cls(blocks, rows, cols)
+
+
+class Q3_KTensor(QuantTensor):
+    """GGUF block_q3_K: 110-byte super-blocks of 256 weights (GGML type 11):
+    {uint8 hmask[32]; uint8 qs[64]; uint8 scales[12]; f16 d}, sixteen sub-blocks of 16 with a
+    6-bit scale each (stored + 32); w = d * scale * q for q in -4..3."""
+
+    ggml_type, block_elems, block_bytes = 11, 256, 110
+
+    @classmethod
+    def from_parts(cls, d, scales, q) -> "Q3_KTensor":
+        """d: f16 [rows, cols/256]; scales: -32..31 [rows, cols/256, 16]; q: -4..3 [rows, cols]."""
+        rows, cols = q.shape
+        nb = rows * cols // 256
+        qv = np.ascontiguousarray(q, np.int16).reshape(nb, 2, 4, 32)  # [block, half, shift, l]
+        low = (qv & 3).astype(np.uint8)                                  # q + 4 when q < 0, else q
+        high = (qv >= 0).astype(np.uint8)
+        qs = (low << (2 * np.arange(4, dtype=np.uint8))[None, None, :, None]).sum(axis=2).astype(np.uint8)
+        hm = (high << (np.arange(2)[:, None] * 4 + np.arange(4)[None, :]).astype(np.uint8)[None, :, :, None])
+        hmask = hm.sum(axis=(1, 2)).astype(np.uint8)
+        u = (np.ascontiguousarray(scales, np.int16).reshape(nb, 16) + 32).astype(np.uint8) & 63
+        sc = np.zeros((nb, 12), np.uint8)
+        sc[:, 0:8] = (u[:, 0:8] & 15) | ((u[:, 8:16] & 15) << 4)
+        for j in range(16):
+            sc[:, 8 + j % 4] |= (u[:, j] >> 4) << (2 * (j // 4))
+        blocks = np.empty((nb, 110), np.uint8)
+        blocks[:, 0:32] = hmask
+        blocks[:, 32:96] = qs.reshape(nb, 64)
+        blocks[:, 96:108] = sc
+        blocks[:, 108:110] = _f16_bytes(d, nb)
         return cls(blocks, rows, cols)
 
 

@@ -218,22 +218,38 @@ int32_t aesir_gemm_quant(aesir_ctx *ctx, const void *A, int64_t a_rows, int64_t 
                          int32_t ggml_type, int64_t b_rows, void *C, int64_t c_rows, int64_t c_cols) {
     AESIR_TRY(bind(ctx));
     if (ggml_type == AESIR_GGML_Q8_0) return aesir_gemm_q8_0(ctx, A, a_rows, a_cols, blocks, b_rows, C, c_rows, c_cols);
-    const char *nm = ggml_type == AESIR_GGML_Q4_0 ? "gemm_q4_0" : ggml_type == AESIR_GGML_Q4_K ? "gemm_q4_k" : "gemm_q6_k";
-    if (!qf_type(ggml_type)) return fail(AESIR_ERR_UNSUPPORTED, "gemm_quant: GGML type %d is not Q4_0, Q8_0, Q4_K or Q6_K", (int)ggml_type);
-    // compute.mojo:877-882 (gemm_q4_0's checks; the K-quant twins raise the same)
+    const int64_t blk = gguf_block_elems(ggml_type);
+    if (blk == 0)
+        return fail(AESIR_ERR_UNSUPPORTED,
+                    "gemm_quant: GGML type %d is not Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K or Q6_K",
+                    (int)ggml_type);
+    const char *nm = "gemm_q6_k";
+    switch (ggml_type) {
+        case AESIR_GGML_Q4_0: nm = "gemm_q4_0"; break;
+        case AESIR_GGML_Q4_1: nm = "gemm_q4_1"; break;
+        case AESIR_GGML_Q5_0: nm = "gemm_q5_0"; break;
+        case AESIR_GGML_Q5_1: nm = "gemm_q5_1"; break;
+        case AESIR_GGML_Q2_K: nm = "gemm_q2_k"; break;
+        case AESIR_GGML_Q3_K: nm = "gemm_q3_k"; break;
+        case AESIR_GGML_Q4_K: nm = "gemm_q4_k"; break;
+        case AESIR_GGML_Q5_K: nm = "gemm_q5_k"; break;
+        default: break;
+    }
+    // compute.mojo:877-882 (gemm_q4_0's checks; gemm_q4_1 / _q5_0 / _q5_1 and the K-quant twins
+    // raise the same)
     if (a_rows <= 0 || a_cols <= 0 || b_rows <= 0) return fail(AESIR_ERR_INVALID, "%s: matrix dimensions must be positive", nm);
-    const int64_t blk = ggml_type == AESIR_GGML_Q4_0 ? 32 : 256;
     if (a_cols % blk != 0)
         return fail(AESIR_ERR_SHAPE, "%s: inner dimension must be a multiple of %lld", nm, (long long)blk);
     if (c_rows != a_rows || c_cols != b_rows) return fail(AESIR_ERR_SHAPE, "%s: output matrix shape mismatch", nm);
     if (!A || !blocks || !C) return fail(AESIR_ERR_INVALID, "%s: null tensor pointer", nm);
-    // Fewer than 16 rows of A on whole 128-weight segments: the blocks are repacked into tiled
-    // records and each row runs the decode GEMV. Otherwise the blocks are dequantized to f16 (the
-    // same values) for the F16 GEMM, on the matrix cores from 16 rows. Both take free well space
-    // for this call, released after enqueueing (later work on the stream runs after these kernels).
+    // Fewer than 16 rows of A on whole 128-weight segments of a repacked type (Q4_0, Q4_K, Q6_K):
+    // the blocks are repacked into tiled records and each row runs the decode GEMV. Otherwise the
+    // blocks are dequantized to f16 (the same values) for the F16 GEMM, on the matrix cores from 16
+    // rows. Both take free well space for this call, released after enqueueing (later work on the
+    // stream runs after these kernels).
     const int64_t K = a_cols, N = b_rows, mark = ctx->well_offset;
     int32_t rc = AESIR_OK;
-    if (a_rows < 16 && qf_gemv_ok(K)) {
+    if (a_rows < 16 && qf_type(ggml_type) && qf_gemv_ok(K)) {
         QFMat w;
         w.type = ggml_type;
         void *planes[4] = {nullptr, nullptr, nullptr, nullptr};

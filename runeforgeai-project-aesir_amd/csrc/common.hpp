@@ -79,7 +79,13 @@ inline GgmlBlock ggml_block(int64_t type) {
         case AESIR_GGML_F16: return {1, 2};
         case AESIR_GGML_Q8_0: return {32, 34};
         case AESIR_GGML_Q4_0: return {32, 18};
+        case AESIR_GGML_Q4_1: return {32, 20};
+        case AESIR_GGML_Q5_0: return {32, 22};
+        case AESIR_GGML_Q5_1: return {32, 24};
+        case AESIR_GGML_Q2_K: return {256, 84};
+        case AESIR_GGML_Q3_K: return {256, 110};
         case AESIR_GGML_Q4_K: return {256, 144};
+        case AESIR_GGML_Q5_K: return {256, 176};
         case AESIR_GGML_Q6_K: return {256, 210};
         default: return {0, 0};
     }

@@ -5,10 +5,11 @@
 // (message text included), then _validate_required_tensors. Where the reference aliases F16
 // tensors into the mmap, this loader uploads them once into the model's arena (Q/K/V
 // concatenated, gate/up interleaved); F32 norms are rounded to f16 as the reference does.
-// One extension: each matrix may also have a block type, Q8_0, Q4_0, Q4_K or Q6_K (GGML types 8,
-// 2, 12, 14), matrix by matrix (files such as Q4_K_M mix them); the model keeps each matrix in
-// its own type (the reference loader stops at "Real inference slice supports only F16 and F32
-// tensors"). Any other matrix type is refused with "GGUF required tensor has an invalid type".
+// One extension: each matrix may also have a block type, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q2_K,
+// Q3_K, Q4_K, Q5_K or Q6_K (GGML types 8, 2, 3, 6, 7, 10, 11, 12, 13, 14), matrix by matrix (files
+// such as Q4_K_M mix them); the model keeps each matrix in its own type or in f16 (the reference
+// loader stops at "Real inference slice supports only F16 and F32 tensors"). Any other matrix
+// type is refused with "GGUF required tensor has an invalid type".
 #include <fcntl.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
@@ -286,11 +287,9 @@ std::vector<std::string> required_tensors(const Gguf &g) {
 }
 
 // Types a matrix may have: F16 as the reference requires, and the block types this library adds
-// (Q8_0, Q4_0, Q4_K, Q6_K), each matrix its own (GGUF files mix them: Q4_K_M and the like).
-bool matrix_type_ok(uint32_t t) {
-    return t == AESIR_GGML_F16 || t == AESIR_GGML_Q8_0 || t == AESIR_GGML_Q4_0 || t == AESIR_GGML_Q4_K ||
-           t == AESIR_GGML_Q6_K;
-}
+// (Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K), each matrix its own (GGUF files
+// mix them: Q4_K_M and the like).
+bool matrix_type_ok(uint32_t t) { return t == AESIR_GGML_F16 || gguf_block_elems((int32_t)t) != 0; }
 
 // Expected (rows, cols) of a required tensor (loader/gguf.mojo:597-628); *norm for the F32 norms.
 void expected_shape(const Gguf &g, const std::string &name, int64_t vocab, int64_t *rows, int64_t *cols, bool *norm) {

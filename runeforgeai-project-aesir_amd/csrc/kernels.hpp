@@ -89,12 +89,15 @@ int32_t launch_qf_dequant(hipStream_t s, const QFMat &w, int64_t rows, int64_t K
 // Seeded synthetic planes: weights of standard deviation near `std`, mean near 0.
 int32_t launch_qf_fill_random(hipStream_t s, const QFMat &w, int64_t rows, int64_t K, int64_t step, uint64_t seed,
                               uint64_t stream, float std);
-// GGUF blocks (rows x K, packed, device memory; Q8_0, Q4_0, Q4_K or Q6_K) -> f16 rows of
-// out_stride weights, straight from the blocks, the same f16 values as launch_qf_dequant and the
-// Q8_0 GEMV (the per-op GEMMs of 16 or more rows, row lengths the GEMV does not take, and the
-// quantized parts of a model matrix stored in f16).
+// GGUF blocks (rows x K, packed, device memory; Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q4_K,
+// Q5_K or Q6_K) -> f16 rows of out_stride weights, straight from the blocks, the same f16 values
+// as launch_qf_dequant and the Q8_0 GEMV (the per-op GEMMs of 16 or more rows, row lengths the
+// GEMV does not take, the types without repacked planes, and the quantized parts of a model
+// matrix stored in f16).
 int32_t launch_gguf_dequant(hipStream_t s, int32_t type, const void *blocks, int64_t rows, int64_t K, void *out,
                             int64_t out_stride);
+// Weights per block of a GGML block type launch_gguf_dequant takes (32 or 256), else 0.
+int64_t gguf_block_elems(int32_t type);
 // The decode GEMV stages x in LDS (2 K bytes) and works on whole 128-weight segments.
 constexpr int64_t kQfGemvMaxK = 28672;
 bool qf_gemv_ok(int64_t K);

@@ -460,6 +460,9 @@ int32_t aesir_model_tensor_type(aesir_model *m, const char *name) {
 
 namespace aesir {
 
+// Types a matrix keeps in HBM as they are (the others are stored in f16).
+static bool stored_native(int32_t t) { return t == AESIR_GGML_F16 || t == AESIR_GGML_Q8_0 || qf_type(t); }
+
 int32_t model_create(aesir_ctx *ctx, const aesir_model_config *cfg, const WeightTypes &types, aesir_model **out) {
     AESIR_TRY(bind(ctx));
     if (!cfg || !out) return fail(AESIR_ERR_INVALID, "aesir_model_create: null argument");
@@ -490,8 +493,17 @@ int32_t model_create(aesir_ctx *ctx, const aesir_model_config *cfg, const Weight
     std::sort(present.begin(), present.end());
     present.erase(std::unique(present.begin(), present.end()), present.end());
     for (int32_t wt : present) {
-        if (wt != AESIR_GGML_F16 && wt != AESIR_GGML_Q8_0 && !qf_type(wt))
-            return fail(AESIR_ERR_UNSUPPORTED, "model: weight type %d is not F16, Q8_0, Q4_0, Q4_K or Q6_K", (int)wt);
+        if (wt != AESIR_GGML_F16 && gguf_block_elems(wt) == 0)
+            return fail(AESIR_ERR_UNSUPPORTED,
+                        "model: weight type %d is not F16, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q4_K, Q5_K or Q6_K",
+                        (int)wt);
+        if (!stored_native(wt)) {
+            // kept in f16, dequantized at upload: whole blocks per row
+            const int64_t blk = gguf_block_elems(wt);
+            if (c.dim % blk != 0 || c.ffn % blk != 0)
+                return fail(AESIR_ERR_UNSUPPORTED, "model: GGML type %d weights need dim and ffn to be multiples of %lld",
+                            (int)wt, (long long)blk);
+        }
         if (wt == AESIR_GGML_Q8_0 && (c.dim % 32 != 0 || c.ffn % 32 != 0 || c.dim > 16384 || c.ffn > 16384))
             return fail(AESIR_ERR_UNSUPPORTED, "model: Q8_0 weights need dim and ffn to be multiples of 32, at most 16384");
         if (qf_type(wt)) {
@@ -546,26 +558,27 @@ int32_t model_create(aesir_ctx *ctx, const aesir_model_config *cfg, const Weight
         take(mul_checked(rows, cols, q8 ? 1 : 2), &w->w);
         if (q8) take(mul_checked(rows, cols / 32, 2), &w->s0);
     };
-    // A fused matrix whose parts differ in type is stored in f16 (each part dequantized at upload).
+    // A fused matrix whose parts differ in type is stored in f16 (each part dequantized at upload),
+    // as is every matrix of a type without a GEMV of its own.
     auto fused = [](std::initializer_list<int32_t> parts) {
         const int32_t t0 = *parts.begin();
         for (int32_t t : parts)
             if (t != t0) return (int32_t)AESIR_GGML_F16;
-        return t0;
+        return stored_native(t0) ? t0 : (int32_t)AESIR_GGML_F16;
     };
-    matrix(V, d, types.embd, &m->embd);
+    matrix(V, d, fused({types.embd}), &m->embd);
     take(d * 2, &m->out_norm);
-    matrix(V, d, types.out, &m->out);
+    matrix(V, d, fused({types.out}), &m->out);
     m->layers.resize((size_t)c.n_layers);
     for (int64_t l = 0; l < c.n_layers; l++) {
         ModelLayer &L = m->layers[l];
         const LayerTypes &t = types.layers[l];
         take(d * 2, &L.attn_norm);
         matrix(d + 2 * kvd, d, fused({t.q, t.k, t.v}), &L.qkv);
-        matrix(d, d, t.o, &L.o);
+        matrix(d, d, fused({t.o}), &L.o);
         take(d * 2, &L.ffn_norm);
         matrix(2 * f, d, fused({t.gate, t.up}), &L.gu);
-        matrix(d, f, t.down, &L.down);
+        matrix(d, f, fused({t.down}), &L.down);
     }
     m->all_f16 = m->embd.type == AESIR_GGML_F16 && m->out.type == AESIR_GGML_F16;
     for (const ModelLayer &L : m->layers)

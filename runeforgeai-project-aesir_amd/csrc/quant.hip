@@ -176,6 +176,29 @@ __device__ __forceinline__ int gguf_q(const uint8_t *row, int64_t e) {
         return i < 16 ? (blk[2 + i] & 15) : (blk[2 + i - 16] >> 4);
     } else if constexpr (T == AESIR_GGML_Q8_0) {
         return (int)(int8_t)row[(e / 32) * 34 + 2 + e % 32];
+    } else if constexpr (T == AESIR_GGML_Q4_1 || T == AESIR_GGML_Q5_0 || T == AESIR_GGML_Q5_1) {
+        // {d, (m), (qh[4]), qs[16]}: nibbles as Q4_0, bit i of the qh word the fifth bit
+        constexpr int bb = T == AESIR_GGML_Q4_1 ? 20 : T == AESIR_GGML_Q5_0 ? 22 : 24;
+        constexpr int qs = T == AESIR_GGML_Q5_0 ? 6 : T == AESIR_GGML_Q4_1 ? 4 : 8;
+        const uint8_t *blk = row + (e / 32) * bb;
+        const int i = (int)(e % 32);
+        const int q = i < 16 ? (blk[qs + i] & 15) : (blk[qs + i - 16] >> 4);
+        if constexpr (T == AESIR_GGML_Q4_1) return q;
+        else return q | (((blk[qs - 4 + i / 8] >> (i % 8)) & 1) << 4);
+    } else if constexpr (T == AESIR_GGML_Q5_K) {
+        const uint8_t *blk = row + (e / 256) * 176, *qh = blk + 16, *qs = blk + 48;
+        const int i = (int)(e % 256), g = i / 64, hi = (i / 32) & 1, l = i % 32;
+        const int q = hi ? (qs[32 * g + l] >> 4) : (qs[32 * g + l] & 15);
+        return q | (((qh[l] >> (2 * g + hi)) & 1) << 4);
+    } else if constexpr (T == AESIR_GGML_Q2_K || T == AESIR_GGML_Q3_K) {
+        // 2-bit values of half h, shift j, position l; Q3_K less 4 unless its hmask bit is set
+        const int i = (int)(e % 256), h = i / 128, j = (i / 32) & 3, l = i % 32;
+        if constexpr (T == AESIR_GGML_Q2_K) {
+            return (row[(e / 256) * 84 + 16 + 32 * h + l] >> (2 * j)) & 3;
+        } else {
+            const uint8_t *blk = row + (e / 256) * 110;
+            return ((blk[32 + 32 * h + l] >> (2 * j)) & 3) - ((blk[l] >> (4 * h + j)) & 1 ? 0 : 4);
+        }
     } else if constexpr (T == AESIR_GGML_Q4_K) {
         const uint8_t *qs = row + (e / 256) * 144 + 16;
         const int i = (int)(e % 256), g = i / 64, l = i % 64;
@@ -202,10 +225,25 @@ __device__ __forceinline__ void q4k_scale_min(const uint8_t *sc, int j, int &s, 
 }
 
 __device__ __forceinline__ int64_t gguf_row_bytes(int T, int64_t K) {
-    return T == AESIR_GGML_Q4_0   ? K / 32 * 18
-           : T == AESIR_GGML_Q8_0 ? K / 32 * 34
-           : T == AESIR_GGML_Q4_K ? K / 256 * 144
-                                  : K / 256 * 210;
+    switch (T) {
+        case AESIR_GGML_Q4_0: return K / 32 * 18;
+        case AESIR_GGML_Q4_1: return K / 32 * 20;
+        case AESIR_GGML_Q5_0: return K / 32 * 22;
+        case AESIR_GGML_Q5_1: return K / 32 * 24;
+        case AESIR_GGML_Q8_0: return K / 32 * 34;
+        case AESIR_GGML_Q2_K: return K / 256 * 84;
+        case AESIR_GGML_Q3_K: return K / 256 * 110;
+        case AESIR_GGML_Q4_K: return K / 256 * 144;
+        case AESIR_GGML_Q5_K: return K / 256 * 176;
+        default: return K / 256 * 210;
+    }
+}
+
+// 16-weight sub-block `is` (0..15) scale of a Q3_K super-block: GGML's packing of 16 6-bit values
+// in 12 bytes (low 4 bits in bytes 0-7, low then high nibble; high 2 bits in bytes 8-11), less 32.
+__device__ __forceinline__ int q3k_scale(const uint8_t *sc, int is) {
+    const int lo = is < 8 ? (sc[is] & 15) : (sc[is - 8] >> 4);
+    return (lo | (((sc[8 + (is & 3)] >> (2 * (is >> 2))) & 3) << 4)) - 32;
 }
 
 // One thread per record: GGUF blocks -> nibble record (+ hb word) and, from the record that
@@ -273,8 +311,13 @@ __global__ __launch_bounds__(256) void qf_dequant_kernel(QFMat w, int64_t rows, 
     st16(dst + 8, o[1]);
 }
 
+// Q4_1 / Q5_1 weight pairs f16(f16(q d) + m): two roundings, the reference's f16 multiply then
+// add (the library is built without multiply-add contraction).
+__device__ __forceinline__ h16x2 q4_1_w2(h16x2 q, h16x2 dd, h16x2 mm) { return q * dd + mm; }
+
 // One thread per record: GGUF blocks -> f16 weights straight from the blocks, with the same
-// weight rules (and instructions) as qf_deq16.
+// weight rules (and instructions) as qf_deq16 for the repacked types; the only path of the types
+// this library keeps in f16 (Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q5_K).
 template <int T>
 __global__ __launch_bounds__(256) void gguf_dequant_kernel(const uint8_t *__restrict__ blocks, int64_t rows, int64_t K,
                                                            h16 *__restrict__ out, int64_t out_stride) {
@@ -283,36 +326,61 @@ __global__ __launch_bounds__(256) void gguf_dequant_kernel(const uint8_t *__rest
     if (gid >= rows * recs) return;
     const int64_t r = gid / recs, rec = gid % recs, k = rec * kRec;
     const uint8_t *src = blocks + r * gguf_row_bytes(T, K);
-    h16x2 aa, nbb;
-    if constexpr (T == AESIR_GGML_Q4_0 || T == AESIR_GGML_Q8_0) {
-        const uint8_t *blk = src + (k / 32) * (T == AESIR_GGML_Q4_0 ? 18 : 34);
-        const h16 d = bits_to_h((uint16_t)(blk[0] | (blk[1] << 8)));
+    auto f16_at = [](const uint8_t *p) { return bits_to_h((uint16_t)(p[0] | (p[1] << 8))); };
+    h16x2 aa, nbb;  // the record's scale pair and negated offset (or added min) pair
+    if constexpr (T == AESIR_GGML_Q4_0 || T == AESIR_GGML_Q8_0 || T == AESIR_GGML_Q5_0) {
+        const h16 d = f16_at(src + (k / 32) * (T == AESIR_GGML_Q4_0 ? 18 : T == AESIR_GGML_Q8_0 ? 34 : 22));
         aa = h16x2{d, d};
-    } else if constexpr (T == AESIR_GGML_Q4_K) {
-        const uint8_t *blk = src + (k / 256) * 144;
+    } else if constexpr (T == AESIR_GGML_Q4_1 || T == AESIR_GGML_Q5_1) {
+        const uint8_t *blk = src + (k / 32) * (T == AESIR_GGML_Q4_1 ? 20 : 24);
+        aa = h16x2{f16_at(blk), f16_at(blk)};
+        nbb = h16x2{f16_at(blk + 2), f16_at(blk + 2)};
+    } else if constexpr (T == AESIR_GGML_Q4_K || T == AESIR_GGML_Q5_K || T == AESIR_GGML_Q2_K) {
         int s, m;
-        q4k_scale_min(blk + 4, (int)((k % 256) / 32), s, m);
-        const h16x2 dd = {bits_to_h((uint16_t)(blk[0] | (blk[1] << 8))), bits_to_h((uint16_t)(blk[2] | (blk[3] << 8)))};
-        const h16x2 ab = q4k_scales(dd, h16x2{(h16)(float)s, (h16)(float)m});
+        const uint8_t *dm;
+        if constexpr (T == AESIR_GGML_Q2_K) {
+            const uint8_t *blk = src + (k / 256) * 84;
+            const int i = (int)(k % 256), is = 8 * (i / 128) + 2 * ((i / 32) & 3) + (i / 16 & 1);
+            s = blk[is] & 15;
+            m = blk[is] >> 4;
+            dm = blk + 80;
+        } else {
+            const uint8_t *blk = src + (k / 256) * (T == AESIR_GGML_Q4_K ? 144 : 176);
+            q4k_scale_min(blk + 4, (int)((k % 256) / 32), s, m);
+            dm = blk;
+        }
+        const h16x2 ab = q4k_scales(h16x2{f16_at(dm), f16_at(dm + 2)}, h16x2{(h16)(float)s, (h16)(float)m});
         aa = h16x2{ab.x, ab.x};
         nbb = h16x2{-ab.y, -ab.y};
+    } else if constexpr (T == AESIR_GGML_Q3_K) {
+        const uint8_t *blk = src + (k / 256) * 110;
+        const int i = (int)(k % 256), is = 8 * (i / 128) + 2 * ((i / 32) & 3) + (i / 16 & 1);
+        const h16 a = q6k_scale(f16_at(blk + 108), q3k_scale(blk + 96, is));
+        aa = h16x2{a, a};
     } else {
         const uint8_t *blk = src + (k / 256) * 210;
-        const h16 a = q6k_scale(bits_to_h((uint16_t)(blk[208] | (blk[209] << 8))), (int8_t)blk[192 + (k % 256) / 16]);
+        const h16 a = q6k_scale(f16_at(blk + 208), (int8_t)blk[192 + (k % 256) / 16]);
         aa = h16x2{a, a};
     }
     unsigned wp[8];  // natural pairs (2 i, 2 i + 1)
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         const int q0 = gguf_q<T>(src, k + 2 * i), q1 = gguf_q<T>(src, k + 2 * i + 1);
+        auto pair = [](int a, int b) { return h16x2{(h16)(float)a, (h16)(float)b}; };
         if constexpr (T == AESIR_GGML_Q4_0)
-            wp[i] = h2_bits(q4_0_w2(h16x2{(h16)(float)(q0 - 8), (h16)(float)(q1 - 8)}, aa));
+            wp[i] = h2_bits(q4_0_w2(pair(q0 - 8, q1 - 8), aa));
+        else if constexpr (T == AESIR_GGML_Q5_0)
+            wp[i] = h2_bits(q4_0_w2(pair(q0 - 16, q1 - 16), aa));
         else if constexpr (T == AESIR_GGML_Q8_0)  // f16(f16(q) * d), as the Q8_0 GEMV
             wp[i] = h2_bits(h16x2{(h16)((float)q0 * (float)aa.x), (h16)((float)q1 * (float)aa.x)});
-        else if constexpr (T == AESIR_GGML_Q4_K)
-            wp[i] = h2_bits(q4k_w2(h16x2{(h16)(float)q0, (h16)(float)q1}, aa, nbb));
+        else if constexpr (T == AESIR_GGML_Q4_1 || T == AESIR_GGML_Q5_1)
+            wp[i] = h2_bits(q4_1_w2(pair(q0, q1), aa, nbb));
+        else if constexpr (T == AESIR_GGML_Q4_K || T == AESIR_GGML_Q5_K || T == AESIR_GGML_Q2_K)
+            wp[i] = h2_bits(q4k_w2(pair(q0, q1), aa, nbb));
+        else if constexpr (T == AESIR_GGML_Q3_K)
+            wp[i] = h2_bits(q6k_w2(pair(q0, q1), aa));
         else
-            wp[i] = h2_bits(q6k_w2(h16x2{(h16)(float)(q0 - 32), (h16)(float)(q1 - 32)}, aa));
+            wp[i] = h2_bits(q6k_w2(pair(q0 - 32, q1 - 32), aa));
     }
     h16 *dst = out + r * out_stride + k;
     st16(dst, u32x4{wp[0], wp[1], wp[2], wp[3]});
@@ -408,28 +476,51 @@ int32_t launch_qf_dequant(hipStream_t s, const QFMat &w, int64_t rows, int64_t K
     return AESIR_OK;
 }
 
+int64_t gguf_block_elems(int32_t type) {
+    switch (type) {
+        case AESIR_GGML_Q4_0:
+        case AESIR_GGML_Q4_1:
+        case AESIR_GGML_Q5_0:
+        case AESIR_GGML_Q5_1:
+        case AESIR_GGML_Q8_0: return 32;
+        case AESIR_GGML_Q2_K:
+        case AESIR_GGML_Q3_K:
+        case AESIR_GGML_Q4_K:
+        case AESIR_GGML_Q5_K:
+        case AESIR_GGML_Q6_K: return 256;
+        default: return 0;
+    }
+}
+
 int32_t launch_gguf_dequant(hipStream_t s, int32_t type, const void *blocks, int64_t rows, int64_t K, void *out,
                             int64_t out_stride) {
-    if (type == AESIR_GGML_Q8_0) {
-        if (K <= 0 || K % 32 != 0)
-            return fail(AESIR_ERR_SHAPE, "gguf_dequant: row length %lld is not a multiple of the 32-weight block", (long long)K);
-    } else {
-        AESIR_TRY(qf_check(type, K, "gguf_dequant"));
-    }
+    const int64_t blk = gguf_block_elems(type);
+    if (blk == 0) return fail(AESIR_ERR_UNSUPPORTED, "gguf_dequant: GGML type %d is not a block type of this library", (int)type);
+    if (K <= 0 || K % blk != 0)
+        return fail(AESIR_ERR_SHAPE, "gguf_dequant: row length %lld is not a multiple of the %lld-weight block",
+                    (long long)K, (long long)blk);
     if (out_stride < K || out_stride % 8 != 0 || ((uintptr_t)out & 15) != 0)
         return fail(AESIR_ERR_SHAPE, "gguf_dequant: output rows must be 16-byte aligned and hold K weights");
     if (rows <= 0) return AESIR_OK;
     const unsigned g = rec_grid(rows, K);
     const uint8_t *b = (const uint8_t *)blocks;
     h16 *o = (h16 *)out;
-    if (type == AESIR_GGML_Q4_0)
-        hipLaunchKernelGGL(gguf_dequant_kernel<AESIR_GGML_Q4_0>, dim3(g), dim3(256), 0, s, b, rows, K, o, out_stride);
-    else if (type == AESIR_GGML_Q8_0)
-        hipLaunchKernelGGL(gguf_dequant_kernel<AESIR_GGML_Q8_0>, dim3(g), dim3(256), 0, s, b, rows, K, o, out_stride);
-    else if (type == AESIR_GGML_Q4_K)
-        hipLaunchKernelGGL(gguf_dequant_kernel<AESIR_GGML_Q4_K>, dim3(g), dim3(256), 0, s, b, rows, K, o, out_stride);
-    else
-        hipLaunchKernelGGL(gguf_dequant_kernel<AESIR_GGML_Q6_K>, dim3(g), dim3(256), 0, s, b, rows, K, o, out_stride);
+#define AESIR_GD(TY)                                                                                               \
+    case TY: hipLaunchKernelGGL(gguf_dequant_kernel<TY>, dim3(g), dim3(256), 0, s, b, rows, K, o, out_stride); break
+    switch (type) {
+        AESIR_GD(AESIR_GGML_Q4_0);
+        AESIR_GD(AESIR_GGML_Q4_1);
+        AESIR_GD(AESIR_GGML_Q5_0);
+        AESIR_GD(AESIR_GGML_Q5_1);
+        AESIR_GD(AESIR_GGML_Q8_0);
+        AESIR_GD(AESIR_GGML_Q2_K);
+        AESIR_GD(AESIR_GGML_Q3_K);
+        AESIR_GD(AESIR_GGML_Q4_K);
+        AESIR_GD(AESIR_GGML_Q5_K);
+        AESIR_GD(AESIR_GGML_Q6_K);
+        default: break;
+    }
+#undef AESIR_GD
     AESIR_LAUNCH_CHECK("gguf_dequant_kernel");
     return AESIR_OK;
 }

@@ -102,7 +102,7 @@ def test_gguf_freq_base_recorded_not_applied(A, oracle, tiny_gguf):
     ("rope_dim", "GGUF RoPE dimension does not match attention head size"),
     ("alignment", "GGUF alignment must be a power of two up to 4096"),
     ("eos", "Tokenizer eos_token_id is out of bounds"),
-    ("q4_1", "Real inference slice supports only F16 and F32 tensors"),
+    ("q8_1", "Real inference slice supports only F16 and F32 tensors"),
     ("f32_matrix", "GGUF required tensor has an invalid type: output.weight"),
     ("overflow", "GGUF tensor byte size overflows the file: token_embd.weight"),
     ("huge", "GGUF tensor byte size overflows the file: token_embd.weight"),
@@ -143,8 +143,8 @@ def test_gguf_contract_errors(A, tiny_gguf, mutation, message):
         size = os.path.getsize(path)
         with open(path, "r+b") as f:
             f.truncate(size - 100)
-    if mutation in ("q4_1", "overflow", "huge"):
-        # q4_1: rewrite the type field of the first tensor to GGML Q4_1 (3), which neither loader
+    if mutation in ("q8_1", "overflow", "huge"):
+        # q8_1: rewrite the type field of the first tensor to GGML Q8_1 (9), which neither loader
         # takes; overflow: dims whose element count wraps int64 (2^33 x 2^31); huge: dims whose
         # byte size fits int64 but exceeds the file (2^20 x 2^20)
         raw = bytearray(open(path, "rb").read())
@@ -152,8 +152,8 @@ def test_gguf_contract_errors(A, tiny_gguf, mutation, message):
         i = raw.index(name) + len(name)
         ndim = int.from_bytes(raw[i:i + 4], "little")
         tpos = i + 4 + 8 * ndim
-        if mutation == "q4_1":
-            raw[tpos:tpos + 4] = (3).to_bytes(4, "little")
+        if mutation == "q8_1":
+            raw[tpos:tpos + 4] = (9).to_bytes(4, "little")
         else:
             ne0, ne1 = (1 << 33, 1 << 31) if mutation == "overflow" else (1 << 20, 1 << 20)
             raw[i + 4:i + 12] = ne0.to_bytes(8, "little")

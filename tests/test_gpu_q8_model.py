@@ -244,8 +244,8 @@ def test_q8_errors(A, ctx):
     bad = A.ModelConfig(80, 1, 4, 4, 256, 64, 16)
     with pytest.raises(A.AesirError, match="Q8_0 weights need dim and ffn to be multiples of 32"):
         A.Model.create(ctx, bad, A.GGML_Q8_0)
-    with pytest.raises(A.AesirError, match="weight type 3 is not F16, Q8_0, Q4_0, Q4_K or Q6_K"):
-        A.Model.create(ctx, A.ModelConfig(64, 1, 4, 4, 64, 64, 16), 3)  # GGML Q4_1
+    with pytest.raises(A.AesirError, match="weight type 9 is not F16, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q2_K"):
+        A.Model.create(ctx, A.ModelConfig(64, 1, 4, 4, 64, 64, 16), 9)  # GGML Q8_1
     m = A.Model.create(ctx, A.ModelConfig(64, 1, 4, 4, 64, 64, 16), A.GGML_Q8_0)
     with pytest.raises(A.AesirError, match="invalid type: blk.0.attn_q.weight"):
         m.set_tensor("blk.0.attn_q.weight", np.zeros((64, 64), np.float16))

@@ -141,8 +141,10 @@ def test_gemm_quant_errors(A, ctx):
         A.gemm_quant(ctx, a, a.ptr, 12, 2, c)
     with pytest.raises(A.AesirError, match="gemm_q6_k: output matrix shape mismatch"):
         A.gemm_quant(ctx, ctx.tensor(1, 256), a.ptr, 14, 3, c)
-    with pytest.raises(A.AesirError, match="is not Q4_0, Q8_0, Q4_K or Q6_K"):
-        A.gemm_quant(ctx, a, a.ptr, 3, 2, c)
+    with pytest.raises(A.AesirError, match="is not Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K or Q6_K"):
+        A.gemm_quant(ctx, a, a.ptr, 9, 2, c)
+    with pytest.raises(A.AesirError, match="gemm_q5_k: inner dimension must be a multiple of 256"):
+        A.gemm_quant(ctx, a, a.ptr, 13, 2, c)
 
 
 def quant_weights(A, oracle, cfg, kind, rng):

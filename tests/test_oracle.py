@@ -834,3 +834,226 @@ def test_k_quant_random_blocks_match_the_formula(oracle):
     sub16 = np.arange(cols) // 16
     want6 = d.astype(np.float64)[:, sub16 // 16] * s6.astype(np.float64).reshape(rows, -1)[:, sub16] * (q6.astype(np.float64) - 32)
     assert np.all(np.abs(got6 - want6) <= 2.0 ** -24 * np.abs(want6))
+
+
+# ---------------------------------------------------------------- Q4_1 / Q5_0 / Q5_1 blocks
+
+def _legacy_block(kind, d, m, qh, qs_byte):
+    """One GGUF block, byte by byte: d, (m), (qh[4]), qs[16] all equal to qs_byte."""
+    blk = [np.array([d], np.float16).view(np.uint8)]
+    if kind in ("q4_1", "q5_1"):
+        blk.append(np.array([m], np.float16).view(np.uint8))
+    if kind in ("q5_0", "q5_1"):
+        blk.append(np.array(qh, np.uint8))
+    blk.append(np.full(16, qs_byte, np.uint8))
+    return np.concatenate(blk).reshape(1, -1)
+
+
+def test_legacy_reference_kats(oracle):
+    """tests/test_legacy_quantization.mojo:48-185, the blocks built there (SIMD constructors splat a
+    scalar, so qh = [1, 1, 1, 1]: elements 0, 8, 16 and 24 carry the fifth bit):
+    Q4_1 d 2, m 1, qs 0x31 -> 1 * 2 + 1 = 3 (lower 16), 3 * 2 + 1 = 7 (upper 16);
+    Q5_0 d 0.5, qs 0x31 -> (1 - 16) 0.5 = -7.5, (3 - 16) 0.5 = -6.5, and 0.5, 1.5 where the bit is set;
+    Q5_1 d 0.5, m 0.2 -> f16(f16(q 0.5) + f16(0.2)) for q = 1, 3, 17, 19.
+    With A = ones, gemm_q* equals gemm_f16 on the dequantized weights (the reference's assertion)."""
+    hb = np.zeros(32, bool)
+    hb[[0, 8, 16, 24]] = True
+    lo = np.r_[np.ones(16), np.full(16, 3)] + 16 * hb  # 5-bit values
+    cases = {
+        "q4_1": (_legacy_block("q4_1", 2.0, 1.0, None, 0x31), np.r_[np.full(16, 3.0), np.full(16, 7.0)]),
+        "q5_0": (_legacy_block("q5_0", 0.5, None, [1, 1, 1, 1], 0x31), (lo - 16) * 0.5),
+        "q5_1": (_legacy_block("q5_1", 0.5, 0.2, [1, 1, 1, 1], 0x31),
+                 (np.float16(lo * 0.5).astype(np.float64) + float(np.float16(0.2))).astype(np.float16)),
+    }
+    for kind, (blk, want) in cases.items():
+        w = oracle.dequantize_legacy(kind, blk, 1)
+        assert np.array_equal(w, np.asarray(want, np.float16)), kind
+        a = np.ones((1, 32), np.float16)
+        assert oracle.gemm_legacy(kind, a, blk, 1)[0, 0] == oracle.gemm_f16(a, w.reshape(1, 32))[0, 0], kind
+    assert oracle.dequantize_legacy("q5_1", cases["q5_1"][0], 1)[0] == np.float16(8.703125)  # 8.5 + 0.2 rounded
+
+
+def test_legacy_fifth_bit_positions(oracle):
+    """Closed form: with one qh bit j set (d 1, every nibble 0), only element j reads 16; the rest 0
+    (Q5_0: -16 and 0; Q5_1 m = 0: 0 and 16)."""
+    for j in range(32):
+        qh = [0, 0, 0, 0]
+        qh[j // 8] = 1 << (j % 8)
+        w0 = oracle.dequantize_legacy("q5_0", _legacy_block("q5_0", 1.0, None, qh, 0), 1)
+        w1 = oracle.dequantize_legacy("q5_1", _legacy_block("q5_1", 1.0, 0.0, qh, 0), 1)
+        want = np.zeros(32)
+        want[j] = 16
+        assert np.array_equal(w0, (want - 16).astype(np.float16)) and np.array_equal(w1, want.astype(np.float16)), j
+
+
+@pytest.mark.parametrize("kind", ["q4_1", "q5_0", "q5_1"])
+def test_legacy_pack_dequant_and_gemm(oracle, kind):
+    """Random blocks through the host packers: the oracle's weights equal the rule evaluated in
+    float64 with numpy's correctly rounded float64 -> float16 at each f16 operation; the gemm is
+    within 1 f16 ulp of f64 on those weights; the packers' nibble and fifth-bit order is the one
+    the closed forms above pin."""
+    import aesir_hip as A
+
+    rng = np.random.default_rng({"q4_1": 41, "q5_0": 50, "q5_1": 51}[kind])
+    rows, cols = 6, 128
+    d = rng.uniform(0.001, 0.05, (rows, cols // 32)).astype(np.float16)
+    m = rng.uniform(-0.1, 0.1, (rows, cols // 32)).astype(np.float16)
+    q = rng.integers(0, 16 if kind == "q4_1" else 32, (rows, cols))
+    t = {"q4_1": lambda: A.Q4_1Tensor.from_parts(d, m, q), "q5_0": lambda: A.Q5_0Tensor.from_parts(d, q),
+         "q5_1": lambda: A.Q5_1Tensor.from_parts(d, m, q)}[kind]()
+    dd, mm = np.repeat(d.astype(np.float64), 32, axis=1), np.repeat(m.astype(np.float64), 32, axis=1)
+    if kind == "q5_0":
+        ref = ((q - 16) * dd).astype(np.float16)
+    else:
+        ref = ((q * dd).astype(np.float16).astype(np.float64) + mm).astype(np.float16)
+    got = oracle.dequantize_legacy(kind, t.blocks, rows * cols // 32).reshape(rows, cols)
+    assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+    x = rng.standard_normal((3, cols)).astype(np.float16)
+    c = oracle.gemm_legacy(kind, x, t.blocks, rows)
+    exact = x.astype(np.float64) @ ref.astype(np.float64).T
+    assert np.all(np.abs(c.astype(np.float64) - exact) <= np.abs(np.spacing(c)).astype(np.float64) + 1e-6)
+    with pytest.raises(oracle.OracleError, match="inner dimension must be a multiple of 32"):
+        oracle.gemm_legacy(kind, np.ones((1, 40), np.float16), t.blocks, 1)
+
+
+# ---------------------------------------------------------------- Q5_K / Q2_K / Q3_K super-blocks
+
+def _q5_k_literal_block():
+    """block_q5_K byte by byte: Q4_K's literal d, dmin, scales and nibbles, and qh[l] =
+    0b10100101 ^ l (bit 2 g + hi of qh[l] is the fifth bit of weight 64 g + 32 hi + l)."""
+    b4, sc, mn, _ = _q4_k_literal_block()
+    qh = (0b10100101 ^ np.arange(32)).astype(np.uint8)
+    blk = np.concatenate([b4[0:16], qh, b4[16:]])
+    want = np.zeros(256)
+    l = np.arange(32)
+    for g in range(4):
+        for hi in range(2):
+            nib = (l % 16) if hi == 0 else (15 - l % 16)
+            q = nib + 16 * ((qh >> (2 * g + hi)) & 1)
+            want[64 * g + 32 * hi + l] = 0.5 * sc[2 * g + hi] * q - 0.25 * mn[2 * g + hi]
+    return blk, sc, mn, want
+
+
+def _q2_k_literal_block():
+    """block_q2_K byte by byte: scales[is] = (is + 1) & 15 | (15 - is) << 4, qs[32 h + l] =
+    (l * 37 + 11 h) & 255, d 0.5, dmin 0.25: weight 128 h + 32 j + l = 0.5 sc q - 0.25 m with
+    q = (qs[32 h + l] >> 2 j) & 3 and sub-block 8 h + 2 j + l // 16."""
+    blk = np.zeros(84, np.uint8)
+    sc = (np.arange(16) + 1) & 15
+    mn = 15 - np.arange(16)
+    blk[0:16] = sc | (mn << 4)
+    for h in range(2):
+        blk[16 + 32 * h:48 + 32 * h] = (np.arange(32) * 37 + 11 * h) & 255
+    blk[80:82] = np.array([0.5], np.float16).view(np.uint8)
+    blk[82:84] = np.array([0.25], np.float16).view(np.uint8)
+    want = np.zeros(256)
+    for h in range(2):
+        for j in range(4):
+            for l in range(32):
+                q = (int(blk[16 + 32 * h + l]) >> (2 * j)) & 3
+                s = 8 * h + 2 * j + l // 16
+                want[128 * h + 32 * j + l] = 0.5 * sc[s] * q - 0.25 * mn[s]
+    return blk, sc, mn, want
+
+
+def _q3_k_literal_block():
+    """block_q3_K byte by byte: sixteen 6-bit scales u = (5 is + 7) & 63 (value u - 32) packed low
+    nibbles in bytes 0-7 (is < 8 low, is >= 8 high) and high 2 bits at bits 2 (is / 4) of byte
+    8 + is % 4; hmask[l] = (l * 29 + 3) & 255, qs[32 h + l] = (l * 53 + 7 h) & 255, d 0.125:
+    weight 128 h + 32 j + l = 0.125 (u - 32) (q - 4 unless bit 4 h + j of hmask[l])."""
+    blk = np.zeros(110, np.uint8)
+    u = (5 * np.arange(16) + 7) & 63
+    blk[0:32] = (np.arange(32) * 29 + 3) & 255
+    for h in range(2):
+        blk[32 + 32 * h:64 + 32 * h] = (np.arange(32) * 53 + 7 * h) & 255
+    for i in range(16):
+        if i < 8:
+            blk[96 + i] |= u[i] & 15
+        else:
+            blk[96 + i - 8] |= (u[i] & 15) << 4
+        blk[104 + i % 4] |= (u[i] >> 4) << (2 * (i // 4))
+    blk[108:110] = np.array([0.125], np.float16).view(np.uint8)
+    want = np.zeros(256)
+    for h in range(2):
+        for j in range(4):
+            for l in range(32):
+                q = (int(blk[32 + 32 * h + l]) >> (2 * j)) & 3
+                if not (int(blk[l]) >> (4 * h + j)) & 1:
+                    q -= 4
+                want[128 * h + 32 * j + l] = 0.125 * (u[8 * h + 2 * j + l // 16] - 32) * q
+    return blk, u - 32, want
+
+
+def test_kquant_literal_blocks(oracle):
+    """GGML block_q5_K / _q2_K / _q3_K decoded from hand-built blocks: every weight equals its
+    sub-block's formula (all products exact in f32), the library's f16 rule equals it too where it
+    is representable, and the host packers produce the same bytes."""
+    import aesir_hip as A
+
+    blk, sc, mn, want = _q5_k_literal_block()
+    assert np.array_equal(oracle.dequantize_kquant("q5_k", blk.reshape(1, -1), 1), want.astype(np.float32))
+    q = np.zeros(256, np.uint8)
+    qh = blk[16:48]
+    for g in range(4):
+        for hi in range(2):
+            nib = (np.arange(32) % 16) if hi == 0 else (15 - np.arange(32) % 16)
+            q[64 * g + 32 * hi:64 * g + 32 * hi + 32] = nib + 16 * ((qh >> (2 * g + hi)) & 1)
+    t = A.Q5_KTensor.from_parts(np.array([[0.5]], np.float16), np.array([[0.25]], np.float16),
+                                np.array(sc, np.uint8).reshape(1, 1, 8), np.array(mn, np.uint8).reshape(1, 1, 8),
+                                q.reshape(1, 256))
+    assert np.array_equal(t.blocks[0], blk)
+    assert np.array_equal(oracle.dequantize_kquant_f16("q5_k", blk.reshape(1, -1), 1), want.astype(np.float16))
+
+    blk, sc, mn, want = _q2_k_literal_block()
+    assert np.array_equal(oracle.dequantize_kquant("q2_k", blk.reshape(1, -1), 1), want.astype(np.float32))
+    q = np.zeros(256, np.uint8)
+    for h in range(2):
+        for j in range(4):
+            q[128 * h + 32 * j:128 * h + 32 * j + 32] = (blk[16 + 32 * h:48 + 32 * h] >> (2 * j)) & 3
+    t = A.Q2_KTensor.from_parts(np.array([[0.5]], np.float16), np.array([[0.25]], np.float16),
+                                sc.reshape(1, 1, 16), mn.reshape(1, 1, 16), q.reshape(1, 256))
+    assert np.array_equal(t.blocks[0], blk)
+    assert np.array_equal(oracle.dequantize_kquant_f16("q2_k", blk.reshape(1, -1), 1), want.astype(np.float16))
+
+    blk, s3, want = _q3_k_literal_block()
+    assert np.array_equal(oracle.dequantize_kquant("q3_k", blk.reshape(1, -1), 1), want.astype(np.float32))
+    q = np.zeros(256, np.int16)
+    for h in range(2):
+        for j in range(4):
+            for l in range(32):
+                v = (int(blk[32 + 32 * h + l]) >> (2 * j)) & 3
+                q[128 * h + 32 * j + l] = v if (int(blk[l]) >> (4 * h + j)) & 1 else v - 4
+    t = A.Q3_KTensor.from_parts(np.array([[0.125]], np.float16), s3.reshape(1, 1, 16), q.reshape(1, 256))
+    assert np.array_equal(t.blocks[0], blk)
+    assert np.array_equal(oracle.dequantize_kquant_f16("q3_k", blk.reshape(1, -1), 1), want.astype(np.float16))
+
+
+def test_kquant_f16_rule_random(oracle):
+    """Random Q5_K / Q2_K / Q3_K super-blocks: the library's f16 weights equal numpy's float64 ->
+    float16 rounding of f16(d sc) q - f16(dmin m) (Q3_K: f16(d sc) q), and stay within half an f16
+    ulp plus the scale roundings of GGML's f32 weights."""
+    import aesir_hip as A
+
+    rng = np.random.default_rng(235)
+    rows, cols = 4, 512
+    nsb = cols // 256
+    d = rng.uniform(1e-4, 0.01, (rows, nsb)).astype(np.float16)
+    dmin = rng.uniform(1e-4, 0.01, (rows, nsb)).astype(np.float16)
+    cases = []
+    sc, mn, q = rng.integers(0, 64, (rows, nsb, 8)), rng.integers(0, 64, (rows, nsb, 8)), rng.integers(0, 32, (rows, cols))
+    cases.append(("q5_k", A.Q5_KTensor.from_parts(d, dmin, sc, mn, q), sc.reshape(rows, -1), mn.reshape(rows, -1), q, 32))
+    sc, mn, q = rng.integers(0, 16, (rows, nsb, 16)), rng.integers(0, 16, (rows, nsb, 16)), rng.integers(0, 4, (rows, cols))
+    cases.append(("q2_k", A.Q2_KTensor.from_parts(d, dmin, sc, mn, q), sc.reshape(rows, -1), mn.reshape(rows, -1), q, 16))
+    sc, q = rng.integers(-32, 32, (rows, nsb, 16)), rng.integers(-4, 4, (rows, cols))
+    cases.append(("q3_k", A.Q3_KTensor.from_parts(d, sc, q), sc.reshape(rows, -1), np.zeros((rows, nsb * 16)), q, 16))
+    for kind, t, s, m, q, sub_n in cases:
+        sub = np.arange(cols) // sub_n
+        dd = d.astype(np.float64)[:, np.arange(cols) // 256]
+        a = (dd * s[:, sub]).astype(np.float16).astype(np.float64)
+        b = (dmin.astype(np.float64)[:, np.arange(cols) // 256] * m[:, sub]).astype(np.float16).astype(np.float64)
+        got = oracle.dequantize_kquant_f16(kind, t.blocks, rows * nsb).reshape(rows, cols)
+        assert np.array_equal(got.view(np.uint16), (a * q - b).astype(np.float16).view(np.uint16)), kind
+        f32 = oracle.dequantize_kquant(kind, t.blocks, rows * nsb).reshape(rows, cols).astype(np.float64)
+        rel = 2.0 ** -11 * (1 + 2.0 ** -10)
+        bound = np.abs(np.spacing(got)).astype(np.float64) / 2 + np.abs(q) * np.abs(a) * rel + np.abs(b) * rel
+        assert np.all(np.abs(got.astype(np.float64) - f32) <= bound), kind

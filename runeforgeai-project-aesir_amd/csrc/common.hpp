@@ -90,6 +90,23 @@ inline GgmlBlock ggml_block(int64_t type) {
         default: return {0, 0};
     }
 }
+inline const char *ggml_type_name(int64_t type) {
+    switch (type) {
+        case AESIR_GGML_F32: return "F32";
+        case AESIR_GGML_F16: return "F16";
+        case AESIR_GGML_Q4_0: return "Q4_0";
+        case AESIR_GGML_Q4_1: return "Q4_1";
+        case AESIR_GGML_Q5_0: return "Q5_0";
+        case AESIR_GGML_Q5_1: return "Q5_1";
+        case AESIR_GGML_Q8_0: return "Q8_0";
+        case AESIR_GGML_Q2_K: return "Q2_K";
+        case AESIR_GGML_Q3_K: return "Q3_K";
+        case AESIR_GGML_Q4_K: return "Q4_K";
+        case AESIR_GGML_Q5_K: return "Q5_K";
+        case AESIR_GGML_Q6_K: return "Q6_K";
+        default: return "?";
+    }
+}
 // Bytes of a rows x cols tensor of a GGML type: -1 for an unknown type, -2 when cols is not a
 // multiple of the block, -3 on overflow.
 inline int64_t ggml_tensor_bytes(int64_t type, int64_t rows, int64_t cols) {

@@ -27,35 +27,49 @@ int32_t launch_gemm_f16(aesir_ctx *ctx, const void *A, int64_t M, int64_t K, con
 int32_t launch_gemm_f16_mfma(aesir_ctx *ctx, const void *A, int64_t M, int64_t K, const void *B, int64_t N,
                              void *C);
 
-// A Q4_0, Q4_K or Q6_K matrix [N][K] in HBM (quant.hip), repacked from its GGUF blocks into
-// records of 16 weights: record r of a row holds weights 16 r .. 16 r + 15.
+// A Q4_0, Q4_1, Q5_0, Q5_1, Q4_K, Q5_K or Q6_K matrix [N][K] in HBM (quant.hip), repacked from
+// its GGUF blocks into records of 16 weights: record r of a row holds weights 16 r .. 16 r + 15.
 //   nib  8 bytes per record: byte j holds weight 16 r + j in its low nibble and 16 r + 8 + j in
-//        its high nibble (Q6_K: the low 4 of the 6 bits);
-//   hb   Q6_K only, 4 bytes per record: the high 2 bits of the record's weights (bit layout in
+//        its high nibble (Q5_*, Q6_K: the low 4 bits);
+//   hb   Q6_K: 4 bytes per record, the high 2 bits of the record's weights; Q5_0 / Q5_1 / Q5_K:
+//        4 bytes per record pair, the fifth bits of both records in one word (bit layout in
 //        quant.hip, qf_hb_pos);
-//   s0   Q4_0: f16 d per 32 weights; Q4_K: (scale, min) bytes per 32 weights, 6-bit values
-//        unpacked; Q6_K: int8 scale per 16 weights;
-//   s1   Q4_K: (d, dmin) f16 pair per 256 weights; Q6_K: f16 d per 256 weights.
+//   s0   Q4_0 / Q5_0: f16 d per 32 weights; Q4_1 / Q5_1: f16 d | f16 m << 16 per 32 weights;
+//        Q4_K / Q5_K: (scale, min) bytes per 32 weights, 6-bit values unpacked; Q6_K: int8 scale
+//        per 16 weights;
+//   s1   Q4_K / Q5_K: (d, dmin) f16 pair per 256 weights; Q6_K: f16 d per 256 weights.
 // The nib, hb and s0 planes are tiled for the matrix-core GEMV: rows in blocks of 16 and records
 // in segments of 8 (128 weights, K a multiple of 128); tile (row block, segment) stores, for
-// record pair q = (record % 8) / 2 and row i of the block, the pair's 16 nibble bytes (8 hb bytes,
-// 2 s0 bytes) at [q][i], so that lane l of a wave reading 16 (8, 2) bytes at l times that size
-// gets row l % 16 and record pair l / 16: the A-operand layout of v_mfma_f32_16x16x32_f16. s1 is
-// [row block][K / 256][row % 16] (the 16 rows' entries of a super-block together). Planes hold
-// qf_rows_alloc(N) rows (whole row blocks). Logical row r of a fused sub-matrix is plane row
-// row0 + r * step (step 2 for the interleaved gate/up rows).
+// record pair q = (record % 8) / 2 and row i of the block, the pair's 16 nibble bytes (8 or 4 hb
+// bytes, 2 or 4 s0 bytes) at [q][i], so that lane l of a wave reading that many bytes at l times
+// that size gets row l % 16 and record pair l / 16: the A-operand layout of
+// v_mfma_f32_16x16x32_f16. s1 is [row block][K / 256][row % 16] (the 16 rows' entries of a
+// super-block together). Planes hold qf_rows_alloc(N) rows (whole row blocks). Logical row r of
+// a fused sub-matrix is plane row row0 + r * step (step 2 for the interleaved gate/up rows).
 struct QFMat {
     int32_t type = 0;
     const void *nib = nullptr, *hb = nullptr, *s0 = nullptr, *s1 = nullptr;
     int64_t row0 = 0;
 };
+// hb bytes per record pair (0 without the plane) and s0 bytes per record pair.
+__host__ __device__ inline int qf_hb_bytes(int32_t type) {
+    return type == AESIR_GGML_Q6_K ? 8
+           : (type == AESIR_GGML_Q5_0 || type == AESIR_GGML_Q5_1 || type == AESIR_GGML_Q5_K) ? 4
+                                                                                            : 0;
+}
+__host__ __device__ inline int qf_s0_bytes(int32_t type) {
+    return (type == AESIR_GGML_Q4_1 || type == AESIR_GGML_Q5_1) ? 4 : 2;
+}
 // Bytes of one row of each plane (0 if the type has no such plane). plane: 0 nib, 1 hb, 2 s0, 3 s1.
 __host__ __device__ inline int64_t qf_plane_row_bytes(int32_t type, int plane, int64_t K) {
     switch (plane) {
         case 0: return K / 2;
-        case 1: return type == AESIR_GGML_Q6_K ? K / 4 : 0;
-        case 2: return type == AESIR_GGML_Q6_K ? K / 16 : K / 32 * 2;
-        case 3: return type == AESIR_GGML_Q4_K ? K / 256 * 4 : type == AESIR_GGML_Q6_K ? K / 256 * 2 : 0;
+        case 1: return K / 32 * qf_hb_bytes(type);
+        case 2: return K / 32 * qf_s0_bytes(type);
+        case 3:
+            return (type == AESIR_GGML_Q4_K || type == AESIR_GGML_Q5_K) ? K / 256 * 4
+                   : type == AESIR_GGML_Q6_K                          ? K / 256 * 2
+                                                                      : 0;
         default: return 0;
     }
 }
@@ -66,13 +80,17 @@ __host__ __device__ inline int64_t qf_tile(int64_t r, int64_t rec, int64_t K) { 
 __host__ __device__ inline int64_t qf_nib_off(int64_t r, int64_t rec, int64_t K) {
     return qf_tile(r, rec, K) * 1024 + ((rec & 7) >> 1) * 256 + (r & 15) * 16 + (rec & 1) * 8;
 }
-__host__ __device__ inline int64_t qf_hbw_off(int64_t r, int64_t rec, int64_t K) {
-    return qf_tile(r, rec, K) * 512 + ((rec & 7) >> 1) * 128 + (r & 15) * 8 + (rec & 1) * 4;
+// hb entry of the record's pair (es = qf_hb_bytes); Q6_K's word of the record is at + 4 (rec & 1)
+__host__ __device__ inline int64_t qf_hb_pair_off(int64_t r, int64_t rec, int64_t K, int es) {
+    return qf_tile(r, rec, K) * 64 * es + ((rec & 7) >> 1) * 16 * es + (r & 15) * es;
 }
-// s0 entry of the record's pair (Q4_0 d, Q4_K scale | min << 8); Q6_K's byte of the record is at
-// + (rec & 1)
-__host__ __device__ inline int64_t qf_s0_off(int64_t r, int64_t rec, int64_t K) {
-    return qf_tile(r, rec, K) * 128 + ((rec & 7) >> 1) * 32 + (r & 15) * 2;
+__host__ __device__ inline int64_t qf_hbw_off(int64_t r, int64_t rec, int64_t K) {
+    return qf_hb_pair_off(r, rec, K, 8) + (rec & 1) * 4;
+}
+// s0 entry of the record's pair (es = qf_s0_bytes: Q4_0 / Q5_0 d, Q4_1 / Q5_1 d | m << 16,
+// Q4_K / Q5_K scale | min << 8); Q6_K's byte of the record is at + (rec & 1)
+__host__ __device__ inline int64_t qf_s0_off(int64_t r, int64_t rec, int64_t K, int es = 2) {
+    return qf_tile(r, rec, K) * 64 * es + ((rec & 7) >> 1) * 16 * es + (r & 15) * es;
 }
 __host__ __device__ inline int64_t qf_s1_off(int64_t r, int64_t rec, int64_t K, int esize) {
     return (((r >> 4) * (K >> 8) + (rec >> 4)) * 16 + (r & 15)) * esize;

@@ -501,18 +501,18 @@ int32_t model_create(aesir_ctx *ctx, const aesir_model_config *cfg, const Weight
             // kept in f16, dequantized at upload: whole blocks per row
             const int64_t blk = gguf_block_elems(wt);
             if (c.dim % blk != 0 || c.ffn % blk != 0)
-                return fail(AESIR_ERR_UNSUPPORTED, "model: GGML type %d weights need dim and ffn to be multiples of %lld",
-                            (int)wt, (long long)blk);
+                return fail(AESIR_ERR_UNSUPPORTED, "model: %s weights need dim and ffn to be multiples of %lld",
+                            ggml_type_name(wt), (long long)blk);
         }
         if (wt == AESIR_GGML_Q8_0 && (c.dim % 32 != 0 || c.ffn % 32 != 0 || c.dim > 16384 || c.ffn > 16384))
             return fail(AESIR_ERR_UNSUPPORTED, "model: Q8_0 weights need dim and ffn to be multiples of 32, at most 16384");
         if (qf_type(wt)) {
             // whole 128-weight segments of the repacked planes; K-quant super-blocks of 256
-            const int64_t blk = wt == AESIR_GGML_Q4_0 ? 128 : 256;
+            const int64_t blk = gguf_block_elems(wt) == 32 ? 128 : 256;
             if (c.dim % blk != 0 || c.ffn % blk != 0 || c.dim > kQfGemvMaxK || c.ffn > kQfGemvMaxK)
                 return fail(AESIR_ERR_UNSUPPORTED,
                             "model: %s weights need dim and ffn to be multiples of %lld, at most 28672",
-                            wt == AESIR_GGML_Q4_0 ? "Q4_0" : wt == AESIR_GGML_Q4_K ? "Q4_K" : "Q6_K", (long long)blk);
+                            ggml_type_name(wt), (long long)blk);
         }
     }
 

@@ -1,13 +1,15 @@
-// 4-bit and K-quant weights on gfx950: GGML Q4_0 (with the reference's gemm_q4_0 rounding,
-// core/compute.mojo:876-912) and GGML's Q4_K / Q6_K super-blocks.
+// 4-, 5- and 6-bit weights on gfx950: GGML Q4_0, Q4_1, Q5_0 and Q5_1 (with the reference's
+// gemm_q4_0 / _q4_1 / _q5_0 / _q5_1 rounding, core/compute.mojo:876-1036) and GGML's Q4_K / Q5_K /
+// Q6_K super-blocks; Q2_K and Q3_K only through gguf_dequant_kernel.
 //
-// GGUF stores these as packed blocks of 18, 144 and 210 bytes whose nibble order suits a CPU
+// GGUF stores these as packed blocks of 18 to 210 bytes whose nibble order suits a CPU
 // loop, not a wave: the bytes of one block are read by one lane, and 210 is not even 4-byte
 // aligned. At upload every matrix is repacked (QFMat in kernels.hpp) into records of 16 weights:
 // 8 nibble bytes per record, byte j holding weights j and 8 + j, so that masking a record word
 // with 0x000F000F or 0x00F000F0 and OR-ing 0x64006400 yields the f16 pair (1024 + q_a, 1024 +
 // q_b) or (1024 + 16 q_a, 1024 + 16 q_b) for weights (a, a + 2); plus small planes of per-block
-// scales and, for Q6_K, one word of high bits per record. The planes are tiled in 16-row x
+// scales and, for Q6_K, one word of high bits per record (for the 5-bit types, one word of fifth
+// bits per record pair). The planes are tiled in 16-row x
 // 128-weight tiles, so that lane l of a wave reading 16 bytes at 16 l gets two records of row
 // l % 16: the A operand of v_mfma_f32_16x16x32_f16 for four matrix-core steps once dequantized.
 // The decode GEMV dequantizes in registers and multiplies on the matrix cores.
@@ -21,6 +23,9 @@
 //         dequantize_q4_k_m (compute.mojo:245-262, q * scale + min in f16).
 //   Q6_K  w = f16(a (q - 32)) with a = f16(d * sc), f16 products as in the reference's
 //         dequantize_q6_k_block (compute.mojo:508-527).
+//   Q4_1, Q5_1  w = f16(f16(q d) + m) (dequantize_q4_1 / _q5_1, compute.mojo:282-340: the f16
+//         product, then the f16 sum); Q5_0  w = f16(f16(q - 16) d) (dequantize_q5_0);
+//   Q5_K  as Q4_K with the 5-bit q.
 // Products with x accumulate in f32 (the matrix cores, as in the F16 path's MFMA GEMMs).
 #include <type_traits>
 
@@ -34,7 +39,26 @@ constexpr int kRec = 16;                  // weights per record
 constexpr int kSeg = 128;                 // weights per tile row (8 records)
 constexpr unsigned kMagic = 0x64006400u;  // f16 1024 in both halves
 
-bool qf_type(int32_t t) { return t == AESIR_GGML_Q4_0 || t == AESIR_GGML_Q4_K || t == AESIR_GGML_Q6_K; }
+bool qf_type(int32_t t) {
+    return t == AESIR_GGML_Q4_0 || t == AESIR_GGML_Q4_1 || t == AESIR_GGML_Q5_0 || t == AESIR_GGML_Q5_1 ||
+           t == AESIR_GGML_Q4_K || t == AESIR_GGML_Q5_K || t == AESIR_GGML_Q6_K;
+}
+
+// Type families of the repacked layout: a fifth-bit word per record pair (Q5_0, Q5_1, Q5_K); an
+// f16 (d, m) pair per 32 weights (Q4_1, Q5_1); the K-quant 6-bit (scale, min) bytes with a
+// super-block (d, dmin) pair (Q4_K, Q5_K).
+template <int T>
+constexpr bool qf_hb5() {
+    return T == AESIR_GGML_Q5_0 || T == AESIR_GGML_Q5_1 || T == AESIR_GGML_Q5_K;
+}
+template <int T>
+constexpr bool qf_dm() {
+    return T == AESIR_GGML_Q4_1 || T == AESIR_GGML_Q5_1;
+}
+template <int T>
+constexpr bool qf_kq() {
+    return T == AESIR_GGML_Q4_K || T == AESIR_GGML_Q5_K;
+}
 
 // Nibble pair f of a record holds weights a and a + 2, a = {0, 1, 4, 5, 8, 9, 12, 13}[f]: pairs
 // 0-3 are low nibbles, 4-7 high nibbles. In the Q6_K high-bit word, pair f's two 2-bit fields sit
@@ -42,6 +66,9 @@ bool qf_type(int32_t t) { return t == AESIR_GGML_Q4_0 || t == AESIR_GGML_Q4_K ||
 // shift by 4 - {0, 2, 8, 10}[f & 3] serves a low pair (fields to bits 4, 20, above its nibbles)
 // and a high pair (to bits 8, 24, above its 16-scaled nibbles).
 __host__ __device__ __forceinline__ int qf_hb_off(int f) { return ((f & 1) << 1) + ((f & 2) << 2) + ((f >> 2) << 2); }
+// The 5-bit types keep a record pair's fifth bits in one word: the even record's at the low bit
+// of each Q6_K field position, the odd record's one above, so that shifting the word right by
+// the record's parity turns it into a Q6_K word whose fields hold only their low bit.
 // Bit position of the high 2 bits of record weight i.
 __host__ __device__ __forceinline__ int qf_hb_pos(int i) {
     const int a = i & ~2, f = (a & 1) | (((a >> 2) & 1) << 1) | (((a >> 3) & 1) << 2);
@@ -59,6 +86,9 @@ __device__ __forceinline__ h16 q6k_scale(h16 d, int sc) { return hmul(d, (h16)(f
 __device__ __forceinline__ h16x2 q4_0_w2(h16x2 q8, h16x2 dd) { return q8 * dd; }
 __device__ __forceinline__ h16x2 q4k_w2(h16x2 q, h16x2 aa, h16x2 nbb) { return __builtin_elementwise_fma(q, aa, nbb); }
 __device__ __forceinline__ h16x2 q6k_w2(h16x2 q32, h16x2 aa) { return q32 * aa; }
+// Q4_1 / Q5_1 weight pairs f16(f16(q d) + m): two roundings, the reference's f16 multiply then
+// add (the library is built without multiply-add contraction).
+__device__ __forceinline__ h16x2 q4_1_w2(h16x2 q, h16x2 dd, h16x2 mm) { return q * dd + mm; }
 
 // ------------------------------------------------------------------ one record
 
@@ -82,16 +112,45 @@ struct QRec<AESIR_GGML_Q6_K> {
     int sc;
     h16 d;
 };
+template <>
+struct QRec<AESIR_GGML_Q4_1> {
+    u32x2 nib;
+    unsigned dm;  // f16 d | f16 m << 16
+    unsigned hb;  // unused
+};
+template <>
+struct QRec<AESIR_GGML_Q5_1> {
+    u32x2 nib;
+    unsigned dm;
+    unsigned hb;  // the fifth bits, shifted to the even record's positions
+};
+template <>
+struct QRec<AESIR_GGML_Q5_0> {
+    u32x2 nib;
+    h16 d;
+    unsigned hb;
+};
+template <>
+struct QRec<AESIR_GGML_Q5_K> {
+    u32x2 nib;
+    unsigned scm;
+    unsigned dd;
+    unsigned hb;
+};
 
 // Record `rec` of plane row `prow`.
 template <int T>
 __device__ __forceinline__ QRec<T> qf_load(const QFMat &w, int64_t prow, int64_t rec, int64_t K) {
     QRec<T> q;
     q.nib = *reinterpret_cast<const u32x2 *>((const uint8_t *)w.nib + qf_nib_off(prow, rec, K));
-    const uint8_t *s0 = (const uint8_t *)w.s0 + qf_s0_off(prow, rec, K);
-    if constexpr (T == AESIR_GGML_Q4_0) {
+    const uint8_t *s0 = (const uint8_t *)w.s0 + qf_s0_off(prow, rec, K, qf_s0_bytes(T));
+    if constexpr (qf_hb5<T>())
+        q.hb = *reinterpret_cast<const uint32_t *>((const uint8_t *)w.hb + qf_hb_pair_off(prow, rec, K, 4)) >> (rec & 1);
+    if constexpr (T == AESIR_GGML_Q4_0 || T == AESIR_GGML_Q5_0) {
         q.d = *reinterpret_cast<const h16 *>(s0);
-    } else if constexpr (T == AESIR_GGML_Q4_K) {
+    } else if constexpr (qf_dm<T>()) {
+        q.dm = *reinterpret_cast<const uint32_t *>(s0);
+    } else if constexpr (qf_kq<T>()) {
         q.scm = *reinterpret_cast<const uint16_t *>(s0);
         q.dd = *reinterpret_cast<const uint32_t *>((const uint8_t *)w.s1 + qf_s1_off(prow, rec, K, 4));
     } else {
@@ -112,14 +171,24 @@ __device__ __forceinline__ unsigned qf_hb_pair(unsigned hb, int f) {
     const int s = 4 - qf_hb_off(f);
     return (s >= 0 ? hb << s : hb >> -s) & 0x00300030u;
 }
+// The fifth bits of nibble pair f (value 16) from a 5-bit record's shifted word.
+__device__ __forceinline__ unsigned qf_hb5_pair(unsigned hb, int f) {
+    const int s = 4 - qf_hb_off(f);
+    return (s >= 0 ? hb << s : hb >> -s) & 0x00100010u;
+}
 
-// Exact f16 pairs of the record's quantized values, pair order: Q4_0 q - 8, Q4_K q, Q6_K q - 32.
+// Exact f16 pairs of the record's quantized values, pair order: Q4_0 q - 8, Q5_0 q - 16, Q4_1 /
+// Q5_1 / Q4_K / Q5_K q, Q6_K q - 32.
 template <int T>
 __device__ __forceinline__ h16x2 qf_qpair(const QRec<T> &q, int f) {
     if constexpr (T == AESIR_GGML_Q4_0) {
         const h16x2 bias = {(h16)1032.0f, (h16)1032.0f};
         return as_h2(qf_pair(q.nib, f) | kMagic) - bias;
-    } else if constexpr (T == AESIR_GGML_Q4_K) {
+    } else if constexpr (qf_hb5<T>()) {
+        const float b = T == AESIR_GGML_Q5_0 ? 1040.0f : 1024.0f;
+        const h16x2 bias = {(h16)b, (h16)b};
+        return as_h2(qf_pair(q.nib, f) | qf_hb5_pair(q.hb, f) | kMagic) - bias;
+    } else if constexpr (T == AESIR_GGML_Q4_1 || T == AESIR_GGML_Q4_K) {
         const h16x2 bias = {(h16)1024.0f, (h16)1024.0f};
         return as_h2(qf_pair(q.nib, f) | kMagic) - bias;
     } else {
@@ -144,9 +213,13 @@ template <int T>
 __device__ __forceinline__ void qf_deq16(const QRec<T> &q, u32x4 (&o)[2]) {
     unsigned wp[8];
     h16x2 aa, nbb;
-    if constexpr (T == AESIR_GGML_Q4_0) {
+    if constexpr (T == AESIR_GGML_Q4_0 || T == AESIR_GGML_Q5_0) {
         aa = h16x2{q.d, q.d};
-    } else if constexpr (T == AESIR_GGML_Q4_K) {
+    } else if constexpr (qf_dm<T>()) {
+        const h16x2 dm = as_h2(q.dm);
+        aa = h16x2{dm.x, dm.x};
+        nbb = h16x2{dm.y, dm.y};  // the added min
+    } else if constexpr (qf_kq<T>()) {
         const h16x2 sm = {(h16)(float)(q.scm & 0xffu), (h16)(float)(q.scm >> 8)};
         const h16x2 ab = q4k_scales(as_h2(q.dd), sm);
         aa = h16x2{ab.x, ab.x};
@@ -158,8 +231,9 @@ __device__ __forceinline__ void qf_deq16(const QRec<T> &q, u32x4 (&o)[2]) {
 #pragma unroll
     for (int f = 0; f < 8; f++) {
         const h16x2 v = qf_qpair(q, f);
-        if constexpr (T == AESIR_GGML_Q4_0) wp[f] = h2_bits(q4_0_w2(v, aa));
-        else if constexpr (T == AESIR_GGML_Q4_K) wp[f] = h2_bits(q4k_w2(v, aa, nbb));
+        if constexpr (T == AESIR_GGML_Q4_0 || T == AESIR_GGML_Q5_0) wp[f] = h2_bits(q4_0_w2(v, aa));
+        else if constexpr (qf_dm<T>()) wp[f] = h2_bits(q4_1_w2(v, aa, nbb));
+        else if constexpr (qf_kq<T>()) wp[f] = h2_bits(q4k_w2(v, aa, nbb));
         else wp[f] = h2_bits(q6k_w2(v, aa));
     }
     qf_unpair(wp, o);
@@ -268,15 +342,29 @@ __global__ __launch_bounds__(256) void qf_repack_kernel(const uint8_t *__restric
         for (int i = 0; i < kRec; i++) hb |= (unsigned)(q[i] >> 4) << qf_hb_pos(i);
         *reinterpret_cast<uint32_t *>((uint8_t *)dst.hb + qf_hbw_off(prow, rec, K)) = hb;
     }
-    *reinterpret_cast<u32x2 *>((uint8_t *)dst.nib + qf_nib_off(prow, rec, K)) = u32x2{nib[0], nib[1]};
-    uint8_t *s0 = (uint8_t *)dst.s0 + qf_s0_off(prow, rec, K);
-    if constexpr (T == AESIR_GGML_Q4_0) {
+    if constexpr (qf_hb5<T>()) {  // the even record writes the pair's word (its bits and the odd record's)
         if (rec % 2 == 0) {
-            const uint8_t *blk = src + (k / 32) * 18;
-            *reinterpret_cast<uint16_t *>(s0) = (uint16_t)(blk[0] | (blk[1] << 8));
+#pragma unroll
+            for (int i = 0; i < kRec; i++) {
+                hb |= (unsigned)((q[i] >> 4) & 1) << qf_hb_pos(i);
+                hb |= (unsigned)((gguf_q<T>(src, k + kRec + i) >> 4) & 1) << (qf_hb_pos(i) + 1);
+            }
+            *reinterpret_cast<uint32_t *>((uint8_t *)dst.hb + qf_hb_pair_off(prow, rec, K, 4)) = hb;
         }
-    } else if constexpr (T == AESIR_GGML_Q4_K) {
-        const uint8_t *blk = src + (k / 256) * 144;
+    }
+    *reinterpret_cast<u32x2 *>((uint8_t *)dst.nib + qf_nib_off(prow, rec, K)) = u32x2{nib[0], nib[1]};
+    uint8_t *s0 = (uint8_t *)dst.s0 + qf_s0_off(prow, rec, K, qf_s0_bytes(T));
+    if constexpr (T == AESIR_GGML_Q4_0 || T == AESIR_GGML_Q5_0 || qf_dm<T>()) {
+        if (rec % 2 == 0) {  // the block's f16 d (and m), the first 2 (4) bytes of every legacy block
+            const uint8_t *blk = src + (k / 32) * (gguf_row_bytes(T, 32));
+            if constexpr (qf_dm<T>())
+                *reinterpret_cast<uint32_t *>(s0) = (uint32_t)blk[0] | ((uint32_t)blk[1] << 8) | ((uint32_t)blk[2] << 16) |
+                                                    ((uint32_t)blk[3] << 24);
+            else
+                *reinterpret_cast<uint16_t *>(s0) = (uint16_t)(blk[0] | (blk[1] << 8));
+        }
+    } else if constexpr (qf_kq<T>()) {
+        const uint8_t *blk = src + (k / 256) * (T == AESIR_GGML_Q4_K ? 144 : 176);
         if (rec % 2 == 0) {
             int s, m;
             q4k_scale_min(blk + 4, (int)((k % 256) / 32), s, m);
@@ -310,10 +398,6 @@ __global__ __launch_bounds__(256) void qf_dequant_kernel(QFMat w, int64_t rows, 
     st16(dst, o[0]);
     st16(dst + 8, o[1]);
 }
-
-// Q4_1 / Q5_1 weight pairs f16(f16(q d) + m): two roundings, the reference's f16 multiply then
-// add (the library is built without multiply-add contraction).
-__device__ __forceinline__ h16x2 q4_1_w2(h16x2 q, h16x2 dd, h16x2 mm) { return q * dd + mm; }
 
 // One thread per record: GGUF blocks -> f16 weights straight from the blocks, with the same
 // weight rules (and instructions) as qf_deq16 for the repacked types; the only path of the types
@@ -400,21 +484,34 @@ __global__ __launch_bounds__(256) void qf_fill_kernel(QFMat w, int64_t rows, int
     const uint64_t a = mix64(base + (uint64_t)(2 * gid + 1) * kGolden);
     const uint64_t b = mix64(base + (uint64_t)(2 * gid + 2) * kGolden);
     *reinterpret_cast<u32x2 *>((uint8_t *)w.nib + qf_nib_off(prow, rec, K)) = u32x2{(unsigned)a, (unsigned)(a >> 32)};
-    uint8_t *s0 = (uint8_t *)w.s0 + qf_s0_off(prow, rec, K);
+    uint8_t *s0 = (uint8_t *)w.s0 + qf_s0_off(prow, rec, K, qf_s0_bytes(T));
     const float u = (float)(b >> 40) * (1.0f / 16777216.0f);  // [0, 1)
-    if constexpr (T == AESIR_GGML_Q4_0) {
-        // q - 8 uniform on [-8, 7]: standard deviation 4.61
-        if (rec % 2 == 0) *reinterpret_cast<h16 *>(s0) = (h16)((0.5f + u) * std / 4.61f);
-    } else if constexpr (T == AESIR_GGML_Q4_K) {
-        // sc in [4, 8], m = round(7.5 sc), dmin = d: w = d sc (q - 7.5) nearly, q uniform on [0, 15]
+    // 5-bit types: uniform fifth bits, one word per record pair (written by the even record)
+    if constexpr (qf_hb5<T>())
+        if (rec % 2 == 0) *reinterpret_cast<uint32_t *>((uint8_t *)w.hb + qf_hb_pair_off(prow, rec, K, 4)) = (uint32_t)(b >> 8);
+    constexpr float qsd = qf_hb5<T>() ? 9.23f : 4.61f;  // standard deviation of q uniform on [0, 31] / [0, 15]
+    constexpr float qmid = qf_hb5<T>() ? 15.5f : 7.5f;
+    if constexpr (T == AESIR_GGML_Q4_0 || T == AESIR_GGML_Q5_0) {
+        // q - 8 (q - 16) uniform on [-8, 7] ([-16, 15])
+        if (rec % 2 == 0) *reinterpret_cast<h16 *>(s0) = (h16)((0.5f + u) * std / qsd);
+    } else if constexpr (qf_dm<T>()) {
+        // m = -f16(qmid d): w = q d + m centred near 0
         if (rec % 2 == 0) {
-            const int s = 4 + (int)((b >> 8) % 5), m = (int)(7.5f * (float)s + 0.5f);
+            const h16 d = (h16)((0.5f + u) * std / qsd), m = (h16)(-qmid * (float)d);
+            *reinterpret_cast<uint32_t *>(s0) = (uint32_t)h_to_bits(d) | ((uint32_t)h_to_bits(m) << 16);
+        }
+    } else if constexpr (qf_kq<T>()) {
+        // sc in [4, 8], m = round(qmid sc / mk), dmin = mk d: w = d sc (q - qmid) nearly, m within
+        // the 6 bits GGML's packing holds
+        constexpr float mk = T == AESIR_GGML_Q5_K ? 2.0f : 1.0f;
+        if (rec % 2 == 0) {
+            const int s = 4 + (int)((b >> 8) % 5), m = (int)(qmid * (float)s / mk + 0.5f);
             *reinterpret_cast<uint16_t *>(s0) = (uint16_t)(s | (m << 8));
         }
         if (rec % 16 == 0) {
-            const h16 d = (h16)((0.5f + u) * std / (6.0f * 4.61f));
-            const uint32_t dv = h_to_bits(d);
-            *reinterpret_cast<uint32_t *>((uint8_t *)w.s1 + qf_s1_off(prow, rec, K, 4)) = dv | (dv << 16);
+            const h16 d = (h16)((0.5f + u) * std / (6.0f * qsd));
+            const uint32_t dv = h_to_bits(d), mv = h_to_bits((h16)(mk * (float)d));
+            *reinterpret_cast<uint32_t *>((uint8_t *)w.s1 + qf_s1_off(prow, rec, K, 4)) = dv | (mv << 16);
         }
     } else {
         // q - 32 uniform on [-32, 31]: standard deviation 18.5; sc in [16, 47]
@@ -429,12 +526,28 @@ __global__ __launch_bounds__(256) void qf_fill_kernel(QFMat w, int64_t rows, int
 static unsigned rec_grid(int64_t rows, int64_t K) { return (unsigned)((rows * (K / kRec) + 255) / 256); }
 
 static int32_t qf_check(int32_t type, int64_t K, const char *name) {
-    if (!qf_type(type)) return fail(AESIR_ERR_UNSUPPORTED, "%s: weight type %d is not Q4_0, Q4_K or Q6_K", name, (int)type);
-    const int64_t blk = type == AESIR_GGML_Q4_0 ? 32 : 256;
+    if (!qf_type(type))
+        return fail(AESIR_ERR_UNSUPPORTED, "%s: weight type %d is not Q4_0, Q4_1, Q5_0, Q5_1, Q4_K, Q5_K or Q6_K", name,
+                    (int)type);
+    const int64_t blk = gguf_block_elems(type);
     if (K <= 0 || K % blk != 0)
         return fail(AESIR_ERR_SHAPE, "%s: row length %lld is not a multiple of the %lld-weight block", name, (long long)K,
                     (long long)blk);
     return AESIR_OK;
+}
+
+// Runs F<T>() for the repacked type `type` (one of qf_type's).
+template <class F>
+static void qf_switch(int32_t type, F &&f) {
+    switch (type) {
+        case AESIR_GGML_Q4_0: f(std::integral_constant<int, AESIR_GGML_Q4_0>{}); break;
+        case AESIR_GGML_Q4_1: f(std::integral_constant<int, AESIR_GGML_Q4_1>{}); break;
+        case AESIR_GGML_Q5_0: f(std::integral_constant<int, AESIR_GGML_Q5_0>{}); break;
+        case AESIR_GGML_Q5_1: f(std::integral_constant<int, AESIR_GGML_Q5_1>{}); break;
+        case AESIR_GGML_Q4_K: f(std::integral_constant<int, AESIR_GGML_Q4_K>{}); break;
+        case AESIR_GGML_Q5_K: f(std::integral_constant<int, AESIR_GGML_Q5_K>{}); break;
+        default: f(std::integral_constant<int, AESIR_GGML_Q6_K>{}); break;
+    }
 }
 
 // The tiled planes need whole 128-weight segments.
@@ -451,12 +564,10 @@ int32_t launch_qf_repack(hipStream_t s, int32_t type, const void *blocks, int64_
     AESIR_TRY(qf_check_planes(type, K, "repack"));
     if (rows <= 0) return AESIR_OK;
     const unsigned g = rec_grid(rows, K);
-    if (type == AESIR_GGML_Q4_0)
-        hipLaunchKernelGGL(qf_repack_kernel<AESIR_GGML_Q4_0>, dim3(g), dim3(256), 0, s, (const uint8_t *)blocks, rows, K, dst, step);
-    else if (type == AESIR_GGML_Q4_K)
-        hipLaunchKernelGGL(qf_repack_kernel<AESIR_GGML_Q4_K>, dim3(g), dim3(256), 0, s, (const uint8_t *)blocks, rows, K, dst, step);
-    else
-        hipLaunchKernelGGL(qf_repack_kernel<AESIR_GGML_Q6_K>, dim3(g), dim3(256), 0, s, (const uint8_t *)blocks, rows, K, dst, step);
+    qf_switch(type, [&](auto t) {
+        hipLaunchKernelGGL(qf_repack_kernel<decltype(t)::value>, dim3(g), dim3(256), 0, s, (const uint8_t *)blocks, rows,
+                           K, dst, step);
+    });
     AESIR_LAUNCH_CHECK("qf_repack_kernel");
     return AESIR_OK;
 }
@@ -466,12 +577,10 @@ int32_t launch_qf_dequant(hipStream_t s, const QFMat &w, int64_t rows, int64_t K
     AESIR_TRY(qf_check_planes(w.type, K, "dequant"));
     if (rows <= 0) return AESIR_OK;
     const unsigned g = rec_grid(rows, K);
-    if (w.type == AESIR_GGML_Q4_0)
-        hipLaunchKernelGGL(qf_dequant_kernel<AESIR_GGML_Q4_0>, dim3(g), dim3(256), 0, s, w, rows, K, step, row_ids, (h16 *)out, out_stride);
-    else if (w.type == AESIR_GGML_Q4_K)
-        hipLaunchKernelGGL(qf_dequant_kernel<AESIR_GGML_Q4_K>, dim3(g), dim3(256), 0, s, w, rows, K, step, row_ids, (h16 *)out, out_stride);
-    else
-        hipLaunchKernelGGL(qf_dequant_kernel<AESIR_GGML_Q6_K>, dim3(g), dim3(256), 0, s, w, rows, K, step, row_ids, (h16 *)out, out_stride);
+    qf_switch(w.type, [&](auto t) {
+        hipLaunchKernelGGL(qf_dequant_kernel<decltype(t)::value>, dim3(g), dim3(256), 0, s, w, rows, K, step, row_ids,
+                           (h16 *)out, out_stride);
+    });
     AESIR_LAUNCH_CHECK("qf_dequant_kernel");
     return AESIR_OK;
 }
@@ -531,12 +640,9 @@ int32_t launch_qf_fill_random(hipStream_t s, const QFMat &w, int64_t rows, int64
     if (rows <= 0) return AESIR_OK;
     const uint64_t base = mix64(seed ^ mix64(stream + kGolden));
     const unsigned g = rec_grid(rows, K);
-    if (w.type == AESIR_GGML_Q4_0)
-        hipLaunchKernelGGL(qf_fill_kernel<AESIR_GGML_Q4_0>, dim3(g), dim3(256), 0, s, w, rows, K, step, base, std);
-    else if (w.type == AESIR_GGML_Q4_K)
-        hipLaunchKernelGGL(qf_fill_kernel<AESIR_GGML_Q4_K>, dim3(g), dim3(256), 0, s, w, rows, K, step, base, std);
-    else
-        hipLaunchKernelGGL(qf_fill_kernel<AESIR_GGML_Q6_K>, dim3(g), dim3(256), 0, s, w, rows, K, step, base, std);
+    qf_switch(w.type, [&](auto t) {
+        hipLaunchKernelGGL(qf_fill_kernel<decltype(t)::value>, dim3(g), dim3(256), 0, s, w, rows, K, step, base, std);
+    });
     AESIR_LAUNCH_CHECK("qf_fill_kernel");
     return AESIR_OK;
 }
@@ -575,8 +681,10 @@ __device__ __forceinline__ unsigned vreg(unsigned v) {
 struct QfRegs {
     unsigned lo, hi, magic;  // nibble masks 0x000F000F / 0x00F000F0, f16 1024 in both halves
     unsigned hlo, hhi;       // Q6_K high-bit masks 0x00300030 / 0x03000300
+    unsigned flo, fhi;       // fifth-bit masks 0x00100010 / 0x01000100
     __device__ __forceinline__ static QfRegs make() {
-        return QfRegs{sreg(0x000F000Fu), sreg(0x00F000F0u), vreg(kMagic), sreg(0x00300030u), sreg(0x03000300u)};
+        return QfRegs{sreg(0x000F000Fu), sreg(0x00F000F0u), vreg(kMagic), sreg(0x00300030u),
+                      sreg(0x03000300u), sreg(0x00100010u), sreg(0x01000100u)};
     }
 };
 
@@ -601,6 +709,30 @@ struct QTile<AESIR_GGML_Q6_K> {
     unsigned s0;  // int8 scales of the two records
     unsigned s1;  // f16 super-block d in the low half
 };
+template <>
+struct QTile<AESIR_GGML_Q5_0> {
+    u32x4 nib;
+    unsigned s0;  // f16 d in the low half
+    unsigned hb;  // fifth bits of the two records
+};
+template <>
+struct QTile<AESIR_GGML_Q4_1> {
+    u32x4 nib;
+    unsigned s0;  // f16 d | f16 m << 16
+};
+template <>
+struct QTile<AESIR_GGML_Q5_1> {
+    u32x4 nib;
+    unsigned s0;  // f16 d | f16 m << 16
+    unsigned hb;
+};
+template <>
+struct QTile<AESIR_GGML_Q5_K> {
+    u32x4 nib;
+    unsigned s0;  // scale | min << 8
+    unsigned s1;  // f16 d | f16 dmin << 16
+    unsigned hb;
+};
 
 // Buffer resources of a matrix's planes (range-checked loads, tile offsets in SGPRs).
 struct QfRsrc {
@@ -621,8 +753,12 @@ template <int T>
 __device__ __forceinline__ QTile<T> qf_tile_load(const QfRsrc &r, int tile, int lane, int s1v, int s1s) {
     QTile<T> q;
     q.nib = __builtin_amdgcn_raw_buffer_load_b128(r.nib, lane * 16, tile * 1024, 2);
-    q.s0 = __builtin_amdgcn_raw_buffer_load_b16(r.s0, lane * 2, tile * 128, 0);
-    if constexpr (T == AESIR_GGML_Q4_K) q.s1 = __builtin_amdgcn_raw_buffer_load_b32(r.s1, s1v, s1s, 0);
+    if constexpr (qf_dm<T>())
+        q.s0 = __builtin_amdgcn_raw_buffer_load_b32(r.s0, lane * 4, tile * 256, 0);
+    else
+        q.s0 = __builtin_amdgcn_raw_buffer_load_b16(r.s0, lane * 2, tile * 128, 0);
+    if constexpr (qf_hb5<T>()) q.hb = __builtin_amdgcn_raw_buffer_load_b32(r.hb, lane * 4, tile * 256, 0);
+    if constexpr (qf_kq<T>()) q.s1 = __builtin_amdgcn_raw_buffer_load_b32(r.s1, s1v, s1s, 0);
     if constexpr (T == AESIR_GGML_Q6_K) {
         q.hb = __builtin_amdgcn_raw_buffer_load_b64(r.hb, lane * 8, tile * 512, 2);
         q.s1 = __builtin_amdgcn_raw_buffer_load_b16(r.s1, s1v, s1s, 0);
@@ -653,19 +789,50 @@ __device__ __forceinline__ void qf_tile_a(const QTile<T> &q, const QfRegs &k, u3
             a[j].z = h2_bits(q4_0_w2(__builtin_elementwise_fma(as_h2((v & k.hi) | k.magic), s16, bhi), dd));
             a[j].w = h2_bits(q4_0_w2(__builtin_elementwise_fma(as_h2((t & k.hi) | k.magic), s16, bhi), dd));
         }
-    } else if constexpr (T == AESIR_GGML_Q4_K) {
-        const h16x2 b1024 = {(h16)-1024.0f, (h16)-1024.0f}, bhi = {(h16)-64.0f, (h16)-64.0f};
-        // (scale, min) bytes into the low byte of each half, then exact through the 1024 exponent
-        const h16x2 sm = as_h2(__builtin_amdgcn_perm(0u, q.s0, 0x0c010c00u) | k.magic) + b1024;
-        const h16x2 ab = q4k_scales(as_h2(q.s1), sm);
-        const h16x2 aa = {ab.x, ab.x}, nbb = {-ab.y, -ab.y};
+    } else if constexpr (T != AESIR_GGML_Q6_K) {
+        // Q4_1, Q5_0, Q5_1, Q4_K, Q5_K: the exact quantized pairs (q - 16 for Q5_0, else q), the
+        // fifth bits OR-ed in at value 16 (low nibbles) or 256 (16-scaled high nibbles), then the
+        // weight rule with the record pair's scales
+        constexpr bool h5 = qf_hb5<T>();
+        constexpr float off = T == AESIR_GGML_Q5_0 ? 16.0f : 0.0f;
+        const h16x2 blo = {(h16)(-1024.0f - off), (h16)(-1024.0f - off)}, bhi = {(h16)(-64.0f - off), (h16)(-64.0f - off)};
+        h16x2 aa, nbb;
+        if constexpr (qf_kq<T>()) {
+            const h16x2 b1024 = {(h16)-1024.0f, (h16)-1024.0f};
+            // (scale, min) bytes into the low byte of each half, then exact through the 1024 exponent
+            const h16x2 sm = as_h2(__builtin_amdgcn_perm(0u, q.s0, 0x0c010c00u) | k.magic) + b1024;
+            const h16x2 ab = q4k_scales(as_h2(q.s1), sm);
+            aa = h16x2{ab.x, ab.x};
+            nbb = h16x2{-ab.y, -ab.y};
+        } else if constexpr (qf_dm<T>()) {
+            const h16x2 dm = as_h2(q.s0);
+            aa = h16x2{dm.x, dm.x};
+            nbb = h16x2{dm.y, dm.y};
+        } else {
+            const h16 d = bits_to_h((uint16_t)(q.s0 & 0xffffu));
+            aa = h16x2{d, d};
+        }
+        auto rule = [&](h16x2 v) {
+            if constexpr (qf_kq<T>()) return q4k_w2(v, aa, nbb);
+            else if constexpr (qf_dm<T>()) return q4_1_w2(v, aa, nbb);
+            else return q4_0_w2(v, aa);
+        };
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const unsigned v = nw[j], t = v >> 8;
-            a[j].x = h2_bits(q4k_w2(as_h2((v & k.lo) | k.magic) + b1024, aa, nbb));
-            a[j].y = h2_bits(q4k_w2(as_h2((t & k.lo) | k.magic) + b1024, aa, nbb));
-            a[j].z = h2_bits(q4k_w2(__builtin_elementwise_fma(as_h2((v & k.hi) | k.magic), s16, bhi), aa, nbb));
-            a[j].w = h2_bits(q4k_w2(__builtin_elementwise_fma(as_h2((t & k.hi) | k.magic), s16, bhi), aa, nbb));
+            unsigned fa = 0u, fb = 0u, ga = 0u, gb = 0u;  // fifth bits of the four pairs
+            if constexpr (h5) {
+                const unsigned h = (j >> 1) ? q.hb >> 1 : q.hb;  // the record's bits at the even positions
+                const unsigned ha = (j & 1) == 0 ? h << 4 : h >> 4, hb = (j & 1) == 0 ? h << 2 : h >> 6;
+                fa = ha & k.flo;
+                ga = ha & k.fhi;
+                fb = hb & k.flo;
+                gb = hb & k.fhi;
+            }
+            a[j].x = h2_bits(rule(as_h2(fa | ((v & k.lo) | k.magic)) + blo));
+            a[j].y = h2_bits(rule(as_h2(fb | ((t & k.lo) | k.magic)) + blo));
+            a[j].z = h2_bits(rule(__builtin_elementwise_fma(as_h2(ga | ((v & k.hi) | k.magic)), s16, bhi)));
+            a[j].w = h2_bits(rule(__builtin_elementwise_fma(as_h2(gb | ((t & k.hi) | k.magic)), s16, bhi)));
         }
     } else {
         const h16x2 blo = {(h16)-1056.0f, (h16)-1056.0f}, bhi = {(h16)-96.0f, (h16)-96.0f};
@@ -735,7 +902,7 @@ __global__ __launch_bounds__(NW * kWave) void gemv_qf_kernel(QFMat w, int64_t N,
     const int blocks = (int)((N + 15) / 16);
     const int pb0 = (int)(w.row0 / 16);  // plane row block of row 0
     const QfRsrc rs = qf_rsrc(w, T, w.row0 + (int64_t)blocks * 16, K);
-    constexpr int es1 = T == AESIR_GGML_Q4_K ? 4 : 2;
+    constexpr int es1 = qf_kq<T>() ? 4 : 2;
     const int sbr = (int)(K / 256);  // s1 entries per row
     const int s1v = (lane & 15) * es1;
     // steps of this workgroup: (block k, round r), r < R, for its nb blocks
@@ -948,12 +1115,7 @@ static int32_t gemv_qf_dispatch(hipStream_t s, const QFMat &w, int64_t N, int64_
     if (mul_checked(w.row0 + qf_rows_alloc(N), qf_plane_row_bytes(w.type, 0, K)) > INT32_MAX)
         return fail(AESIR_ERR_UNSUPPORTED, "%s: matrix of %lld x %lld exceeds 2 GiB of 4-bit weights", name, (long long)N,
                     (long long)K);
-    if (w.type == AESIR_GGML_Q4_0)
-        gemv_qf_launch_t<NORM, Epi, AESIR_GGML_Q4_0>(s, w, N, K, src, nw, eps, epi);
-    else if (w.type == AESIR_GGML_Q4_K)
-        gemv_qf_launch_t<NORM, Epi, AESIR_GGML_Q4_K>(s, w, N, K, src, nw, eps, epi);
-    else
-        gemv_qf_launch_t<NORM, Epi, AESIR_GGML_Q6_K>(s, w, N, K, src, nw, eps, epi);
+    qf_switch(w.type, [&](auto t) { gemv_qf_launch_t<NORM, Epi, decltype(t)::value>(s, w, N, K, src, nw, eps, epi); });
     AESIR_LAUNCH_CHECK(name);
     return AESIR_OK;
 }

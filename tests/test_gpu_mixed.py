@@ -13,15 +13,11 @@ mix types, as Q4_K_M files do) against the CPU oracle.
 import numpy as np
 import pytest
 
-from test_gpu_quant import lib_weights, random_tensor, same_token, within_tol
+from quant_tools import (F16, Q2_K, Q3_K, Q4_0, Q4_1, Q4_K, Q5_0, Q5_1, Q5_K, Q6_K, Q8_0, expected_f16, make_tensor,
+                         same_token, within_tol)
 
 pytestmark = pytest.mark.gpu
 
-F16, Q4_0, Q8_0, Q4_K, Q6_K = 1, 2, 8, 12, 14
-Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q5_K = 3, 6, 7, 10, 11, 13
-KIND = {Q4_0: "q4_0", Q4_K: "q4_k", Q6_K: "q6_k"}
-LEGACY = {Q4_1: "q4_1", Q5_0: "q5_0", Q5_1: "q5_1"}
-KQUANT = {Q2_K: "q2_k", Q3_K: "q3_k", Q5_K: "q5_k"}
 PER = ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")
 
 
@@ -66,58 +62,13 @@ MIXES = {
     # F16 embedding and Q/K/V in a model with quantized matrices elsewhere
     "f16_front": layout(F16, Q4_0, [(F16, F16, F16, Q6_K, Q4_K, Q4_K, Q8_0),
                                     (Q8_0, Q8_0, Q8_0, Q4_0, Q6_K, Q6_K, Q4_K)]),
-    # the types kept in f16 (Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q5_K) beside repacked ones
-    "f16_kept": layout(Q5_K, Q3_K, [(Q5_0, Q5_0, Q5_0, Q4_1, Q5_1, Q5_1, Q2_K),
-                                    (Q5_K, Q5_K, Q6_K, Q3_K, Q4_K, Q4_K, Q5_0)]),
+    # the other GGUF formats: Q4_1, Q5_0, Q5_1, Q5_K repacked (Q5_0 Q/K/V fused, the Q5_K table
+    # looked up apart), Q2_K and Q3_K kept in f16
+    "more_types": layout(Q5_K, Q3_K, [(Q5_0, Q5_0, Q5_0, Q4_1, Q5_1, Q5_1, Q2_K),
+                                      (Q5_K, Q5_K, Q6_K, Q3_K, Q4_K, Q4_K, Q5_0)]),
 }
 
 SMALL = dict(dim=256, n_layers=2, n_heads=4, n_kv_heads=2, ffn=512, vocab=300, ctx_len=160)
-
-
-def make_tensor(A, t, r, c, rng, std=0.02):
-    """Packed blocks of type t (or f16 values) for a r x c matrix of weights of spread near std."""
-    if t == F16:
-        return (rng.standard_normal((r, c)) * std).astype(np.float16)
-    u = lambda shape: rng.uniform(0.5, 1.5, shape)
-    if t == Q8_0:
-        d = (u((r, c // 32)) * std / 64).astype(np.float16)
-        return A.Q8_0Tensor.from_parts(d, rng.integers(-127, 128, (r, c)).astype(np.int8))
-    if t in (Q4_1, Q5_0, Q5_1):
-        top = 16 if t == Q4_1 else 32
-        d = (u((r, c // 32)) * std / (0.29 * top)).astype(np.float16)
-        q = rng.integers(0, top, (r, c))
-        if t == Q5_0:
-            return A.Q5_0Tensor.from_parts(d, q)
-        m = (-(top / 2 - 0.5 + rng.uniform(-1, 1, d.shape)) * d.astype(np.float64)).astype(np.float16)
-        return (A.Q4_1Tensor if t == Q4_1 else A.Q5_1Tensor).from_parts(d, m, q)
-    nsb = c // 256
-    if t == Q5_K:
-        d = (u((r, nsb)) * std / (32 * 9.2)).astype(np.float16)
-        dmin = (d.astype(np.float32) * rng.uniform(0.5, 1.0, (r, nsb))).astype(np.float16)
-        return A.Q5_KTensor.from_parts(d, dmin, rng.integers(1, 64, (r, nsb, 8)), rng.integers(0, 64, (r, nsb, 8)),
-                                       rng.integers(0, 32, (r, c)))
-    if t == Q2_K:
-        d = (u((r, nsb)) * std / (8 * 1.12)).astype(np.float16)
-        dmin = (d.astype(np.float32) * rng.uniform(0.5, 1.0, (r, nsb))).astype(np.float16)
-        return A.Q2_KTensor.from_parts(d, dmin, rng.integers(1, 16, (r, nsb, 16)), rng.integers(0, 16, (r, nsb, 16)),
-                                       rng.integers(0, 4, (r, c)))
-    if t == Q3_K:
-        d = (u((r, nsb)) * std / (18.5 * 2.29)).astype(np.float16)
-        return A.Q3_KTensor.from_parts(d, rng.integers(-32, 32, (r, nsb, 16)), rng.integers(-4, 4, (r, c)))
-    return random_tensor(A, KIND[t], r, c, rng, std)
-
-
-def expected_f16(oracle, t, x):
-    """The f16 weights the library multiplies for tensor x of type t."""
-    if t == F16:
-        return np.asarray(x, np.float16)
-    if t == Q8_0:
-        return oracle.dequantize_q8_0(x.blocks, x.blocks.shape[0]).reshape(x.rows, x.cols)
-    if t in LEGACY:
-        return oracle.dequantize_legacy(LEGACY[t], x.blocks, x.blocks.shape[0]).reshape(x.rows, x.cols)
-    if t in KQUANT:
-        return oracle.dequantize_kquant_f16(KQUANT[t], x.blocks, x.blocks.shape[0]).reshape(x.rows, x.cols)
-    return lib_weights(oracle, KIND[t], x).astype(np.float16)
 
 
 def mixed_weights(A, oracle, cfg, types, rng):
@@ -206,7 +157,7 @@ def test_mixed_batched_prefill_matches_per_position(A, ctx, oracle, mix):
     m.close()
 
 
-@pytest.mark.parametrize("mix", ["embd_apart", "f16_kept"])
+@pytest.mark.parametrize("mix", ["embd_apart", "more_types"])
 def test_mixed_gguf_file_loads_like_set_tensor(A, ctx, oracle, tmp_path, mix):
     from gguf_tools import llama_metadata, write_gguf
 

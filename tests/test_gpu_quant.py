@@ -1,19 +1,22 @@
-"""GPU parity of the Q4_0, Q4_K and Q6_K weight paths (tiled records, the matrix-core decode GEMV
-with the fused epilogues, batched prefill, GGUF loading) against the CPU oracle.
+"""GPU parity of the repacked weight types, Q4_0, Q4_1, Q5_0, Q5_1, Q4_K, Q5_K and Q6_K (tiled
+records, the matrix-core decode GEMV with the fused epilogues, batched prefill, GGUF loading),
+against the CPU oracle.
 
-- aesir_gemm_quant on packed GGUF blocks: Q4_0 within 1 f16 ulp of the oracle's gemm_q4_0
-  (core/compute.mojo:876-912; beyond 1 ulp only where f32 summation noise exceeds it); Q4_K / Q6_K
-  against f64 on the oracle's f16 weights (ao_dequantize_q4_k_f16 / _q6_k_f16, the rule every
-  kernel of the library applies) within one f16 rounding of the output plus f32 summation noise.
-  16 or more rows of A, and Q4_0 rows whose length is not a multiple of 128, take the F16 GEMM on
-  the same f16 weights and are held to f64 on those.
+- aesir_gemm_quant on packed GGUF blocks: Q4_0, Q4_1, Q5_0 and Q5_1 within 1 f16 ulp of the
+  oracle's reference-order gemm_q4_0 / _q4_1 / _q5_0 / _q5_1 (core/compute.mojo:876-1036; beyond
+  1 ulp only where f32 summation noise exceeds it); Q4_K / Q5_K / Q6_K against f64 on the oracle's
+  f16 weights (the rule every kernel of the library applies) within one f16 rounding of the
+  output plus f32 summation noise. 16 or more rows of A, and rows whose length is not a multiple
+  of 128, take the F16 GEMM on the same f16 weights and are held to f64 on those.
 - Models: the F16 oracle holding the weights the model reads back (get_tensor), which are the
-  f16 weights the GEMVs and the prefill multiply for all three types; Q4_0 tokens are identical,
-  K-quant tokens may differ only at a near tie of the oracle's logits, and logits are held to the
+  f16 weights the GEMVs and the prefill multiply for every type; Q4_0 tokens are identical, the
+  others may differ only at a near tie of the oracle's logits, and logits are held to the
   forward-pass tolerance.
 """
 import numpy as np
 import pytest
+
+from quant_tools import expected_f16, make_tensor, same_token, ulp_diff, upload_bytes, within_tol
 
 pytestmark = pytest.mark.gpu
 
@@ -42,53 +45,18 @@ def well_scope(ctx):
     ctx.reset(off)
 
 
-TYPES = {"q4_0": 2, "q4_k": 12, "q6_k": 14}
+TYPES = {"q4_0": 2, "q4_1": 3, "q5_0": 6, "q5_1": 7, "q4_k": 12, "q5_k": 13, "q6_k": 14}
+LEGACY_KINDS = ("q4_1", "q5_0", "q5_1")
 
 
 def random_tensor(A, kind, rows, cols, rng, std=0.02):
     """Packed GGUF blocks of a rows x cols matrix with weights of standard deviation near std."""
-    if kind == "q4_0":
-        d = (rng.uniform(0.5, 1.5, (rows, cols // 32)) * std / 4.6).astype(np.float16)
-        return A.Q4_0Tensor.from_parts(d, rng.integers(0, 16, (rows, cols)).astype(np.uint8))
-    nsb = cols // 256
-    if kind == "q4_k":
-        sc = rng.integers(1, 64, (rows, nsb, 8)).astype(np.uint8)
-        mn = rng.integers(0, 64, (rows, nsb, 8)).astype(np.uint8)
-        d = (rng.uniform(0.5, 1.5, (rows, nsb)) * std / (32 * 4.6)).astype(np.float16)
-        dmin = (d.astype(np.float32) * rng.uniform(0.5, 1.0, (rows, nsb))).astype(np.float16)
-        return A.Q4_KTensor.from_parts(d, dmin, sc, mn, rng.integers(0, 16, (rows, cols)).astype(np.uint8))
-    sc = rng.integers(-127, 128, (rows, nsb, 16)).astype(np.int8)
-    d = (rng.uniform(0.5, 1.5, (rows, nsb)) * std / (64 * 18.5)).astype(np.float16)
-    return A.Q6_KTensor.from_parts(d, sc, rng.integers(0, 64, (rows, cols)).astype(np.uint8))
+    return make_tensor(A, TYPES[kind], rows, cols, rng, std)
 
 
 def lib_weights(oracle, kind, t):
     """The f16 weights the library multiplies, as f64."""
-    nb = t.blocks.shape[0]
-    if kind == "q4_0":
-        w = oracle.dequantize_q4_0(t.blocks, nb)
-    elif kind == "q4_k":
-        w = oracle.dequantize_q4_k_f16(t.blocks, nb)
-    else:
-        w = oracle.dequantize_q6_k_f16(t.blocks, nb)
-    return w.astype(np.float64).reshape(t.rows, t.cols)
-
-
-def upload_bytes(ctx, raw):
-    raw = np.ascontiguousarray(raw, np.uint8).reshape(-1)
-    t = ctx.tensor(1, (raw.size + 1) // 2)
-    buf = np.zeros(t.size * 2, np.uint8)
-    buf[: raw.size] = raw
-    t.upload(buf.view(np.float16))
-    return t.ptr
-
-
-def ulp_diff(a, b):
-    ai = np.asarray(a, np.float16).view(np.int16).astype(np.int32)
-    bi = np.asarray(b, np.float16).view(np.int16).astype(np.int32)
-    ai = np.where(ai < 0, -32768 - ai, ai)
-    bi = np.where(bi < 0, -32768 - bi, bi)
-    return np.abs(ai - bi)
+    return expected_f16(oracle, TYPES[kind], t).astype(np.float64)
 
 
 @pytest.mark.parametrize("kind", list(TYPES))
@@ -103,8 +71,8 @@ def test_gemm_quant_vs_oracle(A, ctx, oracle, kind, M, K, N):
     W = lib_weights(oracle, kind, t)
     xd = x.astype(np.float64)
     noise = 2.0 ** -17 * (np.abs(xd) @ np.abs(W).T)
-    if kind == "q4_0" and M < 16:
-        ref = oracle.gemm_q4_0(x, t.blocks, N)
+    if kind in ("q4_0",) + LEGACY_KINDS and M < 16:
+        ref = oracle.gemm_q4_0(x, t.blocks, N) if kind == "q4_0" else oracle.gemm_legacy(kind, x, t.blocks, N)
         d = ulp_diff(got.astype(np.float16), ref)
         bad = (d > 1) & (np.abs(got - ref.astype(np.float64)) > noise)
         assert not bad.any(), d.max()
@@ -155,18 +123,6 @@ def quant_weights(A, oracle, cfg, kind, rng):
         else:
             w[name] = random_tensor(A, kind, r, c, rng)
     return w
-
-
-def same_token(got, want, ref_logits):
-    if got == want:
-        return True
-    a, b = float(ref_logits[got]), float(ref_logits[want])
-    return abs(a - b) <= 2 * float(np.spacing(np.float16(max(abs(a), abs(b)))))
-
-
-def within_tol(got, ref, atol=2e-2, rtol=1e-2):
-    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
-    return bool(np.all(np.abs(got - ref) <= atol + rtol * np.abs(ref)))
 
 
 def quant_model(A, ctx, oracle, cfg, kind, seed):

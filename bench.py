@@ -206,18 +206,22 @@ def q8_bench(A, seed: int, kv: int, steps: int, warmup: int, kernel_iters: int, 
             "kernel_ms": {k: round(v, 5) for k, v in kt.items()}, "tokens_head": toks[:8]}
 
 
-# Q4_0 / Q4_K / Q6_K matrices in HBM (records of 16 weights): 4-bit nibbles, Q6_K's 2-bit high
-# plane, and the per-block scale planes.
-QF_TYPES = {"q4_0": 2, "q4_k": 12, "q6_k": 14}
+# Repacked matrices in HBM (records of 16 weights): 4-bit nibbles, the 5-bit types' fifth-bit
+# plane, Q6_K's 2-bit high plane, and the per-block scale planes.
+QF_TYPES = {"q4_0": 2, "q4_1": 3, "q5_0": 6, "q5_1": 7, "q4_k": 12, "q5_k": 13, "q6_k": 14}
 
 
 def qf_mat_bytes(kind: str, rows: int, cols: int) -> int:
     per_row = cols // 2
-    if kind == "q4_0":
-        per_row += cols // 32 * 2
-    elif kind == "q4_k":
-        per_row += cols // 32 * 2 + cols // 256 * 4
-    else:
+    if kind in ("q5_0", "q5_1", "q5_k"):
+        per_row += cols // 8  # fifth bits
+    if kind in ("q4_0", "q5_0", "q4_k", "q5_k"):
+        per_row += cols // 32 * 2  # f16 d, or the (scale, min) bytes
+    if kind in ("q4_1", "q5_1"):
+        per_row += cols // 32 * 4  # f16 (d, m)
+    if kind in ("q4_k", "q5_k"):
+        per_row += cols // 256 * 4  # f16 (d, dmin)
+    if kind == "q6_k":
         per_row += cols // 4 + cols // 16 + cols // 256 * 2
     return rows * per_row
 
@@ -228,18 +232,23 @@ def qf_token_bytes(kind: str) -> int:
     return LAYERS * layer + qf_mat_bytes(kind, VOCAB, DIM) + 2 * DIM + qf_mat_bytes(kind, 1, DIM)
 
 
-# llama.cpp's Q4_K_M recipe for a Llama: Q4_K matrices, Q6_K for output and for attn_v / ffn_down of
-# the first and last eighth of the layers and every third layer between. A layer whose V is Q6_K
-# keeps its fused Q/K/V matrix in f16 (parts of one fused matrix share a storage type).
+# llama.cpp's Q4_K_M / Q5_K_M recipes for a Llama: Q4_K (Q5_K) matrices, Q6_K for output and for
+# attn_v / ffn_down of the first and last eighth of the layers and every third layer between. A
+# layer whose V is Q6_K keeps its fused Q/K/V matrix in f16 (parts of one fused matrix share a
+# storage type).
+MIXES = {"q4_k_m": "q4_k", "q5_k_m": "q5_k"}
+
+
 def q4_k_m_more_bits(l: int) -> bool:
     return l < LAYERS // 8 or l >= 7 * LAYERS // 8 or (l - LAYERS // 8) % 3 == 2
 
 
-def q4_k_m_types() -> dict:
-    t = {"token_embd.weight": 12, "output.weight": 14}
+def k_m_types(kind: str) -> dict:
+    base = QF_TYPES[MIXES[kind]]
+    t = {"token_embd.weight": base, "output.weight": 14}
     for l in range(LAYERS):
         for b in ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"):
-            t[f"blk.{l}.{b}.weight"] = 14 if b in ("attn_v", "ffn_down") and q4_k_m_more_bits(l) else 12
+            t[f"blk.{l}.{b}.weight"] = 14 if b in ("attn_v", "ffn_down") and q4_k_m_more_bits(l) else base
     return t
 
 
@@ -251,16 +260,16 @@ def stored_mat_bytes(kind: str, rows: int, cols: int) -> int:
 
 def layer_storage(kind: str, l: int) -> tuple:
     """Stored types of layer l's (qkv, o, gate/up, down) matrices."""
-    if kind != "q4_k_m":
+    if kind not in MIXES:
         return (kind,) * 4
-    more = q4_k_m_more_bits(l)
-    return ("f16" if more else "q4_k", "q4_k", "q4_k", "q6_k" if more else "q4_k")
+    base, more = MIXES[kind], q4_k_m_more_bits(l)
+    return ("f16" if more else base, base, base, "q6_k" if more else base)
 
 
 def quant_token_bytes(kind: str) -> int:
     """Algorithmic weight bytes of one decode token as stored: every matrix once, norms, one
     embedding row."""
-    embd, out = ("q4_k", "q6_k") if kind == "q4_k_m" else (kind, kind)
+    embd, out = (MIXES[kind], "q6_k") if kind in MIXES else (kind, kind)
     total = stored_mat_bytes(out, VOCAB, DIM) + 2 * DIM + stored_mat_bytes(embd, 1, DIM)
     for l in range(LAYERS):
         qkv, o, gu, down = layer_storage(kind, l)
@@ -270,22 +279,24 @@ def quant_token_bytes(kind: str) -> int:
 
 
 assert all(quant_token_bytes(k) == qf_token_bytes(k) for k in QF_TYPES)
-QUANT_KINDS = list(QF_TYPES) + ["q4_k_m"]
+# the default run's quantized decode lines (--quant-only runs every kind)
+QUANT_KINDS = ["q4_0", "q4_k", "q5_k", "q6_k", "q4_k_m", "q5_k_m"]
+ALL_QUANT_KINDS = list(QF_TYPES) + list(MIXES)
 
 
 def quant_bench(A, kind: str, seed: int, kv: int, steps: int, warmup: int, kernel_iters: int,
                 use_graph: bool = True) -> dict:
-    """Batch-1 greedy decode of the Llama-3-8B shape with Q4_0, Q4_K or Q6_K matrices, or the
-    Q4_K_M mix of Q4_K and Q6_K (random records and scales for weights of std 0.02; f16 for the
-    fused matrices the mix stores so), KV cache pre-filled to kv positions; same step structure and
-    timing as the F16 decode."""
+    """Batch-1 greedy decode of the Llama-3-8B shape with matrices of one repacked type (Q4_0,
+    Q4_1, Q5_0, Q5_1, Q4_K, Q5_K, Q6_K), or the Q4_K_M / Q5_K_M mixes with Q6_K (random records and
+    scales for weights of std 0.02; f16 for the fused matrices a mix stores so), KV cache pre-filled
+    to kv positions; same step structure and timing as the F16 decode."""
     ctx_len = kv + max(steps, warmup) + 64
     well = int(quant_token_bytes(kind) + stored_mat_bytes("q6_k", VOCAB, DIM) + 2 * LAYERS * ctx_len * KV_DIM * 2
                + 2 * 2 * FFN * DIM + (512 << 20))
     ctx = A.Context(well)
     cfg = A.ModelConfig(DIM, LAYERS, HEADS, KV_HEADS, FFN, VOCAB, ctx_len)
-    if kind == "q4_k_m":
-        m = A.Model.create_mixed(ctx, cfg, q4_k_m_types())
+    if kind in MIXES:
+        m = A.Model.create_mixed(ctx, cfg, k_m_types(kind))
     else:
         m = A.Model.create(ctx, cfg, QF_TYPES[kind])
     m.init_random(seed, 0.02, 0.0, 0.02)
@@ -305,7 +316,7 @@ def quant_bench(A, kind: str, seed: int, kv: int, steps: int, warmup: int, kerne
     gu_bytes = stored_mat_bytes(gu_kind, 2 * FFN, DIM) + DIM * 2 + DIM * 2 + FFN * 2
     m.close()
     ctx.close()
-    dtype = ("q4_k / q6_k weights (f16 Q/K/V where V is q6_k)" if kind == "q4_k_m" else f"{kind} weights")
+    dtype = (f"{MIXES[kind]} / q6_k weights (f16 Q/K/V where V is q6_k)" if kind in MIXES else f"{kind} weights")
     return {"workload": f"llama3-8b-shape {kind} batch-1 greedy decode, kv {kv}", "value": round(tok_s, 2),
             "unit": "tok/s", "steps": steps, "ms_per_step": round(wall * 1e3 / steps, 4),
             "dtype": f"{dtype}, f16 activations, f32 accumulate",
@@ -455,8 +466,8 @@ def main():
     ap.add_argument("--no-sweep", action="store_true", help="skip the decode at KV 512 / 8192 / 32768")
     ap.add_argument("--no-micro", action="store_true", help="skip the kernel micro-suite and the Q8_0 matvec")
     ap.add_argument("--q8-only", action="store_true", help="run only the Q8_0-weight decode measurement")
-    ap.add_argument("--no-quant", action="store_true", help="skip the Q4_0 / Q4_K / Q6_K decode measurements")
-    ap.add_argument("--quant-only", action="store_true", help="run only the Q4_0 / Q4_K / Q6_K decode measurements")
+    ap.add_argument("--no-quant", action="store_true", help="skip the quantized-weight decode measurements")
+    ap.add_argument("--quant-only", action="store_true", help="run only the quantized-weight decode measurements, every type and mix")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain 256 MiB device-to-device copy (the FETCH_SIZE / WRITE_SIZE calibration "
                          "of the HBM traffic figure) and exit")
@@ -477,7 +488,7 @@ def main():
         return
     if args.quant_only:
         print(json.dumps({"quant": {k: quant_bench(A, k, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters,
-                                                   not args.eager) for k in QUANT_KINDS}}))
+                                                   not args.eager) for k in ALL_QUANT_KINDS}}))
         return
     if args.q8_only:
         q = q8_bench(A, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters, not args.eager)

@@ -188,17 +188,19 @@ int32_t aesir_gemm_q8_0(aesir_ctx *ctx, const void *A, int64_t a_rows, int64_t a
                         int64_t b_rows, void *C, int64_t c_rows, int64_t c_cols);
 /* The reference's quantized branch of gemm_f16 (core/compute.mojo:1763-1800) over packed GGUF
  * blocks of ggml_type: B is b_rows x a_cols weights, C[m, n] = f16(sum_k A[m, k] w[n, k]).
- * AESIR_GGML_Q4_0 follows gemm_q4_0 (:876-912, w = f16(f16(q - 8) * d)); AESIR_GGML_Q8_0 is
- * aesir_gemm_q8_0; AESIR_GGML_Q4_K / AESIR_GGML_Q6_K read GGML's super-blocks with f16 weights
- * in the f16 arithmetic of the reference's dequantize_q4_k_m / dequantize_q6_k_block
- * (:245-262, :508-527): w = f16(f16(d * sc) * q - f16(dmin * m)) (one fused rounding) and
- * w = f16(f16(d * sc) * (q - 32)) (the reference's gemm_q4_k_m / gemm_q6_k read synthetic block
- * layouts that no GGUF file holds). Raises "gemm_q4_0: matrix dimensions must be positive",
- * "...: inner dimension must be a multiple of 32" (256 for the K-quants), "...: output matrix
- * shape mismatch". Takes free well space for the duration of the call: with a_rows < 16 and
- * a_cols a multiple of 128 (at most 28672) the blocks are repacked into the library's tiled
- * planes (about the size of the blocks) for the decode GEMV; otherwise an f16 copy of the
- * weights (2 bytes per weight) for the F16 GEMM. */
+ * AESIR_GGML_Q4_0 / _Q4_1 / _Q5_0 / _Q5_1 follow gemm_q4_0 / _q4_1 / _q5_0 / _q5_1 (:876-1036;
+ * w = f16(f16(q - 8) * d), f16(f16(q * d) + m), f16((q - 16) * d), f16(f16(q * d) + m));
+ * AESIR_GGML_Q8_0 is aesir_gemm_q8_0; AESIR_GGML_Q4_K / _Q5_K / _Q6_K / _Q2_K / _Q3_K read GGML's
+ * super-blocks with f16 weights in the f16 arithmetic of the reference's dequantize_q4_k_m /
+ * dequantize_q6_k_block (:245-262, :508-527): w = f16(f16(d * sc) * q - f16(dmin * m)) (one fused
+ * rounding; Q4_K, Q5_K, Q2_K) and w = f16(f16(d * sc) * q) (Q6_K with q - 32, Q3_K with its signed
+ * q) (the reference's K-quant gemms read synthetic block layouts that no GGUF file holds). Raises
+ * "gemm_q4_0: matrix dimensions must be positive", "...: inner dimension must be a multiple of
+ * 32" (256 for the K-quants), "...: output matrix shape mismatch". Takes free well space for the
+ * duration of the call: with a_rows < 16, a_cols a multiple of 128 (at most 28672) and a type
+ * with repacked planes (Q4_0, Q4_1, Q5_0, Q5_1, Q4_K, Q5_K, Q6_K) the blocks are repacked into the
+ * library's tiled planes (about the size of the blocks) for the decode GEMV; otherwise an f16
+ * copy of the weights (2 bytes per weight) for the F16 GEMM. */
 int32_t aesir_gemm_quant(aesir_ctx *ctx, const void *A, int64_t a_rows, int64_t a_cols, const void *blocks,
                          int32_t ggml_type, int64_t b_rows, void *C, int64_t c_rows, int64_t c_cols);
 /* Q8_0 block matvec with f32 activations and f32 output: y[n] = sum_k x[k] * d*q. Rows of
@@ -270,32 +272,35 @@ typedef struct {
 int32_t aesir_model_create(aesir_ctx *ctx, const aesir_model_config *cfg, aesir_model **out);
 /* aesir_model_create with a weight type for the seven matrix kinds (token_embd, output, attn_q/k/v,
  * attn_output, ffn_gate/up/down): AESIR_GGML_F16 (what aesir_model_create makes), AESIR_GGML_Q8_0,
- * AESIR_GGML_Q4_0, AESIR_GGML_Q4_K or AESIR_GGML_Q6_K. A Q8_0 model keeps each matrix as int8
+ * or one of the GGML block types AESIR_GGML_Q4_0, _Q4_1, _Q5_0, _Q5_1, _Q2_K, _Q3_K, _Q4_K, _Q5_K,
+ * _Q6_K. A Q8_0 model keeps each matrix as int8
  * quants [rows][cols] plus f16 block scales [rows][cols/32] in HBM (same fused row order as F16);
  * dim and ffn must be multiples of 32 (and at most 16384). Every weight is used as
  * w = f16(f16(q) * d), gemm_q8_0's rule (core/compute.mojo:1062-1063), so a Q8_0 model computes
- * what the F16 model holding the dequantized weights computes. A Q4_0 / Q4_K / Q6_K model keeps
- * each matrix repacked into 16-weight records in 16-row x 128-weight tiles (nibble plane,
- * per-block scale planes, Q6_K high-bit plane); dim and ffn must be multiples of 128 (Q4_0) or
- * 256 (K-quants), at most 28672. Q4_0 weights are w = f16(f16(q - 8) * d) (gemm_q4_0,
- * core/compute.mojo:876-912); Q4_K and Q6_K weights are f16(f16(d * sc) * q - f16(dmin * m)) and
- * f16(f16(d * sc) * (q - 32)), as aesir_gemm_quant. Norm vectors stay f16. No reference counterpart as a model (the reference loader has no quantized model
- * path, loader/gguf.mojo:450-463). */
+ * what the F16 model holding the dequantized weights computes. A Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q4_K /
+ * Q5_K / Q6_K model keeps each matrix repacked into 16-weight records in 16-row x 128-weight tiles
+ * (nibble plane, per-block scale planes, a fifth-bit or high-bit plane); dim and ffn must be
+ * multiples of 128 (32-weight blocks) or 256 (K-quants), at most 28672. Q2_K and Q3_K matrices are
+ * kept in f16, dequantized on the device at upload (dim and ffn multiples of 256). Every type's
+ * weights are the f16 values of aesir_gemm_quant's rules, so a model of any type computes what
+ * the F16 model holding its read-back weights computes. Norm vectors stay f16. No reference
+ * counterpart as a model (the reference loader has no quantized model path,
+ * loader/gguf.mojo:450-463). */
 int32_t aesir_model_create_typed(aesir_ctx *ctx, const aesir_model_config *cfg, int32_t weight_type,
                                  aesir_model **out);
 /* aesir_model_create_typed with one type per matrix: tensor_types holds n_types = 2 + 7 * n_layers
  * ids in the order token_embd, output, then per layer attn_q, attn_k, attn_v, attn_output,
- * ffn_gate, ffn_up, ffn_down (each F16, Q8_0, Q4_0, Q4_K or Q6_K, with that type's dim / ffn
- * constraints). Each matrix keeps its own type in HBM, except the two fused ones: a layer's
- * Q/K/V (and its gate/up) matrix is stored in f16 when its parts differ in type, each part
- * dequantized at upload by its type's rule. aesir_model_set_tensor then takes each tensor in its
+ * ffn_gate, ffn_up, ffn_down (each F16 or a type aesir_model_create_typed takes, with that
+ * type's dim / ffn constraints). Each matrix keeps its own type in HBM (Q2_K / Q3_K in f16),
+ * except the two fused ones: a layer's Q/K/V (and its gate/up) matrix is stored in f16 when its
+ * parts differ in type, each part dequantized at upload by its type's rule. aesir_model_set_tensor then takes each tensor in its
  * own type. This is the layout of GGUF files that mix types (Q4_K_M and the like). No reference
  * counterpart (the reference loader takes F16 files only, loader/gguf.mojo:450-463). */
 int32_t aesir_model_create_mixed(aesir_ctx *ctx, const aesir_model_config *cfg, const int32_t *tensor_types,
                                  int64_t n_types, aesir_model **out);
 /* aesir_model_weight_type's value for a model whose matrices differ in type. */
 #define AESIR_WEIGHT_MIXED (-2)
-/* Weight type of the model's matrices (AESIR_GGML_F16, _Q8_0, _Q4_0, _Q4_K or _Q6_K), or
+/* Weight type of the model's matrices (AESIR_GGML_F16 or a GGML block type), or
  * AESIR_WEIGHT_MIXED when they differ (aesir_model_tensor_type gives each). */
 int32_t aesir_model_weight_type(const aesir_model *model);
 /* GGML type that aesir_model_set_tensor takes for the named tensor (norms: AESIR_GGML_F16, which
@@ -307,29 +312,31 @@ int32_t aesir_model_get_config(const aesir_model *model, aesir_model_config *cfg
  * host data in GGUF order (rows x cols, cols fastest). F32 tensors are rounded to f16 as
  * loader/gguf.mojo:486-493 does. Shape and type are checked against
  * _validate_required_tensors (loader/gguf.mojo:567-628) with its messages. The matrices of a
- * quantized model take data of the model's type as GGUF packs it: rows x (cols/32) blocks of 34
- * (Q8_0) or 18 (Q4_0) bytes, rows x (cols/256) blocks of 144 (Q4_K) or 210 (Q6_K) bytes. */
+ * quantized model take data of their type (aesir_model_tensor_type) as GGUF packs it: rows x
+ * (cols/32) blocks of 34 (Q8_0), 18 (Q4_0), 20 (Q4_1), 22 (Q5_0) or 24 (Q5_1) bytes, rows x
+ * (cols/256) blocks of 84 (Q2_K), 110 (Q3_K), 144 (Q4_K), 176 (Q5_K) or 210 (Q6_K) bytes. */
 int32_t aesir_model_set_tensor(aesir_model *model, const char *name, const void *host_data, int64_t rows,
                                int64_t cols, int32_t ggml_type);
 /* Reads a tensor back in GGUF order as f16 (for verification); quantized matrices come back
- * dequantized to the f16 weights the model multiplies: f16(q * d) (Q8_0), f16(f16(q - 8) * d)
- * (Q4_0), the K-quant rules of aesir_model_create_typed (Q4_K, Q6_K). */
+ * dequantized to the f16 weights the model multiplies: f16(q * d) (Q8_0), the rules of
+ * aesir_gemm_quant for the other block types. */
 int32_t aesir_model_get_tensor(aesir_model *model, const char *name, void *host_out, int64_t elements);
 /* Device-side seeded random init: every weight N(0, std), every norm N(norm_mean, norm_std),
  * rounded to f16; element i of tensor t uses the same counter-based Box-Muller stream as the
  * test oracle's generator. For models too large to build on the host. Q8_0 matrices get
  * quants uniform in [-127, 127] and block scales uniform in [0.5, 1.5) * std / 64 (weights of
- * standard deviation near std); Q4_0 / Q4_K / Q6_K matrices get uniform nibbles (and high bits)
- * with scales chosen for a standard deviation near std. */
+ * standard deviation near std); repacked matrices get uniform nibbles (and fifth or high bits)
+ * with scales chosen for a standard deviation near std; Q2_K / Q3_K matrices (kept in f16) are
+ * filled as F16. */
 int32_t aesir_model_init_random(aesir_model *model, uint64_t seed, float std, float norm_mean, float norm_std);
 /* GGUFSeer.mmap_and_load (loader/gguf.mojo:664-690) + AesirEngine.__init__'s layer setup
  * (aesir.mojo:237-296): parses a GGUF v3 Llama F16 file, enforces the reference loader
  * contract, creates the model (KV rows = ctx_len_override if > 0, else llama.context_length)
  * and uploads every tensor into HBM. Beyond the reference loader each matrix may also be Q8_0,
- * Q4_0, Q4_K or Q6_K, matrix by matrix (norms F32): a file whose matrices share one type gives a
- * model of that weight type (aesir_model_create_typed), a file that mixes them (Q4_K_M and the
- * like) the model aesir_model_create_mixed makes for its types. Other matrix types are refused
- * with "GGUF required tensor has an invalid type". */
+ * Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q4_K, Q5_K or Q6_K, matrix by matrix (norms F32): a file
+ * whose matrices share one type gives a model of that weight type (aesir_model_create_typed), a
+ * file that mixes them (Q4_K_M and the like) the model aesir_model_create_mixed makes for its
+ * types. Other matrix types are refused with "GGUF required tensor has an invalid type". */
 int32_t aesir_model_load_gguf(aesir_ctx *ctx, const char *path, int64_t ctx_len_override, aesir_model **out);
 
 /* GGUFSeer.inspect_metadata (loader/gguf.mojo:649-662), extended to the tensor table: parses and

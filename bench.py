@@ -124,13 +124,28 @@ TL_Q8_WEIGHT_BYTES = (TL_GEMM_PARAMS + TL["vocab"] * TL["dim"]) * 34 // 32 + 2 *
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense f16
 
 
-def prefill_bench(A, seed: int, n_prompt: int = 128, n_decode: int = 256, reps: int = 5, q8: bool = False) -> dict:
+def tl_weight_bytes(wtype: str) -> int:
+    """Weight bytes of the TinyLlama shape stored as wtype, as TL_WEIGHT_BYTES counts them (every
+    layer matrix, the norms, one vocabulary table)."""
+    if wtype == "f16":
+        return TL_WEIGHT_BYTES
+    if wtype == "q8_0":
+        return TL_Q8_WEIGHT_BYTES
+    d, kvd, f, L = TL["dim"], TL_KVD, TL["ffn"], TL["layers"]
+    mats = L * (qf_mat_bytes(wtype, d + 2 * kvd, d) + qf_mat_bytes(wtype, d, d) + qf_mat_bytes(wtype, 2 * f, d)
+                + qf_mat_bytes(wtype, d, f))
+    return mats + qf_mat_bytes(wtype, TL["vocab"], d) + 2 * (L * 2 * d + 2 * d)
+
+
+def prefill_bench(A, seed: int, n_prompt: int = 128, n_decode: int = 256, reps: int = 5, wtype: str = "f16") -> dict:
     """Batched prefill of n_prompt positions on the TinyLlama shape (MFMA GEMMs; wall time of the
     blocking aesir_prefill call, host launches included), then n_decode graph-replayed greedy steps.
-    q8: the same with Q8_0 matrices (weights for the GEMMs dequantized per fragment)."""
+    wtype q8_0: Q8_0 matrices (weights for the GEMMs dequantized per fragment); a repacked type
+    (q4_0, q4_k, ...): each layer matrix dequantized to f16 before its GEMM."""
     ctx = A.Context(TL_WEIGHT_BYTES + (1 << 30))
+    types = {"f16": A.GGML_F16, "q8_0": A.GGML_Q8_0, **QF_TYPES}
     m = A.Model.create(ctx, A.ModelConfig(TL["dim"], TL["layers"], TL["heads"], TL["kv_heads"], TL["ffn"],
-                                          TL["vocab"], n_prompt + n_decode + 64), A.GGML_Q8_0 if q8 else A.GGML_F16)
+                                          TL["vocab"], n_prompt + n_decode + 64), types[wtype])
     m.init_random(seed, 0.02, 0.0, 0.02)
     rng = np.random.default_rng(seed)
     prompt = rng.integers(0, TL["vocab"], n_prompt).tolist()
@@ -150,12 +165,12 @@ def prefill_bench(A, seed: int, n_prompt: int = 128, n_decode: int = 256, reps: 
     flops = 2.0 * TL_GEMM_PARAMS * n_prompt
     m.close()
     ctx.close()
-    return {"workload": f"tinyllama-1.1b shape {'q8_0' if q8 else 'f16'}: {n_prompt}-token batched prefill, then "
+    return {"workload": f"tinyllama-1.1b shape {wtype}: {n_prompt}-token batched prefill, then "
                         f"{n_decode} greedy decode steps",
             "prefill_ms": round(best * 1e3, 3), "prefill_tok_s": round(n_prompt / best, 1),
             "gemm_tflops": round(flops / best / 1e12, 2),
             "mfma_frac": round(flops / best / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
-            "weight_gbs": round((TL_Q8_WEIGHT_BYTES if q8 else TL_WEIGHT_BYTES) / best / 1e9, 1),
+            "weight_gbs": round(tl_weight_bytes(wtype) / best / 1e9, 1),
             "decode_tok_s": round(n_decode / dec, 1) if n_decode > 0 else None, "first_tokens": [nxt] + toks[:3]}
 
 
@@ -460,6 +475,8 @@ def main():
     ap.add_argument("--eager", action="store_true", help="launch kernels one by one instead of graph replay")
     ap.add_argument("--no-prefill", action="store_true", help="skip the TinyLlama batched-prefill measurement")
     ap.add_argument("--prefill-only", action="store_true", help="run only the TinyLlama prefill measurement")
+    ap.add_argument("--prefill-type", default="f16",
+                    help="weight type of --prefill-only: f16, q8_0 or a repacked type (q4_0, q4_k, ...)")
     ap.add_argument("--prefill-decode-steps", type=int, default=256,
                     help="greedy decode steps after the prefill in --prefill-only runs (0: none)")
     ap.add_argument("--no-q8", action="store_true", help="skip the Q8_0-weight decode measurement")
@@ -484,7 +501,8 @@ def main():
     import aesir_hip as A
 
     if args.prefill_only:
-        print(json.dumps({"prefill": prefill_bench(A, args.seed, n_decode=args.prefill_decode_steps)}))
+        print(json.dumps({"prefill": prefill_bench(A, args.seed, n_decode=args.prefill_decode_steps,
+                                                   wtype=args.prefill_type)}))
         return
     if args.quant_only:
         print(json.dumps({"quant": {k: quant_bench(A, k, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters,
@@ -492,7 +510,7 @@ def main():
         return
     if args.q8_only:
         q = q8_bench(A, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters, not args.eager)
-        q["prefill"] = prefill_bench(A, args.seed, n_decode=64, q8=True)
+        q["prefill"] = prefill_bench(A, args.seed, n_decode=64, wtype="q8_0")
         print(json.dumps({"q8_0": q}))
         return
 
@@ -562,7 +580,7 @@ def main():
     out["sampler"] = sampler_bench(A, args.seed)
     if not args.no_q8:
         out["q8_0"] = q8_bench(A, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters, use_graph)
-        out["q8_0"]["prefill"] = prefill_bench(A, args.seed, n_decode=64, q8=True)
+        out["q8_0"]["prefill"] = prefill_bench(A, args.seed, n_decode=64, wtype="q8_0")
     if not args.no_quant:
         out["quant"] = {k: quant_bench(A, k, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters, use_graph)
                         for k in QUANT_KINDS}

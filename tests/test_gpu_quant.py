@@ -83,18 +83,19 @@ def test_gemm_quant_vs_oracle(A, ctx, oracle, kind, M, K, N):
     assert np.all(np.abs(got - exact) <= tol), np.max(np.abs(got - exact) / tol)
 
 
+@pytest.mark.parametrize("kind", ("q4_0",) + LEGACY_KINDS)
 @pytest.mark.parametrize("M,K,N", [(1, 160, 24), (3, 96, 40), (1, 28704, 17)])
-def test_gemm_q4_0_rows_off_the_tile_grid(A, ctx, oracle, M, K, N):
-    """Q4_0 rows whose length is not a multiple of 128 (or above the GEMV's 28672) take the f16
-    dequantization + F16 GEMM route: within 1 f16 ulp of the oracle's gemm_q4_0 where f32
-    summation noise does not exceed it."""
-    t = random_tensor(A, "q4_0", N, K, RNG)
+def test_gemm_q4_0_rows_off_the_tile_grid(A, ctx, oracle, kind, M, K, N):
+    """Rows of the 32-weight block types whose length is not a multiple of 128 (or above the GEMV's
+    28672) take the f16 dequantization + F16 GEMM route: within 1 f16 ulp of the oracle's
+    reference-order gemm_q4_0 / _q4_1 / _q5_0 / _q5_1 where f32 summation noise does not exceed it."""
+    t = random_tensor(A, kind, N, K, RNG)
     x = RNG.standard_normal((M, K)).astype(np.float16)
     c = ctx.tensor(M, N)
-    A.gemm_quant(ctx, ctx.from_numpy(x), upload_bytes(ctx, t.blocks), TYPES["q4_0"], N, c)
+    A.gemm_quant(ctx, ctx.from_numpy(x), upload_bytes(ctx, t.blocks), TYPES[kind], N, c)
     got = c.numpy()
-    ref = oracle.gemm_q4_0(x, t.blocks, N)
-    W = lib_weights(oracle, "q4_0", t)
+    ref = oracle.gemm_q4_0(x, t.blocks, N) if kind == "q4_0" else oracle.gemm_legacy(kind, x, t.blocks, N)
+    W = lib_weights(oracle, kind, t)
     noise = 2.0 ** -17 * (np.abs(x.astype(np.float64)) @ np.abs(W).T)
     d = ulp_diff(got, ref)
     assert not ((d > 1) & (np.abs(got.astype(np.float64) - ref.astype(np.float64)) > noise)).any(), d.max()

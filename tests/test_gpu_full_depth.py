@@ -6,6 +6,9 @@
   aesir.mojo:358-445), the first 8 also against the oracle.
 - Llama-3-8B shape at full size with the KV cache filled to 2048 and to 32768 positions:
   graph == eager == forward_pass over 8 steps, finite logits.
+- TinyLlama shape, all 22 layers, quantized (the Q4_K_M recipe; every matrix Q5_1): 64
+  per-position forward passes against the oracle on the read-back weights, the batched prefill
+  against both, 64 greedy steps with graph == eager == host.
 - Llama-3-8B shape with 1 layer at the full 128256 vocabulary and KV 2048 (cache contents mirrored
   on the host): every step's logits and token against the oracle, so the fused lm_head + argmax
   epilogue is checked at the real vocabulary inside a model.
@@ -91,6 +94,56 @@ def test_tinyllama_all_layers_prefill_and_decode(A, oracle):
             cur.append(host[-1])
         assert g == e == host
         print("tinyllama: 256 decode steps, graph == eager == host; tokens", g[:16], flush=True)
+        m.close()
+
+
+def k_m_types(n_layers, base, more_type=14):
+    """llama.cpp's Q4_K_M / Q5_K_M recipe: `base` everywhere, Q6_K for output and for attn_v /
+    ffn_down of the first and last eighth of the layers and every third layer between."""
+    more = lambda l: l < n_layers // 8 or l >= 7 * n_layers // 8 or (l - n_layers // 8) % 3 == 2
+    t = {"token_embd.weight": base, "output.weight": more_type}
+    for l in range(n_layers):
+        for b in ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"):
+            t[f"blk.{l}.{b}.weight"] = more_type if b in ("attn_v", "ffn_down") and more(l) else base
+    return t
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("layout", ["q4_k_m", "q5_1"])
+def test_tinyllama_all_layers_quantized(A, oracle, layout):
+    """TinyLlama shape at all 22 layers with quantized weights from the device generator (the
+    Q4_K_M recipe, whose mixed layers keep an f16 Q/K/V; or every matrix Q5_1, the reference's
+    gemm_q5_1 rule): 64 per-position forward passes against the oracle on the read-back weights,
+    the batched prefill against both, then 64 greedy steps with graph == eager == host loop."""
+    cfg = oracle.Config(dim=2048, n_layers=22, n_heads=32, n_kv_heads=4, ffn=5632, vocab=32000, ctx_len=256)
+    with A.Context(4 << 30) as ctx:
+        if layout == "q4_k_m":
+            m = A.Model.create_mixed(ctx, model_cfg(A, cfg, cfg.ctx_len), k_m_types(cfg.n_layers, A.GGML_Q4_K))
+        else:
+            m = A.Model.create(ctx, model_cfg(A, cfg, cfg.ctx_len), A.GGML_Q5_1)
+        m.init_random(SEED)
+        om = oracle.Model(cfg, read_weights(m, oracle, cfg))
+        prompt = oracle.prompt_tokens(64, cfg.vocab, 13)
+        okv = om.new_kv()
+        ref = []
+        for p in range(len(prompt)):
+            ref.append(om.forward(okv, prompt, p))
+            got = m.forward_pass(prompt, p)
+            assert same_token(got, ref[p][0], ref[p][1], f"{layout} position {p}")
+            assert within_tol(m.logits(), ref[p][1]), p
+        per_pos_logits = m.logits()
+        nxt = m.prefill(prompt, 0)
+        assert same_token(nxt, ref[-1][0], ref[-1][1], f"{layout} prefill vs oracle")
+        assert within_tol(m.logits(), ref[-1][1]) and within_tol(m.logits(), per_pos_logits)
+        g, _ = m.decode_loop(nxt, len(prompt), 64, use_graph=True)
+        e, _ = m.decode_loop(nxt, len(prompt), 64, use_graph=False)
+        cur = list(prompt) + [nxt]
+        host = []
+        for _ in range(64):
+            host.append(m.forward_pass(cur, len(cur) - 1))
+            cur.append(host[-1])
+        assert g == e == host
+        print(f"tinyllama {layout}: 64 positions match the oracle; 64 decode steps, graph == eager == host", flush=True)
         m.close()
 
 

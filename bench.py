@@ -221,9 +221,9 @@ def q8_bench(A, seed: int, kv: int, steps: int, warmup: int, kernel_iters: int, 
             "kernel_ms": {k: round(v, 5) for k, v in kt.items()}, "tokens_head": toks[:8]}
 
 
-# Repacked matrices in HBM (records of 16 weights): 4-bit nibbles, the 5-bit types' fifth-bit
-# plane, Q6_K's 2-bit high plane, and the per-block scale planes.
-QF_TYPES = {"q4_0": 2, "q4_1": 3, "q5_0": 6, "q5_1": 7, "q4_k": 12, "q5_k": 13, "q6_k": 14}
+# Repacked matrices in HBM (records of 16 weights): 4-bit nibbles (Q2_K / Q3_K values included),
+# the 5-bit types' fifth-bit plane, Q6_K's 2-bit high plane, and the per-block scale planes.
+QF_TYPES = {"q4_0": 2, "q4_1": 3, "q5_0": 6, "q5_1": 7, "q2_k": 10, "q3_k": 11, "q4_k": 12, "q5_k": 13, "q6_k": 14}
 
 
 def qf_mat_bytes(kind: str, rows: int, cols: int) -> int:
@@ -236,6 +236,8 @@ def qf_mat_bytes(kind: str, rows: int, cols: int) -> int:
         per_row += cols // 32 * 4  # f16 (d, m)
     if kind in ("q4_k", "q5_k"):
         per_row += cols // 256 * 4  # f16 (d, dmin)
+    if kind in ("q2_k", "q3_k"):
+        per_row += cols // 16 + cols // 256 * (4 if kind == "q2_k" else 2)  # a scale byte per 16, d (dmin)
     if kind == "q6_k":
         per_row += cols // 4 + cols // 16 + cols // 256 * 2
     return rows * per_row
@@ -302,7 +304,7 @@ ALL_QUANT_KINDS = list(QF_TYPES) + list(MIXES)
 def quant_bench(A, kind: str, seed: int, kv: int, steps: int, warmup: int, kernel_iters: int,
                 use_graph: bool = True) -> dict:
     """Batch-1 greedy decode of the Llama-3-8B shape with matrices of one repacked type (Q4_0,
-    Q4_1, Q5_0, Q5_1, Q4_K, Q5_K, Q6_K), or the Q4_K_M / Q5_K_M mixes with Q6_K (random records and
+    Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K), or the Q4_K_M / Q5_K_M mixes with Q6_K (random records and
     scales for weights of std 0.02; f16 for the fused matrices a mix stores so), KV cache pre-filled
     to kv positions; same step structure and timing as the F16 decode."""
     ctx_len = kv + max(steps, warmup) + 64

@@ -27,17 +27,19 @@ int32_t launch_gemm_f16(aesir_ctx *ctx, const void *A, int64_t M, int64_t K, con
 int32_t launch_gemm_f16_mfma(aesir_ctx *ctx, const void *A, int64_t M, int64_t K, const void *B, int64_t N,
                              void *C);
 
-// A Q4_0, Q4_1, Q5_0, Q5_1, Q4_K, Q5_K or Q6_K matrix [N][K] in HBM (quant.hip), repacked from
-// its GGUF blocks into records of 16 weights: record r of a row holds weights 16 r .. 16 r + 15.
+// A Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q4_K, Q5_K or Q6_K matrix [N][K] in HBM (quant.hip),
+// repacked from its GGUF blocks into records of 16 weights: record r of a row holds weights
+// 16 r .. 16 r + 15.
 //   nib  8 bytes per record: byte j holds weight 16 r + j in its low nibble and 16 r + 8 + j in
-//        its high nibble (Q5_*, Q6_K: the low 4 bits);
+//        its high nibble (Q5_*, Q6_K: the low 4 bits; Q2_K: the 2-bit value; Q3_K: the 3-bit
+//        value q + 4, hmask bit included);
 //   hb   Q6_K: 4 bytes per record, the high 2 bits of the record's weights; Q5_0 / Q5_1 / Q5_K:
 //        4 bytes per record pair, the fifth bits of both records in one word (bit layout in
 //        quant.hip, qf_hb_pos);
 //   s0   Q4_0 / Q5_0: f16 d per 32 weights; Q4_1 / Q5_1: f16 d | f16 m << 16 per 32 weights;
-//        Q4_K / Q5_K: (scale, min) bytes per 32 weights, 6-bit values unpacked; Q6_K: int8 scale
-//        per 16 weights;
-//   s1   Q4_K / Q5_K: (d, dmin) f16 pair per 256 weights; Q6_K: f16 d per 256 weights.
+//        Q4_K / Q5_K: (scale, min) bytes per 32 weights, 6-bit values unpacked; Q6_K / Q3_K: int8
+//        scale per 16 weights; Q2_K: GGML's scale | min << 4 byte per 16 weights;
+//   s1   Q2_K / Q4_K / Q5_K: (d, dmin) f16 pair per 256 weights; Q3_K / Q6_K: f16 d per 256 weights.
 // The nib, hb and s0 planes are tiled for the matrix-core GEMV: rows in blocks of 16 and records
 // in segments of 8 (128 weights, K a multiple of 128); tile (row block, segment) stores, for
 // record pair q = (record % 8) / 2 and row i of the block, the pair's 16 nibble bytes (8 or 4 hb
@@ -67,9 +69,9 @@ __host__ __device__ inline int64_t qf_plane_row_bytes(int32_t type, int plane, i
         case 1: return K / 32 * qf_hb_bytes(type);
         case 2: return K / 32 * qf_s0_bytes(type);
         case 3:
-            return (type == AESIR_GGML_Q4_K || type == AESIR_GGML_Q5_K) ? K / 256 * 4
-                   : type == AESIR_GGML_Q6_K                          ? K / 256 * 2
-                                                                      : 0;
+            return (type == AESIR_GGML_Q4_K || type == AESIR_GGML_Q5_K || type == AESIR_GGML_Q2_K) ? K / 256 * 4
+                   : (type == AESIR_GGML_Q6_K || type == AESIR_GGML_Q3_K)                          ? K / 256 * 2
+                                                                                                   : 0;
         default: return 0;
     }
 }

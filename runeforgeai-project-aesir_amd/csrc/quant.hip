@@ -1,6 +1,7 @@
-// 4-, 5- and 6-bit weights on gfx950: GGML Q4_0, Q4_1, Q5_0 and Q5_1 (with the reference's
-// gemm_q4_0 / _q4_1 / _q5_0 / _q5_1 rounding, core/compute.mojo:876-1036) and GGML's Q4_K / Q5_K /
-// Q6_K super-blocks; Q2_K and Q3_K only through gguf_dequant_kernel.
+// 2- to 6-bit weights on gfx950: GGML Q4_0, Q4_1, Q5_0 and Q5_1 (with the reference's
+// gemm_q4_0 / _q4_1 / _q5_0 / _q5_1 rounding, core/compute.mojo:876-1036) and GGML's Q2_K / Q3_K /
+// Q4_K / Q5_K / Q6_K super-blocks. Q2_K and Q3_K values are kept in the nibble plane (0..3 and the
+// 3-bit q + 4), trading 0.17 / 0.06 bytes per weight over GGUF's packing for the 4-bit GEMV.
 //
 // GGUF stores these as packed blocks of 18 to 210 bytes whose nibble order suits a CPU
 // loop, not a wave: the bytes of one block are read by one lane, and 210 is not even 4-byte
@@ -25,7 +26,8 @@
 //         dequantize_q6_k_block (compute.mojo:508-527).
 //   Q4_1, Q5_1  w = f16(f16(q d) + m) (dequantize_q4_1 / _q5_1, compute.mojo:282-340: the f16
 //         product, then the f16 sum); Q5_0  w = f16(f16(q - 16) d) (dequantize_q5_0);
-//   Q5_K  as Q4_K with the 5-bit q.
+//   Q5_K  as Q4_K with the 5-bit q; Q2_K  as Q4_K with GGML's 4-bit scale and min per 16
+//         weights; Q3_K  w = f16(a q) with a = f16(d * sc) and the signed 3-bit q.
 // Products with x accumulate in f32 (the matrix cores, as in the F16 path's MFMA GEMMs).
 #include <type_traits>
 
@@ -41,7 +43,8 @@ constexpr unsigned kMagic = 0x64006400u;  // f16 1024 in both halves
 
 bool qf_type(int32_t t) {
     return t == AESIR_GGML_Q4_0 || t == AESIR_GGML_Q4_1 || t == AESIR_GGML_Q5_0 || t == AESIR_GGML_Q5_1 ||
-           t == AESIR_GGML_Q4_K || t == AESIR_GGML_Q5_K || t == AESIR_GGML_Q6_K;
+           t == AESIR_GGML_Q2_K || t == AESIR_GGML_Q3_K || t == AESIR_GGML_Q4_K || t == AESIR_GGML_Q5_K ||
+           t == AESIR_GGML_Q6_K;
 }
 
 // Type families of the repacked layout: a fifth-bit word per record pair (Q5_0, Q5_1, Q5_K); an
@@ -58,6 +61,11 @@ constexpr bool qf_dm() {
 template <int T>
 constexpr bool qf_kq() {
     return T == AESIR_GGML_Q4_K || T == AESIR_GGML_Q5_K;
+}
+// K-quants with a scale per 16 weights (one s0 byte per record): Q2_K, Q3_K, Q6_K.
+template <int T>
+constexpr bool qf_rs() {
+    return T == AESIR_GGML_Q2_K || T == AESIR_GGML_Q3_K || T == AESIR_GGML_Q6_K;
 }
 
 // Nibble pair f of a record holds weights a and a + 2, a = {0, 1, 4, 5, 8, 9, 12, 13}[f]: pairs
@@ -137,6 +145,18 @@ struct QRec<AESIR_GGML_Q5_K> {
     unsigned dd;
     unsigned hb;
 };
+template <>
+struct QRec<AESIR_GGML_Q2_K> {
+    u32x2 nib;
+    unsigned scm;  // GGML's byte: scale | min << 4
+    unsigned dd;   // f16 d | f16 dmin << 16
+};
+template <>
+struct QRec<AESIR_GGML_Q3_K> {
+    u32x2 nib;
+    int sc;
+    h16 d;
+};
 
 // Record `rec` of plane row `prow`.
 template <int T>
@@ -153,6 +173,12 @@ __device__ __forceinline__ QRec<T> qf_load(const QFMat &w, int64_t prow, int64_t
     } else if constexpr (qf_kq<T>()) {
         q.scm = *reinterpret_cast<const uint16_t *>(s0);
         q.dd = *reinterpret_cast<const uint32_t *>((const uint8_t *)w.s1 + qf_s1_off(prow, rec, K, 4));
+    } else if constexpr (T == AESIR_GGML_Q2_K) {
+        q.scm = s0[rec & 1];
+        q.dd = *reinterpret_cast<const uint32_t *>((const uint8_t *)w.s1 + qf_s1_off(prow, rec, K, 4));
+    } else if constexpr (T == AESIR_GGML_Q3_K) {
+        q.sc = *reinterpret_cast<const int8_t *>(s0 + (rec & 1));
+        q.d = *reinterpret_cast<const h16 *>((const uint8_t *)w.s1 + qf_s1_off(prow, rec, K, 2));
     } else {
         q.hb = *reinterpret_cast<const uint32_t *>((const uint8_t *)w.hb + qf_hbw_off(prow, rec, K));
         q.sc = *reinterpret_cast<const int8_t *>(s0 + (rec & 1));
@@ -188,8 +214,11 @@ __device__ __forceinline__ h16x2 qf_qpair(const QRec<T> &q, int f) {
         const float b = T == AESIR_GGML_Q5_0 ? 1040.0f : 1024.0f;
         const h16x2 bias = {(h16)b, (h16)b};
         return as_h2(qf_pair(q.nib, f) | qf_hb5_pair(q.hb, f) | kMagic) - bias;
-    } else if constexpr (T == AESIR_GGML_Q4_1 || T == AESIR_GGML_Q4_K) {
+    } else if constexpr (T == AESIR_GGML_Q4_1 || T == AESIR_GGML_Q4_K || T == AESIR_GGML_Q2_K) {
         const h16x2 bias = {(h16)1024.0f, (h16)1024.0f};
+        return as_h2(qf_pair(q.nib, f) | kMagic) - bias;
+    } else if constexpr (T == AESIR_GGML_Q3_K) {
+        const h16x2 bias = {(h16)1028.0f, (h16)1028.0f};
         return as_h2(qf_pair(q.nib, f) | kMagic) - bias;
     } else {
         const h16x2 bias = {(h16)1056.0f, (h16)1056.0f};
@@ -219,6 +248,13 @@ __device__ __forceinline__ void qf_deq16(const QRec<T> &q, u32x4 (&o)[2]) {
         const h16x2 dm = as_h2(q.dm);
         aa = h16x2{dm.x, dm.x};
         nbb = h16x2{dm.y, dm.y};  // the added min
+    } else if constexpr (T == AESIR_GGML_Q2_K) {
+        const h16x2 ab = q4k_scales(as_h2(q.dd), h16x2{(h16)(float)(q.scm & 15u), (h16)(float)(q.scm >> 4)});
+        aa = h16x2{ab.x, ab.x};
+        nbb = h16x2{-ab.y, -ab.y};
+    } else if constexpr (T == AESIR_GGML_Q3_K) {
+        const h16 a = q6k_scale(q.d, q.sc);
+        aa = h16x2{a, a};
     } else if constexpr (qf_kq<T>()) {
         const h16x2 sm = {(h16)(float)(q.scm & 0xffu), (h16)(float)(q.scm >> 8)};
         const h16x2 ab = q4k_scales(as_h2(q.dd), sm);
@@ -233,7 +269,7 @@ __device__ __forceinline__ void qf_deq16(const QRec<T> &q, u32x4 (&o)[2]) {
         const h16x2 v = qf_qpair(q, f);
         if constexpr (T == AESIR_GGML_Q4_0 || T == AESIR_GGML_Q5_0) wp[f] = h2_bits(q4_0_w2(v, aa));
         else if constexpr (qf_dm<T>()) wp[f] = h2_bits(q4_1_w2(v, aa, nbb));
-        else if constexpr (qf_kq<T>()) wp[f] = h2_bits(q4k_w2(v, aa, nbb));
+        else if constexpr (qf_kq<T>() || T == AESIR_GGML_Q2_K) wp[f] = h2_bits(q4k_w2(v, aa, nbb));
         else wp[f] = h2_bits(q6k_w2(v, aa));
     }
     qf_unpair(wp, o);
@@ -333,7 +369,7 @@ __global__ __launch_bounds__(256) void qf_repack_kernel(const uint8_t *__restric
     const int64_t prow = dst.row0 + r * step;
     int q[kRec];
 #pragma unroll
-    for (int i = 0; i < kRec; i++) q[i] = gguf_q<T>(src, k + i);
+    for (int i = 0; i < kRec; i++) q[i] = gguf_q<T>(src, k + i) + (T == AESIR_GGML_Q3_K ? 4 : 0);  // Q3_K: 0..7
     unsigned nib[2] = {0u, 0u}, hb = 0u;
 #pragma unroll
     for (int j = 0; j < 8; j++) nib[j >> 2] |= (unsigned)((q[j] & 15) | ((q[8 + j] & 15) << 4)) << (8 * (j & 3));
@@ -362,6 +398,23 @@ __global__ __launch_bounds__(256) void qf_repack_kernel(const uint8_t *__restric
                                                     ((uint32_t)blk[3] << 24);
             else
                 *reinterpret_cast<uint16_t *>(s0) = (uint16_t)(blk[0] | (blk[1] << 8));
+        }
+    } else if constexpr (T == AESIR_GGML_Q2_K || T == AESIR_GGML_Q3_K) {
+        // the record's 16-weight sub-block: its scale byte (Q2_K: scale | min << 4 as GGML packs
+        // it; Q3_K: the unpacked signed scale), and the super-block's d (and dmin)
+        const int i = (int)(k % 256), is = 8 * (i / 128) + 2 * ((i / 32) & 3) + ((i / 16) & 1);
+        if constexpr (T == AESIR_GGML_Q2_K) {
+            const uint8_t *blk = src + (k / 256) * 84;
+            s0[rec & 1] = blk[is];
+            if (rec % 16 == 0)
+                *reinterpret_cast<uint32_t *>((uint8_t *)dst.s1 + qf_s1_off(prow, rec, K, 4)) =
+                    (uint32_t)blk[80] | ((uint32_t)blk[81] << 8) | ((uint32_t)blk[82] << 16) | ((uint32_t)blk[83] << 24);
+        } else {
+            const uint8_t *blk = src + (k / 256) * 110;
+            s0[rec & 1] = (uint8_t)(int8_t)q3k_scale(blk + 96, is);
+            if (rec % 16 == 0)
+                *reinterpret_cast<uint16_t *>((uint8_t *)dst.s1 + qf_s1_off(prow, rec, K, 2)) =
+                    (uint16_t)(blk[108] | (blk[109] << 8));
         }
     } else if constexpr (qf_kq<T>()) {
         const uint8_t *blk = src + (k / 256) * (T == AESIR_GGML_Q4_K ? 144 : 176);
@@ -483,7 +536,10 @@ __global__ __launch_bounds__(256) void qf_fill_kernel(QFMat w, int64_t rows, int
     const int64_t r = gid / recs, rec = gid % recs, prow = w.row0 + r * step;
     const uint64_t a = mix64(base + (uint64_t)(2 * gid + 1) * kGolden);
     const uint64_t b = mix64(base + (uint64_t)(2 * gid + 2) * kGolden);
-    *reinterpret_cast<u32x2 *>((uint8_t *)w.nib + qf_nib_off(prow, rec, K)) = u32x2{(unsigned)a, (unsigned)(a >> 32)};
+    // Q2_K / Q3_K keep 2- / 3-bit values in the nibbles
+    constexpr unsigned nmask = T == AESIR_GGML_Q2_K ? 0x33333333u : T == AESIR_GGML_Q3_K ? 0x77777777u : 0xFFFFFFFFu;
+    *reinterpret_cast<u32x2 *>((uint8_t *)w.nib + qf_nib_off(prow, rec, K)) =
+        u32x2{(unsigned)a & nmask, (unsigned)(a >> 32) & nmask};
     uint8_t *s0 = (uint8_t *)w.s0 + qf_s0_off(prow, rec, K, qf_s0_bytes(T));
     const float u = (float)(b >> 40) * (1.0f / 16777216.0f);  // [0, 1)
     // 5-bit types: uniform fifth bits, one word per record pair (written by the even record)
@@ -500,6 +556,19 @@ __global__ __launch_bounds__(256) void qf_fill_kernel(QFMat w, int64_t rows, int
             const h16 d = (h16)((0.5f + u) * std / qsd), m = (h16)(-qmid * (float)d);
             *reinterpret_cast<uint32_t *>(s0) = (uint32_t)h_to_bits(d) | ((uint32_t)h_to_bits(m) << 16);
         }
+    } else if constexpr (T == AESIR_GGML_Q2_K) {
+        // q uniform on [0, 3] (standard deviation 1.118); sc in [4, 8], m = round(1.5 sc), dmin = d
+        const int sc = 4 + (int)((b >> 8) % 5), m = (int)(1.5f * (float)sc + 0.5f);
+        s0[rec & 1] = (uint8_t)(sc | (m << 4));
+        if (rec % 16 == 0) {
+            const uint32_t dv = h_to_bits((h16)((0.5f + u) * std / (6.0f * 1.118f)));
+            *reinterpret_cast<uint32_t *>((uint8_t *)w.s1 + qf_s1_off(prow, rec, K, 4)) = dv | (dv << 16);
+        }
+    } else if constexpr (T == AESIR_GGML_Q3_K) {
+        // q - 4 uniform on [-4, 3] (standard deviation 2.29); sc in [16, 31]
+        s0[rec & 1] = (uint8_t)(16 + (int)((b >> 4) % 16));
+        if (rec % 16 == 0)
+            *reinterpret_cast<h16 *>((uint8_t *)w.s1 + qf_s1_off(prow, rec, K, 2)) = (h16)((0.5f + u) * std / (24.0f * 2.29f));
     } else if constexpr (qf_kq<T>()) {
         // sc in [4, 8], m = round(qmid sc / mk), dmin = mk d: w = d sc (q - qmid) nearly, m within
         // the 6 bits GGML's packing holds
@@ -527,8 +596,8 @@ static unsigned rec_grid(int64_t rows, int64_t K) { return (unsigned)((rows * (K
 
 static int32_t qf_check(int32_t type, int64_t K, const char *name) {
     if (!qf_type(type))
-        return fail(AESIR_ERR_UNSUPPORTED, "%s: weight type %d is not Q4_0, Q4_1, Q5_0, Q5_1, Q4_K, Q5_K or Q6_K", name,
-                    (int)type);
+        return fail(AESIR_ERR_UNSUPPORTED,
+                    "%s: weight type %d is not Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q4_K, Q5_K or Q6_K", name, (int)type);
     const int64_t blk = gguf_block_elems(type);
     if (K <= 0 || K % blk != 0)
         return fail(AESIR_ERR_SHAPE, "%s: row length %lld is not a multiple of the %lld-weight block", name, (long long)K,
@@ -544,6 +613,8 @@ static void qf_switch(int32_t type, F &&f) {
         case AESIR_GGML_Q4_1: f(std::integral_constant<int, AESIR_GGML_Q4_1>{}); break;
         case AESIR_GGML_Q5_0: f(std::integral_constant<int, AESIR_GGML_Q5_0>{}); break;
         case AESIR_GGML_Q5_1: f(std::integral_constant<int, AESIR_GGML_Q5_1>{}); break;
+        case AESIR_GGML_Q2_K: f(std::integral_constant<int, AESIR_GGML_Q2_K>{}); break;
+        case AESIR_GGML_Q3_K: f(std::integral_constant<int, AESIR_GGML_Q3_K>{}); break;
         case AESIR_GGML_Q4_K: f(std::integral_constant<int, AESIR_GGML_Q4_K>{}); break;
         case AESIR_GGML_Q5_K: f(std::integral_constant<int, AESIR_GGML_Q5_K>{}); break;
         default: f(std::integral_constant<int, AESIR_GGML_Q6_K>{}); break;
@@ -733,6 +804,18 @@ struct QTile<AESIR_GGML_Q5_K> {
     unsigned s1;  // f16 d | f16 dmin << 16
     unsigned hb;
 };
+template <>
+struct QTile<AESIR_GGML_Q2_K> {
+    u32x4 nib;
+    unsigned s0;  // the two records' scale | min << 4 bytes
+    unsigned s1;  // f16 d | f16 dmin << 16
+};
+template <>
+struct QTile<AESIR_GGML_Q3_K> {
+    u32x4 nib;
+    unsigned s0;  // int8 scales of the two records
+    unsigned s1;  // f16 super-block d in the low half
+};
 
 // Buffer resources of a matrix's planes (range-checked loads, tile offsets in SGPRs).
 struct QfRsrc {
@@ -758,7 +841,8 @@ __device__ __forceinline__ QTile<T> qf_tile_load(const QfRsrc &r, int tile, int 
     else
         q.s0 = __builtin_amdgcn_raw_buffer_load_b16(r.s0, lane * 2, tile * 128, 0);
     if constexpr (qf_hb5<T>()) q.hb = __builtin_amdgcn_raw_buffer_load_b32(r.hb, lane * 4, tile * 256, 0);
-    if constexpr (qf_kq<T>()) q.s1 = __builtin_amdgcn_raw_buffer_load_b32(r.s1, s1v, s1s, 0);
+    if constexpr (qf_kq<T>() || T == AESIR_GGML_Q2_K) q.s1 = __builtin_amdgcn_raw_buffer_load_b32(r.s1, s1v, s1s, 0);
+    if constexpr (T == AESIR_GGML_Q3_K) q.s1 = __builtin_amdgcn_raw_buffer_load_b16(r.s1, s1v, s1s, 0);
     if constexpr (T == AESIR_GGML_Q6_K) {
         q.hb = __builtin_amdgcn_raw_buffer_load_b64(r.hb, lane * 8, tile * 512, 2);
         q.s1 = __builtin_amdgcn_raw_buffer_load_b16(r.s1, s1v, s1s, 0);
@@ -788,6 +872,43 @@ __device__ __forceinline__ void qf_tile_a(const QTile<T> &q, const QfRegs &k, u3
             a[j].y = h2_bits(q4_0_w2(as_h2((t & k.lo) | k.magic) + blo, dd));
             a[j].z = h2_bits(q4_0_w2(__builtin_elementwise_fma(as_h2((v & k.hi) | k.magic), s16, bhi), dd));
             a[j].w = h2_bits(q4_0_w2(__builtin_elementwise_fma(as_h2((t & k.hi) | k.magic), s16, bhi), dd));
+        }
+    } else if constexpr (T == AESIR_GGML_Q2_K || T == AESIR_GGML_Q3_K) {
+        // a scale per record (16 weights): the lane's two records have their own; the values are
+        // q (Q2_K) or q - 4 (Q3_K, its nibble holding q + 4), then Q4_K's or Q6_K's rule
+        constexpr float off = T == AESIR_GGML_Q3_K ? 4.0f : 0.0f;
+        const h16x2 blo = {(h16)(-1024.0f - off), (h16)(-1024.0f - off)}, bhi = {(h16)(-64.0f - off), (h16)(-64.0f - off)};
+        h16x2 aa[2], nbb[2];
+        if constexpr (T == AESIR_GGML_Q2_K) {
+            const h16x2 b1024 = {(h16)-1024.0f, (h16)-1024.0f};
+#pragma unroll
+            for (int r = 0; r < 2; r++) {
+                const unsigned x = q.s0 >> (8 * r);  // scale | min << 4
+                const h16x2 sm = as_h2(((x & 15u) | ((x & 0xF0u) << 12)) | k.magic) + b1024;
+                const h16x2 ab = q4k_scales(as_h2(q.s1), sm);
+                aa[r] = h16x2{ab.x, ab.x};
+                nbb[r] = h16x2{-ab.y, -ab.y};
+            }
+        } else {
+            const h16x2 b1152 = {(h16)-1152.0f, (h16)-1152.0f};
+            const h16x2 sc = as_h2(__builtin_amdgcn_perm(0u, q.s0 ^ 0x8080u, 0x0c010c00u) | k.magic) + b1152;
+            const h16 d = bits_to_h((uint16_t)(q.s1 & 0xffffu));
+            const h16x2 a01 = h16x2{d, d} * sc;  // (f16(d sc0), f16(d sc1))
+            aa[0] = h16x2{a01.x, a01.x};
+            aa[1] = h16x2{a01.y, a01.y};
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int r = j >> 1;
+            auto rule = [&](h16x2 v) {
+                if constexpr (T == AESIR_GGML_Q2_K) return q4k_w2(v, aa[r], nbb[r]);
+                else return q6k_w2(v, aa[r]);
+            };
+            const unsigned v = nw[j], t = v >> 8;
+            a[j].x = h2_bits(rule(as_h2((v & k.lo) | k.magic) + blo));
+            a[j].y = h2_bits(rule(as_h2((t & k.lo) | k.magic) + blo));
+            a[j].z = h2_bits(rule(__builtin_elementwise_fma(as_h2((v & k.hi) | k.magic), s16, bhi)));
+            a[j].w = h2_bits(rule(__builtin_elementwise_fma(as_h2((t & k.hi) | k.magic), s16, bhi)));
         }
     } else if constexpr (T != AESIR_GGML_Q6_K) {
         // Q4_1, Q5_0, Q5_1, Q4_K, Q5_K: the exact quantized pairs (q - 16 for Q5_0, else q), the
@@ -902,7 +1023,7 @@ __global__ __launch_bounds__(NW * kWave) void gemv_qf_kernel(QFMat w, int64_t N,
     const int blocks = (int)((N + 15) / 16);
     const int pb0 = (int)(w.row0 / 16);  // plane row block of row 0
     const QfRsrc rs = qf_rsrc(w, T, w.row0 + (int64_t)blocks * 16, K);
-    constexpr int es1 = qf_kq<T>() ? 4 : 2;
+    constexpr int es1 = (qf_kq<T>() || T == AESIR_GGML_Q2_K) ? 4 : 2;
     const int sbr = (int)(K / 256);  // s1 entries per row
     const int s1v = (lane & 15) * es1;
     // steps of this workgroup: (block k, round r), r < R, for its nb blocks

@@ -1,10 +1,10 @@
-"""GPU parity of the repacked weight types, Q4_0, Q4_1, Q5_0, Q5_1, Q4_K, Q5_K and Q6_K (tiled
-records, the matrix-core decode GEMV with the fused epilogues, batched prefill, GGUF loading),
-against the CPU oracle.
+"""GPU parity of the repacked weight types, Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q4_K, Q5_K and Q6_K
+(tiled records, the matrix-core decode GEMV with the fused epilogues, batched prefill, GGUF
+loading), against the CPU oracle.
 
 - aesir_gemm_quant on packed GGUF blocks: Q4_0, Q4_1, Q5_0 and Q5_1 within 1 f16 ulp of the
   oracle's reference-order gemm_q4_0 / _q4_1 / _q5_0 / _q5_1 (core/compute.mojo:876-1036; beyond
-  1 ulp only where f32 summation noise exceeds it); Q4_K / Q5_K / Q6_K against f64 on the oracle's
+  1 ulp only where f32 summation noise exceeds it); the K-quants against f64 on the oracle's
   f16 weights (the rule every kernel of the library applies) within one f16 rounding of the
   output plus f32 summation noise. 16 or more rows of A, and rows whose length is not a multiple
   of 128, take the F16 GEMM on the same f16 weights and are held to f64 on those.
@@ -45,7 +45,7 @@ def well_scope(ctx):
     ctx.reset(off)
 
 
-TYPES = {"q4_0": 2, "q4_1": 3, "q5_0": 6, "q5_1": 7, "q4_k": 12, "q5_k": 13, "q6_k": 14}
+TYPES = {"q4_0": 2, "q4_1": 3, "q5_0": 6, "q5_1": 7, "q2_k": 10, "q3_k": 11, "q4_k": 12, "q5_k": 13, "q6_k": 14}
 LEGACY_KINDS = ("q4_1", "q5_0", "q5_1")
 
 
@@ -76,7 +76,7 @@ def test_gemm_quant_vs_oracle(A, ctx, oracle, kind, M, K, N):
         d = ulp_diff(got.astype(np.float16), ref)
         bad = (d > 1) & (np.abs(got - ref.astype(np.float64)) > noise)
         assert not bad.any(), d.max()
-        assert (d > 0).mean() < 0.02
+        assert (d > 0).mean() < 0.02 or (d > 0).sum() <= 1  # nearly all outputs identical
         return
     exact = xd @ W.T
     tol = np.abs(np.spacing(exact.astype(np.float16))).astype(np.float64) + noise

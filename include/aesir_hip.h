@@ -277,11 +277,10 @@ int32_t aesir_model_create(aesir_ctx *ctx, const aesir_model_config *cfg, aesir_
  * quants [rows][cols] plus f16 block scales [rows][cols/32] in HBM (same fused row order as F16);
  * dim and ffn must be multiples of 32 (and at most 16384). Every weight is used as
  * w = f16(f16(q) * d), gemm_q8_0's rule (core/compute.mojo:1062-1063), so a Q8_0 model computes
- * what the F16 model holding the dequantized weights computes. A Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q4_K /
- * Q5_K / Q6_K model keeps each matrix repacked into 16-weight records in 16-row x 128-weight tiles
- * (nibble plane, per-block scale planes, a fifth-bit or high-bit plane); dim and ffn must be
- * multiples of 128 (32-weight blocks) or 256 (K-quants), at most 28672. Q2_K and Q3_K matrices are
- * kept in f16, dequantized on the device at upload (dim and ffn multiples of 256). Every type's
+ * what the F16 model holding the dequantized weights computes. A model of any other block type
+ * keeps each matrix repacked into 16-weight records in 16-row x 128-weight tiles (nibble plane,
+ * per-block scale planes, a fifth-bit or high-bit plane; Q2_K / Q3_K values in the nibbles); dim
+ * and ffn must be multiples of 128 (32-weight blocks) or 256 (K-quants), at most 28672. Every type's
  * weights are the f16 values of aesir_gemm_quant's rules, so a model of any type computes what
  * the F16 model holding its read-back weights computes. Norm vectors stay f16. No reference
  * counterpart as a model (the reference loader has no quantized model path,
@@ -291,10 +290,10 @@ int32_t aesir_model_create_typed(aesir_ctx *ctx, const aesir_model_config *cfg, 
 /* aesir_model_create_typed with one type per matrix: tensor_types holds n_types = 2 + 7 * n_layers
  * ids in the order token_embd, output, then per layer attn_q, attn_k, attn_v, attn_output,
  * ffn_gate, ffn_up, ffn_down (each F16 or a type aesir_model_create_typed takes, with that
- * type's dim / ffn constraints). Each matrix keeps its own type in HBM (Q2_K / Q3_K in f16),
- * except the two fused ones: a layer's Q/K/V (and its gate/up) matrix is stored in f16 when its
- * parts differ in type, each part dequantized at upload by its type's rule. aesir_model_set_tensor then takes each tensor in its
- * own type. This is the layout of GGUF files that mix types (Q4_K_M and the like). No reference
+ * type's dim / ffn constraints). Each matrix keeps its own type in HBM, except the two fused
+ * ones: a layer's Q/K/V (and its gate/up) matrix is stored in f16 when its parts differ in type,
+ * each part dequantized at upload by its type's rule. aesir_model_set_tensor then takes each
+ * tensor in its own type. This is the layout of GGUF files that mix types (Q4_K_M and the like). No reference
  * counterpart (the reference loader takes F16 files only, loader/gguf.mojo:450-463). */
 int32_t aesir_model_create_mixed(aesir_ctx *ctx, const aesir_model_config *cfg, const int32_t *tensor_types,
                                  int64_t n_types, aesir_model **out);
@@ -326,8 +325,7 @@ int32_t aesir_model_get_tensor(aesir_model *model, const char *name, void *host_
  * test oracle's generator. For models too large to build on the host. Q8_0 matrices get
  * quants uniform in [-127, 127] and block scales uniform in [0.5, 1.5) * std / 64 (weights of
  * standard deviation near std); repacked matrices get uniform nibbles (and fifth or high bits)
- * with scales chosen for a standard deviation near std; Q2_K / Q3_K matrices (kept in f16) are
- * filled as F16. */
+ * with scales chosen for a standard deviation near std. */
 int32_t aesir_model_init_random(aesir_model *model, uint64_t seed, float std, float norm_mean, float norm_std);
 /* GGUFSeer.mmap_and_load (loader/gguf.mojo:664-690) + AesirEngine.__init__'s layer setup
  * (aesir.mojo:237-296): parses a GGUF v3 Llama F16 file, enforces the reference loader

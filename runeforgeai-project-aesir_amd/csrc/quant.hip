@@ -62,11 +62,7 @@ template <int T>
 constexpr bool qf_kq() {
     return T == AESIR_GGML_Q4_K || T == AESIR_GGML_Q5_K;
 }
-// K-quants with a scale per 16 weights (one s0 byte per record): Q2_K, Q3_K, Q6_K.
-template <int T>
-constexpr bool qf_rs() {
-    return T == AESIR_GGML_Q2_K || T == AESIR_GGML_Q3_K || T == AESIR_GGML_Q6_K;
-}
+
 
 // Nibble pair f of a record holds weights a and a + 2, a = {0, 1, 4, 5, 8, 9, 12, 13}[f]: pairs
 // 0-3 are low nibbles, 4-7 high nibbles. In the Q6_K high-bit word, pair f's two 2-bit fields sit
@@ -453,8 +449,8 @@ __global__ __launch_bounds__(256) void qf_dequant_kernel(QFMat w, int64_t rows, 
 }
 
 // One thread per record: GGUF blocks -> f16 weights straight from the blocks, with the same
-// weight rules (and instructions) as qf_deq16 for the repacked types; the only path of the types
-// this library keeps in f16 (Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q5_K).
+// weight rules (and instructions) as qf_deq16 (the f16 route of aesir_gemm_quant, and the parts of
+// a fused model matrix stored in f16).
 template <int T>
 __global__ __launch_bounds__(256) void gguf_dequant_kernel(const uint8_t *__restrict__ blocks, int64_t rows, int64_t K,
                                                            h16 *__restrict__ out, int64_t out_stride) {

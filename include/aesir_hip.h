@@ -125,7 +125,9 @@ int32_t aesir_timer_stop(aesir_ctx *ctx, float *elapsed_ms);
 /* gemm_f16 (core/compute.mojo:1751-1854) and the AMD realm hook gemm_f16_gpu(...,
  * AMD_ROCM_HIP) -> AMDGate.launch_gemm_amd (core/compute.mojo:2554-2556,
  * core/amd_gate.mojo:113-167). C[m,n] = f16(sum_k f32(A[m,k]) * f32(B[n,k])), f32 accumulation.
- * Raises "gemm_f16: matrix dimensions must be positive", "gemm_f16: inner matrix dimension
+ * One row of A runs the decode GEMV; two or more the matrix-core GEMM (a_cols a multiple of 64,
+ * 16-byte aligned operands; other shapes the GEMV per row). Raises "gemm_f16: matrix dimensions
+ * must be positive", "gemm_f16: inner matrix dimension
  * mismatch", "gemm_f16: output matrix shape mismatch". */
 int32_t aesir_gemm_f16(aesir_ctx *ctx, const void *A, int64_t a_rows, int64_t a_cols, const void *B,
                        int64_t b_rows, int64_t b_cols, void *C, int64_t c_rows, int64_t c_cols);
@@ -275,7 +277,7 @@ int32_t aesir_model_create(aesir_ctx *ctx, const aesir_model_config *cfg, aesir_
  * or one of the GGML block types AESIR_GGML_Q4_0, _Q4_1, _Q5_0, _Q5_1, _Q2_K, _Q3_K, _Q4_K, _Q5_K,
  * _Q6_K. A Q8_0 model keeps each matrix as int8
  * quants [rows][cols] plus f16 block scales [rows][cols/32] in HBM (same fused row order as F16);
- * dim and ffn must be multiples of 32 (and at most 16384). Every weight is used as
+ * dim and ffn must be multiples of 32 (and at most 28672). Every weight is used as
  * w = f16(f16(q) * d), gemm_q8_0's rule (core/compute.mojo:1062-1063), so a Q8_0 model computes
  * what the F16 model holding the dequantized weights computes. A model of any other block type
  * keeps each matrix repacked into 16-weight records in 16-row x 128-weight tiles (nibble plane,

@@ -21,7 +21,9 @@ int32_t aesir_gemm_f16(aesir_ctx *ctx, const void *A, int64_t a_rows, int64_t a_
     if (a_cols != b_cols) return fail(AESIR_ERR_SHAPE, "gemm_f16: inner matrix dimension mismatch");
     if (c_rows != a_rows || c_cols != b_rows) return fail(AESIR_ERR_SHAPE, "gemm_f16: output matrix shape mismatch");
     if (!A || !B || !C) return fail(AESIR_ERR_INVALID, "gemm_f16: null tensor pointer");
-    if (a_rows >= 16) return launch_gemm_f16_mfma(ctx, A, a_rows, a_cols, B, b_rows, C);
+    // One row of A: the decode GEMV. More rows: the matrix-core GEMM, which reads B once for all
+    // rows (the GEMV would read it once per row); shapes it does not tile fall back to the GEMV.
+    if (a_rows >= 2) return launch_gemm_f16_mfma(ctx, A, a_rows, a_cols, B, b_rows, C);
     return launch_gemm_f16(ctx, A, a_rows, a_cols, B, b_rows, C);
 }
 
@@ -244,7 +246,7 @@ int32_t aesir_gemm_quant(aesir_ctx *ctx, const void *A, int64_t a_rows, int64_t 
     if (!A || !blocks || !C) return fail(AESIR_ERR_INVALID, "%s: null tensor pointer", nm);
     // Fewer than 16 rows of A on whole 128-weight segments of a repacked type (Q4_0, Q4_K, Q6_K):
     // the blocks are repacked into tiled records and each row runs the decode GEMV. Otherwise the
-    // blocks are dequantized to f16 (the same values) for the F16 GEMM, on the matrix cores from 16
+    // blocks are dequantized to f16 (the same values) for the F16 GEMM, on the matrix cores from 2
     // rows. Both take free well space for this call, released after enqueueing (later work on the
     // stream runs after these kernels).
     const int64_t K = a_cols, N = b_rows, mark = ctx->well_offset;
@@ -269,7 +271,7 @@ int32_t aesir_gemm_quant(aesir_ctx *ctx, const void *A, int64_t a_rows, int64_t 
         rc = well_alloc_bytes(ctx, mul_checked(N, K, 2), &wf);
         if (rc == AESIR_OK) rc = launch_gguf_dequant(ctx->stream, ggml_type, blocks, N, K, wf, K);
         if (rc == AESIR_OK)
-            rc = a_rows >= 16 ? launch_gemm_f16_mfma(ctx, A, a_rows, K, wf, N, C) : launch_gemm_f16(ctx, A, a_rows, K, wf, N, C);
+            rc = a_rows >= 2 ? launch_gemm_f16_mfma(ctx, A, a_rows, K, wf, N, C) : launch_gemm_f16(ctx, A, a_rows, K, wf, N, C);
     }
     ctx->well_offset = mark;
     return rc;

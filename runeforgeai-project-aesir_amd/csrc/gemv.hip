@@ -510,7 +510,7 @@ static int32_t gemv_q8_dispatch(hipStream_t s, const void *Wq, const void *Wd, i
             AESIR_GEMV_Q8(8, 7)
             AESIR_GEMV_Q8(8, 8)
             default:
-                return fail(AESIR_ERR_UNSUPPORTED, "%s: Q8_0 GEMV with K = %lld exceeds 16384", name, (long long)K);
+                return fail(AESIR_ERR_UNSUPPORTED, "%s: Q8_0 GEMV with K = %lld exceeds 28672", name, (long long)K);
         }
     } else {
         switch (ns) {
@@ -518,8 +518,11 @@ static int32_t gemv_q8_dispatch(hipStream_t s, const void *Wq, const void *Wd, i
             AESIR_GEMV_Q8(16, 2)
             AESIR_GEMV_Q8(16, 3)
             AESIR_GEMV_Q8(16, 4)
+            AESIR_GEMV_Q8(16, 5)
+            AESIR_GEMV_Q8(16, 6)
+            AESIR_GEMV_Q8(16, 7)
             default:
-                return fail(AESIR_ERR_UNSUPPORTED, "%s: Q8_0 GEMV with K = %lld exceeds 16384", name, (long long)K);
+                return fail(AESIR_ERR_UNSUPPORTED, "%s: Q8_0 GEMV with K = %lld exceeds 28672", name, (long long)K);
         }
     }
 #undef AESIR_GEMV_Q8

@@ -120,6 +120,8 @@ int32_t launch_gguf_dequant(hipStream_t s, int32_t type, const void *blocks, int
 int64_t gguf_block_elems(int32_t type);
 // The decode GEMV stages x in LDS (2 K bytes) and works on whole 128-weight segments.
 constexpr int64_t kQfGemvMaxK = 28672;
+// The Q8_0 decode GEMV holds x in registers, 16 values per thread per 4096-wide slab, 7 slabs.
+constexpr int64_t kQ8GemvMaxK = 28672;
 bool qf_gemv_ok(int64_t K);
 // y[n] = f16(sum_k x[k] w[n, k]) for one row of x (the per-op GEMV of a repacked matrix).
 int32_t launch_qf_gemv_store(hipStream_t s, const QFMat &w, int64_t N, int64_t K, const void *x, void *y);

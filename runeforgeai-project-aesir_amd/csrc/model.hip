@@ -504,8 +504,8 @@ int32_t model_create(aesir_ctx *ctx, const aesir_model_config *cfg, const Weight
                 return fail(AESIR_ERR_UNSUPPORTED, "model: %s weights need dim and ffn to be multiples of %lld",
                             ggml_type_name(wt), (long long)blk);
         }
-        if (wt == AESIR_GGML_Q8_0 && (c.dim % 32 != 0 || c.ffn % 32 != 0 || c.dim > 16384 || c.ffn > 16384))
-            return fail(AESIR_ERR_UNSUPPORTED, "model: Q8_0 weights need dim and ffn to be multiples of 32, at most 16384");
+        if (wt == AESIR_GGML_Q8_0 && (c.dim % 32 != 0 || c.ffn % 32 != 0 || c.dim > kQ8GemvMaxK || c.ffn > kQ8GemvMaxK))
+            return fail(AESIR_ERR_UNSUPPORTED, "model: Q8_0 weights need dim and ffn to be multiples of 32, at most 28672");
         if (qf_type(wt)) {
             // whole 128-weight segments of the repacked planes; K-quant super-blocks of 256
             const int64_t blk = gguf_block_elems(wt) == 32 ? 128 : 256;

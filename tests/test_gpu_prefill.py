@@ -66,9 +66,10 @@ def gpu_model(A, ctx, ocfg, weights):
 @pytest.mark.parametrize("M,K,N", [(16, 64, 32), (37, 4096, 1000), (128, 2048, 2560), (200, 256, 300),
                                    (128, 5632, 128), (129, 32, 17), (128, 2048, 11264), (100, 1024, 16500),
                                    (64, 128, 16384), (200, 256, 9000), (96, 8192, 256), (65, 384, 4100),
-                                   (128, 4096, 1000)])
+                                   (128, 4096, 1000), (2, 4096, 4096), (8, 2048, 5632), (15, 14336, 512)])
 def test_mfma_gemm_vs_oracle(A, ctx, oracle, M, K, N):
-    """The 32 x 64 kernel (M <= 64 or K % 128 != 0) and the 128-row wide-tile kernel (M > 64,
+    """The 32 x 64 kernel (M <= 64 or K % 128 != 0; from M = 2, rows past M read as zeros) and the
+    128-row wide-tile kernel (M > 64,
     K % 128 == 0): NT = 64 columns from N = 4096 up, else 32; with M and N tails, a single K
     chunk, two M tiles, 8 K splits (96 x 8192 x 256, 128 x 4096 x 1000; fewer where the context's
     partial buffer is smaller) and an odd 3-chunk K without split (65 x 384 x 4100)."""

@@ -5,8 +5,9 @@ A Q8_0 model uses every weight as w = f16(f16(q) * d), gemm_q8_0's rule
 dequantized weights: identical greedy tokens, logits within max-abs 2e-2 / rel 1e-2. Covered:
 - the read-back of every matrix equals the host dequantization bit for bit (repacking into
   quants + scales loses nothing; fused Q|K|V and interleaved gate/up placement included);
-- shapes where K < 4096 (idle threads), K = 4096 and partial last slabs (K = 5632, 14336), the
-  Q8_0 embedding row fused into layer 0, and the Q8_0 lm_head with its argmax;
+- shapes where K < 4096 (idle threads), K = 4096, partial last slabs (K = 5632, 14336, 16896)
+  and the longest row, K = 28672; the Q8_0 embedding row fused into layer 0, and the Q8_0
+  lm_head with its argmax;
 - a GGUF v3 file with Q8_0 matrices loads into the same model as set_tensor builds;
 - graph replay equals eager launches; the batched prefill (Q8_0 MFMA GEMMs) equals the
   per-position oracle; device init draws quants and scales in their stated ranges.
@@ -19,6 +20,10 @@ pytestmark = pytest.mark.gpu
 Q8_SMALL = dict(dim=128, n_layers=2, n_heads=4, n_kv_heads=2, ffn=256, vocab=500, ctx_len=128)
 Q8_TL = dict(dim=2048, n_layers=2, n_heads=32, n_kv_heads=4, ffn=5632, vocab=32000, ctx_len=64)
 Q8_L3 = dict(dim=4096, n_layers=1, n_heads=32, n_kv_heads=8, ffn=14336, vocab=4096, ctx_len=32)
+# rows past 16384 weights: five 4096-wide slabs (the last partial) in QKV, O and the lm_head; seven
+# in ffn_down at a 70B-class ffn of 28672, the longest row the Q8_0 decode GEMV takes
+Q8_WIDE = dict(dim=16896, n_layers=1, n_heads=132, n_kv_heads=11, ffn=256, vocab=256, ctx_len=16)
+Q8_LONG_FFN = dict(dim=256, n_layers=1, n_heads=4, n_kv_heads=2, ffn=28672, vocab=256, ctx_len=16)
 
 
 @pytest.fixture(scope="module")
@@ -129,11 +134,11 @@ def test_q8_small_model_matches_dequantized_oracle(A, ctx, oracle):
     m.close()
 
 
-@pytest.mark.parametrize("shape", ["tinyllama", "llama3"])
+@pytest.mark.parametrize("shape", ["tinyllama", "llama3", "wide", "long_ffn"])
 def test_q8_model_shapes_match_dequantized_oracle(A, ctx, oracle, shape):
     """K = 2048 (half the threads idle) and 5632 (partial second slab); K = 4096 and 14336
-    (partial fourth slab)."""
-    cfg = Q8_TL if shape == "tinyllama" else Q8_L3
+    (partial fourth slab); K = 16896 (partial fifth slab) and 28672 (seven slabs)."""
+    cfg = {"tinyllama": Q8_TL, "llama3": Q8_L3, "wide": Q8_WIDE, "long_ffn": Q8_LONG_FFN}[shape]
     tensors, deq = q8_weights(A, oracle, cfg, 5)
     m = q8_model(A, ctx, cfg, tensors)
     om = oracle.Model(oracle.Config(**cfg), deq)

@@ -372,16 +372,17 @@ def sampler_bench(A, seed: int, reps: int = 50) -> dict:
 
 
 def kv_sweep_bench(A, seed: int, kvs=(512, 8192, 32768), steps: int = 64, warmup: int = 8) -> dict:
-    """The F16 decode of the headline at the other KV lengths of the Llama-3-8B config (one model
-    whose cache is pre-filled to the longest length; each point decodes from that position)."""
-    ctx_len = max(kvs) + steps + warmup + 64
+    """The F16 decode of the headline at the other KV lengths of the Llama-3-8B config, each on a
+    model built as the headline's is: context length kv + steps + warmup + 64, cache pre-filled to
+    kv, decoding from that position."""
     model_bytes = TOKEN_WEIGHT_BYTES - 2 * DIM + 2 * VOCAB * DIM
-    ctx = A.Context(int(model_bytes + 2 * LAYERS * ctx_len * KV_DIM * 2 + (512 << 20)))
-    m = A.Model.create(ctx, A.ModelConfig(DIM, LAYERS, HEADS, KV_HEADS, FFN, VOCAB, ctx_len))
-    m.init_random(seed, 0.02, 0.0, 0.02)
-    m.fill_kv_random(max(kvs) + steps + warmup, seed=seed + 1)
     out = {"workload": "llama3-8b-shape f16 batch-1 greedy decode (graph), KV pre-filled N(0,1)"}
     for kv in kvs:
+        ctx_len = kv + steps + warmup + 64
+        ctx = A.Context(int(model_bytes + 2 * LAYERS * ctx_len * KV_DIM * 2 + (512 << 20)))
+        m = A.Model.create(ctx, A.ModelConfig(DIM, LAYERS, HEADS, KV_HEADS, FFN, VOCAB, ctx_len))
+        m.init_random(seed, 0.02, 0.0, 0.02)
+        m.fill_kv_random(kv, seed=seed + 1)
         m.decode_loop(1, kv, warmup)
         ctx.synchronize()
         t0 = time.perf_counter()
@@ -393,8 +394,8 @@ def kv_sweep_bench(A, seed: int, kvs=(512, 8192, 32768), steps: int = 64, warmup
         out[f"kv{kv}"] = {"tok_s": round(tok_s, 2), "ms_per_step": round(wall * 1e3 / steps, 4),
                           "bytes_per_token": int(step_bytes), "achieved_gbs": round(step_bytes * tok_s / 1e9, 1),
                           "frac": round(step_bytes * tok_s / 1e9 / HBM_PEAK_GBS, 4)}
-    m.close()
-    ctx.close()
+        m.close()
+        ctx.close()
     return out
 
 

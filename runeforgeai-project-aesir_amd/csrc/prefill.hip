@@ -243,7 +243,8 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(const h16 *__re
 }
 
 // Wide-tile kernel for M > 64 and K % 128 == 0: the whole 128-position chunk in one M tile,
-// NT = 64 or 32 columns per workgroup of 8 waves (4 x 2, each 32 x NT / 2), 128-wide K chunks
+// NT = 64 or 32 columns per workgroup of 8 waves (4 x 2, each 32 x NT / 2), or 48 columns (8 x 1,
+// each 16 x 48: 235 workgroups instead of 176 for an 11264-row gate/up), 128-wide K chunks
 // (four MFMA k-steps per chunk), 3 LDS stages of (128 + NT) 256-byte rows. Every copy
 // instruction moves 4 whole 256-byte row chunks (lane l: row l / 16, granule l % 16), granule p
 // of row r holding k-granule p ^ (r & 15), so the 16 rows of a fragment read hit distinct banks.
@@ -255,9 +256,14 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(const h16 *__re
 //   2560 x 2048 (QKV)       10.3 against 11.8    6144 x 4096  21.3 against 27.1
 //   2048 x 2048 (O)          9.5 against  9.6    4096 x 4096  15.3 against 19.3
 //   2048 x 5632 (down)      13.8 against 15.9    4096 x 14336 34.1 against 56.5
-// (hipBLASLt's pick for 11264 x 2048, MT64x128x128: 18.9.)
-constexpr int kWideMT = 128, kWideWM = 4, kWideWN = 2, kWideKC = 128, kWideS = 3;
-constexpr int kWideThreads = kWideWM * kWideWN * kWave;
+// (hipBLASLt's pick for 11264 x 2048, MT64x128x128: 18.9.) In the TinyLlama prefill the gate/up
+// launch takes 21.6 us with 64 columns (176 workgroups) and 20.2 with 48 (235); 48-column QKV
+// tiles (54 x 4 splits instead of 80 x 2) were slower with their reduce (12.9 against 12.5 us).
+constexpr int kWideMT = 128, kWideKC = 128, kWideS = 3;
+constexpr int kWideThreads = 8 * kWave;
+// waves along M and N of an NT-column tile
+__host__ __device__ constexpr int wide_wm(int nt) { return nt == 48 ? 8 : 4; }
+__host__ __device__ constexpr int wide_wn(int nt) { return nt == 48 ? 1 : 2; }
 constexpr int kWideRB = kWideKC * 2;  // bytes of one row chunk
 constexpr int kWideMaxSplits = 8;     // fused row kernels take up to 8 split partials
 constexpr int kWideWgTarget = 256;    // the split count doubles while tiles x splits stays within this
@@ -275,11 +281,14 @@ template <int EPI, int NT, bool Q8>
 __device__ __forceinline__ void gemm_wide_body(const h16 *__restrict__ A, int64_t M, int64_t K,
                                                const void *__restrict__ B, int64_t N, h16 *__restrict__ C,
                                                int64_t ldc, float *__restrict__ P, const h16 *__restrict__ Bs) {
+    constexpr int kWideWM = wide_wm(NT), kWideWN = wide_wn(NT);
     constexpr int kW = kWideWM * kWideWN;
+    static_assert(kW * kWave == kWideThreads, "8 waves");
     constexpr int kStage = wide_stage_bytes(NT, Q8);
-    // f16: (128 + NT) / 4 copies of four 256-byte rows, the same count for every wave
-    constexpr int kCopies = (kWideMT + NT) / 4 / kW;
-    static_assert(Q8 || kCopies * 4 * kW == kWideMT + NT, "whole copy instructions per wave");
+    // f16: (128 + NT) / 4 copies of four 256-byte rows; waves below kExtra issue one more than
+    // kCopies (NT = 48: 44 copies, 6 for waves 0-3 and 5 for waves 4-7)
+    constexpr int kCopies = (kWideMT + NT) / 4 / kW, kExtra = (kWideMT + NT) / 4 % kW;
+    static_assert((kWideMT + NT) % 4 == 0 && (!Q8 || kExtra == 0), "whole copy instructions");
     // Q8_0: 128 / 4 A copies (4 per wave), NT / 8 quant copies (waves 0 .. NT / 8 - 1) and NT / 32
     // scale copies (waves (NT / 8 + s) % 8)
     constexpr int kAq = kWideMT / 4 / kW, kQq = NT / 8, kSq = NT / 32;
@@ -301,12 +310,14 @@ __device__ __forceinline__ void gemm_wide_body(const h16 *__restrict__ A, int64_
         __builtin_amdgcn_make_buffer_rsrc((void *)Bs, 0, Q8 ? (int)(N * KB * 2) : 0, kBufferDword3);
     // f16 copy j of this wave: stage rows 4 (kCopies wave + j) .. + 3 (A rows first, then weights);
     // Q8_0: A copy j rows 4 (kAq wave + j) .. + 3
-    constexpr int kAC = Q8 ? kAq : kCopies;
+    constexpr int kAC = Q8 ? kAq : kCopies + (kExtra ? 1 : 0);
+    const int first = Q8 ? kAq * wave : kCopies * wave + (wave < kExtra ? wave : kExtra);  // first copy
+    const bool extra = kExtra && wave < kExtra;  // wave-uniform: issues copy kAC - 1 too
     int off[kAC], ldsrow[kAC];
     bool isa[kAC];
 #pragma unroll
     for (int j = 0; j < kAC; j++) {
-        const int row0 = 4 * (kAC * wave + j), row = row0 + (lane >> 4);
+        const int row0 = 4 * (first + j), row = row0 + (lane >> 4);
         isa[j] = row0 < kWideMT;
         ldsrow[j] = row0;
         const int64_t grow = isa[j] ? m0 + row : n0 + row - kWideMT;
@@ -324,7 +335,8 @@ __device__ __forceinline__ void gemm_wide_body(const h16 *__restrict__ A, int64_
         uint8_t *sa = lds + stage * kStage;
 #pragma unroll
         for (int j = 0; j < kAC; j++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(isa[j] ? ra : rb,
+            if (!kExtra || j < kCopies || extra)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(isa[j] ? ra : rb,
                                                      (__attribute__((address_space(3))) void *)(sa + ldsrow[j] * kWideRB),
                                                      16, off[j], (int)(c * kWideRB), 0, 0);
         if (Q8) {
@@ -341,7 +353,8 @@ __device__ __forceinline__ void gemm_wide_body(const h16 *__restrict__ A, int64_
     };
     // wait until only the copies of the next chunk are in flight (wave-uniform count)
     auto wait_chunk = [&]() {
-        if (!Q8 || ncopy == kAq) __builtin_amdgcn_s_waitcnt(vm_wait(kAC * (kWideS - 2)));
+        if (kExtra && !extra) __builtin_amdgcn_s_waitcnt(vm_wait(kCopies * (kWideS - 2)));
+        else if (!Q8 || ncopy == kAq) __builtin_amdgcn_s_waitcnt(vm_wait(kAC * (kWideS - 2)));
         else if (ncopy == kAq + 1) __builtin_amdgcn_s_waitcnt(vm_wait((kAq + 1) * (kWideS - 2)));
         else __builtin_amdgcn_s_waitcnt(vm_wait((kAq + 2) * (kWideS - 2)));
     };
@@ -432,6 +445,9 @@ AESIR_WIDE_KERNEL(1, 64, false, )
 AESIR_WIDE_KERNEL(1, 32, false, )
 AESIR_WIDE_KERNEL(2, 64, false, )
 AESIR_WIDE_KERNEL(2, 32, false, )
+AESIR_WIDE_KERNEL(0, 48, false, )
+AESIR_WIDE_KERNEL(1, 48, false, )
+AESIR_WIDE_KERNEL(2, 48, false, )
 AESIR_WIDE_KERNEL(0, 64, true, _q8)
 AESIR_WIDE_KERNEL(0, 32, true, _q8)
 AESIR_WIDE_KERNEL(1, 64, true, _q8)
@@ -448,6 +464,10 @@ static WideKernelFn wide_kernel() {
         if constexpr (EPI == kEpiStore) return NT == 64 ? gemm_wide_kernel_0_64_q8 : gemm_wide_kernel_0_32_q8;
         else if constexpr (EPI == kEpiResidual) return NT == 64 ? gemm_wide_kernel_1_64_q8 : gemm_wide_kernel_1_32_q8;
         else return NT == 64 ? gemm_wide_kernel_2_64_q8 : gemm_wide_kernel_2_32_q8;
+    } else if constexpr (NT == 48) {
+        if constexpr (EPI == kEpiStore) return gemm_wide_kernel_0_48;
+        else if constexpr (EPI == kEpiResidual) return gemm_wide_kernel_1_48;
+        else return gemm_wide_kernel_2_48;
     } else {
         if constexpr (EPI == kEpiStore) return NT == 64 ? gemm_wide_kernel_0_64 : gemm_wide_kernel_0_32;
         else if constexpr (EPI == kEpiResidual) return NT == 64 ? gemm_wide_kernel_1_64 : gemm_wide_kernel_1_32;
@@ -463,14 +483,25 @@ struct WidePlan {
     int nt;
     int64_t splits;
 };
-static WidePlan wide_plan(int64_t M, int64_t K, int64_t N) {
-    const int64_t lim = (int64_t)1 << 31;
-    if (M <= 64 || K % kWideKC != 0 || (M + kWideMT) * K * 2 >= lim || (N + 64) * K * 2 >= lim) return {0, 1};
-    const int nt = N >= 4096 ? 64 : 32;
+static WidePlan wide_plan_nt(int64_t M, int64_t K, int64_t N, int nt) {
     const int64_t tiles = ((N + nt - 1) / nt) * ((M + kWideMT - 1) / kWideMT), nkc = K / kWideKC;
     int64_t s = 1;
     while (2 * s <= kWideMaxSplits && tiles * 2 * s <= kWideWgTarget && nkc % (2 * s) == 0 && nkc / (2 * s) >= 4) s *= 2;
     return {nt, s};
+}
+static int64_t wide_workgroups(int64_t M, int64_t N, const WidePlan &p) {
+    return ((N + p.nt - 1) / p.nt) * ((M + kWideMT - 1) / kWideMT) * p.splits;
+}
+static WidePlan wide_plan(int64_t M, int64_t K, int64_t N, bool q8 = false) {
+    const int64_t lim = (int64_t)1 << 31;
+    if (M <= 64 || K % kWideKC != 0 || (M + kWideMT) * K * 2 >= lim || (N + 64) * K * 2 >= lim) return {0, 1};
+    const WidePlan p = wide_plan_nt(M, K, N, N >= 4096 ? 64 : 32);
+    if (q8 || p.nt != 64) return p;
+    // 48-column tiles (f16 weights) where 64-column ones leave part of the chip idle and 48 fill
+    // more of it in one pass
+    const WidePlan p48 = wide_plan_nt(M, K, N, 48);
+    const int64_t w64 = wide_workgroups(M, N, p), w48 = wide_workgroups(M, N, p48);
+    return w64 < kWideWgTarget && w48 > w64 && w48 <= kWideWgTarget ? p48 : p;
 }
 
 template <int EPI, int NT, bool Q8>
@@ -521,9 +552,11 @@ int64_t prefill_part_floats(int64_t rows, int64_t dim, int64_t qkv_n, int64_t ff
     int64_t most = 0;
     for (auto &kn : shapes) {
         if (kn[0] % 64 != 0) continue;
-        const WidePlan wp = wide_plan(rows, kn[0], kn[1]);
-        const int64_t sp = wp.nt ? wp.splits : gemm_splits(rows, kn[0], kn[1]);
-        if (sp > 1 && sp * rows * kn[1] > most) most = sp * rows * kn[1];
+        for (bool q8 : {false, true}) {
+            const WidePlan wp = wide_plan(rows, kn[0], kn[1], q8);
+            const int64_t sp = wp.nt ? wp.splits : gemm_splits(rows, kn[0], kn[1]);
+            if (sp > 1 && sp * rows * kn[1] > most) most = sp * rows * kn[1];
+        }
     }
     return most;
 }
@@ -538,10 +571,12 @@ static int32_t launch_mfma(hipStream_t s, const void *A, int64_t M, int64_t K, c
     const int64_t gx = (N + kGemmNT - 1) / kGemmNT, gy = (M + kGemmMT - 1) / kGemmMT;
     if (gx > 2147483647 || gy > 65535) return fail(AESIR_ERR_UNSUPPORTED, "%s: GEMM grid too large", name);
     if (EPI == kEpiSwiglu && (N & 1)) return fail(AESIR_ERR_INVALID, "%s: odd gate/up column count", name);
-    if (const WidePlan wp = wide_plan(M, K, N); wp.nt) {
+    if (const WidePlan wp = wide_plan(M, K, N, Bs != nullptr); wp.nt) {
         int64_t splits = wp.splits;
         while (splits > 1 && splits * M * N > part_floats) splits /= 2;
-        if (wp.nt == 64 && Bs)
+        if (wp.nt == 48)
+            AESIR_TRY((launch_wide<EPI, 48, false>(s, A, M, K, B, N, C, ldc, part, splits, nullptr)));
+        else if (wp.nt == 64 && Bs)
             AESIR_TRY((launch_wide<EPI, 64, true>(s, A, M, K, B, N, C, ldc, part, splits, Bs)));
         else if (Bs)
             AESIR_TRY((launch_wide<EPI, 32, true>(s, A, M, K, B, N, C, ldc, part, splits, Bs)));

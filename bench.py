@@ -371,31 +371,26 @@ def sampler_bench(A, seed: int, reps: int = 50) -> dict:
     return out
 
 
-def kv_sweep_bench(A, seed: int, kvs=(512, 8192, 32768), steps: int = 64, warmup: int = 8) -> dict:
-    """The F16 decode of the headline at the other KV lengths of the Llama-3-8B config, each on a
-    model built as the headline's is: context length kv + steps + warmup + 64, cache pre-filled to
-    kv, decoding from that position."""
-    model_bytes = TOKEN_WEIGHT_BYTES - 2 * DIM + 2 * VOCAB * DIM
-    out = {"workload": "llama3-8b-shape f16 batch-1 greedy decode (graph), KV pre-filled N(0,1)"}
+def kv_sweep_bench(seed: int, steps: int, warmup: int, kvs=(512, 8192, 32768)) -> dict:
+    """The F16 decode of the headline at the other KV lengths of the Llama-3-8B config, each
+    measured as the headline is: in a fresh process (a child started with this file's headline
+    options only: the same steps and warm-up), on a model whose context length is kv + steps + warmup + 64, the cache pre-filled
+    to kv, decoding from that position."""
+    import subprocess
+
+    out = {"workload": "llama3-8b-shape f16 batch-1 greedy decode (graph), KV pre-filled N(0,1); "
+                       "each length in its own process"}
     for kv in kvs:
-        ctx_len = kv + steps + warmup + 64
-        ctx = A.Context(int(model_bytes + 2 * LAYERS * ctx_len * KV_DIM * 2 + (512 << 20)))
-        m = A.Model.create(ctx, A.ModelConfig(DIM, LAYERS, HEADS, KV_HEADS, FFN, VOCAB, ctx_len))
-        m.init_random(seed, 0.02, 0.0, 0.02)
-        m.fill_kv_random(kv, seed=seed + 1)
-        m.decode_loop(1, kv, warmup)
-        ctx.synchronize()
-        t0 = time.perf_counter()
-        m.decode_loop(1, kv, steps)
-        ctx.synchronize()
-        wall = time.perf_counter() - t0
-        tok_s = steps / wall
-        step_bytes = TOKEN_WEIGHT_BYTES + KV_BYTES_PER_POS * (kv + (steps - 1) / 2.0 + 1) + KV_BYTES_PER_POS
-        out[f"kv{kv}"] = {"tok_s": round(tok_s, 2), "ms_per_step": round(wall * 1e3 / steps, 4),
-                          "bytes_per_token": int(step_bytes), "achieved_gbs": round(step_bytes * tok_s / 1e9, 1),
-                          "frac": round(step_bytes * tok_s / 1e9 / HBM_PEAK_GBS, 4)}
-        m.close()
-        ctx.close()
+        cmd = [sys.executable, os.path.abspath(__file__), "--kv", str(kv), "--steps", str(steps), "--warmup",
+               str(warmup), "--seed", str(seed), "--no-sweep", "--no-micro", "--no-prefill", "--no-q8",
+               "--no-quant", "--no-cpu-baseline"]
+        r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+        if r.returncode != 0:
+            raise RuntimeError(f"kv_sweep child for KV {kv} failed ({r.returncode}): {r.stderr[-2000:]}")
+        d = json.loads(r.stdout.strip().splitlines()[-1])
+        h = d["step_hbm"]
+        out[f"kv{kv}"] = {"tok_s": d["value"], "ms_per_step": d["ms_per_step"], "bytes_per_token": h["bytes_per_token"],
+                          "achieved_gbs": h["achieved_gbs"], "frac": h["frac"]}
     return out
 
 
@@ -575,7 +570,7 @@ def main():
     m.close()
     ctx.close()
     if not args.no_sweep:
-        out["kv_sweep"] = kv_sweep_bench(A, args.seed)
+        out["kv_sweep"] = kv_sweep_bench(args.seed, args.steps, args.warmup)
     if not args.no_micro:
         out["micro"] = micro_bench(A, args.seed)
     if not args.no_prefill:

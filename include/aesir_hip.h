@@ -199,10 +199,11 @@ int32_t aesir_gemm_q8_0(aesir_ctx *ctx, const void *A, int64_t a_rows, int64_t a
  * q) (the reference's K-quant gemms read synthetic block layouts that no GGUF file holds). Raises
  * "gemm_q4_0: matrix dimensions must be positive", "...: inner dimension must be a multiple of
  * 32" (256 for the K-quants), "...: output matrix shape mismatch". Takes free well space for the
- * duration of the call: with a_rows < 16, a_cols a multiple of 128 (at most 28672) and a type
- * with repacked planes (Q4_0, Q4_1, Q5_0, Q5_1, Q4_K, Q5_K, Q6_K) the blocks are repacked into the
- * library's tiled planes (about the size of the blocks) for the decode GEMV; otherwise an f16
- * copy of the weights (2 bytes per weight) for the F16 GEMM. */
+ * duration of the call: with a_rows < 16 and a_cols a multiple of 128 (at most 28672), or with
+ * a_rows > 64 and a_cols a multiple of 128, the blocks are repacked into the library's tiled
+ * planes (about the size of the blocks) for the decode GEMV per row or the matrix-core GEMM that
+ * dequantizes in registers; otherwise an f16 copy of the weights (2 bytes per weight) for the F16
+ * GEMM. */
 int32_t aesir_gemm_quant(aesir_ctx *ctx, const void *A, int64_t a_rows, int64_t a_cols, const void *blocks,
                          int32_t ggml_type, int64_t b_rows, void *C, int64_t c_rows, int64_t c_cols);
 /* Q8_0 block matvec with f32 activations and f32 output: y[n] = sum_k x[k] * d*q. Rows of

@@ -244,14 +244,16 @@ int32_t aesir_gemm_quant(aesir_ctx *ctx, const void *A, int64_t a_rows, int64_t 
         return fail(AESIR_ERR_SHAPE, "%s: inner dimension must be a multiple of %lld", nm, (long long)blk);
     if (c_rows != a_rows || c_cols != b_rows) return fail(AESIR_ERR_SHAPE, "%s: output matrix shape mismatch", nm);
     if (!A || !blocks || !C) return fail(AESIR_ERR_INVALID, "%s: null tensor pointer", nm);
-    // Fewer than 16 rows of A on whole 128-weight segments of a repacked type (Q4_0, Q4_K, Q6_K):
-    // the blocks are repacked into tiled records and each row runs the decode GEMV. Otherwise the
-    // blocks are dequantized to f16 (the same values) for the F16 GEMM, on the matrix cores from 2
-    // rows. Both take free well space for this call, released after enqueueing (later work on the
+    // Fewer than 16 rows of A on whole 128-weight segments of a repacked type: the blocks are
+    // repacked into the tiled planes and each row runs the decode GEMV; more than 64 rows on whole
+    // 128-weight segments: the same planes on the wide-tile matrix-core GEMM, which dequantizes
+    // them in registers. Otherwise the blocks are dequantized to f16 (the same values) for the F16
+    // GEMM, on the matrix cores from 2 rows. Both take free well space for this call, released after enqueueing (later work on the
     // stream runs after these kernels).
     const int64_t K = a_cols, N = b_rows, mark = ctx->well_offset;
     int32_t rc = AESIR_OK;
-    if (a_rows < 16 && qf_type(ggml_type) && qf_gemv_ok(K)) {
+    const bool wide = qf_type(ggml_type) && K % 128 == 0 && gemm_qf_wide_ok(a_rows, K, N);
+    if ((a_rows < 16 && qf_type(ggml_type) && qf_gemv_ok(K)) || wide) {
         QFMat w;
         w.type = ggml_type;
         void *planes[4] = {nullptr, nullptr, nullptr, nullptr};
@@ -264,7 +266,8 @@ int32_t aesir_gemm_quant(aesir_ctx *ctx, const void *A, int64_t a_rows, int64_t 
         w.s0 = planes[2];
         w.s1 = planes[3];
         if (rc == AESIR_OK) rc = launch_qf_repack(ctx->stream, ggml_type, blocks, N, K, w, 1);
-        for (int64_t r = 0; r < a_rows && rc == AESIR_OK; r++)
+        if (wide && rc == AESIR_OK) rc = launch_gemm_qf_mfma(ctx, A, a_rows, K, w, N, C);
+        for (int64_t r = 0; !wide && r < a_rows && rc == AESIR_OK; r++)
             rc = launch_qf_gemv_store(ctx->stream, w, N, K, (const uint16_t *)A + r * K, (uint16_t *)C + r * N);
     } else {
         void *wf = nullptr;

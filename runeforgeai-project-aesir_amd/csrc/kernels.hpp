@@ -123,6 +123,15 @@ constexpr int64_t kQfGemvMaxK = 28672;
 // The Q8_0 decode GEMV holds x in registers, 16 values per thread per 4096-wide slab, 7 slabs.
 constexpr int64_t kQ8GemvMaxK = 28672;
 bool qf_gemv_ok(int64_t K);
+// Batched-prefill GEMM on a repacked matrix (row0 0, K % 128 == 0): C = epilogue epi (store /
+// residual / SwiGLU, the GemmEpi values) of A [M][K] x W^T, nt = 64 or 32 columns per workgroup,
+// `splits` K splits writing f32 partials to `part` ([splits][M][N]) when above 1.
+int32_t launch_qf_gemm_wide(hipStream_t s, int epi, int nt, const void *A, int64_t M, int64_t K, const QFMat &w,
+                            int64_t N, void *C, int64_t ldc, float *part, int64_t splits);
+// Whether launch_gemm_qf_mfma takes an M x K by N x K product (more than 64 rows, K % 128 == 0,
+// 32-bit byte ranges), and that product stored as f16 C [M][N] (context stream and partials).
+bool gemm_qf_wide_ok(int64_t M, int64_t K, int64_t N);
+int32_t launch_gemm_qf_mfma(aesir_ctx *ctx, const void *A, int64_t M, int64_t K, const QFMat &w, int64_t N, void *C);
 // y[n] = f16(sum_k x[k] w[n, k]) for one row of x (the per-op GEMV of a repacked matrix).
 int32_t launch_qf_gemv_store(hipStream_t s, const QFMat &w, int64_t N, int64_t K, const void *x, void *y);
 // Decode-step GEMVs of repacked matrices with the fused epilogues (see the F16 launchers).

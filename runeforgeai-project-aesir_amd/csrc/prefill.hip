@@ -23,6 +23,7 @@
 #include "common.hpp"
 #include "device.hpp"
 #include "kernels.hpp"
+#include "mfma_gemm.hpp"
 #include "model.hpp"
 
 namespace aesir {
@@ -44,25 +45,6 @@ constexpr int kGemmNW = 16;   // output columns per wave
 constexpr int kGemmNT = kGemmWaves * kGemmNW;
 constexpr int kGemmThreads = kGemmWaves * kWave;
 
-enum GemmEpi : int { kEpiStore = 0, kEpiResidual = 1, kEpiSwiglu = 2 };
-
-// Third dword of a raw buffer resource (V#) on gfx9-family GPUs, gfx950 included.
-constexpr int kBufferDword3 = 0x00020000;
-
-
-// Applies the epilogue to output (m, n) with f32 value v; `partner` is the value of column n ^ 1
-// in the same row (used by kEpiSwiglu: 2i gate, 2i + 1 up -> C[m][i] = f16(up * silu(gate))).
-// kEpiStore: C[m][n] = f16(v); kEpiResidual: C[m][n] = f16(f16(v) + C[m][n]).
-template <int EPI>
-__device__ __forceinline__ void gemm_epilogue(h16 *C, int64_t ldc, int64_t M, int64_t N, int64_t m, int64_t n, float v,
-                                              float partner) {
-    if (EPI == kEpiSwiglu) {
-        if ((n & 1) == 0 && m < M && n + 1 < N) C[m * ldc + n / 2] = hmul((h16)partner, silu_h((h16)v));
-    } else if (m < M && n < N) {
-        h16 *c = C + m * ldc + n;
-        *c = EPI == kEpiResidual ? hadd((h16)v, *c) : (h16)v;
-    }
-}
 
 constexpr int kGemmKC = 64;  // k per chunk (two MFMA k-steps)
 
@@ -91,9 +73,6 @@ constexpr int kDmaStagesQ = 2;  // Q8_0 weights: 2 stages 1.94-1.97 ms, 3 stages
 __device__ __forceinline__ int dma_swz(int row) { return (row >> 1) & 7; }
 __device__ __forceinline__ int dma_swz_q(int row) { return (row >> 2) & 3; }  // 4 granules per quant row
 
-// s_waitcnt immediate that waits until at most n vector-memory operations are outstanding
-// (gfx9 encoding: vmcnt bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima).
-constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
 // Q8: B is Q8_0 (int8 quants [N][K] + f16 block scales Bs [N][K / 32]). A chunk's 64 weight rows
 // are 64-byte quant segments (one copy per wave: 16 rows x 4 granules, granule p of row r holding
@@ -259,8 +238,6 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(const h16 *__re
 // (hipBLASLt's pick for 11264 x 2048, MT64x128x128: 18.9.) In the TinyLlama prefill the gate/up
 // launch takes 21.6 us with 64 columns (176 workgroups) and 20.2 with 48 (235); 48-column QKV
 // tiles (54 x 4 splits instead of 80 x 2) were slower with their reduce (12.9 against 12.5 us).
-constexpr int kWideMT = 128, kWideKC = 128, kWideS = 3;
-constexpr int kWideThreads = 8 * kWave;
 // waves along M and N of an NT-column tile
 __host__ __device__ constexpr int wide_wm(int nt) { return nt == 48 ? 8 : 4; }
 __host__ __device__ constexpr int wide_wn(int nt) { return nt == 48 ? 1 : 2; }
@@ -609,6 +586,50 @@ static int32_t launch_mfma(hipStream_t s, const void *A, int64_t M, int64_t K, c
         const int64_t blocks = (M * N + 255) / 256;
         hipLaunchKernelGGL(gemm_reduce_kernel<EPI>, dim3((unsigned)blocks), dim3(256), 0, s, (const float *)part, splits,
                            M, N, (h16 *)C, ldc);
+        AESIR_LAUNCH_CHECK("gemm_reduce_kernel");
+    }
+    return AESIR_OK;
+}
+
+// A GEMM of the prefill on the model's matrix w (rows N, K wide): repacked types on the wide-tile
+// kernel that dequantizes in registers (launch_qf_gemm_wide) where the wide tile applies, else
+// through an f16 copy in m->pf_wdeq; F16 and Q8_0 weights on launch_mfma. `defer` and *splits_out
+// as launch_mfma's.
+template <int EPI>
+static int32_t prefill_gemm(aesir_model *m, hipStream_t s, const WMat &w, const void *A, int64_t M, int64_t K, int64_t N,
+                            void *C, int64_t ldc, const char *name, bool defer = false, int64_t *splits_out = nullptr) {
+    if (!qf_type(w.type))
+        return launch_mfma<EPI>(s, A, M, K, w.w, N, C, ldc, m->pf_part, m->pf_part_floats, name, defer, splits_out,
+                                w.type == AESIR_GGML_Q8_0 ? w.s0 : nullptr);
+    // the 48-column tile is f16-only: plan as for Q8_0 weights (64 or 32 columns)
+    if (const WidePlan wp = wide_plan(M, K, N, true); wp.nt) {
+        int64_t splits = wp.splits;
+        while (splits > 1 && splits * M * N > m->pf_part_floats) splits /= 2;
+        AESIR_TRY(launch_qf_gemm_wide(s, EPI, wp.nt, A, M, K, wmat_qf(w), N, C, ldc, m->pf_part, splits));
+        if (splits_out) *splits_out = splits;
+        if (splits > 1 && !defer) {
+            const int64_t blocks = (M * N + 255) / 256;
+            hipLaunchKernelGGL(gemm_reduce_kernel<EPI>, dim3((unsigned)blocks), dim3(256), 0, s, (const float *)m->pf_part,
+                               splits, M, N, (h16 *)C, ldc);
+            AESIR_LAUNCH_CHECK("gemm_reduce_kernel");
+        }
+        return AESIR_OK;
+    }
+    AESIR_TRY(launch_qf_dequant(s, wmat_qf(w), N, K, 1, nullptr, m->pf_wdeq, K));
+    return launch_mfma<EPI>(s, A, M, K, m->pf_wdeq, N, C, ldc, m->pf_part, m->pf_part_floats, name, defer, splits_out);
+}
+
+bool gemm_qf_wide_ok(int64_t M, int64_t K, int64_t N) { return wide_plan(M, K, N, true).nt != 0; }
+
+int32_t launch_gemm_qf_mfma(aesir_ctx *ctx, const void *A, int64_t M, int64_t K, const QFMat &w, int64_t N, void *C) {
+    const WidePlan wp = wide_plan(M, K, N, true);
+    if (!wp.nt) return fail(AESIR_ERR_UNSUPPORTED, "gemm_qf_wide: shape not on the wide tile");
+    int64_t splits = wp.splits;
+    while (splits > 1 && splits * M * N > ctx->scratch.attn_part_floats) splits /= 2;
+    AESIR_TRY(launch_qf_gemm_wide(ctx->stream, kEpiStore, wp.nt, A, M, K, w, N, C, N, ctx->scratch.attn_part, splits));
+    if (splits > 1) {
+        hipLaunchKernelGGL(gemm_reduce_kernel<kEpiStore>, dim3((unsigned)((M * N + 255) / 256)), dim3(256), 0,
+                           ctx->stream, (const float *)ctx->scratch.attn_part, splits, M, N, (h16 *)C, N);
         AESIR_LAUNCH_CHECK("gemm_reduce_kernel");
     }
     return AESIR_OK;
@@ -1029,20 +1050,6 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
     const bool mfma = prefill_mfma_ok(m);
     if (!mfma && !m->all_f16)
         return fail(AESIR_ERR_UNSUPPORTED, "prefill: quantized weights need the MFMA GEMM shapes (K %% 64 == 0)");
-    // 4-bit types: each GEMM reads an f16 copy of its matrix, dequantized just before it (the
-    // prefill is not bound by weight bytes at 128 rows; the decode GEMVs read the records)
-    struct W {
-        const void *w, *s;
-    };
-    auto wmat = [&](const WMat &w, int64_t rows, int64_t K, W *out) -> int32_t {
-        if (!qf_type(w.type)) {
-            *out = W{w.w, w.type == AESIR_GGML_Q8_0 ? w.s0 : nullptr};
-            return AESIR_OK;
-        }
-        AESIR_TRY(launch_qf_dequant(s, wmat_qf(w), rows, K, 1, nullptr, m->pf_wdeq, K));
-        *out = W{m->pf_wdeq, nullptr};
-        return AESIR_OK;
-    };
     const bool rowvec = d % kRowVec == 0;  // fused residual + norm rows need whole 8-column groups
     bool xn_ready = false;                 // Xn already holds this layer's attention-norm rows
     auto norm_rows = [&](const void *w) -> int32_t {
@@ -1052,11 +1059,9 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
         return AESIR_OK;
     };
     // residual GEMM into X, then X -> Xn normalized with `next_norm` (if any), fused when split
-    auto residual_gemm = [&](const h16 *in, int64_t K, const void *w, const void *ws, const void *next_norm,
-                             const char *name) -> int32_t {
+    auto residual_gemm = [&](const h16 *in, int64_t K, const WMat &w, const void *next_norm, const char *name) -> int32_t {
         int64_t splits = 1;
-        AESIR_TRY(launch_mfma<kEpiResidual>(s, in, n, K, w, d, X, d, m->pf_part, m->pf_part_floats, name,
-                                            next_norm && rowvec, &splits, ws));
+        AESIR_TRY(prefill_gemm<kEpiResidual>(m, s, w, in, n, K, d, X, d, name, next_norm && rowvec, &splits));
         if (!next_norm) return AESIR_OK;
         if (splits > 1 && rowvec) {
 #define AESIR_RRN(SV)                                                                                           \
@@ -1085,11 +1090,8 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
         if (!xn_ready) AESIR_TRY(norm_rows(L.attn_norm));
         xn_ready = false;
         int64_t qkv_splits = 1;
-        W wq;
-        AESIR_TRY(wmat(L.qkv, qkv_n, d, &wq));
         if (mfma)
-            AESIR_TRY(launch_mfma<kEpiStore>(s, Xn, n, d, wq.w, qkv_n, QKV, qkv_n, m->pf_part, m->pf_part_floats,
-                                             "gemm_mfma_qkv", true, &qkv_splits, wq.s));
+            AESIR_TRY(prefill_gemm<kEpiStore>(m, s, L.qkv, Xn, n, d, qkv_n, QKV, qkv_n, "gemm_mfma_qkv", true, &qkv_splits));
         else
             AESIR_TRY(launch_gemm_f16(m->ctx, Xn, n, d, L.qkv.w, qkv_n, QKV));
         if (qkv_splits > 1) {
@@ -1134,9 +1136,7 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
         AESIR_LAUNCH_CHECK("prefill_attention_kernel");
         // O projection + residual, then the feed-forward norm (inference.mojo:227-241)
         if (mfma) {
-            W wo;
-            AESIR_TRY(wmat(L.o, d, d, &wo));
-            AESIR_TRY(residual_gemm(ATT, d, wo.w, wo.s, L.ffn_norm, "gemm_mfma_o_residual"));
+            AESIR_TRY(residual_gemm(ATT, d, L.o, L.ffn_norm, "gemm_mfma_o_residual"));
         } else {
             AESIR_TRY(launch_gemm_f16(m->ctx, ATT, n, d, L.o.w, d, Xn));
             AESIR_TRY(launch_residual_add(s, X, Xn, n * d));
@@ -1145,13 +1145,9 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
         // feed-forward block (inference.mojo:235-273); the down projection's tail also produces
         // the next layer's attention-norm rows
         if (mfma) {
-            W wgu, wdn;
-            AESIR_TRY(wmat(L.gu, 2 * f, d, &wgu));
-            AESIR_TRY(launch_mfma<kEpiSwiglu>(s, Xn, n, d, wgu.w, 2 * f, ACT, f, m->pf_part, m->pf_part_floats,
-                                                "gemm_mfma_gate_up_swiglu", false, nullptr, wgu.s));
+            AESIR_TRY(prefill_gemm<kEpiSwiglu>(m, s, L.gu, Xn, n, d, 2 * f, ACT, f, "gemm_mfma_gate_up_swiglu"));
             const void *next_norm = l + 1 < c.n_layers ? m->layers[l + 1].attn_norm : nullptr;
-            AESIR_TRY(wmat(L.down, d, f, &wdn));
-            AESIR_TRY(residual_gemm(ACT, f, wdn.w, wdn.s, next_norm, "gemm_mfma_down_residual"));
+            AESIR_TRY(residual_gemm(ACT, f, L.down, next_norm, "gemm_mfma_down_residual"));
             xn_ready = next_norm != nullptr;
         } else {
             // interleaved gate/up rows -> [n][2f] products, then the SwiGLU over the pairs

@@ -34,6 +34,7 @@
 #include "device.hpp"
 #include "gemv_common.hpp"
 #include "kernels.hpp"
+#include "mfma_gemm.hpp"
 
 namespace aesir {
 
@@ -1265,6 +1266,205 @@ int32_t launch_qf_qkv_rope_kv(hipStream_t s, const QkvArgs &a, const EpiQkv &e) 
 int32_t launch_qf_lm_head(hipStream_t s, const LmHeadArgs &a, const EpiLmHead &e) {
     return gemv_qf_dispatch<true>(s, a.wq, a.vocab, a.dim, QFXSrc{(const h16 *)a.x, QFMat{}, nullptr, nullptr},
                                   a.norm_w, a.eps, e, "gemv_qf_lm_head");
+}
+
+// ------------------------------------------------------------------ batched-prefill GEMM
+
+// C = epilogue(A W^T) for a chunk of up to 128 activation rows and a matrix in the tiled planes,
+// on v_mfma_f32_16x16x32_f16 without an f16 copy of the weights. Grid (N / NT, ceil(M / 128),
+// K splits); 8 waves as 4 x 2, each 32 rows x NT / 2 columns. Per 128-wide K chunk (one tile
+// column of the planes) the 128 activation rows (256-byte row chunks, granule p of row r holding
+// k-granule p ^ (r & 15)) and the NT / 16 weight tiles' plane bytes (nibbles 1 KiB, s0, hb and the
+// tile rows' s1 entries, each a contiguous run copied as laid out in memory) go straight into
+// an LDS stage by buffer loads with the LDS destination; 3 stages, two chunks in flight, explicit
+// wait counts per wave. A wave turns its tiles into MFMA operands with qf_tile_a (the decode
+// GEMV's dequantization, so the weights are the same f16 values) and its activation rows into
+// the matching k order with qf_perm_rec. Split z writes f32 partials like the f16 kernels.
+constexpr int kQgA = kWideMT * kWideKC * 2;  // activation bytes per stage
+constexpr int kQgTile = 2048;                // LDS bytes per weight tile: nib 1024, s0 256, hb 512, s1 256
+__host__ __device__ constexpr int qg_stage_bytes(int nt) { return kQgA + nt / 16 * kQgTile; }
+template <int T>
+constexpr bool qg_has_s1() {
+    return qf_kq<T>() || T == AESIR_GGML_Q2_K || T == AESIR_GGML_Q3_K || T == AESIR_GGML_Q6_K;
+}
+template <int T>
+constexpr int qg_hb_copies() {
+    return T == AESIR_GGML_Q6_K ? 2 : qf_hb5<T>() ? 1 : 0;
+}
+template <int T>
+constexpr int qg_tile_copies() {
+    return 2 + qg_hb_copies<T>() + (qg_has_s1<T>() ? 1 : 0);
+}
+
+template <int EPI, int NT, int T>
+__global__ __launch_bounds__(kWideThreads) void gemm_wide_qf_kernel(const h16 *__restrict__ A, int64_t M, int64_t K,
+                                                                   QFMat w, int64_t N, h16 *__restrict__ C,
+                                                                   int64_t ldc, float *__restrict__ P) {
+    constexpr int NTT = NT / 16;                         // weight tiles per workgroup
+    constexpr int NCP = qg_tile_copies<T>(), NB = NTT * NCP;  // copies per tile and per chunk
+    constexpr int NBW = (NB + 7) / 8, NBX = NB % 8;      // per wave: NBW copies below wave NBX, else NB / 8
+    constexpr int kStage = qg_stage_bytes(NT);
+    constexpr int MF = 2, NF = NT / 32;
+    constexpr bool dm = qf_dm<T>();
+    constexpr int s0b = dm ? 4 : 2;                      // s0 bytes per lane
+    constexpr int es1 = (qf_kq<T>() || T == AESIR_GGML_Q2_K) ? 4 : 2;
+    static_assert(NT == 32 || NT == 64, "tile width");
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / 2, wn = wave % 2;
+    const int64_t m0 = (int64_t)blockIdx.y * kWideMT, n0 = (int64_t)blockIdx.x * NT;
+    const int r = lane & 15, g = lane >> 4;
+    const int nseg = (int)(K / kSeg), sbr = (int)(K / 256), pb0 = (int)(n0 / 16);
+    const int64_t splits = gridDim.z, z = blockIdx.z;
+    const int64_t c0 = nseg * z / splits, c1 = nseg * (z + 1) / splits;
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void *)A, 0, (int)(M * K * 2), kBufferDword3);
+    const QfRsrc rs = qf_rsrc(w, T, qf_rows_alloc(N), K);
+    // activation copy j of this wave: rows 16 wave + 4 j .. + 3, lane l row + l / 16, granule l % 16
+    int aoff[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int row = 16 * wave + 4 * j + (lane >> 4);
+        aoff[j] = (int)((m0 + row) * K * 2) + (((lane & 15) ^ (row & 15)) << 4);
+    }
+    const int nbw = NBX == 0 || wave < NBX ? NBW : NBW - 1;  // this wave's weight copies per chunk
+    auto issue = [&](int64_t c, int stage) {
+        c = c < c1 ? c : c1 - 1;  // past the split's end: re-read its last chunk into a free stage
+        uint8_t *sa = lds + stage * kStage;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                ra, (__attribute__((address_space(3))) void *)(sa + (16 * wave + 4 * j) * (kWideKC * 2)), 16, aoff[j],
+                (int)(c * kWideKC * 2), 0, 0);
+        uint8_t *sb = sa + kQgA;
+#pragma unroll
+        for (int jb = 0; jb < NBW; jb++) {
+            const int b = wave + 8 * jb;  // wave-uniform
+            if (b >= NB) break;
+            const int tb = b / NCP, kind = b % NCP, pb = pb0 + tb, pt = pb * nseg + (int)c;
+            uint8_t *dst = sb + tb * kQgTile;
+            if (kind == 0) {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs.nib, (__attribute__((address_space(3))) void *)dst, 16,
+                                                         lane * 16, pt * 1024, 0, 0);
+            } else if (kind == 1) {  // 256 bytes from the tile's s0 (128 of them used with 2 bytes per lane)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs.s0, (__attribute__((address_space(3))) void *)(dst + 1024),
+                                                         4, lane * 4, pt * 64 * s0b, 0, 0);
+            } else if (kind < 2 + qg_hb_copies<T>()) {
+                const int h = kind - 2;  // Q6_K: two 256-byte halves of the tile's 512
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rs.hb, (__attribute__((address_space(3))) void *)(dst + 1280 + 256 * h), 4, lane * 4,
+                    pt * 256 * qg_hb_copies<T>() + 256 * h, 0, 0);
+            } else {  // the row block's s1 entries of the chunk's super-block (and what follows)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs.s1, (__attribute__((address_space(3))) void *)(dst + 1792), 4,
+                                                         lane * 4, (pb * sbr + (int)(c / 2)) * 16 * es1, 0, 0);
+            }
+        }
+    };
+    // wait until only the next chunk's copies are in flight (wave-uniform count)
+    auto wait_chunk = [&]() {
+        if (nbw == NBW) __builtin_amdgcn_s_waitcnt(vm_wait((4 + NBW) * (kWideS - 2)));
+        else __builtin_amdgcn_s_waitcnt(vm_wait((4 + NBW - 1) * (kWideS - 2)));
+    };
+    const QfRegs kr = QfRegs::make();
+    f32x4 acc[MF][NF];
+#pragma unroll
+    for (int i = 0; i < MF; i++)
+#pragma unroll
+        for (int f = 0; f < NF; f++) acc[i][f] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < kWideS - 1; j++) issue(c0 + j, j);
+    for (int64_t c = c0; c < c1; c++) {
+        const int t = (int)((c - c0) % kWideS);
+        wait_chunk();                                      // this wave's copies of chunk c ...
+        __builtin_amdgcn_s_barrier();                      // ... and every wave's
+        issue(c + kWideS - 1, (t + kWideS - 1) % kWideS);  // into the stage chunk c - 1 used
+        const uint8_t *sa = lds + t * kStage, *sb = sa + kQgA;
+        u32x4 ao[MF][4], bo[NF][4];
+#pragma unroll
+        for (int i = 0; i < MF; i++) {
+            const int row = 32 * wm + 16 * i + r;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {  // record 2 g + h of the row's chunk: k-granules 4 g + 2 h, + 1
+                const u32x4 x[2] = {ld16(sa + row * (kWideKC * 2) + (((4 * g + 2 * h) ^ (row & 15)) << 4)),
+                                    ld16(sa + row * (kWideKC * 2) + (((4 * g + 2 * h + 1) ^ (row & 15)) << 4))};
+                u32x4 o[2];
+                qf_perm_rec(x, o);
+                ao[i][2 * h] = o[0];
+                ao[i][2 * h + 1] = o[1];
+            }
+        }
+#pragma unroll
+        for (int f = 0; f < NF; f++) {
+            const uint8_t *tp = sb + (wn * NF + f) * kQgTile;
+            QTile<T> q;
+            q.nib = ld16(tp + lane * 16);
+            if constexpr (dm) q.s0 = *reinterpret_cast<const unsigned *>(tp + 1024 + lane * 4);
+            else q.s0 = *reinterpret_cast<const uint16_t *>(tp + 1024 + lane * 2);
+            if constexpr (qf_hb5<T>()) q.hb = *reinterpret_cast<const unsigned *>(tp + 1280 + lane * 4);
+            if constexpr (T == AESIR_GGML_Q6_K) q.hb = *reinterpret_cast<const u32x2 *>(tp + 1280 + lane * 8);
+            if constexpr (es1 == 4 && qg_has_s1<T>()) q.s1 = *reinterpret_cast<const unsigned *>(tp + 1792 + r * 4);
+            if constexpr (es1 == 2 && qg_has_s1<T>()) q.s1 = *reinterpret_cast<const uint16_t *>(tp + 1792 + r * 2);
+            qf_tile_a<T>(q, kr, bo[f]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int i = 0; i < MF; i++)
+#pragma unroll
+                for (int f = 0; f < NF; f++) acc[i][f] = mfma16x16x32(ao[i][j], bo[f][j], acc[i][f]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    __builtin_amdgcn_s_waitcnt(vm_wait(0));  // no copy may land in LDS after the workgroup ends
+#pragma unroll
+    for (int i = 0; i < MF; i++)
+#pragma unroll
+        for (int f = 0; f < NF; f++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int64_t m = m0 + 32 * wm + 16 * i + 4 * g + e;
+                const int64_t n = n0 + wn * (NT / 2) + 16 * f + r;
+                const float v = acc[i][f][e];
+                if (splits == 1) {
+                    const float partner = dpp_f<kDppXor1>(v);  // lane r ^ 1 holds column n ^ 1
+                    gemm_epilogue<EPI>(C, ldc, M, N, m, n, v, partner);
+                } else if (m < M && n < N) {
+                    P[(z * M + m) * N + n] = v;
+                }
+            }
+}
+
+template <int EPI, int NT, int T>
+static int32_t launch_qf_wide(hipStream_t s, const void *A, int64_t M, int64_t K, const QFMat &w, int64_t N, void *C,
+                              int64_t ldc, float *part, int64_t splits) {
+    static std::atomic<uint64_t> lds_set{0};
+    constexpr int lds = kWideS * qg_stage_bytes(NT);
+    AESIR_TRY(raise_lds_limit(reinterpret_cast<const void *>(gemm_wide_qf_kernel<EPI, NT, T>), lds, lds_set));
+    const dim3 grid((unsigned)((N + NT - 1) / NT), (unsigned)((M + kWideMT - 1) / kWideMT), (unsigned)splits);
+    hipLaunchKernelGGL((gemm_wide_qf_kernel<EPI, NT, T>), grid, dim3(kWideThreads), lds, s, (const h16 *)A, M, K, w, N,
+                       (h16 *)C, ldc, part);
+    return AESIR_OK;
+}
+
+int32_t launch_qf_gemm_wide(hipStream_t s, int epi, int nt, const void *A, int64_t M, int64_t K, const QFMat &w,
+                            int64_t N, void *C, int64_t ldc, float *part, int64_t splits) {
+    if (!qf_type(w.type) || w.row0 != 0 || K % kSeg != 0 || (nt != 32 && nt != 64) || splits < 1 || M < 1 || N < 1 ||
+        (epi == kEpiSwiglu && (N & 1)) || (splits > 1 && !part))
+        return fail(AESIR_ERR_INVALID, "gemm_qf_wide: unsupported arguments");
+    const int64_t lim = (int64_t)1 << 31;
+    if ((M + kWideMT) * K * 2 >= lim || qf_rows_alloc(N) * K >= lim)
+        return fail(AESIR_ERR_UNSUPPORTED, "gemm_qf_wide: operand exceeds a 32-bit byte range");
+    int32_t rc = AESIR_OK;
+    qf_switch(w.type, [&](auto t) {
+        constexpr int T = decltype(t)::value;
+#define AESIR_QG(E, NTV) rc = launch_qf_wide<E, NTV, T>(s, A, M, K, w, N, C, ldc, part, splits)
+        if (epi == kEpiStore) { if (nt == 64) AESIR_QG(kEpiStore, 64); else AESIR_QG(kEpiStore, 32); }
+        else if (epi == kEpiResidual) { if (nt == 64) AESIR_QG(kEpiResidual, 64); else AESIR_QG(kEpiResidual, 32); }
+        else { if (nt == 64) AESIR_QG(kEpiSwiglu, 64); else AESIR_QG(kEpiSwiglu, 32); }
+#undef AESIR_QG
+    });
+    AESIR_TRY(rc);
+    AESIR_LAUNCH_CHECK("gemm_wide_qf_kernel");
+    return AESIR_OK;
 }
 
 }  // namespace aesir

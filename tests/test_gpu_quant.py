@@ -61,8 +61,12 @@ def lib_weights(oracle, kind, t):
 
 @pytest.mark.parametrize("kind", list(TYPES))
 @pytest.mark.parametrize("M,K,N", [(1, 4096, 64), (1, 14336, 40), (3, 2048, 100), (1, 5632, 33), (1, 28672, 8),
-                                   (20, 4096, 48), (1, 512, 16400), (2, 1536, 18000)])
+                                   (20, 4096, 48), (1, 512, 16400), (2, 1536, 18000), (128, 2048, 96),
+                                   (100, 4096, 200), (128, 1024, 5000)])
 def test_gemm_quant_vs_oracle(A, ctx, oracle, kind, M, K, N):
+    """M < 16: the decode GEMV per row on the repacked planes; M > 64: the wide-tile matrix-core
+    GEMM on the same planes (K splits with a reduce, M and N tails, 64- and 32-column tiles);
+    otherwise the F16 GEMM on dequantized weights."""
     t = random_tensor(A, kind, N, K, RNG)
     x = RNG.standard_normal((M, K)).astype(np.float16)
     c = ctx.tensor(M, N)

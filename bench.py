@@ -141,7 +141,7 @@ def prefill_bench(A, seed: int, n_prompt: int = 128, n_decode: int = 256, reps: 
     """Batched prefill of n_prompt positions on the TinyLlama shape (MFMA GEMMs; wall time of the
     blocking aesir_prefill call, host launches included), then n_decode graph-replayed greedy steps.
     wtype q8_0: Q8_0 matrices (weights for the GEMMs dequantized per fragment); a repacked type
-    (q4_0, q4_k, ...): each layer matrix dequantized to f16 before its GEMM."""
+    (q4_0, q4_k, ...): the tiled planes, dequantized in registers by the wide-tile GEMM."""
     ctx = A.Context(TL_WEIGHT_BYTES + (1 << 30))
     types = {"f16": A.GGML_F16, "q8_0": A.GGML_Q8_0, **QF_TYPES}
     m = A.Model.create(ctx, A.ModelConfig(TL["dim"], TL["layers"], TL["heads"], TL["kv_heads"], TL["ffn"],
@@ -582,6 +582,9 @@ def main():
     if not args.no_quant:
         out["quant"] = {k: quant_bench(A, k, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters, use_graph)
                         for k in QUANT_KINDS}
+        for k in ("q4_0", "q4_k"):  # the TinyLlama prefill with these weights (matrix-core GEMM on the planes)
+            if k in out["quant"]:
+                out["quant"][k]["prefill"] = prefill_bench(A, args.seed, n_decode=64, wtype=k)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.kv, args.cpu_reps)
         out["cpu_baseline"]["value"] = round(out["cpu_baseline"]["value"], 4)

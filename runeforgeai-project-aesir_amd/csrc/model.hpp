@@ -96,7 +96,7 @@ struct aesir_model {
     bool all_f16 = true;       // every matrix stored as f16
     aesir::WMat embd, out;     // token_embd [vocab][dim], output [vocab][dim]
     void *out_norm = nullptr;
-    void *pf_wdeq = nullptr;  // 4-bit types: f16 copy of the matrix a prefill GEMM is reading
+    void *pf_wdeq = nullptr;  // repacked types: f16 copy of the matrix a short-chunk prefill GEMM reads
     std::vector<aesir::ModelLayer> layers;
     void *k_cache = nullptr, *v_cache = nullptr;  // [n_layers][ctx_len][kvd]
     void *x = nullptr, *q = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr;

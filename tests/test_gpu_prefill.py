@@ -166,6 +166,24 @@ def test_prefill_tinyllama_shape_mfma(A, ctx, oracle):
     m.close()
 
 
+def test_prefill_48_column_tiles(A, ctx, oracle):
+    """dim 4096 (32 / 8 heads, head_dim 128) with ffn 1024: the QKV GEMM (6144 columns, 2 K splits
+    into the fused QKV tail) and the down GEMM (residual epilogue, 2 K splits into the fused norm
+    tail) take 48-column tiles, which fill more of the chip than 64-column ones; 100 prompt
+    positions and 3 greedy steps against the per-position oracle."""
+    cfg = oracle.Config(dim=4096, n_layers=1, n_heads=32, n_kv_heads=8, ffn=1024, vocab=512, ctx_len=128)
+    w = oracle.synthetic_weights(cfg, 31)
+    om = oracle.Model(cfg, w)
+    prompt = oracle.prompt_tokens(100, cfg.vocab, 6)
+    first, ologits, follow = oracle_prefill(om, prompt, 3)
+    m = gpu_model(A, ctx, cfg, w)
+    got = m.prefill(prompt)
+    assert within_tol(m.logits(), ologits)
+    assert got == first
+    assert gpu_follow(m, prompt, got, 3) == follow
+    m.close()
+
+
 @pytest.mark.parametrize("dim,heads,kv,n_prompt,split", [(512, 8, 1, 300, 0), (512, 4, 1, 150, 0),
                                                         (1024, 8, 1, 140, 70)])
 def test_prefill_grouped_attention_tiles(A, ctx, oracle, dim, heads, kv, n_prompt, split):

@@ -775,7 +775,8 @@ class Model:
 
     def prefill(self, tokens, start_pos: int = 0) -> int:
         """Batched prefill of tokens at positions start_pos..: the same KV cache and next token as
-        forward_pass at each position in turn (aesir.mojo:358-374), one pass per 128-row chunk."""
+        forward_pass at each position in turn (aesir.mojo:358-374), one pass per chunk of up to 512
+        rows."""
         t = np.ascontiguousarray(np.array(tokens, dtype=np.int64))
         nxt = I64()
         _check(_L.aesir_prefill(self.h, t.ctypes.data, len(t), start_pos, C.byref(nxt)))

@@ -138,7 +138,8 @@ int32_t launch_embed_rows(hipStream_t s, const WMat &e, int64_t dim, const int64
 // Batched prefill of tokens[0..n) at positions start_pos.., in chunks of pf_rows rows; *next is the
 // greedy token after the last position.
 int32_t model_prefill(aesir_model *m, const int64_t *tokens, int64_t n, int64_t start_pos, int64_t *next);
-// f32 split-K partial floats the prefill GEMMs of a model with these shapes need at `rows` rows.
+// f32 split-K partial floats the prefill GEMMs of a model with these shapes need for chunks of up
+// to `rows` rows.
 int64_t prefill_part_floats(int64_t rows, int64_t dim, int64_t qkv_n, int64_t ffn);
 // Decode-step helpers shared with the prefill.
 int32_t ensure_rope(aesir_model *m, int64_t max_pos);

@@ -527,14 +527,16 @@ static int64_t gemm_splits(int64_t M, int64_t K, int64_t N) {
 int64_t prefill_part_floats(int64_t rows, int64_t dim, int64_t qkv_n, int64_t ffn) {
     const int64_t shapes[4][2] = {{dim, qkv_n}, {dim, dim}, {dim, 2 * ffn}, {ffn, dim}};  // (K, N)
     int64_t most = 0;
-    for (auto &kn : shapes) {
-        if (kn[0] % 64 != 0) continue;
-        for (bool q8 : {false, true}) {
-            const WidePlan wp = wide_plan(rows, kn[0], kn[1], q8);
-            const int64_t sp = wp.nt ? wp.splits : gemm_splits(rows, kn[0], kn[1]);
-            if (sp > 1 && sp * rows * kn[1] > most) most = sp * rows * kn[1];
+    // every chunk length up to `rows` (a shorter chunk may plan more K splits)
+    for (int64_t m = 1; m <= rows; m++)
+        for (auto &kn : shapes) {
+            if (kn[0] % 64 != 0) continue;
+            for (bool q8 : {false, true}) {
+                const WidePlan wp = wide_plan(m, kn[0], kn[1], q8);
+                const int64_t sp = wp.nt ? wp.splits : gemm_splits(m, kn[0], kn[1]);
+                if (sp > 1 && sp * m * kn[1] > most) most = sp * m * kn[1];
+            }
         }
-    }
     return most;
 }
 

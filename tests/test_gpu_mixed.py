@@ -143,7 +143,8 @@ def test_mixed_model_stream_matches_oracle(A, ctx, oracle, mix):
 
 @pytest.mark.parametrize("mix", list(MIXES))
 def test_mixed_batched_prefill_matches_per_position(A, ctx, oracle, mix):
-    """aesir_prefill of a 140-token prompt (two chunks) against the per-position oracle."""
+    """aesir_prefill of a 140-token prompt (one chunk: two 128-row M tiles of the wide GEMM) against
+    the per-position oracle."""
     cfg = oracle.Config(**SMALL)
     m, _, back = mixed_model(A, ctx, oracle, cfg, MIXES[mix], 6)
     om = oracle.Model(cfg, back)

@@ -129,12 +129,14 @@ def test_prefill_tiny_matches_per_position(A, ctx, oracle):
 
 
 def test_prefill_chunks_and_continuation(A, ctx, oracle):
-    """300 positions = 128-row chunks 128 + 128 + 44; then the same prompt as 100 + 200 positions
+    """1100 positions = 512-row chunks 512 + 512 + 76; then the same prompt as 100 + 1000 positions
     (start_pos 100): both equal the per-position prefill."""
-    cfg = oracle.TINY
+    import dataclasses
+
+    cfg = dataclasses.replace(oracle.TINY, ctx_len=1200)
     w = oracle.synthetic_weights(cfg, 99)
     om = oracle.Model(cfg, w)
-    prompt = oracle.prompt_tokens(300, cfg.vocab, 11)
+    prompt = oracle.prompt_tokens(1100, cfg.vocab, 11)
     first, ologits, follow = oracle_prefill(om, prompt, 4)
     m = gpu_model(A, ctx, cfg, w)
     got = m.prefill(prompt)

@@ -202,7 +202,8 @@ def test_q8_batched_prefill_matches_per_position(A, ctx, oracle, shape, n_prompt
     """aesir_prefill on a Q8_0 model runs the Q8_0 MFMA GEMMs (quants and scales copied into LDS,
     dequantized per fragment): the next token, logits within tolerance and the greedy steps that
     read the prefilled cache equal the per-position oracle on the dequantized weights. 200
-    positions = two 128-row chunks; `split` > 0 prefills the prompt in two calls (start_pos > 0)."""
+    positions = one chunk of two 128-row M tiles; `split` > 0 prefills the prompt in two calls
+    (start_pos > 0)."""
     cfg = dict(Q8_SMALL if shape == "small" else Q8_TL)
     cfg["ctx_len"] = max(cfg["ctx_len"], n_prompt + 8)
     tensors, deq = q8_weights(A, oracle, cfg, 41)

@@ -175,8 +175,10 @@ def test_quant_model_stream_matches_dequantized_oracle(A, ctx, oracle, kind):
 
 @pytest.mark.parametrize("kind", list(TYPES))
 def test_quant_batched_prefill_matches_per_position(A, ctx, oracle, kind):
-    """aesir_prefill of a 140-token prompt (two chunks, matrix cores on f16 copies of the weights)
-    against the per-position oracle: next token (near ties allowed) and logits within tolerance."""
+    """aesir_prefill of a 140-token prompt (one chunk: two 128-row M tiles of the matrix-core GEMM on
+    the repacked planes), and of the same prompt as 100 + 40 positions (the 40-row chunk on f16
+    copies of the weights and 32-row tiles), against the per-position oracle: next token (near
+    ties allowed) and logits within tolerance."""
     cfg = oracle.Config(**SMALL)
     m, om = quant_model(A, ctx, oracle, cfg, kind, 6)
     prompt = oracle.prompt_tokens(140, cfg.vocab, 4)
@@ -187,6 +189,12 @@ def test_quant_batched_prefill_matches_per_position(A, ctx, oracle, kind):
     assert within_tol(m.logits(), ol)
     assert same_token(got, want, ol), (got, want)
     m.close()
+    m2, _ = quant_model(A, ctx, oracle, cfg, kind, 6)
+    m2.prefill(prompt[:100], 0)
+    got2 = m2.prefill(prompt[100:], 100)
+    assert within_tol(m2.logits(), ol)
+    assert same_token(got2, want, ol), (got2, want)
+    m2.close()
 
 
 @pytest.mark.parametrize("kind", list(TYPES))

@@ -575,6 +575,10 @@ def main():
         out["micro"] = micro_bench(A, args.seed)
     if not args.no_prefill:
         out["prefill"] = prefill_bench(A, args.seed)
+        # a 1024-token prompt: two 512-row chunks
+        lp = prefill_bench(A, args.seed, n_prompt=1024, n_decode=0)
+        out["prefill"]["prompt_1024"] = {"prefill_ms": lp["prefill_ms"], "prefill_tok_s": lp["prefill_tok_s"],
+                                         "gemm_tflops": lp["gemm_tflops"]}
     out["sampler"] = sampler_bench(A, args.seed)
     if not args.no_q8:
         out["q8_0"] = q8_bench(A, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters, use_graph)

@@ -575,7 +575,7 @@ def main():
         out["micro"] = micro_bench(A, args.seed)
     if not args.no_prefill:
         out["prefill"] = prefill_bench(A, args.seed)
-        # a 1024-token prompt: two 512-row chunks
+        # a 1024-token prompt (one chunk)
         lp = prefill_bench(A, args.seed, n_prompt=1024, n_decode=0)
         out["prefill"]["prompt_1024"] = {"prefill_ms": lp["prefill_ms"], "prefill_tok_s": lp["prefill_tok_s"],
                                          "gemm_tflops": lp["gemm_tflops"]}

@@ -362,7 +362,7 @@ int32_t aesir_forward_pass_no_cache(aesir_model *model, const int64_t *tokens, i
                                     int64_t *next_token);
 /* Batched prefill: the same result as forward_pass at each position start_pos .. start_pos +
  * n_tokens - 1 in turn (the per-position prefill loop of _run_generation, aesir.mojo:358-374),
- * computed with all positions of a chunk of up to 512 rows going through each layer together: MFMA f16
+ * computed with all positions of a chunk of up to 2048 rows going through each layer together: MFMA f16
  * GEMMs (f32 accumulate), causal GQA attention over the cache, K/V appended for every position.
  * tokens[i] is evaluated at position start_pos + i. Waits; *next_token is the greedy token after
  * the last position and aesir_model_logits returns its logits. f32 summation order differs from

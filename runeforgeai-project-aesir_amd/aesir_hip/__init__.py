@@ -775,7 +775,7 @@ class Model:
 
     def prefill(self, tokens, start_pos: int = 0) -> int:
         """Batched prefill of tokens at positions start_pos..: the same KV cache and next token as
-        forward_pass at each position in turn (aesir.mojo:358-374), one pass per chunk of up to 512
+        forward_pass at each position in turn (aesir.mojo:358-374), one pass per chunk of up to 2048
         rows."""
         t = np.ascontiguousarray(np.array(tokens, dtype=np.int64))
         nxt = I64()

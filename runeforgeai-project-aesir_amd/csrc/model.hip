@@ -601,7 +601,7 @@ int32_t model_create(aesir_ctx *ctx, const aesir_model_config *cfg, const Weight
     take(attention_partial_floats(c.n_heads, hd, max_split) * 4, &p);
     m->attn_part = (float *)p;
     take(lm_head_groups(V) * 8, &m->lm_parts);
-    m->pf_rows = c.ctx_len < 512 ? c.ctx_len : 512;  // batched-prefill chunk
+    m->pf_rows = c.ctx_len < 2048 ? c.ctx_len : 2048;  // batched-prefill chunk
     const int64_t pr = m->pf_rows;
     take(pr * d * 2, &m->pf_x);
     take(pr * d * 2, &m->pf_xn);

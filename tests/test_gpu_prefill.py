@@ -129,14 +129,14 @@ def test_prefill_tiny_matches_per_position(A, ctx, oracle):
 
 
 def test_prefill_chunks_and_continuation(A, ctx, oracle):
-    """1100 positions = 512-row chunks 512 + 512 + 76; then the same prompt as 100 + 1000 positions
-    (start_pos 100): both equal the per-position prefill."""
+    """2200 positions = 2048-row chunks 2048 + 152; then the same prompt as 100 + 2100 positions
+    (start_pos 100: chunks 2048 + 52): both equal the per-position prefill."""
     import dataclasses
 
-    cfg = dataclasses.replace(oracle.TINY, ctx_len=1200)
+    cfg = dataclasses.replace(oracle.TINY, ctx_len=2300)
     w = oracle.synthetic_weights(cfg, 99)
     om = oracle.Model(cfg, w)
-    prompt = oracle.prompt_tokens(1100, cfg.vocab, 11)
+    prompt = oracle.prompt_tokens(2200, cfg.vocab, 11)
     first, ologits, follow = oracle_prefill(om, prompt, 4)
     m = gpu_model(A, ctx, cfg, w)
     got = m.prefill(prompt)

@@ -270,8 +270,9 @@ typedef struct {
 } aesir_model_config;
 
 /* Lays out one model in the well: f16 weights (Q/K/V rows concatenated, gate/up rows
- * interleaved), norms, KV cache [layers][ctx_len][kv_dim] x2, decode workspace. The weights
- * start zeroed. Validates the GGUFModelConfig contract (loader/gguf.mojo:133-149). */
+ * interleaved), norms, KV cache [layers][ctx_len][kv_dim] x2, decode workspace and the batched
+ * prefill's workspace for chunks of min(ctx_len, 2048) rows (about 2 x rows x (6 dim + 3 ffn)
+ * bytes plus the K-split partials; 270 MB for the Llama-3-8B shape). The weights start zeroed. Validates the GGUFModelConfig contract (loader/gguf.mojo:133-149). */
 int32_t aesir_model_create(aesir_ctx *ctx, const aesir_model_config *cfg, aesir_model **out);
 /* aesir_model_create with a weight type for the seven matrix kinds (token_embd, output, attn_q/k/v,
  * attn_output, ffn_gate/up/down): AESIR_GGML_F16 (what aesir_model_create makes), AESIR_GGML_Q8_0,

@@ -49,12 +49,17 @@ extern "C" {
  * (core/compute.mojo:876-912, 266-280) fix the arithmetic: w = f16(f16(q - 8) * d). */
 #define AESIR_GGML_Q4_0 2
 /* GGML's K-quant super-blocks of 256 weights as GGUF files hold them (the ids the reference loader
- * names at loader/gguf.mojo:20-30; its own BlockQ4_K / BlockQ6_K are different, synthetic
- * layouts): block_q4_K {f16 d; f16 dmin; uint8 scales[12]; uint8 qs[128]} (144 bytes),
- * w = d * sc * q - dmin * m with 6-bit sc, m per 32 weights; block_q6_K {uint8 ql[128];
+ * names at loader/gguf.mojo:20-30): block_q4_K {f16 d; f16 dmin; uint8 scales[12]; uint8 qs[128]}
+ * (144 bytes), w = d * sc * q - dmin * m with 6-bit sc, m per 32 weights; block_q6_K {uint8 ql[128];
  * uint8 qh[64]; int8 scales[16]; f16 d} (210 bytes), w = d * sc * (q - 32) with 6-bit q. The
- * library's weights are the f16 values of the reference's f16 dequantization arithmetic
- * (aesir_gemm_quant). */
+ * reference's BlockQ4_K is a different, synthetic 32-weight block {f16 scale; f16 min_val;
+ * uint8 qs[16]} (core/compute.mojo:84-98). Its BlockQ6_K has GGML's fields (:183-199), but its
+ * decoder dequantize_q6_k_block (:508-527) ignores the scales and reads qh[(i + 128) / 2], past
+ * qh's 64 entries, for every upper-half weight (:524); so the library follows GGML's layout and
+ * formula for both. Weights are f16: a = f16(d * sc), b = f16(dmin * m), then Q4_K
+ * w = f16(a * q - b) rounded once (GGML evaluates the formula in f32 and the reference has no
+ * K-quant arithmetic for these blocks, so the library keeps the f16 value nearest the exact
+ * a * q - b) and Q6_K w = f16(a * (q - 32)) (aesir_gemm_quant). */
 #define AESIR_GGML_Q4_K 12
 #define AESIR_GGML_Q6_K 14
 /* The reference's other GGUF-block formats (loader/gguf.mojo:21-29): block_q4_1 {f16 d; f16 m;
@@ -62,9 +67,11 @@ extern "C" {
  * block_q5_1 {f16 d; f16 m; uint8 qh[4]; uint8 qs[16]} (24), the reference's BlockQ4_1 / BlockQ5_0 /
  * BlockQ5_1 (core/compute.mojo:35-83), with its weights: Q4_1 w = f16(f16(q * d) + m), Q5_0
  * w = f16((q - 16) * d), Q5_1 w = f16(f16(q * d) + m) for the 4- or 5-bit q (compute.mojo:282-340,
- * each f16 operation rounded); and GGML's block_q2_K (84 bytes / 256 weights), block_q3_K (110)
- * and block_q5_K (176), whose f16 weights follow the Q4_K / Q6_K rules: a = f16(d * sc),
- * b = f16(dmin * m), w = f16(a * q - b) (Q2_K, Q5_K, one rounding) or f16(a * q) (Q3_K, signed q). */
+ * each f16 operation rounded: these are the reference's own arithmetic on these very blocks, so
+ * Q4_1 / Q5_1 keep its two roundings where the K-quants round once); and GGML's block_q2_K
+ * (84 bytes / 256 weights), block_q3_K (110) and block_q5_K (176), whose f16 weights follow the
+ * Q4_K / Q6_K rules: a = f16(d * sc), b = f16(dmin * m), w = f16(a * q - b) (Q2_K, Q5_K, one
+ * rounding) or f16(a * q) (Q3_K, signed q). */
 #define AESIR_GGML_Q4_1 3
 #define AESIR_GGML_Q5_0 6
 #define AESIR_GGML_Q5_1 7
@@ -162,7 +169,9 @@ int32_t aesir_attn_gqa_decode(aesir_ctx *ctx, const void *query, int64_t query_r
  * split count is halved until it does, and sizes that do not fit with one split are rejected
  * with AESIR_ERR_UNSUPPORTED). It calls no allocator. All calls on one GPU share that array:
  * calls that overlap on one GPU (two streams, or two host threads) race and must be ordered by
- * the caller. */
+ * the caller. The first call on each device resolves the array's device address
+ * (hipGetSymbolAddress) and must be made outside any stream capture; later calls may be captured
+ * into a HIP graph, whose replays recompute every partial they read. */
 int32_t aesir_attn_gqa_decode_static(void *stream, const void *query, int64_t query_rows, const void *keys,
                                      int64_t keys_cols, const void *values, int64_t values_cols, void *output,
                                      int64_t output_rows, int64_t seq_len, int64_t head_dim, int64_t nq,
@@ -271,8 +280,12 @@ typedef struct {
 
 /* Lays out one model in the well: f16 weights (Q/K/V rows concatenated, gate/up rows
  * interleaved), norms, KV cache [layers][ctx_len][kv_dim] x2, decode workspace and the batched
- * prefill's workspace for chunks of min(ctx_len, 2048) rows (about 2 x rows x (6 dim + 3 ffn)
- * bytes plus the K-split partials; 270 MB for the Llama-3-8B shape). The weights start zeroed. Validates the GGUFModelConfig contract (loader/gguf.mojo:133-149). */
+ * prefill's workspace for chunks of R = min(ctx_len, 2048) rows: 2 x R x (5 dim + 2 kv_dim + ffn)
+ * bytes of activations (151 MB for the Llama-3-8B shape) plus the K-split partials, plus
+ * 4 x R x ffn bytes of gate/up products only when dim or ffn is not a multiple of 64 (the shapes
+ * whose prefill GEMMs fall back to the GEMV path). A quantized model of a repacked type also holds
+ * an f16 copy of its largest layer matrix for short prefill chunks (2 x 2 ffn x dim bytes). The
+ * weights start zeroed. Validates the GGUFModelConfig contract (loader/gguf.mojo:133-149). */
 int32_t aesir_model_create(aesir_ctx *ctx, const aesir_model_config *cfg, aesir_model **out);
 /* aesir_model_create with a weight type for the seven matrix kinds (token_embd, output, attn_q/k/v,
  * attn_output, ffn_gate/up/down): AESIR_GGML_F16 (what aesir_model_create makes), AESIR_GGML_Q8_0,

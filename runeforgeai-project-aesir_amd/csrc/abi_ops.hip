@@ -250,10 +250,14 @@ int32_t aesir_gemm_quant(aesir_ctx *ctx, const void *A, int64_t a_rows, int64_t 
     // them in registers. Otherwise the blocks are dequantized to f16 (the same values) for the F16
     // GEMM, on the matrix cores from 2 rows. Both take free well space for this call, released after enqueueing (later work on the
     // stream runs after these kernels).
+    // Both repacked-plane routes read A with 16-byte loads (the GEMV stages x with them, the wide
+    // kernel copies A into LDS with them): an A that is not 16-byte aligned (an offset view) takes
+    // the dequantize-then-F16 route, which checks its own alignment.
     const int64_t K = a_cols, N = b_rows, mark = ctx->well_offset;
     int32_t rc = AESIR_OK;
-    const bool wide = qf_type(ggml_type) && K % 128 == 0 && gemm_qf_wide_ok(a_rows, K, N);
-    if ((a_rows < 16 && qf_type(ggml_type) && qf_gemv_ok(K)) || wide) {
+    const bool a16 = ((uintptr_t)A & 15) == 0;
+    const bool wide = a16 && qf_type(ggml_type) && K % 128 == 0 && gemm_qf_wide_ok(a_rows, K, N);
+    if ((a16 && a_rows < 16 && qf_type(ggml_type) && qf_gemv_ok(K)) || wide) {
         QFMat w;
         w.type = ggml_type;
         void *planes[4] = {nullptr, nullptr, nullptr, nullptr};

@@ -250,8 +250,9 @@ int32_t parse(Gguf &g, const char *path) {
     AESIR_TRY(g.need(data_offset, 0));
     for (auto &t : raw) {  // _map_tensor (loader/gguf.mojo:465-499)
         if (g.by_name.count(t.name)) return fail(AESIR_ERR_FORMAT, "GGUF contains a duplicate tensor name: %s", t.name.c_str());
-        // F16 and F32 as the reference loader; the block types beyond it (Q8_0, Q4_0, Q4_K, Q6_K) by their GGML
-        // block geometry. Every size product is overflow-checked before any range check.
+        // F16 and F32 as the reference loader; the block types beyond it (Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q2_K,
+        // Q3_K, Q4_K, Q5_K, Q6_K) by their GGML block geometry. Every size product is overflow-checked before
+        // any range check.
         const int64_t bytes = ggml_tensor_bytes(t.type, t.rows, t.cols);
         if (bytes == -1) return fail(AESIR_ERR_FORMAT, "Real inference slice supports only F16 and F32 tensors");
         if (bytes == -2)

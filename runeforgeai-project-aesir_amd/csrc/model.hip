@@ -609,7 +609,7 @@ int32_t model_create(aesir_ctx *ctx, const aesir_model_config *cfg, const Weight
     take(pr * d * 2, &m->pf_q);
     take(pr * d * 2, &m->pf_att);
     take(pr * f * 2, &m->pf_act);
-    take(pr * 2 * f * 2, &m->pf_gu);
+    if (!prefill_gemm_shapes_ok(pr, d, d + 2 * kvd, f)) take(pr * 2 * f * 2, &m->pf_gu);  // fallback GEMM only
     take(pr * 8, &m->pf_tokens);
     m->pf_part_floats = prefill_part_floats(pr, d, d + 2 * kvd, f);
     if (m->pf_part_floats > 0) {

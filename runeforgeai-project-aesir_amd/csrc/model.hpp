@@ -141,6 +141,8 @@ int32_t model_prefill(aesir_model *m, const int64_t *tokens, int64_t n, int64_t 
 // f32 split-K partial floats the prefill GEMMs of a model with these shapes need for chunks of up
 // to `rows` rows.
 int64_t prefill_part_floats(int64_t rows, int64_t dim, int64_t qkv_n, int64_t ffn);
+// True when every prefill GEMM of this shape runs on the matrix cores (no fallback buffers needed).
+bool prefill_gemm_shapes_ok(int64_t rows, int64_t dim, int64_t qkv_n, int64_t ffn);
 // Decode-step helpers shared with the prefill.
 int32_t ensure_rope(aesir_model *m, int64_t max_pos);
 int32_t upload_state(aesir_model *m, int64_t token, int64_t pos, int64_t advance, int64_t ring_cap);

@@ -524,6 +524,17 @@ static int64_t gemm_splits(int64_t M, int64_t K, int64_t N) {
     return s < 1 ? 1 : s;
 }
 
+// The shape half of prefill_mfma_ok: true when a model of this shape runs every prefill GEMM on
+// the matrix cores (its arena buffers and weights are 256-byte aligned, which covers the rest), so
+// the f16 gate/up products of the fallback need no buffer.
+bool prefill_gemm_shapes_ok(int64_t rows, int64_t dim, int64_t qkv_n, int64_t ffn) {
+    const int64_t lim = (int64_t)1 << 31;
+    const int64_t shapes[4][2] = {{dim, qkv_n}, {dim, dim}, {dim, 2 * ffn}, {ffn, dim}};  // (K, N)
+    for (auto &kn : shapes)
+        if (kn[0] % 64 != 0 || (rows + kGemmMT) * kn[0] * 2 >= lim || (kn[1] + kGemmNT) * kn[0] * 2 >= lim) return false;
+    return true;
+}
+
 int64_t prefill_part_floats(int64_t rows, int64_t dim, int64_t qkv_n, int64_t ffn) {
     const int64_t shapes[4][2] = {{dim, qkv_n}, {dim, dim}, {dim, 2 * ffn}, {ffn, dim}};  // (K, N)
     int64_t most = 0;
@@ -1153,6 +1164,7 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
             xn_ready = next_norm != nullptr;
         } else {
             // interleaved gate/up rows -> [n][2f] products, then the SwiGLU over the pairs
+            if (!m->pf_gu) return fail(AESIR_ERR_UNSUPPORTED, "prefill: no gate/up buffer for the fallback GEMM");
             AESIR_TRY(launch_gemm_f16(m->ctx, Xn, n, d, L.gu.w, 2 * f, m->pf_gu));
             AESIR_TRY(launch_swiglu_pairs(s, m->pf_gu, ACT, n * f));
             AESIR_TRY(launch_gemm_f16(m->ctx, ACT, n, f, L.down.w, d, Xn));

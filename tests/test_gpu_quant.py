@@ -105,6 +105,28 @@ def test_gemm_q4_0_rows_off_the_tile_grid(A, ctx, oracle, kind, M, K, N):
     assert not ((d > 1) & (np.abs(got.astype(np.float64) - ref.astype(np.float64)) > noise)).any(), d.max()
 
 
+@pytest.mark.parametrize("kind", ("q4_0", "q4_k", "q6_k"))
+@pytest.mark.parametrize("M", (1, 100))
+def test_gemm_quant_unaligned_a(A, ctx, oracle, kind, M):
+    """A as an offset view (2-byte aligned, not 16-byte): the repacked-plane routes need 16-byte
+    loads of A, so the call takes the dequantize-then-F16 route at 1 row (the GEMV's) and at 100
+    rows (the wide kernel's) and still matches f64 on the library's f16 weights."""
+    K, N = 4096, 96
+    t = random_tensor(A, kind, N, K, RNG)
+    x = RNG.standard_normal((M, K)).astype(np.float16)
+    buf = ctx.from_numpy(np.concatenate([np.zeros(1, np.float16), x.reshape(-1)]).reshape(1, -1))
+    a = buf.view(M, K, offset_elems=1)
+    assert a.ptr % 16 != 0
+    c = ctx.tensor(M, N)
+    A.gemm_quant(ctx, a, upload_bytes(ctx, t.blocks), TYPES[kind], N, c)
+    got = c.numpy().astype(np.float64)
+    W = lib_weights(oracle, kind, t)
+    xd = x.astype(np.float64)
+    exact = xd @ W.T
+    tol = np.abs(np.spacing(exact.astype(np.float16))).astype(np.float64) + 2.0 ** -17 * (np.abs(xd) @ np.abs(W).T)
+    assert np.all(np.abs(got - exact) <= tol), np.max(np.abs(got - exact) / tol)
+
+
 def test_gemm_quant_errors(A, ctx):
     a = ctx.tensor(1, 96)
     c = ctx.tensor(1, 2)

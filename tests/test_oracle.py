@@ -908,6 +908,9 @@ def test_legacy_pack_dequant_and_gemm(oracle, kind):
         ref = ((q * dd).astype(np.float16).astype(np.float64) + mm).astype(np.float16)
     got = oracle.dequantize_legacy(kind, t.blocks, rows * cols // 32).reshape(rows, cols)
     assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+    if kind != "q5_0":  # the K-quants' single rounding of q d + m would give other weights here
+        fused = (q * dd + mm).astype(np.float16)
+        assert not np.array_equal(got.view(np.uint16), fused.view(np.uint16))
     x = rng.standard_normal((3, cols)).astype(np.float16)
     c = oracle.gemm_legacy(kind, x, t.blocks, rows)
     exact = x.astype(np.float64) @ ref.astype(np.float64).T
@@ -1053,6 +1056,9 @@ def test_kquant_f16_rule_random(oracle):
         b = (dmin.astype(np.float64)[:, np.arange(cols) // 256] * m[:, sub]).astype(np.float16).astype(np.float64)
         got = oracle.dequantize_kquant_f16(kind, t.blocks, rows * nsb).reshape(rows, cols)
         assert np.array_equal(got.view(np.uint16), (a * q - b).astype(np.float16).view(np.uint16)), kind
+        if kind != "q3_k":  # the two-step rounding of Q4_1 / Q5_1 would give other weights here
+            two_step = ((a * q).astype(np.float16).astype(np.float64) - b).astype(np.float16)
+            assert not np.array_equal(got.view(np.uint16), two_step.view(np.uint16)), kind
         f32 = oracle.dequantize_kquant(kind, t.blocks, rows * nsb).reshape(rows, cols).astype(np.float64)
         rel = 2.0 ** -11 * (1 + 2.0 ** -10)
         bound = np.abs(np.spacing(got)).astype(np.float64) / 2 + np.abs(q) * np.abs(a) * rel + np.abs(b) * rel

@@ -63,3 +63,46 @@ def test_static_attention_rejects_sizes_beyond_its_scratch(A):
         # the reference's silent no-ops stay no-ops (return 0, nothing launched)
         assert A._L.aesir_attn_gqa_decode_static(stream, t.ptr, 1, t.ptr, 256, t.ptr, 256, t.ptr, 1, 0, 256, 1, 1) == 0
         assert A._L.aesir_attn_gqa_decode_static(stream, t.ptr, 1, t.ptr, 256, t.ptr, 256, t.ptr, 1, 4, 128, 3, 2) == 0
+
+
+def test_static_attention_under_graph_capture(A):
+    """Code under HIP graph capture, the caller this entry point is for: after one eager call on
+    the device (which resolves the scratch address; the first call on a device must not be inside
+    a capture), a captured call replays bit for bit like the eager one, also when an eager call
+    with other inputs has rewritten the shared static scratch between replays."""
+    hip = C.CDLL("libamdhip64.so")
+    for f in ("hipStreamCreate", "hipStreamSynchronize", "hipStreamBeginCapture", "hipStreamEndCapture",
+              "hipGraphInstantiate", "hipGraphLaunch", "hipGraphExecDestroy", "hipGraphDestroy", "hipStreamDestroy"):
+        getattr(hip, f).restype = C.c_int
+    rng = np.random.default_rng(23)
+    S, hd, nq, nkv = 2048, 128, 32, 8
+    with A.Context(512 << 20) as ctx:
+        (q, k, v), (tq, tk, tv), out_ref, out_graph = _case(A, ctx, rng, S, hd, nq, nkv)
+        _, (oq, ok_, ov), out_other, _ = _case(A, ctx, rng, 3000, hd, nq, nkv)
+        stream = C.c_void_p()
+        assert hip.hipStreamCreate(C.byref(stream)) == 0
+
+        def static(tq_, tk_, tv_, out, S_):
+            return A._L.aesir_attn_gqa_decode_static(stream, tq_.ptr, 1, tk_.ptr, tk_.cols, tv_.ptr, tv_.cols,
+                                                     out.ptr, 1, S_, hd, nq, nkv)
+
+        assert static(tq, tk, tv, out_ref, S) == 0, A.last_error()  # eager call (also the warm-up)
+        assert hip.hipStreamSynchronize(stream) == 0
+        ref = out_ref.numpy()
+        graph, exe = C.c_void_p(), C.c_void_p()
+        assert hip.hipStreamBeginCapture(stream, 1) == 0  # thread-local capture mode
+        rc = static(tq, tk, tv, out_graph, S)
+        assert hip.hipStreamEndCapture(stream, C.byref(graph)) == 0
+        assert rc == 0, A.last_error()
+        assert hip.hipGraphInstantiate(C.byref(exe), graph, None, None, 0) == 0
+        try:
+            for _ in range(3):
+                out_graph.upload(np.full((1, nq * hd), np.nan, np.float16))
+                assert static(oq, ok_, ov, out_other, 3000) == 0  # eager work on the same scratch
+                assert hip.hipGraphLaunch(exe, stream) == 0
+                assert hip.hipStreamSynchronize(stream) == 0
+                assert np.array_equal(out_graph.numpy().view(np.uint16), ref.view(np.uint16))
+        finally:
+            hip.hipGraphExecDestroy(exe)
+            hip.hipGraphDestroy(graph)
+            hip.hipStreamDestroy(stream)

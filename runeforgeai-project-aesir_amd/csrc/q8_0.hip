@@ -195,7 +195,42 @@ __global__ __launch_bounds__(kQThreads) void q8_0_staged_kernel(const uint8_t *_
 //     groups ahead of the one being summed (every wave issues P one-kilobyte copies per group, the
 //     range check zero-fills past the matrix, so the vmcnt waits are exact counts).
 constexpr int kCus = 256;  // MI355X compute units (the persistent grid's size unit)
+constexpr int kQDirectRpw = 64;  // rows per workgroup of q8_0_direct_kernel (its LDS row sums)
+// 16 bytes loaded from a 4-byte aligned address (gfx950 serves unaligned vector loads)
+typedef unsigned int u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
 constexpr int q8_vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// The four signed 8-bit digit planes of a block's 32 x values (see above): v = rint(x 2^(29 - e)),
+// u = v + 0x808080 has the bytes d0 + 128, d1 + 128, d2 + 128 (each d_j in [-128, 127], d_j = v's
+// nearest-digit recurrence) and the signed top digit d3 = floor(u / 2^24), |d3| <= 64; a 4 x 4 byte
+// transpose (v_perm_b32) gathers digit j of four x values into dg[j][w], and the xor with 0x80 per
+// byte turns d_j + 128 back into d_j. plain: the block holds an inf or NaN (then dg is zero).
+__device__ __forceinline__ void x_digits(const float *xb, int (&dg)[4][8], int &ex, bool &plain) {
+    float xv[32];
+#pragma unroll
+    for (int i = 0; i < 32; i += 4) *reinterpret_cast<u32x4 *>(&xv[i]) = ld16(xb + i);
+    float m = 0.0f;
+    plain = false;
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        m = fmaxf(m, fabsf(xv[i]));
+        plain |= !(fabsf(xv[i]) <= 3.402823466e38f);  // inf or NaN
+    }
+    ex = m > 0.0f && !plain ? ilogbf(m) : 0;
+#pragma unroll
+    for (int w = 0; w < 8; w++) {
+        unsigned u[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            u[k] = plain ? 0x808080u : (unsigned)((int)rintf(ldexpf(xv[4 * w + k], 29 - ex)) + 0x808080);  // |v| <= 2^30
+        const unsigned t01l = __builtin_amdgcn_perm(u[1], u[0], 0x05010400u), t01h = __builtin_amdgcn_perm(u[1], u[0], 0x07030602u);
+        const unsigned t23l = __builtin_amdgcn_perm(u[3], u[2], 0x05010400u), t23h = __builtin_amdgcn_perm(u[3], u[2], 0x07030602u);
+        dg[0][w] = (int)(__builtin_amdgcn_perm(t23l, t01l, 0x05040100u) ^ 0x80808080u);
+        dg[1][w] = (int)(__builtin_amdgcn_perm(t23l, t01l, 0x07060302u) ^ 0x80808080u);
+        dg[2][w] = (int)(__builtin_amdgcn_perm(t23h, t01h, 0x05040100u) ^ 0x80808080u);
+        dg[3][w] = (int)__builtin_amdgcn_perm(t23h, t01h, 0x07060302u);
+    }
+}
 
 template <int NW, int PH, int RT, int S, int P>
 __global__ __launch_bounds__(NW * 64) void q8_0_digits_kernel(const uint8_t *__restrict__ blocks, int64_t N,
@@ -344,6 +379,162 @@ __global__ __launch_bounds__(NW * 64) void q8_0_digits_kernel(const uint8_t *__r
     if (it % kYs) flush(it % kYs, last);
 }
 
+// The same integer-digit arithmetic with the weights loaded straight into registers (no LDS
+// staging), for rows of nb = 64 WPR blocks.
+//   - Lane l of wave w owns block column b = 64 (w % WPR) + l, so a wave covers 64 consecutive
+//     blocks (2176 contiguous bytes) of a row and WPR waves cover the row; the workgroup's PH row
+//     phases (w / WPR) take its rows.
+//   - Per row a lane loads 16 + 16 + 4 bytes: the 32 bytes from the 4-byte aligned word at or below
+//     its block's quants (34 b + 2: two bytes into a word for an even b, on a word boundary for an
+//     odd one) and one more word (the last two quants of an even b, the scale d of an odd b). The
+//     lanes of one instruction read 64 blocks' bytes 34 apart: every cache line of the wave's span
+//     is requested by each instruction that touches it, which the L1 absorbs; HBM sees the row once.
+//   - Rows are dealt out across the grid: at step k workgroup g's phase p takes row
+//     (k G + g) PH + p (G workgroups), so the grid sweeps the matrix front to back together
+//     instead of running G separate streams.
+//   - D rows are in flight per wave: row step k + D is requested as soon as step k has been
+//     consumed, into the registers step k used (the loop is unrolled D times, so the wait before a
+//     row counts exactly the loads issued after it). The first D rows are requested before x is
+//     read and turned into digits.
+//   - A row's 64 block values per wave are summed by recursive halving (two rows at a time); the
+//     wave sums go to LDS and, after the workgroup's last row, WPR of them make each row's y. No
+//     barrier runs before the end.
+template <int WPR, int PH, int D>
+__global__ __launch_bounds__(WPR * PH * 64) void q8_0_direct_kernel(const uint8_t *__restrict__ blocks, int64_t N,
+                                                                   int64_t rowbytes, int64_t rpw,
+                                                                   const float *__restrict__ x, float *__restrict__ y) {
+    constexpr int NW = WPR * PH;
+    static_assert(D == 2 || D == 4, "rows in flight");
+    __shared__ float part[kQDirectRpw][WPR];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = wave % WPR, ph = wave / WPR;
+    const int b = 64 * c + lane;
+    // row of step k of phase p: (k G + g) PH + p, so that at step k the whole grid reads rows
+    // [k G PH, (k + 1) G PH): one sweep through the matrix instead of G separate streams
+    const int64_t G = gridDim.x, g = blockIdx.x;
+    auto row_of = [&](int64_t k, int p) { return (k * G + g) * PH + p; };
+    const int nmine = row_of(0, ph) < N ? (int)((N - 1 - row_of(0, ph)) / (G * PH)) + 1 : 0;  // rows of this wave
+
+    const float *xb = x + 32 * b;
+    int dg[4][8];  // x digits, ex and plain: set after the first weight requests (x_digits below)
+    int ex = 0;
+    bool plain = false;
+    // Quants of block b start at byte 34 b + 2: at byte 2 of the 4-byte aligned word at 34 b for
+    // an even b, at a word boundary for an odd one. A lane loads the 32 bytes from the aligned word
+    // at or below its quants (A, B) and one word C: the one after them for an even b (its last two
+    // quants), the one holding d for an odd b (d sits just before its quants).
+    const bool odd = b & 1;
+    const int qoff = odd ? 34 * b + 2 : 34 * b, coff = odd ? 34 * b - 2 : 34 * b + 32;
+    const unsigned qs = odd ? 0u : 2u;  // byte shift from the loaded words to the quants
+    struct Row {
+        u32x4 a, bq;
+        uint32_t c;
+    };
+    auto load = [&](int k, Row &rw) {  // row k of this wave (rows past the matrix re-read the last one)
+        int64_t r = row_of(k, ph);
+        r = r < N ? r : N - 1;
+        const uint8_t *p = blocks + r * rowbytes;
+        rw.a = *reinterpret_cast<const u32x4_a4 *>(p + qoff);
+        rw.bq = *reinterpret_cast<const u32x4_a4 *>(p + qoff + 16);
+        rw.c = *reinterpret_cast<const uint32_t *>(p + coff);
+    };
+    auto value = [&](const Row &rw) -> float {  // block b of the row
+        const uint32_t w[9] = {rw.a.x, rw.a.y, rw.a.z, rw.a.w, rw.bq.x, rw.bq.y, rw.bq.z, rw.bq.w, rw.c};
+        const h16 d = bits_to_h((uint16_t)(odd ? rw.c >> 16 : rw.a.x & 0xffff));
+        uint32_t q[8];  // quants 4i .. 4i + 3 (for an odd b, alignbyte by 0 ignores its high word)
+#pragma unroll
+        for (int i = 0; i < 8; i++) q[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], qs);
+        if (!plain) {
+            int s0 = 0, s1 = 0, s2 = 0, s3 = 0;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                s0 = __builtin_amdgcn_sdot4((int)q[i], dg[0][i], s0, false);
+                s1 = __builtin_amdgcn_sdot4((int)q[i], dg[1][i], s1, false);
+                s2 = __builtin_amdgcn_sdot4((int)q[i], dg[2][i], s2, false);
+                s3 = __builtin_amdgcn_sdot4((int)q[i], dg[3][i], s3, false);
+            }
+            // exact in f64: |s_j| < 2^20, the sum < 2^44
+            const double v = fma((double)s3, 16777216.0, fma((double)s2, 65536.0, fma((double)s1, 256.0, (double)s0)));
+            return (float)ldexp(v * (double)d, ex - 29);
+        }
+        float v = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; i++) v = fmaf((float)(int8_t)((q[i >> 2] >> (8 * (i & 3))) & 0xff), xb[i], v);
+        return (float)d * v;
+    };
+    // two rows' block values -> their wave sums (lanes 0 .. 31 hold row 0's, 32 .. 63 row 1's)
+    auto emit = [&](int k, float v0, float v1) {
+        float acc[2] = {v0, v1};
+        wave_multi_sum<2>(acc, lane);
+        if ((lane & 31) == 0) {
+            const int kk = k + (lane >> 5);
+            if (kk < nmine) part[kk * PH + ph][c] = acc[0];
+        }
+    };
+    // The first D rows are requested before x, so the weight stream starts at once; x and the
+    // digits follow (waiting for x waits for those rows too, which the first row needs anyway).
+    Row r0, r1, r2, r3;
+    load(0, r0);
+    __builtin_amdgcn_sched_barrier(0);
+    load(1, r1);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (D > 2) {
+        load(2, r2);
+        __builtin_amdgcn_sched_barrier(0);
+        load(3, r3);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    x_digits(xb, dg, ex, plain);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int k = 0; k < nmine; k += D) {
+        const float v0 = value(r0);
+        __builtin_amdgcn_sched_barrier(0);
+        load(k + D, r0);
+        __builtin_amdgcn_sched_barrier(0);
+        const float v1 = value(r1);
+        __builtin_amdgcn_sched_barrier(0);
+        load(k + D + 1, r1);
+        __builtin_amdgcn_sched_barrier(0);
+        emit(k, v0, v1);
+        if constexpr (D > 2) {
+            const float v2 = value(r2);
+            __builtin_amdgcn_sched_barrier(0);
+            load(k + D + 2, r2);
+            __builtin_amdgcn_sched_barrier(0);
+            const float v3 = value(r3);
+            __builtin_amdgcn_sched_barrier(0);
+            load(k + D + 3, r3);
+            __builtin_amdgcn_sched_barrier(0);
+            emit(k + 2, v2, v3);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(q8_vm_wait(0));  // the loads past the last row, before the barrier
+    __syncthreads();
+    for (int i = tid; i < rpw; i += NW * 64) {
+        const int64_t r = row_of(i / PH, i % PH);
+        if (r >= N) continue;
+        float v = 0.0f;
+#pragma unroll
+        for (int j = 0; j < WPR; j++) v += part[i][j];
+        y[r] = v;
+    }
+}
+
+template <int WPR, int PH, int D>
+static int32_t launch_direct(hipStream_t s, const void *blocks, int64_t N, int64_t rowbytes, const float *x, float *y,
+                             int wg_per_cu) {
+    // rpw: rows per workgroup, a multiple of PH (row steps x phases)
+    int64_t steps = (N + (int64_t)kCus * wg_per_cu * PH - 1) / ((int64_t)kCus * wg_per_cu * PH);
+    if (steps * PH > kQDirectRpw) steps = kQDirectRpw / PH;
+    const int64_t rpw = steps * PH;
+    const int64_t grid = (N + rpw - 1) / rpw;
+    hipLaunchKernelGGL((q8_0_direct_kernel<WPR, PH, D>), dim3((unsigned)grid), dim3(WPR * PH * 64), 0, s,
+                       (const uint8_t *)blocks, N, rowbytes, rpw, x, y);
+    AESIR_LAUNCH_CHECK("q8_0_direct_kernel");
+    return AESIR_OK;
+}
+
 template <int NW, int PH, int RT, int S, int P>
 static int32_t launch_digits(hipStream_t s, const void *blocks, int64_t N, int64_t rowbytes, const float *x, float *y,
                              int wg_per_cu) {
@@ -409,11 +600,16 @@ int32_t launch_q8_0_matvec_f32(hipStream_t s, const void *blocks, int64_t N, int
     // workgroups per CU measured on MI355X at 14336 x 4096 (2 per CU, 2 stages: 13.8 us against 17.5
     // for the staged kernel) and 4096 x 14336 (1 per CU, 3 stages: 14.8 us against 19.6).
     if (K % 32 == 0 && ((uintptr_t)blocks & 15) == 0 && ((uintptr_t)x & 15) == 0 && N * rowbytes < ((int64_t)1 << 31)) {
+        // Llama's 4096- and 14336-long rows: the register-direct kernel, one workgroup per CU
+        // (measured on MI355X, 32 calls graph-replayed, weights past the MALL: 14336 x 4096 12.6 us
+        // against 15.2 for the LDS-ring kernel, 4096 x 14336 14.2 against 16.9; 2 or 4 workgroups
+        // per CU, 2 row phases for the 14336-long rows, or 2 rows in flight for the 4096-long rows
+        // measured 13 to 22 us)
         switch (nb) {
             case 64: return launch_digits<4, 4, 2, 2, 5>(s, blocks, N, rowbytes, x, y, 2);     // 8 rows, 17 KB
-            case 128: return launch_digits<4, 2, 4, 2, 9>(s, blocks, N, rowbytes, x, y, 2);    // 8 rows, 34 KB
+            case 128: return launch_direct<2, 2, 4>(s, blocks, N, rowbytes, x, y, 1);
             case 256: return launch_digits<4, 1, 4, 2, 9>(s, blocks, N, rowbytes, x, y, 2);    // 4 rows, 34 KB
-            case 448: return launch_digits<7, 1, 2, 3, 5>(s, blocks, N, rowbytes, x, y, 1);    // 2 rows, 30 KB
+            case 448: return launch_direct<7, 1, 2>(s, blocks, N, rowbytes, x, y, 1);
             case 512: return launch_digits<8, 1, 2, 2, 5>(s, blocks, N, rowbytes, x, y, 1);    // 2 rows, 34 KB
             default: break;
         }

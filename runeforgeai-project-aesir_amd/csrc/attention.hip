@@ -249,7 +249,7 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(AttnArgs a) {
 // ------------------------------------------------------------------ fast path (head_dim 64 / 128)
 //
 // Partial kernel, grid (split, kv_head, head_group). A workgroup owns GH query heads of one KV
-// head and a chunk of whole 64-position rounds (one round for S <= 64 * max_split). All K and V
+// head and every nsplit-th 64-position round of the view (one round for S <= 64 * max_split). All K and V
 // requests of a round are issued together before any of them is used, so a round costs one HBM
 // round trip:
 //   scores   thread t holds dims [16c, 16c + 16) (c = t % TPP) of K rows t / TPP (+ 256 / TPP)
@@ -313,10 +313,14 @@ __global__ __launch_bounds__(kAThreads * NG) void attn_fast_kernel(AttnArgs a) {
     const int split = blockIdx.x;
     const int64_t S = decode_seq_len(a);
     const int64_t chunk = split_chunk(S, a.max_split);
-    const int64_t p0 = (int64_t)split * chunk;
-    if (p0 >= S) return;  // idle workgroup
     const int nsplit = (int)((S + chunk - 1) / chunk);
-    const int64_t p1 = p0 + chunk < S ? p0 + chunk : S;
+    if (split >= nsplit) return;  // idle workgroup
+    // Split s takes the rounds s, s + nsplit, s + 2 nsplit, ... of the view (rounds dealt out, not
+    // a contiguous chunk): at each step the splits together read one contiguous stretch of rows,
+    // so the grid sweeps the cache front to back (KV 32768 at the Llama-3 shape: 31.7 -> 28.0 us
+    // per layer for the partials) and a split's partial still covers chunk positions at most.
+    const int64_t p0 = (int64_t)split * kRound;
+    const int64_t p1 = S;
     const int64_t head0 = (int64_t)g * G + (int64_t)hg * GH;  // first query head of this workgroup
 
     const int sp = tid / TPP, sc_c = tid % TPP;                  // score row / dim chunk
@@ -410,9 +414,10 @@ __global__ __launch_bounds__(kAThreads * NG) void attn_fast_kernel(AttnArgs a) {
     // Rounds with a successor request it before computing (unconditionally, so the compiler's wait
     // counts stay exact and the successor's loads overlap this round); the last round follows.
     if constexpr (NG == 1) {
+        const int64_t step = (int64_t)nsplit * kRound;
         int64_t t0 = p0;
-        for (; t0 + kRound < p1; t0 += kRound) {
-            load_round(t0 + kRound, kn, vn);
+        for (; t0 + step < p1; t0 += step) {
+            load_round(t0 + step, kn, vn);
             round(t0, kr, vr);
 #pragma unroll
             for (int i = 0; i < NSP; i++) {

@@ -1004,7 +1004,7 @@ struct QFXSrc {
 // after the tile requests).
 constexpr int kQfXRegs = 1;
 
-template <int T, int NW, int SP, bool NORM, class Epi>
+template <int T, int NW, int SP, int QD, bool NORM, class Epi>
 __global__ __launch_bounds__(NW * kWave) void gemv_qf_kernel(QFMat w, int64_t N, int64_t K, QFXSrc src,
                                                              const h16 *__restrict__ nw, float eps, Epi epi) {
     constexpr int NT = NW * kWave, XR = kQfXRegs;
@@ -1058,8 +1058,11 @@ __global__ __launch_bounds__(NW * kWave) void gemv_qf_kernel(QFMat w, int64_t N,
         }
     }
 
-    QTile<T> tl[2][SP];
+    // QD steps in flight: step st + QD - 1 is requested when step st starts (steps past the last
+    // re-read the last step's tiles, so every path issues the same loads)
+    QTile<T> tl[QD][SP];
     auto issue = [&](int st, QTile<T>(&buf)[SP]) {
+        st = st < steps ? st : steps - 1;
         const int pb = pb0 + (int)blockIdx.x + (st / R) * (int)gridDim.x, first = wave + NW * SP * (st % R);
 #pragma unroll
         for (int i = 0; i < SP; i++) {
@@ -1067,7 +1070,8 @@ __global__ __launch_bounds__(NW * kWave) void gemv_qf_kernel(QFMat w, int64_t N,
             buf[i] = qf_tile_load<T>(rs, pb * nseg + sg, lane, s1v, (pb * sbr + sg / 2) * 16 * es1);
         }
     };
-    issue(0, tl[0]);
+#pragma unroll
+    for (int j = 0; j + 1 < QD; j++) issue(j, tl[j]);
     // the epilogue operands of this wave's rows (ER rows at en(k)) of the current and next block
     const bool ewave = wave < 16 / ER;
     auto en = [&](int k) { return (int64_t)((int)blockIdx.x + k * (int)gridDim.x) * 16 + wave * ER; };
@@ -1135,11 +1139,11 @@ __global__ __launch_bounds__(NW * kWave) void gemv_qf_kernel(QFMat w, int64_t N,
     const QfRegs kr = QfRegs::make();
     f32x4 acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
     float *fin = nred + NW;  // the block's final row sums, each ER-row part written and read by its epilogue wave
-    // step st: request step st + 1 into nxt (PF), multiply the tiles of cur, and after a block's
+    // step st: request step st + QD - 1 into nxt, multiply the tiles of cur, and after a block's
     // last round reduce its row sums over the waves and run its epilogue
-    auto step = [&](auto pf, int st, const QTile<T>(&cur)[SP], QTile<T>(&nxt)[SP]) {
+    auto step = [&](int st, const QTile<T>(&cur)[SP], QTile<T>(&nxt)[SP]) {
         const int k = st / R, r = st % R;
-        if constexpr (decltype(pf)::value) issue(st + 1, nxt);
+        issue(st + QD - 1, nxt);
         const int first = wave + NW * SP * r;
 #pragma unroll
         for (int i = 0; i < SP; i++) {
@@ -1175,25 +1179,21 @@ __global__ __launch_bounds__(NW * kWave) void gemv_qf_kernel(QFMat w, int64_t N,
             }
         }
     };
-    // the last step requests nothing (no step follows it)
-    using Pf = std::true_type;
-    using NoPf = std::false_type;
-    int st = 0;
-    for (; st + 2 < steps; st += 2) {
-        step(Pf{}, st, tl[0], tl[1]);
-        step(Pf{}, st + 1, tl[1], tl[0]);
-    }
-    if (steps - st == 2) {
-        step(Pf{}, st, tl[0], tl[1]);
-        step(NoPf{}, st + 1, tl[1], tl[0]);
-    } else {
-        step(NoPf{}, st, tl[0], tl[1]);
+    // unrolled QD times so that every buffer keeps its registers
+    for (int base = 0; base < steps; base += QD) {
+#pragma unroll
+        for (int j = 0; j < QD; j++)
+            if (base + j < steps) step(base + j, tl[j], tl[(j + QD - 1) % QD]);
     }
 }
 
 // Waves, round length and workgroups (measured on MI355X over the Llama-3-8B shapes): 8 waves with
 // rounds of half the register budget's tiles; from 1024 blocks on, persistent workgroups (512,
 // or 1024 from 4096 blocks, i.e. 3.5 to 8 blocks each), otherwise one block per workgroup.
+// Steps (rounds of SP tiles) in flight per wave of the decode GEMV. Measured on MI355X
+// (Llama-3-8B shape decode, KV 2048): 2 steps beat 3 and 4 for every type (Q4_0 657 / 621 / 586
+// tok/s, Q4_K 617 / 582 / 551, Q6_K 520 / 496 / 479; gate/up 14.9 / 15.5 / 17.0 us for Q4_0).
+constexpr int kQfDepth = 2;
 struct QfShape {
     int nw, sp;
     int64_t grid;
@@ -1209,8 +1209,8 @@ static void gemv_qf_launch_t(hipStream_t s, const QFMat &w, int64_t N, int64_t K
     constexpr int RD = qf_round<T>();
     const QfShape sh = qf_shape((N + 15) / 16, RD);
     const size_t lds = (size_t)(2 * K) + ((size_t)sh.nw * (2 * 16 + 1) + 16) * sizeof(float);
-    hipLaunchKernelGGL((gemv_qf_kernel<T, 8, RD / 2, NORM, Epi>), dim3((unsigned)sh.grid), dim3(8 * kWave), lds, s, w, N, K,
-                       src, (const h16 *)nwt, eps, epi);
+    hipLaunchKernelGGL((gemv_qf_kernel<T, 8, RD / 2, kQfDepth, NORM, Epi>), dim3((unsigned)sh.grid), dim3(8 * kWave), lds, s,
+                       w, N, K, src, (const h16 *)nwt, eps, epi);
 }
 
 bool qf_gemv_ok(int64_t K) { return K > 0 && K % kSeg == 0 && K <= kQfGemvMaxK; }

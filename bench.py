@@ -266,8 +266,8 @@ def qf_token_bytes(kind: str) -> int:
 
 # llama.cpp's Q4_K_M / Q5_K_M recipes for a Llama: Q4_K (Q5_K) matrices, Q6_K for output and for
 # attn_v / ffn_down of the first and last eighth of the layers and every third layer between. A
-# layer whose V is Q6_K keeps its fused Q/K/V matrix in f16 (parts of one fused matrix share a
-# storage type).
+# layer whose V is Q6_K stores its Q/K/V matrix in two parts (Q and K in Q4_K / Q5_K, V in Q6_K)
+# that one two-part GEMV launch reads.
 MIXES = {"q4_k_m": "q4_k", "q5_k_m": "q5_k"}
 
 
@@ -291,11 +291,11 @@ def stored_mat_bytes(kind: str, rows: int, cols: int) -> int:
 
 
 def layer_storage(kind: str, l: int) -> tuple:
-    """Stored types of layer l's (qkv, o, gate/up, down) matrices."""
+    """Stored types of layer l's (q and k, v, o, gate/up, down) matrices."""
     if kind not in MIXES:
-        return (kind,) * 4
+        return (kind,) * 5
     base, more = MIXES[kind], q4_k_m_more_bits(l)
-    return ("f16" if more else base, base, base, "q6_k" if more else base)
+    return (base, "q6_k" if more else base, base, base, "q6_k" if more else base)
 
 
 def quant_token_bytes(kind: str) -> int:
@@ -304,8 +304,8 @@ def quant_token_bytes(kind: str) -> int:
     embd, out = (MIXES[kind], "q6_k") if kind in MIXES else (kind, kind)
     total = stored_mat_bytes(out, VOCAB, DIM) + 2 * DIM + stored_mat_bytes(embd, 1, DIM)
     for l in range(LAYERS):
-        qkv, o, gu, down = layer_storage(kind, l)
-        total += (stored_mat_bytes(qkv, DIM + 2 * KV_DIM, DIM) + stored_mat_bytes(o, DIM, DIM)
+        qk, v, o, gu, down = layer_storage(kind, l)
+        total += (stored_mat_bytes(qk, DIM + KV_DIM, DIM) + stored_mat_bytes(v, KV_DIM, DIM) + stored_mat_bytes(o, DIM, DIM)
                   + stored_mat_bytes(gu, 2 * FFN, DIM) + stored_mat_bytes(down, DIM, FFN) + 2 * 2 * DIM)
     return total
 
@@ -345,11 +345,11 @@ def quant_bench(A, kind: str, seed: int, kv: int, steps: int, warmup: int, kerne
     check = replay_check(m, kv, toks, use_graph)
     kt = m.kernel_times(kv, iters=kernel_iters)
     gu_ms = kt["gate_up_swiglu"]
-    gu_kind = layer_storage(kind, 0)[2]  # the same in every layer
+    gu_kind = layer_storage(kind, 0)[3]  # the same in every layer
     gu_bytes = stored_mat_bytes(gu_kind, 2 * FFN, DIM) + DIM * 2 + DIM * 2 + FFN * 2
     m.close()
     ctx.close()
-    dtype = (f"{MIXES[kind]} / q6_k weights (f16 Q/K/V where V is q6_k)" if kind in MIXES else f"{kind} weights")
+    dtype = (f"{MIXES[kind]} / q6_k weights (Q/K/V in two parts where V is q6_k)" if kind in MIXES else f"{kind} weights")
     return {"workload": f"llama3-8b-shape {kind} batch-1 greedy decode, kv {kv}", "value": round(tok_s, 2),
             "unit": "tok/s", "steps": steps, "ms_per_step": round(wall * 1e3 / steps, 4),
             "dtype": f"{dtype}, f16 activations, f32 accumulate",

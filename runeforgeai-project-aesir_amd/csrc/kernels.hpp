@@ -158,8 +158,13 @@ struct QkvArgs {
     const void *embd_scale; // layer 0 of a Q8_0 model: token_embd block scales (embd is then int8)
     QFMat wq;               // Q4_0 / Q4_K / Q6_K models: the QKV matrix (w and w_scale unused)
     QFMat eq;               // layer 0 of such a model: token_embd (embd unused)
+    int64_t qkv_split = 0;  // > 0: wq holds rows [0, qkv_split), wq_b the rest, in another type
+    QFMat wq_b;
 };
 int32_t launch_qkv_rope_kv(hipStream_t s, const QkvArgs &a);
+// True when a Q/K/V matrix can be stored as two parts of these repacked types (rows of type_a,
+// then rows of type_b) and run by one two-part GEMV launch.
+bool qf_qkv_pair_ok(int32_t type_a, int32_t type_b);
 
 // x[n] = f16(f16(W x_in)[n] + x[n]) (O projection and down projection with the residual add).
 // w_scale non-null: W is Q8_0 (int8 quants [N][K] + f16 scales [N][K/32]).

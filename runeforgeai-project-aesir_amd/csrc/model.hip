@@ -103,14 +103,19 @@ TensorPlace place_tensor(const aesir_model *m, const TensorRef &ref) {
         return p;
     };
     auto norm = [&](void *base) { return TensorPlace{1, d, base, d, true, 2, nullptr, 0}; };
+    // rows [r0, r0 + rows) of the Q/K/V matrix: in its second part from L->qkv_split on
+    auto qkv_part = [&](int64_t r0, int64_t rows, int32_t in_type) {
+        if (L->qkv_split > 0 && r0 >= L->qkv_split) return mat(rows, d, L->qkv_b, r0 - L->qkv_split, 1, in_type);
+        return mat(rows, d, L->qkv, r0, 1, in_type);
+    };
     switch (ref.kind) {
         case TensorKind::TokenEmbd: return mat(V, d, m->embd, 0, 1, m->types.embd);
         case TensorKind::OutputNorm: return norm(m->out_norm);
         case TensorKind::Output: return mat(V, d, m->out, 0, 1, m->types.out);
         case TensorKind::AttnNorm: return norm(L->attn_norm);
-        case TensorKind::AttnQ: return mat(d, d, L->qkv, 0, 1, T->q);
-        case TensorKind::AttnK: return mat(kvd, d, L->qkv, d, 1, T->k);
-        case TensorKind::AttnV: return mat(kvd, d, L->qkv, d + kvd, 1, T->v);
+        case TensorKind::AttnQ: return qkv_part(0, d, T->q);
+        case TensorKind::AttnK: return qkv_part(d, kvd, T->k);
+        case TensorKind::AttnV: return qkv_part(d + kvd, kvd, T->v);
         case TensorKind::AttnOut: return mat(d, d, L->o, 0, 1, T->o);
         case TensorKind::FfnNorm: return norm(L->ffn_norm);
         case TensorKind::FfnGate: return mat(f, d, L->gu, 0, 2, T->gate);  // gate i -> fused row 2i
@@ -258,7 +263,9 @@ int32_t model_upload(aesir_model *m, const TensorRef &ref, const void *host, int
 
 // The layer-0 QKV GEMV performs the embedding lookup when the table has the QKV matrix's type;
 // otherwise the decode step looks the row up first (embed_lookup).
-static bool embd_fused(const aesir_model *m) { return m->embd.type == m->layers[0].qkv.type; }
+static bool embd_fused(const aesir_model *m) {
+    return m->embd.type == m->layers[0].qkv.type && m->layers[0].qkv_split == 0;
+}
 
 static QkvArgs qkv_args(aesir_model *m, int64_t l) {
     const aesir_model_config &c = m->cfg;
@@ -271,6 +278,10 @@ static QkvArgs qkv_args(aesir_model *m, int64_t l) {
     if (qf_type(L.qkv.type)) {
         a.wq = wmat_qf(L.qkv);
         if (emb) a.eq = wmat_qf(m->embd);
+        if (L.qkv_split > 0) {
+            a.qkv_split = L.qkv_split;
+            a.wq_b = wmat_qf(L.qkv_b);
+        }
     }
     return a;
 }
@@ -574,7 +585,17 @@ int32_t model_create(aesir_ctx *ctx, const aesir_model_config *cfg, const Weight
         ModelLayer &L = m->layers[l];
         const LayerTypes &t = types.layers[l];
         take(d * 2, &L.attn_norm);
-        matrix(d + 2 * kvd, d, fused({t.q, t.k, t.v}), &L.qkv);
+        // Q/K/V in two repacked types split at a part boundary: two parts, one two-part GEMV
+        int64_t split = 0;
+        if (t.q == t.k && t.k != t.v && qf_type(t.q) && qf_type(t.v) && qf_qkv_pair_ok(t.q, t.v)) split = d + kvd;
+        if (t.q != t.k && t.k == t.v && qf_type(t.q) && qf_type(t.k) && qf_qkv_pair_ok(t.q, t.k)) split = d;
+        if (split > 0 && split % 16 == 0 && kvd % 16 == 0) {
+            matrix(split, d, t.q, &L.qkv);
+            matrix(d + 2 * kvd - split, d, t.v, &L.qkv_b);
+            L.qkv_split = split;
+        } else {
+            matrix(d + 2 * kvd, d, fused({t.q, t.k, t.v}), &L.qkv);
+        }
         matrix(d, d, fused({t.o}), &L.o);
         take(d * 2, &L.ffn_norm);
         matrix(2 * f, d, fused({t.gate, t.up}), &L.gu);

@@ -23,15 +23,20 @@ struct WMat {
 struct ModelLayer {
     void *attn_norm = nullptr;  // [dim]
     void *ffn_norm = nullptr;   // [dim]
-    WMat qkv;                   // [dim + 2 kvd][dim]
+    WMat qkv;                   // [dim + 2 kvd][dim], or rows [0, qkv_split) of it
+    WMat qkv_b;                 // qkv_split > 0: rows [qkv_split, dim + 2 kvd), in another repacked type
+    int64_t qkv_split = 0;
     WMat o;                     // [dim][dim]
     WMat gu;                    // [2 ffn][dim]
     WMat down;                  // [dim][ffn]
 };
 
-// GGML types of the model's matrices as the caller uploads them (one per GGUF tensor). A fused
-// matrix whose parts differ (Q, K, V; gate, up) is stored as f16, its parts dequantized at upload
-// to the f16 weights their own type defines, which are the values every path multiplies.
+// GGML types of the model's matrices as the caller uploads them (one per GGUF tensor). A Q/K/V
+// matrix whose parts split into two repacked types at a part boundary (Q and K in one type, V in
+// another, as the K-quant mixes lay it out; or Q in one, K and V in another) is stored as those
+// two parts. Any other fused matrix whose parts differ (Q, K, V; gate, up) is stored as f16, its
+// parts dequantized at upload to the f16 weights their own type defines, which are the values
+// every path multiplies.
 struct LayerTypes {
     int32_t q, k, v, o, gate, up, down;
 };

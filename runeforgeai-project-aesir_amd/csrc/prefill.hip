@@ -1103,10 +1103,19 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
         if (!xn_ready) AESIR_TRY(norm_rows(L.attn_norm));
         xn_ready = false;
         int64_t qkv_splits = 1;
-        if (mfma)
+        if (mfma && L.qkv_split > 0) {
+            // a two-part Q/K/V: both parts dequantized into the f16 scratch matrix, then the F16 GEMM
+            AESIR_TRY(launch_qf_dequant(s, wmat_qf(L.qkv), L.qkv_split, d, 1, nullptr, m->pf_wdeq, d));
+            AESIR_TRY(launch_qf_dequant(s, wmat_qf(L.qkv_b), qkv_n - L.qkv_split, d, 1, nullptr,
+                                        (h16 *)m->pf_wdeq + L.qkv_split * d, d));
+            AESIR_TRY(launch_mfma<kEpiStore>(s, Xn, n, d, m->pf_wdeq, qkv_n, QKV, qkv_n, m->pf_part, m->pf_part_floats,
+                                             "gemm_mfma_qkv", true, &qkv_splits));
+        } else if (mfma) {
             AESIR_TRY(prefill_gemm<kEpiStore>(m, s, L.qkv, Xn, n, d, qkv_n, QKV, qkv_n, "gemm_mfma_qkv", true, &qkv_splits));
-        else
+        } else {
+            if (L.qkv_split > 0) return fail(AESIR_ERR_UNSUPPORTED, "prefill: two-part Q/K/V needs the matrix-core GEMM");
             AESIR_TRY(launch_gemm_f16(m->ctx, Xn, n, d, L.qkv.w, qkv_n, QKV));
+        }
         if (qkv_splits > 1) {
             const dim3 qgrid((unsigned)n, (unsigned)((qkv_n / 2 + kPThreads - 1) / kPThreads));
 #define AESIR_RQP(SV)                                                                                           \

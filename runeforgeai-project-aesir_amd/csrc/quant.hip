@@ -1004,14 +1004,17 @@ struct QFXSrc {
 // after the tile requests).
 constexpr int kQfXRegs = 1;
 
+// The body of the decode GEMV for workgroup bid of nbid working on w's N rows; the epilogue sees
+// row r of w as output row rbase + r of Nall (a matrix may be the second part of a fused one).
 template <int T, int NW, int SP, int QD, bool NORM, class Epi>
-__global__ __launch_bounds__(NW * kWave) void gemv_qf_kernel(QFMat w, int64_t N, int64_t K, QFXSrc src,
-                                                             const h16 *__restrict__ nw, float eps, Epi epi) {
+__device__ __forceinline__ void gemv_qf_body(uint8_t *lds, const QFMat &w, int64_t N, int64_t K, const QFXSrc &src,
+                                             const h16 *__restrict__ nw, float eps, const Epi &epi, int bid, int nbid,
+                                             int64_t rbase, int64_t Nall) {
     constexpr int NT = NW * kWave, XR = kQfXRegs;
     // the lm_head keeps one argmax partial per 8 logits: its epilogue runs per 8 rows
     constexpr int ER = std::is_same<Epi, EpiLmHead>::value ? 8 : 16;
     static_assert(NW >= 16 / ER, "one epilogue wave per row group");
-    extern __shared__ __align__(16) uint8_t lds[];  // x (2 K bytes), the row partials (2 x NW x 16), the norm scratch
+    // lds: x (2 K bytes), the row partials (2 x NW x 16), the norm scratch
     float *red = reinterpret_cast<float *>(lds + 2 * K);
     float *nred = red + 2 * NW * 16;  // NW floats, then 16 for the final row sums
     const int tid = threadIdx.x, lane = tid & 63;
@@ -1025,14 +1028,14 @@ __global__ __launch_bounds__(NW * kWave) void gemv_qf_kernel(QFMat w, int64_t N,
     const int s1v = (lane & 15) * es1;
     // steps of this workgroup: (block k, round r), r < R, for its nb blocks
     const int R = (nseg + NW * SP - 1) / (NW * SP);
-    const int nb = (blocks - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int nb = (blocks - bid + nbid - 1) / nbid;
     const int steps = nb * R;
     if (nb <= 0) return;  // a grid larger than the blocks (never launched so)
 
     // x: record r of x itself, or of row token->token of the embedding table (dequantized)
     const bool embed = src.emb.nib != nullptr;
     const int64_t erow = embed ? src.emb.row0 + src.token->token : 0;
-    h16 *xcopy = (src.xcopy && blockIdx.x == 0) ? src.xcopy : nullptr;
+    h16 *xcopy = (src.xcopy && bid == 0) ? src.xcopy : nullptr;
     auto getx = [&](int r, u32x4(&x)[2]) {
         if (embed) {
             qf_deq16<T>(qf_load<T>(src.emb, erow, r, K), x);
@@ -1063,7 +1066,7 @@ __global__ __launch_bounds__(NW * kWave) void gemv_qf_kernel(QFMat w, int64_t N,
     QTile<T> tl[QD][SP];
     auto issue = [&](int st, QTile<T>(&buf)[SP]) {
         st = st < steps ? st : steps - 1;
-        const int pb = pb0 + (int)blockIdx.x + (st / R) * (int)gridDim.x, first = wave + NW * SP * (st % R);
+        const int pb = pb0 + bid + (st / R) * nbid, first = wave + NW * SP * (st % R);
 #pragma unroll
         for (int i = 0; i < SP; i++) {
             const int sg = first + NW * i < nseg ? first + NW * i : nseg - 1;  // a surplus slot: the last segment
@@ -1074,9 +1077,9 @@ __global__ __launch_bounds__(NW * kWave) void gemv_qf_kernel(QFMat w, int64_t N,
     for (int j = 0; j + 1 < QD; j++) issue(j, tl[j]);
     // the epilogue operands of this wave's rows (ER rows at en(k)) of the current and next block
     const bool ewave = wave < 16 / ER;
-    auto en = [&](int k) { return (int64_t)((int)blockIdx.x + k * (int)gridDim.x) * 16 + wave * ER; };
-    using Pre = decltype(epi.template prefetch<ER>(0, 0, N, 0));
-    Pre pre = epi.template prefetch<ER>(en(0), 0, N, ewave ? lane : kWave);
+    auto en = [&](int k) { return rbase + (int64_t)(bid + k * nbid) * 16 + wave * ER; };
+    using Pre = decltype(epi.template prefetch<ER>(0, 0, Nall, 0));
+    Pre pre = epi.template prefetch<ER>(en(0), 0, Nall, ewave ? lane : kWave);
 
     // stage x: record r at lds + 32 r in the B-operand order, RMS-normalized when NORM
     h16 inv = (h16)1.0f;
@@ -1167,7 +1170,7 @@ __global__ __launch_bounds__(NW * kWave) void gemv_qf_kernel(QFMat w, int64_t N,
             acc[0] = acc[1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
             __syncthreads();
             const Pre now = pre;
-            if (k + 1 < nb) pre = epi.template prefetch<ER>(en(k + 1), 0, N, ewave ? lane : kWave);
+            if (k + 1 < nb) pre = epi.template prefetch<ER>(en(k + 1), 0, Nall, ewave ? lane : kWave);
             if (ewave) {
                 if (lane < ER) {  // lane: row wave * ER + lane, summed over the waves in one order
                     float v = rb[wave * ER + lane];
@@ -1175,7 +1178,7 @@ __global__ __launch_bounds__(NW * kWave) void gemv_qf_kernel(QFMat w, int64_t N,
                     for (int w2 = 1; w2 < NW; w2++) v += rb[w2 * 16 + wave * ER + lane];
                     fin[wave * ER + lane] = v;
                 }
-                epi.template apply<ER>(en(k), 0, N, fin + wave * ER, lane, now);
+                epi.template apply<ER>(en(k), 0, Nall, fin + wave * ER, lane, now);
             }
         }
     };
@@ -1185,6 +1188,29 @@ __global__ __launch_bounds__(NW * kWave) void gemv_qf_kernel(QFMat w, int64_t N,
         for (int j = 0; j < QD; j++)
             if (base + j < steps) step(base + j, tl[j], tl[(j + QD - 1) % QD]);
     }
+}
+
+template <int T, int NW, int SP, int QD, bool NORM, class Epi>
+__global__ __launch_bounds__(NW * kWave) void gemv_qf_kernel(QFMat w, int64_t N, int64_t K, QFXSrc src,
+                                                             const h16 *__restrict__ nw, float eps, Epi epi) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    gemv_qf_body<T, NW, SP, QD, NORM, Epi>(lds, w, N, K, src, nw, eps, epi, (int)blockIdx.x, (int)gridDim.x, 0, N);
+}
+
+// One launch over a fused matrix stored in two parts of different types (a mixed Q/K/V): the
+// first ga workgroups run part A's na rows (type TA), the others part B's nb rows (type TB) as
+// output rows na .. na + nb - 1. Each workgroup keeps one type for its life, so the branch is
+// uniform and both parts stream at once without a second launch's fixed cost.
+template <int TA, int TB, int NW, int SPA, int SPB, int QD, bool NORM, class Epi>
+__global__ __launch_bounds__(NW * kWave) void gemv_qf2_kernel(QFMat wa, int64_t na, int ga, QFMat wb, int64_t nb,
+                                                              int64_t K, QFXSrc src, const h16 *__restrict__ nw,
+                                                              float eps, Epi epi) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    if ((int)blockIdx.x < ga)
+        gemv_qf_body<TA, NW, SPA, QD, NORM, Epi>(lds, wa, na, K, src, nw, eps, epi, (int)blockIdx.x, ga, 0, na + nb);
+    else
+        gemv_qf_body<TB, NW, SPB, QD, NORM, Epi>(lds, wb, nb, K, src, nw, eps, epi, (int)blockIdx.x - ga,
+                                                 (int)gridDim.x - ga, na, na + nb);
 }
 
 // Waves, round length and workgroups (measured on MI355X over the Llama-3-8B shapes): 8 waves with
@@ -1257,10 +1283,60 @@ int32_t launch_qf_gate_up_swiglu(hipStream_t s, const void *x, const void *norm_
                                   "gemv_qf_gate_up");
 }
 
+// Type pairs of a Q/K/V matrix stored in two parts (rows [0, split) of type A, the rest of type B),
+// as the K-quant mixes lay out attn_q / attn_k and attn_v (a higher-bit V, or a higher-bit K and V).
+template <class F>
+static bool qf_pair_switch(int32_t ta, int32_t tb, F &&f) {
+#define AESIR_QF_PAIR(A, B)                                                                          \
+    if (ta == A && tb == B) {                                                                        \
+        f(std::integral_constant<int, A>{}, std::integral_constant<int, B>{});                       \
+        return true;                                                                                 \
+    }
+    AESIR_QF_PAIR(AESIR_GGML_Q4_K, AESIR_GGML_Q6_K)
+    AESIR_QF_PAIR(AESIR_GGML_Q5_K, AESIR_GGML_Q6_K)
+    AESIR_QF_PAIR(AESIR_GGML_Q4_K, AESIR_GGML_Q5_K)
+    AESIR_QF_PAIR(AESIR_GGML_Q3_K, AESIR_GGML_Q4_K)
+    AESIR_QF_PAIR(AESIR_GGML_Q3_K, AESIR_GGML_Q5_K)
+    AESIR_QF_PAIR(AESIR_GGML_Q2_K, AESIR_GGML_Q4_K)
+#undef AESIR_QF_PAIR
+    return false;
+}
+
+bool qf_qkv_pair_ok(int32_t type_a, int32_t type_b) {
+    return qf_pair_switch(type_a, type_b, [](auto, auto) {});
+}
+
 int32_t launch_qf_qkv_rope_kv(hipStream_t s, const QkvArgs &a, const EpiQkv &e) {
     const QFXSrc src = a.eq.nib ? QFXSrc{nullptr, a.eq, a.state, (h16 *)a.x}
                                 : QFXSrc{(const h16 *)a.x, QFMat{}, nullptr, nullptr};
-    return gemv_qf_dispatch<true>(s, a.wq, a.dim + 2 * a.kvd, a.dim, src, a.norm_w, a.eps, e, "gemv_qf_qkv_rope_kv");
+    const int64_t N = a.dim + 2 * a.kvd, K = a.dim;
+    if (a.qkv_split <= 0)
+        return gemv_qf_dispatch<true>(s, a.wq, N, K, src, a.norm_w, a.eps, e, "gemv_qf_qkv_rope_kv");
+    // two parts: one launch, each workgroup on one part (the embedding lookup runs apart)
+    const char *name = "gemv_qf2_qkv_rope_kv";
+    const int64_t na = a.qkv_split, nb = N - na;
+    if (na % 16 != 0 || nb <= 0 || a.eq.nib) return fail(AESIR_ERR_INVALID, "%s: bad part split", name);
+    AESIR_TRY(qf_check(a.wq.type, K, name));
+    AESIR_TRY(qf_check(a.wq_b.type, K, name));
+    if (!qf_gemv_ok(K)) return fail(AESIR_ERR_UNSUPPORTED, "%s: row length %lld", name, (long long)K);
+    if (((uintptr_t)a.wq.nib & 15) || ((uintptr_t)a.wq_b.nib & 15) || ((uintptr_t)a.x & 15) || ((uintptr_t)a.norm_w & 15))
+        return fail(AESIR_ERR_UNSUPPORTED, "%s: quantized GEMV needs 16-byte aligned operands", name);
+    bool launched = false;
+    qf_pair_switch(a.wq.type, a.wq_b.type, [&](auto ta, auto tb) {
+        constexpr int TA = decltype(ta)::value, TB = decltype(tb)::value;
+        constexpr int RA = qf_round<TA>(), RB = qf_round<TB>();
+        const QfShape sa = qf_shape((na + 15) / 16, RA), sb = qf_shape((nb + 15) / 16, RB);
+        const size_t lds = (size_t)(2 * K) + ((size_t)8 * (2 * 16 + 1) + 16) * sizeof(float);
+        hipLaunchKernelGGL((gemv_qf2_kernel<TA, TB, 8, RA / 2, RB / 2, kQfDepth, true, EpiQkv>),
+                           dim3((unsigned)(sa.grid + sb.grid)), dim3(8 * kWave), lds, s, a.wq, na, (int)sa.grid, a.wq_b, nb,
+                           K, src, (const h16 *)a.norm_w, a.eps, e);
+        launched = true;
+    });
+    if (!launched)
+        return fail(AESIR_ERR_UNSUPPORTED, "%s: no two-part GEMV for types %s and %s", name, ggml_type_name(a.wq.type),
+                    ggml_type_name(a.wq_b.type));
+    AESIR_LAUNCH_CHECK(name);
+    return AESIR_OK;
 }
 
 int32_t launch_qf_lm_head(hipStream_t s, const LmHeadArgs &a, const EpiLmHead &e) {

@@ -155,6 +155,22 @@ __device__ __forceinline__ float group_max(float v) {
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<kWave>(v); }
 __device__ __forceinline__ float wave_max(float v) { return group_max<kWave>(v); }
 
+// Minimum of an int over the wave (the same halving steps as group_max); every lane gets it.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
+}
+__device__ __forceinline__ int wave_min_i(int v) {
+    v = min(v, dpp_i<kDppXor1>(v));
+    v = min(v, dpp_i<kDppXor2>(v));
+    v = min(v, dpp_i<kDppHalfMirror>(v));
+    v = min(v, dpp_i<kDppMirror>(v));
+    const auto r16 = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+    v = min((int)r16[0], (int)r16[1]);
+    const auto r32 = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+    return min((int)r32[0], (int)r32[1]);
+}
+
 // Reduces R per-lane partial sums across the wave by recursive halving: after the call, every
 // lane holds the full wave sum of row (lane / (64 / R)) in v[0]. R is a power of two <= 64.
 // Halving steps pair lanes 32 apart, then 16, 8 (15 - x), 4 (7 - x), 2, 1; at each step the

@@ -259,36 +259,50 @@ __global__ __launch_bounds__(kThreads) void gemv_fixed_kernel(const h16 *__restr
 
 // Final argmax over ordered partials (one workgroup). Writes *result and/or the decode state:
 // next_token, and in autoregressive mode token <- next, pos += 1, step += 1, ring[step] = next.
+// Partial g is the first maximum of an index range below partial g + 1's, so the answer is the
+// smallest index among the partials holding the largest value, whatever order they are visited
+// in: thread t keeps the first maximum of partials t, t + 1024, ... (coalesced loads, 16 in
+// flight), then the workgroup takes the largest value and the smallest index holding it (one wave
+// reduction and one LDS exchange each, two barriers in all).
 constexpr int kFinishThreads = 1024;
+constexpr int kFinishWaves = kFinishThreads / kWave;
+constexpr int kFinishBatch = 16;
 __global__ __launch_bounds__(kFinishThreads) void argmax_finish_kernel(const ArgPart *__restrict__ parts,
                                                                         int64_t count, DecodeState *state,
                                                                         int64_t *ring, int64_t *result) {
-    __shared__ ArgPart tree[kFinishThreads];
-    const int tid = threadIdx.x;
-    const int64_t per = (count + kFinishThreads - 1) / kFinishThreads;
-    ArgPart cur{-INFINITY, -1};
-    const int64_t g0 = (int64_t)tid * per, g1 = g0 + per < count ? g0 + per : count;
-    int64_t g = g0;
-    for (; g + 16 <= g1; g += 16) {  // 16 independent loads in flight, combined in order
-        ArgPart v[16];
+    __shared__ float wmax[kFinishWaves];
+    __shared__ int32_t widx[kFinishWaves];
+    const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+    float cv = -INFINITY;
+    int32_t ci = INT32_MAX;
+    for (int64_t g0 = tid; g0 < count; g0 += (int64_t)kFinishBatch * kFinishThreads) {
+        ArgPart v[kFinishBatch];
 #pragma unroll
-        for (int j = 0; j < 16; j++) v[j] = parts[g + j];
+        for (int j = 0; j < kFinishBatch; j++) {
+            const int64_t g = g0 + (int64_t)j * kFinishThreads;
+            v[j] = g < count ? parts[g] : ArgPart{-INFINITY, -1};
+        }
 #pragma unroll
-        for (int j = 0; j < 16; j++) cur = arg_combine(cur, v[j]);
+        for (int j = 0; j < kFinishBatch; j++)
+            if (v[j].v > cv) {  // ascending partials: strict '>' keeps the first maximum
+                cv = v[j].v;
+                ci = v[j].i;
+            }
     }
-    for (; g < g1; g++) cur = arg_combine(cur, parts[g]);
-    tree[tid] = cur;
+    const float wm = wave_max(cv);
+    if (lane == 0) wmax[wave] = wm;
     __syncthreads();
-    for (int st = 1; st < kFinishThreads; st <<= 1) {
-        ArgPart a = tree[tid];
-        if ((tid & (2 * st - 1)) == 0 && tid + st < kFinishThreads) a = arg_combine(a, tree[tid + st]);
-        __syncthreads();
-        tree[tid] = a;
-        __syncthreads();
-    }
+    float vmax = wmax[0];
+#pragma unroll
+    for (int w = 1; w < kFinishWaves; w++) vmax = fmaxf(vmax, wmax[w]);
+    const int32_t wi = wave_min_i(cv == vmax ? ci : INT32_MAX);
+    if (lane == 0) widx[wave] = wi;
+    __syncthreads();
     if (tid != 0) return;
-    const ArgPart best = tree[0];
-    const int64_t idx = (best.v > kArgmaxFloor && best.i >= 0) ? (int64_t)best.i : 0;
+    int32_t bi = widx[0];
+#pragma unroll
+    for (int w = 1; w < kFinishWaves; w++) bi = min(bi, widx[w]);
+    const int64_t idx = (vmax > kArgmaxFloor && bi != INT32_MAX && bi >= 0) ? (int64_t)bi : 0;
     if (result) *result = idx;
     if (state) {
         state->next_token = idx;

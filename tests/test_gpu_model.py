@@ -205,6 +205,33 @@ def test_tinyllama_shape_two_layers(A, ctx, oracle):
     m.close()
 
 
+@pytest.mark.parametrize("ties", [(70000, 131080, 139999), (131080, 139999), (5, 6)])
+def test_lm_head_argmax_ties_past_one_pass(A, ctx, oracle, ties):
+    """A 140000-entry vocabulary gives the lm_head 17500 ordered partials, more than the finishing
+    workgroup takes in one pass (16384). The top output row copied to the planted indices (and
+    zeroed where it was) makes exact ties there: the token is the lowest of them
+    (inference.mojo:508-515), the oracle's argmax of the same logits, graph replay included."""
+    cfg = oracle.Config(dim=64, n_layers=1, n_heads=4, n_kv_heads=4, ffn=64, vocab=140000, ctx_len=16)
+    w = oracle.synthetic_weights(cfg, SEED)
+    m = gpu_model(A, ctx, cfg, w)
+    first = m.forward_pass([3], 0)
+    assert first == oracle.argmax_f16(m.logits())
+    m.close()
+    out = w["output.weight"]
+    top = out[first].copy()
+    out[first] = 0
+    for t in ties:
+        out[t] = top
+    m = gpu_model(A, ctx, cfg, w)
+    got = m.forward_pass([3], 0)
+    lg = m.logits()
+    assert len({float(lg[t]) for t in ties}) == 1 and float(lg[ties[0]]) > 0
+    assert got == oracle.argmax_f16(lg) == min(ties)
+    g, _ = m.decode_loop(3, 0, 2, use_graph=True)
+    assert g[0] == got
+    m.close()
+
+
 @pytest.mark.timeout(300)
 @pytest.mark.parametrize("shape", ["tinyllama", "llama3"])
 def test_long_prompt_decode_shapes(A, ctx, oracle, shape):

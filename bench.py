@@ -298,15 +298,26 @@ def layer_storage(kind: str, l: int) -> tuple:
     return (base, "q6_k" if more else base, base, base, "q6_k" if more else base)
 
 
-def quant_token_bytes(kind: str) -> int:
-    """Algorithmic weight bytes of one decode token as stored: every matrix once, norms, one
-    embedding row."""
+# GGML block (weights, bytes) of each type as a GGUF file holds it (ggml's block_q*_K layouts).
+GGUF_BLOCKS = {"f16": (1, 2), "q8_0": (32, 34), "q4_0": (32, 18), "q4_1": (32, 20), "q5_0": (32, 22),
+               "q5_1": (32, 24), "q2_k": (256, 84), "q3_k": (256, 110), "q4_k": (256, 144),
+               "q5_k": (256, 176), "q6_k": (256, 210)}
+
+
+def gguf_mat_bytes(kind: str, rows: int, cols: int) -> int:
+    n, b = GGUF_BLOCKS[kind]
+    return rows * (cols // n) * b
+
+
+def quant_token_bytes(kind: str, mat_bytes=stored_mat_bytes) -> int:
+    """Algorithmic weight bytes of one decode token as stored (or, with gguf_mat_bytes, as the
+    GGUF file holds them): every matrix once, norms, one embedding row."""
     embd, out = (MIXES[kind], "q6_k") if kind in MIXES else (kind, kind)
-    total = stored_mat_bytes(out, VOCAB, DIM) + 2 * DIM + stored_mat_bytes(embd, 1, DIM)
+    total = mat_bytes(out, VOCAB, DIM) + 2 * DIM + mat_bytes(embd, 1, DIM)
     for l in range(LAYERS):
         qk, v, o, gu, down = layer_storage(kind, l)
-        total += (stored_mat_bytes(qk, DIM + KV_DIM, DIM) + stored_mat_bytes(v, KV_DIM, DIM) + stored_mat_bytes(o, DIM, DIM)
-                  + stored_mat_bytes(gu, 2 * FFN, DIM) + stored_mat_bytes(down, DIM, FFN) + 2 * 2 * DIM)
+        total += (mat_bytes(qk, DIM + KV_DIM, DIM) + mat_bytes(v, KV_DIM, DIM) + mat_bytes(o, DIM, DIM)
+                  + mat_bytes(gu, 2 * FFN, DIM) + mat_bytes(down, DIM, FFN) + 2 * 2 * DIM)
     return total
 
 
@@ -342,6 +353,8 @@ def quant_bench(A, kind: str, seed: int, kv: int, steps: int, warmup: int, kerne
     tok_s = steps / wall
     mean_kv = kv + (steps - 1) / 2.0 + 1
     step_bytes = quant_token_bytes(kind) + KV_BYTES_PER_POS * mean_kv + KV_BYTES_PER_POS
+    # the same token with every matrix at its GGUF size (Q2_K / Q3_K are stored wider, as 4-bit planes)
+    gguf_bytes = quant_token_bytes(kind, gguf_mat_bytes) + KV_BYTES_PER_POS * mean_kv + KV_BYTES_PER_POS
     check = replay_check(m, kv, toks, use_graph)
     kt = m.kernel_times(kv, iters=kernel_iters)
     gu_ms = kt["gate_up_swiglu"]
@@ -356,6 +369,8 @@ def quant_bench(A, kind: str, seed: int, kv: int, steps: int, warmup: int, kerne
             "step_hbm": {"bytes_per_token": int(step_bytes), "achieved_gbs": round(step_bytes * tok_s / 1e9, 1),
                          "frac": round(step_bytes * tok_s / 1e9 / HBM_PEAK_GBS, 4),
                          "event_ms_per_step": round(event_ms / steps, 4)},
+            "step_hbm_gguf": {"bytes_per_token": int(gguf_bytes),
+                              "frac": round(gguf_bytes * tok_s / 1e9 / HBM_PEAK_GBS, 4)},
             "gate_up_swiglu": {"avg_launch_ms": round(gu_ms, 5), "bytes_per_launch": gu_bytes,
                                "achieved_gbs": round(gu_bytes / (gu_ms * 1e-3) / 1e9, 1),
                                "frac": round(gu_bytes / (gu_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
@@ -406,7 +421,8 @@ def kv_sweep_bench(seed: int, steps: int, warmup: int, kvs=(512, 8192, 32768)) -
         d = json.loads(r.stdout.strip().splitlines()[-1])
         h = d["step_hbm"]
         out[f"kv{kv}"] = {"tok_s": d["value"], "ms_per_step": d["ms_per_step"], "bytes_per_token": h["bytes_per_token"],
-                          "achieved_gbs": h["achieved_gbs"], "frac": h["frac"]}
+                          "achieved_gbs": h["achieved_gbs"], "frac": h["frac"],
+                          "attention_us": round(d["kernel_ms"]["attention"] * 1e3, 2)}
     return out
 
 
@@ -530,6 +546,9 @@ def main():
     ap.add_argument("--cpu-reps", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="launch kernels one by one instead of graph replay")
+    ap.add_argument("--no-replay-check", action="store_true",
+                    help="skip re-running the timed steps in the other launch mode (for profiler runs that "
+                         "trace eager launches only)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the TinyLlama batched-prefill measurement")
     ap.add_argument("--prefill-only", action="store_true", help="run only the TinyLlama prefill measurement")
     ap.add_argument("--prefill-type", default="f16",
@@ -596,7 +615,7 @@ def main():
     mean_kv = args.kv + (args.steps - 1) / 2.0 + 1
     step_bytes = TOKEN_WEIGHT_BYTES + KV_BYTES_PER_POS * mean_kv + KV_BYTES_PER_POS
 
-    check = replay_check(m, args.kv, toks, use_graph)
+    check = None if args.no_replay_check else replay_check(m, args.kv, toks, use_graph)
     kt = m.kernel_times(args.kv, iters=args.kernel_iters)
     gu_ms = kt["gate_up_swiglu"]
     gu_gbs = GATE_UP_BYTES / (gu_ms * 1e-3) / 1e9

@@ -242,9 +242,9 @@ QF_TYPES = {"q4_0": 2, "q4_1": 3, "q5_0": 6, "q5_1": 7, "q2_k": 10, "q3_k": 11, 
 
 
 def qf_mat_bytes(kind: str, rows: int, cols: int) -> int:
-    per_row = cols // 2
-    if kind in ("q5_0", "q5_1", "q5_k"):
-        per_row += cols // 8  # fifth bits
+    per_row = cols // 4 if kind in ("q2_k", "q3_k") else cols // 2  # crumb or nibble plane
+    if kind in ("q5_0", "q5_1", "q5_k", "q3_k"):
+        per_row += cols // 8  # fifth (Q3_K: third) bits
     if kind in ("q4_0", "q5_0", "q4_k", "q5_k"):
         per_row += cols // 32 * 2  # f16 d, or the (scale, min) bytes
     if kind in ("q4_1", "q5_1"):

@@ -296,7 +296,8 @@ int32_t aesir_model_create(aesir_ctx *ctx, const aesir_model_config *cfg, aesir_
  * w = f16(f16(q) * d), gemm_q8_0's rule (core/compute.mojo:1062-1063), so a Q8_0 model computes
  * what the F16 model holding the dequantized weights computes. A model of any other block type
  * keeps each matrix repacked into 16-weight records in 16-row x 128-weight tiles (nibble plane,
- * per-block scale planes, a fifth-bit or high-bit plane; Q2_K / Q3_K values in the nibbles); dim
+ * per-block scale planes, a fifth-bit or high-bit plane; Q2_K / Q3_K at GGUF's bit width: a 2-bit
+ * crumb plane, plus Q3_K's third-bit plane); dim
  * and ffn must be multiples of 128 (32-weight blocks) or 256 (K-quants), at most 28672. Every type's
  * weights are the f16 values of aesir_gemm_quant's rules, so a model of any type computes what
  * the F16 model holding its read-back weights computes. Norm vectors stay f16. No reference

@@ -53,6 +53,11 @@ struct QFMat {
     const void *nib = nullptr, *hb = nullptr, *s0 = nullptr, *s1 = nullptr;
     int64_t row0 = 0;
 };
+// Bytes per lane (record pair) of a tile's quant plane: 16 nibble bytes, or for Q2_K the two
+// records' 2-bit crumb words (8), for Q3_K those plus the pair's third-bit word (12).
+__host__ __device__ constexpr int qf_lane_bytes(int32_t type) {
+    return type == AESIR_GGML_Q2_K ? 8 : type == AESIR_GGML_Q3_K ? 12 : 16;
+}
 // hb bytes per record pair (0 without the plane) and s0 bytes per record pair.
 __host__ __device__ inline int qf_hb_bytes(int32_t type) {
     return type == AESIR_GGML_Q6_K ? 8
@@ -65,7 +70,7 @@ __host__ __device__ inline int qf_s0_bytes(int32_t type) {
 // Bytes of one row of each plane (0 if the type has no such plane). plane: 0 nib, 1 hb, 2 s0, 3 s1.
 __host__ __device__ inline int64_t qf_plane_row_bytes(int32_t type, int plane, int64_t K) {
     switch (plane) {
-        case 0: return K / 2;
+        case 0: return K / 32 * qf_lane_bytes(type);
         case 1: return K / 32 * qf_hb_bytes(type);
         case 2: return K / 32 * qf_s0_bytes(type);
         case 3:
@@ -79,8 +84,13 @@ __host__ __device__ inline int64_t qf_plane_row_bytes(int32_t type, int plane, i
 __host__ __device__ inline int64_t qf_rows_alloc(int64_t N) { return (N + 15) / 16 * 16; }
 // Tile of (plane row r, record rec) and the byte offsets of the record's planes.
 __host__ __device__ inline int64_t qf_tile(int64_t r, int64_t rec, int64_t K) { return (r >> 4) * (K >> 7) + (rec >> 3); }
+// The quant-plane bytes of the record's pair: lane l of a wave reading lb bytes at lb l gets the
+// pair of records 2 (l / 16), + 1 of row l % 16 in the tile (lb = qf_lane_bytes).
+__host__ __device__ inline int64_t qf_qlane_off(int64_t r, int64_t rec, int64_t K, int lb) {
+    return qf_tile(r, rec, K) * 64 * lb + (((rec & 7) >> 1) * 16 + (r & 15)) * lb;
+}
 __host__ __device__ inline int64_t qf_nib_off(int64_t r, int64_t rec, int64_t K) {
-    return qf_tile(r, rec, K) * 1024 + ((rec & 7) >> 1) * 256 + (r & 15) * 16 + (rec & 1) * 8;
+    return qf_qlane_off(r, rec, K, 16) + (rec & 1) * 8;
 }
 // hb entry of the record's pair (es = qf_hb_bytes); Q6_K's word of the record is at + 4 (rec & 1)
 __host__ __device__ inline int64_t qf_hb_pair_off(int64_t r, int64_t rec, int64_t K, int es) {

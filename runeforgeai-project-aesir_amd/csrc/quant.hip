@@ -1,7 +1,9 @@
 // 2- to 6-bit weights on gfx950: GGML Q4_0, Q4_1, Q5_0 and Q5_1 (with the reference's
 // gemm_q4_0 / _q4_1 / _q5_0 / _q5_1 rounding, core/compute.mojo:876-1036) and GGML's Q2_K / Q3_K /
-// Q4_K / Q5_K / Q6_K super-blocks. Q2_K and Q3_K values are kept in the nibble plane (0..3 and the
-// 3-bit q + 4), trading 0.17 / 0.06 bytes per weight over GGUF's packing for the 4-bit GEMV.
+// Q4_K / Q5_K / Q6_K super-blocks. Q2_K and Q3_K keep GGUF's bit width: the low 2 bits of each
+// weight as crumbs (4 bytes per record) and, for Q3_K, the third bits in a word per record pair,
+// next to the crumbs in the quant plane; a lane spreads them into the nibble words the 4-bit
+// dequantization takes.
 //
 // GGUF stores these as packed blocks of 18 to 210 bytes whose nibble order suits a CPU
 // loop, not a wave: the bytes of one block are read by one lane, and 210 is not even 4-byte
@@ -62,6 +64,28 @@ constexpr bool qf_dm() {
 template <int T>
 constexpr bool qf_kq() {
     return T == AESIR_GGML_Q4_K || T == AESIR_GGML_Q5_K;
+}
+template <int T>
+constexpr bool qf_crumb() {
+    return T == AESIR_GGML_Q2_K || T == AESIR_GGML_Q3_K;
+}
+
+// Crumb records (Q2_K, Q3_K). Nibble i of a record's crumb word holds the low 2 bits of nibble i
+// of its two nibble words (bits 0-1: word 0, bits 2-3: word 1), so each word is one shift and mask
+// away. The Q3_K third bits of a record pair share one word: nibble i holds them for nibble i of
+// the odd record's words 0 and 1 (bits 0, 1) and the even record's (bits 2, 3); shifting the word
+// left by 2 for the odd record puts its bits where the even record's are.
+constexpr unsigned kCrumbMask = 0x33333333u, kThirdMask = 0x44444444u;
+__host__ __device__ __forceinline__ unsigned crumb_word(unsigned w0, unsigned w1) {
+    return (w0 & kCrumbMask) | ((w1 & kCrumbMask) << 2);
+}
+__host__ __device__ __forceinline__ unsigned third_bits(unsigned w0, unsigned w1, int odd) {
+    return odd ? ((w0 & kThirdMask) >> 2) | ((w1 & kThirdMask) >> 1) : (w0 & kThirdMask) | ((w1 & kThirdMask) << 1);
+}
+// Nibble words of a crumb record; h: the pair's third-bit word shifted to the even record's
+// positions (0 for Q2_K).
+__device__ __forceinline__ u32x2 crumb_nibbles(unsigned c, unsigned h) {
+    return u32x2{(c & kCrumbMask) | (h & kThirdMask), ((c >> 2) & kCrumbMask) | ((h >> 1) & kThirdMask)};
 }
 
 
@@ -159,7 +183,15 @@ struct QRec<AESIR_GGML_Q3_K> {
 template <int T>
 __device__ __forceinline__ QRec<T> qf_load(const QFMat &w, int64_t prow, int64_t rec, int64_t K) {
     QRec<T> q;
-    q.nib = *reinterpret_cast<const u32x2 *>((const uint8_t *)w.nib + qf_nib_off(prow, rec, K));
+    if constexpr (qf_crumb<T>()) {
+        const uint8_t *pr = (const uint8_t *)w.nib + qf_qlane_off(prow, rec, K, qf_lane_bytes(T));
+        const unsigned c = *reinterpret_cast<const uint32_t *>(pr + 4 * (rec & 1));
+        unsigned h = 0u;
+        if constexpr (T == AESIR_GGML_Q3_K) h = *reinterpret_cast<const uint32_t *>(pr + 8) << (2 * (rec & 1));
+        q.nib = crumb_nibbles(c, h);
+    } else {
+        q.nib = *reinterpret_cast<const u32x2 *>((const uint8_t *)w.nib + qf_nib_off(prow, rec, K));
+    }
     const uint8_t *s0 = (const uint8_t *)w.s0 + qf_s0_off(prow, rec, K, qf_s0_bytes(T));
     if constexpr (qf_hb5<T>())
         q.hb = *reinterpret_cast<const uint32_t *>((const uint8_t *)w.hb + qf_hb_pair_off(prow, rec, K, 4)) >> (rec & 1);
@@ -385,7 +417,22 @@ __global__ __launch_bounds__(256) void qf_repack_kernel(const uint8_t *__restric
             *reinterpret_cast<uint32_t *>((uint8_t *)dst.hb + qf_hb_pair_off(prow, rec, K, 4)) = hb;
         }
     }
-    *reinterpret_cast<u32x2 *>((uint8_t *)dst.nib + qf_nib_off(prow, rec, K)) = u32x2{nib[0], nib[1]};
+    if constexpr (qf_crumb<T>()) {
+        uint8_t *pr = (uint8_t *)dst.nib + qf_qlane_off(prow, rec, K, qf_lane_bytes(T));
+        *reinterpret_cast<uint32_t *>(pr + 4 * (rec & 1)) = crumb_word(nib[0], nib[1]);
+        if constexpr (T == AESIR_GGML_Q3_K) {
+            if (rec % 2 == 0) {  // the even record writes the pair's third bits (its own and the odd record's)
+                unsigned nib1[2] = {0u, 0u};
+#pragma unroll
+                for (int j = 0; j < 8; j++)
+                    nib1[j >> 2] |= (unsigned)((gguf_q<T>(src, k + kRec + j) + 4) | ((gguf_q<T>(src, k + kRec + 8 + j) + 4) << 4))
+                                    << (8 * (j & 3));
+                *reinterpret_cast<uint32_t *>(pr + 8) = third_bits(nib[0], nib[1], 0) | third_bits(nib1[0], nib1[1], 1);
+            }
+        }
+    } else {
+        *reinterpret_cast<u32x2 *>((uint8_t *)dst.nib + qf_nib_off(prow, rec, K)) = u32x2{nib[0], nib[1]};
+    }
     uint8_t *s0 = (uint8_t *)dst.s0 + qf_s0_off(prow, rec, K, qf_s0_bytes(T));
     if constexpr (T == AESIR_GGML_Q4_0 || T == AESIR_GGML_Q5_0 || qf_dm<T>()) {
         if (rec % 2 == 0) {  // the block's f16 d (and m), the first 2 (4) bytes of every legacy block
@@ -533,10 +580,15 @@ __global__ __launch_bounds__(256) void qf_fill_kernel(QFMat w, int64_t rows, int
     const int64_t r = gid / recs, rec = gid % recs, prow = w.row0 + r * step;
     const uint64_t a = mix64(base + (uint64_t)(2 * gid + 1) * kGolden);
     const uint64_t b = mix64(base + (uint64_t)(2 * gid + 2) * kGolden);
-    // Q2_K / Q3_K keep 2- / 3-bit values in the nibbles
-    constexpr unsigned nmask = T == AESIR_GGML_Q2_K ? 0x33333333u : T == AESIR_GGML_Q3_K ? 0x77777777u : 0xFFFFFFFFu;
-    *reinterpret_cast<u32x2 *>((uint8_t *)w.nib + qf_nib_off(prow, rec, K)) =
-        u32x2{(unsigned)a & nmask, (unsigned)(a >> 32) & nmask};
+    if constexpr (qf_crumb<T>()) {
+        // Q2_K / Q3_K: 16 uniform crumbs; Q3_K's pair word of uniform third bits (even record)
+        uint8_t *pr = (uint8_t *)w.nib + qf_qlane_off(prow, rec, K, qf_lane_bytes(T));
+        *reinterpret_cast<uint32_t *>(pr + 4 * (rec & 1)) = (unsigned)a;
+        if constexpr (T == AESIR_GGML_Q3_K)
+            if (rec % 2 == 0) *reinterpret_cast<uint32_t *>(pr + 8) = (unsigned)(a >> 32);
+    } else {
+        *reinterpret_cast<u32x2 *>((uint8_t *)w.nib + qf_nib_off(prow, rec, K)) = u32x2{(unsigned)a, (unsigned)(a >> 32)};
+    }
     uint8_t *s0 = (uint8_t *)w.s0 + qf_s0_off(prow, rec, K, qf_s0_bytes(T));
     const float u = (float)(b >> 40) * (1.0f / 16777216.0f);  // [0, 1)
     // 5-bit types: uniform fifth bits, one word per record pair (written by the even record)
@@ -803,13 +855,14 @@ struct QTile<AESIR_GGML_Q5_K> {
 };
 template <>
 struct QTile<AESIR_GGML_Q2_K> {
-    u32x4 nib;
+    u32x2 cr;     // crumb words of the two records
     unsigned s0;  // the two records' scale | min << 4 bytes
     unsigned s1;  // f16 d | f16 dmin << 16
 };
 template <>
 struct QTile<AESIR_GGML_Q3_K> {
-    u32x4 nib;
+    u32x2 cr;     // crumb words of the two records
+    unsigned hb;  // third bits of the record pair
     unsigned s0;  // int8 scales of the two records
     unsigned s1;  // f16 super-block d in the low half
 };
@@ -832,7 +885,15 @@ __device__ __forceinline__ QfRsrc qf_rsrc(const QFMat &w, int32_t type, int64_t 
 template <int T>
 __device__ __forceinline__ QTile<T> qf_tile_load(const QfRsrc &r, int tile, int lane, int s1v, int s1s) {
     QTile<T> q;
-    q.nib = __builtin_amdgcn_raw_buffer_load_b128(r.nib, lane * 16, tile * 1024, 2);
+    if constexpr (T == AESIR_GGML_Q2_K) {
+        q.cr = __builtin_amdgcn_raw_buffer_load_b64(r.nib, lane * 8, tile * 512, 2);
+    } else if constexpr (T == AESIR_GGML_Q3_K) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b96(r.nib, lane * 12, tile * 768, 2);
+        q.cr = u32x2{(unsigned)v[0], (unsigned)v[1]};
+        q.hb = (unsigned)v[2];
+    } else {
+        q.nib = __builtin_amdgcn_raw_buffer_load_b128(r.nib, lane * 16, tile * 1024, 2);
+    }
     if constexpr (qf_dm<T>())
         q.s0 = __builtin_amdgcn_raw_buffer_load_b32(r.s0, lane * 4, tile * 256, 0);
     else
@@ -856,7 +917,21 @@ __device__ __forceinline__ QTile<T> qf_tile_load(const QfRsrc &r, int tile, int 
 // the four pair positions of the record).
 template <int T>
 __device__ __forceinline__ void qf_tile_a(const QTile<T> &q, const QfRegs &k, u32x4 (&a)[4]) {
-    const unsigned nw[4] = {q.nib.x, q.nib.y, q.nib.z, q.nib.w};
+    unsigned nw[4];
+    if constexpr (qf_crumb<T>()) {  // spread the crumbs (and Q3_K's third bits) into nibble words
+        unsigned h = 0u;
+        if constexpr (T == AESIR_GGML_Q3_K) h = q.hb;
+        const u32x2 e = crumb_nibbles(q.cr.x, h), o = crumb_nibbles(q.cr.y, h << 2);
+        nw[0] = e.x;
+        nw[1] = e.y;
+        nw[2] = o.x;
+        nw[3] = o.y;
+    } else {
+        nw[0] = q.nib.x;
+        nw[1] = q.nib.y;
+        nw[2] = q.nib.z;
+        nw[3] = q.nib.w;
+    }
     const h16x2 s16 = {(h16)0.0625f, (h16)0.0625f};
     if constexpr (T == AESIR_GGML_Q4_0) {
         const h16 d = bits_to_h((uint16_t)(q.s0 & 0xffffu));
@@ -1418,9 +1493,11 @@ __global__ __launch_bounds__(kWideThreads) void gemm_wide_qf_kernel(const h16 *_
             if (b >= NB) break;
             const int tb = b / NCP, kind = b % NCP, pb = pb0 + tb, pt = pb * nseg + (int)c;
             uint8_t *dst = sb + tb * kQgTile;
-            if (kind == 0) {
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs.nib, (__attribute__((address_space(3))) void *)dst, 16,
-                                                         lane * 16, pt * 1024, 0, 0);
+            constexpr int QB = 64 * qf_lane_bytes(T);  // quant-plane bytes per tile: 1024, 512 or 768
+            if (kind == 0) {  // 16 bytes per lane, the first QB / 16 lanes
+                if (QB == 1024 || lane < QB / 16)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs.nib, (__attribute__((address_space(3))) void *)dst, 16,
+                                                             lane * 16, pt * QB, 0, 0);
             } else if (kind == 1) {  // 256 bytes from the tile's s0 (128 of them used with 2 bytes per lane)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rs.s0, (__attribute__((address_space(3))) void *)(dst + 1024),
                                                          4, lane * 4, pt * 64 * s0b, 0, 0);
@@ -1472,7 +1549,15 @@ __global__ __launch_bounds__(kWideThreads) void gemm_wide_qf_kernel(const h16 *_
         for (int f = 0; f < NF; f++) {
             const uint8_t *tp = sb + (wn * NF + f) * kQgTile;
             QTile<T> q;
-            q.nib = ld16(tp + lane * 16);
+            if constexpr (T == AESIR_GGML_Q2_K) {
+                q.cr = *reinterpret_cast<const u32x2 *>(tp + lane * 8);
+            } else if constexpr (T == AESIR_GGML_Q3_K) {
+                const unsigned *pq = reinterpret_cast<const unsigned *>(tp + lane * 12);
+                q.cr = u32x2{pq[0], pq[1]};
+                q.hb = pq[2];
+            } else {
+                q.nib = ld16(tp + lane * 16);
+            }
             if constexpr (dm) q.s0 = *reinterpret_cast<const unsigned *>(tp + 1024 + lane * 4);
             else q.s0 = *reinterpret_cast<const uint16_t *>(tp + 1024 + lane * 2);
             if constexpr (qf_hb5<T>()) q.hb = *reinterpret_cast<const unsigned *>(tp + 1280 + lane * 4);

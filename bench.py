@@ -188,11 +188,16 @@ Q8_TOKEN_WEIGHT_BYTES = LAYERS * Q8_LAYER_BYTES + q8_mat_bytes(VOCAB, DIM) + 2 *
 Q8_GATE_UP_BYTES = q8_mat_bytes(2 * FFN, DIM) + DIM * 2 + DIM * 2 + FFN * 2
 
 
-def replay_check(m, kv: int, toks: list, use_graph: bool, n: int = 16) -> dict:
+REPLAY_CHECK = True  # --no-replay-check clears it (profiler runs that trace eager launches only)
+
+
+def replay_check(m, kv: int, toks: list, use_graph: bool, n: int = 16):
     """Correctness evidence for a timed run, outside the timed region: the first n steps are run
     again from the same position and token with the other launch mode (eager launches after a
     graph-replayed run). The KV rows they rewrite are the ones the timed steps wrote, so the same
-    tokens must come out."""
+    tokens must come out. None when REPLAY_CHECK is off."""
+    if not REPLAY_CHECK:
+        return None
     n = min(n, len(toks))
     other, _ = m.decode_loop(1, kv, n, use_graph=not use_graph)
     return {"mode": "eager" if use_graph else "graph", "steps": n, "identical": other == toks[:n],
@@ -458,13 +463,15 @@ def graph_replay_ms(A, ctx, fn, n: int) -> float:
         hip.hipGraphDestroy(graph)
 
 
-def micro_bench(A, seed: int, iters: int = 64, copies: int = 16) -> dict:
+def micro_bench(A, seed: int, iters: int = 64, copies: int = 16, eager: bool = False) -> dict:
     """The kernel micro-suite (GEMV 4096 x 4096, RMSNorm, RoPE, argmax) and the Q8_0 GGUF-block matvec on the
     Llama-3-8B FFN shapes, through the C-ABI
     ops. Weight-sized operands rotate through `copies` buffers (more than the 256 MB MALL) so every
     call reads HBM; time per call is the HIP-event time of a graph replay of `iters` back-to-back
     calls on the context stream (argmax returns its index to the host, so its figure is a blocking
-    round trip timed from the host loop; the Q8_0 lines also give the host-loop time per call)."""
+    round trip timed from the host loop; the Q8_0 lines also give the host-loop time per call).
+    eager: every op timed from the host loop instead (for profiler runs that trace eager launches
+    only)."""
     rng = np.random.default_rng(seed)
     ctx = A.Context(int(copies * (DIM * DIM * 2 + 1_835_008 * 34) + (512 << 20)))
     out = {}
@@ -482,6 +489,8 @@ def micro_bench(A, seed: int, iters: int = 64, copies: int = 16) -> dict:
         and the replay is timed with HIP events, so the Python loop's per-call overhead (which a
         C or Mojo caller does not pay) cannot starve the GPU. The first call runs eagerly outside
         the capture (it builds any cached table the op uses)."""
+        if eager:
+            return host_timed(fn, n)
         fn(0)
         ctx.synchronize()
         return graph_replay_ms(A, ctx, fn, n) / n
@@ -568,6 +577,8 @@ def main():
     if args.calibrate_copy:
         calibrate_copy()
         return
+    global REPLAY_CHECK
+    REPLAY_CHECK = not args.no_replay_check
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU only (the decode path is single-GPU; multi-GPU tensor "
@@ -586,7 +597,7 @@ def main():
         return
     if args.q8_only:
         q = q8_bench(A, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters, not args.eager)
-        q["prefill"] = prefill_bench(A, args.seed, n_decode=64, wtype="q8_0")
+        q["prefill"] = prefill_bench(A, args.seed, n_decode=min(64, args.prefill_decode_steps), wtype="q8_0")
         print(json.dumps({"q8_0": q}))
         return
 
@@ -615,7 +626,7 @@ def main():
     mean_kv = args.kv + (args.steps - 1) / 2.0 + 1
     step_bytes = TOKEN_WEIGHT_BYTES + KV_BYTES_PER_POS * mean_kv + KV_BYTES_PER_POS
 
-    check = None if args.no_replay_check else replay_check(m, args.kv, toks, use_graph)
+    check = replay_check(m, args.kv, toks, use_graph)
     kt = m.kernel_times(args.kv, iters=args.kernel_iters)
     gu_ms = kt["gate_up_swiglu"]
     gu_gbs = GATE_UP_BYTES / (gu_ms * 1e-3) / 1e9
@@ -652,7 +663,7 @@ def main():
     if not args.no_sweep:
         out["kv_sweep"] = kv_sweep_bench(args.seed, args.steps, args.warmup)
     if not args.no_micro:
-        out["micro"] = micro_bench(A, args.seed)
+        out["micro"] = micro_bench(A, args.seed, eager=args.eager)
     if not args.no_prefill:
         out["prefill"] = prefill_bench(A, args.seed)
         # a 1024-token prompt (one chunk)

@@ -64,13 +64,20 @@ MIXES = {
                                     (Q8_0, Q8_0, Q8_0, Q4_0, Q6_K, Q6_K, Q4_K)]),
     # the other GGUF formats: Q4_1, Q5_0, Q5_1, Q5_K, Q2_K and Q3_K repacked as standalone matrices
     # (Q5_0 Q/K/V fused, the Q5_K table looked up apart, a Q2_K down, a Q3_K O and lm_head), and
-    # layer 1's Q5_K / Q6_K Q/K/V mix stored in f16
+    # layer 1's Q5_K / Q6_K Q/K/V in two parts (Q and K in Q5_K, V in Q6_K)
     "more_types": layout(Q5_K, Q3_K, [(Q5_0, Q5_0, Q5_0, Q4_1, Q5_1, Q5_1, Q2_K),
                                       (Q5_K, Q5_K, Q6_K, Q3_K, Q4_K, Q4_K, Q5_0)]),
     # fused matrices whose parts are Q2_K and Q3_K: Q/K/V and gate/up stored in f16, each part
     # dequantized by its own type's rule
     "kquant_parts_f16": layout(Q4_K, Q2_K, [(Q3_K, Q2_K, Q3_K, Q2_K, Q2_K, Q3_K, Q3_K),
                                             (Q2_K, Q3_K, Q2_K, Q3_K, Q3_K, Q2_K, Q2_K)]),
+    # Q/K/V in two parts read by one two-part launch: Q alone, K and V in another type (Q2_K | Q4_K),
+    # and Q and K in one type, V in another (Q3_K | Q5_K)
+    "qkv_two_parts_a": layout(Q4_K, Q6_K, [(Q2_K, Q4_K, Q4_K, Q4_K, Q4_K, Q4_K, Q6_K),
+                                           (Q3_K, Q3_K, Q5_K, Q4_K, Q5_K, Q5_K, Q4_K)]),
+    # the other pairs: Q4_K | Q5_K and Q3_K | Q4_K
+    "qkv_two_parts_b": layout(Q5_K, Q4_K, [(Q4_K, Q4_K, Q5_K, Q6_K, Q4_K, Q4_K, Q5_K),
+                                           (Q3_K, Q4_K, Q4_K, Q4_K, Q6_K, Q6_K, Q4_K)]),
 }
 
 SMALL = dict(dim=256, n_layers=2, n_heads=4, n_kv_heads=2, ffn=512, vocab=300, ctx_len=160)

@@ -1139,17 +1139,26 @@ __device__ __forceinline__ void gemv_qf_body(uint8_t *lds, const QFMat &w, int64
     // QD steps in flight: step st + QD - 1 is requested when step st starts (steps past the last
     // re-read the last step's tiles, so every path issues the same loads)
     QTile<T> tl[QD][SP];
-    auto issue = [&](int st, QTile<T>(&buf)[SP]) {
-        st = st < steps ? st : steps - 1;
-        const int pb = pb0 + bid + (st / R) * nbid, first = wave + NW * SP * (st % R);
+    // the next step to request: its index, block ik and round ir, counted up step by step (no
+    // division in the loop); past the last step the last one is requested again
+    int ist = 0, ik = 0, ir = 0;
+    auto issue_next = [&](QTile<T>(&buf)[SP]) {
+        const bool live = ist < steps;
+        const int kk = live ? ik : nb - 1, rr = live ? ir : R - 1;
+        const int pb = pb0 + bid + kk * nbid, first = wave + NW * SP * rr;
 #pragma unroll
         for (int i = 0; i < SP; i++) {
             const int sg = first + NW * i < nseg ? first + NW * i : nseg - 1;  // a surplus slot: the last segment
-            buf[i] = qf_tile_load<T>(rs, pb * nseg + sg, lane, s1v, (pb * sbr + sg / 2) * 16 * es1);
+            buf[i] = qf_tile_load<T>(rs, pb * nseg + sg, lane, s1v, (pb * sbr + (int)((unsigned)sg >> 1)) * 16 * es1);
+        }
+        ++ist;
+        if (++ir == R) {
+            ir = 0;
+            ++ik;
         }
     };
 #pragma unroll
-    for (int j = 0; j + 1 < QD; j++) issue(j, tl[j]);
+    for (int j = 0; j + 1 < QD; j++) issue_next(tl[j]);
     // the epilogue operands of this wave's rows (ER rows at en(k)) of the current and next block
     const bool ewave = wave < 16 / ER;
     auto en = [&](int k) { return rbase + (int64_t)(bid + k * nbid) * 16 + wave * ER; };
@@ -1217,11 +1226,16 @@ __device__ __forceinline__ void gemv_qf_body(uint8_t *lds, const QFMat &w, int64
     const QfRegs kr = QfRegs::make();
     f32x4 acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
     float *fin = nred + NW;  // the block's final row sums, each ER-row part written and read by its epilogue wave
-    // step st: request step st + QD - 1 into nxt, multiply the tiles of cur, and after a block's
+    // a step: request the step QD - 1 ahead into nxt, multiply the tiles of cur, and after a block's
     // last round reduce its row sums over the waves and run its epilogue
-    auto step = [&](int st, const QTile<T>(&cur)[SP], QTile<T>(&nxt)[SP]) {
-        const int k = st / R, r = st % R;
-        issue(st + QD - 1, nxt);
+    int ck = 0, cr = 0;  // block and round of the current step
+    auto step = [&](const QTile<T>(&cur)[SP], QTile<T>(&nxt)[SP]) {
+        const int k = ck, r = cr;
+        if (++cr == R) {
+            cr = 0;
+            ++ck;
+        }
+        issue_next(nxt);
         const int first = wave + NW * SP * r;
 #pragma unroll
         for (int i = 0; i < SP; i++) {
@@ -1261,7 +1275,7 @@ __device__ __forceinline__ void gemv_qf_body(uint8_t *lds, const QFMat &w, int64
     for (int base = 0; base < steps; base += QD) {
 #pragma unroll
         for (int j = 0; j < QD; j++)
-            if (base + j < steps) step(base + j, tl[j], tl[(j + QD - 1) % QD]);
+            if (base + j < steps) step(tl[j], tl[(j + QD - 1) % QD]);
     }
 }
 

@@ -378,12 +378,18 @@ template <>
 struct QVec<16> {
     u32x4 v;
     __device__ __forceinline__ static QVec load(const int8_t *p) { return QVec{ld16_stream(p)}; }
+    __device__ __forceinline__ static QVec load(__amdgpu_buffer_rsrc_t r, int v, int s) {
+        return QVec{__builtin_amdgcn_raw_buffer_load_b128(r, v, s, 2)};
+    }
 };
 template <>
 struct QVec<8> {
     u32x2 v;
     __device__ __forceinline__ static QVec load(const int8_t *p) {
         return QVec{__builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(p))};
+    }
+    __device__ __forceinline__ static QVec load(__amdgpu_buffer_rsrc_t r, int v, int s) {
+        return QVec{__builtin_amdgcn_raw_buffer_load_b64(r, v, s, 2)};
     }
 };
 // f16(q * d) of the QW quants as QW / 8 chunks of 8 f16
@@ -407,10 +413,12 @@ __global__ __launch_bounds__(kThreads) void gemv_q8_kernel(const int8_t *__restr
     const int64_t nbase = (int64_t)blockIdx.x * G * ROWS;
     const int64_t k0 = (int64_t)tid * QW;
     const int64_t KB = K / 32;
-    auto row = [&](int g, int r) -> int64_t {
-        const int64_t n = nbase + (int64_t)g * ROWS + r;
-        return n < N ? n : N - 1;
-    };
+    // the workgroup's G * ROWS rows through one buffer resource each for quants and scales: 32-bit
+    // row offsets in scalar registers, and rows past N read zeros (their sums are never stored)
+    const int Ki = (int)K, KBi = (int)KB;
+    const int nrows = N - nbase < G * ROWS ? (int)(N - nbase) : G * ROWS;
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void *)(Wq + nbase * K), 0, nrows * Ki, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc((void *)(Wd + nbase * KB), 0, nrows * KBi * 2, 0x00020000);
     u32x4 xr[NS][XC], nr[NS][XC];
     bool live[NS];
     QVec<QW> eqv[NS];
@@ -443,12 +451,12 @@ __global__ __launch_bounds__(kThreads) void gemv_q8_kernel(const int8_t *__restr
     auto request = [&](int st) {
         const int g = st / NS, i = st % NS;
         const int64_t k = k0 + (int64_t)i * SLAB;
-        const int64_t kc = k < K ? k : kf;  // dead lanes of a partial slab re-read their first chunk
+        const int kc = (int)(k < K ? k : kf);  // dead lanes of a partial slab re-read their first chunk
 #pragma unroll
         for (int r = 0; r < ROWS; r++) {
-            const int64_t n = row(g, r);
-            qb[st % D][r] = QVec<QW>::load(Wq + n * K + kc);
-            db[st % D][r] = Wd[n * KB + kc / 32];
+            const int rr = g * ROWS + r;
+            qb[st % D][r] = QVec<QW>::load(rq, kc, rr * Ki);
+            db[st % D][r] = __builtin_bit_cast(h16, __builtin_amdgcn_raw_buffer_load_b16(rd, (kc >> 5) * 2, rr * KBi * 2, 0));
         }
     };
 #pragma unroll

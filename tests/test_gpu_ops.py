@@ -212,7 +212,13 @@ def test_attention_single_position_maps_heads(A, ctx):
                                          # head, many tiles per split
                                          (31, 128, 32, 8), (33, 128, 32, 8), (2049, 128, 32, 8),
                                          (100, 128, 16, 8), (777, 64, 8, 8), (300, 64, 12, 4),
-                                         (1000, 64, 32, 4), (4097, 64, 32, 4), (32768, 128, 32, 8)])
+                                         (1000, 64, 32, 4), (4097, 64, 32, 4), (32768, 128, 32, 8),
+                                         # views of 64 rounds and more (every split takes several
+                                         # rounds): 4, 2 and 1 heads per KV head at head_dim 128
+                                         # and 64, 3 heads per KV head, 65 rounds
+                                         (4160, 128, 32, 8), (8192, 128, 16, 8), (5000, 128, 8, 8),
+                                         (6000, 64, 16, 8), (5000, 64, 8, 8), (4500, 128, 24, 8),
+                                         (20000, 64, 32, 4)])
 def test_attention_vs_oracle_and_f64(A, ctx, oracle, S, hd, nq, nkv):
     q, K, V, out = attn_case(ctx, A, S, hd, nq, nkv)
     if S <= 8192:  # beyond this the reference's per-position f16 accumulator itself drifts
@@ -238,7 +244,16 @@ def test_attention_repeated_calls_varying_split_counts(A, ctx):
         assert within_tol(out[0], f64_attention(q, K, V, S, hd, nq, nkv), atol=2e-3, rtol=2e-3), S
 
 
-@pytest.mark.parametrize("S,hd,nq,nkv", [(2048, 128, 32, 8), (3000, 64, 16, 4), (130, 128, 8, 8)])
+def test_attention_alternating_long_and_short_views(A, ctx):
+    """Views split 64 ways (one to three rounds a split), 33 ways and not at all alternate through
+    one partial buffer: each merge must use its own call's split plan."""
+    hd, nq, nkv = 128, 32, 8
+    for S in (8192, 4096, 4097, 40, 12000, 2049, 4160):
+        q, K, V, out = attn_case(ctx, A, S, hd, nq, nkv)
+        assert within_tol(out[0], f64_attention(q, K, V, S, hd, nq, nkv), atol=2e-3, rtol=2e-3), S
+
+
+@pytest.mark.parametrize("S,hd,nq,nkv", [(2048, 128, 32, 8), (3000, 64, 16, 4), (130, 128, 8, 8), (5000, 128, 32, 8)])
 def test_attention_merge_sees_every_partial(A, ctx, S, hd, nq, nkv):
     """The split merge reads partials that the split workgroups wrote into the context's shared
     partial buffer. Two inputs alternate 60 times through the same buffers: every result must

@@ -36,7 +36,7 @@ CXXFLAGS = [
 ]
 
 SOURCES = ["ctx.hip", "gemv.hip", "quant.hip", "attention.hip", "basic.hip", "q8_0.hip", "abi_ops.hip", "model.hip",
-           "prefill.hip", "gguf.hip", "sampler.hip"]
+           "prefill.hip", "gguf.hip", "sampler.hip", "blas.hip"]
 
 
 def _compile(src: str) -> str:
@@ -58,7 +58,9 @@ def build(jobs: int | None = None) -> str:
     with cf.ThreadPoolExecutor(jobs) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    # hipBLASLt for the prefill GEMMs of long chunks (blas.hip)
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, "-L/opt/rocm/lib", "-lhipblaslt",
+           "-Wl,-rpath,/opt/rocm/lib"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")

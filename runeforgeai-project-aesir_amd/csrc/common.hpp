@@ -165,6 +165,7 @@ struct aesir_ctx {
     std::vector<aesir::RopeTable> rope_tables;
     int64_t *pinned_i64 = nullptr;  // small pinned staging area (64 entries)
     aesir::SamplerWork *sampler = nullptr;  // grown on the first aesir_sample_token call
+    void *blas = nullptr;  // hipBLASLt handle and per-shape plans, made by the first library GEMM
 };
 
 struct aesir_kv {
@@ -182,6 +183,8 @@ int32_t bind(aesir_ctx *ctx);
 int32_t rope_table(aesir_ctx *ctx, float theta, int64_t head_dim, int64_t min_pos, const void **table);
 // Frees the sampler workspace of a context.
 void sampler_release(aesir_ctx *ctx);
+// Frees a context's hipBLASLt state (blas.hip).
+void blas_release(aesir_ctx *ctx);
 // Bump allocation in bytes from the well (256-byte aligned).
 int32_t well_alloc_bytes(aesir_ctx *ctx, int64_t bytes, void **out);
 

@@ -167,6 +167,7 @@ int32_t aesir_ctx_destroy(aesir_ctx *ctx) {
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     for (auto &t : ctx->rope_tables) (void)hipFree(t.dev);
     sampler_release(ctx);
+    blas_release(ctx);
     if (ctx->scratch.base) (void)hipFree(ctx->scratch.base);
     if (ctx->well_base) (void)hipFree(ctx->well_base);
     if (ctx->pinned_i64) (void)hipHostFree(ctx->pinned_i64);

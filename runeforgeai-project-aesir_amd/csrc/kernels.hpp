@@ -206,6 +206,13 @@ int32_t launch_argmax_finish(hipStream_t s, const void *partials, int64_t count,
                              int64_t *result);
 int64_t lm_head_groups(int64_t vocab);
 
+// ------------------------------------------------------------------ library GEMM (blas.hip)
+// D[M][N] = A[M][K] W[N][K]^T on hipBLASLt: f16 operands, f32 accumulation, D in f16 or f32 (row
+// major, leading dimension N); ws: workspace of ws_bytes. AESIR_ERR_UNSUPPORTED when the library
+// has no algorithm for the shape (the caller then takes its own kernel).
+int32_t blas_gemm_nt(aesir_ctx *ctx, hipStream_t s, const void *A, int64_t M, int64_t K, const void *W, int64_t N,
+                     void *D, bool f32_out, void *ws, int64_t ws_bytes);
+
 // ------------------------------------------------------------------ attention (attention.hip)
 struct AttnArgs {
     const void *q;              // [nq * hd]

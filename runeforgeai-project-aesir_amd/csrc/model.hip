@@ -630,7 +630,15 @@ int32_t model_create(aesir_ctx *ctx, const aesir_model_config *cfg, const Weight
     take(pr * d * 2, &m->pf_q);
     take(pr * d * 2, &m->pf_att);
     take(pr * f * 2, &m->pf_act);
-    if (!prefill_gemm_shapes_ok(pr, d, d + 2 * kvd, f)) take(pr * 2 * f * 2, &m->pf_gu);  // fallback GEMM only
+    // chunks of many rows run their F16 GEMMs on hipBLASLt, whose gate/up (f16) and residual (f32)
+    // products pass through pf_gu
+    bool f16_mats = false;
+    for (const ModelLayer &L : m->layers)
+        for (const WMat *w : {&L.qkv, &L.o, &L.gu, &L.down}) f16_mats = f16_mats || w->type == AESIR_GGML_F16;
+    const bool blas = f16_mats && pr >= prefill_blas_min_rows();
+    if (!prefill_gemm_shapes_ok(pr, d, d + 2 * kvd, f) || blas)
+        take(pr * 2 * f * 2 > pr * d * 4 ? pr * 2 * f * 2 : pr * d * 4, &m->pf_gu);
+    if (blas) take(prefill_blas_workspace(), &m->pf_blas_ws);
     take(pr * 8, &m->pf_tokens);
     m->pf_part_floats = prefill_part_floats(pr, d, d + 2 * kvd, f);
     if (m->pf_part_floats > 0) {

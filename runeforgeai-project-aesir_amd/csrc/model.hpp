@@ -108,10 +108,11 @@ struct aesir_model {
     float *attn_part = nullptr;
     int64_t attn_max_split = 1;
     // batched prefill workspace: pf_rows rows of x, normed x, q|k|v, q, attention out, act,
-    // gate/up products (non-MFMA shapes only) and the rows' token IDs
+    // gate/up products (non-MFMA shapes, and the library GEMMs' f16 gate/up or f32 residual
+    // products) and the rows' token IDs; the library GEMMs' workspace
     int64_t pf_rows = 0;
     void *pf_x = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_att = nullptr, *pf_act = nullptr;
-    void *pf_gu = nullptr, *pf_tokens = nullptr;
+    void *pf_gu = nullptr, *pf_tokens = nullptr, *pf_blas_ws = nullptr;
     float *pf_part = nullptr;  // f32 split-K partials of the prefill GEMMs
     int64_t pf_part_floats = 0;
     void *lm_parts = nullptr;
@@ -148,6 +149,9 @@ int32_t model_prefill(aesir_model *m, const int64_t *tokens, int64_t n, int64_t 
 int64_t prefill_part_floats(int64_t rows, int64_t dim, int64_t qkv_n, int64_t ffn);
 // True when every prefill GEMM of this shape runs on the matrix cores (no fallback buffers needed).
 bool prefill_gemm_shapes_ok(int64_t rows, int64_t dim, int64_t qkv_n, int64_t ffn);
+// Chunk rows from which F16 prefill GEMMs run on hipBLASLt, and the workspace bytes they get.
+int64_t prefill_blas_min_rows();
+int64_t prefill_blas_workspace();
 // Decode-step helpers shared with the prefill.
 int32_t ensure_rope(aesir_model *m, int64_t max_pos);
 int32_t upload_state(aesir_model *m, int64_t token, int64_t pos, int64_t advance, int64_t ring_cap);

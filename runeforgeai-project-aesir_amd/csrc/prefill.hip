@@ -604,13 +604,63 @@ static int32_t launch_mfma(hipStream_t s, const void *A, int64_t M, int64_t K, c
     return AESIR_OK;
 }
 
-// A GEMM of the prefill on the model's matrix w (rows N, K wide): repacked types on the wide-tile
+static int32_t launch_swiglu_pairs(hipStream_t s, const void *gu, void *act, int64_t n);
+
+// F16 GEMMs of chunks of at least this many rows run on hipBLASLt (blas.hip): from here on the
+// library tile is faster than the wide-tile kernel plus the row kernel the library path needs for
+// its epilogue. Measured on MI355X, TinyLlama shapes, 1024 rows (µs per GEMM, library / wide tile):
+// QKV 16 / 33, gate/up 36 / 104, down 30 / 57.
+constexpr int64_t kBlasMinRows = 256;
+constexpr int64_t kBlasWorkspace = 32 << 20;
+
+// The library path of prefill_gemm: the plain product in f16 (store; gate/up pairs, then the SwiGLU
+// row kernel) or in f32 (residual: one partial for the caller's fused residual + norm row kernel,
+// or gemm_reduce_kernel when not deferred), so every rounding is the epilogue's own.
+// AESIR_ERR_UNSUPPORTED when the library has no algorithm (the caller takes its own kernel).
+template <int EPI>
+static int32_t prefill_gemm_blas(aesir_model *m, hipStream_t s, const void *W, const void *A, int64_t M, int64_t K,
+                                 int64_t N, void *C, int64_t ldc, bool defer, int64_t *splits_out, const float **part_out) {
+    aesir_ctx *ctx = m->ctx;
+    if (EPI == kEpiStore) {
+        if (ldc != N) return AESIR_ERR_UNSUPPORTED;
+        AESIR_TRY(blas_gemm_nt(ctx, s, A, M, K, W, N, C, false, m->pf_blas_ws, kBlasWorkspace));
+    } else if (EPI == kEpiSwiglu) {
+        if (ldc != N / 2) return AESIR_ERR_UNSUPPORTED;
+        AESIR_TRY(blas_gemm_nt(ctx, s, A, M, K, W, N, m->pf_gu, false, m->pf_blas_ws, kBlasWorkspace));
+        AESIR_TRY(launch_swiglu_pairs(s, m->pf_gu, C, M * (N / 2)));
+    } else {
+        const float *part = (const float *)m->pf_gu;
+        AESIR_TRY(blas_gemm_nt(ctx, s, A, M, K, W, N, m->pf_gu, true, m->pf_blas_ws, kBlasWorkspace));
+        if (defer) {
+            if (splits_out) *splits_out = 1;
+            if (part_out) *part_out = part;
+            return AESIR_OK;
+        }
+        const int64_t blocks = (M * N + 255) / 256;
+        hipLaunchKernelGGL(gemm_reduce_kernel<EPI>, dim3((unsigned)blocks), dim3(256), 0, s, part, (int64_t)1, M, N,
+                           (h16 *)C, ldc);
+        AESIR_LAUNCH_CHECK("gemm_reduce_kernel");
+    }
+    if (splits_out) *splits_out = 1;
+    if (part_out) *part_out = nullptr;
+    return AESIR_OK;
+}
+
+// A GEMM of the prefill on the model's matrix w (rows N, K wide): F16 weights in chunks of
+// kBlasMinRows rows or more on hipBLASLt (prefill_gemm_blas); repacked types on the wide-tile
 // kernel that dequantizes in registers (launch_qf_gemm_wide) where the wide tile applies, else
 // through an f16 copy in m->pf_wdeq; F16 and Q8_0 weights on launch_mfma. `defer` and *splits_out
-// as launch_mfma's.
+// as launch_mfma's (split partials left in m->pf_part). *part_out: the library path's deferred
+// partial (one, in m->pf_gu), else nullptr.
 template <int EPI>
 static int32_t prefill_gemm(aesir_model *m, hipStream_t s, const WMat &w, const void *A, int64_t M, int64_t K, int64_t N,
-                            void *C, int64_t ldc, const char *name, bool defer = false, int64_t *splits_out = nullptr) {
+                            void *C, int64_t ldc, const char *name, bool defer = false, int64_t *splits_out = nullptr,
+                            const float **part_out = nullptr) {
+    if (w.type == AESIR_GGML_F16 && M >= kBlasMinRows && m->pf_blas_ws) {
+        const int32_t rc = prefill_gemm_blas<EPI>(m, s, w.w, A, M, K, N, C, ldc, defer, splits_out, part_out);
+        if (rc != AESIR_ERR_UNSUPPORTED) return rc;
+    }
+    if (part_out) *part_out = nullptr;
     if (!qf_type(w.type))
         return launch_mfma<EPI>(s, A, M, K, w.w, N, C, ldc, m->pf_part, m->pf_part_floats, name, defer, splits_out,
                                 w.type == AESIR_GGML_Q8_0 ? w.s0 : nullptr);
@@ -631,6 +681,9 @@ static int32_t prefill_gemm(aesir_model *m, hipStream_t s, const WMat &w, const 
     AESIR_TRY(launch_qf_dequant(s, wmat_qf(w), N, K, 1, nullptr, m->pf_wdeq, K));
     return launch_mfma<EPI>(s, A, M, K, m->pf_wdeq, N, C, ldc, m->pf_part, m->pf_part_floats, name, defer, splits_out);
 }
+
+int64_t prefill_blas_min_rows() { return kBlasMinRows; }
+int64_t prefill_blas_workspace() { return kBlasWorkspace; }
 
 bool gemm_qf_wide_ok(int64_t M, int64_t K, int64_t N) { return wide_plan(M, K, N, true).nt != 0; }
 
@@ -1074,13 +1127,16 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
     // residual GEMM into X, then X -> Xn normalized with `next_norm` (if any), fused when split
     auto residual_gemm = [&](const h16 *in, int64_t K, const WMat &w, const void *next_norm, const char *name) -> int32_t {
         int64_t splits = 1;
-        AESIR_TRY(prefill_gemm<kEpiResidual>(m, s, w, in, n, K, d, X, d, name, next_norm && rowvec, &splits));
+        const float *part = nullptr;
+        AESIR_TRY(prefill_gemm<kEpiResidual>(m, s, w, in, n, K, d, X, d, name, next_norm && rowvec, &splits, &part));
         if (!next_norm) return AESIR_OK;
-        if (splits > 1 && rowvec) {
+        if ((splits > 1 || part) && rowvec) {  // partials left for the fused residual + norm rows
+            if (!part) part = m->pf_part;
 #define AESIR_RRN(SV)                                                                                           \
     hipLaunchKernelGGL(reduce_residual_norm_rows_kernel<SV>, dim3((unsigned)n), dim3(kPThreads), 0, s,            \
-                       (const float *)m->pf_part, splits, n, d, X, Xn, (const h16 *)next_norm, c.rms_eps)
+                       part, splits, n, d, X, Xn, (const h16 *)next_norm, c.rms_eps)
             switch (splits) {
+                case 1: AESIR_RRN(1); break;
                 case 2: AESIR_RRN(2); break;
                 case 3: AESIR_RRN(3); break;
                 case 4: AESIR_RRN(4); break;

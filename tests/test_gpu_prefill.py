@@ -168,6 +168,24 @@ def test_prefill_tinyllama_shape_mfma(A, ctx, oracle):
     m.close()
 
 
+def test_prefill_library_gemms_tinyllama_width(A, ctx, oracle):
+    """TinyLlama widths (dim 2048, 32/4 heads, ffn 5632; 2 layers, vocab 512) with a 264-position
+    prompt: a chunk of 256 rows or more runs its F16 GEMMs on hipBLASLt (QKV stored straight, the
+    gate/up pairs through the SwiGLU row kernel, O and down in f32 through the fused residual +
+    RMSNorm rows). Next token, logits and the following greedy steps equal the per-position oracle."""
+    cfg = oracle.Config(dim=2048, n_layers=2, n_heads=32, n_kv_heads=4, ffn=5632, vocab=512, ctx_len=300)
+    w = oracle.synthetic_weights(cfg, 23)
+    om = oracle.Model(cfg, w)
+    prompt = oracle.prompt_tokens(264, cfg.vocab, 8)
+    first, ologits, follow = oracle_prefill(om, prompt, 3)
+    m = gpu_model(A, ctx, cfg, w)
+    got = m.prefill(prompt)
+    assert within_tol(m.logits(), ologits)
+    assert got == first
+    assert gpu_follow(m, prompt, got, 3) == follow
+    m.close()
+
+
 def test_prefill_48_column_tiles(A, ctx, oracle):
     """dim 4096 (32 / 8 heads, head_dim 128) with ffn 1024: the QKV GEMM (6144 columns, 2 K splits
     into the fused QKV tail) and the down GEMM (residual epilogue, 2 K splits into the fused norm

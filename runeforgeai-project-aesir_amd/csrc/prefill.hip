@@ -1074,6 +1074,196 @@ __global__ __launch_bounds__(kPThreads) void prefill_attention_tile_kernel(
     }
 }
 
+// The same causal attention on the matrix cores, for chunks of many rows (no ring wrap inside the
+// chunk). A 512-thread workgroup owns BQ = 128 / G consecutive rows and one KV head; wave w takes
+// query head g G + w / (BQ / 16) on rows 16 (w % (BQ / 16)) .. + 15 of the block, so the 8 waves
+// share every K/V tile of 64 keys, which the workgroup stages in LDS (the next tile's rows are
+// requested into registers while the current one is used). Per tile and wave:
+//   scores  S^T[64 keys][16 queries] = K Q^T on v_mfma_f32_16x16x32_f16 (A = K rows from LDS,
+//           B = the wave's 16 query rows, held in registers): lane l holds query l % 16 and keys
+//           16 t + 4 (l / 16) + i of sub-tile t; keys past a row's position are masked
+//   softmax f32 online softmax per query: the lane's 16 values, then lanes l ^ 16, l ^ 32
+//           (permlane swaps)
+//   P V     O[16 queries][16 dims] += P V per 32-key step, A = the probabilities as they sit in
+//           the score registers (slot 4 t + i of lane group q is key 16 t + 4 q + i), split into
+//           two f16 terms (hi = f16(p), lo = f16(p - hi)) so that they keep f32 precision; B = V
+//           read transposed from LDS with ds_read_b64_tr_b16 (V chunk c of row m at slot
+//           c ^ 2 ((m / RPS) & SWM), which spreads the transposed reads over the banks)
+// A tile entirely past a wave's last row is skipped by that wave. Scores and sums are f32, as in
+// prefill_attention_tile_kernel; only the accumulation order differs.
+typedef short short4_t __attribute__((ext_vector_type(4)));
+constexpr int kPfBK = 64;            // keys per tile
+constexpr int kPfWaves = 8;
+constexpr int64_t kPfMfmaMinRows = 256;  // chunks from here on use the matrix-core attention
+template <int HD, int G>
+__global__ __launch_bounds__(kPfWaves * kWave) void prefill_attention_mfma_kernel(
+    const h16 *__restrict__ Q, const h16 *__restrict__ kc, const h16 *__restrict__ vc, h16 *__restrict__ out,
+    int64_t n, int64_t dim, int64_t kvd, int64_t p0, float scale) {
+    constexpr int BQ = 16 * kPfWaves / G;  // rows per workgroup
+    constexpr int RBLK = BQ / 16;          // 16-row blocks per head
+    constexpr int NJ = HD / 32;            // score k-steps
+    constexpr int NT = HD / 16;            // O dim tiles
+    constexpr int KR = HD + 8;             // padded K row (halves)
+    constexpr int RB = HD * 2;             // V row bytes
+    constexpr int RPS = 256 / RB;          // V rows per 256 LDS bytes
+    constexpr int SWM = RB / 32 - 1;
+    constexpr int CH = HD / 8;             // 16-byte chunks per row
+    constexpr int NLD = kPfBK * CH / (kPfWaves * kWave);  // K (and V) chunks per thread per tile
+    static_assert(RBLK * G == kPfWaves && NLD >= 1 && NLD * kPfWaves * kWave == kPfBK * CH, "shape");
+    __shared__ __align__(16) h16 ks[kPfBK][KR];
+    __shared__ __align__(16) uint8_t vs[kPfBK * RB];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int q4 = lane >> 4, c16 = lane & 15;
+    const int64_t g = blockIdx.y;
+    const int64_t rb0 = (int64_t)blockIdx.x * BQ;                 // first row of the workgroup
+    const int64_t rlast = (rb0 + BQ < n ? rb0 + BQ : n) - 1;      // last valid row
+    const int64_t kend = p0 + rlast + 1;                          // keys of the workgroup
+    const int hw = wave / RBLK;
+    const int64_t r0w = rb0 + 16 * (wave % RBLK);                 // first row of the wave
+    const int64_t rmax_w = r0w + 15 < rlast ? r0w + 15 : rlast;   // last valid row of the wave
+    const int64_t head = g * G + hw;
+    // this lane's query row (rows past the chunk are clamped: computed, never stored)
+    const int64_t rq = r0w + c16 < rlast ? r0w + c16 : rlast;
+    const int64_t kq = p0 + rq;  // last key the query sees
+    u32x4 qb[NJ];
+    {
+        const h16 *qp = Q + rq * dim + head * HD + 8 * q4;
+#pragma unroll
+        for (int j = 0; j < NJ; j++) qb[j] = ld16(qp + 32 * j);
+    }
+    const h16 *Kg = kc + g * HD, *Vg = vc + g * HD;
+    u32x4 kr[NLD], vr[NLD];
+    auto load_tile = [&](int64_t t0) {
+#pragma unroll
+        for (int i = 0; i < NLD; i++) {
+            const int e = tid + i * kPfWaves * kWave, row = e / CH, c = e % CH;
+            const int64_t p = t0 + row < kend ? t0 + row : kend - 1;
+            kr[i] = ld16(Kg + p * kvd + 8 * c);
+            vr[i] = ld16(Vg + p * kvd + 8 * c);
+        }
+    };
+    auto read_vt = [&](int nt, int m0) -> u32x2 {  // rows m0 + lane / 4, dims 16 nt + 4 (lane % 4) .. + 3
+        const int m = m0 + (lane >> 2);
+        const int c = 2 * nt + ((lane & 3) >> 1);
+        const int sl = c ^ (2 * ((m / RPS) & SWM));
+        return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                             (__attribute__((address_space(3))) short4_t *)(vs + m * RB + 16 * sl + 8 * (lane & 1))));
+    };
+    float m_run = -INFINITY, l_run = 0.0f;  // query c16 (the same in the four lane groups)
+    f32x4 o[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) o[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    load_tile(0);
+    for (int64_t t0 = 0; t0 < kend; t0 += kPfBK) {
+        __syncthreads();  // the previous tile is no longer read
+#pragma unroll
+        for (int i = 0; i < NLD; i++) {
+            const int e = tid + i * kPfWaves * kWave, row = e / CH, c = e % CH;
+            st16(&ks[row][8 * c], kr[i]);
+            st16(vs + row * RB + 16 * (c ^ (2 * ((row / RPS) & SWM))), vr[i]);
+        }
+        __syncthreads();
+        if (t0 + kPfBK < kend) load_tile(t0 + kPfBK);
+        if (t0 > p0 + rmax_w) continue;  // every key of the tile is past this wave's rows
+        f32x4 st[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            st[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int j = 0; j < NJ; j++) st[t] = mfma16x16x32(ld16(&ks[16 * t + c16][32 * j + 8 * q4]), qb[j], st[t]);
+        }
+        float sv[4][4], mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int64_t key = t0 + 16 * t + 4 * q4 + i;
+                sv[t][i] = key <= kq ? st[t][i] * scale : -INFINITY;
+                mx = fmaxf(mx, sv[t][i]);
+            }
+        mx = swap_pair_max<32>(swap_pair_max<16>(mx));
+        const float mn = fmaxf(m_run, mx);  // finite: key 0 is in the first tile of every query
+        const float al = expf(m_run - mn);   // 0 on the first tile
+        float ps = 0.0f;
+        u32x4 ph[2], pl[2];  // k-steps: keys of sub-tiles 2 kk and 2 kk + 1
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++) {
+            h16 hi[8], lo[8];
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float p = expf(sv[2 * kk + t][i] - mn);  // 0 where masked
+                    ps += p;
+                    hi[4 * t + i] = (h16)p;
+                    lo[4 * t + i] = (h16)(p - (float)hi[4 * t + i]);
+                }
+            ph[kk] = u32x4{h2_bits(h16x2{hi[0], hi[1]}), h2_bits(h16x2{hi[2], hi[3]}), h2_bits(h16x2{hi[4], hi[5]}),
+                           h2_bits(h16x2{hi[6], hi[7]})};
+            pl[kk] = u32x4{h2_bits(h16x2{lo[0], lo[1]}), h2_bits(h16x2{lo[2], lo[3]}), h2_bits(h16x2{lo[4], lo[5]}),
+                           h2_bits(h16x2{lo[6], lo[7]})};
+        }
+        ps = swap_pair_sum<16>(ps, ps);
+        ps = swap_pair_sum<32>(ps, ps);
+        l_run = l_run * al + ps;
+        m_run = mn;
+        // O rows of this lane are queries 4 q4 + i, whose factor sits in lane 4 q4 + i
+        float alr[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            alr[i] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(4 * (4 * q4 + i), __builtin_bit_cast(int, al)));
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) o[nt][i] *= alr[i];
+#pragma unroll
+            for (int kk = 0; kk < 2; kk++) {
+                const u32x2 v0 = read_vt(nt, 32 * kk), v1 = read_vt(nt, 32 * kk + 16);
+                const u32x4 vb = u32x4{v0.x, v0.y, v1.x, v1.y};
+                o[nt] = mfma16x16x32(ph[kk], vb, o[nt]);
+                o[nt] = mfma16x16x32(pl[kk], vb, o[nt]);
+            }
+        }
+    }
+    float lr[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        lr[i] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(4 * (4 * q4 + i), __builtin_bit_cast(int, l_run)));
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int64_t r = r0w + 4 * q4 + i;
+        if (r > rlast) continue;
+        h16 *orow = out + r * dim + head * HD + c16;
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) orow[16 * nt] = (h16)(o[nt][i] / lr[i]);
+    }
+}
+
+// Launches prefill_attention_mfma_kernel for the shapes it is instantiated for;
+// AESIR_ERR_UNSUPPORTED otherwise (the caller takes the tile kernels).
+static int32_t launch_prefill_attention_mfma(hipStream_t s, int64_t hd, int64_t G, const h16 *Q, const h16 *kc,
+                                             const h16 *vc, h16 *out, int64_t n, int64_t dim, int64_t kvd, int64_t p0,
+                                             int64_t nkv, float scale) {
+#define AESIR_PF_MMA(HDV, GV)                                                                                   \
+    if (hd == HDV && G == GV) {                                                                                \
+        constexpr int BQ = 16 * kPfWaves / GV;                                                                 \
+        hipLaunchKernelGGL((prefill_attention_mfma_kernel<HDV, GV>), dim3((unsigned)((n + BQ - 1) / BQ), (unsigned)nkv), \
+                           dim3(kPfWaves * kWave), 0, s, Q, kc, vc, out, n, dim, kvd, p0, scale);              \
+        AESIR_LAUNCH_CHECK("prefill_attention_mfma_kernel");                                                   \
+        return AESIR_OK;                                                                                       \
+    }
+    AESIR_PF_MMA(64, 8)
+    AESIR_PF_MMA(64, 4)
+    AESIR_PF_MMA(64, 2)
+    AESIR_PF_MMA(64, 1)
+    AESIR_PF_MMA(128, 8)
+    AESIR_PF_MMA(128, 4)
+    AESIR_PF_MMA(128, 2)
+    AESIR_PF_MMA(128, 1)
+#undef AESIR_PF_MMA
+    return AESIR_ERR_UNSUPPORTED;
+}
+
 // act[i] = f16(up * silu(gate)) over interleaved [gate, up] pairs gu[2i], gu[2i + 1]
 // (inference.mojo:257-260 on the gate/up GEMM rows as this build lays them out).
 __global__ __launch_bounds__(kPThreads) void swiglu_pairs_kernel(const h16 *__restrict__ gu, h16 *__restrict__ act,
@@ -1196,22 +1386,31 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
         }
         const int64_t G = c.n_heads / c.n_kv_heads;
         const dim3 tgrid((unsigned)n, (unsigned)c.n_kv_heads);
+        bool att_done = false;
+        if (n >= kPfMfmaMinRows && p0 + n <= c.ctx_len) {  // long chunk without ring wrap: matrix cores
+            const int32_t rc = launch_prefill_attention_mfma(s, hd, G, Q, kc, vc, ATT, n, d, kvd, p0, c.n_kv_heads,
+                                                             m->attn_scale);
+            if (rc == AESIR_OK) att_done = true;
+            else if (rc != AESIR_ERR_UNSUPPORTED) return rc;
+        }
+        if (!att_done) {
 #define AESIR_PF_ATT(HDV, GV)                                                                                      \
     if (hd == HDV && G == GV)                                                                                     \
         hipLaunchKernelGGL((prefill_attention_tile_kernel<HDV, GV>), tgrid, dim3(kPThreads), 0, s, Q, kc, vc, ATT, d, \
                            kvd, p0, c.ctx_len, m->attn_scale);                                                   \
     else
-        AESIR_PF_ATT(64, 8)
-        AESIR_PF_ATT(128, 8)
-        AESIR_PF_ATT(128, 4)
+            AESIR_PF_ATT(64, 8)
+            AESIR_PF_ATT(128, 8)
+            AESIR_PF_ATT(128, 4)
 #undef AESIR_PF_ATT
-        if (hd % 8 == 0)  // rows of K are then 16-byte aligned (kvd and the cache base are)
-            hipLaunchKernelGGL(prefill_attention_kernel<true>, dim3((unsigned)n, (unsigned)c.n_heads), dim3(kWave), 0,
-                               s, Q, kc, vc, ATT, d, kvd, hd, c.n_heads / c.n_kv_heads, p0, c.ctx_len, m->attn_scale);
-        else
-            hipLaunchKernelGGL(prefill_attention_kernel<false>, dim3((unsigned)n, (unsigned)c.n_heads), dim3(kWave), 0,
-                               s, Q, kc, vc, ATT, d, kvd, hd, c.n_heads / c.n_kv_heads, p0, c.ctx_len, m->attn_scale);
-        AESIR_LAUNCH_CHECK("prefill_attention_kernel");
+            if (hd % 8 == 0)  // rows of K are then 16-byte aligned (kvd and the cache base are)
+                hipLaunchKernelGGL(prefill_attention_kernel<true>, dim3((unsigned)n, (unsigned)c.n_heads), dim3(kWave), 0,
+                                   s, Q, kc, vc, ATT, d, kvd, hd, c.n_heads / c.n_kv_heads, p0, c.ctx_len, m->attn_scale);
+            else
+                hipLaunchKernelGGL(prefill_attention_kernel<false>, dim3((unsigned)n, (unsigned)c.n_heads), dim3(kWave), 0,
+                                   s, Q, kc, vc, ATT, d, kvd, hd, c.n_heads / c.n_kv_heads, p0, c.ctx_len, m->attn_scale);
+            AESIR_LAUNCH_CHECK("prefill_attention_kernel");
+        }
         // O projection + residual, then the feed-forward norm (inference.mojo:227-241)
         if (mfma) {
             AESIR_TRY(residual_gemm(ATT, d, L.o, L.ffn_norm, "gemm_mfma_o_residual"));

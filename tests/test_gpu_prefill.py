@@ -204,13 +204,24 @@ def test_prefill_48_column_tiles(A, ctx, oracle):
     m.close()
 
 
-@pytest.mark.parametrize("dim,heads,kv,n_prompt,split", [(512, 8, 1, 300, 0), (512, 4, 1, 150, 0),
-                                                        (1024, 8, 1, 140, 70)])
+@pytest.mark.parametrize("dim,heads,kv,n_prompt,split", [(512, 8, 1, 150, 0), (512, 4, 1, 150, 0),
+                                                        (1024, 8, 1, 140, 70),
+                                                        # matrix-core attention (chunks of 256 rows
+                                                        # or more): head_dim 64 / 128 with 8, 4, 2
+                                                        # and 1 query heads per KV head, partial row
+                                                        # blocks, continuations at start_pos > 0
+                                                        (512, 8, 1, 300, 0), (256, 4, 1, 300, 0),
+                                                        (256, 4, 2, 290, 0), (256, 4, 4, 400, 100),
+                                                        (1024, 8, 1, 270, 0), (1024, 8, 2, 300, 0),
+                                                        (512, 4, 2, 300, 0), (512, 4, 4, 280, 0),
+                                                        (512, 8, 1, 420, 120)])
 def test_prefill_grouped_attention_tiles(A, ctx, oracle, dim, heads, kv, n_prompt, split):
-    """The GQA-grouped prefill attention (one workgroup per row and KV head, 128-position LDS
-    tiles): head_dim 64 with 8 query heads per KV head, head_dim 128 with 4 and with 8; prompts
-    longer than one tile (300 positions: three tiles for the last rows) and a continuation at
-    start_pos 70. Next token, logits and the following greedy steps equal the per-position oracle."""
+    """The GQA-grouped prefill attention: chunks under 256 rows on the tile kernel (one workgroup
+    per row and KV head, 128-position LDS tiles; head_dim 64 with 8 query heads per KV head,
+    head_dim 128 with 4 and with 8, a continuation at start_pos 70), longer chunks on the
+    matrix-core kernel (every head_dim / group instance, row counts that leave the last row block
+    partial, and second chunks of 300 rows after 100 or 120 positions). Next token, logits and
+    the following greedy steps equal the per-position oracle."""
     cfg = oracle.Config(dim=dim, n_layers=2, n_heads=heads, n_kv_heads=kv, ffn=2 * dim, vocab=512,
                         ctx_len=n_prompt + 16)
     w = oracle.synthetic_weights(cfg, 77)

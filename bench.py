@@ -564,6 +564,8 @@ def main():
                     help="weight type of --prefill-only: f16, q8_0 or a repacked type (q4_0, q4_k, ...)")
     ap.add_argument("--prefill-decode-steps", type=int, default=256,
                     help="greedy decode steps after the prefill in --prefill-only runs (0: none)")
+    ap.add_argument("--prefill-prompt", type=int, default=128,
+                    help="prompt positions of --prefill-only runs (one chunk up to 2048)")
     ap.add_argument("--no-q8", action="store_true", help="skip the Q8_0-weight decode measurement")
     ap.add_argument("--no-sweep", action="store_true", help="skip the decode at KV 512 / 8192 / 32768")
     ap.add_argument("--no-micro", action="store_true", help="skip the kernel micro-suite and the Q8_0 matvec")
@@ -588,8 +590,8 @@ def main():
     import aesir_hip as A
 
     if args.prefill_only:
-        print(json.dumps({"prefill": prefill_bench(A, args.seed, n_decode=args.prefill_decode_steps,
-                                                   wtype=args.prefill_type)}))
+        print(json.dumps({"prefill": prefill_bench(A, args.seed, n_prompt=args.prefill_prompt,
+                                                   n_decode=args.prefill_decode_steps, wtype=args.prefill_type)}))
         return
     if args.quant_only:
         print(json.dumps({"quant": {k: quant_bench(A, k, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters,

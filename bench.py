@@ -210,7 +210,9 @@ def q8_bench(A, seed: int, kv: int, steps: int, warmup: int, kernel_iters: int, 
     pre-filled to kv positions; same step structure as the F16 decode (graph replay unless
     use_graph is False)."""
     ctx_len = kv + max(steps, warmup) + 64
-    well = int(Q8_TOKEN_WEIGHT_BYTES + q8_mat_bytes(VOCAB - 1, DIM) + 2 * LAYERS * ctx_len * KV_DIM * 2 + (512 << 20))
+    # (+ the f16 copy of the largest layer matrix that long-chunk prefills dequantize into)
+    well = int(Q8_TOKEN_WEIGHT_BYTES + q8_mat_bytes(VOCAB - 1, DIM) + 2 * LAYERS * ctx_len * KV_DIM * 2
+               + 2 * 2 * FFN * DIM + (512 << 20))
     ctx = A.Context(well)
     m = A.Model.create(ctx, A.ModelConfig(DIM, LAYERS, HEADS, KV_HEADS, FFN, VOCAB, ctx_len), A.GGML_Q8_0)
     m.init_random(seed, 0.02, NORM_MEAN, 0.02)

@@ -604,7 +604,14 @@ int32_t model_create(aesir_ctx *ctx, const aesir_model_config *cfg, const Weight
     m->all_f16 = m->embd.type == AESIR_GGML_F16 && m->out.type == AESIR_GGML_F16;
     for (const ModelLayer &L : m->layers)
         for (const WMat *w : {&L.qkv, &L.o, &L.gu, &L.down}) m->all_f16 = m->all_f16 && w->type == AESIR_GGML_F16;
-    if (any_qf) {  // f16 copy of the largest layer matrix for the prefill GEMMs
+    // f16 copy of the largest layer matrix for the prefill GEMMs: repacked types dequantize into it
+    // for short chunks off the wide tile, and every quantized matrix for the library GEMMs of long
+    // chunks (Q8_0 only then)
+    const int64_t pr_max = c.ctx_len < 2048 ? c.ctx_len : 2048;
+    bool q8_mats = false;
+    for (const ModelLayer &L : m->layers)
+        for (const WMat *w : {&L.qkv, &L.qkv_b, &L.o, &L.gu, &L.down}) q8_mats = q8_mats || w->type == AESIR_GGML_Q8_0;
+    if (any_qf || (q8_mats && pr_max >= prefill_blas_min_rows())) {
         int64_t big = (d + 2 * kvd) * d;
         if (2 * f * d > big) big = 2 * f * d;
         take(mul_checked(big, 2), &m->pf_wdeq);
@@ -630,12 +637,9 @@ int32_t model_create(aesir_ctx *ctx, const aesir_model_config *cfg, const Weight
     take(pr * d * 2, &m->pf_q);
     take(pr * d * 2, &m->pf_att);
     take(pr * f * 2, &m->pf_act);
-    // chunks of many rows run their F16 GEMMs on hipBLASLt, whose gate/up (f16) and residual (f32)
-    // products pass through pf_gu
-    bool f16_mats = false;
-    for (const ModelLayer &L : m->layers)
-        for (const WMat *w : {&L.qkv, &L.o, &L.gu, &L.down}) f16_mats = f16_mats || w->type == AESIR_GGML_F16;
-    const bool blas = f16_mats && pr >= prefill_blas_min_rows();
+    // chunks of many rows run their GEMMs on hipBLASLt (quantized matrices through the f16 copy in
+    // pf_wdeq), whose gate/up (f16) and residual (f32) products pass through pf_gu
+    const bool blas = pr >= prefill_blas_min_rows();
     if (!prefill_gemm_shapes_ok(pr, d, d + 2 * kvd, f) || blas)
         take(pr * 2 * f * 2 > pr * d * 4 ? pr * 2 * f * 2 : pr * d * 4, &m->pf_gu);
     if (blas) take(prefill_blas_workspace(), &m->pf_blas_ws);

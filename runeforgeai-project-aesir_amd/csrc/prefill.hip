@@ -606,6 +606,37 @@ static int32_t launch_mfma(hipStream_t s, const void *A, int64_t M, int64_t K, c
 
 static int32_t launch_swiglu_pairs(hipStream_t s, const void *gu, void *act, int64_t n);
 
+// Q8_0 planes (int8 quants [N][K], f16 block scales [N][K / 32]) -> f16 [N][K] with
+// w = f16(f16(q) d) per weight (dequant_q8x4: the rounding of gemm_q8_0, compute.mojo:1062-1063,
+// and of every Q8_0 kernel here). K % 32 == 0; each thread converts 16 weights of one block.
+__global__ __launch_bounds__(256) void q8_dequant_rows_kernel(const int8_t *__restrict__ q, const h16 *__restrict__ d,
+                                                              int64_t N, int64_t K, h16 *__restrict__ out) {
+    const int64_t total = N * K / 16;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        const int64_t e = i * 16, n = e / K, k = e % K;
+        const u32x4 qv = ld16(q + e);
+        const h16 dd = d[n * (K / 32) + k / 32];
+        unsigned w[8];
+        dequant_q8x4(qv.x, dd, w[0], w[1]);
+        dequant_q8x4(qv.y, dd, w[2], w[3]);
+        dequant_q8x4(qv.z, dd, w[4], w[5]);
+        dequant_q8x4(qv.w, dd, w[6], w[7]);
+        st16(out + e, u32x4{w[0], w[1], w[2], w[3]});
+        st16(out + e + 8, u32x4{w[4], w[5], w[6], w[7]});
+    }
+}
+
+static int32_t launch_q8_dequant_rows(hipStream_t s, const void *q, const void *d, int64_t N, int64_t K, void *out) {
+    if (K % 32 != 0 || ((uintptr_t)q & 15) || ((uintptr_t)out & 15))
+        return fail(AESIR_ERR_UNSUPPORTED, "q8_dequant_rows: K %% 32 and 16-byte aligned rows required");
+    int64_t g = (N * K / 16 + 255) / 256;
+    if (g > 16384) g = 16384;
+    hipLaunchKernelGGL(q8_dequant_rows_kernel, dim3((unsigned)g), dim3(256), 0, s, (const int8_t *)q, (const h16 *)d, N,
+                       K, (h16 *)out);
+    AESIR_LAUNCH_CHECK("q8_dequant_rows_kernel");
+    return AESIR_OK;
+}
+
 // F16 GEMMs of chunks of at least this many rows run on hipBLASLt (blas.hip): from here on the
 // library tile is faster than the wide-tile kernel plus the row kernel the library path needs for
 // its epilogue. Measured on MI355X, TinyLlama shapes, 1024 rows (µs per GEMM, library / wide tile):
@@ -656,9 +687,20 @@ template <int EPI>
 static int32_t prefill_gemm(aesir_model *m, hipStream_t s, const WMat &w, const void *A, int64_t M, int64_t K, int64_t N,
                             void *C, int64_t ldc, const char *name, bool defer = false, int64_t *splits_out = nullptr,
                             const float **part_out = nullptr) {
-    if (w.type == AESIR_GGML_F16 && M >= kBlasMinRows && m->pf_blas_ws) {
-        const int32_t rc = prefill_gemm_blas<EPI>(m, s, w.w, A, M, K, N, C, ldc, defer, splits_out, part_out);
-        if (rc != AESIR_ERR_UNSUPPORTED) return rc;
+    if (M >= kBlasMinRows && m->pf_blas_ws) {
+        const void *W = nullptr;
+        if (w.type == AESIR_GGML_F16) {
+            W = w.w;
+        } else if (m->pf_wdeq && (qf_type(w.type) || (w.type == AESIR_GGML_Q8_0 && K % 32 == 0))) {
+            // quantized: one f16 copy per chunk, with the rounding of the type's own GEMM kernels
+            if (qf_type(w.type)) AESIR_TRY(launch_qf_dequant(s, wmat_qf(w), N, K, 1, nullptr, m->pf_wdeq, K));
+            else AESIR_TRY(launch_q8_dequant_rows(s, w.w, w.s0, N, K, m->pf_wdeq));
+            W = m->pf_wdeq;
+        }
+        if (W) {
+            const int32_t rc = prefill_gemm_blas<EPI>(m, s, W, A, M, K, N, C, ldc, defer, splits_out, part_out);
+            if (rc != AESIR_ERR_UNSUPPORTED) return rc;
+        }
     }
     if (part_out) *part_out = nullptr;
     if (!qf_type(w.type))
@@ -1354,8 +1396,15 @@ static int32_t prefill_chunk(aesir_model *m, const int64_t *tokens_host, int64_t
             AESIR_TRY(launch_qf_dequant(s, wmat_qf(L.qkv), L.qkv_split, d, 1, nullptr, m->pf_wdeq, d));
             AESIR_TRY(launch_qf_dequant(s, wmat_qf(L.qkv_b), qkv_n - L.qkv_split, d, 1, nullptr,
                                         (h16 *)m->pf_wdeq + L.qkv_split * d, d));
-            AESIR_TRY(launch_mfma<kEpiStore>(s, Xn, n, d, m->pf_wdeq, qkv_n, QKV, qkv_n, m->pf_part, m->pf_part_floats,
-                                             "gemm_mfma_qkv", true, &qkv_splits));
+            int32_t rc = AESIR_ERR_UNSUPPORTED;
+            if (n >= kBlasMinRows && m->pf_blas_ws)
+                rc = prefill_gemm_blas<kEpiStore>(m, s, m->pf_wdeq, Xn, n, d, qkv_n, QKV, qkv_n, false, &qkv_splits,
+                                                  nullptr);
+            if (rc == AESIR_ERR_UNSUPPORTED)
+                AESIR_TRY(launch_mfma<kEpiStore>(s, Xn, n, d, m->pf_wdeq, qkv_n, QKV, qkv_n, m->pf_part,
+                                                 m->pf_part_floats, "gemm_mfma_qkv", true, &qkv_splits));
+            else if (rc != AESIR_OK)
+                return rc;
         } else if (mfma) {
             AESIR_TRY(prefill_gemm<kEpiStore>(m, s, L.qkv, Xn, n, d, qkv_n, QKV, qkv_n, "gemm_mfma_qkv", true, &qkv_splits));
         } else {

@@ -170,6 +170,23 @@ def test_mixed_batched_prefill_matches_per_position(A, ctx, oracle, mix):
     m.close()
 
 
+@pytest.mark.parametrize("mix", list(MIXES))
+def test_mixed_long_chunk_prefill_matches_per_position(A, ctx, oracle, mix):
+    """A 300-row chunk of every mix: each matrix (a two-part Q/K/V as one f16 copy of both parts)
+    dequantized and multiplied on hipBLASLt, against the per-position oracle."""
+    cfg = oracle.Config(**{**SMALL, "ctx_len": 320})
+    m, _, back = mixed_model(A, ctx, oracle, cfg, MIXES[mix], 8)
+    om = oracle.Model(cfg, back)
+    prompt = oracle.prompt_tokens(300, cfg.vocab, 6)
+    okv = om.new_kv()
+    for p in range(len(prompt)):
+        want, ol = om.forward(okv, prompt, p)
+    got = m.prefill(prompt, 0)
+    assert within_tol(m.logits(), ol)
+    assert same_token(got, want, ol), (got, want)
+    m.close()
+
+
 @pytest.mark.parametrize("mix", ["embd_apart", "more_types"])
 def test_mixed_gguf_file_loads_like_set_tensor(A, ctx, oracle, tmp_path, mix):
     from gguf_tools import llama_metadata, write_gguf

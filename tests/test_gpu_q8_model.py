@@ -197,13 +197,15 @@ def test_q8_graph_eager_prefill_agree(A, ctx, oracle):
         mm.close()
 
 
-@pytest.mark.parametrize("shape,n_prompt,split", [("small", 40, 0), ("small", 200, 77), ("tinyllama", 100, 0)])
+@pytest.mark.parametrize("shape,n_prompt,split", [("small", 40, 0), ("small", 200, 77), ("tinyllama", 100, 0),
+                                                   ("small", 300, 0), ("small", 420, 120)])
 def test_q8_batched_prefill_matches_per_position(A, ctx, oracle, shape, n_prompt, split):
     """aesir_prefill on a Q8_0 model runs the Q8_0 MFMA GEMMs (quants and scales copied into LDS,
     dequantized per fragment): the next token, logits within tolerance and the greedy steps that
     read the prefilled cache equal the per-position oracle on the dequantized weights. 200
     positions = one chunk of two 128-row M tiles; `split` > 0 prefills the prompt in two calls
-    (start_pos > 0)."""
+    (start_pos > 0). Chunks of 300 rows take the long-chunk path instead: the matrices
+    dequantized to f16 (f16(f16(q) d)) and multiplied on hipBLASLt."""
     cfg = dict(Q8_SMALL if shape == "small" else Q8_TL)
     cfg["ctx_len"] = max(cfg["ctx_len"], n_prompt + 8)
     tensors, deq = q8_weights(A, oracle, cfg, 41)

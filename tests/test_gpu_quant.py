@@ -196,6 +196,23 @@ def test_quant_model_stream_matches_dequantized_oracle(A, ctx, oracle, kind):
 
 
 @pytest.mark.parametrize("kind", list(TYPES))
+def test_quant_long_chunk_prefill_matches_per_position(A, ctx, oracle, kind):
+    """A 300-row chunk: every GEMM dequantizes its matrix into the f16 copy (the type's own
+    rounding) and runs on hipBLASLt, attention on the matrix-core kernel; next token (near ties
+    allowed) and logits against the per-position oracle on the read-back weights."""
+    cfg = oracle.Config(**{**SMALL, "ctx_len": 320})
+    m, om = quant_model(A, ctx, oracle, cfg, kind, 7)
+    prompt = oracle.prompt_tokens(300, cfg.vocab, 5)
+    okv = om.new_kv()
+    for p in range(len(prompt)):
+        want, ol = om.forward(okv, prompt, p)
+    got = m.prefill(prompt, 0)
+    assert within_tol(m.logits(), ol)
+    assert same_token(got, want, ol), (got, want)
+    m.close()
+
+
+@pytest.mark.parametrize("kind", list(TYPES))
 def test_quant_batched_prefill_matches_per_position(A, ctx, oracle, kind):
     """aesir_prefill of a 140-token prompt (one chunk: two 128-row M tiles of the matrix-core GEMM on
     the repacked planes), and of the same prompt as 100 + 40 positions (the 40-row chunk on f16

@@ -186,6 +186,27 @@ def test_prefill_library_gemms_tinyllama_width(A, ctx, oracle):
     m.close()
 
 
+def test_prefill_long_chunk_llama3_width_matches_per_position(A, ctx, oracle):
+    """Llama-3-8B widths (dim 4096, 32/8 heads, head_dim 128, ffn 14336; 1 layer, vocab 4096) with a
+    300-row chunk (library GEMMs, matrix-core attention with 4 query heads per KV head): next token
+    and logits equal the per-position forward_pass of the same weights (the decode kernels, which
+    the other tests pin to the oracle)."""
+    cfg = oracle.Config(dim=4096, n_layers=1, n_heads=32, n_kv_heads=8, ffn=14336, vocab=4096, ctx_len=320,
+                        theta=500000.0)
+    w = oracle.synthetic_weights(cfg, 19)
+    prompt = oracle.prompt_tokens(300, cfg.vocab, 9)
+    m = gpu_model(A, ctx, cfg, w)
+    got = m.prefill(prompt)
+    lp = m.logits().astype(np.float32)
+    m.close()
+    m = gpu_model(A, ctx, cfg, w)
+    for p in range(len(prompt)):
+        want = m.forward_pass(prompt, p)
+    assert within_tol(lp, m.logits())
+    assert got == want
+    m.close()
+
+
 def test_prefill_48_column_tiles(A, ctx, oracle):
     """dim 4096 (32 / 8 heads, head_dim 128) with ffn 1024: the QKV GEMM (6144 columns, 2 K splits
     into the fused QKV tail) and the down GEMM (residual epilogue, 2 K splits into the fused norm

@@ -1308,16 +1308,39 @@ static int32_t launch_prefill_attention_mfma(hipStream_t s, int64_t hd, int64_t 
 
 // act[i] = f16(up * silu(gate)) over interleaved [gate, up] pairs gu[2i], gu[2i + 1]
 // (inference.mojo:257-260 on the gate/up GEMM rows as this build lays them out).
+// VEC: n % 8 == 0 and 16-byte aligned buffers; each thread then takes 8 outputs (two 16-byte
+// loads of pairs, one 16-byte store).
+template <bool VEC>
 __global__ __launch_bounds__(kPThreads) void swiglu_pairs_kernel(const h16 *__restrict__ gu, h16 *__restrict__ act,
                                                                  int64_t n) {
-    for (int64_t i = (int64_t)blockIdx.x * kPThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kPThreads)
-        act[i] = hmul(gu[2 * i + 1], silu_h(gu[2 * i]));
+    if constexpr (VEC) {
+        for (int64_t i = (int64_t)blockIdx.x * kPThreads + threadIdx.x; i < n / 8; i += (int64_t)gridDim.x * kPThreads) {
+            const u32x4 a = ld16(gu + 16 * i), b = ld16(gu + 16 * i + 8);
+            const unsigned w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            unsigned o[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const h16x2 p0 = as_h2(w[2 * j]), p1 = as_h2(w[2 * j + 1]);  // (gate, up) pairs
+                o[j] = h2_bits(h16x2{hmul(p0.y, silu_h(p0.x)), hmul(p1.y, silu_h(p1.x))});
+            }
+            st16(act + 8 * i, u32x4{o[0], o[1], o[2], o[3]});
+        }
+    } else {
+        for (int64_t i = (int64_t)blockIdx.x * kPThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kPThreads)
+            act[i] = hmul(gu[2 * i + 1], silu_h(gu[2 * i]));
+    }
 }
 
 static int32_t launch_swiglu_pairs(hipStream_t s, const void *gu, void *act, int64_t n) {
-    int64_t g = (n + kPThreads - 1) / kPThreads;
+    const bool vec = n % 8 == 0 && ((uintptr_t)gu & 15) == 0 && ((uintptr_t)act & 15) == 0;
+    int64_t g = ((vec ? n / 8 : n) + kPThreads - 1) / kPThreads;
     if (g > 65536) g = 65536;
-    hipLaunchKernelGGL(swiglu_pairs_kernel, dim3((unsigned)g), dim3(kPThreads), 0, s, (const h16 *)gu, (h16 *)act, n);
+    if (vec)
+        hipLaunchKernelGGL(swiglu_pairs_kernel<true>, dim3((unsigned)g), dim3(kPThreads), 0, s, (const h16 *)gu,
+                           (h16 *)act, n);
+    else
+        hipLaunchKernelGGL(swiglu_pairs_kernel<false>, dim3((unsigned)g), dim3(kPThreads), 0, s, (const h16 *)gu,
+                           (h16 *)act, n);
     AESIR_LAUNCH_CHECK("swiglu_pairs_kernel");
     return AESIR_OK;
 }

@@ -1137,8 +1137,11 @@ typedef short short4_t __attribute__((ext_vector_type(4)));
 constexpr int kPfBK = 64;            // keys per tile
 constexpr int kPfWaves = 8;
 constexpr int64_t kPfMfmaMinRows = 256;  // chunks from here on use the matrix-core attention
-template <int HD, int G>
-__global__ __launch_bounds__(kPfWaves * kWave) void prefill_attention_mfma_kernel(
+// Groups of 8 waves splitting a row block's key tiles (head_dim 64; at head_dim 128 the 1024-thread
+// workgroup's 128-VGPR budget spills, so one group).
+constexpr int kPfKeyGroups = 2;
+template <int HD, int G, int KS>
+__global__ __launch_bounds__(KS * kPfWaves * kWave) void prefill_attention_mfma_kernel(
     const h16 *__restrict__ Q, const h16 *__restrict__ kc, const h16 *__restrict__ vc, h16 *__restrict__ out,
     int64_t n, int64_t dim, int64_t kvd, int64_t p0, float scale) {
     constexpr int BQ = 16 * kPfWaves / G;  // rows per workgroup
@@ -1150,16 +1153,24 @@ __global__ __launch_bounds__(kPfWaves * kWave) void prefill_attention_mfma_kerne
     constexpr int RPS = 256 / RB;          // V rows per 256 LDS bytes
     constexpr int SWM = RB / 32 - 1;
     constexpr int CH = HD / 8;             // 16-byte chunks per row
-    constexpr int NLD = kPfBK * CH / (kPfWaves * kWave);  // K (and V) chunks per thread per tile
-    static_assert(RBLK * G == kPfWaves && NLD >= 1 && NLD * kPfWaves * kWave == kPfBK * CH, "shape");
-    __shared__ __align__(16) h16 ks[kPfBK][KR];
-    __shared__ __align__(16) uint8_t vs[kPfBK * RB];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    constexpr int GT = kPfWaves * kWave;   // threads of a key group
+    constexpr int NLD = kPfBK * CH / GT;   // K (and V) chunks per thread per tile
+    constexpr int KB = kPfBK * KR * 2;     // K tile bytes (padded rows)
+    constexpr int TB = KB + kPfBK * RB;    // K + V tile bytes of a key group
+    static_assert(RBLK * G == kPfWaves && NLD >= 1 && NLD * GT == kPfBK * CH, "shape");
+    static_assert(KS == 1 || kPfWaves * kWave * NT * 16 <= KS * TB, "the second group's O fits the tiles' LDS");
+    __shared__ __align__(16) uint8_t smem[KS * TB];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int kg = tid / GT, gt = tid % GT, wave = gt >> 6;  // key group, thread and wave in it
+    uint8_t *kbase = smem + kg * TB, *vs = kbase + KB;
+    auto ks = [&](int row, int col) -> h16 * { return reinterpret_cast<h16 *>(kbase) + row * KR + col; };
     const int q4 = lane >> 4, c16 = lane & 15;
     const int64_t g = blockIdx.y;
     const int64_t rb0 = (int64_t)blockIdx.x * BQ;                 // first row of the workgroup
     const int64_t rlast = (rb0 + BQ < n ? rb0 + BQ : n) - 1;      // last valid row
     const int64_t kend = p0 + rlast + 1;                          // keys of the workgroup
+    const int64_t ntile = (kend + kPfBK - 1) / kPfBK;
+    const int64_t niter = (ntile + KS - 1) / KS;                  // tile rounds (group kg: tiles KS it + kg)
     const int hw = wave / RBLK;
     const int64_t r0w = rb0 + 16 * (wave % RBLK);                 // first row of the wave
     const int64_t rmax_w = r0w + 15 < rlast ? r0w + 15 : rlast;   // last valid row of the wave
@@ -1175,10 +1186,10 @@ __global__ __launch_bounds__(kPfWaves * kWave) void prefill_attention_mfma_kerne
     }
     const h16 *Kg = kc + g * HD, *Vg = vc + g * HD;
     u32x4 kr[NLD], vr[NLD];
-    auto load_tile = [&](int64_t t0) {
+    auto load_tile = [&](int64_t t0) {  // rows past the workgroup's keys re-read its last key
 #pragma unroll
         for (int i = 0; i < NLD; i++) {
-            const int e = tid + i * kPfWaves * kWave, row = e / CH, c = e % CH;
+            const int e = gt + i * GT, row = e / CH, c = e % CH;
             const int64_t p = t0 + row < kend ? t0 + row : kend - 1;
             kr[i] = ld16(Kg + p * kvd + 8 * c);
             vr[i] = ld16(Vg + p * kvd + 8 * c);
@@ -1195,24 +1206,25 @@ __global__ __launch_bounds__(kPfWaves * kWave) void prefill_attention_mfma_kerne
     f32x4 o[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) o[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    load_tile(0);
-    for (int64_t t0 = 0; t0 < kend; t0 += kPfBK) {
-        __syncthreads();  // the previous tile is no longer read
+    load_tile((int64_t)kg * kPfBK);
+    for (int64_t it = 0; it < niter; it++) {
+        const int64_t t0 = (it * KS + kg) * kPfBK;  // past kend: a surplus round of this group
+        __syncthreads();  // the previous tiles are no longer read
 #pragma unroll
         for (int i = 0; i < NLD; i++) {
-            const int e = tid + i * kPfWaves * kWave, row = e / CH, c = e % CH;
-            st16(&ks[row][8 * c], kr[i]);
+            const int e = gt + i * GT, row = e / CH, c = e % CH;
+            st16(ks(row, 8 * c), kr[i]);
             st16(vs + row * RB + 16 * (c ^ (2 * ((row / RPS) & SWM))), vr[i]);
         }
         __syncthreads();
-        if (t0 + kPfBK < kend) load_tile(t0 + kPfBK);
+        if (it + 1 < niter) load_tile(t0 + KS * kPfBK);
         if (t0 > p0 + rmax_w) continue;  // every key of the tile is past this wave's rows
         f32x4 st[4];
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             st[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int j = 0; j < NJ; j++) st[t] = mfma16x16x32(ld16(&ks[16 * t + c16][32 * j + 8 * q4]), qb[j], st[t]);
+            for (int j = 0; j < NJ; j++) st[t] = mfma16x16x32(ld16(ks(16 * t + c16, 32 * j + 8 * q4)), qb[j], st[t]);
         }
         float sv[4][4], mx = -INFINITY;
 #pragma unroll
@@ -1224,8 +1236,10 @@ __global__ __launch_bounds__(kPfWaves * kWave) void prefill_attention_mfma_kerne
                 mx = fmaxf(mx, sv[t][i]);
             }
         mx = swap_pair_max<32>(swap_pair_max<16>(mx));
-        const float mn = fmaxf(m_run, mx);  // finite: key 0 is in the first tile of every query
-        const float al = expf(m_run - mn);   // 0 on the first tile
+        // the tile holds a key the query sees (t0 <= p0 + rq for every row of the wave but
+        // clamped rows past the chunk, which are never stored), so mx is finite
+        const float mn = fmaxf(m_run, mx);
+        const float al = expf(m_run - mn);   // 0 on the group's first tile
         float ps = 0.0f;
         u32x4 ph[2], pl[2];  // k-steps: keys of sub-tiles 2 kk and 2 kk + 1
 #pragma unroll
@@ -1267,6 +1281,40 @@ __global__ __launch_bounds__(kPfWaves * kWave) void prefill_attention_mfma_kerne
             }
         }
     }
+    if constexpr (KS == 2) {
+        // group 1 hands (m, l, O) to the group-0 wave of the same rows and head through the tiles'
+        // LDS: w = exp(m_g - max m) per query, l = sum w l_g, O = sum w O_g
+        __syncthreads();  // every tile read is done
+        f32x4 *ox = reinterpret_cast<f32x4 *>(smem);           // [wave][nt][lane]
+        float *mx1 = reinterpret_cast<float *>(smem + kPfWaves * kWave * NT * 16);  // [wave][m: 16, l: 16]
+        static_assert(kPfWaves * (kWave * NT * 16 + 32 * 4) <= KS * TB, "exchange fits");
+        if (kg == 1) {
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) ox[(wave * NT + nt) * kWave + lane] = o[nt];
+            if (q4 == 0) {
+                mx1[wave * 32 + c16] = m_run;
+                mx1[wave * 32 + 16 + c16] = l_run;
+            }
+        }
+        __syncthreads();
+        if (kg == 1) return;
+        const float m1 = mx1[wave * 32 + c16], l1 = mx1[wave * 32 + 16 + c16];
+        const float M = fmaxf(m_run, m1);   // m_run finite: group 0 holds tile 0
+        const float e0 = expf(m_run - M), e1 = expf(m1 - M);  // e1 = 0 for a group without tiles
+        l_run = l_run * e0 + l1 * e1;
+        float e0r[4], e1r[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            e0r[i] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(4 * (4 * q4 + i), __builtin_bit_cast(int, e0)));
+            e1r[i] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(4 * (4 * q4 + i), __builtin_bit_cast(int, e1)));
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const f32x4 b = ox[(wave * NT + nt) * kWave + lane];
+#pragma unroll
+            for (int i = 0; i < 4; i++) o[nt][i] = o[nt][i] * e0r[i] + b[i] * e1r[i];
+        }
+    }
     float lr[4];
 #pragma unroll
     for (int i = 0; i < 4; i++)
@@ -1288,9 +1336,9 @@ static int32_t launch_prefill_attention_mfma(hipStream_t s, int64_t hd, int64_t 
                                              int64_t nkv, float scale) {
 #define AESIR_PF_MMA(HDV, GV)                                                                                   \
     if (hd == HDV && G == GV) {                                                                                \
-        constexpr int BQ = 16 * kPfWaves / GV;                                                                 \
-        hipLaunchKernelGGL((prefill_attention_mfma_kernel<HDV, GV>), dim3((unsigned)((n + BQ - 1) / BQ), (unsigned)nkv), \
-                           dim3(kPfWaves * kWave), 0, s, Q, kc, vc, out, n, dim, kvd, p0, scale);              \
+        constexpr int BQ = 16 * kPfWaves / GV, KS = HDV == 64 ? kPfKeyGroups : 1;                              \
+        hipLaunchKernelGGL((prefill_attention_mfma_kernel<HDV, GV, KS>), dim3((unsigned)((n + BQ - 1) / BQ), (unsigned)nkv), \
+                           dim3(KS * kPfWaves * kWave), 0, s, Q, kc, vc, out, n, dim, kvd, p0, scale);         \
         AESIR_LAUNCH_CHECK("prefill_attention_mfma_kernel");                                                   \
         return AESIR_OK;                                                                                       \
     }

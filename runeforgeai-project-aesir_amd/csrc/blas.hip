@@ -34,6 +34,8 @@ struct BlasPlan {
     size_t ws = 0;
 };
 
+constexpr size_t kMaxPlans = 256;
+
 struct BlasState {
     hipblasLtHandle_t handle = nullptr;
     std::vector<BlasPlan> plans;
@@ -94,6 +96,11 @@ int32_t blas_gemm_nt(aesir_ctx *ctx, hipStream_t s, const void *A, int64_t M, in
     for (BlasPlan &p : st->plans)
         if (p.M == M && p.N == N && p.K == K && p.f32_out == f32_out) plan = &p;
     if (!plan) {
+        // every distinct chunk length brings its shapes: keep the most recent kMaxPlans
+        if (st->plans.size() >= kMaxPlans) {
+            destroy_plan(st->plans.front());
+            st->plans.erase(st->plans.begin());
+        }
         BlasPlan p;
         p.M = M, p.N = N, p.K = K, p.f32_out = f32_out;
         make_plan(st->handle, p, (size_t)ws_bytes);

@@ -141,10 +141,12 @@ def tl_weight_bytes(wtype: str) -> int:
 
 
 def prefill_bench(A, seed: int, n_prompt: int = 128, n_decode: int = 256, reps: int = 5, wtype: str = "f16") -> dict:
-    """Batched prefill of n_prompt positions on the TinyLlama shape (MFMA GEMMs; wall time of the
-    blocking aesir_prefill call, host launches included), then n_decode graph-replayed greedy steps.
-    wtype q8_0: Q8_0 matrices (weights for the GEMMs dequantized per fragment); a repacked type
-    (q4_0, q4_k, ...): the tiled planes, dequantized in registers by the wide-tile GEMM."""
+    """Batched prefill of n_prompt positions on the TinyLlama shape (one chunk up to 2048 rows: MFMA
+    GEMMs, or hipBLASLt from 256 rows on; wall time of the blocking aesir_prefill call, host launches
+    included), then n_decode graph-replayed greedy steps. wtype q8_0: Q8_0 matrices (weights
+    dequantized per fragment, or per chunk into an f16 copy for the library GEMMs); a repacked type
+    (q4_0, q4_k, ...): the tiled planes, dequantized in registers by the wide-tile GEMM, or per
+    chunk into the f16 copy."""
     ctx = A.Context(TL_WEIGHT_BYTES + (1 << 30))
     types = {"f16": A.GGML_F16, "q8_0": A.GGML_Q8_0, **QF_TYPES}
     m = A.Model.create(ctx, A.ModelConfig(TL["dim"], TL["layers"], TL["heads"], TL["kv_heads"], TL["ffn"],
@@ -678,12 +680,18 @@ def main():
     if not args.no_q8:
         out["q8_0"] = q8_bench(A, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters, use_graph)
         out["q8_0"]["prefill"] = prefill_bench(A, args.seed, n_decode=64, wtype="q8_0")
+        lp = prefill_bench(A, args.seed, n_prompt=1024, n_decode=0, wtype="q8_0")
+        out["q8_0"]["prefill"]["prompt_1024"] = {"prefill_ms": lp["prefill_ms"], "prefill_tok_s": lp["prefill_tok_s"]}
     if not args.no_quant:
         out["quant"] = {k: quant_bench(A, k, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters, use_graph)
                         for k in QUANT_KINDS}
         for k in ("q4_0", "q4_k"):  # the TinyLlama prefill with these weights (matrix-core GEMM on the planes)
             if k in out["quant"]:
                 out["quant"][k]["prefill"] = prefill_bench(A, args.seed, n_decode=64, wtype=k)
+                # a 1024-token prompt (one chunk: matrices dequantized to f16 for the library GEMMs)
+                lp = prefill_bench(A, args.seed, n_prompt=1024, n_decode=0, wtype=k)
+                out["quant"][k]["prefill"]["prompt_1024"] = {"prefill_ms": lp["prefill_ms"],
+                                                             "prefill_tok_s": lp["prefill_tok_s"]}
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.kv, args.cpu_reps)
         out["cpu_baseline"]["value"] = round(out["cpu_baseline"]["value"], 4)

@@ -8,10 +8,11 @@
 //             (descending logit key, index). Equal logits (-0 == +0) keep index order, which is the
 //             order the reference's stable insertion sort (:92-104) produces; every later stage of
 //             the stack sees an already sorted prefix, so one sort serves all of them
-//   tail      one workgroup: the exps in parallel, one LDS tile at a time, and the f32 running sums
-//             of apply_top_p, apply_min_p and the final draw in thread 0 in candidate order (f32
-//             addition is not associative; the sums must follow the reference's order to choose
-//             the same token)
+//   tail      one workgroup: the f32 running sums of apply_top_p, apply_min_p and the final draw
+//             in one lane in candidate order (f32 addition is not associative; the sums must follow
+//             the reference's order to choose the same token), with the next LDS tile of exps
+//             computed by the other waves meanwhile. The draw's inverse-CDF walk repeats the sum's
+//             running values, so the sum records one every 32 terms and the walk re-adds one block
 //   greedy    temperature <= 0 or top_k == 1: the first maximum of the sanitized, masked logits
 //
 // The random number comes from RuneRNG on the host (one draw per sampled token, consumed only
@@ -135,119 +136,154 @@ __global__ __launch_bounds__(1024) void sampler_greedy_kernel(const h16 *__restr
 }
 
 // Truncations and the draw over the candidate list: value i is vals[order ? order[i] : i].
-// Every running f32 sum of the reference is evaluated in candidate order by thread 0: the
-// workgroup computes a tile of kSeqTile exps in parallel into LDS, thread 0 consumes the tile in
-// index order, and the next tile follows.
-constexpr int kSeqTile = 8192;
+// Every running f32 sum of the reference is evaluated in candidate order by lane 0 of wave 0
+// (f32 addition is not associative, so the order fixes the token drawn). The terms come from
+// two LDS tiles: while lane 0 adds one tile, waves 1-3 compute the next tile's terms into the
+// other, so the exps cost nothing beside the serial adds.
+constexpr int kSeqTile = 4096;   // terms per LDS tile (two tiles)
+constexpr int kMarkBlock = 32;   // terms per recorded running sum of the final draw's sum
+
+// Lane 0's adds over one tile, acc += buf[e] for e in [0, cnt), 32 terms per block with the next
+// block's LDS reads in flight. kHit: stops at the first e with target <= acc (returned in hit,
+// -1 when none); a block is added first and re-added term by term only when the target falls
+// inside it (terms are >= 0, so acc never decreases). kMarks: marks[b] = acc after block b.
+template <bool kHit, bool kMarks>
+__device__ __forceinline__ float chain_tile(const float *buf, int cnt, float acc, float target, int &hit,
+                                            float *marks) {
+    const int nb = cnt / kMarkBlock;
+    f32x4 ra[8], rb[8];
+    auto load = [&](f32x4(&r)[8], int b) {
+#pragma unroll
+        for (int q = 0; q < 8; q++) r[q] = *reinterpret_cast<const f32x4 *>(&buf[kMarkBlock * b + 4 * q]);
+    };
+    auto add = [&](const f32x4(&r)[8], int b) -> bool {
+        float a = acc;
+#pragma unroll
+        for (int q = 0; q < 8; q++)
+#pragma unroll
+            for (int u = 0; u < 4; u++) a += r[q][u];
+        if (kHit && target <= a) {
+            float c = acc;
+#pragma unroll
+            for (int q = 0; q < 8; q++)
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    c += r[q][u];
+                    if (target <= c) {
+                        hit = kMarkBlock * b + 4 * q + u;
+                        acc = c;
+                        return true;
+                    }
+                }
+        }
+        acc = a;
+        if (kMarks) marks[b] = a;
+        return false;
+    };
+    hit = -1;
+    if (nb > 0) load(ra, 0);
+    for (int b = 0; b < nb; b += 2) {
+        if (b + 1 < nb) load(rb, b + 1);
+        if (add(ra, b)) return acc;
+        if (b + 1 < nb) {
+            if (b + 2 < nb) load(ra, b + 2);
+            if (add(rb, b + 1)) return acc;
+        }
+    }
+    for (int e = kMarkBlock * nb; e < cnt; e++) {  // the short last block of the last tile
+        acc += buf[e];
+        if (kHit && target <= acc) {
+            hit = e;
+            return acc;
+        }
+    }
+    if (kMarks && cnt % kMarkBlock) marks[nb] = acc;
+    return acc;
+}
+
+// acc_i = acc_{i-1} + term(i) in f32 over i in [0, m), m >= 1, in index order. Returns the first
+// i with target <= acc_i (m when none) under kHit, else m; the running sum where the chain
+// stopped goes to total (every thread). kMarks: marks[j] = acc at the end of term block j.
+// Enter and leave with the workgroup converged; tile0/tile1 and n_sh/f_sh are free on entry.
+template <bool kHit, bool kMarks, class Term>
+__device__ __forceinline__ int64_t ordered_chain(float *tile0, float *tile1, int64_t m, Term term, float target,
+                                                 float *marks, float &total, int64_t *n_sh, float *f_sh) {
+    const int tid = threadIdx.x;
+    const int64_t nt = (m + kSeqTile - 1) / kSeqTile;
+    auto tile_cnt = [&](int64_t k) -> int {
+        const int64_t r = m - k * kSeqTile;
+        return (int)(r < kSeqTile ? r : kSeqTile);
+    };
+    {
+        const int c = tile_cnt(0);
+        for (int e = tid; e < c; e += kTailThreads) tile0[e] = term((int64_t)e);
+    }
+    __syncthreads();
+    float acc = 0.0f;
+    int64_t hit = m;
+    for (int64_t k = 0; k < nt; k++) {
+        float *cur = (k & 1) ? tile1 : tile0;
+        float *nxt = (k & 1) ? tile0 : tile1;
+        if (tid < 64) {
+            if (tid == 0) {
+                int he;
+                acc = chain_tile<kHit, kMarks>(cur, tile_cnt(k), acc, target, he,
+                                               kMarks ? marks + k * (kSeqTile / kMarkBlock) : nullptr);
+                // two slots: the others read slot k&1 between barriers k and k+1, lane 0 writes
+                // slot (k+1)&1 only after barrier k
+                if (kHit) n_sh[k & 1] = he >= 0 ? k * kSeqTile + he : m;
+            }
+        } else if (k + 1 < nt) {
+            const int64_t base = (k + 1) * kSeqTile;
+            const int c = tile_cnt(k + 1);
+            for (int e = tid - 64; e < c; e += kTailThreads - 64) nxt[e] = term(base + e);
+        }
+        __syncthreads();
+        if (kHit) {
+            hit = n_sh[k & 1];
+            if (hit < m) break;
+        }
+    }
+    if (tid == 0) *f_sh = acc;
+    __syncthreads();
+    total = *f_sh;
+    __syncthreads();
+    return hit;
+}
+
 __global__ __launch_bounds__(kTailThreads) void sampler_tail_kernel(const float *__restrict__ vals,
                                                                     const int32_t *__restrict__ order, int64_t V,
-                                                                    SampleParams p, int64_t *out) {
-    __shared__ __align__(16) float tile[kSeqTile];
+                                                                    SampleParams p, float *__restrict__ marks,
+                                                                    int64_t *out) {
+    __shared__ __align__(16) float tile[2][kSeqTile];
     __shared__ float red[kTailThreads];
-    __shared__ int64_t n_sh;
+    __shared__ int64_t ired[kTailThreads];
+    __shared__ int64_t n_sh[2];
     __shared__ float f_sh;
     const int tid = threadIdx.x;
     auto val = [&](int64_t i) -> float { return vals[order ? order[i] : i]; };
     int64_t n = V;
     if (p.top_k > 0 && p.top_k < n) n = p.top_k;  // apply_top_k (:107-116)
 
-    // Ordered passes over e_i = exp_f32(val(i) - mx), i in [0, m), one LDS tile at a time.
-    auto fill = [&](int64_t t0, int cnt, float mx) {
-        for (int e = tid; e < cnt; e += kTailThreads) tile[e] = exp_f32(val(t0 + e) - mx);
-        __syncthreads();
-    };
-    // sum_i e_i in index order (thread 0), broadcast
-    auto seq_sum = [&](int64_t m, float mx) -> float {
-        float sum = 0.0f;
-        for (int64_t t0 = 0; t0 < m; t0 += kSeqTile) {
-            const int cnt = (int)(m - t0 < kSeqTile ? m - t0 : kSeqTile);
-            fill(t0, cnt, mx);
-            if (tid == 0) {
-                // 16 values per block, the next block's LDS reads issued before this block's adds
-                const int nb = cnt / 16;
-                f32x4 cur[4], nxt[4];
-                if (nb > 0)
-#pragma unroll
-                    for (int q = 0; q < 4; q++) cur[q] = *reinterpret_cast<const f32x4 *>(&tile[4 * q]);
-                for (int b = 0; b < nb; b++) {
-                    const int nbase = b + 1 < nb ? 16 * (b + 1) : 16 * b;
-#pragma unroll
-                    for (int q = 0; q < 4; q++) nxt[q] = *reinterpret_cast<const f32x4 *>(&tile[nbase + 4 * q]);
-#pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        sum += cur[q][0];
-                        sum += cur[q][1];
-                        sum += cur[q][2];
-                        sum += cur[q][3];
-                    }
-#pragma unroll
-                    for (int q = 0; q < 4; q++) cur[q] = nxt[q];
-                }
-                for (int e = 16 * nb; e < cnt; e++) sum += tile[e];
-            }
-            __syncthreads();
-        }
-        if (tid == 0) f_sh = sum;
-        __syncthreads();
-        const float r = f_sh;
-        __syncthreads();
-        return r;
-    };
-    // First i with target <= acc_i, acc_i = acc_{i-1} + term(e_i) in f32 (thread 0), or m. The
-    // terms are >= 0, so acc never decreases: a block of 16 is added first and rescanned term by
-    // term only when the target falls inside it.
-    auto seq_reach = [&](int64_t m, float mx, float target, auto term) -> int64_t {
-        float acc = 0.0f;
-        int64_t hit = m;
-        for (int64_t t0 = 0; t0 < m; t0 += kSeqTile) {
-            const int cnt = (int)(m - t0 < kSeqTile ? m - t0 : kSeqTile);
-            fill(t0, cnt, mx);
-            if (tid == 0) {
-                for (int b = 0; b < cnt && hit == m; b += 16) {
-                    const int be = b + 16 < cnt ? b + 16 : cnt;
-                    float a = acc;
-                    if (be - b == 16) {
-                        f32x4 v[4];
-#pragma unroll
-                        for (int q = 0; q < 4; q++) v[q] = *reinterpret_cast<const f32x4 *>(&tile[b + 4 * q]);
-#pragma unroll
-                        for (int q = 0; q < 4; q++)
-#pragma unroll
-                            for (int u = 0; u < 4; u++) a += term(v[q][u]);
-                    } else {
-                        for (int e = b; e < be; e++) a += term(tile[e]);
-                    }
-                    if (target <= a) {  // the crossing is in this block
-                        for (int e = b; e < be; e++) {
-                            acc += term(tile[e]);
-                            if (target <= acc) {
-                                hit = t0 + e;
-                                break;
-                            }
-                        }
-                    } else {
-                        acc = a;
-                    }
-                }
-                n_sh = hit;
-            }
-            __syncthreads();
-            hit = n_sh;
-            __syncthreads();
-            if (hit < m) break;
-        }
-        return hit;
-    };
-
     if (p.top_p < 1.0f && n > 1) {  // apply_top_p (:119-147): exps relative to the first (largest) logit
         const float mx = val(0);
-        const float sum = seq_sum(n, mx);
-        const int64_t cut = seq_reach(n, mx, p.top_p, [&](float e) { return sum > 0.0f ? e / sum : e; });
+        float sum, stop;
+        ordered_chain<false, false>(tile[0], tile[1], n, [&](int64_t i) { return exp_f32(val(i) - mx); }, 0.0f,
+                                    nullptr, sum, n_sh, &f_sh);
+        const int64_t cut = ordered_chain<true, false>(
+            tile[0], tile[1], n,
+            [&](int64_t i) {
+                const float e = exp_f32(val(i) - mx);
+                return sum > 0.0f ? e / sum : e;
+            },
+            p.top_p, nullptr, stop, n_sh, &f_sh);
         n = cut < n ? cut + 1 : n;
     }
     if (p.min_p > 0.0f && p.min_p < 1.0f && n > 1) {  // apply_min_p (:166-194)
         const float mx = val(0);
-        const float sum = seq_sum(n, mx);
+        float sum;
+        ordered_chain<false, false>(tile[0], tile[1], n, [&](int64_t i) { return exp_f32(val(i) - mx); }, 0.0f,
+                                    nullptr, sum, n_sh, &f_sh);
         const float e0 = exp_f32(0.0f);  // the first candidate's exp (val(0) - mx = 0)
         const float p0 = sum > 0.0f ? e0 / sum : e0;
         const float threshold = p.min_p * p0;
@@ -256,10 +292,11 @@ __global__ __launch_bounds__(kTailThreads) void sampler_tail_kernel(const float 
         int64_t kept = n;
         for (int64_t t0 = 0; t0 < n && kept == n; t0 += kSeqTile) {
             const int cnt = (int)(n - t0 < kSeqTile ? n - t0 : kSeqTile);
-            fill(t0, cnt, mx);
+            for (int e = tid; e < cnt; e += kTailThreads) tile[0][e] = exp_f32(val(t0 + e) - mx);
+            __syncthreads();
             int first = cnt;
             for (int e = tid; e < cnt; e += kTailThreads) {
-                const float pr = sum > 0.0f ? tile[e] / sum : tile[e];
+                const float pr = sum > 0.0f ? tile[0][e] / sum : tile[0][e];
                 if (!(pr >= threshold)) {
                     first = e;
                     break;
@@ -288,7 +325,9 @@ __global__ __launch_bounds__(kTailThreads) void sampler_tail_kernel(const float 
     }
     mx = red[0];
     __syncthreads();
-    const float sum_e = seq_sum(n, mx);
+    float sum_e;
+    ordered_chain<false, true>(tile[0], tile[1], n, [&](int64_t i) { return exp_f32(val(i) - mx); }, 0.0f, marks,
+                               sum_e, n_sh, &f_sh);
     const int64_t first = order ? order[0] : 0;
     if (!(sum_e > 0.0f)) {
         if (tid == 0) {
@@ -297,9 +336,38 @@ __global__ __launch_bounds__(kTailThreads) void sampler_tail_kernel(const float 
         }
         return;
     }
+    // The draw's running sum is the sum pass's running sum term for term (same terms, same order),
+    // so the first i with r <= acc_i lies in the first block whose recorded end sum reaches r;
+    // blocks ending below r form a prefix (acc never decreases) and are counted in parallel, and
+    // that block is re-added from the previous block's recorded sum.
     const float r = p.u * sum_e;
-    int64_t pick = seq_reach(n, mx, r, [](float e) { return e; });
-    if (pick >= n) pick = n - 1;
+    const int64_t nb = (n + kMarkBlock - 1) / kMarkBlock;
+    int64_t below = 0;
+    for (int64_t j = tid; j < nb; j += kTailThreads) below += marks[j] < r ? 1 : 0;
+    ired[tid] = below;
+    __syncthreads();
+    for (int st = kTailThreads / 2; st > 0; st >>= 1) {
+        if (tid < st) ired[tid] += ired[tid + st];
+        __syncthreads();
+    }
+    const int64_t jb = ired[0];
+    int64_t pick = n - 1;
+    if (jb < nb) {
+        const int64_t i0 = jb * kMarkBlock;
+        const int c = (int)(n - i0 < kMarkBlock ? n - i0 : kMarkBlock);
+        if (tid < c) tile[0][tid] = exp_f32(val(i0 + tid) - mx);
+        __syncthreads();
+        if (tid == 0) {
+            float acc = jb > 0 ? marks[jb - 1] : 0.0f;
+            for (int e = 0; e < c; e++) {
+                acc += tile[0][e];
+                if (r <= acc) {
+                    pick = i0 + e;
+                    break;
+                }
+            }
+        }
+    }
     if (tid == 0) {
         out[0] = order ? order[pick] : pick;
         out[1] = 1;
@@ -314,6 +382,7 @@ struct SamplerWork {
     float *vals = nullptr;
     uint32_t *keys = nullptr, *keys_out = nullptr;
     int32_t *idx = nullptr, *idx_out = nullptr;
+    float *marks = nullptr;    // the final draw's running sum at the end of every kMarkBlock terms
     int64_t *lists = nullptr;  // context tokens then suppress ids
     int64_t *result = nullptr;
     void *sort_tmp = nullptr;
@@ -321,8 +390,8 @@ struct SamplerWork {
 };
 
 static void free_work(SamplerWork *w) {
-    void *ps[] = {w->counts, w->mask, w->vals, w->keys, w->keys_out, w->idx, w->idx_out, w->lists,
-                  w->result, w->sort_tmp};
+    void *ps[] = {w->counts, w->mask, w->vals, w->keys, w->keys_out, w->idx, w->idx_out, w->marks,
+                  w->lists, w->result, w->sort_tmp};
     for (void *p : ps)
         if (p) (void)hipFree(p);
     *w = SamplerWork{};
@@ -355,6 +424,7 @@ static int32_t ensure_work(aesir_ctx *ctx, int64_t V, int64_t n_lists) {
         AESIR_HIP_TRY(hipMalloc((void **)&w->keys_out, (size_t)V * 4));
         AESIR_HIP_TRY(hipMalloc((void **)&w->idx, (size_t)V * 4));
         AESIR_HIP_TRY(hipMalloc((void **)&w->idx_out, (size_t)V * 4));
+        AESIR_HIP_TRY(hipMalloc((void **)&w->marks, (size_t)(V / kMarkBlock + 1) * 4));
         size_t bytes = 0;
         AESIR_HIP_TRY(rocprim::radix_sort_pairs(nullptr, bytes, w->keys, w->keys_out, w->idx, w->idx_out,
                                                 (unsigned)V, 0, 32, ctx->stream));
@@ -463,7 +533,7 @@ int32_t aesir_sample_token(aesir_ctx *ctx, const void *logits, int64_t vocab, co
                                                     (unsigned)vocab, 0, 32, s));
         }
         hipLaunchKernelGGL(sampler_tail_kernel, dim3(1), dim3(kTailThreads), 0, s, w->vals,
-                           p.sort ? (const int32_t *)w->idx_out : nullptr, vocab, p, w->result);
+                           p.sort ? (const int32_t *)w->idx_out : nullptr, vocab, p, w->marks, w->result);
         AESIR_LAUNCH_CHECK("sampler_tail_kernel");
         st = peek;
     }

@@ -1,8 +1,9 @@
 """GPU parity of the sampler stack (aesir_sample_token, sample_token_from_logits at
 core/sampler.mojo:217-305) against the CPU oracle: the sampled token and the RuneRNG state must be
 identical, draw after draw, for every stage combination (greedy branch, penalties, temperature,
-top-k, top-p, min-p, suppress list), at vocabulary sizes from 512 to 128256, with many tied logits
-so the stable-sort order is exercised. Both sides compute exp as the correctly rounded f32 value
+top-k, top-p, min-p, suppress list), at vocabulary sizes from 512 to 128256 (1000 and 4099 end
+in a short block of the draw's recorded running sums, 4099 also in a short LDS tile), with many
+tied logits so the stable-sort order is exercised. Both sides compute exp as the correctly rounded f32 value
 and keep the reference's sequential f32 sums, so equality is exact."""
 import numpy as np
 import pytest
@@ -46,7 +47,7 @@ CONFIGS = [
 ]
 
 
-@pytest.mark.parametrize("vocab", [512, 32000, 128256])
+@pytest.mark.parametrize("vocab", [512, 1000, 4099, 32000, 128256])
 @pytest.mark.parametrize("cfgd", CONFIGS)
 def test_sampler_matches_oracle(A, ctx, oracle, vocab, cfgd):
     rng = np.random.default_rng(vocab + len(cfgd))

@@ -8,15 +8,18 @@
 //             (descending logit key, index). Equal logits (-0 == +0) keep index order, which is the
 //             order the reference's stable insertion sort (:92-104) produces; every later stage of
 //             the stack sees an already sorted prefix, so one sort serves all of them
-//   tail      one workgroup: the f32 running sums of apply_top_p, apply_min_p and the final draw
-//             in one lane in candidate order (f32 addition is not associative; the sums must follow
-//             the reference's order to choose the same token), with the next LDS tile of exps
-//             computed by the other waves meanwhile. The draw's inverse-CDF walk repeats the sum's
-//             running values, so the sum records one every 32 terms and the walk re-adds one block
+//   tail      one workgroup: the f32 running sums of apply_top_p and apply_min_p in one lane in
+//             candidate order (f32 addition is not associative; the sums must follow the
+//             reference's order to choose the same cut), with the next LDS tile of exps computed
+//             by the other waves meanwhile
+//   draw      the final draw: chunk maxima, exps and per-chunk binade increments over the whole
+//             device, then one wave that reproduces the sequential f32 sum bit for bit with one
+//             integer add per chunk where no rounding depends on the order, and the inverse-CDF
+//             walk over one recorded chunk
 //   greedy    temperature <= 0 or top_k == 1: the first maximum of the sanitized, masked logits
 //
 // The random number comes from RuneRNG on the host (one draw per sampled token, consumed only
-// when the reference consumes it: a positive final sum). exp is evaluated as the correctly
+// when the reference consumes it: a final sum that is not <= 0, NaN included). exp is evaluated as the correctly
 // rounded f32 value (f64 exp rounded once) so that the CPU oracle computes the same bits.
 #include <cstring>
 #include <rocprim/device/device_radix_sort.hpp>
@@ -48,6 +51,7 @@ struct SampleParams {
     float top_p;    // < 1: nucleus
     float min_p;    // in (0, 1): min-p
     float u;        // RuneRNG.next_float32 for the draw
+    int draw_here;  // top_k <= kSeqTile: the tail kernel makes the final draw itself
 };
 
 __global__ void sampler_clear_kernel(int32_t *__restrict__ counts, uint8_t *__restrict__ mask, int64_t V) {
@@ -135,26 +139,24 @@ __global__ __launch_bounds__(1024) void sampler_greedy_kernel(const h16 *__restr
     }
 }
 
-// Truncations and the draw over the candidate list: value i is vals[order ? order[i] : i].
-// Every running f32 sum of the reference is evaluated in candidate order by lane 0 of wave 0
-// (f32 addition is not associative, so the order fixes the token drawn). The terms come from
-// two LDS tiles: while lane 0 adds one tile, waves 1-3 compute the next tile's terms into the
-// other, so the exps cost nothing beside the serial adds.
-constexpr int kSeqTile = 4096;   // terms per LDS tile (two tiles)
-constexpr int kMarkBlock = 32;   // terms per recorded running sum of the final draw's sum
+// Truncations over the candidate list: value i is vals[order ? order[i] : i]. The running f32
+// sums of apply_top_p and apply_min_p are evaluated in candidate order by lane 0 of wave 0 (f32
+// addition is not associative, so the order fixes the cut). The terms come from two LDS tiles:
+// while lane 0 adds one tile, waves 1-3 compute the next tile's terms into the other.
+constexpr int kSeqTile = 4096;  // terms per LDS tile (two tiles)
+constexpr int kSeqBlock = 32;   // terms per block of lane 0's adds
 
 // Lane 0's adds over one tile, acc += buf[e] for e in [0, cnt), 32 terms per block with the next
 // block's LDS reads in flight. kHit: stops at the first e with target <= acc (returned in hit,
 // -1 when none); a block is added first and re-added term by term only when the target falls
-// inside it (terms are >= 0, so acc never decreases). kMarks: marks[b] = acc after block b.
-template <bool kHit, bool kMarks>
-__device__ __forceinline__ float chain_tile(const float *buf, int cnt, float acc, float target, int &hit,
-                                            float *marks) {
-    const int nb = cnt / kMarkBlock;
+// inside it (terms are >= 0, so acc never decreases).
+template <bool kHit>
+__device__ __forceinline__ float chain_tile(const float *buf, int cnt, float acc, float target, int &hit) {
+    const int nb = cnt / kSeqBlock;
     f32x4 ra[8], rb[8];
     auto load = [&](f32x4(&r)[8], int b) {
 #pragma unroll
-        for (int q = 0; q < 8; q++) r[q] = *reinterpret_cast<const f32x4 *>(&buf[kMarkBlock * b + 4 * q]);
+        for (int q = 0; q < 8; q++) r[q] = *reinterpret_cast<const f32x4 *>(&buf[kSeqBlock * b + 4 * q]);
     };
     auto add = [&](const f32x4(&r)[8], int b) -> bool {
         float a = acc;
@@ -170,14 +172,13 @@ __device__ __forceinline__ float chain_tile(const float *buf, int cnt, float acc
                 for (int u = 0; u < 4; u++) {
                     c += r[q][u];
                     if (target <= c) {
-                        hit = kMarkBlock * b + 4 * q + u;
+                        hit = kSeqBlock * b + 4 * q + u;
                         acc = c;
                         return true;
                     }
                 }
         }
         acc = a;
-        if (kMarks) marks[b] = a;
         return false;
     };
     hit = -1;
@@ -190,24 +191,23 @@ __device__ __forceinline__ float chain_tile(const float *buf, int cnt, float acc
             if (add(rb, b + 1)) return acc;
         }
     }
-    for (int e = kMarkBlock * nb; e < cnt; e++) {  // the short last block of the last tile
+    for (int e = kSeqBlock * nb; e < cnt; e++) {  // the short last block of the last tile
         acc += buf[e];
         if (kHit && target <= acc) {
             hit = e;
             return acc;
         }
     }
-    if (kMarks && cnt % kMarkBlock) marks[nb] = acc;
     return acc;
 }
 
 // acc_i = acc_{i-1} + term(i) in f32 over i in [0, m), m >= 1, in index order. Returns the first
 // i with target <= acc_i (m when none) under kHit, else m; the running sum where the chain
-// stopped goes to total (every thread). kMarks: marks[j] = acc at the end of term block j.
-// Enter and leave with the workgroup converged; tile0/tile1 and n_sh/f_sh are free on entry.
-template <bool kHit, bool kMarks, class Term>
+// stopped goes to total (every thread). Enter and leave with the workgroup converged;
+// tile0/tile1 and n_sh/f_sh are free on entry.
+template <bool kHit, class Term>
 __device__ __forceinline__ int64_t ordered_chain(float *tile0, float *tile1, int64_t m, Term term, float target,
-                                                 float *marks, float &total, int64_t *n_sh, float *f_sh) {
+                                                 float &total, int64_t *n_sh, float *f_sh) {
     const int tid = threadIdx.x;
     const int64_t nt = (m + kSeqTile - 1) / kSeqTile;
     auto tile_cnt = [&](int64_t k) -> int {
@@ -227,8 +227,7 @@ __device__ __forceinline__ int64_t ordered_chain(float *tile0, float *tile1, int
         if (tid < 64) {
             if (tid == 0) {
                 int he;
-                acc = chain_tile<kHit, kMarks>(cur, tile_cnt(k), acc, target, he,
-                                               kMarks ? marks + k * (kSeqTile / kMarkBlock) : nullptr);
+                acc = chain_tile<kHit>(cur, tile_cnt(k), acc, target, he);
                 // two slots: the others read slot k&1 between barriers k and k+1, lane 0 writes
                 // slot (k+1)&1 only after barrier k
                 if (kHit) n_sh[k & 1] = he >= 0 ? k * kSeqTile + he : m;
@@ -251,13 +250,19 @@ __device__ __forceinline__ int64_t ordered_chain(float *tile0, float *tile1, int
     return hit;
 }
 
+// Candidate count after apply_top_k, apply_top_p and apply_min_p, for the final draw's kernels,
+// and the count of chunks the draw's records kernel lists as likely slow.
+struct DrawHdr {
+    int64_t n;
+    uint32_t n_slow;
+    uint32_t pad;
+};
+
 __global__ __launch_bounds__(kTailThreads) void sampler_tail_kernel(const float *__restrict__ vals,
                                                                     const int32_t *__restrict__ order, int64_t V,
-                                                                    SampleParams p, float *__restrict__ marks,
-                                                                    int64_t *out) {
+                                                                    SampleParams p, DrawHdr *hdr, int64_t *out) {
     __shared__ __align__(16) float tile[2][kSeqTile];
     __shared__ float red[kTailThreads];
-    __shared__ int64_t ired[kTailThreads];
     __shared__ int64_t n_sh[2];
     __shared__ float f_sh;
     const int tid = threadIdx.x;
@@ -268,22 +273,22 @@ __global__ __launch_bounds__(kTailThreads) void sampler_tail_kernel(const float 
     if (p.top_p < 1.0f && n > 1) {  // apply_top_p (:119-147): exps relative to the first (largest) logit
         const float mx = val(0);
         float sum, stop;
-        ordered_chain<false, false>(tile[0], tile[1], n, [&](int64_t i) { return exp_f32(val(i) - mx); }, 0.0f,
-                                    nullptr, sum, n_sh, &f_sh);
-        const int64_t cut = ordered_chain<true, false>(
+        ordered_chain<false>(tile[0], tile[1], n, [&](int64_t i) { return exp_f32(val(i) - mx); }, 0.0f, sum, n_sh,
+                             &f_sh);
+        const int64_t cut = ordered_chain<true>(
             tile[0], tile[1], n,
             [&](int64_t i) {
                 const float e = exp_f32(val(i) - mx);
                 return sum > 0.0f ? e / sum : e;
             },
-            p.top_p, nullptr, stop, n_sh, &f_sh);
+            p.top_p, stop, n_sh, &f_sh);
         n = cut < n ? cut + 1 : n;
     }
     if (p.min_p > 0.0f && p.min_p < 1.0f && n > 1) {  // apply_min_p (:166-194)
         const float mx = val(0);
         float sum;
-        ordered_chain<false, false>(tile[0], tile[1], n, [&](int64_t i) { return exp_f32(val(i) - mx); }, 0.0f,
-                                    nullptr, sum, n_sh, &f_sh);
+        ordered_chain<false>(tile[0], tile[1], n, [&](int64_t i) { return exp_f32(val(i) - mx); }, 0.0f, sum, n_sh,
+                             &f_sh);
         const float e0 = exp_f32(0.0f);  // the first candidate's exp (val(0) - mx = 0)
         const float p0 = sum > 0.0f ? e0 / sum : e0;
         const float threshold = p.min_p * p0;
@@ -313,8 +318,15 @@ __global__ __launch_bounds__(kTailThreads) void sampler_tail_kernel(const float 
         }
         n = kept > 0 ? kept : n;
     }
-
-    // final draw (:284-305): max over the candidates, exps, sequential sum, inverse CDF
+    if (!p.draw_here) {
+        if (tid == 0) {
+            hdr->n = n;
+            hdr->n_slow = 0;
+        }
+        return;
+    }
+    // At most kSeqTile candidates: the final draw (:284-305) here, its exps in one LDS tile and
+    // both running sums (sum_e, then the inverse-CDF walk) in lane 0 in candidate order.
     float mx = -INFINITY;
     for (int64_t i = tid; i < n; i += kTailThreads) mx = fmaxf(mx, val(i));
     red[tid] = mx;
@@ -324,48 +336,536 @@ __global__ __launch_bounds__(kTailThreads) void sampler_tail_kernel(const float 
         __syncthreads();
     }
     mx = red[0];
+    for (int e = tid; e < (int)n; e += kTailThreads) tile[0][e] = exp_f32(val(e) - mx);
     __syncthreads();
-    float sum_e;
-    ordered_chain<false, true>(tile[0], tile[1], n, [&](int64_t i) { return exp_f32(val(i) - mx); }, 0.0f, marks,
-                               sum_e, n_sh, &f_sh);
-    const int64_t first = order ? order[0] : 0;
-    if (!(sum_e > 0.0f)) {
+    if (tid == 0) {
+        int he;
+        const float sum_e = chain_tile<false>(tile[0], (int)n, 0.0f, 0.0f, he);
+        if (sum_e <= 0.0f) {  // a NaN sum goes on to the walk, as in the reference
+            out[0] = order ? order[0] : 0;
+            out[1] = 0;
+        } else {
+            const float r = p.u * sum_e;
+            chain_tile<true>(tile[0], (int)n, 0.0f, r, he);
+            const int64_t pick = he >= 0 ? he : n - 1;
+            out[0] = order ? order[pick] : pick;
+            out[1] = 1;
+        }
+    }
+}
+
+// ------------------------------------------------------------------ the final draw (:284-305)
+//
+// max over the candidates, e_i = exp(x_i - max), sum_e = the f32 running sum of the e_i in
+// candidate order, r = u * sum_e, and the first i whose running sum reaches r.
+//
+// The running sum acc_i = fl(acc_{i-1} + e_i) is evaluated exactly without one add per term. While
+// acc stays in one binade [2^E, 2^(E+1)) its bit pattern counts ulps u = 2^(E-23), and for a term
+// e >= 0, fl(acc + e) = acc + RN(e / u) ulps, unless e / u lies exactly halfway between two
+// integers (the parity of acc then decides) or the result leaves the binade. So for a block of
+// terms and a binade E, K_E = sum RN(e / u) is the exact advance of acc's bit pattern whenever acc
+// enters the block in binade E, no term of the block is a halfway case for E and mantissa(acc) +
+// K_E < 2^23, i.e. whenever acc's bits lie in [E's first pattern, E's last pattern - K_E]. These
+// increments are computed for every block in parallel for the two binades that an f64 estimate of
+// the running sum puts the chunk in (E_a and E_a + 1); one wave then walks the chunks in order,
+// advancing acc by one range test and one integer add per chunk where the conditions hold, else
+// per 32-term block, else by re-adding the block's terms one by one. Every value it produces is
+// the sequential sum's value at that index, bit for bit. The running sum at the start of every
+// batch of kBatch chunks is recorded; the draw's walk (the same terms in the same order, so the
+// same running sums) finds its batch from these in parallel, steps through at most kBatch chunks
+// of it the same way, and re-adds one chunk term by term.
+constexpr int kDrawThreads = 256;
+constexpr int kDrawChunk = 256;                      // terms per chunk (one workgroup of the parallel kernels)
+constexpr int kDrawSub = 32;                         // terms per block inside a chunk
+constexpr int kDrawSubs = kDrawChunk / kDrawSub;     // 8
+constexpr int kHeadWords = 8;                        // per chunk: lo, span, K for E_a and E_a + 1; E_a; flags
+constexpr int kBlockWords = 6;                       // per block: lo, span, K for E_a and E_a + 1
+constexpr int kSubWords = kBlockWords * kDrawSubs;   // per chunk: its blocks' ranges (48 words)
+constexpr int kBatch = 64 / kHeadWords;              // chunk headers per vector load of the walk (8)
+constexpr int kRoundBatches = 64;                    // header batches staged in LDS per round of the walk
+constexpr int kStage = 32;                           // likely-slow chunks staged in LDS for the walk (<= 64)
+constexpr int kNoBinade = -1000;                     // E_a of a chunk without an estimate
+constexpr uint32_t kUlpCap = 1u << 24;               // saturated increment (fails every mantissa check)
+constexpr uint32_t kLikelySlow = 1u << 16;           // header flag: the chunk may need its blocks
+constexpr int kSlowListMax = 4096;                   // likely-slow chunk ids the records kernel lists
+static_assert(kDrawThreads == kDrawChunk, "one thread per term of a chunk");
+static_assert(kDrawSubs <= 8, "block flags take 8 bits per binade");
+
+__device__ __forceinline__ float block_max_f32(float v, float *sh) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    const int w = threadIdx.x / 64;
+    if ((threadIdx.x & 63) == 0) sh[w] = v;
+    __syncthreads();
+    v = sh[0];
+    for (int k = 1; k < kDrawThreads / 64; k++) v = fmaxf(v, sh[k]);
+    __syncthreads();
+    return v;
+}
+
+__device__ __forceinline__ double block_sum_f64(double v, double *sh) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    const int w = threadIdx.x / 64;
+    if ((threadIdx.x & 63) == 0) sh[w] = v;
+    __syncthreads();
+    v = sh[0];
+    for (int k = 1; k < kDrawThreads / 64; k++) v += sh[k];
+    __syncthreads();
+    return v;
+}
+
+// Per-chunk maxima of the candidates (fmaxf: a NaN candidate is skipped here, and it makes sum_e
+// NaN whatever the maximum, as it does in the reference).
+__global__ __launch_bounds__(kDrawThreads) void sampler_chunk_max_kernel(const float *__restrict__ vals,
+                                                                         const int32_t *__restrict__ order,
+                                                                         const DrawHdr *__restrict__ hdr,
+                                                                         float *__restrict__ cmax) {
+    __shared__ float sh[kDrawThreads / 64];
+    const int64_t n = hdr->n;
+    const int64_t base = (int64_t)blockIdx.x * kDrawChunk;
+    if (base >= n) return;
+    const int64_t i = base + threadIdx.x;
+    float v = -INFINITY;
+    if (i < n) v = vals[order ? order[i] : i];
+    v = block_max_f32(v, sh);
+    if (threadIdx.x == 0) cmax[blockIdx.x] = v;
+}
+
+// e_i = exp(x_i - max) for one chunk, and the chunk's f64 sum (an estimate for the binades).
+__global__ __launch_bounds__(kDrawThreads) void sampler_terms_kernel(const float *__restrict__ vals,
+                                                                     const int32_t *__restrict__ order,
+                                                                     const DrawHdr *__restrict__ hdr,
+                                                                     const float *__restrict__ cmax,
+                                                                     float *__restrict__ terms,
+                                                                     double *__restrict__ csum) {
+    __shared__ float shf[kDrawThreads / 64];
+    __shared__ double shd[kDrawThreads / 64];
+    const int64_t n = hdr->n;
+    const int64_t base = (int64_t)blockIdx.x * kDrawChunk;
+    if (base >= n) return;
+    const int64_t nch = (n + kDrawChunk - 1) / kDrawChunk;
+    float mx = -INFINITY;
+    for (int64_t c = threadIdx.x; c < nch; c += kDrawThreads) mx = fmaxf(mx, cmax[c]);
+    mx = block_max_f32(mx, shf);
+    const int64_t i = base + threadIdx.x;
+    float t = 0.0f;
+    if (i < n) {
+        t = exp_f32(vals[order ? order[i] : i] - mx);
+        terms[i] = t;
+    }
+    const double s = block_sum_f64((double)t, shd);
+    if (threadIdx.x == 0) csum[blockIdx.x] = s;
+}
+
+// RN(t / 2^(E-23)) for E in [-100, 101], with the halfway flag. NaN, infinite or negative terms
+// are flagged so that their block is re-added; increments of 2^24 or more saturate.
+__device__ __forceinline__ uint32_t ulps_of(float t, int E, bool &half) {
+    if (!(t >= 0.0f) || isinf(t)) {
+        half = true;
+        return kUlpCap;
+    }
+    const double x = ldexp((double)t, 23 - E);
+    half = false;
+    if (x >= 16777216.0) return kUlpCap;
+    const double f = floor(x);
+    const double r = x - f;  // exact: x carries at most 24 significant bits
+    half = r == 0.5;
+    return (uint32_t)f + (r > 0.5 ? 1u : 0u);
+}
+
+// One chunk's header and its blocks' ranges. E_a comes from the f64 running-sum estimate at
+// the chunk's start, shifted down by 1/64 so that E_a or E_a + 1 holds the true sum (the
+// sequential f32 sum of k terms is within k * 2^-24 of the exact one). Header: for E_a and
+// E_a + 1, the first bit pattern lo, the span of patterns from which the chunk-wide increment K
+// applies, and K (an empty range, lo = 0xFFFFFFFF with span 0 and K 0, when a halfway term or the
+// missing estimate rules the binade out); then E_a; then the blocks' halfway flags (bits 0-7 for
+// E_a, 8-15 for E_a + 1) and kLikelySlow when the estimate over the chunk, widened by its typical
+// error (2^-12), straddles a binade boundary (or there is no estimate, or a halfway term); such a
+// chunk is also appended to slow_list (any order), which only decides what the walk stages in
+// LDS. Each 32-term block gets the same six words for its own increments.
+__global__ __launch_bounds__(kDrawThreads) void sampler_records_kernel(const float *__restrict__ terms,
+                                                                       const double *__restrict__ csum,
+                                                                       DrawHdr *__restrict__ hdr_rw,
+                                                                       uint32_t *__restrict__ heads,
+                                                                       uint32_t *__restrict__ subk,
+                                                                       uint32_t *__restrict__ slow_list) {
+    __shared__ double shd[kDrawThreads / 64];
+    __shared__ uint32_t ka_s[kDrawSubs], kb_s[kDrawSubs], half_s[kDrawSubs];
+    const int64_t n = hdr_rw->n;
+    const int64_t base = (int64_t)blockIdx.x * kDrawChunk;
+    if (base >= n) return;
+    const int tid = threadIdx.x;
+    double s = 0.0;
+    for (int64_t c = tid; c < (int64_t)blockIdx.x; c += kDrawThreads) s += csum[c];
+    s = block_sum_f64(s, shd);
+    const double s_end = s + csum[blockIdx.x];
+    int Ea = kNoBinade;
+    bool straddle = true;
+    if (s > 0.0 && s < 1e30) {
+        const int e = ilogb(s * (1.0 - 1.0 / 64));
+        if (e >= -100 && e <= 100) {
+            Ea = e;
+            straddle = !(s_end < 1e30) || ilogb(s * (1.0 - 1.0 / 4096)) != ilogb(s_end * (1.0 + 1.0 / 4096));
+        }
+    }
+    uint32_t qa = 0, qb = 0;
+    bool ha = false, hb = false;
+    const int64_t i = base + tid;
+    if (i < n && Ea != kNoBinade) {
+        const float t = terms[i];
+        qa = ulps_of(t, Ea, ha);
+        qb = ulps_of(t, Ea + 1, hb);
+    }
+    // 32-term blocks are half waves: sums (each term <= 2^24, so a block < 2^29) and flags
+    for (int o = 16; o > 0; o >>= 1) {
+        qa += __shfl_xor(qa, o);
+        qb += __shfl_xor(qb, o);
+    }
+    const uint64_t ba = __ballot(ha), bb = __ballot(hb);
+    const int lane = tid & 63;
+    if ((lane & 31) == 0) {
+        const int sb = tid / kDrawSub;
+        const uint32_t ka = qa < kUlpCap ? qa : kUlpCap, kb = qb < kUlpCap ? qb : kUlpCap;
+        const bool half_a = (uint32_t)(ba >> lane) != 0u, half_b = (uint32_t)(bb >> lane) != 0u;
+        ka_s[sb] = ka;
+        kb_s[sb] = kb;
+        half_s[sb] = (half_a ? 1u : 0u) | (half_b ? 2u : 0u);
+        const bool ok_a = Ea != kNoBinade && !half_a && ka <= 0x7FFFFFu;
+        const bool ok_b = Ea != kNoBinade && !half_b && kb <= 0x7FFFFFu;
+        uint32_t *r = subk + (int64_t)blockIdx.x * kSubWords + sb * kBlockWords;
+        r[0] = ok_a ? (uint32_t)(Ea + 127) << 23 : 0xFFFFFFFFu;
+        r[1] = ok_a ? 0x7FFFFFu - ka : 0u;
+        r[2] = ok_a ? ka : 0u;
+        r[3] = ok_b ? (uint32_t)(Ea + 128) << 23 : 0xFFFFFFFFu;
+        r[4] = ok_b ? 0x7FFFFFu - kb : 0u;
+        r[5] = ok_b ? kb : 0u;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t ka = 0, kb = 0, fl = 0;
+        for (int k = 0; k < kDrawSubs; k++) {
+            ka += ka_s[k];
+            kb += kb_s[k];
+            fl |= (half_s[k] & 1u) << k;
+            fl |= ((half_s[k] >> 1) & 1u) << (8 + k);
+        }
+        const bool ok_a = Ea != kNoBinade && (fl & 0xFFu) == 0u && ka <= 0x7FFFFFu;
+        const bool ok_b = Ea != kNoBinade && (fl & 0xFF00u) == 0u && kb <= 0x7FFFFFu;
+        if (straddle || (fl & 0xFFFFu) != 0u) {
+            fl |= kLikelySlow;
+            const uint32_t k = atomicAdd(&hdr_rw->n_slow, 1u);
+            if (k < (uint32_t)kSlowListMax) slow_list[k] = blockIdx.x;
+        }
+        uint32_t *h = heads + (int64_t)blockIdx.x * kHeadWords;
+        h[0] = ok_a ? (uint32_t)(Ea + 127) << 23 : 0xFFFFFFFFu;
+        h[1] = ok_a ? 0x7FFFFFu - ka : 0u;
+        h[2] = ok_a ? ka : 0u;
+        h[3] = ok_b ? (uint32_t)(Ea + 128) << 23 : 0xFFFFFFFFu;
+        h[4] = ok_b ? 0x7FFFFFu - kb : 0u;
+        h[5] = ok_b ? kb : 0u;
+        h[6] = (uint32_t)Ea;
+        h[7] = fl;
+    }
+}
+
+// The walk and the draw. The walk goes round by round, kRoundBatches batches of kBatch chunks
+// at a time. For each round the workgroup stages the chunk headers in LDS, reduces every batch to
+// one header of the same form (a range and an increment for each binade, valid when every chunk
+// of the batch has one for the first chunk's binade; the chunks' tests then all hold exactly when
+// the batch's holds), and stages the block ranges and terms of the round's chunks on the
+// likely-slow list.
+// Wave 0 then walks the round on scalar registers: a batch header or a chunk's header is read into
+// one VGPR, one word per lane, and taken apart with readlane.
+__global__ __launch_bounds__(kDrawThreads) void sampler_draw_kernel(const float *__restrict__ terms,
+                                                                    const uint32_t *__restrict__ heads,
+                                                                    const uint32_t *__restrict__ subk,
+                                                                    const uint32_t *__restrict__ slow_list,
+                                                                    const DrawHdr *__restrict__ hdr,
+                                                                    const int32_t *__restrict__ order, float u,
+                                                                    uint32_t *__restrict__ marks,
+                                                                    int64_t *__restrict__ out) {
+    constexpr int kRoundWords = kRoundBatches * 64;
+    __shared__ __align__(16) uint32_t rh[kRoundWords];
+    __shared__ uint32_t ragg[kRoundBatches * kHeadWords];
+    __shared__ __align__(16) float st_terms[kStage * kDrawChunk];
+    __shared__ uint32_t st_subk[kStage * kSubWords];
+    __shared__ int st_id[kStage];
+    __shared__ __align__(16) float tile[kDrawChunk];
+    __shared__ int st_n, wcnt[kDrawThreads / 64];
+    __shared__ uint32_t sum_bits, start_bits;
+    __shared__ int64_t chunk_s;
+    __shared__ int64_t cnt_s[kDrawThreads / 64];
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
+    const int lane = tid & 63;
+    const int64_t n = hdr->n;
+    const int64_t nch = (n + kDrawChunk - 1) / kDrawChunk;
+    const int64_t nbat = (nch + kBatch - 1) / kBatch;  // heads holds nbat whole batches
+    const int n_list = (int)(hdr->n_slow < (uint32_t)kSlowListMax ? hdr->n_slow : (uint32_t)kSlowListMax);
+
+    // Stages round b0's headers, batch headers and likely-slow chunks; returns the batch count.
+    auto stage_round = [&](int64_t b0) -> int {
+        const int nb = (int)(nbat - b0 < kRoundBatches ? nbat - b0 : kRoundBatches);
+        const int64_t c_lo = b0 * kBatch, c_hi = (b0 + nb) * kBatch;
+        uint32_t first_ids = tid < n_list ? slow_list[tid] : 0xFFFFFFFFu;  // in flight with the headers
+        {  // headers: independent 16-byte loads, all in flight together
+            const u32x4 *src = reinterpret_cast<const u32x4 *>(heads + b0 * 64);
+            u32x4 *dst = reinterpret_cast<u32x4 *>(rh);
+            constexpr int kPer = kRoundWords / 4 / kDrawThreads;
+            u32x4 v[kPer];
+#pragma unroll
+            for (int j = 0; j < kPer; j++) {
+                const int k = j * kDrawThreads + tid;
+                if (k < nb * 16) v[j] = src[k];
+            }
+#pragma unroll
+            for (int j = 0; j < kPer; j++) {
+                const int k = j * kDrawThreads + tid;
+                if (k < nb * 16) dst[k] = v[j];
+            }
+        }
+        if (tid == 0) st_n = 0;
+        __syncthreads();
+        // batch headers, one wave per batch; lane = chunk q * kHeadWords + word w
+        const int w = lane & (kHeadWords - 1), q = lane / kHeadWords;
+        for (int bi = wave; bi < nb; bi += kDrawThreads / 64) {
+            const int64_t cb = (b0 + bi) * kBatch;
+            const int qn = (int)(nch - cb < kBatch ? nch - cb : kBatch);
+            const uint32_t v = rh[bi * 64 + lane];
+            uint32_t res = 0;
+            for (int wl = 0; wl < 6; wl += 3) {
+                const uint32_t lo0 = __shfl(v, wl);
+                const bool bad = __ballot(w == wl && q < qn && v != lo0) != 0u;
+                uint32_t kk = (w == wl + 2 && q < qn) ? v : 0u;
+                kk += __shfl_xor(kk, 8);
+                kk += __shfl_xor(kk, 16);
+                kk += __shfl_xor(kk, 32);
+                const uint32_t ks = __shfl(kk, wl + 2);
+                const bool ok = !bad && lo0 != 0xFFFFFFFFu && ks <= 0x7FFFFFu;
+                if (lane == wl) res = ok ? lo0 : 0xFFFFFFFFu;
+                if (lane == wl + 1) res = ok ? 0x7FFFFFu - ks : 0u;
+                if (lane == wl + 2) res = ok ? ks : 0u;
+            }
+            if (lane < kHeadWords) ragg[bi * kHeadWords + lane] = res;
+        }
+        // the round's chunks on the likely-slow list, up to kStage of them
+        for (int e0 = 0; e0 < n_list; e0 += kDrawThreads) {
+            const int base_n = st_n;
+            if (base_n >= kStage) break;
+            const uint32_t id = e0 == 0 ? first_ids : (e0 + tid < n_list ? slow_list[e0 + tid] : 0xFFFFFFFFu);
+            const bool f = e0 + tid < n_list && (int64_t)id >= c_lo && (int64_t)id < c_hi && (int64_t)id < nch;
+            const uint64_t bal = __ballot(f);
+            if (lane == 0) wcnt[wave] = __popcll(bal);
+            __syncthreads();
+            int before = base_n;
+            for (int k = 0; k < wave; k++) before += wcnt[k];
+            const int slot = before + __popcll(bal & ((1ull << lane) - 1ull));
+            if (f && slot < kStage) st_id[slot] = (int)id;
+            __syncthreads();
+            if (tid == 0) {
+                int tot = base_n;
+                for (int k = 0; k < kDrawThreads / 64; k++) tot += wcnt[k];
+                st_n = tot < kStage ? tot : kStage;
+            }
+            __syncthreads();
+        }
+        const int nst = st_n;
+        {  // their terms (four per thread per load) and block ranges, loads all in flight
+            constexpr int kPer = kStage * kDrawChunk / 4 / kDrawThreads;
+            f32x4 v[kPer];
+#pragma unroll
+            for (int j = 0; j < kPer; j++) {
+                const int k = j * kDrawThreads + tid;  // float4 index: slot k / 64, offset 4 * (k % 64)
+                if (k < nst * (kDrawChunk / 4)) {
+                    const int64_t i = (int64_t)st_id[k / (kDrawChunk / 4)] * kDrawChunk + 4 * (k % (kDrawChunk / 4));
+                    v[j] = i + 4 <= n ? *reinterpret_cast<const f32x4 *>(terms + i)
+                                      : f32x4{i < n ? terms[i] : 0.0f, i + 1 < n ? terms[i + 1] : 0.0f,
+                                              i + 2 < n ? terms[i + 2] : 0.0f, 0.0f};
+                }
+            }
+            uint32_t sk[kStage * kSubWords / kDrawThreads];
+#pragma unroll
+            for (int j = 0; j < kStage * kSubWords / kDrawThreads; j++) {
+                const int k = j * kDrawThreads + tid;
+                if (k < nst * kSubWords) sk[j] = subk[(int64_t)st_id[k / kSubWords] * kSubWords + k % kSubWords];
+            }
+#pragma unroll
+            for (int j = 0; j < kPer; j++) {
+                const int k = j * kDrawThreads + tid;
+                if (k < nst * (kDrawChunk / 4)) reinterpret_cast<f32x4 *>(st_terms)[k] = v[j];
+            }
+#pragma unroll
+            for (int j = 0; j < kStage * kSubWords / kDrawThreads; j++) {
+                const int k = j * kDrawThreads + tid;
+                if (k < nst * kSubWords) st_subk[k] = sk[j];
+            }
+        }
+        __syncthreads();
+        return nb;
+    };
+
+    // One chunk's or one batch's range tests on the header words base..base+5 of hv.
+    auto range_step = [&](uint32_t &A, uint32_t hv, int base) -> bool {
+        const uint32_t lo_a = __builtin_amdgcn_readlane(hv, base + 0);
+        const uint32_t sp_a = __builtin_amdgcn_readlane(hv, base + 1);
+        const uint32_t k_a = __builtin_amdgcn_readlane(hv, base + 2);
+        const uint32_t lo_b = __builtin_amdgcn_readlane(hv, base + 3);
+        const uint32_t sp_b = __builtin_amdgcn_readlane(hv, base + 4);
+        const uint32_t k_b = __builtin_amdgcn_readlane(hv, base + 5);
+        const bool ok_a = A - lo_a <= sp_a, ok_b = A - lo_b <= sp_b;
+        A += ok_a ? k_a : (ok_b ? k_b : 0u);
+        return ok_a || ok_b;
+    };
+    // One chunk from A (bits of the running sum at its start, wave-uniform) to its end: the
+    // chunk's range tests; else runs of blocks, lane s holding block s: the longest run from
+    // block s0 that one binade takes (an inclusive prefix sum of the blocks' increments and a
+    // ballot of the first block whose range test fails; within a run every block's own test
+    // holds, since A + prefix stays in the binade), else block s0's terms one per lane, added in
+    // order through readlane. The block ranges come from LDS when the chunk is staged; stv holds
+    // the staged chunk ids, one per lane.
+    auto step = [&](uint32_t A, uint32_t hv, int q, int64_t c, int stv) -> uint32_t {
+        A = __builtin_amdgcn_readfirstlane(A);  // wave-uniform: keep the walk on scalar registers
+        if (range_step(A, hv, kHeadWords * q)) return A;
+        const uint64_t hit = __ballot(stv == (int)c);
+        const bool staged = hit != 0u;
+        const int slot = staged ? __builtin_ctzll(hit) : 0;
+        const uint32_t kv = lane < kSubWords ? (staged ? st_subk[slot * kSubWords + lane] : subk[c * kSubWords + lane]) : 0u;
+        const float *rt = staged ? st_terms + slot * kDrawChunk : terms + c * kDrawChunk;
+        const int64_t left = n - c * kDrawChunk;
+        const int nbk = (int)(left >= kDrawChunk ? kDrawSubs : (left + kDrawSub - 1) / kDrawSub);
+        const int bl = lane & (kDrawSubs - 1);
+        uint32_t lo_x[2], k_x[2];
+#pragma unroll
+        for (int x = 0; x < 2; x++) {
+            lo_x[x] = __shfl(kv, kBlockWords * bl + 3 * x);
+            k_x[x] = __shfl(kv, kBlockWords * bl + 3 * x + 2);
+        }
+        const uint32_t ea = __builtin_amdgcn_readlane(hv, kHeadWords * q + 6);
+        int s0 = 0;
+        while (s0 < nbk) {
+            bool moved = false;
+#pragma unroll
+            for (int x = 0; x < 2; x++) {
+                const uint32_t lo = (ea + 127u + (uint32_t)x) << 23;  // every valid block's lo
+                const uint32_t base = A - lo;
+                if (moved || base > 0x7FFFFFu) continue;
+                const bool in = lane >= s0 && lane < nbk;
+                uint32_t P = in ? k_x[x] : 0u;
+                P += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)P, 0x111, 0xF, 0xF, true);  // row_shr:1
+                P += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)P, 0x112, 0xF, 0xF, true);  // row_shr:2
+                P += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)P, 0x114, 0xF, 0xF, true);  // row_shr:4
+                const bool ok = lo_x[x] == lo && P <= 0x7FFFFFu - base;  // K <= 2^23 - 1, so P < 2^26
+                const uint64_t fail = __ballot(in && !ok);
+                const int se = fail != 0u ? __builtin_ctzll(fail) : nbk;
+                if (se > s0) {
+                    A += __builtin_amdgcn_readlane(P, se - 1);
+                    s0 = se;
+                    moved = true;
+                }
+            }
+            if (moved) continue;
+            const int64_t sb = c * kDrawChunk + s0 * kDrawSub;
+            const int m = (int)(n - sb < kDrawSub ? n - sb : kDrawSub);
+            const int tb = __builtin_bit_cast(int, lane < m ? rt[s0 * kDrawSub + lane] : 0.0f);
+            float a = __builtin_bit_cast(float, A);
+            if (m == kDrawSub) {
+#pragma unroll
+                for (int j = 0; j < kDrawSub; j++) a += __builtin_bit_cast(float, __builtin_amdgcn_readlane(tb, j));
+            } else {
+                for (int j = 0; j < m; j++) a += __builtin_bit_cast(float, __builtin_amdgcn_readlane(tb, j));
+            }
+            A = __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, a));
+            s0++;
+        }
+        return A;
+    };
+
+    uint32_t A = 0;  // bits of the running sum (wave 0)
+    int mk = 0;      // marks of 64 batches gather in one VGPR of wave 0 (lane b % 64), stored together
+    for (int64_t b0 = 0; b0 < nbat; b0 += kRoundBatches) {
+        const int nb = stage_round(b0);
+        if (wave == 0) {
+            const int stv = lane < st_n ? st_id[lane] : -1;
+            uint32_t nc = rh[lane], na = ragg[lane & (kHeadWords - 1)];
+            for (int bi = 0; bi < nb; bi++) {
+                const int64_t b = b0 + bi;
+                const uint32_t cur = nc, ag = na;
+                if (bi + 1 < nb) {  // the next batch's reads in flight during this one
+                    nc = rh[(bi + 1) * 64 + lane];
+                    na = ragg[(bi + 1) * kHeadWords + (lane & (kHeadWords - 1))];
+                }
+                mk = lane == (int)(b & 63) ? (int)A : mk;
+                if ((b & 63) == 63 || b == nbat - 1) {
+                    if (lane <= (int)(b & 63)) marks[(b & ~(int64_t)63) + lane] = (uint32_t)mk;
+                }
+                A = __builtin_amdgcn_readfirstlane(A);
+                if (range_step(A, ag, 0)) continue;
+                // chunk by chunk (not unrolled: one copy of the rarely used block path stays in the
+                // instruction cache)
+                const int qn = (int)(nch - b * kBatch < kBatch ? nch - b * kBatch : kBatch);
+#pragma unroll 1
+                for (int q = 0; q < qn; q++) A = step(A, cur, q, b * kBatch + q, stv);
+            }
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        marks[nbat] = A;
+        sum_bits = A;
+    }
+    __syncthreads();
+    const float sum_e = __builtin_bit_cast(float, sum_bits);
+    if (sum_e <= 0.0f) {  // sampler.mojo:295-296 (a NaN sum goes on to the walk, as there)
         if (tid == 0) {
-            out[0] = first;
+            out[0] = order ? order[0] : 0;
             out[1] = 0;
         }
         return;
     }
-    // The draw's running sum is the sum pass's running sum term for term (same terms, same order),
-    // so the first i with r <= acc_i lies in the first block whose recorded end sum reaches r;
-    // blocks ending below r form a prefix (acc never decreases) and are counted in parallel, and
-    // that block is re-added from the previous block's recorded sum.
-    const float r = p.u * sum_e;
-    const int64_t nb = (n + kMarkBlock - 1) / kMarkBlock;
+    const float r = u * sum_e;
+    // batches whose end sum is below r form a prefix (the sums never decrease); a NaN r counts
+    // none and the walk below finds no index, as the reference's
     int64_t below = 0;
-    for (int64_t j = tid; j < nb; j += kTailThreads) below += marks[j] < r ? 1 : 0;
-    ired[tid] = below;
+    for (int64_t k = tid; k < nbat; k += kDrawThreads) below += __builtin_bit_cast(float, marks[k + 1]) < r ? 1 : 0;
+    for (int o = 32; o > 0; o >>= 1) below += __shfl_xor(below, o);
+    if (lane == 0) cnt_s[wave] = below;
     __syncthreads();
-    for (int st = kTailThreads / 2; st > 0; st >>= 1) {
-        if (tid < st) ired[tid] += ired[tid + st];
-        __syncthreads();
-    }
-    const int64_t jb = ired[0];
-    int64_t pick = n - 1;
-    if (jb < nb) {
-        const int64_t i0 = jb * kMarkBlock;
-        const int c = (int)(n - i0 < kMarkBlock ? n - i0 : kMarkBlock);
-        if (tid < c) tile[0][tid] = exp_f32(val(i0 + tid) - mx);
-        __syncthreads();
-        if (tid == 0) {
-            float acc = jb > 0 ? marks[jb - 1] : 0.0f;
-            for (int e = 0; e < c; e++) {
-                acc += tile[0][e];
-                if (r <= acc) {
-                    pick = i0 + e;
+    int64_t bb = 0;
+    for (int k = 0; k < kDrawThreads / 64; k++) bb += cnt_s[k];
+    // the batch's chunks again from its recorded start, up to the first whose end reaches r
+    if (wave == 0) {
+        int64_t jc = -1;
+        uint32_t B = 0;
+        if (bb < nbat) {
+            B = marks[bb];
+            const uint32_t cur = heads[bb * 64 + lane];
+            for (int q = 0; q < kBatch; q++) {
+                const int64_t c = bb * kBatch + q;
+                if (c >= nch) break;
+                const uint32_t E = step(B, cur, q, c, -1);
+                if (r <= __builtin_bit_cast(float, E)) {
+                    jc = c;
                     break;
                 }
+                B = E;
             }
+        }
+        if (tid == 0) {
+            chunk_s = jc;
+            start_bits = B;
+        }
+    }
+    __syncthreads();
+    const int64_t jc = chunk_s;
+    int64_t pick = n - 1;
+    if (jc >= 0) {  // that chunk's terms through LDS, re-added from its start in lane 0
+        const int64_t i0 = jc * kDrawChunk;
+        const int cnt = (int)(n - i0 < kDrawChunk ? n - i0 : kDrawChunk);
+        if (tid < cnt) tile[tid] = terms[i0 + tid];
+        __syncthreads();
+        if (tid == 0) {
+            int he;
+            chain_tile<true>(tile, cnt, __builtin_bit_cast(float, start_bits), r, he);
+            if (he >= 0) pick = i0 + he;
         }
     }
     if (tid == 0) {
@@ -382,7 +882,14 @@ struct SamplerWork {
     float *vals = nullptr;
     uint32_t *keys = nullptr, *keys_out = nullptr;
     int32_t *idx = nullptr, *idx_out = nullptr;
-    float *marks = nullptr;    // the final draw's running sum at the end of every kMarkBlock terms
+    DrawHdr *hdr = nullptr;    // candidate count after the truncations
+    float *cmax = nullptr;     // per-chunk maxima of the candidates
+    float *terms = nullptr;    // the final draw's exps
+    double *csum = nullptr;    // per-chunk f64 sums of the exps
+    uint32_t *heads = nullptr; // per-chunk headers (kHeadWords each), whole batches
+    uint32_t *subk = nullptr;  // per-chunk block ranges (kSubWords each)
+    uint32_t *slow_list = nullptr;  // chunks the records kernel lists as likely slow
+    uint32_t *marks = nullptr; // bits of the running sum at the start of every batch of chunks, then the total
     int64_t *lists = nullptr;  // context tokens then suppress ids
     int64_t *result = nullptr;
     void *sort_tmp = nullptr;
@@ -390,8 +897,8 @@ struct SamplerWork {
 };
 
 static void free_work(SamplerWork *w) {
-    void *ps[] = {w->counts, w->mask, w->vals, w->keys, w->keys_out, w->idx, w->idx_out, w->marks,
-                  w->lists, w->result, w->sort_tmp};
+    void *ps[] = {w->counts, w->mask, w->vals,  w->keys, w->keys_out, w->idx, w->idx_out, w->hdr,   w->cmax,
+                  w->terms,  w->csum, w->heads, w->subk, w->slow_list, w->marks, w->lists,  w->result, w->sort_tmp};
     for (void *p : ps)
         if (p) (void)hipFree(p);
     *w = SamplerWork{};
@@ -424,7 +931,16 @@ static int32_t ensure_work(aesir_ctx *ctx, int64_t V, int64_t n_lists) {
         AESIR_HIP_TRY(hipMalloc((void **)&w->keys_out, (size_t)V * 4));
         AESIR_HIP_TRY(hipMalloc((void **)&w->idx, (size_t)V * 4));
         AESIR_HIP_TRY(hipMalloc((void **)&w->idx_out, (size_t)V * 4));
-        AESIR_HIP_TRY(hipMalloc((void **)&w->marks, (size_t)(V / kMarkBlock + 1) * 4));
+        const int64_t nch = (V + kDrawChunk - 1) / kDrawChunk;
+        AESIR_HIP_TRY(hipMalloc((void **)&w->hdr, sizeof(DrawHdr)));
+        AESIR_HIP_TRY(hipMalloc((void **)&w->cmax, (size_t)nch * 4));
+        AESIR_HIP_TRY(hipMalloc((void **)&w->terms, (size_t)V * 4));
+        AESIR_HIP_TRY(hipMalloc((void **)&w->csum, (size_t)nch * 8));
+        const int64_t nbat = (nch + kBatch - 1) / kBatch;
+        AESIR_HIP_TRY(hipMalloc((void **)&w->heads, (size_t)nbat * 64 * 4));
+        AESIR_HIP_TRY(hipMalloc((void **)&w->subk, (size_t)nch * kSubWords * 4));
+        AESIR_HIP_TRY(hipMalloc((void **)&w->slow_list, (size_t)kSlowListMax * 4));
+        AESIR_HIP_TRY(hipMalloc((void **)&w->marks, (size_t)(nbat + 1) * 4));
         size_t bytes = 0;
         AESIR_HIP_TRY(rocprim::radix_sort_pairs(nullptr, bytes, w->keys, w->keys_out, w->idx, w->idx_out,
                                                 (unsigned)V, 0, 32, ctx->stream));
@@ -532,9 +1048,27 @@ int32_t aesir_sample_token(aesir_ctx *ctx, const void *logits, int64_t vocab, co
             AESIR_HIP_TRY(rocprim::radix_sort_pairs(w->sort_tmp, bytes, w->keys, w->keys_out, w->idx, w->idx_out,
                                                     (unsigned)vocab, 0, 32, s));
         }
-        hipLaunchKernelGGL(sampler_tail_kernel, dim3(1), dim3(kTailThreads), 0, s, w->vals,
-                           p.sort ? (const int32_t *)w->idx_out : nullptr, vocab, p, w->marks, w->result);
+        const int32_t *order = p.sort ? (const int32_t *)w->idx_out : nullptr;
+        p.draw_here = k_on && cfg->top_k <= kSeqTile;
+        hipLaunchKernelGGL(sampler_tail_kernel, dim3(1), dim3(kTailThreads), 0, s, w->vals, order, vocab, p, w->hdr,
+                           w->result);
         AESIR_LAUNCH_CHECK("sampler_tail_kernel");
+        if (!p.draw_here) {
+            // the final draw over the hdr->n candidates; chunks past the count exit at once
+            const unsigned nch = (unsigned)((vocab + kDrawChunk - 1) / kDrawChunk);
+            hipLaunchKernelGGL(sampler_chunk_max_kernel, dim3(nch), dim3(kDrawThreads), 0, s, w->vals, order, w->hdr,
+                               w->cmax);
+            AESIR_LAUNCH_CHECK("sampler_chunk_max_kernel");
+            hipLaunchKernelGGL(sampler_terms_kernel, dim3(nch), dim3(kDrawThreads), 0, s, w->vals, order, w->hdr,
+                               w->cmax, w->terms, w->csum);
+            AESIR_LAUNCH_CHECK("sampler_terms_kernel");
+            hipLaunchKernelGGL(sampler_records_kernel, dim3(nch), dim3(kDrawThreads), 0, s, w->terms, w->csum, w->hdr,
+                               w->heads, w->subk, w->slow_list);
+            AESIR_LAUNCH_CHECK("sampler_records_kernel");
+            hipLaunchKernelGGL(sampler_draw_kernel, dim3(1), dim3(kDrawThreads), 0, s, w->terms, w->heads, w->subk,
+                               w->slow_list, w->hdr, order, p.u, w->marks, w->result);
+            AESIR_LAUNCH_CHECK("sampler_draw_kernel");
+        }
         st = peek;
     }
     int64_t res[2];

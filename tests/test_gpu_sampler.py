@@ -1,10 +1,13 @@
 """GPU parity of the sampler stack (aesir_sample_token, sample_token_from_logits at
 core/sampler.mojo:217-305) against the CPU oracle: the sampled token and the RuneRNG state must be
 identical, draw after draw, for every stage combination (greedy branch, penalties, temperature,
-top-k, top-p, min-p, suppress list), at vocabulary sizes from 512 to 128256 (1000 and 4099 end
-in a short block of the draw's recorded running sums, 4099 also in a short LDS tile), with many
-tied logits so the stable-sort order is exercised. Both sides compute exp as the correctly rounded f32 value
-and keep the reference's sequential f32 sums, so equality is exact."""
+top-k, top-p, min-p, suppress list), at vocabulary sizes from 512 to 300000 (1000 and 4099 end in
+a short 32-term block and a short chunk of the draw, 4099 also in a short LDS tile of the
+truncations), with many tied logits so the stable-sort order is exercised. Both sides compute exp
+as the correctly rounded f32 value and keep the reference's sequential f32 sums, so equality is
+exact. The device evaluates the final draw's running sum in parallel (one integer add per chunk
+wherever no rounding depends on the order); these tests are what pin that to the sequential
+sum."""
 import numpy as np
 import pytest
 
@@ -44,6 +47,11 @@ CONFIGS = [
     dict(temperature=1.5, min_p=0.1),
     dict(temperature=0.8, top_k=200, repetition_penalty=1.3, frequency_penalty=0.2, presence_penalty=0.4),
     dict(temperature=1.1, top_p=0.5, repetition_penalty=0.8),
+    # more candidates than one LDS tile after top-k: the sorted list goes to the chunked draw
+    dict(temperature=1.0, top_k=5000),
+    # 1 / temperature overflows to inf: zero logits become NaN, sum_e is NaN, and the reference
+    # still consumes the random number and returns its last candidate
+    dict(temperature=1e-39),
 ]
 
 
@@ -91,3 +99,24 @@ def test_sampler_greedy_consumes_no_random_number(A, ctx, oracle):
     assert rng.state == st
     A.sample_token(ctx, ctx.from_numpy(x), A.SamplerConfig(temperature=1.0), rng)
     assert rng.state != st
+
+
+@pytest.mark.parametrize("cfgd", [dict(temperature=1.0), dict(temperature=0.7, top_k=20000),
+                                  dict(temperature=1.3, repetition_penalty=1.2)])
+def test_sampler_long_vocabulary_matches_oracle(A, ctx, oracle, cfgd):
+    """300000 candidates: the final draw's walk over chunk headers takes three rounds of LDS
+    staging (131072 candidates each) and stores its recorded running sums in several groups of
+    64; logits in N(0, 2) rounded to f16, as a model's are."""
+    vocab = 300000
+    rng = np.random.default_rng(77)
+    gcfg, ocfg = A.SamplerConfig(**cfgd), oracle.SamplerConfig(**cfgd)
+    g_rng = A.RuneRNG(99)
+    o_state = oracle.rune_rng_state(99)
+    for d in range(4):
+        logits = (rng.standard_normal(vocab) * 2.0).astype(np.float16)
+        context = rng.integers(0, vocab, 128).tolist()
+        t = ctx.from_numpy(logits.reshape(1, -1))
+        got = A.sample_token(ctx, t, gcfg, g_rng, context)
+        want, o_state = oracle.sample_token_f16(logits, ocfg, o_state, context, [])
+        assert got == want, (d, got, want)
+        assert g_rng.state == o_state, d

@@ -404,7 +404,7 @@ __global__ __launch_bounds__(WPR * PH * 64) void q8_0_direct_kernel(const uint8_
                                                                    int64_t rowbytes, int64_t rpw,
                                                                    const float *__restrict__ x, float *__restrict__ y) {
     constexpr int NW = WPR * PH;
-    static_assert(D == 2 || D == 4, "rows in flight");
+    static_assert(D % 2 == 0 && D >= 2 && D <= 8, "rows in flight: an even count, 3 loads each under vmcnt's 63");
     __shared__ float part[kQDirectRpw][WPR];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -474,39 +474,26 @@ __global__ __launch_bounds__(WPR * PH * 64) void q8_0_direct_kernel(const uint8_
     };
     // The first D rows are requested before x, so the weight stream starts at once; x and the
     // digits follow (waiting for x waits for those rows too, which the first row needs anyway).
-    Row r0, r1, r2, r3;
-    load(0, r0);
-    __builtin_amdgcn_sched_barrier(0);
-    load(1, r1);
-    __builtin_amdgcn_sched_barrier(0);
-    if constexpr (D > 2) {
-        load(2, r2);
-        __builtin_amdgcn_sched_barrier(0);
-        load(3, r3);
+    Row rr[D];
+#pragma unroll
+    for (int j = 0; j < D; j++) {
+        load(j, rr[j]);
         __builtin_amdgcn_sched_barrier(0);
     }
     x_digits(xb, dg, ex, plain);
     __builtin_amdgcn_sched_barrier(0);
     for (int k = 0; k < nmine; k += D) {
-        const float v0 = value(r0);
-        __builtin_amdgcn_sched_barrier(0);
-        load(k + D, r0);
-        __builtin_amdgcn_sched_barrier(0);
-        const float v1 = value(r1);
-        __builtin_amdgcn_sched_barrier(0);
-        load(k + D + 1, r1);
-        __builtin_amdgcn_sched_barrier(0);
-        emit(k, v0, v1);
-        if constexpr (D > 2) {
-            const float v2 = value(r2);
+#pragma unroll
+        for (int j = 0; j < D; j += 2) {
+            const float v0 = value(rr[j]);
             __builtin_amdgcn_sched_barrier(0);
-            load(k + D + 2, r2);
+            load(k + D + j, rr[j]);
             __builtin_amdgcn_sched_barrier(0);
-            const float v3 = value(r3);
+            const float v1 = value(rr[j + 1]);
             __builtin_amdgcn_sched_barrier(0);
-            load(k + D + 3, r3);
+            load(k + D + j + 1, rr[j + 1]);
             __builtin_amdgcn_sched_barrier(0);
-            emit(k + 2, v2, v3);
+            emit(k + j, v0, v1);
         }
     }
     __builtin_amdgcn_s_waitcnt(q8_vm_wait(0));  // the loads past the last row, before the barrier

@@ -8,14 +8,15 @@
 //             (descending logit key, index). Equal logits (-0 == +0) keep index order, which is the
 //             order the reference's stable insertion sort (:92-104) produces; every later stage of
 //             the stack sees an already sorted prefix, so one sort serves all of them
-//   tail      one workgroup: the f32 running sums of apply_top_p and apply_min_p in one lane in
-//             candidate order (f32 addition is not associative; the sums must follow the
-//             reference's order to choose the same cut), with the next LDS tile of exps computed
-//             by the other waves meanwhile
-//   draw      the final draw: chunk maxima, exps and per-chunk binade increments over the whole
-//             device, then one wave that reproduces the sequential f32 sum bit for bit with one
-//             integer add per chunk where no rounding depends on the order, and the inverse-CDF
-//             walk over one recorded chunk
+//   tail      top_k <= 4096: one workgroup makes the truncations and the draw, the running sums
+//             of apply_top_p, apply_min_p and the draw in one lane in candidate order (f32
+//             addition is not associative; the sums must follow the reference's order to choose
+//             the same cut and token), the next LDS tile of exps computed by the other waves
+//   chunked   longer candidate lists: each running sum (top-p's sum and cut, min-p's sum, the
+//             final draw's sum and walk) is a terms pass and a records pass over the whole device
+//             and one wave that reproduces the sequential f32 sum bit for bit, with one integer
+//             add per chunk where no rounding depends on the order; the candidate count stays on
+//             the device between the stages
 //   greedy    temperature <= 0 or top_k == 1: the first maximum of the sanitized, masked logits
 //
 // The random number comes from RuneRNG on the host (one draw per sampled token, consumed only
@@ -51,7 +52,6 @@ struct SampleParams {
     float top_p;    // < 1: nucleus
     float min_p;    // in (0, 1): min-p
     float u;        // RuneRNG.next_float32 for the draw
-    int draw_here;  // top_k <= kSeqTile: the tail kernel makes the final draw itself
 };
 
 __global__ void sampler_clear_kernel(int32_t *__restrict__ counts, uint8_t *__restrict__ mask, int64_t V) {
@@ -139,10 +139,12 @@ __global__ __launch_bounds__(1024) void sampler_greedy_kernel(const h16 *__restr
     }
 }
 
-// Truncations over the candidate list: value i is vals[order ? order[i] : i]. The running f32
-// sums of apply_top_p and apply_min_p are evaluated in candidate order by lane 0 of wave 0 (f32
-// addition is not associative, so the order fixes the cut). The terms come from two LDS tiles:
-// while lane 0 adds one tile, waves 1-3 compute the next tile's terms into the other.
+// Truncations and the draw over at most kSeqTile candidates (top_k <= kSeqTile), in one
+// workgroup: value i is vals[order ? order[i] : i]. The running f32 sums of apply_top_p and
+// apply_min_p are evaluated in candidate order by lane 0 of wave 0 (f32 addition is not
+// associative, so the order fixes the cut). The terms come from two LDS tiles: while lane 0 adds
+// one tile, waves 1-3 compute the next tile's terms into the other. Longer candidate lists take
+// the chunked stages below.
 constexpr int kSeqTile = 4096;  // terms per LDS tile (two tiles)
 constexpr int kSeqBlock = 32;   // terms per block of lane 0's adds
 
@@ -250,17 +252,19 @@ __device__ __forceinline__ int64_t ordered_chain(float *tile0, float *tile1, int
     return hit;
 }
 
-// Candidate count after apply_top_k, apply_top_p and apply_min_p, for the final draw's kernels,
-// and the count of chunks the draw's records kernel lists as likely slow.
+// Device-side state of the chunked stages: the candidate count as the truncations leave it, the
+// count of chunks a records pass lists as likely slow, the last sum pass's total and min-p's first
+// failing index.
 struct DrawHdr {
     int64_t n;
     uint32_t n_slow;
-    uint32_t pad;
+    float sum;
+    int64_t kept;
 };
 
 __global__ __launch_bounds__(kTailThreads) void sampler_tail_kernel(const float *__restrict__ vals,
                                                                     const int32_t *__restrict__ order, int64_t V,
-                                                                    SampleParams p, DrawHdr *hdr, int64_t *out) {
+                                                                    SampleParams p, int64_t *out) {
     __shared__ __align__(16) float tile[2][kSeqTile];
     __shared__ float red[kTailThreads];
     __shared__ int64_t n_sh[2];
@@ -317,13 +321,6 @@ __global__ __launch_bounds__(kTailThreads) void sampler_tail_kernel(const float 
             __syncthreads();
         }
         n = kept > 0 ? kept : n;
-    }
-    if (!p.draw_here) {
-        if (tid == 0) {
-            hdr->n = n;
-            hdr->n_slow = 0;
-        }
-        return;
     }
     // At most kSeqTile candidates: the final draw (:284-305) here, its exps in one LDS tile and
     // both running sums (sum_e, then the inverse-CDF walk) in lane 0 in candidate order.
@@ -430,10 +427,18 @@ __global__ __launch_bounds__(kDrawThreads) void sampler_chunk_max_kernel(const f
     if (threadIdx.x == 0) cmax[blockIdx.x] = v;
 }
 
-// e_i = exp(x_i - max) for one chunk, and the chunk's f64 sum (an estimate for the binades).
+// The terms of one chunk of a running sum, and the chunk's f64 sum (an estimate for the binades):
+//   kTermsDraw   e_i = exp(x_i - max), max over the chunk maxima (the final draw, :284-293)
+//   kTermsExp    e_i = exp(x_i - x_0), x_0 the first (largest) candidate (apply_top_p :128-134,
+//                apply_min_p :175-181)
+//   kTermsProb   p_i = e_i / sum (e_i when sum <= 0), sum the previous pass's total (:136-138)
+// The truncation modes do nothing for one candidate or fewer (the reference returns early). Block
+// 0 also clears the likely-slow count for the records pass that follows.
+enum { kTermsDraw, kTermsExp, kTermsProb };
+template <int MODE>
 __global__ __launch_bounds__(kDrawThreads) void sampler_terms_kernel(const float *__restrict__ vals,
                                                                      const int32_t *__restrict__ order,
-                                                                     const DrawHdr *__restrict__ hdr,
+                                                                     DrawHdr *__restrict__ hdr,
                                                                      const float *__restrict__ cmax,
                                                                      float *__restrict__ terms,
                                                                      double *__restrict__ csum) {
@@ -441,19 +446,71 @@ __global__ __launch_bounds__(kDrawThreads) void sampler_terms_kernel(const float
     __shared__ double shd[kDrawThreads / 64];
     const int64_t n = hdr->n;
     const int64_t base = (int64_t)blockIdx.x * kDrawChunk;
+    if (MODE != kTermsDraw && n <= 1) return;
     if (base >= n) return;
-    const int64_t nch = (n + kDrawChunk - 1) / kDrawChunk;
-    float mx = -INFINITY;
-    for (int64_t c = threadIdx.x; c < nch; c += kDrawThreads) mx = fmaxf(mx, cmax[c]);
-    mx = block_max_f32(mx, shf);
+    if (blockIdx.x == 0 && threadIdx.x == 0) hdr->n_slow = 0;
+    auto val = [&](int64_t i) -> float { return vals[order ? order[i] : i]; };
+    float mx;
+    if constexpr (MODE == kTermsDraw) {
+        const int64_t nch = (n + kDrawChunk - 1) / kDrawChunk;
+        mx = -INFINITY;
+        for (int64_t c = threadIdx.x; c < nch; c += kDrawThreads) mx = fmaxf(mx, cmax[c]);
+        mx = block_max_f32(mx, shf);
+    } else {
+        mx = val(0);
+    }
     const int64_t i = base + threadIdx.x;
     float t = 0.0f;
     if (i < n) {
-        t = exp_f32(vals[order ? order[i] : i] - mx);
+        t = exp_f32(val(i) - mx);
+        if constexpr (MODE == kTermsProb) {
+            const float sum = hdr->sum;
+            t = sum > 0.0f ? t / sum : t;
+        }
         terms[i] = t;
     }
     const double s = block_sum_f64((double)t, shd);
     if (threadIdx.x == 0) csum[blockIdx.x] = s;
+}
+
+// The first candidate count of the chunked stages: top_k's cut (:107-116) or the vocabulary.
+__global__ void sampler_set_n_kernel(DrawHdr *hdr, int64_t n) {
+    hdr->n = n;
+    hdr->n_slow = 0;
+}
+
+// apply_min_p's cut (:183-194) after its sum pass: p_i = e_i / sum (e_i when sum <= 0) against
+// min_p * p_0. The probabilities never increase along the sorted candidates, so the kept ones are
+// the prefix before the first failing index, which the workgroups find with an atomic minimum.
+__global__ __launch_bounds__(kDrawThreads) void sampler_minp_cut_kernel(const float *__restrict__ vals,
+                                                                        const int32_t *__restrict__ order,
+                                                                        DrawHdr *__restrict__ hdr, float min_p) {
+    __shared__ int64_t first_s;
+    const int64_t n = hdr->n;
+    const int64_t base = (int64_t)blockIdx.x * kDrawChunk;
+    if (n <= 1 || base >= n) return;
+    if (threadIdx.x == 0) first_s = n;
+    __syncthreads();
+    const float sum = hdr->sum;
+    const float mx = vals[order[0]];
+    const float e0 = exp_f32(0.0f);  // the first candidate's exp (x_0 - x_0 = 0)
+    const float p0 = sum > 0.0f ? e0 / sum : e0;
+    const float threshold = min_p * p0;
+    const int64_t i = base + threadIdx.x;
+    if (i < n) {
+        const float e = exp_f32(vals[order[i]] - mx);
+        const float pr = sum > 0.0f ? e / sum : e;
+        if (!(pr >= threshold)) atomicMin(reinterpret_cast<unsigned long long *>(&first_s), (unsigned long long)i);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0 && first_s < n)
+        atomicMin(reinterpret_cast<unsigned long long *>(&hdr->kept), (unsigned long long)first_s);
+}
+
+// n = the kept prefix when it is not empty (:196-197).
+__global__ void sampler_minp_finish_kernel(DrawHdr *hdr) {
+    const int64_t n = hdr->n, kept = hdr->kept;
+    if (n > 1 && kept > 0 && kept < n) hdr->n = kept;
 }
 
 // RN(t / 2^(E-23)) for E in [-100, 101], with the halfway flag. NaN, infinite or negative terms
@@ -567,7 +624,10 @@ __global__ __launch_bounds__(kDrawThreads) void sampler_records_kernel(const flo
     }
 }
 
-// The walk and the draw. The walk goes round by round, kRoundBatches batches of kBatch chunks
+// The walk, then one of: the total (kWalkSum: to hdr->sum, with hdr->kept reset for min-p);
+// apply_top_p's cut (kWalkCut: the first i whose running sum of probabilities reaches top_p,
+// hdr->n = i + 1, or unchanged when there is none, :140-147); or the final draw (kWalkDraw).
+// The walk goes round by round, kRoundBatches batches of kBatch chunks
 // at a time. For each round the workgroup stages the chunk headers in LDS, reduces every batch to
 // one header of the same form (a range and an increment for each binade, valid when every chunk
 // of the batch has one for the first chunk's binade; the chunks' tests then all hold exactly when
@@ -575,13 +635,15 @@ __global__ __launch_bounds__(kDrawThreads) void sampler_records_kernel(const flo
 // likely-slow list.
 // Wave 0 then walks the round on scalar registers: a batch header or a chunk's header is read into
 // one VGPR, one word per lane, and taken apart with readlane.
+enum { kWalkSum, kWalkCut, kWalkDraw };
+template <int MODE>
 __global__ __launch_bounds__(kDrawThreads) void sampler_draw_kernel(const float *__restrict__ terms,
                                                                     const uint32_t *__restrict__ heads,
                                                                     const uint32_t *__restrict__ subk,
                                                                     const uint32_t *__restrict__ slow_list,
-                                                                    const DrawHdr *__restrict__ hdr,
-                                                                    const int32_t *__restrict__ order, float u,
-                                                                    uint32_t *__restrict__ marks,
+                                                                    DrawHdr *__restrict__ hdr,
+                                                                    const int32_t *__restrict__ order,
+                                                                    float target_arg, uint32_t *__restrict__ marks,
                                                                     int64_t *__restrict__ out) {
     constexpr int kRoundWords = kRoundBatches * 64;
     __shared__ __align__(16) uint32_t rh[kRoundWords];
@@ -598,6 +660,7 @@ __global__ __launch_bounds__(kDrawThreads) void sampler_draw_kernel(const float 
     const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
     const int lane = tid & 63;
     const int64_t n = hdr->n;
+    if (MODE != kWalkDraw && n <= 1) return;  // the truncations leave one candidate alone
     const int64_t nch = (n + kDrawChunk - 1) / kDrawChunk;
     const int64_t nbat = (nch + kBatch - 1) / kBatch;  // heads holds nbat whole batches
     const int n_list = (int)(hdr->n_slow < (uint32_t)kSlowListMax ? hdr->n_slow : (uint32_t)kSlowListMax);
@@ -811,17 +874,22 @@ __global__ __launch_bounds__(kDrawThreads) void sampler_draw_kernel(const float 
     if (tid == 0) {
         marks[nbat] = A;
         sum_bits = A;
+        if (MODE == kWalkSum) {
+            hdr->sum = __builtin_bit_cast(float, A);
+            hdr->kept = n;
+        }
     }
+    if (MODE == kWalkSum) return;
     __syncthreads();
     const float sum_e = __builtin_bit_cast(float, sum_bits);
-    if (sum_e <= 0.0f) {  // sampler.mojo:295-296 (a NaN sum goes on to the walk, as there)
+    if (MODE == kWalkDraw && sum_e <= 0.0f) {  // sampler.mojo:295-296 (a NaN sum goes on to the walk, as there)
         if (tid == 0) {
             out[0] = order ? order[0] : 0;
             out[1] = 0;
         }
         return;
     }
-    const float r = u * sum_e;
+    const float r = MODE == kWalkDraw ? target_arg * sum_e : target_arg;  // r = u * sum_e, or top_p
     // batches whose end sum is below r form a prefix (the sums never decrease); a NaN r counts
     // none and the walk below finds no index, as the reference's
     int64_t below = 0;
@@ -869,8 +937,12 @@ __global__ __launch_bounds__(kDrawThreads) void sampler_draw_kernel(const float 
         }
     }
     if (tid == 0) {
-        out[0] = order ? order[pick] : pick;
-        out[1] = 1;
+        if (MODE == kWalkCut) {
+            hdr->n = pick + 1;  // the cut index, n - 1 when there is none
+        } else {
+            out[0] = order ? order[pick] : pick;
+            out[1] = 1;
+        }
     }
 }
 
@@ -1049,25 +1121,49 @@ int32_t aesir_sample_token(aesir_ctx *ctx, const void *logits, int64_t vocab, co
                                                     (unsigned)vocab, 0, 32, s));
         }
         const int32_t *order = p.sort ? (const int32_t *)w->idx_out : nullptr;
-        p.draw_here = k_on && cfg->top_k <= kSeqTile;
-        hipLaunchKernelGGL(sampler_tail_kernel, dim3(1), dim3(kTailThreads), 0, s, w->vals, order, vocab, p, w->hdr,
-                           w->result);
-        AESIR_LAUNCH_CHECK("sampler_tail_kernel");
-        if (!p.draw_here) {
-            // the final draw over the hdr->n candidates; chunks past the count exit at once
+        if (k_on && cfg->top_k <= kSeqTile) {
+            // at most one LDS tile of candidates: truncations and the draw in one workgroup
+            hipLaunchKernelGGL(sampler_tail_kernel, dim3(1), dim3(kTailThreads), 0, s, w->vals, order, vocab, p,
+                               w->result);
+            AESIR_LAUNCH_CHECK("sampler_tail_kernel");
+        } else {
+            // the chunked stages over hdr->n candidates (chunks past the count exit at once): each
+            // running sum is a terms pass, a records pass and a walk
             const unsigned nch = (unsigned)((vocab + kDrawChunk - 1) / kDrawChunk);
+            auto running_sum = [&](auto terms_mode, auto walk_mode, float target) -> int32_t {
+                constexpr int TM = decltype(terms_mode)::value, WM = decltype(walk_mode)::value;
+                hipLaunchKernelGGL(sampler_terms_kernel<TM>, dim3(nch), dim3(kDrawThreads), 0, s, w->vals, order,
+                                   w->hdr, w->cmax, w->terms, w->csum);
+                AESIR_LAUNCH_CHECK("sampler_terms_kernel");
+                hipLaunchKernelGGL(sampler_records_kernel, dim3(nch), dim3(kDrawThreads), 0, s, w->terms, w->csum,
+                                   w->hdr, w->heads, w->subk, w->slow_list);
+                AESIR_LAUNCH_CHECK("sampler_records_kernel");
+                hipLaunchKernelGGL(sampler_draw_kernel<WM>, dim3(1), dim3(kDrawThreads), 0, s, w->terms, w->heads,
+                                   w->subk, w->slow_list, w->hdr, order, target, w->marks, w->result);
+                AESIR_LAUNCH_CHECK("sampler_draw_kernel");
+                return AESIR_OK;
+            };
+            using std::integral_constant;
+            hipLaunchKernelGGL(sampler_set_n_kernel, dim3(1), dim3(1), 0, s, w->hdr, k_on ? cfg->top_k : vocab);
+            AESIR_LAUNCH_CHECK("sampler_set_n_kernel");
+            if (p_on) {  // apply_top_p (:119-147): the sum of the exps, then the cut on the probabilities
+                AESIR_TRY(running_sum(integral_constant<int, kTermsExp>{}, integral_constant<int, kWalkSum>{}, 0.0f));
+                AESIR_TRY(running_sum(integral_constant<int, kTermsProb>{}, integral_constant<int, kWalkCut>{},
+                                      cfg->top_p));
+            }
+            if (m_on) {  // apply_min_p (:166-194): the sum of the exps, then the threshold cut
+                AESIR_TRY(running_sum(integral_constant<int, kTermsExp>{}, integral_constant<int, kWalkSum>{}, 0.0f));
+                hipLaunchKernelGGL(sampler_minp_cut_kernel, dim3(nch), dim3(kDrawThreads), 0, s, w->vals, order,
+                                   w->hdr, cfg->min_p);
+                AESIR_LAUNCH_CHECK("sampler_minp_cut_kernel");
+                hipLaunchKernelGGL(sampler_minp_finish_kernel, dim3(1), dim3(1), 0, s, w->hdr);
+                AESIR_LAUNCH_CHECK("sampler_minp_finish_kernel");
+            }
+            // the final draw (:284-305)
             hipLaunchKernelGGL(sampler_chunk_max_kernel, dim3(nch), dim3(kDrawThreads), 0, s, w->vals, order, w->hdr,
                                w->cmax);
             AESIR_LAUNCH_CHECK("sampler_chunk_max_kernel");
-            hipLaunchKernelGGL(sampler_terms_kernel, dim3(nch), dim3(kDrawThreads), 0, s, w->vals, order, w->hdr,
-                               w->cmax, w->terms, w->csum);
-            AESIR_LAUNCH_CHECK("sampler_terms_kernel");
-            hipLaunchKernelGGL(sampler_records_kernel, dim3(nch), dim3(kDrawThreads), 0, s, w->terms, w->csum, w->hdr,
-                               w->heads, w->subk, w->slow_list);
-            AESIR_LAUNCH_CHECK("sampler_records_kernel");
-            hipLaunchKernelGGL(sampler_draw_kernel, dim3(1), dim3(kDrawThreads), 0, s, w->terms, w->heads, w->subk,
-                               w->slow_list, w->hdr, order, p.u, w->marks, w->result);
-            AESIR_LAUNCH_CHECK("sampler_draw_kernel");
+            AESIR_TRY(running_sum(integral_constant<int, kTermsDraw>{}, integral_constant<int, kWalkDraw>{}, p.u));
         }
         st = peek;
     }

@@ -47,8 +47,12 @@ CONFIGS = [
     dict(temperature=1.5, min_p=0.1),
     dict(temperature=0.8, top_k=200, repetition_penalty=1.3, frequency_penalty=0.2, presence_penalty=0.4),
     dict(temperature=1.1, top_p=0.5, repetition_penalty=0.8),
-    # more candidates than one LDS tile after top-k: the sorted list goes to the chunked draw
+    # more candidates than one LDS tile after top-k: the truncations and the draw run as chunked
+    # stages (exact parallel running sums, device-side candidate counts)
     dict(temperature=1.0, top_k=5000),
+    dict(temperature=0.9, top_k=5000, top_p=0.9),
+    dict(temperature=1.2, top_k=6000, min_p=0.02),
+    dict(temperature=0.8, top_p=0.95, min_p=0.01, frequency_penalty=0.3),
     # 1 / temperature overflows to inf: zero logits become NaN, sum_e is NaN, and the reference
     # still consumes the random number and returns its last candidate
     dict(temperature=1e-39),
@@ -102,7 +106,8 @@ def test_sampler_greedy_consumes_no_random_number(A, ctx, oracle):
 
 
 @pytest.mark.parametrize("cfgd", [dict(temperature=1.0), dict(temperature=0.7, top_k=20000),
-                                  dict(temperature=1.3, repetition_penalty=1.2)])
+                                  dict(temperature=1.3, repetition_penalty=1.2), dict(temperature=0.9, top_p=0.9),
+                                  dict(temperature=1.0, min_p=0.05)])
 def test_sampler_long_vocabulary_matches_oracle(A, ctx, oracle, cfgd):
     """300000 candidates: the final draw's walk over chunk headers takes three rounds of LDS
     staging (131072 candidates each) and stores its recorded running sums in several groups of

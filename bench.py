@@ -389,15 +389,17 @@ def quant_bench(A, kind: str, seed: int, kv: int, steps: int, warmup: int, kerne
 def sampler_bench(A, seed: int, reps: int = 50) -> dict:
     """aesir_sample_token (sample_token_from_logits on the device) over Llama-3's 128256 f16 logits
     with 256 context tokens: wall time per blocking call (host round trip included) for the greedy
-    branch, a top-k 40 / top-p 0.95 / temperature 0.8 / repetition 1.1 draw, and a full-vocabulary
-    temperature-1 draw."""
+    branch, a top-k 40 / top-p 0.95 / temperature 0.8 / repetition 1.1 draw, a full-vocabulary
+    temperature-1 draw, and top-p 0.9 at temperature 0.9 without top-k (the truncation's two
+    running sums over the whole vocabulary)."""
     rng = np.random.default_rng(seed)
     ctx = A.Context(64 << 20)
     logits = ctx.from_numpy((rng.standard_normal((1, VOCAB)) * 2.0).astype(np.float16))
     context = rng.integers(0, VOCAB, 256).tolist()
     cfgs = {"greedy_us": A.SamplerConfig(temperature=0.0),
             "topk_topp_us": A.SamplerConfig(temperature=0.8, top_k=40, top_p=0.95, repetition_penalty=1.1),
-            "full_vocab_us": A.SamplerConfig(temperature=1.0)}
+            "full_vocab_us": A.SamplerConfig(temperature=1.0),
+            "topp_only_us": A.SamplerConfig(temperature=0.9, top_p=0.9)}
     out = {"workload": f"sample_token_from_logits over {VOCAB} f16 logits, 256 context tokens"}
     r = A.RuneRNG(seed)
     for name, cfg in cfgs.items():
@@ -574,6 +576,7 @@ def main():
     ap.add_argument("--no-sweep", action="store_true", help="skip the decode at KV 512 / 8192 / 32768")
     ap.add_argument("--no-micro", action="store_true", help="skip the kernel micro-suite and the Q8_0 matvec")
     ap.add_argument("--q8-only", action="store_true", help="run only the Q8_0-weight decode measurement")
+    ap.add_argument("--sampler-only", action="store_true", help="run only the sampler timings")
     ap.add_argument("--no-quant", action="store_true", help="skip the quantized-weight decode measurements")
     ap.add_argument("--quant-only", action="store_true", help="run only the quantized-weight decode measurements, every type and mix")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -600,6 +603,9 @@ def main():
     if args.quant_only:
         print(json.dumps({"quant": {k: quant_bench(A, k, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters,
                                                    not args.eager) for k in ALL_QUANT_KINDS}}))
+        return
+    if args.sampler_only:
+        print(json.dumps({"sampler": sampler_bench(A, args.seed)}))
         return
     if args.q8_only:
         q = q8_bench(A, args.seed, args.kv, args.steps, args.warmup, args.kernel_iters, not args.eager)

@@ -18,6 +18,7 @@
 //             add per chunk where no rounding depends on the order; the candidate count stays on
 //             the device between the stages
 //   greedy    temperature <= 0 or top_k == 1: the first maximum of the sanitized, masked logits
+//             (per-workgroup maxima over strided ranges, then one workgroup)
 //
 // The random number comes from RuneRNG on the host (one draw per sampled token, consumed only
 // when the reference consumes it: a final sum that is not <= 0, NaN included). exp is evaluated as the correctly
@@ -100,41 +101,73 @@ __global__ void sampler_prepare_kernel(const h16 *__restrict__ logits, int64_t V
 }
 
 // Greedy branch (:241-261): best = 0, max = value of index 0, strict '>' ascending; values are
-// sanitized and suppressed ones are -1e9. Equivalent to the lowest index of the maximum.
-__global__ __launch_bounds__(1024) void sampler_greedy_kernel(const h16 *__restrict__ logits, int64_t V,
-                                                              const uint8_t *__restrict__ mask, int64_t *out) {
-    __shared__ float bv[1024];
-    __shared__ int64_t bi[1024];
-    const int tid = threadIdx.x;
-    float best = -INFINITY;
-    int64_t besti = -1;
-    // strided (coalesced) scan; each thread sees its indices in increasing order, so strict '>'
-    // keeps its first maximum, and the tree below resolves equal values to the lower index
-    for (int64_t i = tid; i < V; i += 1024) {
+// sanitized and suppressed ones are -1e9. Equivalent to the lowest index of the maximum, which two
+// launches find: kGreedyParts workgroups take strided ranges of the logits (each thread sees its
+// indices in increasing order, so strict '>' keeps its first maximum) and reduce them to one
+// (value, index) pair each, the larger value winning and equal values going to the lower index;
+// one workgroup then reduces the pairs the same way.
+constexpr int kGreedyParts = 128;
+constexpr int kGreedyThreads = 256;
+
+__device__ __forceinline__ void greedy_pick(float &bv, int64_t &bi, float v, int64_t i) {
+    if (i >= 0 && (bi < 0 || v > bv || (v == bv && i < bi))) {
+        bv = v;
+        bi = i;
+    }
+}
+
+__device__ __forceinline__ void greedy_block_reduce(float &bv, int64_t &bi, float *sv, int64_t *si) {
+    for (int o = 32; o > 0; o >>= 1) {
+        const float v = __shfl_xor(bv, o);
+        const int64_t i = __shfl_xor(bi, o);
+        greedy_pick(bv, bi, v, i);
+    }
+    const int w = threadIdx.x / 64;
+    if ((threadIdx.x & 63) == 0) {
+        sv[w] = bv;
+        si[w] = bi;
+    }
+    __syncthreads();
+    bv = sv[0];
+    bi = si[0];
+    for (int k = 1; k < kGreedyThreads / 64; k++) greedy_pick(bv, bi, sv[k], si[k]);
+}
+
+__global__ __launch_bounds__(kGreedyThreads) void sampler_greedy_part_kernel(const h16 *__restrict__ logits, int64_t V,
+                                                                             const uint8_t *__restrict__ mask,
+                                                                             float *__restrict__ pv,
+                                                                             int64_t *__restrict__ pi) {
+    __shared__ float sv[kGreedyThreads / 64];
+    __shared__ int64_t si[kGreedyThreads / 64];
+    float bv = -INFINITY;
+    int64_t bi = -1;
+    for (int64_t i = (int64_t)blockIdx.x * kGreedyThreads + threadIdx.x; i < V;
+         i += (int64_t)gridDim.x * kGreedyThreads) {
         float v = sanitize_logit((float)logits[i]);
         if (mask && mask[i]) v = -1e9f;
-        if (besti < 0 || v > best) {
-            best = v;
-            besti = i;
+        if (bi < 0 || v > bv) {
+            bv = v;
+            bi = i;
         }
     }
-    bv[tid] = best;
-    bi[tid] = besti;
-    __syncthreads();
-    for (int st = 512; st > 0; st >>= 1) {
-        if (tid < st) {
-            // the larger value wins; equal values go to the lower index (first maximum)
-            const bool take = bi[tid + st] >= 0 &&
-                              (bi[tid] < 0 || bv[tid + st] > bv[tid] || (bv[tid + st] == bv[tid] && bi[tid + st] < bi[tid]));
-            if (take) {
-                bv[tid] = bv[tid + st];
-                bi[tid] = bi[tid + st];
-            }
-        }
-        __syncthreads();
+    greedy_block_reduce(bv, bi, sv, si);
+    if (threadIdx.x == 0) {
+        pv[blockIdx.x] = bv;
+        pi[blockIdx.x] = bi;
     }
-    if (tid == 0) {
-        out[0] = bi[0] < 0 ? 0 : bi[0];
+}
+
+__global__ __launch_bounds__(kGreedyThreads) void sampler_greedy_finish_kernel(const float *__restrict__ pv,
+                                                                               const int64_t *__restrict__ pi,
+                                                                               int nparts, int64_t *out) {
+    __shared__ float sv[kGreedyThreads / 64];
+    __shared__ int64_t si[kGreedyThreads / 64];
+    float bv = -INFINITY;
+    int64_t bi = -1;
+    for (int k = threadIdx.x; k < nparts; k += kGreedyThreads) greedy_pick(bv, bi, pv[k], pi[k]);
+    greedy_block_reduce(bv, bi, sv, si);
+    if (threadIdx.x == 0) {
+        out[0] = bi < 0 ? 0 : bi;
         out[1] = 0;  // no random number consumed
     }
 }
@@ -964,13 +997,16 @@ struct SamplerWork {
     uint32_t *marks = nullptr; // bits of the running sum at the start of every batch of chunks, then the total
     int64_t *lists = nullptr;  // context tokens then suppress ids
     int64_t *result = nullptr;
+    float *gpv = nullptr;      // the greedy branch's per-workgroup best values
+    int64_t *gpi = nullptr;    // and their indices
     void *sort_tmp = nullptr;
     size_t sort_tmp_bytes = 0;
 };
 
 static void free_work(SamplerWork *w) {
-    void *ps[] = {w->counts, w->mask, w->vals,  w->keys, w->keys_out, w->idx, w->idx_out, w->hdr,   w->cmax,
-                  w->terms,  w->csum, w->heads, w->subk, w->slow_list, w->marks, w->lists,  w->result, w->sort_tmp};
+    void *ps[] = {w->counts, w->mask,  w->vals,  w->keys,      w->keys_out, w->idx,   w->idx_out,
+                  w->hdr,    w->cmax,  w->terms, w->csum,      w->heads,    w->subk,  w->slow_list,
+                  w->marks,  w->lists, w->result, w->gpv,      w->gpi,      w->sort_tmp};
     for (void *p : ps)
         if (p) (void)hipFree(p);
     *w = SamplerWork{};
@@ -1029,6 +1065,21 @@ static int32_t ensure_work(aesir_ctx *ctx, int64_t V, int64_t n_lists) {
         w->cap_ctx = cap;
     }
     if (!w->result) AESIR_HIP_TRY(hipMalloc((void **)&w->result, 16));
+    if (!w->gpv) AESIR_HIP_TRY(hipMalloc((void **)&w->gpv, kGreedyParts * sizeof(float)));
+    if (!w->gpi) AESIR_HIP_TRY(hipMalloc((void **)&w->gpi, kGreedyParts * sizeof(int64_t)));
+    return AESIR_OK;
+}
+
+// The greedy branch's two launches: partial maxima of (at most) kGreedyParts workgroups, then one.
+static int32_t launch_greedy(hipStream_t s, const h16 *logits, int64_t V, const uint8_t *mask, SamplerWork *w) {
+    const int64_t want = (V + kGreedyThreads - 1) / kGreedyThreads;
+    const int parts = (int)(want < kGreedyParts ? want : kGreedyParts);
+    hipLaunchKernelGGL(sampler_greedy_part_kernel, dim3((unsigned)parts), dim3(kGreedyThreads), 0, s, logits, V, mask,
+                       w->gpv, w->gpi);
+    AESIR_LAUNCH_CHECK("sampler_greedy_part_kernel");
+    hipLaunchKernelGGL(sampler_greedy_finish_kernel, dim3(1), dim3(kGreedyThreads), 0, s, w->gpv, w->gpi, parts,
+                       w->result);
+    AESIR_LAUNCH_CHECK("sampler_greedy_finish_kernel");
     return AESIR_OK;
 }
 
@@ -1068,9 +1119,7 @@ int32_t aesir_sample_token(aesir_ctx *ctx, const void *logits, int64_t vocab, co
     hipStream_t s = ctx->stream;
     const bool greedy = cfg->temperature <= 0.0f || cfg->top_k == 1;  // sampler.mojo:235
     if (greedy && n_suppress == 0) {  // the greedy branch reads no penalty state: argmax of the logits
-        hipLaunchKernelGGL(sampler_greedy_kernel, dim3(1), dim3(1024), 0, s, (const h16 *)logits, vocab,
-                           (const uint8_t *)nullptr, w->result);
-        AESIR_LAUNCH_CHECK("sampler_greedy_kernel");
+        AESIR_TRY(launch_greedy(s, (const h16 *)logits, vocab, nullptr, w));
         AESIR_HIP_TRY(hipMemcpyAsync(ctx->pinned_i64, w->result, 16, hipMemcpyDeviceToHost, s));
         AESIR_HIP_TRY(hipStreamSynchronize(s));
         *token = ctx->pinned_i64[0];
@@ -1091,9 +1140,7 @@ int32_t aesir_sample_token(aesir_ctx *ctx, const void *logits, int64_t vocab, co
     }
     uint64_t st = *rng_state;
     if (greedy) {
-        hipLaunchKernelGGL(sampler_greedy_kernel, dim3(1), dim3(1024), 0, s, (const h16 *)logits, vocab, w->mask,
-                           w->result);
-        AESIR_LAUNCH_CHECK("sampler_greedy_kernel");
+        AESIR_TRY(launch_greedy(s, (const h16 *)logits, vocab, w->mask, w));
     } else {
         SampleParams p{};
         p.repetition_penalty = cfg->repetition_penalty;

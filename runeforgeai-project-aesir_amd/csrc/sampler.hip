@@ -996,6 +996,8 @@ struct SamplerWork {
     uint32_t *slow_list = nullptr;  // chunks the records kernel lists as likely slow
     uint32_t *marks = nullptr; // bits of the running sum at the start of every batch of chunks, then the total
     int64_t *lists = nullptr;  // context tokens then suppress ids
+    int64_t *lists_host = nullptr;       // pinned staging of the lists (hipHostMalloc), reused per call
+    hipEvent_t lists_copied = nullptr;   // the last copy out of lists_host
     int64_t *result = nullptr;
     float *gpv = nullptr;      // the greedy branch's per-workgroup best values
     int64_t *gpi = nullptr;    // and their indices
@@ -1009,6 +1011,8 @@ static void free_work(SamplerWork *w) {
                   w->marks,  w->lists, w->result, w->gpv,      w->gpi,      w->sort_tmp};
     for (void *p : ps)
         if (p) (void)hipFree(p);
+    if (w->lists_host) (void)hipHostFree(w->lists_host);
+    if (w->lists_copied) (void)hipEventDestroy(w->lists_copied);
     *w = SamplerWork{};
 }
 
@@ -1025,11 +1029,16 @@ static int32_t ensure_work(aesir_ctx *ctx, int64_t V, int64_t n_lists) {
     if (V > w->cap_v) {
         AESIR_HIP_TRY(hipStreamSynchronize(ctx->stream));
         const int64_t keep_lists = w->cap_ctx;
-        int64_t *old_lists = w->lists, *old_result = w->result;
+        int64_t *old_lists = w->lists, *old_result = w->result, *old_host = w->lists_host;
+        hipEvent_t old_event = w->lists_copied;
         w->lists = nullptr;
+        w->lists_host = nullptr;
+        w->lists_copied = nullptr;
         w->result = nullptr;
         free_work(w);
         w->lists = old_lists;
+        w->lists_host = old_host;
+        w->lists_copied = old_event;
         w->result = old_result;
         w->cap_ctx = keep_lists;
         AESIR_HIP_TRY(hipMalloc((void **)&w->counts, (size_t)V * 4));
@@ -1059,11 +1068,15 @@ static int32_t ensure_work(aesir_ctx *ctx, int64_t V, int64_t n_lists) {
     if (n_lists > w->cap_ctx || !w->lists) {
         AESIR_HIP_TRY(hipStreamSynchronize(ctx->stream));
         if (w->lists) (void)hipFree(w->lists);
+        if (w->lists_host) (void)hipHostFree(w->lists_host);
         w->lists = nullptr;
+        w->lists_host = nullptr;
         const int64_t cap = n_lists > 1024 ? n_lists : 1024;
         AESIR_HIP_TRY(hipMalloc((void **)&w->lists, (size_t)cap * 8));
+        AESIR_HIP_TRY(hipHostMalloc((void **)&w->lists_host, (size_t)cap * 8, hipHostMallocDefault));
         w->cap_ctx = cap;
     }
+    if (!w->lists_copied) AESIR_HIP_TRY(hipEventCreateWithFlags(&w->lists_copied, hipEventDisableTiming));
     if (!w->result) AESIR_HIP_TRY(hipMalloc((void **)&w->result, 16));
     if (!w->gpv) AESIR_HIP_TRY(hipMalloc((void **)&w->gpv, kGreedyParts * sizeof(float)));
     if (!w->gpi) AESIR_HIP_TRY(hipMalloc((void **)&w->gpi, kGreedyParts * sizeof(int64_t)));
@@ -1125,10 +1138,15 @@ int32_t aesir_sample_token(aesir_ctx *ctx, const void *logits, int64_t vocab, co
         *token = ctx->pinned_i64[0];
         return AESIR_OK;
     }
-    if (n_context > 0)
-        AESIR_HIP_TRY(hipMemcpyAsync(w->lists, context, (size_t)n_context * 8, hipMemcpyHostToDevice, s));
-    if (n_suppress > 0)
-        AESIR_HIP_TRY(hipMemcpyAsync(w->lists + n_context, suppress, (size_t)n_suppress * 8, hipMemcpyHostToDevice, s));
+    if (n_lists > 0) {
+        // through the pinned staging buffer (an asynchronous copy; a pageable source would be
+        // staged synchronously by the runtime), once the previous call's copy out of it is done
+        AESIR_HIP_TRY(hipEventSynchronize(w->lists_copied));
+        if (n_context > 0) std::memcpy(w->lists_host, context, (size_t)n_context * 8);
+        if (n_suppress > 0) std::memcpy(w->lists_host + n_context, suppress, (size_t)n_suppress * 8);
+        AESIR_HIP_TRY(hipMemcpyAsync(w->lists, w->lists_host, (size_t)n_lists * 8, hipMemcpyHostToDevice, s));
+        AESIR_HIP_TRY(hipEventRecord(w->lists_copied, s));
+    }
     const unsigned g = (unsigned)((vocab + kSThreads - 1) / kSThreads < 4096 ? (vocab + kSThreads - 1) / kSThreads : 4096);
     hipLaunchKernelGGL(sampler_clear_kernel, dim3(g), dim3(kSThreads), 0, s, w->counts, w->mask, vocab);
     AESIR_LAUNCH_CHECK("sampler_clear_kernel");

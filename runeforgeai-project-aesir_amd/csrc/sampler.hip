@@ -7,7 +7,9 @@
 //   sort      when top-k, top-p or min-p truncates: one stable LSD radix sort (rocPRIM) of
 //             (descending logit key, index). Equal logits (-0 == +0) keep index order, which is the
 //             order the reference's stable insertion sort (:92-104) produces; every later stage of
-//             the stack sees an already sorted prefix, so one sort serves all of them
+//             the stack sees an already sorted prefix, so one sort serves all of them. With
+//             top_k <= 4096 only that prefix is found: a radix select of the k-th key, an
+//             index-order compaction and a sort of the k selected pairs (same order, no full sort)
 //   tail      top_k <= 4096: one workgroup makes the truncations and the draw, the running sums
 //             of apply_top_p, apply_min_p and the draw in one lane in candidate order (f32
 //             addition is not associative; the sums must follow the reference's order to choose
@@ -34,6 +36,7 @@ namespace aesir {
 
 constexpr int kSThreads = 256;
 constexpr int kTailThreads = 256;
+constexpr int kSeqTile = 4096;  // terms per LDS tile of the tail (two tiles); its candidate limit
 
 __device__ __forceinline__ float sanitize_logit(float v) { return (isnan(v) || isinf(v)) ? -1e9f : v; }
 __device__ __forceinline__ float exp_f32(float x) { return (float)exp((double)x); }
@@ -55,11 +58,15 @@ struct SampleParams {
     float u;        // RuneRNG.next_float32 for the draw
 };
 
-__global__ void sampler_clear_kernel(int32_t *__restrict__ counts, uint8_t *__restrict__ mask, int64_t V) {
-    for (int64_t i = (int64_t)blockIdx.x * kSThreads + threadIdx.x; i < V; i += (int64_t)gridDim.x * kSThreads) {
+// Clears the context histogram and suppress flags, and the top-k selection's key histograms.
+__global__ void sampler_clear_kernel(int32_t *__restrict__ counts, uint8_t *__restrict__ mask, int64_t V,
+                                     uint32_t *__restrict__ hist, int nhist) {
+    const int64_t t0 = (int64_t)blockIdx.x * kSThreads + threadIdx.x, step = (int64_t)gridDim.x * kSThreads;
+    for (int64_t i = t0; i < V; i += step) {
         counts[i] = 0;
         mask[i] = 0;
     }
+    for (int64_t i = t0; i < nhist; i += step) hist[i] = 0;
 }
 
 // Occurrence counts of the context tokens and the suppress flags (ids outside the vocabulary
@@ -98,6 +105,244 @@ __global__ void sampler_prepare_kernel(const h16 *__restrict__ logits, int64_t V
             idx[i] = (int32_t)i;
         }
     }
+}
+
+// ------------------------------------------------------------------ top-k selection
+//
+// With top_k <= kSeqTile only the first top_k candidates of the stable descending sort are ever
+// read, so instead of sorting the vocabulary the stages find them exactly:
+//   1. the k-th smallest radix key T (ascending key order is the sort's order) by a radix select,
+//      three histogram passes over the key's digits (bits 21-31, 10-20, 0-9); pass p counts the
+//      keys that match the digits already fixed, each workgroup deriving those digits from the
+//      earlier passes' histograms (a scan of 2048 bins per pass)
+//   2. per workgroup, the counts of keys below T and equal to T; then the compaction, in index
+//      order: every key below T, and the lowest-index keys equal to T that complete top_k (the
+//      stable sort keeps equal keys in index order)
+//   3. one workgroup sorts the top_k (key, index) pairs as 64-bit values in LDS (bitonic); the
+//      pairs are distinct, so any correct sort gives the stable sort's order
+constexpr int kSelBins = 2048;
+constexpr int kSelPer = 4;                              // keys per thread of the selection passes
+constexpr int kSelBlock = kSThreads * kSelPer;          // keys per workgroup
+constexpr int kSelShift[3] = {21, 10, 0};
+constexpr uint32_t kSelMask[3] = {0x7FFu, 0x7FFu, 0x3FFu};
+
+struct SelState {
+    uint32_t prefix;  // digits fixed so far
+    uint32_t rank;    // 1-based rank of the wanted key among the keys matching prefix
+    uint32_t lt;      // keys below every key matching prefix
+};
+
+// The digits fixed by passes 0 .. np-1, from their histograms (the whole workgroup takes part).
+__device__ SelState sel_state(const uint32_t *__restrict__ hist, int np, uint32_t k, uint32_t *sh) {
+    SelState st{0u, k, 0u};
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    constexpr int per = kSelBins / kSThreads;  // 8 bins per thread
+    for (int q = 0; q < np; q++) {
+        const uint32_t *h = hist + q * kSelBins;
+        uint32_t v[per], sum = 0;
+#pragma unroll
+        for (int j = 0; j < per; j++) {
+            v[j] = h[tid * per + j];
+            sum += v[j];
+        }
+        // exclusive prefix of the thread sums over the workgroup
+        uint32_t incl = sum;
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t t = __shfl_up(incl, o);
+            if (lane >= o) incl += t;
+        }
+        if (lane == 63) sh[wave] = incl;
+        __syncthreads();
+        uint32_t base = 0;
+        for (int w = 0; w < wave; w++) base += sh[w];
+        uint32_t c = base + incl - sum;  // keys in bins before this thread's
+        if (c < st.rank && st.rank <= c + sum) {
+            uint32_t d = 0;
+#pragma unroll
+            for (int j = 0; j < per; j++) {
+                if (c + v[j] >= st.rank) {
+                    d = (uint32_t)(tid * per + j);
+                    break;
+                }
+                c += v[j];
+            }
+            sh[4] = d;
+            sh[5] = c;
+        }
+        __syncthreads();
+        const uint32_t d = sh[4], before = sh[5];
+        st.lt += before;
+        st.rank -= before;
+        st.prefix |= d << kSelShift[q];
+        __syncthreads();
+    }
+    return st;
+}
+
+__device__ __forceinline__ bool sel_match(uint32_t key, const SelState &st, int np) {
+    return np == 0 || (key >> kSelShift[np - 1]) == (st.prefix >> kSelShift[np - 1]);
+}
+
+template <int NP>
+__global__ __launch_bounds__(kSThreads) void sampler_select_hist_kernel(const uint32_t *__restrict__ keys, int64_t V,
+                                                                        uint32_t *__restrict__ hist, uint32_t k) {
+    __shared__ uint32_t lh[kSelBins];
+    __shared__ uint32_t sh[8];
+    const int tid = threadIdx.x;
+    for (int b = tid; b < kSelBins; b += kSThreads) lh[b] = 0;
+    const SelState st = sel_state(hist, NP, k, sh);
+    __syncthreads();  // lh is clear (sel_state synchronizes only when NP > 0)
+    const int64_t base = (int64_t)blockIdx.x * kSelBlock;
+#pragma unroll
+    for (int j = 0; j < kSelPer; j++) {
+        const int64_t i = base + j * kSThreads + tid;
+        if (i < V) {
+            const uint32_t key = keys[i];
+            if (sel_match(key, st, NP)) atomicAdd(&lh[(key >> kSelShift[NP]) & kSelMask[NP]], 1u);
+        }
+    }
+    __syncthreads();
+    uint32_t *gh = hist + NP * kSelBins;
+    for (int b = tid; b < kSelBins; b += kSThreads)
+        if (lh[b]) atomicAdd(&gh[b], lh[b]);
+}
+
+// Per workgroup of kSelBlock keys: how many are below T and how many equal it.
+__global__ __launch_bounds__(kSThreads) void sampler_select_count_kernel(const uint32_t *__restrict__ keys, int64_t V,
+                                                                         const uint32_t *__restrict__ hist, uint32_t k,
+                                                                         uint32_t *__restrict__ cnt) {
+    __shared__ uint32_t sh[8];
+    __shared__ uint32_t red[2][kSThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const SelState st = sel_state(hist, 3, k, sh);
+    const uint32_t T = st.prefix;
+    const int64_t base = (int64_t)blockIdx.x * kSelBlock;
+    uint32_t lt = 0, eq = 0;
+#pragma unroll
+    for (int j = 0; j < kSelPer; j++) {
+        const int64_t i = base + j * kSThreads + tid;
+        if (i < V) {
+            const uint32_t key = keys[i];
+            lt += key < T;
+            eq += key == T;
+        }
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        lt += __shfl_xor(lt, o);
+        eq += __shfl_xor(eq, o);
+    }
+    if (lane == 0) {
+        red[0][wave] = lt;
+        red[1][wave] = eq;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t a = 0, b = 0;
+        for (int w = 0; w < kSThreads / 64; w++) {
+            a += red[0][w];
+            b += red[1][w];
+        }
+        cnt[2 * blockIdx.x] = a;
+        cnt[2 * blockIdx.x + 1] = b;
+    }
+}
+
+// The compaction: key-below-T entries at their index-order rank among them, the first
+// `rank` equal-key entries (in index order) after them; 64-bit (key, index) values.
+__global__ __launch_bounds__(kSThreads) void sampler_select_compact_kernel(const uint32_t *__restrict__ keys, int64_t V,
+                                                                           const uint32_t *__restrict__ hist, uint32_t k,
+                                                                           const uint32_t *__restrict__ cnt,
+                                                                           uint64_t *__restrict__ cand) {
+    __shared__ uint32_t sh[8];
+    __shared__ uint32_t wl[kSThreads / 64], we[kSThreads / 64];
+    __shared__ uint32_t pre_s[2];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const SelState st = sel_state(hist, 3, k, sh);
+    const uint32_t T = st.prefix, need = st.rank, total_lt = st.lt;
+    // keys below T and equal to T in the workgroups before this one
+    {
+        uint32_t a = 0, b = 0;
+        for (int w = tid; w < (int)blockIdx.x; w += kSThreads) {
+            a += cnt[2 * w];
+            b += cnt[2 * w + 1];
+        }
+        for (int o = 32; o > 0; o >>= 1) {
+            a += __shfl_xor(a, o);
+            b += __shfl_xor(b, o);
+        }
+        if (lane == 0) {
+            wl[wave] = a;
+            we[wave] = b;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            uint32_t x = 0, y = 0;
+            for (int w = 0; w < kSThreads / 64; w++) {
+                x += wl[w];
+                y += we[w];
+            }
+            pre_s[0] = x;
+            pre_s[1] = y;
+        }
+        __syncthreads();
+    }
+    uint32_t run_lt = pre_s[0], run_eq = pre_s[1];
+    const int64_t base = (int64_t)blockIdx.x * kSelBlock;
+    for (int j = 0; j < kSelPer; j++) {  // index order: pass j covers keys base + j * 256 + [0, 256)
+        const int64_t i = base + j * kSThreads + tid;
+        const uint32_t key = i < V ? keys[i] : 0xFFFFFFFFu;
+        const bool is_lt = i < V && key < T, is_eq = i < V && key == T;
+        const uint64_t bl = __ballot(is_lt), be = __ballot(is_eq);
+        const uint32_t rl = (uint32_t)__popcll(bl & ((1ull << lane) - 1ull));
+        const uint32_t re = (uint32_t)__popcll(be & ((1ull << lane) - 1ull));
+        __syncthreads();  // wl / we of the previous pass have been read
+        if (lane == 0) {
+            wl[wave] = (uint32_t)__popcll(bl);
+            we[wave] = (uint32_t)__popcll(be);
+        }
+        __syncthreads();
+        uint32_t ol = run_lt, oe = run_eq;
+        for (int w = 0; w < wave; w++) {
+            ol += wl[w];
+            oe += we[w];
+        }
+        // the slots stay below k by construction (total_lt + need = k); the bounds are checked anyway
+        if (is_lt && ol + rl < k) cand[ol + rl] = ((uint64_t)key << 32) | (uint64_t)i;
+        if (is_eq && oe + re < need && total_lt + oe + re < k)
+            cand[total_lt + oe + re] = ((uint64_t)key << 32) | (uint64_t)i;
+        for (int w = 0; w < kSThreads / 64; w++) {
+            run_lt += wl[w];
+            run_eq += we[w];
+        }
+    }
+}
+
+// Sorts the k <= kSeqTile selected (key, index) values (bitonic, in LDS) and writes the indices.
+constexpr int kSelSortThreads = 1024;
+__global__ __launch_bounds__(kSelSortThreads) void sampler_select_sort_kernel(const uint64_t *__restrict__ cand,
+                                                                              int k, int32_t *__restrict__ order) {
+    __shared__ uint64_t v[kSeqTile];
+    int m = 1;
+    while (m < k) m <<= 1;
+    for (int i = threadIdx.x; i < m; i += kSelSortThreads) v[i] = i < k ? cand[i] : ~0ull;
+    __syncthreads();
+    for (int size = 2; size <= m; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = threadIdx.x; i < m; i += kSelSortThreads) {
+                const int j = i ^ stride;
+                if (j > i) {
+                    const bool up = (i & size) == 0;
+                    const uint64_t a = v[i], b = v[j];
+                    if ((a > b) == up) {
+                        v[i] = b;
+                        v[j] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    for (int i = threadIdx.x; i < k; i += kSelSortThreads) order[i] = (int32_t)(v[i] & 0xFFFFFFFFull);
 }
 
 // Greedy branch (:241-261): best = 0, max = value of index 0, strict '>' ascending; values are
@@ -178,7 +423,6 @@ __global__ __launch_bounds__(kGreedyThreads) void sampler_greedy_finish_kernel(c
 // associative, so the order fixes the cut). The terms come from two LDS tiles: while lane 0 adds
 // one tile, waves 1-3 compute the next tile's terms into the other. Longer candidate lists take
 // the chunked stages below.
-constexpr int kSeqTile = 4096;  // terms per LDS tile (two tiles)
 constexpr int kSeqBlock = 32;   // terms per block of lane 0's adds
 
 // Lane 0's adds over one tile, acc += buf[e] for e in [0, cnt), 32 terms per block with the next
@@ -999,6 +1243,9 @@ struct SamplerWork {
     int64_t *lists_host = nullptr;       // pinned staging of the lists (hipHostMalloc), reused per call
     hipEvent_t lists_copied = nullptr;   // the last copy out of lists_host
     int64_t *result = nullptr;
+    uint32_t *sel_hist = nullptr;  // top-k selection: 3 digit histograms of kSelBins
+    uint32_t *sel_cnt = nullptr;   // per-workgroup counts below / equal to the threshold key
+    uint64_t *sel_cand = nullptr;  // the selected (key, index) values, kSeqTile
     float *gpv = nullptr;      // the greedy branch's per-workgroup best values
     int64_t *gpi = nullptr;    // and their indices
     void *sort_tmp = nullptr;
@@ -1008,7 +1255,8 @@ struct SamplerWork {
 static void free_work(SamplerWork *w) {
     void *ps[] = {w->counts, w->mask,  w->vals,  w->keys,      w->keys_out, w->idx,   w->idx_out,
                   w->hdr,    w->cmax,  w->terms, w->csum,      w->heads,    w->subk,  w->slow_list,
-                  w->marks,  w->lists, w->result, w->gpv,      w->gpi,      w->sort_tmp};
+                  w->marks,  w->lists, w->result, w->gpv,      w->gpi,      w->sort_tmp,
+                  w->sel_hist, w->sel_cnt, w->sel_cand};
     for (void *p : ps)
         if (p) (void)hipFree(p);
     if (w->lists_host) (void)hipHostFree(w->lists_host);
@@ -1057,6 +1305,9 @@ static int32_t ensure_work(aesir_ctx *ctx, int64_t V, int64_t n_lists) {
         AESIR_HIP_TRY(hipMalloc((void **)&w->heads, (size_t)nbat * 64 * 4));
         AESIR_HIP_TRY(hipMalloc((void **)&w->subk, (size_t)nch * kSubWords * 4));
         AESIR_HIP_TRY(hipMalloc((void **)&w->slow_list, (size_t)kSlowListMax * 4));
+        AESIR_HIP_TRY(hipMalloc((void **)&w->sel_hist, (size_t)3 * kSelBins * 4));
+        AESIR_HIP_TRY(hipMalloc((void **)&w->sel_cnt, (size_t)2 * ((V + kSelBlock - 1) / kSelBlock) * 4));
+        AESIR_HIP_TRY(hipMalloc((void **)&w->sel_cand, (size_t)kSeqTile * 8));
         AESIR_HIP_TRY(hipMalloc((void **)&w->marks, (size_t)(nbat + 1) * 4));
         size_t bytes = 0;
         AESIR_HIP_TRY(rocprim::radix_sort_pairs(nullptr, bytes, w->keys, w->keys_out, w->idx, w->idx_out,
@@ -1148,7 +1399,8 @@ int32_t aesir_sample_token(aesir_ctx *ctx, const void *logits, int64_t vocab, co
         AESIR_HIP_TRY(hipEventRecord(w->lists_copied, s));
     }
     const unsigned g = (unsigned)((vocab + kSThreads - 1) / kSThreads < 4096 ? (vocab + kSThreads - 1) / kSThreads : 4096);
-    hipLaunchKernelGGL(sampler_clear_kernel, dim3(g), dim3(kSThreads), 0, s, w->counts, w->mask, vocab);
+    hipLaunchKernelGGL(sampler_clear_kernel, dim3(g), dim3(kSThreads), 0, s, w->counts, w->mask, vocab, w->sel_hist,
+                       3 * kSelBins);
     AESIR_LAUNCH_CHECK("sampler_clear_kernel");
     if (n_lists > 0) {
         const unsigned gl = (unsigned)((n_lists + kSThreads - 1) / kSThreads < 4096 ? (n_lists + kSThreads - 1) / kSThreads : 4096);
@@ -1180,13 +1432,30 @@ int32_t aesir_sample_token(aesir_ctx *ctx, const void *logits, int64_t vocab, co
         hipLaunchKernelGGL(sampler_prepare_kernel, dim3(g), dim3(kSThreads), 0, s, (const h16 *)logits, vocab,
                            w->counts, w->mask, p, w->vals, w->keys, w->idx);
         AESIR_LAUNCH_CHECK("sampler_prepare_kernel");
-        if (p.sort) {
+        const bool select_k = k_on && cfg->top_k <= kSeqTile;
+        if (select_k) {  // the first top_k of the stable sort, found without sorting the vocabulary
+            const unsigned nb = (unsigned)((vocab + kSelBlock - 1) / kSelBlock);
+            const uint32_t k = (uint32_t)cfg->top_k;
+            hipLaunchKernelGGL(sampler_select_hist_kernel<0>, dim3(nb), dim3(kSThreads), 0, s, w->keys, vocab, w->sel_hist, k);
+            hipLaunchKernelGGL(sampler_select_hist_kernel<1>, dim3(nb), dim3(kSThreads), 0, s, w->keys, vocab, w->sel_hist, k);
+            hipLaunchKernelGGL(sampler_select_hist_kernel<2>, dim3(nb), dim3(kSThreads), 0, s, w->keys, vocab, w->sel_hist, k);
+            AESIR_LAUNCH_CHECK("sampler_select_hist_kernel");
+            hipLaunchKernelGGL(sampler_select_count_kernel, dim3(nb), dim3(kSThreads), 0, s, w->keys, vocab, w->sel_hist, k,
+                               w->sel_cnt);
+            AESIR_LAUNCH_CHECK("sampler_select_count_kernel");
+            hipLaunchKernelGGL(sampler_select_compact_kernel, dim3(nb), dim3(kSThreads), 0, s, w->keys, vocab,
+                               w->sel_hist, k, w->sel_cnt, w->sel_cand);
+            AESIR_LAUNCH_CHECK("sampler_select_compact_kernel");
+            hipLaunchKernelGGL(sampler_select_sort_kernel, dim3(1), dim3(kSelSortThreads), 0, s, w->sel_cand, (int)k,
+                               w->idx_out);
+            AESIR_LAUNCH_CHECK("sampler_select_sort_kernel");
+        } else if (p.sort) {
             size_t bytes = w->sort_tmp_bytes;
             AESIR_HIP_TRY(rocprim::radix_sort_pairs(w->sort_tmp, bytes, w->keys, w->keys_out, w->idx, w->idx_out,
                                                     (unsigned)vocab, 0, 32, s));
         }
         const int32_t *order = p.sort ? (const int32_t *)w->idx_out : nullptr;
-        if (k_on && cfg->top_k <= kSeqTile) {
+        if (select_k) {
             // at most one LDS tile of candidates: truncations and the draw in one workgroup
             hipLaunchKernelGGL(sampler_tail_kernel, dim3(1), dim3(kTailThreads), 0, s, w->vals, order, vocab, p,
                                w->result);

@@ -125,3 +125,30 @@ def test_sampler_long_vocabulary_matches_oracle(A, ctx, oracle, cfgd):
         want, o_state = oracle.sample_token_f16(logits, ocfg, o_state, context, [])
         assert got == want, (d, got, want)
         assert g_rng.state == o_state, d
+
+
+@pytest.mark.parametrize("vocab", [4097, 10000, 128256])
+@pytest.mark.parametrize("top_k", [2, 3, 4095, 4096])
+@pytest.mark.parametrize("logit_kind", ["equal", "two_values", "grid"])
+def test_sampler_topk_selection_matches_oracle(A, ctx, oracle, vocab, top_k, logit_kind):
+    """top_k <= 4096 takes the first top_k of the stable descending sort without sorting the
+    vocabulary (radix select of the k-th key, index-order compaction, a sort of the k selected).
+    Ties at the threshold key must keep the lowest indices: all-equal logits (every key equals the
+    threshold), two values, and a coarse grid."""
+    rng = np.random.default_rng(vocab + top_k)
+    cfgd = dict(temperature=0.9, top_k=top_k)
+    gcfg, ocfg = A.SamplerConfig(**cfgd), oracle.SamplerConfig(**cfgd)
+    g_rng = A.RuneRNG(7)
+    o_state = oracle.rune_rng_state(7)
+    for d in range(3):
+        if logit_kind == "equal":
+            logits = np.full(vocab, 1.5, np.float16)
+        elif logit_kind == "two_values":
+            logits = np.where(rng.random(vocab) < 0.001, 3.0, -1.0).astype(np.float16)
+        else:
+            logits = (rng.integers(-20, 20, vocab) * 0.5).astype(np.float16)
+        t = ctx.from_numpy(logits.reshape(1, -1))
+        got = A.sample_token(ctx, t, gcfg, g_rng, [])
+        want, o_state = oracle.sample_token_f16(logits, ocfg, o_state, [], [])
+        assert got == want, (d, got, want)
+        assert g_rng.state == o_state, d

@@ -1324,6 +1324,17 @@ static void gemv_qf_launch_t(hipStream_t s, const QFMat &w, int64_t N, int64_t K
     constexpr int RD = qf_round<T>();
     const QfShape sh = qf_shape((N + 15) / 16, RD);
     const size_t lds = (size_t)(2 * K) + ((size_t)sh.nw * (2 * 16 + 1) + 16) * sizeof(float);
+    // Q6_K rows of at least 8192 weights (the down projection: few row blocks, one per workgroup,
+    // each a long sequence of rounds) take rounds of 2 tiles, as the other types; shorter ones keep
+    // 1. Measured at the Llama-3-8B shape in alternating runs: down 12.2-12.5 -> 11.8-12.1 us with 2
+    // tiles, while gate/up (21.6-22.2 -> 21.6-23.3 us) and lm_head (75-76 -> 76-80 us) lose.
+    if constexpr (T == AESIR_GGML_Q6_K) {
+        if (K >= 8192) {
+            hipLaunchKernelGGL((gemv_qf_kernel<T, 8, 2, kQfDepth, NORM, Epi>), dim3((unsigned)sh.grid), dim3(8 * kWave),
+                               lds, s, w, N, K, src, (const h16 *)nwt, eps, epi);
+            return;
+        }
+    }
     hipLaunchKernelGGL((gemv_qf_kernel<T, 8, RD / 2, kQfDepth, NORM, Epi>), dim3((unsigned)sh.grid), dim3(8 * kWave), lds, s,
                        w, N, K, src, (const h16 *)nwt, eps, epi);
 }

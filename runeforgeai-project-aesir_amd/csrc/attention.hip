@@ -273,10 +273,14 @@ __device__ __forceinline__ int64_t decode_seq_len(const AttnArgs &a) {
     return pos + 1 < a.max_seq ? pos + 1 : a.max_seq;
 }
 
-// Positions per split for S positions (whole rounds, at most max_split splits).
-__device__ __forceinline__ int64_t split_chunk(int64_t S, int64_t max_split) {
-    int64_t chunk = (S + max_split - 1) / max_split;
-    return (chunk + kRound - 1) / kRound * kRound;
+// Splits of S positions: each covers at most ceil(rounds / max_split) 64-position rounds, so
+// nsplit = ceil(rounds / per) with per = ceil(rounds / max_split) (the same as whole-round chunks
+// of ceil(S / max_split) positions, by ceil(ceil(a / b) / c) = ceil(a / (b c))). 32-bit divisions:
+// a 64-bit one is a long dependent sequence at the head of both kernels.
+__device__ __forceinline__ int split_count(int64_t S, int64_t max_split) {
+    const uint32_t rounds = (uint32_t)((S + kRound - 1) / kRound), ms = (uint32_t)max_split;
+    const uint32_t per = (rounds + ms - 1) / ms;
+    return (int)((rounds + per - 1) / per);
 }
 
 // NG > 1 (short views, one split): NG groups of 256 threads share the workgroup; group q takes
@@ -312,13 +316,13 @@ __global__ __launch_bounds__(kAThreads * NG) void attn_fast_kernel(AttnArgs a) {
     const int g = blockIdx.y, hg = blockIdx.z;
     const int split = blockIdx.x;
     const int64_t S = decode_seq_len(a);
-    const int64_t chunk = split_chunk(S, a.max_split);
-    const int nsplit = (int)((S + chunk - 1) / chunk);
+    const int nsplit = split_count(S, a.max_split);
     if (split >= nsplit) return;  // idle workgroup
     // Split s takes the rounds s, s + nsplit, s + 2 nsplit, ... of the view (rounds dealt out, not
     // a contiguous chunk): at each step the splits together read one contiguous stretch of rows,
     // so the grid sweeps the cache front to back (KV 32768 at the Llama-3 shape: 31.7 -> 28.0 us
-    // per layer for the partials) and a split's partial still covers chunk positions at most.
+    // per layer for the partials) and a split's partial still covers ceil(rounds / max_split)
+    // rounds at most.
     const int64_t p0 = (int64_t)split * kRound;
     const int64_t p1 = S;
     const int64_t head0 = (int64_t)g * G + (int64_t)hg * GH;  // first query head of this workgroup
@@ -540,8 +544,7 @@ __global__ __launch_bounds__(kAThreads) void attn_fast_merge_kernel(AttnArgs a) 
     __shared__ float2 gx[NG][NDP];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t S = decode_seq_len(a);
-    const int64_t chunk = split_chunk(S, a.max_split);
-    const int nsplit = (int)((S + chunk - 1) / chunk);
+    const int nsplit = split_count(S, a.max_split);
     if (nsplit <= 1) return;  // the partial kernel wrote the output
     const int64_t h = blockIdx.x;
     const float *base = a.part + h * a.max_split * (HD + 2);

@@ -312,7 +312,7 @@ __global__ __launch_bounds__(kAThreads * NG) void attn_fast_kernel(AttnArgs a) {
     auto &mrun = mruns[grp];
     auto &lrun = lruns[grp];
     auto &pvx = pvxs[grp];
-    const int64_t G = a.nq / a.nkv;
+    const int64_t G = (int64_t)GH * gridDim.z;  // query heads per KV head (the grid's z is G / GH)
     const int g = blockIdx.y, hg = blockIdx.z;
     const int split = blockIdx.x;
     const int64_t S = decode_seq_len(a);

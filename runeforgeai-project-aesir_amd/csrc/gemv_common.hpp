@@ -92,12 +92,13 @@ struct EpiQkv {
     const DecodeState *state;
     int64_t dim, kvd, hd, max_seq;
     struct Pre {
-        int64_t pos;
-        h16x2 cs;  // cos/sin of this thread's pair (Q and K rows)
+        int64_t pos, slot;  // position and its cache row (pos % max_seq, taken while the weights stream)
+        h16x2 cs;           // cos/sin of this thread's pair (Q and K rows)
     };
     template <int ROWS>
     __device__ __forceinline__ Pre prefetch(int64_t n0, int64_t, int64_t N, int tid) const {
-        Pre p{state->pos, h16x2{(h16)1.0f, (h16)0.0f}};
+        Pre p{state->pos, 0, h16x2{(h16)1.0f, (h16)0.0f}};
+        p.slot = p.pos % max_seq;
         const int64_t n = n0 + 2 * tid;
         if (tid < ROWS / 2 && n < N && n < dim + kvd) {
             const int64_t nn = n < dim ? n : n - dim;
@@ -112,8 +113,7 @@ struct EpiQkv {
         const int64_t n = n0 + 2 * tid;
         if (n >= N) return;
         const h16 s0 = (h16)s[2 * tid], s1 = (h16)s[2 * tid + 1];
-        const int64_t pos = pre.pos;
-        const int64_t slot = pos % max_seq;
+        const int64_t slot = pre.slot;
         if (n < dim + kvd) {
             const int64_t nn = n < dim ? n : n - dim;
             const h16x2 cs = pre.cs;
